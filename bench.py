@@ -1,0 +1,228 @@
+"""Benchmark: VoxCPM2 BaseLM Q8_0 decode at batch 1 on one MI355X.
+
+Workload (the 28-layer decode benchmark): hidden 2048, 28 layers, 16/2 heads x
+128, FFN 6144, vocab 73448, Q8_0 weights (d = f16(|N(0,1)|*0.01), q ~ U[-127,127]),
+F16 tied embedding N(0,0.02). A 256-token prefill fills the KV cache, then K
+decode steps at positions 256..256+K-1 with token ids uniform from the vocab;
+each step is one hipGraph replay of the fused decode step (LM head off, the
+*_gpu_only semantics). A "step" is one decoded token.
+
+Prints one JSON line: tok/s, the per-kernel roofline of the dominant kernel
+(the gate/up SwiGLU matvec) from HIP events on the engine stream, the whole
+matvec-family bandwidth, and the CPU oracle's throughput on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "Q8_0 BaseLM decode tok/s @ batch 1; matvec HBM GB/s (% of 8 TB/s peak)"
+
+# Algorithmic bytes per launch of each decode kernel at the benchmark shapes
+# (Q8_0: 34 B per 32 weights; activations f32; KV f16).
+H, KV, F, L, V = 2048, 256, 6144, 28, 73448
+
+
+def q8(rows, cols):
+    return rows * cols // 32 * 34
+
+
+KERNEL_BYTES = {
+    # weights + hidden + attn_norm in + q/k/v out + K/V cache row writes
+    "baselm.qkv": q8(H + 2 * KV, H) + 2 * H * 4 + (H + 2 * KV) * 4 + 2 * KV * 2,
+    "baselm.attn_out": q8(H, H) + H * 4 + 2 * H * 4,                 # weights + x + hidden rw
+    "baselm.swiglu": 2 * q8(F, H) + 2 * H * 4 + F * 4,               # gate+up + hidden,norm + out
+    "baselm.down": q8(H, F) + F * 4 + 2 * H * 4,                     # weights + x + hidden rw
+}
+
+
+def attention_bytes(pos):
+    return 2 * (pos + 1) * KV * 2 + H * 4 * 2  # K and V rows read + q in + out
+
+
+def step_bytes(pos, lm_head=False):
+    """Algorithmic HBM bytes of one decode step at position pos (28 layers)."""
+    per_layer = sum(KERNEL_BYTES.values()) + attention_bytes(pos)
+    b = L * per_layer + H * 2 + H * 4 * 2  # embedding row (f16) + output norm
+    if lm_head:
+        b += V * H * 2 + V * 4
+    return b
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prefill", type=int, default=256)
+    ap.add_argument("--lm-head", action="store_true", help="include the tied F16 LM head per step")
+    ap.add_argument("--cpu-steps", type=int, default=-1, help="CPU oracle sample size (-1 = auto)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference"])
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: the BaseLM decode path has no multi-GPU form "
+              f"(got --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    from voxgen_amd import abi, synth
+    from voxgen_amd.baselm import BaseLmEngine
+    from voxgen_amd.runtime import Context, Model
+
+    abi.load()
+    K, W, P = args.steps, args.warmup, args.prefill
+    active = P + max(K, W) + 1
+    cfg = synth.baselm_config(active_context=max(active, 512))
+    t0 = time.perf_counter()
+    m = synth.build_baselm(cfg, seed=0x5EED0002)
+    log(f"synthetic 28-layer Q8_0 model: {m.data.nbytes / 1e9:.2f} GB in {time.perf_counter() - t0:.1f}s")
+    tokens = synth.uniform_u32(P + max(K, W), 0x5EED0012, cfg["vocab_size"]).astype(np.uint32)
+    ctx = Context(0)
+    info = ctx.info()
+    model = Model(ctx, m.data, m.tensors)
+    eng = BaseLmEngine(ctx, model, cfg, exec_mode=args.mode, strict_geometry=True)
+    log(f"device {info['name']} {info['arch']} CUs={info['compute_units']}; model on device "
+        f"{model.device_bytes / 1e9:.2f} GB")
+
+    def run_steps(start, toks):
+        eng.set_position(start)
+        if args.lm_head:
+            for t in toks:
+                eng.decode_token(int(t))
+        else:
+            eng.decode_tokens_gpu_only(toks)
+
+    eng.decode_tokens_gpu_only(tokens[:P])              # prefill positions 0..P-1
+    run_steps(P, tokens[P:P + W])                         # warmup (also captures the graph)
+    ctx.sync()
+    timed = tokens[P:P + K]
+    ctx.sync()
+    t0 = time.perf_counter()
+    run_steps(P, timed)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    tok_s = K / elapsed
+    log(f"timed {K} steps at positions {P}..{P + K - 1}: {elapsed * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
+
+    # Per-kernel durations from HIP events around each kernel on the engine stream,
+    # over the same K steps (positions P..P+K-1 again).
+    eng.set_position(P)
+    prof = eng.profile_steps(timed)
+    per_kernel = {}
+    fam_bytes = fam_ms = 0.0
+    for name, nbytes in KERNEL_BYTES.items():
+        e = prof.get(name)
+        if not e:
+            continue
+        gbps = nbytes / (e["avg_ms"] * 1e-3) / 1e9
+        per_kernel[name] = dict(avg_us=round(e["avg_ms"] * 1e3, 3), calls=e["calls"], bytes=nbytes,
+                                GBps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
+        fam_bytes += nbytes * e["calls"]
+        fam_ms += e["total_ms"]
+    for name in ("baselm.attention", "baselm.embedding", "baselm.output_norm", "baselm.logits"):
+        if name in prof:
+            per_kernel[name] = dict(avg_us=round(prof[name]["avg_ms"] * 1e3, 3), calls=prof[name]["calls"])
+    fam_gbps = fam_bytes / (fam_ms * 1e-3) / 1e9 if fam_ms else 0.0
+    dom = per_kernel["baselm.swiglu"]
+    mean_step_bytes = float(np.mean([step_bytes(p, args.lm_head) for p in range(P, P + K)]))
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_swiglu.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = dict(bound="hbm", achieved=dom["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
+                    frac=dom["frac"], traffic=traffic, kernel="k_swiglu (gate+up Q8_0 matvec)",
+                    bytes_per_launch=dom["bytes"], avg_us=dom["avg_us"])
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, m, eng, tokens, P, args)
+    eng.close()
+    model.free()
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(elapsed * 1e3 / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "baselm_q8_0_decode_28L_batch1", "layers": L, "hidden": H, "ffn": F,
+                   "heads": "16q/2kv x 128", "vocab": V, "prefill": P,
+                   "positions": f"{P}..{P + K - 1}", "lm_head": bool(args.lm_head),
+                   "exec": args.mode, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "matvec_family": {"achieved": round(fam_gbps, 1), "unit": "GB/s",
+                          "frac": round(fam_gbps / HBM_PEAK_GBPS, 4)},
+        "step": {"bytes_mean": int(mean_step_bytes),
+                 "achieved_GBps": round(mean_step_bytes * tok_s / 1e9, 1),
+                 "frac": round(mean_step_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4)},
+        "per_kernel": per_kernel,
+        "cpu_baseline": cpu,
+        "device": f"{info['name']} ({info['arch']})",
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(cfg, m, eng, tokens, P, args):
+    """The oracle's 28-layer decode on the host cores, on a bounded sample."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import voxref
+    o = voxref.BaseLm(m.data, {t.name: t for t in m.tensors}, cfg)
+    # KV cache of the prefill, from the GPU run.
+    o.kv_k[:] = eng.buffer("kv_k").download(np.uint16, o.kv_k.size)
+    o.kv_v[:] = eng.buffer("kv_v").download(np.uint16, o.kv_v.size)
+    t0 = time.perf_counter()
+    o.decode_token(int(tokens[P]), P, logits=args.lm_head)
+    one = time.perf_counter() - t0
+    n = args.cpu_steps if args.cpu_steps > 0 else int(max(2, min(64, 15.0 // max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for i in range(n):
+        o.decode_token(int(tokens[P + 1 + i]), P + 1 + i, logits=args.lm_head)
+    el = time.perf_counter() - t0
+    thr = voxref.threads()
+    log(f"cpu oracle: {n} steps in {el:.2f}s on {thr} threads")
+    return {"value": round(n / el, 3), "unit": "tok/s", "cores": thr, "kind": "port",
+            "sample": f"{n} decode steps at positions {P + 1}..{P + n} of the same 28-layer Q8_0 model "
+                      f"and tokens (KV cache from the GPU prefill), C oracle with OpenMP over rows",
+            "cpu": cpu_model()}
+
+
+def cpu_model():
+    try:
+        for l in open("/proc/cpuinfo"):
+            if l.startswith("model name"):
+                return l.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,483 @@
+/*
+ * voxhip.h — C ABI of the MI355X (gfx950) BaseLM compute library.
+ *
+ * This is the drop-in boundary that replaces VoxGen's Vulkan dispatch layer
+ * (src/vulkan.rs) for the VoxCPM2 BaseLM path. Every per-op entry point takes
+ * the same #[repr(C)] push struct the reference shaders consume (field order and
+ * types identical), plus the buffers the reference binds to that pipeline.
+ * Plain C types only: pointers, sizes, u32/f32 push structs. No torch types.
+ *
+ * Conventions
+ *   - Every function returns vx_status (0 = OK, negative = error) unless noted.
+ *     The message of the last failure on the calling thread is vx_last_error().
+ *     The library never aborts the process.
+ *   - One vx_ctx = one device + one in-order HIP stream. Calls on one context are
+ *     serialised by the caller (the reference holds a per-engine Mutex,
+ *     runtime.rs:168-188). Work is enqueued asynchronously; vx_sync() waits.
+ *     Stream order replaces the reference's buffer barriers (vulkan.rs:691-802),
+ *     which therefore have no counterpart here.
+ *   - Weights live in a vx_model (the uploaded GGUF data region). Ops address a
+ *     weight by its u32 byte offset into that region, exactly as the reference
+ *     push structs do (baselm.rs:1257-1260). The offset must start a tensor of the
+ *     model's table; Q8_0 matrices are repacked on upload for coalesced loads and
+ *     resolved through that table.
+ *   - Ownership: the caller owns every vx_buf / vx_model / vx_baselm it creates and
+ *     frees it with the matching *_free / *_destroy call.
+ */
+#ifndef VOXHIP_H
+#define VOXHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VX_ABI_VERSION 1
+
+/* ------------------------------------------------------------------------- */
+/* Status codes. The conditions mirror the reference's anyhow bails.          */
+/* ------------------------------------------------------------------------- */
+typedef enum vx_status {
+    VX_OK = 0,
+    VX_ERR_INVALID_ARG = -1,   /* null handle, zero size, bad enum            */
+    VX_ERR_HIP = -2,           /* HIP runtime error (message has the hipError) */
+    VX_ERR_OOM = -3,           /* device allocation failed (runtime.rs:265-272) */
+    VX_ERR_SHAPE = -4,         /* shape / dtype mismatch (baselm.rs:1083-1088,1124-1130,1163-1168) */
+    VX_ERR_BOUNDS = -5,        /* a bound buffer is too small for the push extents */
+    VX_ERR_UNSUPPORTED = -6,   /* dtype or geometry this build does not run     */
+    VX_ERR_CONTEXT_FULL = -7,  /* KV cache full (baselm.rs:882-890)             */
+    VX_ERR_TOKEN_RANGE = -8,   /* token id >= vocab (baselm.rs:629-631)         */
+    VX_ERR_GGUF = -9,          /* GGUF magic/version/truncation (gguf.rs:226-228,281-284) */
+    VX_ERR_NOT_FOUND = -10,    /* missing tensor or metadata key                */
+    VX_ERR_OFFSET = -11,       /* data region >= 4 GiB (baselm.rs:468-470)      */
+    VX_ERR_CANCELLED = -12,    /* cancel flag set before a step (runtime.rs:745-808) */
+    VX_ERR_NO_DEVICE = -13,    /* no HIP device / index out of range            */
+    VX_ERR_STATE = -14         /* call not valid in the current state           */
+} vx_status;
+
+/* GGML dtype codes carried in push structs: dtype_code (baselm.rs:1239-1245),
+ * GgmlType::from_raw (gguf.rs:31-33). */
+#define VX_DTYPE_F32 0u
+#define VX_DTYPE_F16 1u
+#define VX_DTYPE_Q8_0 8u
+
+typedef struct vx_ctx vx_ctx;
+typedef struct vx_buf vx_buf;
+typedef struct vx_model vx_model;
+typedef struct vx_graph vx_graph;
+typedef struct vx_baselm vx_baselm;
+typedef struct vx_gguf vx_gguf;
+
+/* ------------------------------------------------------------------------- */
+/* Push structs: identical layout to the reference's #[repr(C)] structs.      */
+/* ------------------------------------------------------------------------- */
+typedef struct vx_embedding_push {  /* EmbeddingPush baselm.rs:287-295 */
+    uint32_t weight_offset, cols, token_id, dtype;
+    float alpha;
+} vx_embedding_push;
+
+typedef struct vx_rms_push {        /* RmsPush baselm.rs:296-302 */
+    uint32_t weight_offset, n;
+    float eps;
+} vx_rms_push;
+
+typedef struct vx_matvec_push {     /* MatvecPush baselm.rs:303-312 */
+    uint32_t weight_offset, rows, cols, dtype, row_base;
+    float alpha;
+} vx_matvec_push;
+
+typedef struct vx_rope_push {       /* RopePush baselm.rs:313-323 */
+    uint32_t factor_offset, position, q_heads, kv_heads, head_dim;
+    float rope_theta, scaling_factor;
+} vx_rope_push;
+
+typedef struct vx_store_kv_push {   /* StoreKvPush baselm.rs:324-331 */
+    uint32_t layer, position, context, kv_dim;
+} vx_store_kv_push;
+
+typedef struct vx_attention_push {  /* AttentionPush baselm.rs:332-341 */
+    uint32_t layer, context, position, head_dim, q_per_kv, kv_heads;
+} vx_attention_push;
+
+typedef struct vx_softmax_push {    /* SoftmaxPush baselm.rs:342-347 */
+    uint32_t context, position;
+} vx_softmax_push;
+
+typedef struct vx_qkv_push {        /* QkvPush baselm.rs:348-361 */
+    uint32_t q_weight_offset, k_weight_offset, v_weight_offset;
+    uint32_t q_rows, kv_rows, cols;
+    uint32_t q_dtype, k_dtype, v_dtype;
+    uint32_t row_base;
+} vx_qkv_push;
+
+typedef struct vx_swiglu_push {     /* SwigluPush baselm.rs:363-372 */
+    uint32_t gate_weight_offset, up_weight_offset, rows, cols, dtype, row_base;
+} vx_swiglu_push;
+
+typedef struct vx_residual_rms_push { /* ResidualRmsPush baselm.rs:373-380 */
+    uint32_t weight_offset, n;
+    float eps, scale;
+} vx_residual_rms_push;
+
+typedef struct vx_linear_bias_push {  /* LinearBiasPush acoustic.rs:237-247 */
+    uint32_t weight_offset, bias_offset, rows, cols, weight_dtype, bias_dtype, row_base;
+    float alpha;
+} vx_linear_bias_push;
+
+typedef struct vx_fusion_push {     /* FusionPush acoustic.rs:257-268 */
+    uint32_t weight_offset, bias_offset, rows, left_cols, right_cols;
+    uint32_t weight_dtype, bias_dtype, row_base;
+} vx_fusion_push;
+
+/* ------------------------------------------------------------------------- */
+/* Context, buffers, streams (replaces VulkanContext, vulkan.rs:96-113).      */
+/* ------------------------------------------------------------------------- */
+int vx_abi_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char *vx_last_error(void);
+
+/* VulkanContext::new (vulkan.rs:284-466): select one device, one queue. */
+int vx_init(int device_index, vx_ctx **out);
+int vx_destroy(vx_ctx *ctx);
+typedef struct vx_device_info {
+    char name[256];
+    char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    uint64_t total_global_mem;
+    uint32_t compute_units;
+    uint32_t wavefront_size;
+    uint32_t l2_cache_bytes;
+    uint32_t lds_bytes_per_block;
+    uint32_t clock_khz;
+    uint32_t memory_clock_khz;
+    uint32_t memory_bus_width;
+} vx_device_info;
+int vx_device_info_get(vx_ctx *ctx, vx_device_info *out);
+
+/* create_buffer (vulkan.rs:488-535) + GpuBuffer Drop (vulkan.rs:87-94). */
+int vx_alloc(vx_ctx *ctx, uint64_t bytes, vx_buf **out);
+int vx_free(vx_ctx *ctx, vx_buf *buf);
+uint64_t vx_buf_size(const vx_buf *buf);
+/* Raw device address, for interop (e.g. wrapping in a framework tensor). */
+void *vx_buf_device_ptr(const vx_buf *buf);
+/* upload_f32 / upload_device_local (vulkan.rs:804-866); synchronous w.r.t. src. */
+int vx_upload(vx_ctx *ctx, vx_buf *dst, uint64_t dst_offset, const void *src, uint64_t bytes);
+/* read_f32 (vulkan.rs:905-955); waits for queued work first. */
+int vx_download(vx_ctx *ctx, const vx_buf *src, uint64_t src_offset, void *dst, uint64_t bytes);
+/* cmd_copy_buffer (baselm.rs:804-813); enqueued on the context stream. */
+int vx_copy(vx_ctx *ctx, vx_buf *dst, uint64_t dst_offset, const vx_buf *src,
+            uint64_t src_offset, uint64_t bytes);
+/* Fill `count` u32 words with `value` using a kernel (safe inside graph capture). */
+int vx_fill_u32(vx_ctx *ctx, vx_buf *dst, uint64_t dst_offset, uint32_t value, uint64_t count);
+/* submit_and_wait (vulkan.rs:637-657): block until the stream drains. */
+int vx_sync(vx_ctx *ctx);
+
+/* Graph capture of enqueued work (replaces recording one command buffer). */
+int vx_graph_begin(vx_ctx *ctx);
+int vx_graph_end(vx_ctx *ctx, vx_graph **out);
+int vx_graph_launch(vx_ctx *ctx, vx_graph *graph);
+int vx_graph_free(vx_ctx *ctx, vx_graph *graph);
+
+/* GPU profiling: gpu_profile_begin/end/snapshot/reset (vulkan.rs:587-635).
+ * When enabled, every op and engine kernel is bracketed by HIP events on the
+ * context stream; totals are collected at vx_sync() and aggregated by name. */
+typedef struct vx_prof_entry {
+    char name[64];
+    double total_ms;
+    uint64_t calls;
+    double avg_ms;
+} vx_prof_entry;
+int vx_prof_enable(vx_ctx *ctx, int enabled);
+int vx_prof_reset(vx_ctx *ctx);
+/* Copies up to `cap` entries; *count receives the number of distinct names. */
+int vx_prof_snapshot(vx_ctx *ctx, vx_prof_entry *out, uint32_t cap, uint32_t *count);
+
+/* ------------------------------------------------------------------------- */
+/* Model data (upload_device_local of the GGUF data region, baselm.rs:472-477)*/
+/* ------------------------------------------------------------------------- */
+typedef struct vx_tensor_info {     /* TensorInfo gguf.rs:51-59 */
+    char name[96];
+    uint32_t ggml_type;             /* VX_DTYPE_* */
+    uint32_t n_dims;
+    uint64_t dims[4];               /* GGUF order: dims[0] is the contiguous axis */
+    uint64_t offset;                /* byte offset into the data region */
+    uint64_t bytes;
+} vx_tensor_info;
+
+/* Upload `bytes` of GGUF data region plus its tensor table. Rank-2 Q8_0 tensors
+ * are additionally repacked on the device into the coalesced layout the matvec
+ * and GEMM kernels read; the original bytes stay resident for bit-exact gathers.
+ * Fails with VX_ERR_OFFSET if the region is >= 4 GiB (u32 push offsets). */
+int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes,
+                    const vx_tensor_info *tensors, uint32_t n_tensors, vx_model **out);
+int vx_model_free(vx_ctx *ctx, vx_model *model);
+uint32_t vx_model_tensor_count(const vx_model *model);
+int vx_model_tensor_at(const vx_model *model, uint32_t index, vx_tensor_info *out);
+/* GgufSummary::tensor (gguf.rs:84-87). */
+int vx_model_find(const vx_model *model, const char *name, vx_tensor_info *out);
+/* Device bytes held by the model (raw region + repacked copies). */
+uint64_t vx_model_device_bytes(const vx_model *model);
+/* Dequantize rows [0,rows) of the weight at `weight_offset` into f32 `out`
+ * (row-major rows x cols) from the same device layout the matvecs read. Pins the
+ * Q8_0 repack: the result must equal d*float(q) (matvec.comp:32-44) bit for bit. */
+int vx_dequant(vx_ctx *ctx, const vx_model *model, uint32_t weight_offset, uint32_t rows,
+               uint32_t cols, uint32_t dtype, vx_buf *out);
+
+/* ------------------------------------------------------------------------- */
+/* Per-op entry points: one per reference pipeline. Each runs the whole       */
+/* dispatch loop of the corresponding host helper (rows row_base..rows), and  */
+/* checks bound buffer sizes against the push extents before launching.       */
+/* ------------------------------------------------------------------------- */
+/* embedding.comp:43-48, dispatch baselm.rs:634-647 */
+int vx_embedding(vx_ctx *ctx, const vx_model *model, vx_buf *hidden, const vx_embedding_push *pc);
+/* Same, token id read from device u32 tokens[position[0]] (graph replay). */
+int vx_embedding_devtok(vx_ctx *ctx, const vx_model *model, vx_buf *hidden, const vx_buf *tokens,
+                        const vx_buf *position, const vx_embedding_push *pc);
+/* rmsnorm.comp:21-42, dispatch_rms baselm.rs:1054-1073 */
+int vx_rmsnorm(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_rms_push *pc);
+/* residual_rmsnorm.comp:23-42, dispatch_residual_rms baselm.rs:1190-1202 */
+int vx_residual_rmsnorm(vx_ctx *ctx, const vx_model *model, vx_buf *hidden, const vx_buf *branch,
+                        vx_buf *y, const vx_residual_rms_push *pc);
+/* matvec.comp:46-62, dispatch_matvec baselm.rs:1115-1153 */
+int vx_matvec(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_matvec_push *pc);
+/* qkv_matvec.comp:53-95, dispatch_qkv baselm.rs:1075-1113 */
+int vx_qkv_matvec(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *q, vx_buf *k,
+                  vx_buf *v, const vx_qkv_push *pc);
+/* matvec_swiglu.comp:44-69, dispatch_swiglu baselm.rs:1155-1188 */
+int vx_matvec_swiglu(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y,
+                     const vx_swiglu_push *pc);
+/* rope.comp:22-51, dispatch baselm.rs:933-953 */
+int vx_rope(vx_ctx *ctx, const vx_model *model, vx_buf *q, vx_buf *k, const vx_rope_push *pc);
+/* Same, position read from device u32 position[0]; pc->position is ignored. */
+int vx_rope_devpos(vx_ctx *ctx, const vx_model *model, vx_buf *q, vx_buf *k, const vx_buf *position,
+                   const vx_rope_push *pc);
+/* store_kv.comp:16-24, dispatch baselm.rs:956-967. k_cache/v_cache are the
+ * packed f16 caches [layer][context][kv_dim]. */
+int vx_store_kv(vx_ctx *ctx, const vx_buf *k, const vx_buf *v, vx_buf *k_cache, vx_buf *v_cache,
+                const vx_store_kv_push *pc);
+int vx_store_kv_devpos(vx_ctx *ctx, const vx_buf *k, const vx_buf *v, vx_buf *k_cache,
+                       vx_buf *v_cache, const vx_buf *position, const vx_store_kv_push *pc);
+/* attn_scores.comp:27-44, dispatch baselm.rs:969-980 (grid (position+1) x q_heads);
+ * q_heads = q_per_kv * kv_heads. scores is f32 [q_heads][context]. */
+int vx_attn_scores(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, vx_buf *scores,
+                   const vx_attention_push *pc);
+int vx_attn_scores_devpos(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, vx_buf *scores,
+                          const vx_buf *position, const vx_attention_push *pc);
+/* softmax.comp:15-47, dispatch baselm.rs:982-991 (grid = heads). */
+int vx_softmax(vx_ctx *ctx, vx_buf *scores, uint32_t heads, const vx_softmax_push *pc);
+int vx_softmax_devpos(vx_ctx *ctx, vx_buf *scores, uint32_t heads, const vx_buf *position,
+                      const vx_softmax_push *pc);
+/* attn_values.comp:25-37, dispatch baselm.rs:993-996 (grid = q heads). */
+int vx_attn_values(vx_ctx *ctx, const vx_buf *scores, const vx_buf *v_cache, vx_buf *out,
+                   const vx_attention_push *pc);
+int vx_attn_values_devpos(vx_ctx *ctx, const vx_buf *scores, const vx_buf *v_cache, vx_buf *out,
+                          const vx_buf *position, const vx_attention_push *pc);
+/* linear_bias.comp:63-82, dispatch acoustic.rs:1130-1161 */
+int vx_linear_bias(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y,
+                   const vx_linear_bias_push *pc);
+/* fusion_linear.comp:56-78, dispatch acoustic.rs:941-966 (two identical outputs). */
+int vx_fusion_linear(vx_ctx *ctx, const vx_model *model, const vx_buf *left, const vx_buf *right,
+                     vx_buf *y, vx_buf *snapshot, const vx_fusion_push *pc);
+
+/* ------------------------------------------------------------------------- */
+/* Fused decode kernels used by the engine's graph (no single reference       */
+/* pipeline: each is the composition of the reference ops named).            */
+/* All read the decode position from device u32 position[0].                  */
+/* ------------------------------------------------------------------------- */
+typedef struct vx_fused_qkv_args {
+    uint32_t norm_offset;           /* attn_norm weight (f32), rmsnorm.comp */
+    float eps;
+    uint32_t q_weight_offset, k_weight_offset, v_weight_offset;
+    uint32_t q_rows, kv_rows, cols; /* q_rows = q_heads*head_dim, kv_rows = kv_heads*head_dim */
+    uint32_t dtype;                 /* shared by q/k/v: VX_DTYPE_Q8_0 or VX_DTYPE_F16 */
+    uint32_t factor_offset;         /* LongRoPE ext factors (f32[head_dim/2]) */
+    uint32_t head_dim;
+    float rope_theta, scaling_factor;
+    uint32_t layer, context;
+} vx_fused_qkv_args;
+/* rmsnorm(hidden)*w -> qkv_matvec -> rope -> store_kv, one launch.
+ * (rmsnorm.comp + qkv_matvec.comp + rope.comp + store_kv.comp; baselm.rs:915-967) */
+int vx_fused_qkv_rope_store(vx_ctx *ctx, const vx_model *model, const vx_buf *hidden, vx_buf *q,
+                            vx_buf *k, vx_buf *v, vx_buf *k_cache, vx_buf *v_cache,
+                            const vx_buf *position, const vx_fused_qkv_args *a);
+
+typedef struct vx_fused_attn_args {
+    uint32_t layer, context, head_dim, q_heads, kv_heads;
+    uint32_t splits;                /* context splits per kv head (grid = splits x kv_heads) */
+} vx_fused_attn_args;
+/* Split-context single-query attention with an in-kernel combine:
+ * attn_scores.comp + softmax.comp + attn_values.comp (baselm.rs:969-996).
+ * `scratch` must hold vx_fused_attention_scratch_bytes(a) bytes and its first
+ * kv_heads u32 words must be zero before the first call (kernels restore it). */
+uint64_t vx_fused_attention_scratch_bytes(const vx_fused_attn_args *a);
+int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, const vx_buf *v_cache,
+                       vx_buf *out, vx_buf *scratch, const vx_buf *position,
+                       const vx_fused_attn_args *a);
+
+typedef struct vx_fused_residual_args {
+    uint32_t weight_offset, rows, cols, dtype;
+    float scale;                    /* residual_scale (effective) */
+} vx_fused_residual_args;
+/* hidden += scale * (W . x): matvec.comp then the residual half of
+ * residual_rmsnorm.comp (baselm.rs:998-1011,1022-1037). `branch`, if not NULL,
+ * receives W . x. */
+int vx_fused_matvec_residual(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *hidden,
+                             vx_buf *branch, const vx_fused_residual_args *a);
+
+typedef struct vx_fused_swiglu_args {
+    uint32_t norm_offset;           /* ffn_norm weight (f32) */
+    float eps;
+    uint32_t gate_weight_offset, up_weight_offset, rows, cols, dtype;
+} vx_fused_swiglu_args;
+/* rmsnorm(hidden)*w -> matvec_swiglu (rmsnorm half of residual_rmsnorm.comp +
+ * matvec_swiglu.comp; baselm.rs:1007-1021). */
+int vx_fused_rms_swiglu(vx_ctx *ctx, const vx_model *model, const vx_buf *hidden, vx_buf *y,
+                        const vx_fused_swiglu_args *a);
+
+/* ------------------------------------------------------------------------- */
+/* GGUF (gguf.rs:222-286): host-side parse of a model file.                   */
+/* ------------------------------------------------------------------------- */
+int vx_gguf_open(const char *path, vx_gguf **out);
+int vx_gguf_close(vx_gguf *g);
+typedef struct vx_gguf_summary {    /* GgufSummary gguf.rs:61-81 (scalar part) */
+    uint32_t version;
+    uint64_t tensor_count, metadata_count, alignment, data_offset, file_bytes, tensor_bytes;
+} vx_gguf_summary;
+int vx_gguf_summary_get(const vx_gguf *g, vx_gguf_summary *out);
+int vx_gguf_tensor_at(const vx_gguf *g, uint32_t index, vx_tensor_info *out);
+int vx_gguf_find(const vx_gguf *g, const char *name, vx_tensor_info *out);
+/* Metadata value rendered as text, as GgufSummary::metadata stores it. */
+int vx_gguf_meta(const vx_gguf *g, const char *key, char *out, uint32_t cap);
+/* GgufSummary::primary_base_format (gguf.rs:117-133): 8 = Q8_0, 1 = F16. */
+int vx_gguf_primary_format(const vx_gguf *g, uint32_t *dtype_out);
+/* Upload the file's data region and tensor table as a vx_model. */
+int vx_model_upload_gguf(vx_ctx *ctx, const vx_gguf *g, vx_model **out);
+
+/* ------------------------------------------------------------------------- */
+/* BaseLM engine (BaseLmEngine, baselm.rs:423-890).                           */
+/* ------------------------------------------------------------------------- */
+typedef struct vx_baselm_config {   /* BaseLmConfig baselm.rs:34-56 */
+    uint32_t context_length;
+    uint32_t active_context_length;
+    uint32_t embedding_length;
+    uint32_t block_count;
+    uint32_t feed_forward_length;
+    uint32_t vocab_size;
+    uint32_t head_count;
+    uint32_t head_count_kv;
+    uint32_t head_dim;
+    uint32_t kv_dim;
+    float rms_epsilon;
+    float rope_theta;
+    uint32_t rope_dimension_count;
+    uint32_t rope_original_context_length;
+    uint32_t rope_longrope;         /* 1: rope_scaling_type == "longrope", 0: "none" */
+    float embedding_scale;
+    float residual_scale;
+    float logit_scale;
+    uint32_t tied_output;
+} vx_baselm_config;
+
+/* BaseLmConfig::from_gguf (baselm.rs:60-180), including every geometry check. */
+int vx_baselm_config_from_gguf(const vx_gguf *g, uint32_t active_context_length,
+                               vx_baselm_config *out);
+/* BaseLmConfig::rope_scaling_factor (baselm.rs:194-205). */
+float vx_baselm_rope_scaling_factor(const vx_baselm_config *cfg);
+/* BaseLmConfig::kv_cache_bytes / per_cache_bytes (baselm.rs:182-192). */
+uint64_t vx_baselm_kv_cache_bytes(const vx_baselm_config *cfg);
+
+/* Execution modes of the engine. */
+#define VX_EXEC_GRAPH 0u     /* fused kernels, each step replayed as one hipGraph */
+#define VX_EXEC_FUSED 1u     /* fused kernels launched eagerly                   */
+#define VX_EXEC_REFERENCE 2u /* the reference's 11 per-op dispatches per layer   */
+
+typedef struct vx_baselm_options {
+    uint32_t exec_mode;          /* VX_EXEC_* */
+    uint32_t strict_geometry;    /* 1: enforce the VoxCPM2 geometry (baselm.rs:102-113);
+                                    0: allow other layer counts/sizes for harnesses */
+    uint32_t attn_splits;        /* 0 = choose from active_context_length */
+} vx_baselm_options;
+
+/* BaseLmEngine::new (baselm.rs:451-586). Validates every tensor of the model
+ * against the config (validate_layer baselm.rs:227-262) and allocates the
+ * activation buffers and the packed f16 KV caches. */
+int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config *cfg,
+                     const vx_baselm_options *opt, vx_baselm **out);
+int vx_baselm_destroy(vx_baselm *eng);
+/* reset (baselm.rs:616-620): position := 0, cache contents left in place. */
+int vx_baselm_reset(vx_baselm *eng);
+uint32_t vx_baselm_position(const vx_baselm *eng);
+/* Harness hook: set the next decode position (e.g. after filling the cache). */
+int vx_baselm_set_position(vx_baselm *eng, uint32_t position);
+
+typedef struct vx_top_logit {       /* TopLogit baselm.rs:398-402 */
+    uint32_t token_id;
+    float logit;
+} vx_top_logit;
+typedef struct vx_step_result {     /* BaseLmStepResult baselm.rs:404-411 */
+    uint32_t position;
+    double elapsed_ms;
+    double final_hidden_checksum;
+    double final_hidden_l2;
+    uint32_t n_top;                 /* entries written to the caller's top array */
+} vx_step_result;
+
+/* top_k_logits (baselm.rs:1296-1311): finite logits sorted descending (ties by
+ * ascending id), first min(k, finite count) written to out. Host-only. */
+int vx_top_k_logits(const float *logits, uint32_t n, uint32_t k, vx_top_logit *out, uint32_t *n_out);
+
+/* decode_token (baselm.rs:622-655): embedding + layers + LM head, then
+ * readback of the final hidden state and the top_k logits into `top`
+ * (caller array of top_k entries; may be NULL when top_k == 0). */
+int vx_baselm_decode_token(vx_baselm *eng, uint32_t token_id, uint32_t top_k,
+                           vx_step_result *res, vx_top_logit *top);
+/* decode_embedding (baselm.rs:657-680): host f32[embedding_length] input. */
+int vx_baselm_decode_embedding(vx_baselm *eng, const float *embedding, uint32_t n, uint32_t top_k,
+                               vx_step_result *res, vx_top_logit *top);
+/* decode_token_gpu_only (baselm.rs:689-721): no LM head, no readback. */
+int vx_baselm_decode_token_gpu_only(vx_baselm *eng, uint32_t token_id, uint32_t *position_out);
+/* decode_embedding_gpu_only (baselm.rs:764-791). */
+int vx_baselm_decode_embedding_gpu_only(vx_baselm *eng, const float *embedding, uint32_t n,
+                                        uint32_t *position_out);
+/* decode_embedding_from_gpu_only (baselm.rs:793-821): device f32 source. */
+int vx_baselm_decode_embedding_from_gpu_only(vx_baselm *eng, const vx_buf *source,
+                                             uint32_t *position_out);
+/* Token-only steps for n tokens enqueued back to back without host waits
+ * (the batching record_token_gpu_only_in provides, baselm.rs:726-762). */
+int vx_baselm_decode_tokens_gpu_only(vx_baselm *eng, const uint32_t *tokens, uint32_t n);
+/* prefill_tokens (baselm.rs:823-839): sequential decode of every token. */
+int vx_baselm_prefill_tokens(vx_baselm *eng, const uint32_t *tokens, uint32_t n, uint32_t top_k_last,
+                             vx_step_result *res, vx_top_logit *top);
+typedef struct vx_baselm_benchmark_result { /* BaseLmBenchmark baselm.rs:413-421 */
+    uint32_t iterations, token_id;
+    double mean_ms, min_ms, max_ms, tokens_per_second;
+} vx_baselm_benchmark_result;
+/* benchmark (baselm.rs:841-880). */
+int vx_baselm_benchmark(vx_baselm *eng, uint32_t token_id, uint32_t warmup, uint32_t iterations,
+                        vx_baselm_benchmark_result *out);
+/* Engine-owned buffers: output_buffer (norm, baselm.rs:608-612) and the rest. */
+#define VX_BASELM_BUF_HIDDEN 0u
+#define VX_BASELM_BUF_NORM 1u
+#define VX_BASELM_BUF_Q 2u
+#define VX_BASELM_BUF_K 3u
+#define VX_BASELM_BUF_V 4u
+#define VX_BASELM_BUF_ATTENTION 5u
+#define VX_BASELM_BUF_GATE 6u
+#define VX_BASELM_BUF_BRANCH 7u
+#define VX_BASELM_BUF_LOGITS 8u
+#define VX_BASELM_BUF_SCORES 9u
+#define VX_BASELM_BUF_KV_K 10u
+#define VX_BASELM_BUF_KV_V 11u
+#define VX_BASELM_BUF_POSITION 12u
+vx_buf *vx_baselm_buffer(vx_baselm *eng, uint32_t which);
+/* Per-kernel timing of `n` token-only steps, each kernel bracketed by HIP events
+ * on the engine stream (mirrors the reference's "baselm.*" profile spans).
+ * Fills up to `cap` entries; *count receives the number of kernel names. */
+int vx_baselm_profile_steps(vx_baselm *eng, const uint32_t *tokens, uint32_t n,
+                            vx_prof_entry *out, uint32_t cap, uint32_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VOXHIP_H */

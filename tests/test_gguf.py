@@ -1,0 +1,172 @@
+"""GGUF parsing and BaseLmConfig::from_gguf through the C ABI (host only, no GPU).
+
+Files are written by voxgen_amd.gguf; full-geometry models use a sparse data
+region so the 28-layer table can be validated without 1.7 GB of disk.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+from voxgen_amd import abi, gguf, synth
+from voxgen_amd.gguf import Gguf
+
+
+def full_model(tmp_path, mutate=None, cfg_over=None, drop=None, meta_over=None, version=3):
+    cfg = synth.baselm_config(context_length=32768, **(cfg_over or {}))
+    m = synth.build_baselm(cfg, with_data=False)
+    tensors = [t for t in m.tensors if t.name != drop]
+    if mutate:
+        tensors = [mutate(t) for t in tensors]
+    meta = dict(m.metadata)
+    meta.update(meta_over or {})
+    size = max(t.offset + t.nbytes for t in tensors)
+    return gguf.write(tmp_path / "m.gguf", meta, tensors, None, data_bytes=size, version=version)
+
+
+def test_summary_and_tensor_table(tmp_path):
+    cfg = synth.baselm_config(layers=2, hidden=256, ffn=512, vocab=64, q_heads=2, kv_heads=1)
+    m = synth.build_baselm(cfg, seed=5)
+    meta = dict(m.metadata)
+    meta["tokenizer.ggml.tokens"] = (9, (8, ["a", "b", "c"]))
+    meta["general.name"] = (8, "x" * 600)  # over 512 chars: dropped like gguf.rs:240
+    p = gguf.write(tmp_path / "s.gguf", meta, m.tensors, m.data)
+    g = Gguf(p)
+    s = g.summary()
+    assert s["version"] == 3 and s["tensor_count"] == len(m.tensors)
+    assert s["metadata_count"] == len(meta) and s["alignment"] == 32
+    assert s["data_offset"] % 32 == 0 and s["file_bytes"] == p.stat().st_size
+    assert s["tensor_bytes"] == sum(t.nbytes for t in m.tensors)
+    got = {t.name: t for t in g.tensors()}
+    for t in m.tensors:
+        assert got[t.name].dims == t.dims and got[t.name].offset == t.offset
+        assert got[t.name].ggml_type == t.ggml_type and got[t.name].nbytes == t.nbytes
+    assert g.meta("general.architecture") == "minicpm4"
+    assert g.meta("minicpm4.block_count") == "2"
+    with pytest.raises(abi.VxError) as e:
+        g.meta("general.name")
+    assert e.value.name == "VX_ERR_NOT_FOUND"
+    assert g.primary_format() == abi.DTYPE_Q8_0
+    # Data region bytes are where the table says.
+    raw = p.read_bytes()
+    t = m.tensor("blk.1.ffn_down.weight")
+    a = s["data_offset"] + t.offset
+    assert raw[a:a + t.nbytes] == m.data[t.offset:t.offset + t.nbytes].tobytes()
+
+
+def test_config_from_full_geometry_gguf(tmp_path):
+    g = Gguf(full_model(tmp_path))
+    c = g.baselm_config(8192)
+    assert (c["embedding_length"], c["block_count"], c["feed_forward_length"]) == (2048, 28, 6144)
+    assert (c["head_count"], c["head_count_kv"], c["head_dim"], c["kv_dim"]) == (16, 2, 128, 256)
+    assert c["vocab_size"] == 73448 and c["tied_output"] == 1 and c["rope_longrope"] == 1
+    assert c["active_context_length"] == 8192 and c["context_length"] == 32768
+    assert abs(c["rms_epsilon"] - 1e-6) < 1e-12 and c["rope_theta"] == 10000.0
+    assert c["embedding_scale"] == 0.0 and c["residual_scale"] == 0.0
+
+
+@pytest.mark.parametrize("case,code", [
+    ("active0", "VX_ERR_INVALID_ARG"),
+    ("active_big", "VX_ERR_INVALID_ARG"),
+    ("layers27", "VX_ERR_UNSUPPORTED"),
+    ("arch", "VX_ERR_UNSUPPORTED"),
+    ("scaling", "VX_ERR_UNSUPPORTED"),
+    ("missing_tensor", "VX_ERR_NOT_FOUND"),
+    ("bad_dims", "VX_ERR_SHAPE"),
+    ("norm_f16", "VX_ERR_SHAPE"),
+    ("missing_meta", "VX_ERR_NOT_FOUND"),
+])
+def test_config_validation_errors(tmp_path, case, code):
+    active = 8192
+    kw = {}
+    if case == "active0":
+        active = 0
+    elif case == "active_big":
+        active = 40000
+    elif case == "layers27":
+        kw["meta_over"] = {"minicpm4.block_count": (4, 27)}
+    elif case == "arch":
+        kw["meta_over"] = {"general.architecture": (8, "llama")}
+    elif case == "scaling":
+        kw["meta_over"] = {"minicpm4.rope.scaling.type": (8, "yarn")}
+    elif case == "missing_tensor":
+        kw["drop"] = "blk.13.ffn_up.weight"
+    elif case == "bad_dims":
+        def mutate(t):
+            if t.name == "blk.3.attn_k.weight":
+                t = synth.TensorDesc(t.name, t.ggml_type, (2048, 512), t.offset)
+            return t
+        kw["mutate"] = mutate
+    elif case == "norm_f16":
+        def mutate(t):
+            if t.name == "blk.0.attn_norm.weight":
+                t = synth.TensorDesc(t.name, abi.DTYPE_F16, t.dims, t.offset)
+            return t
+        kw["mutate"] = mutate
+    elif case == "missing_meta":
+        path = full_model(tmp_path)
+        m = synth.build_baselm(synth.baselm_config(context_length=32768), with_data=False)
+        meta = dict(m.metadata)
+        del meta["minicpm4.feed_forward_length"]
+        size = max(t.offset + t.nbytes for t in m.tensors)
+        path = gguf.write(tmp_path / "n.gguf", meta, m.tensors, None, data_bytes=size)
+        with pytest.raises(abi.VxError) as e:
+            Gguf(path).baselm_config(active)
+        assert e.value.name == code
+        return
+    with pytest.raises(abi.VxError) as e:
+        Gguf(full_model(tmp_path, **kw)).baselm_config(active)
+    assert e.value.name == code
+
+
+def test_head_dim_falls_back_to_rope_dimension_count(tmp_path):
+    m = synth.build_baselm(synth.baselm_config(context_length=32768), with_data=False)
+    meta = dict(m.metadata)
+    del meta["minicpm4.attention.key_length"]
+    size = max(t.offset + t.nbytes for t in m.tensors)
+    p = gguf.write(tmp_path / "k.gguf", meta, m.tensors, None, data_bytes=size)
+    assert Gguf(p).baselm_config(4096)["head_dim"] == 128
+
+
+def test_rope_original_context_and_long_factor_scaling(tmp_path):
+    p = full_model(tmp_path, meta_over={"minicpm4.rope.scaling.original_context_length": (4, 4096)})
+    c = Gguf(p).baselm_config(8192)
+    assert c["rope_original_context_length"] == 4096
+
+
+@pytest.mark.parametrize("how", ["magic", "version1", "version4", "truncated_header", "tensor_past_eof",
+                                 "bad_type", "rank0", "q8_not_div32"])
+def test_parse_errors(tmp_path, how):
+    cfg = synth.baselm_config(layers=1, hidden=256, ffn=512, vocab=64, q_heads=2, kv_heads=1)
+    m = synth.build_baselm(cfg, seed=1)
+    tensors, data, version = list(m.tensors), m.data, 3
+    if how == "version1":
+        version = 1
+    if how == "version4":
+        version = 4
+    if how == "bad_type":
+        tensors[0] = synth.TensorDesc(tensors[0].name, 2, tensors[0].dims, tensors[0].offset, 64)
+    if how == "rank0":
+        tensors[1] = synth.TensorDesc(tensors[1].name, 0, (), tensors[1].offset, 4)
+    if how == "q8_not_div32":
+        t = tensors[-1]
+        tensors[-1] = synth.TensorDesc(t.name, 8, (40, 2), t.offset, 102)
+    p = gguf.write(tmp_path / "e.gguf", m.metadata, tensors, data, version=version)
+    raw = bytearray(p.read_bytes())
+    if how == "magic":
+        raw[0:4] = b"GGUX"
+    if how == "truncated_header":
+        raw = raw[:40]
+    if how == "tensor_past_eof":
+        raw = raw[:-4096]
+    p.write_bytes(bytes(raw))
+    with pytest.raises(abi.VxError) as e:
+        Gguf(p)
+    assert e.value.name == "VX_ERR_GGUF"
+
+
+def test_writer_layout_is_gguf_v3():
+    hdr = gguf.header_bytes({"a": (4, 7)}, [synth.TensorDesc("t", 0, (3,), 0)])
+    magic, ver, nt, nm = struct.unpack_from("<IIQQ", hdr)
+    assert (magic, ver, nt, nm) == (0x46554747, 3, 1, 1)
+    assert len(hdr) % 32 == 0

@@ -1,0 +1,430 @@
+"""Per-op parity of the HIP kernels against the CPU oracle, through the C ABI.
+
+Bit-exact: Q8_0/F16 dequant, embedding gathers, KV-cache placement.
+Float ops: rel-L2 <= 1e-3 against the oracle on identical seeded inputs.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import voxref
+from conftest import rel_l2
+from voxgen_amd import abi, synth
+from voxgen_amd.runtime import Model
+from voxgen_amd.synth import Region
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+RNG = np.random.default_rng(20251201)
+
+SPECS = {  # name: (dtype, GGUF dims [cols, rows])
+    "wq": (8, (2048, 2048)), "wk": (8, (2048, 256)), "wv": (8, (2048, 256)),
+    "wo": (8, (2048, 2048)), "wg": (8, (2048, 6144)), "wu": (8, (2048, 6144)),
+    "wd": (8, (6144, 2048)), "f16_out": (1, (2048, 5000)), "f16_sq": (1, (2048, 2048)),
+    "f16_g": (1, (2048, 512)), "f16_u": (1, (2048, 512)),
+    "q8_odd": (8, (96, 37)), "q8_wide": (8, (10240, 8)), "q8_1k": (8, (1024, 100)),
+    "f16_odd": (1, (40, 13)), "f16_ragged": (1, (36, 5)), "f32_w": (0, (128, 64)),
+    "fus": (1, (4096, 2048)), "fus_q8": (8, (4096, 256)),
+    "n1": (0, (2048,)), "n2": (0, (2048,)), "b32": (0, (6144,)), "b16": (1, (6144,)),
+    "factors": (0, (64,)), "factors64": (0, (32,)), "emb_f16": (1, (2048, 300)), "emb_q8": (8, (2048, 300)),
+}
+
+
+@pytest.fixture(scope="module")
+def ops(ctx):
+    reg = Region()
+    ts = {k: reg.add(k, dt, dims) for k, (dt, dims) in SPECS.items()}
+    data = np.zeros((reg.size + 255) // 256 * 256, np.uint8)
+    for i, (k, t) in enumerate(ts.items()):
+        n = int(np.prod(t.dims))
+        s = 0x5EED0000 + i
+        if t.ggml_type == 8:
+            data[t.offset:t.offset + t.nbytes] = synth.q8_0_blocks(n // 32, s)
+        elif t.ggml_type == 1:
+            data[t.offset:t.offset + t.nbytes] = synth.normal_f16(n, s, 0.0, 0.05).view(np.uint8)
+        else:
+            data[t.offset:t.offset + t.nbytes] = synth.normal_f32(n, s, 1.0, 0.02).view(np.uint8)
+    for name in ("factors", "factors64"):
+        t = ts[name]
+        data[t.offset:t.offset + t.nbytes].view(np.float32)[:] = 1.0 + np.arange(t.dims[0]) / 16.0
+    model = Model(ctx, data, ts.values())
+    yield data, ts, model
+    model.free()
+
+
+def run(ctx, fn, *args):
+    abi.call(fn, ctx.handle, *args)
+
+
+def buf(ctx, arr):
+    return ctx.array(np.ascontiguousarray(arr))
+
+
+def out(ctx, n, dtype=np.float32):
+    return ctx.zeros(max(n * np.dtype(dtype).itemsize, 4))
+
+
+def H(b):
+    return b.handle
+
+
+# ---------------------------------------------------------------- dequant
+@pytest.mark.parametrize("name", ["wq", "wk", "wd", "q8_odd", "q8_wide", "q8_1k", "f16_sq", "f16_odd", "f32_w"])
+def test_dequant_bit_exact(ctx, ops, name):
+    data, ts, model = ops
+    t = ts[name]
+    cols, rows = t.dims
+    o = out(ctx, rows * cols)
+    run(ctx, "vx_dequant", model.handle, t.offset, rows, cols, t.ggml_type, H(o))
+    got = o.download(np.float32, rows * cols).reshape(rows, cols)
+    want = voxref.dequant(data, t.offset, t.ggml_type, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- matvec
+@pytest.mark.parametrize("name,alpha,row_base", [
+    ("wq", 1.0, 0), ("wk", 1.0, 0), ("wd", 1.0, 0), ("wo", 0.5, 100), ("f16_out", 0.125, 0),
+    ("f16_sq", 1.0, 0), ("q8_odd", 1.0, 0), ("q8_wide", 2.0, 0), ("q8_1k", 1.0, 3), ("f16_odd", 1.0, 0),
+    ("f16_ragged", 1.0, 0), ("wg", 1.0, 6000)])
+def test_matvec(ctx, ops, name, alpha, row_base):
+    data, ts, model = ops
+    t = ts[name]
+    cols, rows = t.dims
+    x = RNG.standard_normal(cols).astype(np.float32)
+    p = abi.MatvecPush(t.offset, rows, cols, t.ggml_type, row_base, alpha)
+    y0 = np.full(rows, -3.0, np.float32)
+    xb, yb = buf(ctx, x), buf(ctx, y0)
+    run(ctx, "vx_matvec", model.handle, H(xb), H(yb), C.byref(p))
+    got = yb.download(np.float32, rows)
+    want = voxref.matvec(data, x, p, y=y0.copy())
+    assert np.all(got[:row_base] == -3.0)
+    assert rel_l2(got[row_base:], want[row_base:]) < TOL
+
+
+def test_matvec_c0_shape_is_f32_accurate(ctx, ops):
+    """The 2048x2048 Q8_0 matvec (benchmark config 0) against float64."""
+    data, ts, model = ops
+    t = ts["wq"]
+    x = synth.normal_f32(2048, 0x5EED0000)
+    p = abi.MatvecPush(t.offset, 2048, 2048, 8, 0, 1.0)
+    xb, yb = buf(ctx, x), out(ctx, 2048)
+    run(ctx, "vx_matvec", model.handle, H(xb), H(yb), C.byref(p))
+    W = voxref.dequant(data, t.offset, 8, 2048, 2048).astype(np.float64)
+    assert rel_l2(yb.download(np.float32, 2048), W @ x.astype(np.float64)) < 1e-5
+
+
+@pytest.mark.parametrize("row_base", [0, 2100, 2400])
+def test_qkv_matvec(ctx, ops, row_base):
+    data, ts, model = ops
+    x = RNG.standard_normal(2048).astype(np.float32)
+    p = abi.QkvPush(ts["wq"].offset, ts["wk"].offset, ts["wv"].offset, 2048, 256, 2048, 8, 8, 8, row_base)
+    xb = buf(ctx, x)
+    qb, kb, vb = (buf(ctx, np.full(n, 9.0, np.float32)) for n in (2048, 256, 256))
+    run(ctx, "vx_qkv_matvec", model.handle, H(xb), H(qb), H(kb), H(vb), C.byref(p))
+    q, k, v = voxref.qkv_matvec(data, x, p)
+    got = np.concatenate([qb.download(np.float32, 2048), kb.download(np.float32, 256), vb.download(np.float32, 256)])
+    want = np.concatenate([q, k, v])
+    assert np.all(got[:row_base] == 9.0)
+    assert rel_l2(got[row_base:], want[row_base:]) < TOL
+
+
+@pytest.mark.parametrize("g,u,rows", [("wg", "wu", 6144), ("f16_g", "f16_u", 512)])
+def test_matvec_swiglu(ctx, ops, g, u, rows):
+    data, ts, model = ops
+    dt = ts[g].ggml_type
+    x = (RNG.standard_normal(2048) * 0.03).astype(np.float32)
+    p = abi.SwigluPush(ts[g].offset, ts[u].offset, rows, 2048, dt, 0)
+    xb, yb = buf(ctx, x), out(ctx, rows)
+    run(ctx, "vx_matvec_swiglu", model.handle, H(xb), H(yb), C.byref(p))
+    assert rel_l2(yb.download(np.float32, rows), voxref.matvec_swiglu(data, x, p)) < TOL
+
+
+# ------------------------------------------------------------------ norms
+def test_rmsnorm_and_residual(ctx, ops):
+    data, ts, model = ops
+    x = (RNG.standard_normal(2048) * 30).astype(np.float32)
+    b = (RNG.standard_normal(2048) * 1000).astype(np.float32)
+    p = abi.RmsPush(ts["n1"].offset, 2048, 1e-6)
+    xb, yb = buf(ctx, x), out(ctx, 2048)
+    run(ctx, "vx_rmsnorm", model.handle, H(xb), H(yb), C.byref(p))
+    assert rel_l2(yb.download(np.float32, 2048), voxref.rmsnorm(data, x, p)) < 1e-5
+    rp = abi.ResidualRmsPush(ts["n2"].offset, 2048, 1e-6, 0.7)
+    hb, bb, y2 = buf(ctx, x), buf(ctx, b), out(ctx, 2048)
+    run(ctx, "vx_residual_rmsnorm", model.handle, H(hb), H(bb), H(y2), C.byref(rp))
+    h_want, y_want = voxref.residual_rmsnorm(data, x, b, rp)
+    assert rel_l2(hb.download(np.float32, 2048), h_want) < 1e-6
+    assert rel_l2(y2.download(np.float32, 2048), y_want) < 1e-5
+
+
+# ------------------------------------------------------------------- rope
+@pytest.mark.parametrize("pos,hd", [(0, 128), (513, 128), (8191, 128), (77, 64)])
+def test_rope(ctx, ops, pos, hd):
+    data, ts, model = ops
+    fac = ts["factors"] if hd == 128 else ts["factors64"]
+    qh, kh = 16, 2
+    q = (RNG.standard_normal(qh * hd) * 30).astype(np.float32)
+    k = (RNG.standard_normal(kh * hd) * 30).astype(np.float32)
+    p = abi.RopePush(fac.offset, pos, qh, kh, hd, 10000.0, 1.0)
+    qw, kw = voxref.rope(data, q, k, p)
+    for devpos in (False, True):
+        qb, kb = buf(ctx, q), buf(ctx, k)
+        if devpos:
+            pb = buf(ctx, np.array([pos, 0, 0, 0], np.uint32))
+            p2 = abi.RopePush(fac.offset, 12345, qh, kh, hd, 10000.0, 1.0)
+            run(ctx, "vx_rope_devpos", model.handle, H(qb), H(kb), H(pb), C.byref(p2))
+        else:
+            run(ctx, "vx_rope", model.handle, H(qb), H(kb), C.byref(p))
+        # At position 8191 the f32 angle pos*inv_freq/ext reaches ~8e3 rad, where the
+        # device and host libm cos/sin/pow differ by a few ulp: 1e-4, still 10x under
+        # the 1e-3 per-op bar.
+        tol = 1e-5 if pos < 4096 else 1e-4
+        assert rel_l2(qb.download(np.float32, qh * hd), qw) < tol
+        assert rel_l2(kb.download(np.float32, kh * hd), kw) < tol
+
+
+# ----------------------------------------------------------- KV placement
+@pytest.mark.parametrize("devpos", [False, True])
+def test_store_kv_bit_exact(ctx, devpos):
+    L, ctxlen, kv = 3, 64, 256
+    k = (RNG.standard_normal(kv) * 300).astype(np.float32)
+    v = RNG.standard_normal(kv).astype(np.float32)
+    kc0 = synth.normal_f16(L * ctxlen * kv, 5).view(np.uint16).copy()
+    vc0 = synth.normal_f16(L * ctxlen * kv, 6).view(np.uint16).copy()
+    kcw, vcw = kc0.copy(), vc0.copy()
+    p = abi.StoreKvPush(2, 37, ctxlen, kv)
+    voxref.store_kv(k, v, kcw, vcw, p)
+    kb, vb, kcb, vcb = buf(ctx, k), buf(ctx, v), buf(ctx, kc0), buf(ctx, vc0)
+    if devpos:
+        pb = buf(ctx, np.array([37], np.uint32))
+        run(ctx, "vx_store_kv_devpos", H(kb), H(vb), H(kcb), H(vcb), H(pb), C.byref(abi.StoreKvPush(2, 0, ctxlen, kv)))
+    else:
+        run(ctx, "vx_store_kv", H(kb), H(vb), H(kcb), H(vcb), C.byref(p))
+    assert np.array_equal(kcb.download(np.uint16, kc0.size), kcw)
+    assert np.array_equal(vcb.download(np.uint16, vc0.size), vcw)
+
+
+# -------------------------------------------------------------- attention
+def attn_inputs(L, ctxlen, hd, kvh, qh, seed):
+    kc = synth.normal_f16(L * ctxlen * kvh * hd, seed).view(np.uint16).copy()
+    vc = synth.normal_f16(L * ctxlen * kvh * hd, seed + 1).view(np.uint16).copy()
+    q = (synth.normal_f32(qh * hd, seed + 2) * 0.5).astype(np.float32)
+    return kc, vc, q
+
+
+@pytest.mark.parametrize("pos", [0, 1, 512])
+def test_attention_three_ops(ctx, pos):
+    L, ctxlen, hd, kvh, qpk = 2, 1024, 128, 2, 8
+    qh = kvh * qpk
+    kc, vc, q = attn_inputs(L, ctxlen, hd, kvh, qh, 40 + pos)
+    ap = abi.AttentionPush(1, ctxlen, pos, hd, qpk, kvh)
+    s_w = voxref.attn_scores(q, kc, qh, ap)
+    p_w = voxref.softmax(s_w, qh, abi.SoftmaxPush(ctxlen, pos))
+    o_w = voxref.attn_values(p_w, vc, qh, ap)
+    for devpos in (False, True):
+        qb, kcb, vcb = buf(ctx, q), buf(ctx, kc), buf(ctx, vc)
+        sb, ob = out(ctx, qh * ctxlen), out(ctx, qh * hd)
+        if devpos:
+            pb = buf(ctx, np.array([pos], np.uint32))
+            ap2 = abi.AttentionPush(1, ctxlen, 0, hd, qpk, kvh)
+            run(ctx, "vx_attn_scores_devpos", H(qb), H(kcb), H(sb), H(pb), C.byref(ap2))
+            run(ctx, "vx_softmax_devpos", H(sb), qh, H(pb), C.byref(abi.SoftmaxPush(ctxlen, 0)))
+            run(ctx, "vx_attn_values_devpos", H(sb), H(vcb), H(ob), H(pb), C.byref(ap2))
+        else:
+            run(ctx, "vx_attn_scores", H(qb), H(kcb), H(sb), C.byref(ap))
+            s = sb.download(np.float32, qh * ctxlen).reshape(qh, ctxlen)
+            assert rel_l2(s[:, :pos + 1], s_w.reshape(qh, ctxlen)[:, :pos + 1]) < 1e-5
+            run(ctx, "vx_softmax", H(sb), qh, C.byref(abi.SoftmaxPush(ctxlen, pos)))
+            pr = sb.download(np.float32, qh * ctxlen).reshape(qh, ctxlen)
+            assert rel_l2(pr[:, :pos + 1], p_w.reshape(qh, ctxlen)[:, :pos + 1]) < 1e-4
+            run(ctx, "vx_attn_values", H(sb), H(vcb), H(ob), C.byref(ap))
+        assert rel_l2(ob.download(np.float32, qh * hd), o_w) < TOL
+
+
+# -------------------------------------------------------------- embedding
+@pytest.mark.parametrize("name,tok,alpha", [("emb_f16", 0, 1.0), ("emb_f16", 299, 1.0), ("emb_q8", 123, 1.0),
+                                            ("emb_q8", 299, 12.0)])
+def test_embedding_bit_exact(ctx, ops, name, tok, alpha):
+    data, ts, model = ops
+    t = ts[name]
+    p = abi.EmbeddingPush(t.offset, 2048, tok, t.ggml_type, alpha)
+    hb = out(ctx, 2048)
+    run(ctx, "vx_embedding", model.handle, H(hb), C.byref(p))
+    want = voxref.embedding(data, p)
+    assert np.array_equal(hb.download(np.float32, 2048), want)
+    tokens = buf(ctx, np.array([0, 0, tok, 0], np.uint32))
+    pos = buf(ctx, np.array([2], np.uint32))
+    h2 = out(ctx, 2048)
+    run(ctx, "vx_embedding_devtok", model.handle, H(h2), H(tokens), H(pos), C.byref(p))
+    assert np.array_equal(h2.download(np.float32, 2048), want)
+
+
+def test_embedding_token_out_of_range(ctx, ops):
+    data, ts, model = ops
+    t = ts["emb_f16"]
+    hb = out(ctx, 2048)
+    with pytest.raises(abi.VxError) as e:
+        run(ctx, "vx_embedding", model.handle, H(hb), C.byref(abi.EmbeddingPush(t.offset, 2048, 300, 1, 1.0)))
+    assert e.value.name == "VX_ERR_TOKEN_RANGE"
+    # Device token ids past the vocabulary produce NaN rows, never an out-of-range read.
+    tokens, pos = buf(ctx, np.array([300], np.uint32)), buf(ctx, np.array([0], np.uint32))
+    run(ctx, "vx_embedding_devtok", model.handle, H(hb), H(tokens), H(pos),
+        C.byref(abi.EmbeddingPush(t.offset, 2048, 0, 1, 1.0)))
+    assert np.all(np.isnan(hb.download(np.float32, 2048)))
+
+
+# --------------------------------------------------- linear_bias / fusion
+@pytest.mark.parametrize("wname,bname,bdt", [("f32_w", "b32", 0), ("f16_sq", "b16", 1), ("wo", "b32", 0),
+                                             ("wk", "b16", 7)])
+def test_linear_bias(ctx, ops, wname, bname, bdt):
+    data, ts, model = ops
+    t = ts[wname]
+    cols, rows = t.dims
+    x = RNG.standard_normal(cols).astype(np.float32)
+    p = abi.LinearBiasPush(t.offset, ts[bname].offset, rows, cols, t.ggml_type, bdt, 0, 0.5)
+    xb, yb = buf(ctx, x), out(ctx, rows)
+    run(ctx, "vx_linear_bias", model.handle, H(xb), H(yb), C.byref(p))
+    assert rel_l2(yb.download(np.float32, rows), voxref.linear_bias(data, x, p)) < TOL
+
+
+@pytest.mark.parametrize("wname,bdt", [("fus", 0), ("fus_q8", 1)])
+def test_fusion_linear(ctx, ops, wname, bdt):
+    data, ts, model = ops
+    t = ts[wname]
+    rows = t.dims[1]
+    left = RNG.standard_normal(2048).astype(np.float32)
+    right = RNG.standard_normal(2048).astype(np.float32)
+    bias = ts["b32"] if bdt == 0 else ts["b16"]
+    p = abi.FusionPush(t.offset, bias.offset, rows, 2048, 2048, t.ggml_type, bdt, 0)
+    lb, rb, yb, sb = buf(ctx, left), buf(ctx, right), out(ctx, rows), out(ctx, rows)
+    run(ctx, "vx_fusion_linear", model.handle, H(lb), H(rb), H(yb), H(sb), C.byref(p))
+    yw, sw = voxref.fusion_linear(data, left, right, p)
+    y = yb.download(np.float32, rows)
+    assert np.array_equal(y, sb.download(np.float32, rows))
+    assert rel_l2(y, yw) < TOL
+
+
+# ------------------------------------------------------------ fused ops
+def fused_qkv_args(ts, layer, ctxlen, hd=128):
+    return abi.FusedQkvArgs(ts["n1"].offset, 1e-6, ts["wq"].offset, ts["wk"].offset, ts["wv"].offset,
+                            2048, 256, 2048, 8, ts["factors"].offset, hd, 10000.0, 1.0, layer, ctxlen)
+
+
+@pytest.mark.parametrize("pos", [0, 300])
+def test_fused_qkv_rope_store(ctx, ops, pos):
+    data, ts, model = ops
+    L, ctxlen = 2, 512
+    h = (RNG.standard_normal(2048) * 40).astype(np.float32)
+    kc0 = synth.normal_f16(L * ctxlen * 256, 8).view(np.uint16).copy()
+    vc0 = synth.normal_f16(L * ctxlen * 256, 9).view(np.uint16).copy()
+    # Oracle composition: rmsnorm -> qkv_matvec -> rope -> store_kv (baselm.rs:915-967).
+    n = voxref.rmsnorm(data, h, abi.RmsPush(ts["n1"].offset, 2048, 1e-6))
+    q, k, v = voxref.qkv_matvec(data, n, abi.QkvPush(ts["wq"].offset, ts["wk"].offset, ts["wv"].offset,
+                                                    2048, 256, 2048, 8, 8, 8, 0))
+    q, k = voxref.rope(data, q, k, abi.RopePush(ts["factors"].offset, pos, 16, 2, 128, 10000.0, 1.0))
+    kcw, vcw = kc0.copy(), vc0.copy()
+    voxref.store_kv(k, v, kcw, vcw, abi.StoreKvPush(1, pos, ctxlen, 256))
+    hb, qb, kb, vb = buf(ctx, h), out(ctx, 2048), out(ctx, 256), out(ctx, 256)
+    kcb, vcb, pb = buf(ctx, kc0), buf(ctx, vc0), buf(ctx, np.array([pos], np.uint32))
+    run(ctx, "vx_fused_qkv_rope_store", model.handle, H(hb), H(qb), H(kb), H(vb), H(kcb), H(vcb), H(pb),
+        C.byref(fused_qkv_args(ts, 1, ctxlen)))
+    qg, kg, vg = qb.download(np.float32, 2048), kb.download(np.float32, 256), vb.download(np.float32, 256)
+    assert rel_l2(qg, q) < TOL and rel_l2(kg, k) < TOL and rel_l2(vg, v) < TOL
+    kcg = kcb.download(np.uint16, kc0.size).reshape(L, ctxlen, 256)
+    vcg = vcb.download(np.uint16, vc0.size).reshape(L, ctxlen, 256)
+    # Placement: only row (layer 1, pos) changed, and it holds f16(RNE) of the kernel's own k/v.
+    mask = np.ones((L, ctxlen), bool)
+    mask[1, pos] = False
+    assert np.array_equal(kcg[mask], kc0.reshape(L, ctxlen, 256)[mask])
+    assert np.array_equal(vcg[mask], vc0.reshape(L, ctxlen, 256)[mask])
+    assert np.array_equal(kcg[1, pos], kg.astype(np.float16).view(np.uint16))
+    assert np.array_equal(vcg[1, pos], vg.astype(np.float16).view(np.uint16))
+    assert rel_l2(kcg[1, pos].view(np.float16), kcw.reshape(L, ctxlen, 256)[1, pos].view(np.float16)) < TOL
+
+
+@pytest.mark.parametrize("pos,splits,hd", [(0, 16, 128), (31, 16, 128), (32, 16, 128), (33, 4, 128),
+                                           (512, 16, 128), (2047, 64, 128), (2047, 1, 128), (100, 8, 64)])
+def test_fused_attention(ctx, pos, splits, hd):
+    L, ctxlen, kvh, qpk = 2, 2048, 2, 8
+    qh = kvh * qpk
+    kc, vc, q = attn_inputs(L, ctxlen, hd, kvh, qh, 70 + pos)
+    ap = abi.AttentionPush(1, ctxlen, pos, hd, qpk, kvh)
+    s = voxref.attn_scores(q, kc, qh, ap)
+    pr = voxref.softmax(s, qh, abi.SoftmaxPush(ctxlen, pos))
+    want = voxref.attn_values(pr, vc, qh, ap)
+    a = abi.FusedAttnArgs(1, ctxlen, hd, qh, kvh, splits)
+    scratch = ctx.zeros(abi.load().vx_fused_attention_scratch_bytes(C.byref(a)))
+    qb, kcb, vcb, ob = buf(ctx, q), buf(ctx, kc), buf(ctx, vc), out(ctx, qh * hd)
+    pb = buf(ctx, np.array([pos], np.uint32))
+    for _ in range(2):  # second call checks the completion tickets were restored
+        run(ctx, "vx_fused_attention", H(qb), H(kcb), H(vcb), H(ob), H(scratch), H(pb), C.byref(a))
+        assert rel_l2(ob.download(np.float32, qh * hd), want) < TOL
+    assert np.all(scratch.download(np.uint32, kvh) == 0)
+
+
+def test_fused_matvec_residual(ctx, ops):
+    data, ts, model = ops
+    x = RNG.standard_normal(6144).astype(np.float32)
+    h = (RNG.standard_normal(2048) * 100).astype(np.float32)
+    a = abi.FusedResidualArgs(ts["wd"].offset, 2048, 6144, 8, 0.5)
+    xb, hb, bb = buf(ctx, x), buf(ctx, h), out(ctx, 2048)
+    run(ctx, "vx_fused_matvec_residual", model.handle, H(xb), H(hb), H(bb), C.byref(a))
+    branch = voxref.matvec(data, x, abi.MatvecPush(ts["wd"].offset, 2048, 6144, 8, 0, 1.0))
+    assert rel_l2(bb.download(np.float32, 2048), branch) < TOL
+    assert rel_l2(hb.download(np.float32, 2048), h + np.float32(0.5) * branch) < TOL
+
+
+def test_fused_rms_swiglu(ctx, ops):
+    data, ts, model = ops
+    h = (RNG.standard_normal(2048) * 500).astype(np.float32)
+    a = abi.FusedSwigluArgs(ts["n2"].offset, 1e-6, ts["wg"].offset, ts["wu"].offset, 6144, 2048, 8)
+    hb, yb = buf(ctx, h), out(ctx, 6144)
+    run(ctx, "vx_fused_rms_swiglu", model.handle, H(hb), H(yb), C.byref(a))
+    n = voxref.rmsnorm(data, h, abi.RmsPush(ts["n2"].offset, 2048, 1e-6))
+    want = voxref.matvec_swiglu(data, n, abi.SwigluPush(ts["wg"].offset, ts["wu"].offset, 6144, 2048, 8, 0))
+    assert rel_l2(yb.download(np.float32, 6144), want) < TOL
+
+
+# ---------------------------------------------------------- graph replay
+def test_graph_replay_reads_device_position(ctx):
+    """A captured attention graph replays correctly with eager work between replays."""
+    L, ctxlen, hd, kvh, qpk = 1, 1024, 128, 2, 8
+    qh = kvh * qpk
+    kc, vc, q = attn_inputs(L, ctxlen, hd, kvh, qh, 99)
+    a = abi.FusedAttnArgs(0, ctxlen, hd, qh, kvh, 32)
+    scratch = ctx.zeros(abi.load().vx_fused_attention_scratch_bytes(C.byref(a)))
+    qb, kcb, vcb, ob = buf(ctx, q), buf(ctx, kc), buf(ctx, vc), out(ctx, qh * hd)
+    pb = buf(ctx, np.array([0], np.uint32))
+    ctx.sync()
+    ctx.graph_begin()
+    run(ctx, "vx_fused_attention", H(qb), H(kcb), H(vcb), H(ob), H(scratch), H(pb), C.byref(a))
+    g = ctx.graph_end()
+    try:
+        for pos in (5, 700, 63, 1023):
+            pb.upload(np.array([pos], np.uint32))
+            ctx.graph_launch(g)
+            ctx.sync()
+            ap = abi.AttentionPush(0, ctxlen, pos, hd, qpk, kvh)
+            pr = voxref.softmax(voxref.attn_scores(q, kc, qh, ap), qh, abi.SoftmaxPush(ctxlen, pos))
+            assert rel_l2(ob.download(np.float32, qh * hd), voxref.attn_values(pr, vc, qh, ap)) < TOL
+    finally:
+        ctx.graph_free(g)
+
+
+# ------------------------------------------------------------ error paths
+def test_host_side_validation_errors(ctx, ops):
+    data, ts, model = ops
+    t = ts["wq"]
+    small, x = out(ctx, 100), buf(ctx, np.zeros(2048, np.float32))
+    cases = [
+        ("VX_ERR_BOUNDS", "vx_matvec", (model.handle, H(x), H(small), C.byref(abi.MatvecPush(t.offset, 2048, 2048, 8, 0, 1.0)))),
+        ("VX_ERR_NOT_FOUND", "vx_matvec", (model.handle, H(x), H(small), C.byref(abi.MatvecPush(t.offset + 32, 8, 2048, 8, 0, 1.0)))),
+        ("VX_ERR_SHAPE", "vx_matvec", (model.handle, H(x), H(small), C.byref(abi.MatvecPush(t.offset, 8, 2048, 1, 0, 1.0)))),
+        ("VX_ERR_SHAPE", "vx_matvec", (model.handle, H(x), H(small), C.byref(abi.MatvecPush(t.offset, 8, 1024, 8, 0, 1.0)))),
+        ("VX_ERR_UNSUPPORTED", "vx_matvec", (model.handle, H(x), H(small), C.byref(abi.MatvecPush(ts["f32_w"].offset, 8, 128, 0, 0, 1.0)))),
+        ("VX_ERR_CONTEXT_FULL", "vx_softmax", (H(small), 1, C.byref(abi.SoftmaxPush(16, 16)))),
+    ]
+    for code, fn, args in cases:
+        with pytest.raises(abi.VxError) as e:
+            run(ctx, fn, *args)
+        assert e.value.name == code, (fn, e.value)

@@ -1,0 +1,85 @@
+"""Builds the in-tree shared libraries of voxgen_amd.
+
+  voxgen_amd/libvoxhip.so    HIP kernels for gfx950 + C ABI (include/voxhip.h)
+  voxgen_amd/libvoxsynth.so  host-side deterministic input generator
+
+Device code is compiled with packed-FP32 instructions disabled
+(-Xclang -target-feature -Xclang -packed-fp32-ops).
+Run as a script or call build_all(); every call recompiles.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+ROOT = PKG.parent
+OBJ = ROOT / "_build" / "voxhip"
+ARCH = os.environ.get("VOXHIP_ARCH", "gfx950")
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+HIP_FLAGS = [
+    "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-result",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("command failed:\n" + " ".join(cmd) + "\n" + proc.stdout)
+    out = "\n".join(l for l in proc.stdout.splitlines()
+                    if "packed-fp32-ops" not in l and l.strip())
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def _compile(src: Path) -> Path:
+    OBJ.mkdir(parents=True, exist_ok=True)
+    obj = OBJ / (src.name + ".o")
+    # hipcc treats .cpp as HIP source too; both get the gfx950 device flags.
+    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    _run(cmd)
+    return obj
+
+
+def build_voxhip(jobs: int | None = None) -> Path:
+    sources = sorted(CSRC.glob("*.hip")) + sorted(
+        p for p in CSRC.glob("*.cpp"))
+    jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, sources))
+    out = PKG / "libvoxhip.so"
+    tmp = PKG / "libvoxhip.so.tmp"
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, out)
+    return out
+
+
+def build_synth() -> Path:
+    out = PKG / "libvoxsynth.so"
+    tmp = PKG / "libvoxsynth.so.tmp"
+    _run(["gcc", "-O3", "-march=x86-64-v3", "-fopenmp", "-fPIC", "-shared", "-std=c11",
+          "-Wall", "-o", str(tmp), str(CSRC / "synth.c"), "-lm"])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all(verbose: bool = False) -> None:
+    with cf.ThreadPoolExecutor(max_workers=1) as ex:
+        f_syn = ex.submit(build_synth)
+        hip = build_voxhip()
+        syn = f_syn.result()
+    if verbose:
+        for p in (hip, syn):
+            print(f"built {p.relative_to(ROOT)}")
+
+
+if __name__ == "__main__":
+    build_all(verbose=True)

@@ -1,0 +1,784 @@
+// BaseLM engine: the host side of BaseLmEngine (baselm.rs:423-890) over HIP.
+//
+// Decode step in the default (graph) mode, all reading the decode position and
+// the token id from device memory so one captured hipGraph is replayed per token:
+//   embedding gather                                  embedding.comp
+//   per layer:
+//     k_qkv_fused      rmsnorm(h)*attn_norm -> Q/K/V -> RoPE -> f16 KV store
+//     k_attn_decode    split-context single-query attention + combine
+//     k_matvec (resid) h += Wo . attn
+//     k_swiglu (norm)  gate = silu(Wg . n) * (Wu . n), n = rmsnorm(h)*ffn_norm
+//     k_matvec (resid) h += Wdown . gate
+//   k_rmsnorm          norm = rmsnorm(h)*output_norm, then position += 1
+//   [LM head matvec]   logits = logit_scale * Wout . norm
+// This is record_transformer's op order (baselm.rs:892-1052) with each
+// residual_rmsnorm split between the producing matvec (residual add) and the
+// consuming matvec (normalisation), which removes 2 launches per layer.
+// VX_EXEC_REFERENCE instead issues the reference's 11 per-op dispatches.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "vx_internal.h"
+
+using namespace vx;
+
+namespace {
+
+struct Layer {
+    WRef q, k, v, o, gate, up, down;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+
+float effective_scale(float v) { return v == 0.0f ? 1.0f : v; }  // baselm.rs:1262-1264
+
+}  // namespace
+
+struct vx_baselm {
+    vx_ctx *ctx = nullptr;
+    const vx_model *model = nullptr;
+    vx_baselm_config cfg{};
+    vx_baselm_options opt{};
+    vx_buf *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    vx_buf *attention = nullptr, *gate = nullptr, *branch = nullptr, *logits = nullptr;
+    vx_buf *scores = nullptr, *kv_k = nullptr, *kv_v = nullptr, *position = nullptr;
+    vx_buf *tokens = nullptr, *attn_scratch = nullptr;
+    std::vector<Layer> layers;
+    uint32_t embd_offset = 0, embd_dtype = 1;
+    WRef output;
+    const float *output_norm = nullptr, *rope_factors = nullptr;
+    float residual_scale = 1.f, embedding_alpha = 1.f, logit_alpha = 1.f, rope_scaling = 1.f;
+    uint32_t splits = 16;
+    uint32_t pos = 0;
+    vx_graph *graphs[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+};
+
+namespace {
+
+int find(const vx_model *m, const std::string &name, const vx_tensor_info **out) {
+    auto it = m->by_name.find(name);
+    if (it == m->by_name.end())
+        return fail(VX_ERR_NOT_FOUND, "required GGUF tensor \"%s\" is missing", name.c_str());
+    *out = &m->tensors[it->second];
+    return VX_OK;
+}
+
+int require_dims(const vx_tensor_info *t, std::initializer_list<uint64_t> dims) {
+    bool ok = t->n_dims == dims.size();
+    uint32_t i = 0;
+    for (uint64_t d : dims) {
+        if (!ok) break;
+        ok = t->dims[i++] == d;
+    }
+    if (!ok) {  // require_dims baselm.rs:264-269
+        std::string want, got;
+        for (uint64_t d : dims) want += std::to_string(d) + ",";
+        for (uint32_t j = 0; j < t->n_dims; ++j) got += std::to_string(t->dims[j]) + ",";
+        return fail(VX_ERR_SHAPE, "tensor %s has dimensions [%s], expected [%s]", t->name, got.c_str(),
+                    want.c_str());
+    }
+    return VX_OK;
+}
+
+int require_f32(const vx_tensor_info *t) {
+    if (t->ggml_type != VX_DTYPE_F32)
+        return fail(VX_ERR_SHAPE, "tensor %s is type %u, expected F32", t->name, t->ggml_type);
+    return VX_OK;
+}
+
+int require_matrix_type(const vx_tensor_info *t) {  // baselm.rs:276-284
+    if (t->ggml_type != VX_DTYPE_F16 && t->ggml_type != VX_DTYPE_Q8_0)
+        return fail(VX_ERR_SHAPE, "matrix %s uses unsupported type %u", t->name, t->ggml_type);
+    if (t->ggml_type == VX_DTYPE_Q8_0 && t->dims[0] % 32u)
+        return fail(VX_ERR_SHAPE, "Q8_0 matrix %s has row width %llu, not divisible by 32", t->name,
+                    (unsigned long long)t->dims[0]);
+    return VX_OK;
+}
+
+int matrix(const vx_model *m, const std::string &name, uint64_t cols, uint64_t rows, WRef *out) {
+    const vx_tensor_info *t;
+    VX_CHECK(find(m, name, &t));
+    VX_CHECK(require_dims(t, {cols, rows}));
+    VX_CHECK(require_matrix_type(t));
+    return resolve_matrix(m, (uint32_t)t->offset, t->ggml_type, (uint32_t)rows, (uint32_t)cols, out,
+                          name.c_str());
+}
+
+int vec_f32(const vx_model *m, const std::string &name, uint64_t n, const float **out, uint32_t *off = nullptr) {
+    const vx_tensor_info *t;
+    VX_CHECK(find(m, name, &t));
+    VX_CHECK(require_dims(t, {n}));
+    VX_CHECK(require_f32(t));
+    const void *p;
+    VX_CHECK(resolve_vector(m, (uint32_t)t->offset, VX_DTYPE_F32, (uint32_t)n, &p, name.c_str()));
+    *out = static_cast<const float *>(p);
+    if (off) *off = (uint32_t)t->offset;
+    return VX_OK;
+}
+
+int validate_config(const vx_baselm_config &c, bool strict) {
+    if (c.active_context_length == 0 || c.active_context_length > c.context_length)
+        return fail(VX_ERR_INVALID_ARG, "--max-context must be in 1..=%u, got %u", c.context_length,
+                    c.active_context_length);
+    if (strict && (c.embedding_length != 2048 || c.block_count != 28 || c.feed_forward_length != 6144 ||
+                   c.head_count != 16 || c.head_count_kv != 2 || c.head_dim != 128 ||
+                   c.rope_dimension_count != 128))  // baselm.rs:102-113
+        return fail(VX_ERR_UNSUPPORTED,
+                    "unsupported MiniCPM4 BaseLM geometry: embd=%u, layers=%u, ffn=%u, heads=%u, "
+                    "kv_heads=%u, head_dim=%u, rope_dim=%u",
+                    c.embedding_length, c.block_count, c.feed_forward_length, c.head_count,
+                    c.head_count_kv, c.head_dim, c.rope_dimension_count);
+    if (c.head_count_kv == 0 || c.head_count % c.head_count_kv)
+        return fail(VX_ERR_SHAPE, "head_count %u is not divisible by head_count_kv %u", c.head_count,
+                    c.head_count_kv);
+    if (c.rope_dimension_count != c.head_dim)
+        return fail(VX_ERR_UNSUPPORTED, "partial RoPE is not implemented: rope_dimension_count=%u, head_dim=%u",
+                    c.rope_dimension_count, c.head_dim);
+    if (c.kv_dim != c.head_count_kv * c.head_dim)
+        return fail(VX_ERR_SHAPE, "kv_dim %u != head_count_kv*head_dim", c.kv_dim);
+    if (c.head_count * c.head_dim != c.embedding_length)
+        return fail(VX_ERR_SHAPE, "head_count*head_dim must equal embedding_length");
+    if (!c.rope_longrope)  // baselm.rs:902-912
+        return fail(VX_ERR_UNSUPPORTED, "MiniCPM4 BaseLM without LongRoPE factors is not enabled");
+    if (c.block_count == 0) return fail(VX_ERR_SHAPE, "block_count is zero");
+    return VX_OK;
+}
+
+int alloc(vx_ctx *ctx, uint64_t bytes, vx_buf **out) { return vx_alloc(ctx, bytes, out); }
+
+void free_all(vx_baselm *e) {
+    for (auto &row : e->graphs)
+        for (auto &g : row)
+            if (g) {
+                vx_graph_free(e->ctx, g);
+                g = nullptr;
+            }
+    vx_buf **bufs[] = {&e->hidden, &e->norm,   &e->q,      &e->k,        &e->v,
+                       &e->attention, &e->gate, &e->branch, &e->logits, &e->scores,
+                       &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch};
+    for (vx_buf **b : bufs) {
+        vx_free(e->ctx, *b);
+        *b = nullptr;
+    }
+}
+
+inline float *F(vx_buf *b) { return static_cast<float *>(b->ptr); }
+inline uint32_t *U(vx_buf *b) { return static_cast<uint32_t *>(b->ptr); }
+inline __half *H(vx_buf *b) { return static_cast<__half *>(b->ptr); }
+
+// The fused decode step, enqueued on the context stream.
+int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_baselm_config &c = e->cfg;
+    if (with_embedding) {
+        ProfSpan sp(ctx, "baselm.embedding");
+        VX_CHECK(launch_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, c.embedding_length, 0,
+                                  U(e->tokens), U(e->position), c.vocab_size, e->embedding_alpha, F(e->hidden),
+                                  c.active_context_length));
+    }
+    for (uint32_t l = 0; l < c.block_count; ++l) {
+        const Layer &L = e->layers[l];
+        {
+            ProfSpan sp(ctx, "baselm.qkv");
+            QkvFusedLaunch a;
+            a.q = L.q;
+            a.k = L.k;
+            a.v = L.v;
+            a.hidden = F(e->hidden);
+            a.norm = L.attn_norm;
+            a.eps = c.rms_epsilon;
+            a.q_rows = c.embedding_length;
+            a.kv_rows = c.kv_dim;
+            a.cols = c.embedding_length;
+            a.head_dim = c.head_dim;
+            a.factors = e->rope_factors;
+            a.theta = c.rope_theta;
+            a.scaling = e->rope_scaling;
+            a.layer = l;
+            a.context = c.active_context_length;
+            a.qo = F(e->q);
+            a.ko = F(e->k);
+            a.vo = F(e->v);
+            a.kc = H(e->kv_k);
+            a.vc = H(e->kv_v);
+            a.position = U(e->position);
+            VX_CHECK(launch_qkv_fused(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.attention");
+            AttnLaunch a;
+            a.q = F(e->q);
+            a.kc = H(e->kv_k);
+            a.vc = H(e->kv_v);
+            a.out = F(e->attention);
+            a.partials = F(e->attn_scratch);
+            a.counters = U(e->attn_scratch);
+            a.position = U(e->position);
+            a.layer = l;
+            a.context = c.active_context_length;
+            a.head_dim = c.head_dim;
+            a.q_heads = c.head_count;
+            a.kv_heads = c.head_count_kv;
+            a.splits = e->splits;
+            VX_CHECK(launch_attn_decode(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.attn_out");
+            MatvecLaunch a;
+            a.w = L.o;
+            a.xl = F(e->attention);
+            a.rows = c.embedding_length;
+            a.cols = c.embedding_length;
+            a.epi = EPI_RESIDUAL;
+            a.y = F(e->hidden);
+            a.scale = e->residual_scale;
+            VX_CHECK(launch_matvec(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.swiglu");
+            SwigluLaunch a;
+            a.g = L.gate;
+            a.u = L.up;
+            a.x = F(e->hidden);
+            a.norm = L.ffn_norm;
+            a.eps = c.rms_epsilon;
+            a.rows = c.feed_forward_length;
+            a.cols = c.embedding_length;
+            a.y = F(e->gate);
+            VX_CHECK(launch_swiglu(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.down");
+            MatvecLaunch a;
+            a.w = L.down;
+            a.xl = F(e->gate);
+            a.rows = c.embedding_length;
+            a.cols = c.feed_forward_length;
+            a.epi = EPI_RESIDUAL;
+            a.y = F(e->hidden);
+            a.scale = e->residual_scale;
+            VX_CHECK(launch_matvec(s, a));
+        }
+    }
+    {
+        ProfSpan sp(ctx, "baselm.output_norm");
+        VX_CHECK(launch_rmsnorm(s, F(e->hidden), F(e->norm), e->output_norm, c.embedding_length, c.rms_epsilon,
+                                U(e->position)));
+    }
+    if (logits) {
+        ProfSpan sp(ctx, "baselm.logits");
+        MatvecLaunch a;
+        a.w = e->output;
+        a.xl = F(e->norm);
+        a.rows = c.vocab_size;
+        a.cols = c.embedding_length;
+        a.alpha = e->logit_alpha;
+        a.epi = EPI_STORE;
+        a.y = F(e->logits);
+        VX_CHECK(launch_matvec(s, a));
+    }
+    return VX_OK;
+}
+
+// The reference's dispatch sequence (record_transformer) with a host position.
+int enqueue_reference(vx_baselm *e, uint32_t position, bool with_embedding, uint32_t token, bool logits) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_baselm_config &c = e->cfg;
+    const uint32_t q_per_kv = c.head_count / c.head_count_kv;
+    if (with_embedding) {
+        ProfSpan sp(ctx, "baselm.embedding");
+        VX_CHECK(launch_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, c.embedding_length, token,
+                                  nullptr, nullptr, c.vocab_size, e->embedding_alpha, F(e->hidden)));
+    }
+    {
+        ProfSpan sp(ctx, "baselm.rmsnorm");
+        VX_CHECK(launch_rmsnorm(s, F(e->hidden), F(e->norm), e->layers[0].attn_norm, c.embedding_length,
+                                c.rms_epsilon, nullptr));
+    }
+    auto mv = [&](const WRef &w, const float *x, float *y, uint32_t rows, uint32_t cols, float alpha) {
+        MatvecLaunch a;
+        a.w = w;
+        a.xl = x;
+        a.rows = rows;
+        a.cols = cols;
+        a.alpha = alpha;
+        a.epi = EPI_STORE;
+        a.y = y;
+        return launch_matvec(s, a);
+    };
+    for (uint32_t l = 0; l < c.block_count; ++l) {
+        const Layer &L = e->layers[l];
+        {
+            ProfSpan sp(ctx, "baselm.qkv");
+            VX_CHECK(mv(L.q, F(e->norm), F(e->q), c.embedding_length, c.embedding_length, 1.f));
+            VX_CHECK(mv(L.k, F(e->norm), F(e->k), c.kv_dim, c.embedding_length, 1.f));
+            VX_CHECK(mv(L.v, F(e->norm), F(e->v), c.kv_dim, c.embedding_length, 1.f));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.rope");
+            VX_CHECK(launch_rope(s, F(e->q), F(e->k), e->rope_factors, position, nullptr, c.head_count,
+                                 c.head_count_kv, c.head_dim, c.rope_theta, e->rope_scaling));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.store_kv");
+            VX_CHECK(launch_store_kv(s, F(e->k), F(e->v), H(e->kv_k), H(e->kv_v), l, position, nullptr,
+                                     c.active_context_length, c.kv_dim));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.attn_scores");
+            VX_CHECK(launch_attn_scores(s, F(e->q), H(e->kv_k), F(e->scores), l, c.active_context_length,
+                                        position, nullptr, c.head_dim, q_per_kv, c.head_count_kv, c.head_count));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.softmax");
+            VX_CHECK(launch_softmax(s, F(e->scores), c.head_count, c.active_context_length, position, nullptr));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.attn_values");
+            VX_CHECK(launch_attn_values(s, F(e->scores), H(e->kv_v), F(e->attention), l, c.active_context_length,
+                                        position, nullptr, c.head_dim, q_per_kv, c.head_count_kv, c.head_count));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.matvec");
+            VX_CHECK(mv(L.o, F(e->attention), F(e->branch), c.embedding_length, c.embedding_length, 1.f));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.residual_rmsnorm");
+            VX_CHECK(launch_residual_rmsnorm(s, F(e->hidden), F(e->branch), F(e->norm), L.ffn_norm,
+                                             c.embedding_length, c.rms_epsilon, e->residual_scale));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.swiglu");
+            SwigluLaunch a;
+            a.g = L.gate;
+            a.u = L.up;
+            a.x = F(e->norm);
+            a.rows = c.feed_forward_length;
+            a.cols = c.embedding_length;
+            a.y = F(e->gate);
+            VX_CHECK(launch_swiglu(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.matvec");
+            VX_CHECK(mv(L.down, F(e->gate), F(e->branch), c.embedding_length, c.feed_forward_length, 1.f));
+        }
+        {
+            ProfSpan sp(ctx, "baselm.residual_rmsnorm");
+            const float *next = l + 1 < c.block_count ? e->layers[l + 1].attn_norm : e->output_norm;
+            VX_CHECK(launch_residual_rmsnorm(s, F(e->hidden), F(e->branch), F(e->norm), next, c.embedding_length,
+                                             c.rms_epsilon, e->residual_scale));
+        }
+    }
+    if (logits) {
+        ProfSpan sp(ctx, "baselm.matvec");
+        VX_CHECK(mv(e->output, F(e->norm), F(e->logits), c.vocab_size, c.embedding_length, e->logit_alpha));
+    }
+    // Keep the device position in step with the host (the fused path advances it).
+    return launch_set_step(s, U(e->tokens), U(e->position), position + 1u, 0, 0);
+}
+
+// One step at host position e->pos. The device position buffer already holds it.
+int run_step(vx_baselm *e, bool with_embedding, uint32_t token, bool logits) {
+    if (e->opt.exec_mode == VX_EXEC_REFERENCE) return enqueue_reference(e, e->pos, with_embedding, token, logits);
+    if (e->opt.exec_mode == VX_EXEC_FUSED || e->ctx->prof_enabled) return enqueue_fused(e, with_embedding, logits);
+    vx_graph *&g = e->graphs[with_embedding ? 1 : 0][logits ? 1 : 0];
+    if (!g) {
+        VX_CHECK(vx_graph_begin(e->ctx));
+        int st = enqueue_fused(e, with_embedding, logits);
+        vx_graph *ng = nullptr;
+        int st2 = vx_graph_end(e->ctx, &ng);
+        if (st != VX_OK) {
+            if (ng) vx_graph_free(e->ctx, ng);
+            return st;
+        }
+        VX_CHECK(st2);
+        g = ng;
+    }
+    return vx_graph_launch(e->ctx, g);
+}
+
+int ensure_context(const vx_baselm *e, uint32_t steps) {  // baselm.rs:882-890
+    if ((uint64_t)e->pos + steps > e->cfg.active_context_length)
+        return fail(VX_ERR_CONTEXT_FULL, "BaseLM KV cache is full at %u tokens; reset or increase --max-context",
+                    e->cfg.active_context_length);
+    return VX_OK;
+}
+
+int check_token(const vx_baselm *e, uint32_t token) {  // baselm.rs:629-631
+    if (token >= e->cfg.vocab_size)
+        return fail(VX_ERR_TOKEN_RANGE, "token id %u is outside vocabulary 0..%u", token, e->cfg.vocab_size);
+    return VX_OK;
+}
+
+double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// collect_result (baselm.rs:1204-1231).
+int collect_result(vx_baselm *e, uint32_t position, double elapsed_ms, uint32_t top_k, vx_step_result *res,
+                   vx_top_logit *top) {
+    const uint32_t n = e->cfg.embedding_length;
+    std::vector<float> h(n);
+    VX_CHECK(vx_download(e->ctx, e->norm, 0, h.data(), (uint64_t)n * 4u));
+    double sum = 0.0, sq = 0.0;
+    for (float x : h) {
+        sum += (double)x;
+        sq += (double)x * (double)x;
+    }
+    uint32_t n_top = 0;
+    if (top_k > 0 && top) {
+        const uint32_t vocab = e->cfg.vocab_size;
+        std::vector<float> lg(vocab);
+        VX_CHECK(vx_download(e->ctx, e->logits, 0, lg.data(), (uint64_t)vocab * 4u));
+        VX_CHECK(vx_top_k_logits(lg.data(), vocab, top_k, top, &n_top));
+    }
+    if (res) {
+        res->position = position;
+        res->elapsed_ms = elapsed_ms;
+        res->final_hidden_checksum = sum;
+        res->final_hidden_l2 = std::sqrt(sq);
+        res->n_top = n_top;
+    }
+    return VX_OK;
+}
+
+int upload_embedding(vx_baselm *e, const float *emb, uint32_t n) {
+    if (!emb) return fail(VX_ERR_INVALID_ARG, "external embedding is null");
+    if (n != e->cfg.embedding_length)
+        return fail(VX_ERR_SHAPE, "external embedding has %u floats; expected %u", n, e->cfg.embedding_length);
+    VX_HIP(hipStreamSynchronize(e->ctx->stream));
+    VX_HIP(hipMemcpyAsync(e->hidden->ptr, emb, (size_t)n * 4u, hipMemcpyHostToDevice, e->ctx->stream));
+    VX_HIP(hipStreamSynchronize(e->ctx->stream));
+    return VX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vx_top_k_logits(const float *logits, uint32_t n, uint32_t k, vx_top_logit *out, uint32_t *n_out) {
+    if ((!logits && n) || (!out && k)) return fail(VX_ERR_INVALID_ARG, "vx_top_k_logits: null argument");
+    std::vector<uint32_t> idx;
+    idx.reserve(n);
+    for (uint32_t i = 0; i < n; ++i)
+        if (std::isfinite(logits[i])) idx.push_back(i);
+    const uint32_t m = std::min<uint32_t>(k, (uint32_t)idx.size());
+    std::partial_sort(idx.begin(), idx.begin() + m, idx.end(), [&](uint32_t a, uint32_t b) {
+        return logits[a] > logits[b] || (logits[a] == logits[b] && a < b);
+    });
+    for (uint32_t i = 0; i < m; ++i) out[i] = vx_top_logit{idx[i], logits[idx[i]]};
+    if (n_out) *n_out = m;
+    return VX_OK;
+}
+
+float vx_baselm_rope_scaling_factor(const vx_baselm_config *c) {
+    if (!c) return 1.0f;
+    if (!c->rope_longrope || c->context_length <= c->rope_original_context_length ||
+        c->rope_original_context_length <= 1u)
+        return 1.0f;
+    const float max = (float)c->context_length;
+    const float original = (float)c->rope_original_context_length;
+    return std::sqrt(1.0f + std::log(max / original) / std::log(original));
+}
+
+uint64_t vx_baselm_kv_cache_bytes(const vx_baselm_config *c) {
+    if (!c) return 0;
+    return (uint64_t)c->block_count * c->active_context_length * c->kv_dim * 2u * 2u;
+}
+
+int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config *cfg,
+                     const vx_baselm_options *opt, vx_baselm **out) {
+    if (!ctx || !model || !cfg || !out) return fail(VX_ERR_INVALID_ARG, "vx_baselm_create: null argument");
+    *out = nullptr;
+    vx_baselm_options o{};
+    o.exec_mode = VX_EXEC_GRAPH;
+    o.strict_geometry = 1;
+    if (opt) o = *opt;
+    if (o.exec_mode > VX_EXEC_REFERENCE) return fail(VX_ERR_INVALID_ARG, "unknown exec_mode %u", o.exec_mode);
+    VX_CHECK(validate_config(*cfg, o.strict_geometry != 0));
+    const vx_baselm_config &c = *cfg;
+    vx_baselm *e = new vx_baselm();
+    e->ctx = ctx;
+    e->model = model;
+    e->cfg = c;
+    e->opt = o;
+    auto bail = [&](int st) {
+        free_all(e);
+        delete e;
+        return st;
+    };
+    // Tensor validation (BaseLmConfig::from_gguf / validate_layer, baselm.rs:123-180, 227-262).
+    const vx_tensor_info *embd;
+    int st = find(model, "token_embd.weight", &embd);
+    if (st) return bail(st);
+    if (embd->n_dims != 2) return bail(fail(VX_ERR_SHAPE, "token_embd.weight must be rank 2"));
+    if ((st = require_dims(embd, {c.embedding_length, c.vocab_size}))) return bail(st);
+    if ((st = require_matrix_type(embd))) return bail(st);
+    e->embd_offset = (uint32_t)embd->offset;
+    e->embd_dtype = embd->ggml_type;
+    if (model->by_name.count("output.weight")) {
+        if ((st = matrix(model, "output.weight", c.embedding_length, c.vocab_size, &e->output))) return bail(st);
+    } else {
+        if ((st = matrix(model, "token_embd.weight", c.embedding_length, c.vocab_size, &e->output))) return bail(st);
+    }
+    if ((st = vec_f32(model, "output_norm.weight", c.embedding_length, &e->output_norm))) return bail(st);
+    const char *factor_name = c.context_length > c.rope_original_context_length ? "rope_factors_long.weight"
+                                                                                 : "rope_factors_short.weight";
+    if ((st = vec_f32(model, "rope_factors_short.weight", c.head_dim / 2u, &e->rope_factors))) return bail(st);
+    if ((st = vec_f32(model, "rope_factors_long.weight", c.head_dim / 2u, &e->rope_factors))) return bail(st);
+    if ((st = vec_f32(model, factor_name, c.head_dim / 2u, &e->rope_factors))) return bail(st);
+    e->layers.resize(c.block_count);
+    for (uint32_t l = 0; l < c.block_count; ++l) {
+        Layer &L = e->layers[l];
+        const std::string p = "blk." + std::to_string(l) + ".";
+        const uint64_t H = c.embedding_length, KV = c.kv_dim, FF = c.feed_forward_length;
+        if ((st = vec_f32(model, p + "attn_norm.weight", H, &L.attn_norm))) return bail(st);
+        if ((st = vec_f32(model, p + "ffn_norm.weight", H, &L.ffn_norm))) return bail(st);
+        if ((st = matrix(model, p + "attn_q.weight", H, H, &L.q))) return bail(st);
+        if ((st = matrix(model, p + "attn_k.weight", H, KV, &L.k))) return bail(st);
+        if ((st = matrix(model, p + "attn_v.weight", H, KV, &L.v))) return bail(st);
+        if ((st = matrix(model, p + "attn_output.weight", H, H, &L.o))) return bail(st);
+        if ((st = matrix(model, p + "ffn_gate.weight", H, FF, &L.gate))) return bail(st);
+        if ((st = matrix(model, p + "ffn_up.weight", H, FF, &L.up))) return bail(st);
+        if ((st = matrix(model, p + "ffn_down.weight", FF, H, &L.down))) return bail(st);
+        if (L.gate.dtype != L.up.dtype)  // dispatch_swiglu baselm.rs:1166-1168
+            return bail(fail(VX_ERR_SHAPE, "SwiGLU gate/up dtypes differ in layer %u", l));
+        if (o.exec_mode != VX_EXEC_REFERENCE && (L.q.dtype != L.k.dtype || L.q.dtype != L.v.dtype))
+            return bail(fail(VX_ERR_UNSUPPORTED, "fused QKV needs one dtype for q/k/v (layer %u)", l));
+    }
+    if (c.head_count / c.head_count_kv > 16u || (c.head_dim != 64u && c.head_dim != 128u))
+        if (o.exec_mode != VX_EXEC_REFERENCE)
+            return bail(fail(VX_ERR_UNSUPPORTED, "fused attention needs head_dim 64/128 and q_per_kv <= 16"));
+    e->residual_scale = effective_scale(c.residual_scale);
+    e->embedding_alpha = effective_scale(c.embedding_scale);
+    e->logit_alpha = effective_scale(c.logit_scale);
+    e->rope_scaling = vx_baselm_rope_scaling_factor(&c);
+    uint32_t splits = o.attn_splits;
+    if (splits == 0) splits = std::min<uint32_t>(128u, std::max<uint32_t>(1u, (c.active_context_length + 31u) / 32u));
+    e->splits = splits;
+    // Buffers (BaseLmEngine::new, baselm.rs:479-506).
+    const uint64_t f = 4;
+    const uint64_t cache = vx_baselm_kv_cache_bytes(&c) / 2u;
+    if ((st = alloc(ctx, c.embedding_length * f, &e->hidden)) || (st = alloc(ctx, c.embedding_length * f, &e->norm)) ||
+        (st = alloc(ctx, c.embedding_length * f, &e->q)) || (st = alloc(ctx, c.kv_dim * f, &e->k)) ||
+        (st = alloc(ctx, c.kv_dim * f, &e->v)) || (st = alloc(ctx, c.embedding_length * f, &e->attention)) ||
+        (st = alloc(ctx, c.feed_forward_length * f, &e->gate)) ||
+        (st = alloc(ctx, c.embedding_length * f, &e->branch)) || (st = alloc(ctx, c.vocab_size * f, &e->logits)) ||
+        (st = alloc(ctx, (uint64_t)c.head_count * c.active_context_length * f, &e->scores)) ||
+        (st = alloc(ctx, cache, &e->kv_k)) || (st = alloc(ctx, cache, &e->kv_v)) ||
+        (st = alloc(ctx, 256, &e->position)) || (st = alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->tokens)) ||
+        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, splits), &e->attn_scratch)))
+        return bail(st);
+    // Zero state once (outside any graph). Cache contents are otherwise only ever
+    // overwritten, as in the reference (reset leaves stale KV, baselm.rs:616-620).
+    vx_buf *zero[] = {e->hidden, e->norm, e->kv_k, e->kv_v, e->position, e->tokens, e->attn_scratch, e->logits};
+    for (vx_buf *b : zero)
+        if (hipMemsetAsync(b->ptr, 0, b->bytes, ctx->stream) != hipSuccess)
+            return bail(fail(VX_ERR_HIP, "hipMemsetAsync of engine state failed"));
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return bail(fail(VX_ERR_HIP, "engine init sync failed"));
+    *out = e;
+    return VX_OK;
+}
+
+int vx_baselm_destroy(vx_baselm *e) {
+    if (!e) return VX_OK;
+    (void)hipStreamSynchronize(e->ctx->stream);
+    free_all(e);
+    delete e;
+    return VX_OK;
+}
+
+int vx_baselm_reset(vx_baselm *e) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_reset: null engine");
+    e->pos = 0;
+    return VX_OK;
+}
+
+uint32_t vx_baselm_position(const vx_baselm *e) { return e ? e->pos : 0u; }
+
+int vx_baselm_set_position(vx_baselm *e, uint32_t position) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_set_position: null engine");
+    if (position > e->cfg.active_context_length)
+        return fail(VX_ERR_CONTEXT_FULL, "position %u beyond context %u", position, e->cfg.active_context_length);
+    e->pos = position;
+    return VX_OK;
+}
+
+int vx_baselm_decode_token(vx_baselm *e, uint32_t token_id, uint32_t top_k, vx_step_result *res, vx_top_logit *top) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_token: null engine");
+    VX_CHECK(check_token(e, token_id));
+    VX_CHECK(ensure_context(e, 1));
+    const uint32_t position = e->pos;
+    const double t0 = now_ms();
+    VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), position, token_id, 1));
+    VX_CHECK(run_step(e, true, token_id, true));
+    VX_CHECK(vx_sync(e->ctx));
+    const double elapsed = now_ms() - t0;
+    e->pos += 1;
+    return collect_result(e, position, elapsed, top_k, res, top);
+}
+
+int vx_baselm_decode_embedding(vx_baselm *e, const float *embedding, uint32_t n, uint32_t top_k,
+                               vx_step_result *res, vx_top_logit *top) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_embedding: null engine");
+    VX_CHECK(ensure_context(e, 1));
+    VX_CHECK(upload_embedding(e, embedding, n));
+    const uint32_t position = e->pos;
+    const double t0 = now_ms();
+    VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), position, 0, 0));
+    VX_CHECK(run_step(e, false, 0, true));
+    VX_CHECK(vx_sync(e->ctx));
+    const double elapsed = now_ms() - t0;
+    e->pos += 1;
+    return collect_result(e, position, elapsed, top_k, res, top);
+}
+
+int vx_baselm_decode_token_gpu_only(vx_baselm *e, uint32_t token_id, uint32_t *position_out) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_token_gpu_only: null engine");
+    VX_CHECK(check_token(e, token_id));
+    VX_CHECK(ensure_context(e, 1));
+    const uint32_t position = e->pos;
+    VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), position, token_id, 1));
+    VX_CHECK(run_step(e, true, token_id, false));
+    e->pos += 1;
+    if (position_out) *position_out = position;
+    return VX_OK;
+}
+
+int vx_baselm_decode_embedding_gpu_only(vx_baselm *e, const float *embedding, uint32_t n, uint32_t *position_out) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_embedding_gpu_only: null engine");
+    VX_CHECK(ensure_context(e, 1));
+    VX_CHECK(upload_embedding(e, embedding, n));
+    const uint32_t position = e->pos;
+    VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), position, 0, 0));
+    VX_CHECK(run_step(e, false, 0, false));
+    e->pos += 1;
+    if (position_out) *position_out = position;
+    return VX_OK;
+}
+
+int vx_baselm_decode_embedding_from_gpu_only(vx_baselm *e, const vx_buf *source, uint32_t *position_out) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_embedding_from_gpu_only: null engine");
+    if (!source || source->bytes < (uint64_t)e->cfg.embedding_length * 4u)  // baselm.rs:799-801
+        return fail(VX_ERR_BOUNDS, "GPU embedding source is too small for BaseLM %u-float input",
+                    e->cfg.embedding_length);
+    VX_CHECK(ensure_context(e, 1));
+    const uint32_t position = e->pos;
+    VX_HIP(hipMemcpyAsync(e->hidden->ptr, source->ptr, (size_t)e->cfg.embedding_length * 4u,
+                          hipMemcpyDeviceToDevice, e->ctx->stream));
+    VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), position, 0, 0));
+    VX_CHECK(run_step(e, false, 0, false));
+    e->pos += 1;
+    if (position_out) *position_out = position;
+    return VX_OK;
+}
+
+int vx_baselm_decode_tokens_gpu_only(vx_baselm *e, const uint32_t *tokens, uint32_t n) {
+    if (!e || (!tokens && n)) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_tokens_gpu_only: null argument");
+    if (n == 0) return VX_OK;
+    for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
+    VX_CHECK(ensure_context(e, n));
+    VX_HIP(hipMemcpyAsync(U(e->tokens) + e->pos, tokens, (size_t)n * 4u, hipMemcpyHostToDevice, e->ctx->stream));
+    VX_HIP(hipStreamSynchronize(e->ctx->stream));
+    VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), e->pos, 0, 0));
+    for (uint32_t i = 0; i < n; ++i) {
+        if (e->opt.exec_mode == VX_EXEC_REFERENCE) {
+            VX_CHECK(enqueue_reference(e, e->pos, true, tokens[i], false));
+        } else {
+            VX_CHECK(run_step(e, true, tokens[i], false));
+        }
+        e->pos += 1;
+    }
+    return VX_OK;
+}
+
+int vx_baselm_prefill_tokens(vx_baselm *e, const uint32_t *tokens, uint32_t n, uint32_t top_k_last,
+                             vx_step_result *res, vx_top_logit *top) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_prefill_tokens: null engine");
+    if (!tokens || n == 0) return fail(VX_ERR_INVALID_ARG, "prefill token list is empty");
+    for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
+    VX_CHECK(ensure_context(e, n));
+    // Every token is a decode step (baselm.rs:823-839). Only the last step's
+    // logits are observable, so earlier steps skip the LM head.
+    if (n > 1) VX_CHECK(vx_baselm_decode_tokens_gpu_only(e, tokens, n - 1));
+    return vx_baselm_decode_token(e, tokens[n - 1], top_k_last, res, top);
+}
+
+int vx_baselm_benchmark(vx_baselm *e, uint32_t token_id, uint32_t warmup, uint32_t iterations,
+                        vx_baselm_benchmark_result *out) {
+    if (!e || !out) return fail(VX_ERR_INVALID_ARG, "vx_baselm_benchmark: null argument");
+    if (iterations == 0) return fail(VX_ERR_INVALID_ARG, "benchmark iterations must be > 0");
+    const uint64_t needed = (uint64_t)warmup + iterations;
+    if (needed > e->cfg.active_context_length)
+        return fail(VX_ERR_CONTEXT_FULL, "benchmark needs %llu context positions but --max-context is %u",
+                    (unsigned long long)needed, e->cfg.active_context_length);
+    e->pos = 0;  // reset (baselm.rs:857)
+    for (uint32_t i = 0; i < warmup; ++i) VX_CHECK(vx_baselm_decode_token(e, token_id, 0, nullptr, nullptr));
+    double sum = 0.0, mn = INFINITY, mx = 0.0;
+    for (uint32_t i = 0; i < iterations; ++i) {
+        vx_step_result r;
+        VX_CHECK(vx_baselm_decode_token(e, token_id, 0, &r, nullptr));
+        sum += r.elapsed_ms;
+        mn = std::min(mn, r.elapsed_ms);
+        mx = std::max(mx, r.elapsed_ms);
+    }
+    out->iterations = iterations;
+    out->token_id = token_id;
+    out->mean_ms = sum / iterations;
+    out->min_ms = mn;
+    out->max_ms = mx;
+    out->tokens_per_second = 1000.0 / out->mean_ms;
+    return VX_OK;
+}
+
+vx_buf *vx_baselm_buffer(vx_baselm *e, uint32_t which) {
+    if (!e) return nullptr;
+    switch (which) {
+        case VX_BASELM_BUF_HIDDEN: return e->hidden;
+        case VX_BASELM_BUF_NORM: return e->norm;
+        case VX_BASELM_BUF_Q: return e->q;
+        case VX_BASELM_BUF_K: return e->k;
+        case VX_BASELM_BUF_V: return e->v;
+        case VX_BASELM_BUF_ATTENTION: return e->attention;
+        case VX_BASELM_BUF_GATE: return e->gate;
+        case VX_BASELM_BUF_BRANCH: return e->branch;
+        case VX_BASELM_BUF_LOGITS: return e->logits;
+        case VX_BASELM_BUF_SCORES: return e->scores;
+        case VX_BASELM_BUF_KV_K: return e->kv_k;
+        case VX_BASELM_BUF_KV_V: return e->kv_v;
+        case VX_BASELM_BUF_POSITION: return e->position;
+        default: return nullptr;
+    }
+}
+
+int vx_baselm_profile_steps(vx_baselm *e, const uint32_t *tokens, uint32_t n, vx_prof_entry *out, uint32_t cap,
+                            uint32_t *count) {
+    if (!e || (!tokens && n)) return fail(VX_ERR_INVALID_ARG, "vx_baselm_profile_steps: null argument");
+    for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
+    VX_CHECK(ensure_context(e, n));
+    vx_ctx *ctx = e->ctx;
+    VX_CHECK(vx_prof_reset(ctx));
+    const bool was = ctx->prof_enabled;
+    ctx->prof_enabled = true;
+    int st = VX_OK;
+    for (uint32_t i = 0; i < n && st == VX_OK; ++i) {
+        st = launch_set_step(ctx->stream, U(e->tokens), U(e->position), e->pos, tokens[i], 1);
+        if (st == VX_OK) {
+            if (e->opt.exec_mode == VX_EXEC_REFERENCE)
+                st = enqueue_reference(e, e->pos, true, tokens[i], false);
+            else
+                st = enqueue_fused(e, true, false);
+        }
+        if (st == VX_OK) st = vx_sync(ctx);
+        e->pos += 1;
+    }
+    ctx->prof_enabled = was;
+    VX_CHECK(st);
+    return vx_prof_snapshot(ctx, out, cap, count);
+}
+
+}  // extern "C"

@@ -1,0 +1,684 @@
+// Batch-1 matrix-vector kernels for gfx950 (the HBM-bound "matvec family").
+//
+// Design (one wave64 owns RPW whole rows):
+//   * Lane l of a wave holds a fixed 32-column fragment of x per 2048-column
+//     group in registers and reuses it for every row the wave streams.
+//       Q8_0: columns [2048g + 32l, +32)        (one Q8_0 block per lane)
+//       F16 : columns [2048g + 512k + 8l, +8), k = 0..3
+//     so every weight load instruction of a wave reads 1 KB of contiguous bytes.
+//   * Q8_0 rows come from the repacked layout (model.cpp): per lane and group one
+//     16 B load of the block's low half, one of its high half and one f16 scale.
+//     Bytes are flipped to q+128 and converted with v_cvt_f32_ubyteN; the bias is
+//     removed with the per-lane sum of x: d*(sum (q+128)x - 128 sum x).
+//   * All weight loads of the wave's rows are issued before any arithmetic, then
+//     x is loaded, so HBM latency is paid once per wave.
+//   * fp32 accumulation, wave reduction by lane shuffles, lane 0 runs the epilogue.
+// No MFMA: at batch 1 the arithmetic intensity is ~1 FLOP/byte.
+#include "vx_internal.h"
+
+namespace vx {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float h2f(unsigned short bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+__device__ __forceinline__ float2 h2f2(uint32_t bits) {
+    return make_float2(h2f((unsigned short)(bits & 0xffffu)), h2f((unsigned short)(bits >> 16)));
+}
+
+template <int WT>
+__device__ __forceinline__ uint32_t frag_col(int g, int lane, int j) {
+    if constexpr (WT == WT_Q8)
+        return 2048u * (uint32_t)g + 32u * (uint32_t)lane + (uint32_t)j;
+    else
+        return 2048u * (uint32_t)g + 512u * (uint32_t)(j >> 3) + 8u * (uint32_t)lane +
+               (uint32_t)(j & 7);
+}
+
+template <int NG>
+struct Frag {
+    float v[NG][32];
+};
+
+// Loads are branch-free: an out-of-range element is read from a clamped, valid
+// address and replaced by zero with a select.
+
+// x fragment of a contiguous vector x[0..cols) (cols % 4 == 0, x 16-byte aligned).
+template <int WT, int NG>
+__device__ __forceinline__ void load_frag(Frag<NG> &f, const float *x, uint32_t cols, int lane) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+        for (int j = 0; j < 32; j += 4) {
+            const uint32_t c = frag_col<WT>(g, lane, j);
+            const bool ok = c < cols;
+            const float4 v = *reinterpret_cast<const float4 *>(x + (ok ? c : 0u));
+            f.v[g][j] = ok ? v.x : 0.f;
+            f.v[g][j + 1] = ok ? v.y : 0.f;
+            f.v[g][j + 2] = ok ? v.z : 0.f;
+            f.v[g][j + 3] = ok ? v.w : 0.f;
+        }
+    }
+}
+
+// x fragment of x = xl[0..left) ++ xr[0..cols-left) (fusion_linear.comp:63).
+template <int WT, int NG>
+__device__ __forceinline__ void load_frag_concat(Frag<NG> &f, const float *xl, const float *xr,
+                                                 uint32_t left, uint32_t cols, int lane) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const uint32_t c = frag_col<WT>(g, lane, j);
+            const bool ok = c < cols;
+            const uint32_t cc = ok ? c : 0u;
+            const float *p = cc < left ? xl + cc : xr + (cc - left);
+            const float v = *p;
+            f.v[g][j] = ok ? v : 0.f;
+        }
+    }
+}
+
+// x = rmsnorm(h) * w with the wave covering all of h (rmsnorm.comp:21-42 math).
+template <int WT, int NG>
+__device__ __forceinline__ void load_frag_normed(Frag<NG> &f, const float *h, const float *w,
+                                                 uint32_t cols, float eps, int lane) {
+    Frag<NG> wf;
+    load_frag<WT, NG>(f, h, cols, lane);
+    load_frag<WT, NG>(wf, w, cols, lane);
+    float ss = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int j = 0; j < 32; ++j) ss = fmaf(f.v[g][j], f.v[g][j], ss);
+    ss = wave_sum(ss);
+    const float inv_rms = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int j = 0; j < 32; ++j) f.v[g][j] = f.v[g][j] * inv_rms * wf.v[g][j];
+}
+
+// ---------------------------------------------------------------- Q8_0 rows
+template <int NG>
+struct Q8Row {
+    uint4 lo[NG], hi[NG];
+    unsigned short d[NG];
+};
+
+template <int NG>
+__device__ __forceinline__ void load_row(Q8Row<NG> &r, const WRef &w, uint32_t row, uint32_t cols,
+                                         int lane) {
+    const uint32_t nb = cols >> 5;
+    const int8_t *qrow = static_cast<const int8_t *>(w.ptr) + (size_t)row * cols;
+    const unsigned short *drow = reinterpret_cast<const unsigned short *>(w.d) + (size_t)row * nb;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        int nbg = (int)nb - 64 * g;
+        nbg = nbg > 64 ? 64 : nbg;
+        // Lanes past the row's last block read block 0 of the row and get scale 0,
+        // so they contribute d * (...) = 0.
+        const bool ok = lane < nbg;
+        const int gc = ok ? g : 0;
+        const int nc = ok ? nbg : (nb < 64u ? (int)nb : 64);
+        const int lc = ok ? lane : 0;
+        const int8_t *base = qrow + 2048 * gc;
+        r.lo[g] = *reinterpret_cast<const uint4 *>(base + 16 * lc);
+        r.hi[g] = *reinterpret_cast<const uint4 *>(base + 16 * nc + 16 * lc);
+        const unsigned short dv = drow[64 * gc + lc];
+        r.d[g] = ok ? dv : (unsigned short)0;
+    }
+}
+
+__device__ __forceinline__ float dot16_biased(uint4 q, const float *x) {
+    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u,
+                           q.w ^ 0x80808080u};
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s0 = fmaf((float)(w[i] & 0xffu), x[4 * i + 0], s0);
+        s1 = fmaf((float)((w[i] >> 8) & 0xffu), x[4 * i + 1], s1);
+        s0 = fmaf((float)((w[i] >> 16) & 0xffu), x[4 * i + 2], s0);
+        s1 = fmaf((float)(w[i] >> 24), x[4 * i + 3], s1);
+    }
+    return s0 + s1;
+}
+
+template <int NG>
+__device__ __forceinline__ float row_dot(const Q8Row<NG> &r, const Frag<NG> &f, const float (&sx)[NG]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const float s = dot16_biased(r.lo[g], &f.v[g][0]) + dot16_biased(r.hi[g], &f.v[g][16]);
+        acc = fmaf(h2f(r.d[g]), s - 128.f * sx[g], acc);
+    }
+    return acc;
+}
+
+// ----------------------------------------------------------------- F16 rows
+template <int NG>
+struct F16Row {
+    uint4 c[NG][4];
+};
+
+template <int NG>
+__device__ __forceinline__ void load_row(F16Row<NG> &r, const WRef &w, uint32_t row, uint32_t cols,
+                                         int lane) {
+    const __half *wrow = static_cast<const __half *>(w.ptr) + (size_t)row * cols;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t col = 2048u * g + 512u * k + 8u * lane;
+            const bool ok = col < cols;
+            const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (ok ? col : 0u));
+            r.c[g][k] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+}
+
+
+template <int NG>
+__device__ __forceinline__ float row_dot(const F16Row<NG> &r, const Frag<NG> &f, const float (&)[NG]) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t u[4] = {r.c[g][k].x, r.c[g][k].y, r.c[g][k].z, r.c[g][k].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 wv = h2f2(u[i]);
+                s0 = fmaf(wv.x, f.v[g][8 * k + 2 * i], s0);
+                s1 = fmaf(wv.y, f.v[g][8 * k + 2 * i + 1], s1);
+            }
+        }
+    return s0 + s1;
+}
+
+template <int WT, int NG>
+using RowT = typename std::conditional<WT == WT_Q8, Q8Row<NG>, F16Row<NG>>::type;
+
+template <int NG>
+__device__ __forceinline__ void frag_sums(const Frag<NG> &f, float (&sx)[NG]) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) s += f.v[g][j];
+        sx[g] = s;
+    }
+}
+
+// ------------------------------------------------------------ plain matvec
+struct MvArgs {
+    WRef w;
+    const float *xl, *xr;
+    uint32_t left, rows, cols, row_base;
+    float alpha;
+    int epi;
+    const void *bias;
+    uint32_t bias_dtype;
+    float *y, *y2;
+    float scale;
+    int concat;  // x is xl ++ xr rather than one aligned vector
+};
+
+__device__ __forceinline__ float load_bias(const void *bias, uint32_t dtype, uint32_t row) {
+    if (dtype == 0u) return static_cast<const float *>(bias)[row];
+    if (dtype == 1u) return h2f(static_cast<const unsigned short *>(bias)[row]);
+    return 0.f;
+}
+
+__device__ __forceinline__ void mv_epilogue(const MvArgs &a, uint32_t row, float acc) {
+    switch (a.epi) {
+        case EPI_STORE:  // matvec.comp:61
+            a.y[row] = acc * a.alpha;
+            break;
+        case EPI_BIAS:  // linear_bias.comp:78-81
+            a.y[row] = (acc + load_bias(a.bias, a.bias_dtype, row)) * a.alpha;
+            break;
+        case EPI_FUSION: {  // fusion_linear.comp:72-77
+            const float b = a.bias_dtype == 0u ? static_cast<const float *>(a.bias)[row]
+                                                : h2f(static_cast<const unsigned short *>(a.bias)[row]);
+            const float v = acc + b;
+            a.y[row] = v;
+            a.y2[row] = v;
+            break;
+        }
+        default:  // EPI_RESIDUAL: residual_rmsnorm.comp:27-28 with branch = acc
+            if (a.y2) a.y2[row] = acc;
+            a.y[row] = a.y[row] + acc * a.scale;
+            break;
+    }
+}
+
+template <int WT, int NG, int RPW>
+__global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
+    if (row0 >= a.rows) return;
+    RowT<WT, NG> r[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+        if (row0 + i < a.rows) load_row(r[i], a.w, row0 + i, a.cols, lane);
+    Frag<NG> f;
+    if (a.concat)
+        load_frag_concat<WT, NG>(f, a.xl, a.xr, a.left, a.cols, lane);
+    else
+        load_frag<WT, NG>(f, a.xl, a.cols, lane);
+    float sx[NG];
+    frag_sums(f, sx);
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) acc[i] = row0 + i < a.rows ? row_dot(r[i], f, sx) : 0.f;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) acc[i] = wave_sum(acc[i]);
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i)
+            if (row0 + i < a.rows) mv_epilogue(a, row0 + i, acc[i]);
+    }
+}
+
+// Reference-shaped fallback for any dtype/shape (matvec.comp / linear_bias.comp):
+// one 256-thread block per row, reading the GGUF layout from the raw region.
+__device__ __forceinline__ float raw_weight(const uint8_t *raw, uint32_t off, uint32_t dtype,
+                                            uint32_t cols, uint32_t row, uint32_t col) {
+    if (dtype == VX_DTYPE_F32) {
+        float v;
+        memcpy(&v, raw + off + ((size_t)row * cols + col) * 4u, 4);
+        return v;
+    }
+    if (dtype == VX_DTYPE_F16)
+        return h2f(*reinterpret_cast<const unsigned short *>(raw + off + ((size_t)row * cols + col) * 2u));
+    const size_t block = (size_t)row * (cols / 32u) + col / 32u;
+    const uint8_t *b = raw + off + block * 34u;
+    const int q = (int)(int8_t)b[2 + (col & 31u)];
+    return h2f((unsigned short)(b[0] | (b[1] << 8))) * (float)q;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+    return t;
+}
+
+__global__ __launch_bounds__(kBlock) void k_matvec_generic(MvArgs a) {
+    __shared__ float red[kBlock / 64];
+    const uint32_t row = a.row_base + blockIdx.x;
+    if (row >= a.rows) return;
+    float s = 0.f;
+    for (uint32_t c = threadIdx.x; c < a.cols; c += kBlock) {
+        const float x = c < a.left ? a.xl[c] : a.xr[c - a.left];
+        s += raw_weight(a.w.raw, a.w.raw_offset, a.w.dtype, a.cols, row, c) * x;
+    }
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) mv_epilogue(a, row, s);
+}
+
+// --------------------------------------------------------------- SwiGLU
+struct SwArgs {
+    WRef g, u;
+    const float *x, *norm;
+    float eps;
+    uint32_t rows, cols, row_base;
+    float *y;
+};
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return (g / (1.0f + expf(-g))) * u;  // matvec_swiglu.comp:67
+}
+
+template <int WT, int NG, int RPW, bool NORM>
+__global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
+    if (row0 >= a.rows) return;
+    RowT<WT, NG> rg[RPW], ru[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+        if (row0 + i < a.rows) {
+            load_row(rg[i], a.g, row0 + i, a.cols, lane);
+            load_row(ru[i], a.u, row0 + i, a.cols, lane);
+        }
+    Frag<NG> f;
+    if constexpr (NORM)
+        load_frag_normed<WT, NG>(f, a.x, a.norm, a.cols, a.eps, lane);
+    else
+        load_frag<WT, NG>(f, a.x, a.cols, lane);
+    float sx[NG];
+    frag_sums(f, sx);
+    float gs[RPW], us[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const bool ok = row0 + i < a.rows;
+        gs[i] = ok ? row_dot(rg[i], f, sx) : 0.f;
+        us[i] = ok ? row_dot(ru[i], f, sx) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        gs[i] = wave_sum(gs[i]);
+        us[i] = wave_sum(us[i]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i)
+            if (row0 + i < a.rows) a.y[row0 + i] = silu_mul(gs[i], us[i]);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_swiglu_generic(SwArgs a) {
+    __shared__ float red[kBlock / 64];
+    __shared__ float inv_s;
+    const uint32_t row = a.row_base + blockIdx.x;
+    if (row >= a.rows) return;
+    float inv_rms = 1.f;
+    if (a.norm) {
+        float ss = 0.f;
+        for (uint32_t c = threadIdx.x; c < a.cols; c += kBlock) ss += a.x[c] * a.x[c];
+        ss = block_sum(ss, red);
+        if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+        __syncthreads();
+        inv_rms = inv_s;
+    }
+    float gs = 0.f, us = 0.f;
+    for (uint32_t c = threadIdx.x; c < a.cols; c += kBlock) {
+        const float x = a.norm ? a.x[c] * inv_rms * a.norm[c] : a.x[c];
+        gs += raw_weight(a.g.raw, a.g.raw_offset, a.g.dtype, a.cols, row, c) * x;
+        us += raw_weight(a.u.raw, a.u.raw_offset, a.u.dtype, a.cols, row, c) * x;
+    }
+    gs = block_sum(gs, red);
+    us = block_sum(us, red);
+    if (threadIdx.x == 0) a.y[row] = silu_mul(gs, us);
+}
+
+// ------------------------------------------- fused rmsnorm+QKV+RoPE+KV store
+struct QkvArgs {
+    WRef q, k, v;
+    const float *hidden, *norm;
+    float eps;
+    uint32_t q_rows, kv_rows, cols, head_dim;
+    const float *factors;
+    float theta, scaling;
+    uint32_t layer, context;
+    float *qo, *ko, *vo;
+    __half *kc, *vc;
+    const uint32_t *position;
+};
+
+// One wave per rotary pair: Q/K rows (i, i + head_dim/2) of a head, or two
+// adjacent V rows. RoPE (rope.comp:28-49) and the f16 cache store
+// (store_kv.comp:21-23) run on the reduced pair in lane 0.
+template <int WT, int NG>
+__global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t p = blockIdx.x * kWavesPerBlock + wave;
+    const uint32_t half_dim = a.head_dim >> 1;
+    const uint32_t pq = a.q_rows >> 1, pk = a.kv_rows >> 1;
+    if (p >= pq + 2u * pk) return;
+    int seg;
+    uint32_t r0, r1;
+    if (p < pq + pk) {
+        seg = p < pq ? 0 : 1;
+        const uint32_t pp = seg == 0 ? p : p - pq;
+        const uint32_t head = pp / half_dim, i = pp % half_dim;
+        r0 = head * a.head_dim + i;
+        r1 = r0 + half_dim;
+    } else {
+        seg = 2;
+        r0 = 2u * (p - pq - pk);
+        r1 = r0 + 1u;
+    }
+    const WRef &w = seg == 0 ? a.q : (seg == 1 ? a.k : a.v);
+    RowT<WT, NG> rr[2];
+    load_row(rr[0], w, r0, a.cols, lane);
+    load_row(rr[1], w, r1, a.cols, lane);
+    Frag<NG> f;
+    load_frag_normed<WT, NG>(f, a.hidden, a.norm, a.cols, a.eps, lane);
+    float sx[NG];
+    frag_sums(f, sx);
+    float v0 = wave_sum(row_dot(rr[0], f, sx));
+    float v1 = wave_sum(row_dot(rr[1], f, sx));
+    if (lane != 0) return;
+    const uint32_t pos = *a.position;
+    if (seg < 2) {
+        const uint32_t i = r0 % a.head_dim;
+        const float ext = a.factors[i];
+        const float exponent = (float)(i * 2u) / (float)a.head_dim;
+        const float inv_freq = 1.0f / powf(a.theta, exponent);
+        const float angle = (float)pos * inv_freq / ext;
+        const float c = cosf(angle) * a.scaling;
+        const float s = sinf(angle) * a.scaling;
+        const float n0 = v0 * c - v1 * s;
+        const float n1 = v1 * c + v0 * s;
+        v0 = n0;
+        v1 = n1;
+    }
+    float *dst = seg == 0 ? a.qo : (seg == 1 ? a.ko : a.vo);
+    dst[r0] = v0;
+    dst[r1] = v1;
+    if (seg > 0 && pos < a.context) {
+        __half *cache = seg == 1 ? a.kc : a.vc;
+        const size_t base = ((size_t)a.layer * a.context + pos) * a.kv_rows;
+        cache[base + r0] = __float2half_rn(v0);
+        cache[base + r1] = __float2half_rn(v1);
+    }
+}
+
+// --------------------------------------------------------------- utility
+__global__ void k_dequant(WRef w, uint32_t rows, uint32_t cols, float *out) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * cols) return;
+    const uint32_t row = (uint32_t)(idx / cols), col = (uint32_t)(idx % cols);
+    float v;
+    if (w.wt == WT_Q8) {
+        const uint32_t nb = cols >> 5;
+        const uint32_t g = col >> 11, jb = (col & 2047u) >> 5, i = col & 31u;
+        int nbg = (int)nb - 64 * (int)g;
+        nbg = nbg > 64 ? 64 : nbg;
+        const int8_t *qrow = static_cast<const int8_t *>(w.ptr) + (size_t)row * cols + 2048u * g;
+        const int8_t q = i < 16u ? qrow[16u * jb + i] : qrow[16u * nbg + 16u * jb + (i - 16u)];
+        const float d = h2f(reinterpret_cast<const unsigned short *>(w.d)[(size_t)row * nb + (col >> 5)]);
+        v = d * (float)q;
+    } else {
+        v = raw_weight(w.raw, w.raw_offset, w.dtype, cols, row, col);
+    }
+    out[idx] = v;
+}
+
+// One thread per Q8_0 block: raw 34-byte GGUF block -> repacked quants + scale.
+__global__ void k_repack_q8(const uint8_t *raw, uint32_t rows, uint32_t cols, int8_t *qs,
+                            unsigned short *d) {
+    const uint32_t nb = cols >> 5;
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= (size_t)rows * nb) return;
+    const uint32_t row = (uint32_t)(b / nb), jb = (uint32_t)(b % nb);
+    const uint32_t g = jb >> 6, j = jb & 63u;
+    int nbg = (int)nb - 64 * (int)g;
+    nbg = nbg > 64 ? 64 : nbg;
+    const unsigned short *src = reinterpret_cast<const unsigned short *>(raw + b * 34u);
+    uint32_t words[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        words[k] = (uint32_t)src[1 + 2 * k] | ((uint32_t)src[2 + 2 * k] << 16);
+    d[b] = src[0];
+    int8_t *qrow = qs + (size_t)row * cols + 2048u * g;
+    uint32_t *lo = reinterpret_cast<uint32_t *>(qrow + 16u * j);
+    uint32_t *hi = reinterpret_cast<uint32_t *>(qrow + 16u * (uint32_t)nbg + 16u * j);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        lo[k] = words[k];
+        hi[k] = words[4 + k];
+    }
+}
+
+template <int WT>
+int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
+    const uint32_t n = a.rows - a.row_base;
+    const bool big = n > 8192u && ng == 1u;
+#define VX_MV(NGV, RPWV)                                                                   \
+    do {                                                                                   \
+        const uint32_t per_block = kWavesPerBlock * (RPWV);                               \
+        k_matvec<WT, NGV, RPWV><<<(n + per_block - 1) / per_block, kBlock, 0, s>>>(a);    \
+    } while (0)
+    switch (ng) {
+        case 1:
+            if (big) VX_MV(1, 4); else VX_MV(1, 2);
+            break;
+        case 2: VX_MV(2, 2); break;
+        case 3: VX_MV(3, 2); break;
+        default: VX_MV(4, 2); break;
+    }
+#undef VX_MV
+    VX_LAUNCHED("k_matvec");
+    return VX_OK;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool fast_weight_ok(const WRef &w, uint32_t cols) {
+    if (w.wt == WT_Q8) return cols % 32u == 0 && aligned16(w.ptr) && ((uintptr_t)w.d & 1u) == 0;
+    if (w.wt == WT_F16) return cols % 8u == 0 && aligned16(w.ptr);
+    return false;
+}
+
+}  // namespace
+
+int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
+    if (l.rows <= l.row_base || l.cols == 0) return VX_OK;
+    MvArgs a{};
+    a.w = l.w;
+    a.xl = l.xl;
+    a.xr = l.xr ? l.xr : l.xl;
+    a.left = l.xr ? l.left_cols : l.cols;
+    a.rows = l.rows;
+    a.cols = l.cols;
+    a.row_base = l.row_base;
+    a.alpha = l.alpha;
+    a.epi = l.epi;
+    a.bias = l.bias;
+    a.bias_dtype = l.bias_dtype;
+    a.y = l.y;
+    a.y2 = l.y2;
+    a.scale = l.scale;
+    a.concat = l.xr != nullptr;
+    const uint32_t ng = (l.cols + 2047u) / 2048u;
+    if (ng <= 4u && fast_weight_ok(l.w, l.cols) && aligned16(l.xl)) {
+        if (l.w.wt == WT_Q8) return dispatch_matvec_ng<WT_Q8>(s, a, ng);
+        return dispatch_matvec_ng<WT_F16>(s, a, ng);
+    }
+    k_matvec_generic<<<l.rows - l.row_base, kBlock, 0, s>>>(a);
+    VX_LAUNCHED("k_matvec_generic");
+    return VX_OK;
+}
+
+int launch_swiglu(hipStream_t s, const SwigluLaunch &l) {
+    if (l.rows <= l.row_base || l.cols == 0) return VX_OK;
+    SwArgs a{l.g, l.u, l.x, l.norm, l.eps, l.rows, l.cols, l.row_base, l.y};
+    const uint32_t ng = (l.cols + 2047u) / 2048u;
+    const uint32_t n = l.rows - l.row_base;
+    const bool fast = ng <= 4u && l.g.wt == l.u.wt && fast_weight_ok(l.g, l.cols) &&
+                      fast_weight_ok(l.u, l.cols) && aligned16(l.x) && (!l.norm || aligned16(l.norm));
+    if (!fast) {
+        k_swiglu_generic<<<n, kBlock, 0, s>>>(a);
+        VX_LAUNCHED("k_swiglu_generic");
+        return VX_OK;
+    }
+    constexpr uint32_t per_block = kWavesPerBlock * 2;
+    const uint32_t grid = (n + per_block - 1) / per_block;
+#define VX_SW(WTV, NGV)                                                         \
+    do {                                                                        \
+        if (l.norm)                                                             \
+            k_swiglu<WTV, NGV, 2, true><<<grid, kBlock, 0, s>>>(a);             \
+        else                                                                    \
+            k_swiglu<WTV, NGV, 2, false><<<grid, kBlock, 0, s>>>(a);            \
+    } while (0)
+    if (l.g.wt == WT_Q8) {
+        switch (ng) {
+            case 1: VX_SW(WT_Q8, 1); break;
+            case 2: VX_SW(WT_Q8, 2); break;
+            case 3: VX_SW(WT_Q8, 3); break;
+            default: VX_SW(WT_Q8, 4); break;
+        }
+    } else {
+        switch (ng) {
+            case 1: VX_SW(WT_F16, 1); break;
+            case 2: VX_SW(WT_F16, 2); break;
+            case 3: VX_SW(WT_F16, 3); break;
+            default: VX_SW(WT_F16, 4); break;
+        }
+    }
+#undef VX_SW
+    VX_LAUNCHED("k_swiglu");
+    return VX_OK;
+}
+
+int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &l) {
+    const uint32_t ng = (l.cols + 2047u) / 2048u;
+    if (ng > 4u || !fast_weight_ok(l.q, l.cols) || !fast_weight_ok(l.k, l.cols) ||
+        !fast_weight_ok(l.v, l.cols) || l.q.wt != l.k.wt || l.q.wt != l.v.wt ||
+        !aligned16(l.hidden) || !aligned16(l.norm) || (l.q_rows & 1u) || (l.kv_rows & 1u) ||
+        (l.head_dim & 1u) || l.head_dim == 0)
+        return fail(VX_ERR_UNSUPPORTED,
+                    "fused QKV needs Q8_0/F16 weights of one dtype, cols <= 8192 and aligned buffers");
+    QkvArgs a{l.q,      l.k,        l.v,       l.hidden,  l.norm,  l.eps,    l.q_rows, l.kv_rows,
+              l.cols,   l.head_dim, l.factors, l.theta,   l.scaling, l.layer, l.context, l.qo,
+              l.ko,     l.vo,       l.kc,      l.vc,      l.position};
+    const uint32_t pairs = (l.q_rows + 2u * l.kv_rows) / 2u;
+    const uint32_t grid = (pairs + kWavesPerBlock - 1) / kWavesPerBlock;
+#define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV><<<grid, kBlock, 0, s>>>(a)
+    if (l.q.wt == WT_Q8) {
+        switch (ng) {
+            case 1: VX_QKV(WT_Q8, 1); break;
+            case 2: VX_QKV(WT_Q8, 2); break;
+            case 3: VX_QKV(WT_Q8, 3); break;
+            default: VX_QKV(WT_Q8, 4); break;
+        }
+    } else {
+        switch (ng) {
+            case 1: VX_QKV(WT_F16, 1); break;
+            case 2: VX_QKV(WT_F16, 2); break;
+            case 3: VX_QKV(WT_F16, 3); break;
+            default: VX_QKV(WT_F16, 4); break;
+        }
+    }
+#undef VX_QKV
+    VX_LAUNCHED("k_qkv_fused");
+    return VX_OK;
+}
+
+int launch_dequant(hipStream_t s, const WRef &w, uint32_t rows, uint32_t cols, float *out) {
+    const size_t n = (size_t)rows * cols;
+    k_dequant<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(w, rows, cols, out);
+    VX_LAUNCHED("k_dequant");
+    return VX_OK;
+}
+
+int launch_repack_q8(hipStream_t s, const uint8_t *raw_tensor, uint32_t rows, uint32_t cols,
+                     int8_t *qs, __half *d) {
+    const size_t nblocks = (size_t)rows * (cols / 32u);
+    if (!nblocks) return VX_OK;
+    k_repack_q8<<<(unsigned)((nblocks + 255) / 256), 256, 0, s>>>(raw_tensor, rows, cols, qs,
+                                                                 reinterpret_cast<unsigned short *>(d));
+    VX_LAUNCHED("k_repack_q8");
+    return VX_OK;
+}
+
+}  // namespace vx

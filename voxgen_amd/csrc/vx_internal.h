@@ -1,0 +1,233 @@
+// Internal declarations shared by the host runtime (.cpp) and kernel (.hip) files
+// of libvoxhip.so. Nothing here is part of the public ABI (include/voxhip.h).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/voxhip.h"
+
+namespace vx {
+
+// ------------------------------------------------------------------ errors
+void set_error_v(const char *fmt, va_list ap);
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define VX_HIP(call)                                                                      \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return ::vx::fail(VX_ERR_HIP, "%s failed: %s (%s:%d)", #call,                 \
+                              hipGetErrorString(e_), __FILE__, __LINE__);                 \
+    } while (0)
+
+#define VX_CHECK(expr)                        \
+    do {                                      \
+        int s_ = (expr);                      \
+        if (s_ != VX_OK) return s_;           \
+    } while (0)
+
+// Launch-error check after a <<<>>> launch.
+#define VX_LAUNCHED(name)                                                                 \
+    do {                                                                                  \
+        hipError_t e_ = hipGetLastError();                                                \
+        if (e_ != hipSuccess)                                                             \
+            return ::vx::fail(VX_ERR_HIP, "launch of %s failed: %s", name,                \
+                              hipGetErrorString(e_));                                     \
+    } while (0)
+
+// ------------------------------------------------------- weight references
+enum WeightType : uint32_t { WT_Q8 = 0, WT_F16 = 1, WT_F32 = 2 };
+
+// A matrix the kernels can stream. Q8_0 matrices are referenced in the repacked
+// layout (see model.cpp): qs = int8 [rows][cols] with each 2048-column group of a
+// row stored as the low 16-byte halves of its blocks followed by the high halves,
+// and d = f16 scales [rows][cols/32]. F16/F32 matrices use the GGUF layout.
+struct WRef {
+    uint32_t wt = WT_F16;        // WeightType of the fast path
+    uint32_t dtype = 1;          // GGML dtype code
+    const void *ptr = nullptr;   // qs (Q8) or element data (F16/F32)
+    const __half *d = nullptr;   // Q8 scales
+    uint32_t rows = 0, cols = 0; // matrix extent available
+    const uint8_t *raw = nullptr;   // raw data region on the device
+    uint32_t raw_offset = 0;        // byte offset of the tensor in the region
+};
+
+// ------------------------------------------------------------- profiling
+struct ProfPending {
+    std::string name;
+    hipEvent_t start, end;
+};
+struct ProfTotal {
+    double total_ms = 0.0;
+    uint64_t calls = 0;
+};
+
+}  // namespace vx
+
+struct vx_buf {
+    void *ptr = nullptr;
+    uint64_t bytes = 0;
+    bool owned = true;
+};
+
+struct vx_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool capturing = false;
+    bool prof_enabled = false;
+    std::vector<vx::ProfPending> prof_pending;
+    std::vector<hipEvent_t> event_pool;
+    std::unordered_map<std::string, vx::ProfTotal> prof_totals;
+    std::vector<std::string> prof_order;
+    hipDeviceProp_t props{};
+};
+
+struct vx_model {
+    vx_ctx *ctx = nullptr;
+    uint8_t *raw = nullptr;       // device copy of the data region
+    uint64_t raw_bytes = 0;
+    uint8_t *packed = nullptr;    // device arena of repacked Q8_0 matrices
+    uint64_t packed_bytes = 0;
+    std::vector<vx_tensor_info> tensors;
+    std::vector<uint64_t> packed_qs;   // per tensor: offset of qs in arena (or UINT64_MAX)
+    std::vector<uint64_t> packed_d;    // per tensor: offset of d in arena
+    std::unordered_map<uint64_t, uint32_t> by_offset;
+    std::unordered_map<std::string, uint32_t> by_name;
+};
+
+struct vx_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace vx {
+
+// ------------------------------------------------------------ runtime glue
+// Profiling span around enqueued work (no-op unless ctx->prof_enabled and not
+// capturing). Mirrors gpu_profile_begin/end (vulkan.rs:587-612).
+class ProfSpan {
+  public:
+    ProfSpan(vx_ctx *ctx, const char *name);
+    ~ProfSpan();
+    ProfSpan(const ProfSpan &) = delete;
+    ProfSpan &operator=(const ProfSpan &) = delete;
+
+  private:
+    vx_ctx *ctx_;
+    hipEvent_t start_ = nullptr;
+    std::string name_;
+};
+int collect_profile(vx_ctx *ctx);
+
+// Model lookups.
+int find_tensor_at(const vx_model *m, uint32_t offset, const vx_tensor_info **out);
+// Resolve a weight matrix at `offset` whose GGUF dims are [cols, >=rows].
+int resolve_matrix(const vx_model *m, uint32_t offset, uint32_t dtype, uint32_t rows, uint32_t cols,
+                   WRef *out, const char *what);
+// Resolve a vector of n elements of `dtype` (0 = F32, 1 = F16) at `offset`.
+int resolve_vector(const vx_model *m, uint32_t offset, uint32_t dtype, uint32_t n,
+                   const void **out, const char *what);
+
+// Buffer validation.
+int need_buf(const vx_buf *b, uint64_t bytes, const char *what);
+
+// ------------------------------------------------------------ launchers
+// Epilogues of the matvec kernel.
+enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_FUSION = 2, EPI_RESIDUAL = 3 };
+
+struct MatvecLaunch {
+    WRef w;
+    const float *xl = nullptr;    // x = xl[0..left_cols) ++ xr
+    const float *xr = nullptr;
+    uint32_t left_cols = 0;
+    uint32_t rows = 0, cols = 0, row_base = 0;
+    float alpha = 1.0f;
+    int epi = EPI_STORE;
+    const void *bias = nullptr;
+    uint32_t bias_dtype = 0;
+    float *y = nullptr;           // STORE/BIAS/FUSION output; RESIDUAL: hidden (in/out)
+    float *y2 = nullptr;          // FUSION snapshot; RESIDUAL: branch (nullable)
+    float scale = 1.0f;           // RESIDUAL scale
+};
+int launch_matvec(hipStream_t s, const MatvecLaunch &a);
+
+struct SwigluLaunch {
+    WRef g, u;
+    const float *x = nullptr;     // plain input, or hidden when norm != nullptr
+    const float *norm = nullptr;  // fused rmsnorm weight (f32), nullable
+    float eps = 0.0f;
+    uint32_t rows = 0, cols = 0, row_base = 0;
+    float *y = nullptr;
+};
+int launch_swiglu(hipStream_t s, const SwigluLaunch &a);
+
+struct QkvFusedLaunch {
+    WRef q, k, v;
+    const float *hidden = nullptr;
+    const float *norm = nullptr;
+    float eps = 0.0f;
+    uint32_t q_rows = 0, kv_rows = 0, cols = 0, head_dim = 0;
+    const float *factors = nullptr;
+    float theta = 10000.0f, scaling = 1.0f;
+    uint32_t layer = 0, context = 0;
+    float *qo = nullptr, *ko = nullptr, *vo = nullptr;
+    __half *kc = nullptr, *vc = nullptr;
+    const uint32_t *position = nullptr;
+};
+int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &a);
+
+struct AttnLaunch {
+    const float *q = nullptr;
+    const __half *kc = nullptr, *vc = nullptr;
+    float *out = nullptr;
+    float *partials = nullptr;
+    uint32_t *counters = nullptr;
+    const uint32_t *position = nullptr;
+    uint32_t layer = 0, context = 0, head_dim = 0, q_heads = 0, kv_heads = 0, splits = 0;
+};
+uint64_t attn_scratch_bytes(uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads, uint32_t splits);
+int launch_attn_decode(hipStream_t s, const AttnLaunch &a);
+
+// Reference-granular kernels.
+int launch_rmsnorm(hipStream_t s, const float *x, float *y, const float *w, uint32_t n, float eps,
+                   uint32_t *advance_position);
+int launch_residual_rmsnorm(hipStream_t s, float *h, const float *branch, float *y, const float *w,
+                            uint32_t n, float eps, float scale);
+int launch_rope(hipStream_t s, float *q, float *k, const float *factors, uint32_t position,
+                const uint32_t *dev_position, uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim,
+                float theta, float scaling);
+int launch_store_kv(hipStream_t s, const float *k, const float *v, __half *kc, __half *vc,
+                    uint32_t layer, uint32_t position, const uint32_t *dev_position,
+                    uint32_t context, uint32_t kv_dim);
+int launch_attn_scores(hipStream_t s, const float *q, const __half *kc, float *scores,
+                       uint32_t layer, uint32_t context, uint32_t position,
+                       const uint32_t *dev_position, uint32_t head_dim, uint32_t q_per_kv,
+                       uint32_t kv_heads, uint32_t q_heads);
+int launch_softmax(hipStream_t s, float *scores, uint32_t heads, uint32_t context,
+                   uint32_t position, const uint32_t *dev_position);
+int launch_attn_values(hipStream_t s, const float *scores, const __half *vc, float *out,
+                       uint32_t layer, uint32_t context, uint32_t position,
+                       const uint32_t *dev_position, uint32_t head_dim, uint32_t q_per_kv,
+                       uint32_t kv_heads, uint32_t q_heads);
+// Token id from `token`, or dev_tokens[dev_position[0]] when dev_tokens is set
+// (tokens_len entries). Ids >= vocab produce NaN rows instead of reading out of range.
+int launch_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, uint32_t dtype,
+                     uint32_t cols, uint32_t token, const uint32_t *dev_tokens,
+                     const uint32_t *dev_position, uint32_t vocab, float alpha, float *hidden,
+                     uint32_t tokens_len = 0);
+int launch_set_step(hipStream_t s, uint32_t *tokens, uint32_t *position, uint32_t pos,
+                    uint32_t token, int write_token);
+int launch_fill_u32(hipStream_t s, uint32_t *dst, uint32_t value, uint64_t count);
+int launch_dequant(hipStream_t s, const WRef &w, uint32_t rows, uint32_t cols, float *out);
+int launch_repack_q8(hipStream_t s, const uint8_t *raw_tensor, uint32_t rows, uint32_t cols,
+                     int8_t *qs, __half *d);
+
+}  // namespace vx

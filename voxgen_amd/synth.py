@@ -1,0 +1,208 @@
+"""Synthetic VoxCPM2 BaseLM models and inputs (no checkpoints are available).
+
+The generator (csrc/synth.c, libvoxsynth.so) is counter-based, so every value is a
+function of (seed, index) and the same model is produced wherever it runs.
+Distributions follow the benchmark workloads:
+  Q8_0 matrices  d = f16(|N(0,1)| * 0.01), q ~ U{-127..127}
+  F16 matrices   N(0, 0.02)
+  token_embd     F16 N(0, 0.02)
+  norm gains     F32 N(1, 0.02)
+  rope factors   F32 ones (LongRoPE with ext == 1)
+Tensor names, dims and dtypes are those BaseLmConfig::from_gguf validates
+(baselm.rs:60-180, 227-262).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+from . import abi
+from .runtime import TensorDesc, storage_bytes
+
+LIB_PATH = Path(__file__).resolve().parent / "libvoxsynth.so"
+ALIGN = 32  # GGUF default general.alignment (gguf.rs:7)
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is missing: run `python voxgen_amd/build.py`")
+        L = C.CDLL(str(LIB_PATH))
+        u64, f32, vp = C.c_uint64, C.c_float, C.c_void_p
+        L.vs_u64.restype = u64
+        L.vs_u64.argtypes = [u64, u64]
+        L.vs_normal.restype = C.c_double
+        L.vs_normal.argtypes = [u64, u64]
+        L.vs_fill_u64.argtypes = [vp, u64, u64, u64]
+        L.vs_fill_normal_f32.argtypes = [vp, u64, u64, f32, f32]
+        L.vs_fill_normal_f16.argtypes = [vp, u64, u64, f32, f32]
+        L.vs_fill_uniform_u32.argtypes = [vp, u64, u64, C.c_uint32]
+        L.vs_fill_q8_0.argtypes = [vp, u64, u64, f32]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray, byte_offset: int = 0) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data + byte_offset)
+
+
+def derive_seed(seed: int, k: int) -> int:
+    return int(lib().vs_u64(seed & 0xFFFFFFFFFFFFFFFF, k))
+
+
+def normal_f32(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().vs_fill_normal_f32(_ptr(out), n, seed, mean, std)
+    return out
+
+
+def normal_f16(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    lib().vs_fill_normal_f16(_ptr(out), n, seed, mean, std)
+    return out.view(np.float16)
+
+
+def uniform_u32(n: int, seed: int, bound: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    lib().vs_fill_uniform_u32(_ptr(out), n, seed, bound)
+    return out
+
+
+def q8_0_blocks(n_blocks: int, seed: int, scale_sigma: float = 0.01) -> np.ndarray:
+    out = np.empty(n_blocks * 34, np.uint8)
+    lib().vs_fill_q8_0(_ptr(out), n_blocks, seed, scale_sigma)
+    return out
+
+
+@dataclass
+class Region:
+    """A GGUF-style data region under construction."""
+    tensors: list = field(default_factory=list)
+    size: int = 0
+
+    def add(self, name: str, ggml_type: int, dims: tuple) -> TensorDesc:
+        off = (self.size + ALIGN - 1) // ALIGN * ALIGN
+        t = TensorDesc(name, ggml_type, tuple(int(d) for d in dims), off)
+        self.tensors.append(t)
+        self.size = off + t.nbytes
+        return t
+
+
+@dataclass
+class SynthModel:
+    data: np.ndarray               # uint8 data region
+    tensors: list                  # TensorDesc list
+    config: dict                   # vx_baselm_config fields
+    metadata: dict                 # GGUF metadata (key -> (gguf type, value))
+
+    def tensor(self, name: str) -> TensorDesc:
+        for t in self.tensors:
+            if t.name == name:
+                return t
+        raise KeyError(name)
+
+    def offset(self, name: str) -> int:
+        return self.tensor(name).offset
+
+
+def baselm_config(layers=28, hidden=2048, ffn=6144, vocab=73448, q_heads=16, kv_heads=2,
+                  head_dim=128, context_length=32768, active_context=None, eps=1e-6,
+                  theta=10000.0, original_context=None, embedding_scale=0.0,
+                  residual_scale=0.0, logit_scale=0.0, tied=True) -> dict:
+    """vx_baselm_config fields. Defaults give rope scaling 1 (context == original)."""
+    if original_context is None:
+        original_context = context_length
+    return dict(context_length=context_length,
+                active_context_length=active_context or min(context_length, 8192),
+                embedding_length=hidden, block_count=layers, feed_forward_length=ffn,
+                vocab_size=vocab, head_count=q_heads, head_count_kv=kv_heads, head_dim=head_dim,
+                kv_dim=kv_heads * head_dim, rms_epsilon=eps, rope_theta=theta,
+                rope_dimension_count=head_dim, rope_original_context_length=original_context,
+                rope_longrope=1, embedding_scale=embedding_scale, residual_scale=residual_scale,
+                logit_scale=logit_scale, tied_output=1 if tied else 0)
+
+
+def build_baselm(config: dict | None = None, seed: int = 0x5EED0002, weight_type: str = "q8_0",
+                 embd_type: str = "f16", q8_scale_sigma: float = 0.01, f16_std: float = 0.02,
+                 with_data: bool = True, **kw) -> SynthModel:
+    """Synthetic MiniCPM4 BaseLM data region with the reference tensor table."""
+    cfg = dict(config or baselm_config(**kw))
+    H, F, V = cfg["embedding_length"], cfg["feed_forward_length"], cfg["vocab_size"]
+    KV, L, hd = cfg["kv_dim"], cfg["block_count"], cfg["head_dim"]
+    wt = abi.DTYPE_Q8_0 if weight_type == "q8_0" else abi.DTYPE_F16
+    et = abi.DTYPE_Q8_0 if embd_type == "q8_0" else abi.DTYPE_F16
+    reg = Region()
+    reg.add("token_embd.weight", et, (H, V))
+    reg.add("output_norm.weight", abi.DTYPE_F32, (H,))
+    reg.add("rope_factors_short.weight", abi.DTYPE_F32, (hd // 2,))
+    reg.add("rope_factors_long.weight", abi.DTYPE_F32, (hd // 2,))
+    if not cfg.get("tied_output", 1):
+        reg.add("output.weight", et, (H, V))
+    for l in range(L):
+        p = f"blk.{l}."
+        reg.add(p + "attn_norm.weight", abi.DTYPE_F32, (H,))
+        reg.add(p + "attn_q.weight", wt, (H, H))
+        reg.add(p + "attn_k.weight", wt, (H, KV))
+        reg.add(p + "attn_v.weight", wt, (H, KV))
+        reg.add(p + "attn_output.weight", wt, (H, H))
+        reg.add(p + "ffn_norm.weight", abi.DTYPE_F32, (H,))
+        reg.add(p + "ffn_gate.weight", wt, (H, F))
+        reg.add(p + "ffn_up.weight", wt, (H, F))
+        reg.add(p + "ffn_down.weight", wt, (F, H))
+    size = (reg.size + 255) // 256 * 256
+    data = np.zeros(size if with_data else 0, np.uint8)
+    if with_data:
+        for i, t in enumerate(reg.tensors):
+            s = derive_seed(seed, i)
+            n = int(np.prod(t.dims))
+            if t.ggml_type == abi.DTYPE_Q8_0:
+                lib().vs_fill_q8_0(_ptr(data, t.offset), n // 32, s, q8_scale_sigma)
+            elif t.name.startswith("rope_factors"):
+                data[t.offset:t.offset + t.nbytes].view(np.float32)[:] = 1.0
+            elif t.ggml_type == abi.DTYPE_F32:
+                lib().vs_fill_normal_f32(_ptr(data, t.offset), n, s, 1.0, 0.02)
+            else:
+                std = 0.02 if t.name in ("token_embd.weight", "output.weight") else f16_std
+                lib().vs_fill_normal_f16(_ptr(data, t.offset), n, s, 0.0, std)
+    meta = gguf_metadata(cfg)
+    return SynthModel(data, reg.tensors, cfg, meta)
+
+
+def gguf_metadata(cfg: dict) -> dict:
+    """Metadata BaseLmConfig::from_gguf reads (baselm.rs:60-99), as (gguf type, value)."""
+    U32, F32, STR = 4, 6, 8
+    m = {
+        "general.architecture": (STR, "minicpm4"),
+        "general.alignment": (U32, ALIGN),
+        "minicpm4.context_length": (U32, cfg["context_length"]),
+        "minicpm4.embedding_length": (U32, cfg["embedding_length"]),
+        "minicpm4.block_count": (U32, cfg["block_count"]),
+        "minicpm4.feed_forward_length": (U32, cfg["feed_forward_length"]),
+        "minicpm4.attention.head_count": (U32, cfg["head_count"]),
+        "minicpm4.attention.head_count_kv": (U32, cfg["head_count_kv"]),
+        "minicpm4.attention.key_length": (U32, cfg["head_dim"]),
+        "minicpm4.rope.dimension_count": (U32, cfg["rope_dimension_count"]),
+        "minicpm4.attention.layer_norm_rms_epsilon": (F32, cfg["rms_epsilon"]),
+        "minicpm4.rope.freq_base": (F32, cfg["rope_theta"]),
+        "minicpm4.rope.scaling.type": (STR, "longrope" if cfg["rope_longrope"] else "none"),
+        "minicpm4.rope.scaling.original_context_length": (U32, cfg["rope_original_context_length"]),
+    }
+    for k in ("embedding_scale", "residual_scale", "logit_scale"):
+        if cfg.get(k):
+            m["minicpm4." + k] = (F32, cfg[k])
+    return m
+
+
+def kv_cache_fill(layers: int, context: int, kv_dim: int, filled: int, seed: int) -> np.ndarray:
+    """Packed f16 cache [layer][context][kv_dim] with N(0,1) in positions < filled."""
+    c = np.zeros((layers, context, kv_dim), np.float16)
+    if filled:
+        v = normal_f16(layers * filled * kv_dim, seed).reshape(layers, filled, kv_dim)
+        c[:, :filled, :] = v
+    return c
