@@ -306,10 +306,10 @@ typedef struct vx_fused_attn_args {
     uint32_t layer, context, head_dim, q_heads, kv_heads;
     uint32_t splits;                /* context splits per kv head (grid = splits x kv_heads) */
 } vx_fused_attn_args;
-/* Split-context single-query attention with an in-kernel combine:
+/* Split-context single-query attention: a partials kernel (online softmax per
+ * context slice, all q heads of a KV head together) and a combine kernel;
  * attn_scores.comp + softmax.comp + attn_values.comp (baselm.rs:969-996).
- * `scratch` must hold vx_fused_attention_scratch_bytes(a) bytes and its first
- * kv_heads u32 words must be zero before the first call (kernels restore it). */
+ * `scratch` must hold vx_fused_attention_scratch_bytes(a) bytes. */
 uint64_t vx_fused_attention_scratch_bytes(const vx_fused_attn_args *a);
 int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, const vx_buf *v_cache,
                        vx_buf *out, vx_buf *scratch, const vx_buf *position,
@@ -334,6 +334,18 @@ typedef struct vx_fused_swiglu_args {
  * matvec_swiglu.comp; baselm.rs:1007-1021). */
 int vx_fused_rms_swiglu(vx_ctx *ctx, const vx_model *model, const vx_buf *hidden, vx_buf *y,
                         const vx_fused_swiglu_args *a);
+
+/* ------------------------------------------------------------------------- */
+/* Diagnostics (no reference counterpart): plain streaming kernels that       */
+/* calibrate the HBM roofline and the PMC byte counters.                      */
+/* ------------------------------------------------------------------------- */
+/* Read `bytes` of src at `offset` (both multiples of 16) with `blocks` x 256
+ * threads and `unroll` (1, 2, 4, 8) 16-byte loads in flight per thread; sink
+ * receives one word per wave (blocks * 16 bytes). */
+int vx_diag_stream_read(vx_ctx *ctx, const vx_buf *src, uint64_t offset, uint64_t bytes, vx_buf *sink,
+                        uint32_t blocks, uint32_t unroll);
+/* Copy `bytes` (multiple of 16) from src to dst with `blocks` x 256 threads. */
+int vx_diag_stream_copy(vx_ctx *ctx, vx_buf *dst, const vx_buf *src, uint64_t bytes, uint32_t blocks);
 
 /* ------------------------------------------------------------------------- */
 /* GGUF (gguf.rs:222-286): host-side parse of a model file.                   */

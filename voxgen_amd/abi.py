@@ -168,6 +168,8 @@ PROTOTYPES = {
     "vx_fused_attention": (i32, [CTX, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP, P(FusedAttnArgs)]),
     "vx_fused_matvec_residual": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, P(FusedResidualArgs)]),
     "vx_fused_rms_swiglu": (i32, [CTX, MODEL, BUFP, BUFP, P(FusedSwigluArgs)]),
+    "vx_diag_stream_read": (i32, [CTX, BUFP, u64, u64, BUFP, u32, u32]),
+    "vx_diag_stream_copy": (i32, [CTX, BUFP, BUFP, u64, u32]),
     "vx_gguf_open": (i32, [C.c_char_p, P(GGUF)]),
     "vx_gguf_close": (i32, [GGUF]),
     "vx_gguf_summary_get": (i32, [GGUF, P(GgufSummary)]),

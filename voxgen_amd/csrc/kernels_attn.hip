@@ -1,13 +1,13 @@
 // Single-query (decode) attention over the packed f16 KV cache.
 //
-// k_attn_decode: grid = splits x kv_heads. Each workgroup takes one KV head and a
-// contiguous slice of the context, stages 32-key tiles of K and V in LDS, and
+// k_attn_partial: grid = splits x kv_heads. Each workgroup takes one KV head and
+// a contiguous slice of the context, stages 32-key tiles of K and V in LDS, and
 // runs all q_per_kv query heads of that KV head against them (the GQA sharing of
-// attn_scores.comp's kvh = qh / q_per_kv), with an online softmax. Partial
-// (max, sum, acc) triples go to scratch; the last workgroup of each KV head (an
-// atomic ticket) merges them and restores its ticket to zero, so the kernel can
-// be replayed inside a graph without a memset node. Mathematically this is
-// attn_scores.comp -> softmax.comp -> attn_values.comp (baselm.rs:969-996).
+// attn_scores.comp's kvh = qh / q_per_kv), with an online softmax, writing a
+// (max, sum, acc) partial per head. k_attn_combine merges the partials of each
+// query head. The kernel boundary orders the two, so no device-scope fence or
+// atomic is needed. Mathematically this is attn_scores.comp -> softmax.comp ->
+// attn_values.comp (baselm.rs:969-996).
 //
 // The reference-granular kernels below keep the exact three-dispatch shape.
 #include <cfloat>
@@ -41,34 +41,43 @@ struct AttnArgs {
     const float *q;
     const __half *kc, *vc;
     float *out, *part;
-    uint32_t *counters;
     const uint32_t *position;
     uint32_t layer, context, q_heads, kv_heads, splits;
 };
 
-// part layout: [kv_heads][splits][qpk][HD + 2] floats: m, l, acc[HD].
+// Split of the context [0, pos] into `active` contiguous chunks, identical in
+// the partial and the combine kernel.
+struct SplitPlan {
+    uint32_t n, active, chunk;
+};
+__device__ __forceinline__ SplitPlan split_plan(const AttnArgs &a) {
+    uint32_t pos = *a.position;
+    if (pos >= a.context) pos = a.context - 1u;
+    SplitPlan p;
+    p.n = pos + 1u;
+    p.active = min(a.splits, (p.n + kTile - 1u) / kTile);
+    p.chunk = (p.n + p.active - 1u) / p.active;
+    return p;
+}
+
+// Partials: part layout [kv_heads][splits][qpk][HD + 2] floats = m, l, acc[HD].
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_partial(AttnArgs a) {
     constexpr int KSTRIDE = HD / 2 + 1;  // words per K row in LDS (+1 word: no bank conflicts)
     __shared__ __align__(16) float qs[kMaxQpk][HD];
     __shared__ __align__(16) uint32_t ks[kTile][KSTRIDE];
     __shared__ __align__(16) __half vs[kTile][HD];
     __shared__ float ps[kMaxQpk][kTile];
     __shared__ float m_s[kMaxQpk], l_s[kMaxQpk], corr_s[kMaxQpk];
-    __shared__ int last_s;
 
     const int tid = threadIdx.x;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y;
     const uint32_t qpk = a.q_heads / a.kv_heads;
     const uint32_t kv_dim = a.kv_heads * HD;
-    uint32_t pos = *a.position;
-    if (pos >= a.context) pos = a.context - 1u;
-    const uint32_t n = pos + 1u;
-    uint32_t active = (n + kTile - 1) / kTile;
-    if (active > a.splits) active = a.splits;
-    const uint32_t chunk = (n + active - 1u) / active;
-    const uint32_t t_begin = split * chunk;
-    const uint32_t t_end = min(n, t_begin + chunk);
+    const SplitPlan plan = split_plan(a);
+    if (split >= plan.active) return;
+    const uint32_t t_begin = split * plan.chunk;
+    const uint32_t t_end = min(plan.n, t_begin + plan.chunk);
     const float inv_sqrt = 1.0f / sqrtf((float)HD);
 
     constexpr int OUT_PER_T = (kMaxQpk * HD) / 256;
@@ -76,119 +85,113 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < OUT_PER_T; ++j) acc[j] = 0.f;
 
-    if (split < active) {
-        for (uint32_t i = tid; i < qpk * HD; i += 256)
-            qs[i / HD][i % HD] = a.q[(size_t)(kvh * qpk + i / HD) * HD + (i % HD)];
-        if (tid < (int)qpk) {
-            m_s[tid] = -FLT_MAX;
-            l_s[tid] = 0.f;
+    for (uint32_t i = tid; i < qpk * HD; i += 256)
+        qs[i / HD][i % HD] = a.q[(size_t)(kvh * qpk + i / HD) * HD + (i % HD)];
+    if (tid < (int)qpk) {
+        m_s[tid] = -FLT_MAX;
+        l_s[tid] = 0.f;
+    }
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += kTile) {
+        const uint32_t nt = min((uint32_t)kTile, t_end - t0);
+        __syncthreads();
+        // Stage K and V rows t0..t0+nt (HD halves each, 16 B per thread-load).
+        constexpr int CHUNKS = HD / 8;
+        for (int i = tid; i < kTile * CHUNKS; i += 256) {
+            const int j = i / CHUNKS, c = i % CHUNKS;
+            const bool ok = (uint32_t)j < nt;
+            const size_t base = ((size_t)a.layer * a.context + t0 + (ok ? j : 0)) * kv_dim + kvh * HD + 8 * c;
+            uint4 kv = *reinterpret_cast<const uint4 *>(a.kc + base);
+            uint4 vv = *reinterpret_cast<const uint4 *>(a.vc + base);
+            if (!ok) kv = vv = make_uint4(0u, 0u, 0u, 0u);
+            ks[j][4 * c + 0] = kv.x;
+            ks[j][4 * c + 1] = kv.y;
+            ks[j][4 * c + 2] = kv.z;
+            ks[j][4 * c + 3] = kv.w;
+            *reinterpret_cast<uint4 *>(&vs[j][8 * c]) = vv;
         }
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += kTile) {
-            const uint32_t nt = min((uint32_t)kTile, t_end - t0);
-            __syncthreads();
-            // Stage K and V rows t0..t0+nt (HD halves each, 16 B per thread-load).
-            constexpr int CHUNKS = HD / 8;  // uint4 per row
-            for (int i = tid; i < kTile * CHUNKS; i += 256) {
-                const int j = i / CHUNKS, c = i % CHUNKS;
-                uint4 kv = make_uint4(0u, 0u, 0u, 0u), vv = make_uint4(0u, 0u, 0u, 0u);
-                if ((uint32_t)j < nt) {
-                    const size_t base = ((size_t)a.layer * a.context + t0 + j) * kv_dim + kvh * HD + 8 * c;
-                    kv = *reinterpret_cast<const uint4 *>(a.kc + base);
-                    vv = *reinterpret_cast<const uint4 *>(a.vc + base);
-                }
-                ks[j][4 * c + 0] = kv.x;
-                ks[j][4 * c + 1] = kv.y;
-                ks[j][4 * c + 2] = kv.z;
-                ks[j][4 * c + 3] = kv.w;
-                *reinterpret_cast<uint4 *>(&vs[j][8 * c]) = vv;
-            }
-            __syncthreads();
-            // Scores for (head h, key j).
-            for (uint32_t idx = tid; idx < qpk * kTile; idx += 256) {
-                const uint32_t h = idx / kTile, j = idx % kTile;
-                float s = -FLT_MAX;
-                if (j < nt) {
-                    float d0 = 0.f, d1 = 0.f;
+        __syncthreads();
+        // Scores: a half-wave (32 lanes) holds one head's 32 keys; the per-head
+        // tile max and exp-sum are half-wave shuffles.
+        for (uint32_t idx = tid; idx < qpk * kTile; idx += 256) {
+            const uint32_t h = idx / kTile, j = idx % kTile;
+            float s = -FLT_MAX;
+            if (j < nt) {
+                float d0 = 0.f, d1 = 0.f;
 #pragma unroll 8
-                    for (int w = 0; w < HD / 2; ++w) {
-                        const float2 kf = h2f2(ks[j][w]);
-                        d0 = fmaf(qs[h][2 * w], kf.x, d0);
-                        d1 = fmaf(qs[h][2 * w + 1], kf.y, d1);
-                    }
-                    s = (d0 + d1) * inv_sqrt;
+                for (int w = 0; w < HD / 2; ++w) {
+                    const float2 kf = h2f2(ks[j][w]);
+                    d0 = fmaf(qs[h][2 * w], kf.x, d0);
+                    d1 = fmaf(qs[h][2 * w + 1], kf.y, d1);
                 }
-                ps[h][j] = s;
+                s = (d0 + d1) * inv_sqrt;
             }
-            __syncthreads();
-            // Online softmax update per head.
-            if (tid < (int)qpk) {
-                const int h = tid;
-                float tmax = -FLT_MAX;
-                for (uint32_t j = 0; j < nt; ++j) tmax = fmaxf(tmax, ps[h][j]);
-                const float m_old = m_s[h];
-                const float m_new = fmaxf(m_old, tmax);
-                const float corr = expf(m_old - m_new);
-                float sum = 0.f;
-                for (uint32_t j = 0; j < nt; ++j) {
-                    const float p = expf(ps[h][j] - m_new);
-                    ps[h][j] = p;
-                    sum += p;
-                }
-                for (uint32_t j = nt; j < (uint32_t)kTile; ++j) ps[h][j] = 0.f;
-                l_s[h] = l_s[h] * corr + sum;
-                m_s[h] = m_new;
-                corr_s[h] = corr;
-            }
-            __syncthreads();
+            float tmax = s;
 #pragma unroll
-            for (int jj = 0; jj < OUT_PER_T; ++jj) {
-                const uint32_t o = tid + 256u * jj;
-                const uint32_t h = o / HD, d = o % HD;
-                if (h < qpk) {
-                    float v = acc[jj] * corr_s[h];
-                    for (uint32_t j = 0; j < nt; ++j) v = fmaf(ps[h][j], __half2float(vs[j][d]), v);
-                    acc[jj] = v;
-                }
+            for (int o = 16; o >= 1; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 32));
+            const float m_old = m_s[h];
+            const float m_new = fmaxf(m_old, tmax);
+            const float p = j < nt ? expf(s - m_new) : 0.f;
+            float psum = p;
+#pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) psum += __shfl_xor(psum, o, 32);
+            ps[h][j] = p;
+            if (j == 0) {
+                const float corr = expf(m_old - m_new);
+                corr_s[h] = corr;
+                l_s[h] = l_s[h] * corr + psum;
+                m_s[h] = m_new;
             }
         }
         __syncthreads();
-        float *part = a.part + ((size_t)(kvh * a.splits + split) * qpk) * (HD + 2);
 #pragma unroll
         for (int jj = 0; jj < OUT_PER_T; ++jj) {
             const uint32_t o = tid + 256u * jj;
             const uint32_t h = o / HD, d = o % HD;
-            if (h < qpk) part[h * (HD + 2) + 2 + d] = acc[jj];
-        }
-        if (tid < (int)qpk) {
-            part[tid * (HD + 2)] = m_s[tid];
-            part[tid * (HD + 2) + 1] = l_s[tid];
+            if (h < qpk) {
+                float v = acc[jj] * corr_s[h];
+                for (uint32_t j = 0; j < nt; ++j) v = fmaf(ps[h][j], __half2float(vs[j][d]), v);
+                acc[jj] = v;
+            }
         }
     }
-    // Completion ticket: the last workgroup of this KV head merges the splits.
-    __threadfence();
     __syncthreads();
-    if (tid == 0) {
-        const uint32_t ticket = atomicAdd(&a.counters[kvh], 1u);
-        last_s = ticket == a.splits - 1u;
-    }
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
-    const float *part0 = a.part + (size_t)kvh * a.splits * qpk * (HD + 2);
-    for (uint32_t o = tid; o < qpk * HD; o += 256) {
+    float *part = a.part + ((size_t)(kvh * a.splits + split) * qpk) * (HD + 2);
+#pragma unroll
+    for (int jj = 0; jj < OUT_PER_T; ++jj) {
+        const uint32_t o = tid + 256u * jj;
         const uint32_t h = o / HD, d = o % HD;
-        float m = -FLT_MAX;
-        for (uint32_t s = 0; s < active; ++s) m = fmaxf(m, part0[(s * qpk + h) * (HD + 2)]);
-        float l = 0.f, v = 0.f;
-        for (uint32_t s = 0; s < active; ++s) {
-            const float *p = part0 + (s * qpk + h) * (HD + 2);
-            const float e = expf(p[0] - m);
-            l = fmaf(p[1], e, l);
-            v = fmaf(p[2 + d], e, v);
-        }
-        a.out[(size_t)(kvh * qpk + h) * HD + d] = v / l;
+        if (h < qpk) part[h * (HD + 2) + 2 + d] = acc[jj];
     }
-    if (tid == 0) atomicExch(&a.counters[kvh], 0u);
+    if (tid < (int)qpk) {
+        part[tid * (HD + 2)] = m_s[tid];
+        part[tid * (HD + 2) + 1] = l_s[tid];
+    }
+}
+
+// Merge the active splits of one query head: one block per head, one lane per dim.
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a) {
+    __shared__ float w_s[1024];
+    __shared__ float inv_l_s;
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const uint32_t qpk = a.q_heads / a.kv_heads;
+    const uint32_t kvh = h / qpk, hh = h % qpk;
+    const SplitPlan plan = split_plan(a);
+    const float *part0 = a.part + ((size_t)kvh * a.splits * qpk + hh) * (HD + 2);
+    const size_t stride = (size_t)qpk * (HD + 2);
+    float m = -FLT_MAX;
+    for (uint32_t s = 0; s < plan.active; ++s) m = fmaxf(m, part0[s * stride]);
+    for (uint32_t s = d; s < plan.active; s += HD) w_s[s] = expf(part0[s * stride] - m);
+    __syncthreads();
+    if (d == 0) {
+        float l = 0.f;
+        for (uint32_t s = 0; s < plan.active; ++s) l = fmaf(part0[s * stride + 1], w_s[s], l);
+        inv_l_s = 1.0f / l;
+    }
+    __syncthreads();
+    float v = 0.f;
+    for (uint32_t s = 0; s < plan.active; ++s) v = fmaf(part0[s * stride + 2 + d], w_s[s], v);
+    a.out[(size_t)h * HD + d] = v * inv_l_s;
 }
 
 // ------------------------------------------------ reference-granular kernels
@@ -269,27 +272,28 @@ __global__ __launch_bounds__(128) void k_attn_values(const float *scores, const 
 }  // namespace
 
 uint64_t attn_scratch_bytes(uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads, uint32_t splits) {
-    const uint64_t counters = 256;  // kv_heads u32 tickets, padded
     const uint64_t qpk = kv_heads ? q_heads / kv_heads : 0;
-    return counters + (uint64_t)kv_heads * splits * qpk * (head_dim + 2u) * 4u;
+    return 256u + (uint64_t)kv_heads * splits * qpk * (head_dim + 2u) * 4u;
 }
 
 int launch_attn_decode(hipStream_t s, const AttnLaunch &l) {
     if (l.kv_heads == 0 || l.q_heads % l.kv_heads || l.q_heads / l.kv_heads > (uint32_t)kMaxQpk)
         return fail(VX_ERR_UNSUPPORTED, "decode attention needs q_heads/kv_heads <= %d", kMaxQpk);
-    if (l.kv_heads > 64u) return fail(VX_ERR_UNSUPPORTED, "decode attention supports <= 64 kv heads");
     if (l.splits == 0 || l.splits > 1024u) return fail(VX_ERR_INVALID_ARG, "splits must be 1..1024");
     if (l.context == 0) return fail(VX_ERR_INVALID_ARG, "context is zero");
     AttnArgs a{l.q, l.kc, l.vc, l.out, reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(l.partials) + 256),
-               l.counters, l.position, l.layer, l.context, l.q_heads, l.kv_heads, l.splits};
+               l.position, l.layer, l.context, l.q_heads, l.kv_heads, l.splits};
     dim3 grid(l.splits, l.kv_heads);
-    if (l.head_dim == 128)
-        k_attn_decode<128><<<grid, 256, 0, s>>>(a);
-    else if (l.head_dim == 64)
-        k_attn_decode<64><<<grid, 256, 0, s>>>(a);
-    else
+    if (l.head_dim == 128) {
+        k_attn_partial<128><<<grid, 256, 0, s>>>(a);
+        k_attn_combine<128><<<l.q_heads, 128, 0, s>>>(a);
+    } else if (l.head_dim == 64) {
+        k_attn_partial<64><<<grid, 256, 0, s>>>(a);
+        k_attn_combine<64><<<l.q_heads, 64, 0, s>>>(a);
+    } else {
         return fail(VX_ERR_UNSUPPORTED, "decode attention supports head_dim 64 or 128, got %u", l.head_dim);
-    VX_LAUNCHED("k_attn_decode");
+    }
+    VX_LAUNCHED("k_attn_partial/k_attn_combine");
     return VX_OK;
 }
 

@@ -28,6 +28,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP reduction of a wave64 (gfx9 row/broadcast controls): quad swaps, row
+// mirrors, then row_bcast15/31 fold the four 16-lane rows into lane 63, which is
+// read back as a wave-uniform value. No LDS traffic.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp<0xb1>(v);         // quad_perm [1,0,3,2]
+    v += dpp<0x4e>(v);         // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);        // row_half_mirror
+    v += dpp<0x140>(v);        // row_mirror
+    v += dpp<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ float h2f(unsigned short bits) {
     return (float)__builtin_bit_cast(_Float16, bits);
 }
@@ -52,22 +70,42 @@ struct Frag {
 // Loads are branch-free: an out-of-range element is read from a clamped, valid
 // address and replaced by zero with a select.
 
-// x fragment of a contiguous vector x[0..cols) (cols % 4 == 0, x 16-byte aligned).
+// x fragment of a contiguous vector x[0..cols) (cols % 4 == 0, x 16-byte aligned):
+// load_frag_raw issues the loads (out-of-range columns read column 0), and
+// mask_frag zeroes those columns once the data is needed, so that no select
+// sits between these loads and the weight loads issued after them.
 template <int WT, int NG>
-__device__ __forceinline__ void load_frag(Frag<NG> &f, const float *x, uint32_t cols, int lane) {
+__device__ __forceinline__ void load_frag_raw(Frag<NG> &f, const float *x, uint32_t cols, int lane) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
         for (int j = 0; j < 32; j += 4) {
             const uint32_t c = frag_col<WT>(g, lane, j);
-            const bool ok = c < cols;
-            const float4 v = *reinterpret_cast<const float4 *>(x + (ok ? c : 0u));
-            f.v[g][j] = ok ? v.x : 0.f;
-            f.v[g][j + 1] = ok ? v.y : 0.f;
-            f.v[g][j + 2] = ok ? v.z : 0.f;
-            f.v[g][j + 3] = ok ? v.w : 0.f;
+            const float4 v = *reinterpret_cast<const float4 *>(x + (c < cols ? c : 0u));
+            f.v[g][j] = v.x;
+            f.v[g][j + 1] = v.y;
+            f.v[g][j + 2] = v.z;
+            f.v[g][j + 3] = v.w;
         }
     }
+}
+
+template <int WT, int NG>
+__device__ __forceinline__ void mask_frag(Frag<NG> &f, uint32_t cols, int lane) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int j = 0; j < 32; j += 4) {
+            const bool ok = frag_col<WT>(g, lane, j) < cols;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) f.v[g][j + t] = ok ? f.v[g][j + t] : 0.f;
+        }
+}
+
+template <int WT, int NG>
+__device__ __forceinline__ void load_frag(Frag<NG> &f, const float *x, uint32_t cols, int lane) {
+    load_frag_raw<WT, NG>(f, x, cols, lane);
+    mask_frag<WT, NG>(f, cols, lane);
 }
 
 // x fragment of x = xl[0..left) ++ xr[0..cols-left) (fusion_linear.comp:63).
@@ -89,18 +127,15 @@ __device__ __forceinline__ void load_frag_concat(Frag<NG> &f, const float *xl, c
 }
 
 // x = rmsnorm(h) * w with the wave covering all of h (rmsnorm.comp:21-42 math).
-template <int WT, int NG>
-__device__ __forceinline__ void load_frag_normed(Frag<NG> &f, const float *h, const float *w,
-                                                 uint32_t cols, float eps, int lane) {
-    Frag<NG> wf;
-    load_frag<WT, NG>(f, h, cols, lane);
-    load_frag<WT, NG>(wf, w, cols, lane);
+// f holds h and wf holds w on entry; f holds x on return.
+template <int NG>
+__device__ __forceinline__ void normalize_frag(Frag<NG> &f, const Frag<NG> &wf, uint32_t cols, float eps) {
     float ss = 0.f;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
         for (int j = 0; j < 32; ++j) ss = fmaf(f.v[g][j], f.v[g][j], ss);
-    ss = wave_sum(ss);
+    ss = wave_sum_dpp(ss);
     const float inv_rms = 1.0f / sqrtf(ss / (float)cols + eps);
 #pragma unroll
     for (int g = 0; g < NG; ++g)
@@ -224,7 +259,6 @@ struct MvArgs {
     const float *xl, *xr;
     uint32_t left, rows, cols, row_base;
     float alpha;
-    int epi;
     const void *bias;
     uint32_t bias_dtype;
     float *y, *y2;
@@ -232,61 +266,68 @@ struct MvArgs {
     int concat;  // x is xl ++ xr rather than one aligned vector
 };
 
-__device__ __forceinline__ float load_bias(const void *bias, uint32_t dtype, uint32_t row) {
-    if (dtype == 0u) return static_cast<const float *>(bias)[row];
-    if (dtype == 1u) return h2f(static_cast<const unsigned short *>(bias)[row]);
-    return 0.f;
-}
+// Epilogue variants are compile-time: each kernel instance has one
+// straight-line epilogue, with no runtime branch on the bias dtype.
+enum Ep : int {
+    EP_STORE = 0,       // y = alpha * acc                      (matvec.comp:61; linear_bias without bias)
+    EP_BIAS_F32,        // y = alpha * (acc + f32 bias)         (linear_bias.comp:78-81)
+    EP_BIAS_F16,        // y = alpha * (acc + f16 bias)
+    EP_FUSION_F32,      // y = snapshot = acc + f32 bias        (fusion_linear.comp:72-77)
+    EP_FUSION_F16,      // y = snapshot = acc + f16 bias
+    EP_RESIDUAL,        // hidden += scale * acc                (residual_rmsnorm.comp:27-28)
+    EP_RESIDUAL_BRANCH  // branch = acc; hidden += scale * acc
+};
 
-__device__ __forceinline__ void mv_epilogue(const MvArgs &a, uint32_t row, float acc) {
-    switch (a.epi) {
-        case EPI_STORE:  // matvec.comp:61
-            a.y[row] = acc * a.alpha;
-            break;
-        case EPI_BIAS:  // linear_bias.comp:78-81
-            a.y[row] = (acc + load_bias(a.bias, a.bias_dtype, row)) * a.alpha;
-            break;
-        case EPI_FUSION: {  // fusion_linear.comp:72-77
-            const float b = a.bias_dtype == 0u ? static_cast<const float *>(a.bias)[row]
-                                                : h2f(static_cast<const unsigned short *>(a.bias)[row]);
-            const float v = acc + b;
-            a.y[row] = v;
-            a.y2[row] = v;
-            break;
-        }
-        default:  // EPI_RESIDUAL: residual_rmsnorm.comp:27-28 with branch = acc
-            if (a.y2) a.y2[row] = acc;
-            a.y[row] = a.y[row] + acc * a.scale;
-            break;
+template <int EP>
+__device__ __forceinline__ void epilogue(const MvArgs &a, uint32_t row, float acc) {
+    if constexpr (EP == EP_STORE) {
+        a.y[row] = acc * a.alpha;
+    } else if constexpr (EP == EP_BIAS_F32) {
+        a.y[row] = (acc + static_cast<const float *>(a.bias)[row]) * a.alpha;
+    } else if constexpr (EP == EP_BIAS_F16) {
+        a.y[row] = (acc + h2f(static_cast<const unsigned short *>(a.bias)[row])) * a.alpha;
+    } else if constexpr (EP == EP_FUSION_F32 || EP == EP_FUSION_F16) {
+        const float b = EP == EP_FUSION_F32 ? static_cast<const float *>(a.bias)[row]
+                                            : h2f(static_cast<const unsigned short *>(a.bias)[row]);
+        const float v = acc + b;
+        a.y[row] = v;
+        a.y2[row] = v;
+    } else {
+        if constexpr (EP == EP_RESIDUAL_BRANCH) a.y2[row] = acc;
+        a.y[row] = a.y[row] + acc * a.scale;
     }
 }
 
-template <int WT, int NG, int RPW>
+// Issue order per wave: x fragment (L2-resident) first, then the weight rows
+// (HBM), so that vmcnt's in-order accounting lets the x math proceed while the
+// weights are in flight. Rows past the end are clamped to a valid row and their
+// results dropped, which keeps every load unconditional.
+template <int WT, int NG, int RPW, int EP>
 __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
     if (row0 >= a.rows) return;
-    RowT<WT, NG> r[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i)
-        if (row0 + i < a.rows) load_row(r[i], a.w, row0 + i, a.cols, lane);
     Frag<NG> f;
     if (a.concat)
         load_frag_concat<WT, NG>(f, a.xl, a.xr, a.left, a.cols, lane);
     else
-        load_frag<WT, NG>(f, a.xl, a.cols, lane);
+        load_frag_raw<WT, NG>(f, a.xl, a.cols, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    RowT<WT, NG> r[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_row(r[i], a.w, min(row0 + i, a.rows - 1u), a.cols, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!a.concat) mask_frag<WT, NG>(f, a.cols, lane);
     float sx[NG];
     frag_sums(f, sx);
     float acc[RPW];
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) acc[i] = row0 + i < a.rows ? row_dot(r[i], f, sx) : 0.f;
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) acc[i] = wave_sum(acc[i]);
+    for (int i = 0; i < RPW; ++i) acc[i] = wave_sum_dpp(row_dot(r[i], f, sx));
     if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < RPW; ++i)
-            if (row0 + i < a.rows) mv_epilogue(a, row0 + i, acc[i]);
+            if (row0 + i < a.rows) epilogue<EP>(a, row0 + i, acc[i]);
     }
 }
 
@@ -318,6 +359,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return t;
 }
 
+template <int EP>
 __global__ __launch_bounds__(kBlock) void k_matvec_generic(MvArgs a) {
     __shared__ float red[kBlock / 64];
     const uint32_t row = a.row_base + blockIdx.x;
@@ -328,7 +370,7 @@ __global__ __launch_bounds__(kBlock) void k_matvec_generic(MvArgs a) {
         s += raw_weight(a.w.raw, a.w.raw_offset, a.w.dtype, a.cols, row, c) * x;
     }
     s = block_sum(s, red);
-    if (threadIdx.x == 0) mv_epilogue(a, row, s);
+    if (threadIdx.x == 0) epilogue<EP>(a, row, s);
 }
 
 // --------------------------------------------------------------- SwiGLU
@@ -350,31 +392,27 @@ __global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
     const int wave = threadIdx.x >> 6;
     const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
     if (row0 >= a.rows) return;
+    Frag<NG> f, wf;
+    load_frag_raw<WT, NG>(f, a.x, a.cols, lane);
+    if constexpr (NORM) load_frag_raw<WT, NG>(wf, a.norm, a.cols, lane);
+    __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> rg[RPW], ru[RPW];
 #pragma unroll
-    for (int i = 0; i < RPW; ++i)
-        if (row0 + i < a.rows) {
-            load_row(rg[i], a.g, row0 + i, a.cols, lane);
-            load_row(ru[i], a.u, row0 + i, a.cols, lane);
-        }
-    Frag<NG> f;
-    if constexpr (NORM)
-        load_frag_normed<WT, NG>(f, a.x, a.norm, a.cols, a.eps, lane);
-    else
-        load_frag<WT, NG>(f, a.x, a.cols, lane);
+    for (int i = 0; i < RPW; ++i) {
+        const uint32_t row = min(row0 + i, a.rows - 1u);
+        load_row(rg[i], a.g, row, a.cols, lane);
+        load_row(ru[i], a.u, row, a.cols, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mask_frag<WT, NG>(f, a.cols, lane);
+    if constexpr (NORM) normalize_frag(f, wf, a.cols, a.eps);
     float sx[NG];
     frag_sums(f, sx);
     float gs[RPW], us[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        const bool ok = row0 + i < a.rows;
-        gs[i] = ok ? row_dot(rg[i], f, sx) : 0.f;
-        us[i] = ok ? row_dot(ru[i], f, sx) : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        gs[i] = wave_sum(gs[i]);
-        us[i] = wave_sum(us[i]);
+        gs[i] = wave_sum_dpp(row_dot(rg[i], f, sx));
+        us[i] = wave_sum_dpp(row_dot(ru[i], f, sx));
     }
     if (lane == 0) {
 #pragma unroll
@@ -447,15 +485,20 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
         r1 = r0 + 1u;
     }
     const WRef &w = seg == 0 ? a.q : (seg == 1 ? a.k : a.v);
+    Frag<NG> f, wf;
+    load_frag_raw<WT, NG>(f, a.hidden, a.cols, lane);
+    load_frag_raw<WT, NG>(wf, a.norm, a.cols, lane);
+    __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> rr[2];
     load_row(rr[0], w, r0, a.cols, lane);
     load_row(rr[1], w, r1, a.cols, lane);
-    Frag<NG> f;
-    load_frag_normed<WT, NG>(f, a.hidden, a.norm, a.cols, a.eps, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mask_frag<WT, NG>(f, a.cols, lane);
+    normalize_frag(f, wf, a.cols, a.eps);
     float sx[NG];
     frag_sums(f, sx);
-    float v0 = wave_sum(row_dot(rr[0], f, sx));
-    float v1 = wave_sum(row_dot(rr[1], f, sx));
+    float v0 = wave_sum_dpp(row_dot(rr[0], f, sx));
+    float v1 = wave_sum_dpp(row_dot(rr[1], f, sx));
     if (lane != 0) return;
     const uint32_t pos = *a.position;
     if (seg < 2) {
@@ -529,14 +572,14 @@ __global__ void k_repack_q8(const uint8_t *raw, uint32_t rows, uint32_t cols, in
     }
 }
 
-template <int WT>
+template <int WT, int EP>
 int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
     const uint32_t n = a.rows - a.row_base;
     const bool big = n > 8192u && ng == 1u;
-#define VX_MV(NGV, RPWV)                                                                   \
-    do {                                                                                   \
-        const uint32_t per_block = kWavesPerBlock * (RPWV);                               \
-        k_matvec<WT, NGV, RPWV><<<(n + per_block - 1) / per_block, kBlock, 0, s>>>(a);    \
+#define VX_MV(NGV, RPWV)                                                                    \
+    do {                                                                                    \
+        const uint32_t per_block = kWavesPerBlock * (RPWV);                                \
+        k_matvec<WT, NGV, RPWV, EP><<<(n + per_block - 1) / per_block, kBlock, 0, s>>>(a);  \
     } while (0)
     switch (ng) {
         case 1:
@@ -548,6 +591,17 @@ int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
     }
 #undef VX_MV
     VX_LAUNCHED("k_matvec");
+    return VX_OK;
+}
+
+template <int EP>
+int launch_matvec_ep(hipStream_t s, const MvArgs &a, const WRef &w, bool fast, uint32_t ng) {
+    if (fast) {
+        if (w.wt == WT_Q8) return dispatch_matvec_ng<WT_Q8, EP>(s, a, ng);
+        return dispatch_matvec_ng<WT_F16, EP>(s, a, ng);
+    }
+    k_matvec_generic<EP><<<a.rows - a.row_base, kBlock, 0, s>>>(a);
+    VX_LAUNCHED("k_matvec_generic");
     return VX_OK;
 }
 
@@ -572,7 +626,6 @@ int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
     a.cols = l.cols;
     a.row_base = l.row_base;
     a.alpha = l.alpha;
-    a.epi = l.epi;
     a.bias = l.bias;
     a.bias_dtype = l.bias_dtype;
     a.y = l.y;
@@ -580,13 +633,23 @@ int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
     a.scale = l.scale;
     a.concat = l.xr != nullptr;
     const uint32_t ng = (l.cols + 2047u) / 2048u;
-    if (ng <= 4u && fast_weight_ok(l.w, l.cols) && aligned16(l.xl)) {
-        if (l.w.wt == WT_Q8) return dispatch_matvec_ng<WT_Q8>(s, a, ng);
-        return dispatch_matvec_ng<WT_F16>(s, a, ng);
+    const bool fast = ng <= 4u && fast_weight_ok(l.w, l.cols) && aligned16(l.xl);
+    const bool has_bias = l.bias != nullptr && l.bias_dtype <= 1u;
+    switch (l.epi) {
+        case EPI_STORE: return launch_matvec_ep<EP_STORE>(s, a, l.w, fast, ng);
+        case EPI_BIAS:
+            if (!has_bias) return launch_matvec_ep<EP_STORE>(s, a, l.w, fast, ng);
+            if (l.bias_dtype == 0u) return launch_matvec_ep<EP_BIAS_F32>(s, a, l.w, fast, ng);
+            return launch_matvec_ep<EP_BIAS_F16>(s, a, l.w, fast, ng);
+        case EPI_FUSION:
+            if (!l.bias || !l.y2) return fail(VX_ERR_INVALID_ARG, "fusion epilogue needs a bias and a snapshot");
+            if (l.bias_dtype == 0u) return launch_matvec_ep<EP_FUSION_F32>(s, a, l.w, fast, ng);
+            return launch_matvec_ep<EP_FUSION_F16>(s, a, l.w, fast, ng);
+        case EPI_RESIDUAL:
+            if (l.y2) return launch_matvec_ep<EP_RESIDUAL_BRANCH>(s, a, l.w, fast, ng);
+            return launch_matvec_ep<EP_RESIDUAL>(s, a, l.w, fast, ng);
+        default: return fail(VX_ERR_INVALID_ARG, "unknown matvec epilogue %d", l.epi);
     }
-    k_matvec_generic<<<l.rows - l.row_base, kBlock, 0, s>>>(a);
-    VX_LAUNCHED("k_matvec_generic");
-    return VX_OK;
 }
 
 int launch_swiglu(hipStream_t s, const SwigluLaunch &l) {
