@@ -50,7 +50,8 @@ struct vx_baselm {
     WRef output;
     const float *output_norm = nullptr, *rope_factors = nullptr;
     float residual_scale = 1.f, embedding_alpha = 1.f, logit_alpha = 1.f, rope_scaling = 1.f;
-    uint32_t splits = 16;
+    uint32_t splits = 8;
+    bool fold_attn_merge = false;  // attention merge folded into the attn_out matvec
     uint32_t pos = 0;
     vx_graph *graphs[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
 };
@@ -207,35 +208,50 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
             a.position = U(e->position);
             VX_CHECK(launch_qkv_fused(s, a));
         }
-        {
-            ProfSpan sp(ctx, "baselm.attention");
-            AttnLaunch a;
-            a.q = F(e->q);
-            a.kc = H(e->kv_k);
-            a.vc = H(e->kv_v);
-            a.out = F(e->attention);
-            a.partials = F(e->attn_scratch);
-            a.counters = U(e->attn_scratch);
-            a.position = U(e->position);
-            a.layer = l;
-            a.context = c.active_context_length;
-            a.head_dim = c.head_dim;
-            a.q_heads = c.head_count;
-            a.kv_heads = c.head_count_kv;
-            a.splits = e->splits;
-            VX_CHECK(launch_attn_decode(s, a));
-        }
-        {
+        AttnLaunch at;
+        at.q = F(e->q);
+        at.kc = H(e->kv_k);
+        at.vc = H(e->kv_v);
+        at.out = F(e->attention);
+        at.partials = F(e->attn_scratch);
+        at.position = U(e->position);
+        at.layer = l;
+        at.context = c.active_context_length;
+        at.head_dim = c.head_dim;
+        at.q_heads = c.head_count;
+        at.kv_heads = c.head_count_kv;
+        at.splits = e->splits;
+        MatvecLaunch ao;
+        ao.w = L.o;
+        ao.xl = F(e->attention);
+        ao.rows = c.embedding_length;
+        ao.cols = c.embedding_length;
+        ao.epi = EPI_RESIDUAL;
+        ao.y = F(e->hidden);
+        ao.scale = e->residual_scale;
+        if (e->fold_attn_merge) {
+            {
+                ProfSpan sp(ctx, "baselm.attention");
+                VX_CHECK(launch_attn_partials(s, at));
+            }
             ProfSpan sp(ctx, "baselm.attn_out");
-            MatvecLaunch a;
-            a.w = L.o;
-            a.xl = F(e->attention);
-            a.rows = c.embedding_length;
-            a.cols = c.embedding_length;
-            a.epi = EPI_RESIDUAL;
-            a.y = F(e->hidden);
-            a.scale = e->residual_scale;
-            VX_CHECK(launch_matvec(s, a));
+            AttnOutLaunch a;
+            a.mv = ao;
+            a.partials = at.partials;
+            a.attn_out = F(e->attention);
+            a.position = at.position;
+            a.context = at.context;
+            a.splits = at.splits;
+            a.q_heads = at.q_heads;
+            a.head_dim = at.head_dim;
+            VX_CHECK(launch_attn_out(s, a));
+        } else {
+            {
+                ProfSpan sp(ctx, "baselm.attention");
+                VX_CHECK(launch_attn_decode(s, at));
+            }
+            ProfSpan sp(ctx, "baselm.attn_out");
+            VX_CHECK(launch_matvec(s, ao));
         }
         {
             ProfSpan sp(ctx, "baselm.swiglu");
@@ -557,9 +573,17 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
     e->embedding_alpha = effective_scale(c.embedding_scale);
     e->logit_alpha = effective_scale(c.logit_scale);
     e->rope_scaling = vx_baselm_rope_scaling_factor(&c);
+    // Context splits of the decode attention: one per 64 positions of the active
+    // context, at most kMaxFoldedSplits so that attn_out can merge them itself.
     uint32_t splits = o.attn_splits;
-    if (splits == 0) splits = std::min<uint32_t>(128u, std::max<uint32_t>(1u, (c.active_context_length + 31u) / 32u));
+    if (splits == 0)
+        splits = std::min<uint32_t>(kMaxFoldedSplits, std::max<uint32_t>(1u, (c.active_context_length + 63u) / 64u));
+    if (splits > kMaxAttnSplits)
+        return bail(fail(VX_ERR_INVALID_ARG, "attn_splits must be at most %u", kMaxAttnSplits));
     e->splits = splits;
+    e->fold_attn_merge = splits <= kMaxFoldedSplits && c.head_count * c.head_dim == c.embedding_length &&
+                         (c.embedding_length == 1024u || c.embedding_length == 2048u) &&
+                         (c.head_dim == 64u || c.head_dim == 128u);
     // Buffers (BaseLmEngine::new, baselm.rs:479-506).
     const uint64_t f = 4;
     const uint64_t cache = vx_baselm_kv_cache_bytes(&c) / 2u;

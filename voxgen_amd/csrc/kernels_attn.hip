@@ -1,13 +1,16 @@
 // Single-query (decode) attention over the packed f16 KV cache.
 //
-// k_attn_partial: grid = splits x kv_heads. Each workgroup takes one KV head and
-// a contiguous slice of the context, stages 32-key tiles of K and V in LDS, and
-// runs all q_per_kv query heads of that KV head against them (the GQA sharing of
-// attn_scores.comp's kvh = qh / q_per_kv), with an online softmax, writing a
-// (max, sum, acc) partial per head. k_attn_combine merges the partials of each
-// query head. The kernel boundary orders the two, so no device-scope fence or
-// atomic is needed. Mathematically this is attn_scores.comp -> softmax.comp ->
-// attn_values.comp (baselm.rs:969-996).
+// k_attn_chunk: grid = splits x q_heads. Each workgroup takes one query head and
+// one contiguous slice of the context [0, position] and runs an online softmax
+// over 64-key tiles of it: the 256 threads are 64 keys x 4 quarters of the head
+// dimension for the scores (a quad reduction per key), then head_dim dims x
+// 256/head_dim key groups for P.V out of LDS. It writes one (max, sum, acc)
+// partial per (head, slice). Every load a tile needs (q, K and V rows) is issued
+// before any of it is used. The GQA map is attn_scores.comp's kvh = qh / q_per_kv.
+// k_attn_combine merges the slices of each head; the engine's decode step folds
+// that merge into the attn_out matvec instead (k_attn_out in kernels_matvec.hip).
+// Mathematically this is attn_scores.comp -> softmax.comp -> attn_values.comp
+// (baselm.rs:969-996).
 //
 // The reference-granular kernels below keep the exact three-dispatch shape.
 #include <cfloat>
@@ -17,8 +20,7 @@
 namespace vx {
 namespace {
 
-constexpr int kTile = 32;
-constexpr int kMaxQpk = 16;
+constexpr int kTile = 64;
 
 __device__ __forceinline__ float2 h2f2(uint32_t bits) {
     const _Float16 lo = __builtin_bit_cast(_Float16, (unsigned short)(bits & 0xffffu));
@@ -45,153 +47,132 @@ struct AttnArgs {
     uint32_t layer, context, q_heads, kv_heads, splits;
 };
 
-// Split of the context [0, pos] into `active` contiguous chunks, identical in
-// the partial and the combine kernel.
-struct SplitPlan {
-    uint32_t n, active, chunk;
-};
-__device__ __forceinline__ SplitPlan split_plan(const AttnArgs &a) {
-    uint32_t pos = *a.position;
-    if (pos >= a.context) pos = a.context - 1u;
-    SplitPlan p;
-    p.n = pos + 1u;
-    p.active = min(a.splits, (p.n + kTile - 1u) / kTile);
-    p.chunk = (p.n + p.active - 1u) / p.active;
-    return p;
-}
-
-// Partials: part layout [kv_heads][splits][qpk][HD + 2] floats = m, l, acc[HD].
+// Partial record of one (head, slice): m, l, 2 pad words, acc[HD] (16-byte aligned acc).
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_partial(AttnArgs a) {
-    constexpr int KSTRIDE = HD / 2 + 1;  // words per K row in LDS (+1 word: no bank conflicts)
-    __shared__ __align__(16) float qs[kMaxQpk][HD];
-    __shared__ __align__(16) uint32_t ks[kTile][KSTRIDE];
+__device__ __forceinline__ float *part_rec(const AttnArgs &a, uint32_t h, uint32_t s) {
+    return a.part + ((size_t)h * a.splits + s) * (HD + 4);
+}
+
+// k_attn_chunk: see the file comment.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
+    constexpr int R = HD / 4;            // dims per quarter (scores)
+    constexpr int KG = 256 / HD;         // key groups (P.V)
+    constexpr int KPG = kTile / KG;      // keys per group
     __shared__ __align__(16) __half vs[kTile][HD];
-    __shared__ float ps[kMaxQpk][kTile];
-    __shared__ float m_s[kMaxQpk], l_s[kMaxQpk], corr_s[kMaxQpk];
+    __shared__ float ps[kTile];
+    __shared__ float red[2][4];
+    __shared__ float accs[256];
 
-    const int tid = threadIdx.x;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y;
-    const uint32_t qpk = a.q_heads / a.kv_heads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t s = blockIdx.x, h = blockIdx.y;
+    const uint32_t kvh = h / (a.q_heads / a.kv_heads);
     const uint32_t kv_dim = a.kv_heads * HD;
-    const SplitPlan plan = split_plan(a);
-    if (split >= plan.active) return;
-    const uint32_t t_begin = split * plan.chunk;
-    const uint32_t t_end = min(plan.n, t_begin + plan.chunk);
+    const int j = tid >> 2, r = tid & 3;
+
+    // q quarter (independent of the position) and the position, issued together.
+    float qv[R];
+#pragma unroll
+    for (int i = 0; i < R; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + r * R + i);
+        qv[i] = v.x;
+        qv[i + 1] = v.y;
+        qv[i + 2] = v.z;
+        qv[i + 3] = v.w;
+    }
+    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
+    if (s >= plan.active) return;
+    const uint32_t t0 = s * plan.chunk;
+    const uint32_t t1 = min(plan.n, t0 + plan.chunk);
     const float inv_sqrt = 1.0f / sqrtf((float)HD);
+    const size_t layer_base = (size_t)a.layer * a.context;
 
-    constexpr int OUT_PER_T = (kMaxQpk * HD) / 256;
-    float acc[OUT_PER_T];
+    float m_run = -FLT_MAX, l_run = 0.f, acc = 0.f;
+    for (uint32_t tb = t0; tb < t1; tb += kTile) {
+        const uint32_t key = tb + (uint32_t)j;
+        const bool valid = key < t1;
+        const size_t row = (layer_base + (valid ? key : t0)) * kv_dim + (size_t)kvh * HD + (size_t)r * R;
+        uint4 kw[R / 8], vw[R / 8];
 #pragma unroll
-    for (int j = 0; j < OUT_PER_T; ++j) acc[j] = 0.f;
-
-    for (uint32_t i = tid; i < qpk * HD; i += 256)
-        qs[i / HD][i % HD] = a.q[(size_t)(kvh * qpk + i / HD) * HD + (i % HD)];
-    if (tid < (int)qpk) {
-        m_s[tid] = -FLT_MAX;
-        l_s[tid] = 0.f;
-    }
-    for (uint32_t t0 = t_begin; t0 < t_end; t0 += kTile) {
-        const uint32_t nt = min((uint32_t)kTile, t_end - t0);
-        __syncthreads();
-        // Stage K and V rows t0..t0+nt (HD halves each, 16 B per thread-load).
-        constexpr int CHUNKS = HD / 8;
-        for (int i = tid; i < kTile * CHUNKS; i += 256) {
-            const int j = i / CHUNKS, c = i % CHUNKS;
-            const bool ok = (uint32_t)j < nt;
-            const size_t base = ((size_t)a.layer * a.context + t0 + (ok ? j : 0)) * kv_dim + kvh * HD + 8 * c;
-            uint4 kv = *reinterpret_cast<const uint4 *>(a.kc + base);
-            uint4 vv = *reinterpret_cast<const uint4 *>(a.vc + base);
-            if (!ok) kv = vv = make_uint4(0u, 0u, 0u, 0u);
-            ks[j][4 * c + 0] = kv.x;
-            ks[j][4 * c + 1] = kv.y;
-            ks[j][4 * c + 2] = kv.z;
-            ks[j][4 * c + 3] = kv.w;
-            *reinterpret_cast<uint4 *>(&vs[j][8 * c]) = vv;
+        for (int i = 0; i < R / 8; ++i) {
+            kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 8 * i);
+            vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 8 * i);
         }
+        // Score of key j: quarter dot product, then a quad reduction.
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < R / 8; ++i) {
+            const uint32_t w4[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float2 kf = h2f2(w4[t]);
+                d0 = fmaf(qv[8 * i + 2 * t], kf.x, d0);
+                d1 = fmaf(qv[8 * i + 2 * t + 1], kf.y, d1);
+            }
+        }
+        float sc = d0 + d1;
+        sc += __shfl_xor(sc, 1, 64);
+        sc += __shfl_xor(sc, 2, 64);
+        sc = valid ? sc * inv_sqrt : -FLT_MAX;
+        // Tile max across the workgroup.
+        const float wm = wave_max(sc);
+        if (lane == 0) red[0][wave] = wm;
         __syncthreads();
-        // Scores: a half-wave (32 lanes) holds one head's 32 keys; the per-head
-        // tile max and exp-sum are half-wave shuffles.
-        for (uint32_t idx = tid; idx < qpk * kTile; idx += 256) {
-            const uint32_t h = idx / kTile, j = idx % kTile;
-            float s = -FLT_MAX;
-            if (j < nt) {
-                float d0 = 0.f, d1 = 0.f;
+        const float tmax = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+        const float m_new = fmaxf(m_run, tmax);
+        const float p = valid ? expf(sc - m_new) : 0.f;
+        // V rows of the tile and p to LDS; each key's p counted once (quarter 0).
+#pragma unroll
+        for (int i = 0; i < R / 8; ++i) *reinterpret_cast<uint4 *>(&vs[j][r * R + 8 * i]) = vw[i];
+        if (r == 0) ps[j] = p;
+        const float ws = wave_sum(r == 0 ? p : 0.f);
+        if (lane == 0) red[1][wave] = ws;
+        __syncthreads();
+        const float tsum = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+        const float corr = expf(m_run - m_new);
+        l_run = l_run * corr + tsum;
+        m_run = m_new;
+        // P.V: thread = (key group, dim).
+        const int d = tid % HD, kg = tid / HD;
+        float v = 0.f;
 #pragma unroll 8
-                for (int w = 0; w < HD / 2; ++w) {
-                    const float2 kf = h2f2(ks[j][w]);
-                    d0 = fmaf(qs[h][2 * w], kf.x, d0);
-                    d1 = fmaf(qs[h][2 * w + 1], kf.y, d1);
-                }
-                s = (d0 + d1) * inv_sqrt;
-            }
-            float tmax = s;
-#pragma unroll
-            for (int o = 16; o >= 1; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 32));
-            const float m_old = m_s[h];
-            const float m_new = fmaxf(m_old, tmax);
-            const float p = j < nt ? expf(s - m_new) : 0.f;
-            float psum = p;
-#pragma unroll
-            for (int o = 16; o >= 1; o >>= 1) psum += __shfl_xor(psum, o, 32);
-            ps[h][j] = p;
-            if (j == 0) {
-                const float corr = expf(m_old - m_new);
-                corr_s[h] = corr;
-                l_s[h] = l_s[h] * corr + psum;
-                m_s[h] = m_new;
-            }
+        for (int jj = 0; jj < KPG; ++jj) {
+            const int k = kg * KPG + jj;
+            v = fmaf(ps[k], __half2float(vs[k][d]), v);
         }
+        acc = acc * corr + v;
         __syncthreads();
-#pragma unroll
-        for (int jj = 0; jj < OUT_PER_T; ++jj) {
-            const uint32_t o = tid + 256u * jj;
-            const uint32_t h = o / HD, d = o % HD;
-            if (h < qpk) {
-                float v = acc[jj] * corr_s[h];
-                for (uint32_t j = 0; j < nt; ++j) v = fmaf(ps[h][j], __half2float(vs[j][d]), v);
-                acc[jj] = v;
-            }
-        }
     }
+    accs[tid] = acc;
     __syncthreads();
-    float *part = a.part + ((size_t)(kvh * a.splits + split) * qpk) * (HD + 2);
+    float *rec = part_rec<HD>(a, h, s);
+    if (tid < HD) {
+        float t = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < OUT_PER_T; ++jj) {
-        const uint32_t o = tid + 256u * jj;
-        const uint32_t h = o / HD, d = o % HD;
-        if (h < qpk) part[h * (HD + 2) + 2 + d] = acc[jj];
+        for (int kg = 0; kg < KG; ++kg) t += accs[kg * HD + tid];
+        rec[4 + tid] = t;
     }
-    if (tid < (int)qpk) {
-        part[tid * (HD + 2)] = m_s[tid];
-        part[tid * (HD + 2) + 1] = l_s[tid];
+    if (tid == 0) {
+        rec[0] = m_run;
+        rec[1] = l_run;
     }
 }
 
-// Merge the active splits of one query head: one block per head, one lane per dim.
+// Merge the active slices of one query head: one block per head, one lane per dim.
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a) {
-    __shared__ float w_s[1024];
-    __shared__ float inv_l_s;
     const uint32_t h = blockIdx.x, d = threadIdx.x;
-    const uint32_t qpk = a.q_heads / a.kv_heads;
-    const uint32_t kvh = h / qpk, hh = h % qpk;
-    const SplitPlan plan = split_plan(a);
-    const float *part0 = a.part + ((size_t)kvh * a.splits * qpk + hh) * (HD + 2);
-    const size_t stride = (size_t)qpk * (HD + 2);
+    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
     float m = -FLT_MAX;
-    for (uint32_t s = 0; s < plan.active; ++s) m = fmaxf(m, part0[s * stride]);
-    for (uint32_t s = d; s < plan.active; s += HD) w_s[s] = expf(part0[s * stride] - m);
-    __syncthreads();
-    if (d == 0) {
-        float l = 0.f;
-        for (uint32_t s = 0; s < plan.active; ++s) l = fmaf(part0[s * stride + 1], w_s[s], l);
-        inv_l_s = 1.0f / l;
+    for (uint32_t s = 0; s < plan.active; ++s) m = fmaxf(m, part_rec<HD>(a, h, s)[0]);
+    float l = 0.f, v = 0.f;
+    for (uint32_t s = 0; s < plan.active; ++s) {
+        const float *rec = part_rec<HD>(a, h, s);
+        const float w = expf(rec[0] - m);
+        l = fmaf(rec[1], w, l);
+        v = fmaf(rec[4 + d], w, v);
     }
-    __syncthreads();
-    float v = 0.f;
-    for (uint32_t s = 0; s < plan.active; ++s) v = fmaf(part0[s * stride + 2 + d], w_s[s], v);
-    a.out[(size_t)h * HD + d] = v * inv_l_s;
+    a.out[(size_t)h * HD + d] = v / l;
 }
 
 // ------------------------------------------------ reference-granular kernels
@@ -272,28 +253,47 @@ __global__ __launch_bounds__(128) void k_attn_values(const float *scores, const 
 }  // namespace
 
 uint64_t attn_scratch_bytes(uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads, uint32_t splits) {
-    const uint64_t qpk = kv_heads ? q_heads / kv_heads : 0;
-    return 256u + (uint64_t)kv_heads * splits * qpk * (head_dim + 2u) * 4u;
+    (void)kv_heads;
+    return 256u + (uint64_t)q_heads * splits * (head_dim + 4u) * 4u;
+}
+
+namespace {
+int attn_validate(const AttnLaunch &l) {
+    if (l.kv_heads == 0 || l.q_heads % l.kv_heads)
+        return fail(VX_ERR_UNSUPPORTED, "decode attention needs q_heads to be a multiple of kv_heads");
+    if (l.splits == 0 || l.splits > kMaxAttnSplits)
+        return fail(VX_ERR_INVALID_ARG, "splits must be 1..%u", kMaxAttnSplits);
+    if (l.context == 0) return fail(VX_ERR_INVALID_ARG, "context is zero");
+    if (l.head_dim != 128 && l.head_dim != 64)
+        return fail(VX_ERR_UNSUPPORTED, "decode attention supports head_dim 64 or 128, got %u", l.head_dim);
+    return VX_OK;
+}
+AttnArgs attn_args(const AttnLaunch &l) {
+    return AttnArgs{l.q, l.kc, l.vc, l.out, reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(l.partials) + 256),
+                    l.position, l.layer, l.context, l.q_heads, l.kv_heads, l.splits};
+}
+}  // namespace
+
+int launch_attn_partials(hipStream_t s, const AttnLaunch &l) {
+    VX_CHECK(attn_validate(l));
+    const AttnArgs a = attn_args(l);
+    dim3 grid(l.splits, l.q_heads);
+    if (l.head_dim == 128)
+        k_attn_chunk<128><<<grid, 256, 0, s>>>(a);
+    else
+        k_attn_chunk<64><<<grid, 256, 0, s>>>(a);
+    VX_LAUNCHED("k_attn_chunk");
+    return VX_OK;
 }
 
 int launch_attn_decode(hipStream_t s, const AttnLaunch &l) {
-    if (l.kv_heads == 0 || l.q_heads % l.kv_heads || l.q_heads / l.kv_heads > (uint32_t)kMaxQpk)
-        return fail(VX_ERR_UNSUPPORTED, "decode attention needs q_heads/kv_heads <= %d", kMaxQpk);
-    if (l.splits == 0 || l.splits > 1024u) return fail(VX_ERR_INVALID_ARG, "splits must be 1..1024");
-    if (l.context == 0) return fail(VX_ERR_INVALID_ARG, "context is zero");
-    AttnArgs a{l.q, l.kc, l.vc, l.out, reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(l.partials) + 256),
-               l.position, l.layer, l.context, l.q_heads, l.kv_heads, l.splits};
-    dim3 grid(l.splits, l.kv_heads);
-    if (l.head_dim == 128) {
-        k_attn_partial<128><<<grid, 256, 0, s>>>(a);
+    VX_CHECK(launch_attn_partials(s, l));
+    const AttnArgs a = attn_args(l);
+    if (l.head_dim == 128)
         k_attn_combine<128><<<l.q_heads, 128, 0, s>>>(a);
-    } else if (l.head_dim == 64) {
-        k_attn_partial<64><<<grid, 256, 0, s>>>(a);
+    else
         k_attn_combine<64><<<l.q_heads, 64, 0, s>>>(a);
-    } else {
-        return fail(VX_ERR_UNSUPPORTED, "decode attention supports head_dim 64 or 128, got %u", l.head_dim);
-    }
-    VX_LAUNCHED("k_attn_partial/k_attn_combine");
+    VX_LAUNCHED("k_attn_combine");
     return VX_OK;
 }
 

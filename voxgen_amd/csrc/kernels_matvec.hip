@@ -1,18 +1,20 @@
 // Batch-1 matrix-vector kernels for gfx950 (the HBM-bound "matvec family").
 //
 // Design (one wave64 owns RPW whole rows):
-//   * Lane l of a wave holds a fixed 32-column fragment of x per 2048-column
-//     group in registers and reuses it for every row the wave streams.
-//       Q8_0: columns [2048g + 32l, +32)        (one Q8_0 block per lane)
-//       F16 : columns [2048g + 512k + 8l, +8), k = 0..3
-//     so every weight load instruction of a wave reads 1 KB of contiguous bytes.
-//   * Q8_0 rows come from the repacked layout (model.cpp): per lane and group one
-//     16 B load of the block's low half, one of its high half and one f16 scale.
-//     Bytes are flipped to q+128 and converted with v_cvt_f32_ubyteN; the bias is
-//     removed with the per-lane sum of x: d*(sum (q+128)x - 128 sum x).
-//   * All weight loads of the wave's rows are issued before any arithmetic, then
-//     x is loaded, so HBM latency is paid once per wave.
-//   * fp32 accumulation, wave reduction by lane shuffles, lane 0 runs the epilogue.
+//   * Columns are taken in 1024-column groups. In each group lane l owns 16
+//     columns whose x values are float4 loads contiguous across the wave:
+//       Q8_0: columns 1024g + 256k + 4l + j      (k, j < 4; fragment index 4k + j)
+//       F16 : columns 1024g + 512h + 8l + j      (h < 2, j < 8; index 8h + j)
+//     The lane keeps these x values in registers for every row the wave streams.
+//   * Q8_0 rows come from the lane-interleaved repack (model.cpp): per lane and
+//     group one 16 B load of quants and one 8 B load of its four block scales,
+//     so every weight load instruction of a wave reads contiguous bytes. Bytes
+//     are flipped to q+128 and converted with v_cvt_f32_ubyteN; the bias is
+//     removed with the per-chunk sum of x: d*(sum (q+128)x - 128 sum x).
+//   * F16 rows: two 16 B loads per lane and group, straight from the GGUF layout.
+//   * All weight loads of the wave's rows are issued before any arithmetic, right
+//     after the x loads, so HBM latency is paid once per wave.
+//   * fp32 accumulation, DPP wave reduction, lane 0 runs the epilogue.
 // No MFMA: at batch 1 the arithmetic intensity is ~1 FLOP/byte.
 #include "vx_internal.h"
 
@@ -21,6 +23,7 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = 256;
+constexpr uint32_t kGroupCols = 1024;
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -54,17 +57,16 @@ __device__ __forceinline__ float2 h2f2(uint32_t bits) {
 }
 
 template <int WT>
-__device__ __forceinline__ uint32_t frag_col(int g, int lane, int j) {
+__device__ __forceinline__ uint32_t frag_col(int g, int lane, int i) {
     if constexpr (WT == WT_Q8)
-        return 2048u * (uint32_t)g + 32u * (uint32_t)lane + (uint32_t)j;
+        return kGroupCols * (uint32_t)g + 256u * (uint32_t)(i >> 2) + 4u * (uint32_t)lane + (uint32_t)(i & 3);
     else
-        return 2048u * (uint32_t)g + 512u * (uint32_t)(j >> 3) + 8u * (uint32_t)lane +
-               (uint32_t)(j & 7);
+        return kGroupCols * (uint32_t)g + 512u * (uint32_t)(i >> 3) + 8u * (uint32_t)lane + (uint32_t)(i & 7);
 }
 
 template <int NG>
 struct Frag {
-    float v[NG][32];
+    float v[NG][16];
 };
 
 // Loads are branch-free: an out-of-range element is read from a clamped, valid
@@ -79,13 +81,13 @@ __device__ __forceinline__ void load_frag_raw(Frag<NG> &f, const float *x, uint3
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
-        for (int j = 0; j < 32; j += 4) {
-            const uint32_t c = frag_col<WT>(g, lane, j);
+        for (int i = 0; i < 16; i += 4) {
+            const uint32_t c = frag_col<WT>(g, lane, i);
             const float4 v = *reinterpret_cast<const float4 *>(x + (c < cols ? c : 0u));
-            f.v[g][j] = v.x;
-            f.v[g][j + 1] = v.y;
-            f.v[g][j + 2] = v.z;
-            f.v[g][j + 3] = v.w;
+            f.v[g][i] = v.x;
+            f.v[g][i + 1] = v.y;
+            f.v[g][i + 2] = v.z;
+            f.v[g][i + 3] = v.w;
         }
     }
 }
@@ -95,10 +97,10 @@ __device__ __forceinline__ void mask_frag(Frag<NG> &f, uint32_t cols, int lane) 
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
-        for (int j = 0; j < 32; j += 4) {
-            const bool ok = frag_col<WT>(g, lane, j) < cols;
+        for (int i = 0; i < 16; i += 4) {
+            const bool ok = frag_col<WT>(g, lane, i) < cols;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) f.v[g][j + t] = ok ? f.v[g][j + t] : 0.f;
+            for (int t = 0; t < 4; ++t) f.v[g][i + t] = ok ? f.v[g][i + t] : 0.f;
         }
 }
 
@@ -115,13 +117,13 @@ __device__ __forceinline__ void load_frag_concat(Frag<NG> &f, const float *xl, c
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const uint32_t c = frag_col<WT>(g, lane, j);
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t c = frag_col<WT>(g, lane, i);
             const bool ok = c < cols;
             const uint32_t cc = ok ? c : 0u;
             const float *p = cc < left ? xl + cc : xr + (cc - left);
             const float v = *p;
-            f.v[g][j] = ok ? v : 0.f;
+            f.v[g][i] = ok ? v : 0.f;
         }
     }
 }
@@ -134,75 +136,79 @@ __device__ __forceinline__ void normalize_frag(Frag<NG> &f, const Frag<NG> &wf, 
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
-        for (int j = 0; j < 32; ++j) ss = fmaf(f.v[g][j], f.v[g][j], ss);
+        for (int i = 0; i < 16; ++i) ss = fmaf(f.v[g][i], f.v[g][i], ss);
     ss = wave_sum_dpp(ss);
     const float inv_rms = 1.0f / sqrtf(ss / (float)cols + eps);
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
-        for (int j = 0; j < 32; ++j) f.v[g][j] = f.v[g][j] * inv_rms * wf.v[g][j];
+        for (int i = 0; i < 16; ++i) f.v[g][i] = f.v[g][i] * inv_rms * wf.v[g][i];
+}
+
+// Per-chunk sums of the x fragment (the Q8_0 bias correction): sx[g][k] is the
+// sum of the four x values lane-chunk k of group g multiplies.
+template <int NG>
+struct FragSums {
+    float s[NG][4];
+};
+template <int NG>
+__device__ __forceinline__ void frag_sums(const Frag<NG> &f, FragSums<NG> &sx) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            sx.s[g][k] = (f.v[g][4 * k] + f.v[g][4 * k + 1]) + (f.v[g][4 * k + 2] + f.v[g][4 * k + 3]);
 }
 
 // ---------------------------------------------------------------- Q8_0 rows
 template <int NG>
 struct Q8Row {
-    uint4 lo[NG], hi[NG];
-    unsigned short d[NG];
+    uint4 q[NG];
+    uint2 d[NG];
 };
 
 template <int NG>
 __device__ __forceinline__ void load_row(Q8Row<NG> &r, const WRef &w, uint32_t row, uint32_t cols,
                                          int lane) {
-    const uint32_t nb = cols >> 5;
     const int8_t *qrow = static_cast<const int8_t *>(w.ptr) + (size_t)row * cols;
-    const unsigned short *drow = reinterpret_cast<const unsigned short *>(w.d) + (size_t)row * nb;
+    const unsigned short *drow = reinterpret_cast<const unsigned short *>(w.d) + (size_t)row * (cols >> 5);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-        int nbg = (int)nb - 64 * g;
-        nbg = nbg > 64 ? 64 : nbg;
-        // Lanes past the row's last block read block 0 of the row and get scale 0,
-        // so they contribute d * (...) = 0.
-        const bool ok = lane < nbg;
-        const int gc = ok ? g : 0;
-        const int nc = ok ? nbg : (nb < 64u ? (int)nb : 64);
-        const int lc = ok ? lane : 0;
-        const int8_t *base = qrow + 2048 * gc;
-        r.lo[g] = *reinterpret_cast<const uint4 *>(base + 16 * lc);
-        r.hi[g] = *reinterpret_cast<const uint4 *>(base + 16 * nc + 16 * lc);
-        const unsigned short dv = drow[64 * gc + lc];
-        r.d[g] = ok ? dv : (unsigned short)0;
+        r.q[g] = *reinterpret_cast<const uint4 *>(qrow + kGroupCols * g + 16 * lane);
+        r.d[g] = *reinterpret_cast<const uint2 *>(drow + 32 * g + 4 * (lane >> 3));
     }
-}
-
-__device__ __forceinline__ float dot16_biased(uint4 q, const float *x) {
-    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u,
-                           q.w ^ 0x80808080u};
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        s0 = fmaf((float)(w[i] & 0xffu), x[4 * i + 0], s0);
-        s1 = fmaf((float)((w[i] >> 8) & 0xffu), x[4 * i + 1], s1);
-        s0 = fmaf((float)((w[i] >> 16) & 0xffu), x[4 * i + 2], s0);
-        s1 = fmaf((float)(w[i] >> 24), x[4 * i + 3], s1);
-    }
-    return s0 + s1;
 }
 
 template <int NG>
-__device__ __forceinline__ float row_dot(const Q8Row<NG> &r, const Frag<NG> &f, const float (&sx)[NG]) {
-    float acc = 0.f;
+__device__ __forceinline__ float row_dot(const Q8Row<NG> &r, const Frag<NG> &f, const FragSums<NG> &sx) {
+    float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-        const float s = dot16_biased(r.lo[g], &f.v[g][0]) + dot16_biased(r.hi[g], &f.v[g][16]);
-        acc = fmaf(h2f(r.d[g]), s - 128.f * sx[g], acc);
+        const uint32_t qw[4] = {r.q[g].x ^ 0x80808080u, r.q[g].y ^ 0x80808080u, r.q[g].z ^ 0x80808080u,
+                                r.q[g].w ^ 0x80808080u};
+        const float dk[4] = {h2f((unsigned short)(r.d[g].x & 0xffffu)), h2f((unsigned short)(r.d[g].x >> 16)),
+                             h2f((unsigned short)(r.d[g].y & 0xffffu)), h2f((unsigned short)(r.d[g].y >> 16))};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float *x = &f.v[g][4 * k];
+            float t0 = (float)(qw[k] & 0xffu) * x[0];
+            float t1 = (float)((qw[k] >> 8) & 0xffu) * x[1];
+            t0 = fmaf((float)((qw[k] >> 16) & 0xffu), x[2], t0);
+            t1 = fmaf((float)(qw[k] >> 24), x[3], t1);
+            const float t = fmaf(-128.f, sx.s[g][k], t0 + t1);
+            if (k & 1)
+                acc1 = fmaf(dk[k], t, acc1);
+            else
+                acc0 = fmaf(dk[k], t, acc0);
+        }
     }
-    return acc;
+    return acc0 + acc1;
 }
 
 // ----------------------------------------------------------------- F16 rows
 template <int NG>
 struct F16Row {
-    uint4 c[NG][4];
+    uint4 c[NG][2];
 };
 
 template <int NG>
@@ -212,28 +218,27 @@ __device__ __forceinline__ void load_row(F16Row<NG> &r, const WRef &w, uint32_t 
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t col = 2048u * g + 512u * k + 8u * lane;
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t col = kGroupCols * g + 512u * h + 8u * lane;
             const bool ok = col < cols;
             const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (ok ? col : 0u));
-            r.c[g][k] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+            r.c[g][h] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
         }
 }
 
-
 template <int NG>
-__device__ __forceinline__ float row_dot(const F16Row<NG> &r, const Frag<NG> &f, const float (&)[NG]) {
+__device__ __forceinline__ float row_dot(const F16Row<NG> &r, const Frag<NG> &f, const FragSums<NG> &) {
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t u[4] = {r.c[g][k].x, r.c[g][k].y, r.c[g][k].z, r.c[g][k].w};
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t u[4] = {r.c[g][h].x, r.c[g][h].y, r.c[g][h].z, r.c[g][h].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float2 wv = h2f2(u[i]);
-                s0 = fmaf(wv.x, f.v[g][8 * k + 2 * i], s0);
-                s1 = fmaf(wv.y, f.v[g][8 * k + 2 * i + 1], s1);
+                s0 = fmaf(wv.x, f.v[g][8 * h + 2 * i], s0);
+                s1 = fmaf(wv.y, f.v[g][8 * h + 2 * i + 1], s1);
             }
         }
     return s0 + s1;
@@ -241,17 +246,6 @@ __device__ __forceinline__ float row_dot(const F16Row<NG> &r, const Frag<NG> &f,
 
 template <int WT, int NG>
 using RowT = typename std::conditional<WT == WT_Q8, Q8Row<NG>, F16Row<NG>>::type;
-
-template <int NG>
-__device__ __forceinline__ void frag_sums(const Frag<NG> &f, float (&sx)[NG]) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) s += f.v[g][j];
-        sx[g] = s;
-    }
-}
 
 // ------------------------------------------------------------ plain matvec
 struct MvArgs {
@@ -278,30 +272,38 @@ enum Ep : int {
     EP_RESIDUAL_BRANCH  // branch = acc; hidden += scale * acc
 };
 
+// Epilogue operand of a row (old hidden value, or the bias), loaded at kernel
+// start so that no global load sits between the reduction and the store.
 template <int EP>
-__device__ __forceinline__ void epilogue(const MvArgs &a, uint32_t row, float acc) {
+__device__ __forceinline__ float epilogue_operand(const MvArgs &a, uint32_t row) {
+    if constexpr (EP == EP_BIAS_F32 || EP == EP_FUSION_F32) return static_cast<const float *>(a.bias)[row];
+    else if constexpr (EP == EP_BIAS_F16 || EP == EP_FUSION_F16)
+        return h2f(static_cast<const unsigned short *>(a.bias)[row]);
+    else if constexpr (EP == EP_RESIDUAL || EP == EP_RESIDUAL_BRANCH) return a.y[row];
+    else return 0.f;
+}
+
+template <int EP>
+__device__ __forceinline__ void epilogue(const MvArgs &a, uint32_t row, float acc, float op) {
     if constexpr (EP == EP_STORE) {
-        a.y[row] = acc * a.alpha;
-    } else if constexpr (EP == EP_BIAS_F32) {
-        a.y[row] = (acc + static_cast<const float *>(a.bias)[row]) * a.alpha;
-    } else if constexpr (EP == EP_BIAS_F16) {
-        a.y[row] = (acc + h2f(static_cast<const unsigned short *>(a.bias)[row])) * a.alpha;
+        a.y[row] = acc * a.alpha;                        // matvec.comp:61
+    } else if constexpr (EP == EP_BIAS_F32 || EP == EP_BIAS_F16) {
+        a.y[row] = (acc + op) * a.alpha;                 // linear_bias.comp:78-81
     } else if constexpr (EP == EP_FUSION_F32 || EP == EP_FUSION_F16) {
-        const float b = EP == EP_FUSION_F32 ? static_cast<const float *>(a.bias)[row]
-                                            : h2f(static_cast<const unsigned short *>(a.bias)[row]);
-        const float v = acc + b;
+        const float v = acc + op;                        // fusion_linear.comp:72-77
         a.y[row] = v;
         a.y2[row] = v;
     } else {
         if constexpr (EP == EP_RESIDUAL_BRANCH) a.y2[row] = acc;
-        a.y[row] = a.y[row] + acc * a.scale;
+        a.y[row] = op + acc * a.scale;                   // residual_rmsnorm.comp:27-28
     }
 }
 
 // Issue order per wave: x fragment (L2-resident) first, then the weight rows
-// (HBM), so that vmcnt's in-order accounting lets the x math proceed while the
-// weights are in flight. Rows past the end are clamped to a valid row and their
-// results dropped, which keeps every load unconditional.
+// (HBM), then the epilogue operands, so that vmcnt's in-order accounting lets
+// the x math proceed while the weights are in flight. Rows past the end are
+// clamped to a valid row and their results dropped, which keeps every load
+// unconditional.
 template <int WT, int NG, int RPW, int EP>
 __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
     const int lane = threadIdx.x & 63;
@@ -317,9 +319,12 @@ __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
     RowT<WT, NG> r[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) load_row(r[i], a.w, min(row0 + i, a.rows - 1u), a.cols, lane);
+    float op[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) op[i] = epilogue_operand<EP>(a, min(row0 + i, a.rows - 1u));
     __builtin_amdgcn_sched_barrier(0);
     if (!a.concat) mask_frag<WT, NG>(f, a.cols, lane);
-    float sx[NG];
+    FragSums<NG> sx;
     frag_sums(f, sx);
     float acc[RPW];
 #pragma unroll
@@ -327,7 +332,101 @@ __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
     if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < RPW; ++i)
-            if (row0 + i < a.rows) epilogue<EP>(a, row0 + i, acc[i]);
+            if (row0 + i < a.rows) epilogue<EP>(a, row0 + i, acc[i], op[i]);
+    }
+}
+
+// attn_out with the attention merge folded in: hidden += scale * Wo . attn, where
+// attn is merged from the k_attn_chunk partials of every query head. The wave's
+// weight rows are requested first; the 256 threads then merge the partials into
+// LDS (each thread 4*NG consecutive outputs of one head, every split's record
+// loaded before any is used) while those rows stream in, and every wave reads
+// its x fragment from LDS. cols == q_heads * HD == 1024 * NG.
+struct AttnOutArgs {
+    MvArgs mv;
+    float *attn;             // nullable: workgroup 0 also stores the merged vector here
+    const float *part;
+    const uint32_t *position;
+    uint32_t context, splits;
+};
+
+template <int WT, int NG, int RPW, int HD, bool BRANCH>
+__global__ __launch_bounds__(kBlock) void k_attn_out(AttnOutArgs a) {
+    constexpr int E = 4 * NG;  // outputs merged per thread
+    __shared__ __align__(16) float xs[NG * kGroupCols];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const MvArgs &m = a.mv;
+    const uint32_t row0 = (blockIdx.x * kWavesPerBlock + wave) * RPW;  // no early exit: barrier below
+    RowT<WT, NG> r[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_row(r[i], m.w, min(row0 + i, m.rows - 1u), m.cols, lane);
+    float op[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) op[i] = m.y[min(row0 + i, m.rows - 1u)];
+    __builtin_amdgcn_sched_barrier(0);
+    // Merge of the partials (k_attn_combine's arithmetic).
+    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
+    const uint32_t o0 = (uint32_t)(E * tid), hh = o0 / HD, d0 = o0 % HD;
+    float2 ml[kMaxFoldedSplits];
+    float4 av[kMaxFoldedSplits][E / 4];
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+        const float *rec = a.part + ((size_t)hh * a.splits + (s < plan.active ? s : 0u)) * (HD + 4);
+        ml[s] = *reinterpret_cast<const float2 *>(rec);
+#pragma unroll
+        for (int e = 0; e < E / 4; ++e) av[s][e] = *reinterpret_cast<const float4 *>(rec + 4 + d0 + 4 * e);
+    }
+    float mx = -3.402823466e+38f;
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s)
+        if (s < plan.active) mx = fmaxf(mx, ml[s].x);
+    float l = 0.f, o[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0.f;
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+        const float w = s < plan.active ? expf(ml[s].x - mx) : 0.f;
+        l = fmaf(ml[s].y, w, l);
+#pragma unroll
+        for (int e = 0; e < E / 4; ++e) {
+            o[4 * e] = fmaf(av[s][e].x, w, o[4 * e]);
+            o[4 * e + 1] = fmaf(av[s][e].y, w, o[4 * e + 1]);
+            o[4 * e + 2] = fmaf(av[s][e].z, w, o[4 * e + 2]);
+            o[4 * e + 3] = fmaf(av[s][e].w, w, o[4 * e + 3]);
+        }
+    }
+    const float inv_l = 1.0f / l;
+#pragma unroll
+    for (int e = 0; e < E; e += 4)
+    {
+        const float4 v = make_float4(o[e] * inv_l, o[e + 1] * inv_l, o[e + 2] * inv_l, o[e + 3] * inv_l);
+        *reinterpret_cast<float4 *>(&xs[o0 + e]) = v;
+        if (a.attn && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.attn + o0 + e) = v;
+    }
+    __syncthreads();
+    Frag<NG> f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(&xs[frag_col<WT>(g, lane, i)]);
+            f.v[g][i] = v.x;
+            f.v[g][i + 1] = v.y;
+            f.v[g][i + 2] = v.z;
+            f.v[g][i + 3] = v.w;
+        }
+    FragSums<NG> sx;
+    frag_sums(f, sx);
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) acc[i] = wave_sum_dpp(row_dot(r[i], f, sx));
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i)
+            if (row0 + i < m.rows) {
+                if constexpr (BRANCH) m.y2[row0 + i] = acc[i];
+                m.y[row0 + i] = op[i] + acc[i] * m.scale;
+            }
     }
 }
 
@@ -370,7 +469,7 @@ __global__ __launch_bounds__(kBlock) void k_matvec_generic(MvArgs a) {
         s += raw_weight(a.w.raw, a.w.raw_offset, a.w.dtype, a.cols, row, c) * x;
     }
     s = block_sum(s, red);
-    if (threadIdx.x == 0) epilogue<EP>(a, row, s);
+    if (threadIdx.x == 0) epilogue<EP>(a, row, s, epilogue_operand<EP>(a, row));
 }
 
 // --------------------------------------------------------------- SwiGLU
@@ -406,7 +505,7 @@ __global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     mask_frag<WT, NG>(f, a.cols, lane);
     if constexpr (NORM) normalize_frag(f, wf, a.cols, a.eps);
-    float sx[NG];
+    FragSums<NG> sx;
     frag_sums(f, sx);
     float gs[RPW], us[RPW];
 #pragma unroll
@@ -492,18 +591,18 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
     RowT<WT, NG> rr[2];
     load_row(rr[0], w, r0, a.cols, lane);
     load_row(rr[1], w, r1, a.cols, lane);
+    const uint32_t pos = *a.position;
+    const float ext = seg < 2 ? a.factors[r0 % a.head_dim] : 1.f;
     __builtin_amdgcn_sched_barrier(0);
     mask_frag<WT, NG>(f, a.cols, lane);
     normalize_frag(f, wf, a.cols, a.eps);
-    float sx[NG];
+    FragSums<NG> sx;
     frag_sums(f, sx);
     float v0 = wave_sum_dpp(row_dot(rr[0], f, sx));
     float v1 = wave_sum_dpp(row_dot(rr[1], f, sx));
     if (lane != 0) return;
-    const uint32_t pos = *a.position;
     if (seg < 2) {
         const uint32_t i = r0 % a.head_dim;
-        const float ext = a.factors[i];
         const float exponent = (float)(i * 2u) / (float)a.head_dim;
         const float inv_freq = 1.0f / powf(a.theta, exponent);
         const float angle = (float)pos * inv_freq / ext;
@@ -531,51 +630,52 @@ __global__ void k_dequant(WRef w, uint32_t rows, uint32_t cols, float *out) {
     if (idx >= (size_t)rows * cols) return;
     const uint32_t row = (uint32_t)(idx / cols), col = (uint32_t)(idx % cols);
     float v;
-    if (w.wt == WT_Q8) {
-        const uint32_t nb = cols >> 5;
-        const uint32_t g = col >> 11, jb = (col & 2047u) >> 5, i = col & 31u;
-        int nbg = (int)nb - 64 * (int)g;
-        nbg = nbg > 64 ? 64 : nbg;
-        const int8_t *qrow = static_cast<const int8_t *>(w.ptr) + (size_t)row * cols + 2048u * g;
-        const int8_t q = i < 16u ? qrow[16u * jb + i] : qrow[16u * nbg + 16u * jb + (i - 16u)];
-        const float d = h2f(reinterpret_cast<const unsigned short *>(w.d)[(size_t)row * nb + (col >> 5)]);
-        v = d * (float)q;
+    if (w.wt == WT_Q8 && w.ptr) {
+        // Inverse of the repack: column c = 1024g + 256k + 4l + j.
+        const uint32_t g = col >> 10, k = (col >> 8) & 3u, l = (col >> 2) & 63u, j = col & 3u;
+        const int8_t q = static_cast<const int8_t *>(w.ptr)[(size_t)row * cols + 1024u * g + 16u * l + 4u * k + j];
+        const uint32_t m = l >> 3;
+        const unsigned short dbits =
+            reinterpret_cast<const unsigned short *>(w.d)[(size_t)row * (cols >> 5) + 32u * g + 4u * m + k];
+        v = h2f(dbits) * (float)q;
     } else {
         v = raw_weight(w.raw, w.raw_offset, w.dtype, cols, row, col);
     }
     out[idx] = v;
 }
 
-// One thread per Q8_0 block: raw 34-byte GGUF block -> repacked quants + scale.
+// One thread per (row, 1024-column group, lane): gathers the lane's 16 quants of
+// the group from four GGUF blocks and, for lanes 8m, the group's four scales of
+// lane group m. cols % 1024 == 0.
 __global__ void k_repack_q8(const uint8_t *raw, uint32_t rows, uint32_t cols, int8_t *qs,
                             unsigned short *d) {
-    const uint32_t nb = cols >> 5;
-    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= (size_t)rows * nb) return;
-    const uint32_t row = (uint32_t)(b / nb), jb = (uint32_t)(b % nb);
-    const uint32_t g = jb >> 6, j = jb & 63u;
-    int nbg = (int)nb - 64 * (int)g;
-    nbg = nbg > 64 ? 64 : nbg;
-    const unsigned short *src = reinterpret_cast<const unsigned short *>(raw + b * 34u);
-    uint32_t words[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-        words[k] = (uint32_t)src[1 + 2 * k] | ((uint32_t)src[2 + 2 * k] << 16);
-    d[b] = src[0];
-    int8_t *qrow = qs + (size_t)row * cols + 2048u * g;
-    uint32_t *lo = reinterpret_cast<uint32_t *>(qrow + 16u * j);
-    uint32_t *hi = reinterpret_cast<uint32_t *>(qrow + 16u * (uint32_t)nbg + 16u * j);
+    const uint32_t nb = cols >> 5, ng = cols >> 10;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)rows * ng * 64u) return;
+    const uint32_t lane = (uint32_t)(t & 63u);
+    const uint32_t g = (uint32_t)((t >> 6) % ng);
+    const uint32_t row = (uint32_t)((t >> 6) / ng);
+    const uint32_t m = lane >> 3, within = 4u * (lane & 7u);
+    uint32_t words[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        lo[k] = words[k];
-        hi[k] = words[4 + k];
+        const uint8_t *blk = raw + ((size_t)row * nb + 32u * g + 8u * k + m) * 34u;
+        words[k] = (uint32_t)blk[2 + within] | ((uint32_t)blk[3 + within] << 8) |
+                   ((uint32_t)blk[4 + within] << 16) | ((uint32_t)blk[5 + within] << 24);
+        if ((lane & 7u) == 0u)
+            d[(size_t)row * nb + 32u * g + 4u * m + k] = (unsigned short)(blk[0] | (blk[1] << 8));
     }
+    *reinterpret_cast<uint4 *>(qs + (size_t)row * cols + 1024u * g + 16u * lane) =
+        make_uint4(words[0], words[1], words[2], words[3]);
 }
+
+// Column-group counts (cols / 1024, rounded up) with compiled fast paths.
+bool ng_supported(uint32_t ng) { return ng == 1u || ng == 2u || ng == 3u || ng == 4u || ng == 6u || ng == 8u; }
 
 template <int WT, int EP>
 int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
     const uint32_t n = a.rows - a.row_base;
-    const bool big = n > 8192u && ng == 1u;
+    const bool big = n > 8192u && ng <= 2u;
 #define VX_MV(NGV, RPWV)                                                                    \
     do {                                                                                    \
         const uint32_t per_block = kWavesPerBlock * (RPWV);                                \
@@ -585,9 +685,13 @@ int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
         case 1:
             if (big) VX_MV(1, 4); else VX_MV(1, 2);
             break;
-        case 2: VX_MV(2, 2); break;
+        case 2:
+            if (big) VX_MV(2, 4); else VX_MV(2, 2);
+            break;
         case 3: VX_MV(3, 2); break;
-        default: VX_MV(4, 2); break;
+        case 4: VX_MV(4, 2); break;
+        case 6: VX_MV(6, 2); break;
+        default: VX_MV(8, 1); break;
     }
 #undef VX_MV
     VX_LAUNCHED("k_matvec");
@@ -607,8 +711,12 @@ int launch_matvec_ep(hipStream_t s, const MvArgs &a, const WRef &w, bool fast, u
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Fast (wave-per-row) path: Q8_0 in the repacked layout with cols % 1024 == 0,
+// or F16 with cols % 8 == 0; and a compiled column-group count.
 bool fast_weight_ok(const WRef &w, uint32_t cols) {
-    if (w.wt == WT_Q8) return cols % 32u == 0 && aligned16(w.ptr) && ((uintptr_t)w.d & 1u) == 0;
+    if (!ng_supported((cols + kGroupCols - 1) / kGroupCols)) return false;
+    if (w.wt == WT_Q8)
+        return w.ptr && w.d && cols % kGroupCols == 0 && aligned16(w.ptr) && ((uintptr_t)w.d & 7u) == 0;
     if (w.wt == WT_F16) return cols % 8u == 0 && aligned16(w.ptr);
     return false;
 }
@@ -632,8 +740,8 @@ int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
     a.y2 = l.y2;
     a.scale = l.scale;
     a.concat = l.xr != nullptr;
-    const uint32_t ng = (l.cols + 2047u) / 2048u;
-    const bool fast = ng <= 4u && fast_weight_ok(l.w, l.cols) && aligned16(l.xl);
+    const uint32_t ng = (l.cols + kGroupCols - 1) / kGroupCols;
+    const bool fast = fast_weight_ok(l.w, l.cols) && aligned16(l.xl);
     const bool has_bias = l.bias != nullptr && l.bias_dtype <= 1u;
     switch (l.epi) {
         case EPI_STORE: return launch_matvec_ep<EP_STORE>(s, a, l.w, fast, ng);
@@ -655,75 +763,121 @@ int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
 int launch_swiglu(hipStream_t s, const SwigluLaunch &l) {
     if (l.rows <= l.row_base || l.cols == 0) return VX_OK;
     SwArgs a{l.g, l.u, l.x, l.norm, l.eps, l.rows, l.cols, l.row_base, l.y};
-    const uint32_t ng = (l.cols + 2047u) / 2048u;
+    const uint32_t ng = (l.cols + kGroupCols - 1) / kGroupCols;
     const uint32_t n = l.rows - l.row_base;
-    const bool fast = ng <= 4u && l.g.wt == l.u.wt && fast_weight_ok(l.g, l.cols) &&
-                      fast_weight_ok(l.u, l.cols) && aligned16(l.x) && (!l.norm || aligned16(l.norm));
+    const bool fast = l.g.wt == l.u.wt && fast_weight_ok(l.g, l.cols) && fast_weight_ok(l.u, l.cols) &&
+                      aligned16(l.x) && (!l.norm || aligned16(l.norm));
     if (!fast) {
         k_swiglu_generic<<<n, kBlock, 0, s>>>(a);
         VX_LAUNCHED("k_swiglu_generic");
         return VX_OK;
     }
-    constexpr uint32_t per_block = kWavesPerBlock * 2;
-    const uint32_t grid = (n + per_block - 1) / per_block;
-#define VX_SW(WTV, NGV)                                                         \
-    do {                                                                        \
-        if (l.norm)                                                             \
-            k_swiglu<WTV, NGV, 2, true><<<grid, kBlock, 0, s>>>(a);             \
-        else                                                                    \
-            k_swiglu<WTV, NGV, 2, false><<<grid, kBlock, 0, s>>>(a);            \
+#define VX_SW(WTV, NGV, RPWV)                                                                           \
+    do {                                                                                                \
+        const uint32_t grid = (n + kWavesPerBlock * (RPWV) - 1) / (kWavesPerBlock * (RPWV));            \
+        if (l.norm)                                                                                     \
+            k_swiglu<WTV, NGV, RPWV, true><<<grid, kBlock, 0, s>>>(a);                                  \
+        else                                                                                            \
+            k_swiglu<WTV, NGV, RPWV, false><<<grid, kBlock, 0, s>>>(a);                                 \
     } while (0)
-    if (l.g.wt == WT_Q8) {
-        switch (ng) {
-            case 1: VX_SW(WT_Q8, 1); break;
-            case 2: VX_SW(WT_Q8, 2); break;
-            case 3: VX_SW(WT_Q8, 3); break;
-            default: VX_SW(WT_Q8, 4); break;
-        }
-    } else {
-        switch (ng) {
-            case 1: VX_SW(WT_F16, 1); break;
-            case 2: VX_SW(WT_F16, 2); break;
-            case 3: VX_SW(WT_F16, 3); break;
-            default: VX_SW(WT_F16, 4); break;
-        }
+#define VX_SW_NG(WTV)                          \
+    switch (ng) {                              \
+        case 1: VX_SW(WTV, 1, 2); break;       \
+        case 2: VX_SW(WTV, 2, 2); break;       \
+        case 3: VX_SW(WTV, 3, 2); break;       \
+        case 4: VX_SW(WTV, 4, 2); break;       \
+        case 6: VX_SW(WTV, 6, 1); break;       \
+        default: VX_SW(WTV, 8, 1); break;      \
     }
+    if (l.g.wt == WT_Q8) {
+        VX_SW_NG(WT_Q8)
+    } else {
+        VX_SW_NG(WT_F16)
+    }
+#undef VX_SW_NG
 #undef VX_SW
     VX_LAUNCHED("k_swiglu");
     return VX_OK;
 }
 
 int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &l) {
-    const uint32_t ng = (l.cols + 2047u) / 2048u;
-    if (ng > 4u || !fast_weight_ok(l.q, l.cols) || !fast_weight_ok(l.k, l.cols) ||
+    const uint32_t ng = (l.cols + kGroupCols - 1) / kGroupCols;
+    if (!fast_weight_ok(l.q, l.cols) || !fast_weight_ok(l.k, l.cols) ||
         !fast_weight_ok(l.v, l.cols) || l.q.wt != l.k.wt || l.q.wt != l.v.wt ||
         !aligned16(l.hidden) || !aligned16(l.norm) || (l.q_rows & 1u) || (l.kv_rows & 1u) ||
         (l.head_dim & 1u) || l.head_dim == 0)
         return fail(VX_ERR_UNSUPPORTED,
-                    "fused QKV needs Q8_0/F16 weights of one dtype, cols <= 8192 and aligned buffers");
+                    "fused QKV needs Q8_0 (cols %% 1024 == 0) or F16 weights of one dtype, a compiled "
+                    "column count and aligned buffers");
     QkvArgs a{l.q,      l.k,        l.v,       l.hidden,  l.norm,  l.eps,    l.q_rows, l.kv_rows,
               l.cols,   l.head_dim, l.factors, l.theta,   l.scaling, l.layer, l.context, l.qo,
               l.ko,     l.vo,       l.kc,      l.vc,      l.position};
     const uint32_t pairs = (l.q_rows + 2u * l.kv_rows) / 2u;
     const uint32_t grid = (pairs + kWavesPerBlock - 1) / kWavesPerBlock;
 #define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV><<<grid, kBlock, 0, s>>>(a)
-    if (l.q.wt == WT_Q8) {
-        switch (ng) {
-            case 1: VX_QKV(WT_Q8, 1); break;
-            case 2: VX_QKV(WT_Q8, 2); break;
-            case 3: VX_QKV(WT_Q8, 3); break;
-            default: VX_QKV(WT_Q8, 4); break;
-        }
-    } else {
-        switch (ng) {
-            case 1: VX_QKV(WT_F16, 1); break;
-            case 2: VX_QKV(WT_F16, 2); break;
-            case 3: VX_QKV(WT_F16, 3); break;
-            default: VX_QKV(WT_F16, 4); break;
-        }
+#define VX_QKV_NG(WTV)                      \
+    switch (ng) {                           \
+        case 1: VX_QKV(WTV, 1); break;      \
+        case 2: VX_QKV(WTV, 2); break;      \
+        case 3: VX_QKV(WTV, 3); break;      \
+        case 4: VX_QKV(WTV, 4); break;      \
+        case 6: VX_QKV(WTV, 6); break;      \
+        default: VX_QKV(WTV, 8); break;     \
     }
+    if (l.q.wt == WT_Q8) {
+        VX_QKV_NG(WT_Q8)
+    } else {
+        VX_QKV_NG(WT_F16)
+    }
+#undef VX_QKV_NG
 #undef VX_QKV
     VX_LAUNCHED("k_qkv_fused");
+    return VX_OK;
+}
+
+int launch_attn_out(hipStream_t s, const AttnOutLaunch &l) {
+    const uint32_t ng = l.mv.cols / kGroupCols;
+    if (l.mv.cols != l.q_heads * l.head_dim || l.mv.cols % kGroupCols || (ng != 1u && ng != 2u) ||
+        (l.head_dim != 64u && l.head_dim != 128u) || l.splits == 0 || l.splits > kMaxFoldedSplits ||
+        !fast_weight_ok(l.mv.w, l.mv.cols) || l.mv.row_base != 0 || l.mv.epi != EPI_RESIDUAL)
+        return fail(VX_ERR_UNSUPPORTED,
+                    "attn_out merge needs cols = q_heads*head_dim in {1024, 2048}, head_dim 64/128, "
+                    "<= %u splits and a fast-path weight", kMaxFoldedSplits);
+    AttnOutArgs a{};
+    a.mv.w = l.mv.w;
+    a.mv.rows = l.mv.rows;
+    a.mv.cols = l.mv.cols;
+    a.mv.y = l.mv.y;
+    a.mv.y2 = l.mv.y2;
+    a.mv.scale = l.mv.scale;
+    a.attn = l.attn_out;
+    a.part = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(l.partials) + 256);
+    a.position = l.position;
+    a.context = l.context;
+    a.splits = l.splits;
+    constexpr uint32_t RPW = 2;
+    const uint32_t grid = (l.mv.rows + kWavesPerBlock * RPW - 1) / (kWavesPerBlock * RPW);
+#define VX_AO(WTV, NGV, HDV)                                                                   \
+    do {                                                                                       \
+        if (l.mv.y2)                                                                           \
+            k_attn_out<WTV, NGV, RPW, HDV, true><<<grid, kBlock, 0, s>>>(a);                  \
+        else                                                                                   \
+            k_attn_out<WTV, NGV, RPW, HDV, false><<<grid, kBlock, 0, s>>>(a);                 \
+    } while (0)
+#define VX_AO_WT(WTV)                                          \
+    if (ng == 2u) {                                            \
+        if (l.head_dim == 128u) VX_AO(WTV, 2, 128); else VX_AO(WTV, 2, 64); \
+    } else {                                                   \
+        if (l.head_dim == 128u) VX_AO(WTV, 1, 128); else VX_AO(WTV, 1, 64); \
+    }
+    if (l.mv.w.wt == WT_Q8) {
+        VX_AO_WT(WT_Q8)
+    } else {
+        VX_AO_WT(WT_F16)
+    }
+#undef VX_AO_WT
+#undef VX_AO
+    VX_LAUNCHED("k_attn_out");
     return VX_OK;
 }
 
@@ -736,10 +890,11 @@ int launch_dequant(hipStream_t s, const WRef &w, uint32_t rows, uint32_t cols, f
 
 int launch_repack_q8(hipStream_t s, const uint8_t *raw_tensor, uint32_t rows, uint32_t cols,
                      int8_t *qs, __half *d) {
-    const size_t nblocks = (size_t)rows * (cols / 32u);
-    if (!nblocks) return VX_OK;
-    k_repack_q8<<<(unsigned)((nblocks + 255) / 256), 256, 0, s>>>(raw_tensor, rows, cols, qs,
-                                                                 reinterpret_cast<unsigned short *>(d));
+    if (cols % kGroupCols) return fail(VX_ERR_INVALID_ARG, "Q8_0 repack needs cols %% 1024 == 0");
+    const size_t threads = (size_t)rows * (cols / kGroupCols) * 64u;
+    if (!threads) return VX_OK;
+    k_repack_q8<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(raw_tensor, rows, cols, qs,
+                                                                  reinterpret_cast<unsigned short *>(d));
     VX_LAUNCHED("k_repack_q8");
     return VX_OK;
 }

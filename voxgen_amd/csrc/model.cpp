@@ -1,14 +1,12 @@
 // Model data region on the device (upload_device_local, baselm.rs:472-477) and
 // the tensor table the per-op entry points resolve u32 weight offsets through.
 //
-// Rank-2 Q8_0 tensors are repacked once on upload into the layout the matvec
-// and GEMM kernels stream with 128-bit loads (see WRef in vx_internal.h):
-//   qs: int8 [rows][cols]; inside each 2048-column group of a row the 16-byte low
-//       halves of the group's blocks come first, then the high halves, so one
-//       wave64 load of 16 B per lane reads 1 KB of contiguous quants;
-//   d:  f16 [rows][cols/32] block scales.
-// Quants and scales are moved, never re-rounded, so dequantised values are
-// bit-identical to the GGUF blocks (gguf.rs:41-45, matvec.comp:36-43).
+// Rank-2 Q8_0 tensors whose row width is a multiple of 1024 are repacked once on
+// upload into the lane-interleaved layout the matvec kernels stream with 128-bit
+// loads (see WRef in vx_internal.h). Quants and scales are moved, never
+// re-rounded, so dequantised values are bit-identical to the GGUF blocks
+// (gguf.rs:41-45, matvec.comp:36-43). Other Q8_0 tensors stay in the GGUF
+// layout and are read from the raw region.
 #include <cstring>
 
 #include "vx_internal.h"
@@ -59,11 +57,11 @@ int resolve_matrix(const vx_model *m, uint32_t offset, uint32_t dtype, uint32_t 
     w.raw = m->raw;
     w.raw_offset = offset;
     if (dtype == VX_DTYPE_Q8_0) {
-        if (m->packed_qs[idx] == UINT64_MAX)
-            return fail(VX_ERR_UNSUPPORTED, "%s: Q8_0 tensor %s was not repacked", what, t.name);
         w.wt = WT_Q8;
-        w.ptr = m->packed + m->packed_qs[idx];
-        w.d = (const __half *)(m->packed + m->packed_d[idx]);
+        if (m->packed_qs[idx] != UINT64_MAX) {  // else: raw GGUF blocks only
+            w.ptr = m->packed + m->packed_qs[idx];
+            w.d = (const __half *)(m->packed + m->packed_d[idx]);
+        }
     } else if (dtype == VX_DTYPE_F16) {
         w.wt = WT_F16;
         w.ptr = m->raw + offset;
@@ -134,6 +132,7 @@ int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes, const vx_tens
                             t.name, (unsigned long long)cols);
             if (t.offset % 2u)
                 return fail(VX_ERR_UNSUPPORTED, "Q8_0 matrix %.96s at odd offset", t.name);
+            if (cols % 1024u) continue;  // read in place from the raw region
             pq[i] = packed_total;
             packed_total += (rows * cols + 255u) & ~255ull;
             pd[i] = packed_total;

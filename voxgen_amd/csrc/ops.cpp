@@ -436,7 +436,6 @@ int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, cons
     l.vc = static_cast<const __half *>(v_cache->ptr);
     l.out = F(out);
     l.partials = F(scratch);
-    l.counters = static_cast<uint32_t *>(scratch->ptr);
     l.position = CU(position);
     l.layer = a->layer;
     l.context = a->context;

@@ -46,10 +46,19 @@ void clear_error();
 // ------------------------------------------------------- weight references
 enum WeightType : uint32_t { WT_Q8 = 0, WT_F16 = 1, WT_F32 = 2 };
 
-// A matrix the kernels can stream. Q8_0 matrices are referenced in the repacked
-// layout (see model.cpp): qs = int8 [rows][cols] with each 2048-column group of a
-// row stored as the low 16-byte halves of its blocks followed by the high halves,
-// and d = f16 scales [rows][cols/32]. F16/F32 matrices use the GGUF layout.
+// A matrix the kernels can stream. Q8_0 matrices with cols % 1024 == 0 are
+// referenced in the repacked layout (model.cpp), built for wave64 loads in which
+// lane l owns columns 1024g + 256k + 4l + j (k, j < 4) of every 1024-column
+// group g of a row:
+//   qs: int8 [rows][cols]; byte 1024g + 16l + 4k + j of a row holds the quant of
+//       column 1024g + 256k + 4l + j, so lane l reads its 16 quants of group g
+//       with one 16-byte load and a wave reads 1 KB of contiguous bytes;
+//   d:  f16 [rows][cols/32]; element 32g + 4m + k of a row is the scale of block
+//       32g + 8k + m (the block of lane 8m..8m+7's chunk k), so lane l reads its
+//       four scales of group g with one 8-byte load.
+// The x values a lane needs, x[1024g + 256k + 4l .. +3], are then float4 loads
+// that are contiguous across the wave. Other Q8_0 matrices have ptr == nullptr
+// and are read from the raw GGUF region. F16/F32 matrices use the GGUF layout.
 struct WRef {
     uint32_t wt = WT_F16;        // WeightType of the fast path
     uint32_t dtype = 1;          // GGML dtype code
@@ -189,11 +198,40 @@ struct AttnLaunch {
     const __half *kc = nullptr, *vc = nullptr;
     float *out = nullptr;
     float *partials = nullptr;
-    uint32_t *counters = nullptr;
     const uint32_t *position = nullptr;
     uint32_t layer = 0, context = 0, head_dim = 0, q_heads = 0, kv_heads = 0, splits = 0;
 };
+// Partials: 256 bytes of header, then per (q head, split) a record of head_dim+4
+// floats: max, sum, 2 pad words, acc[head_dim].
 uint64_t attn_scratch_bytes(uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads, uint32_t splits);
+constexpr uint32_t kMaxAttnSplits = 64;     // splits of a standalone attention call
+constexpr uint32_t kMaxFoldedSplits = 8;    // splits the attn_out prologue merges
+constexpr uint32_t kAttnMinChunk = 32;      // fewest keys per active split
+// Split of the context [0, position] into `active` contiguous chunks, identical
+// in every kernel that reads the partials.
+struct SplitPlan {
+    uint32_t n, active, chunk;
+};
+__device__ __forceinline__ SplitPlan split_plan(const uint32_t *position, uint32_t context, uint32_t splits) {
+    uint32_t pos = *position;
+    if (pos >= context) pos = context - 1u;
+    SplitPlan p;
+    p.n = pos + 1u;
+    p.active = min(splits, (p.n + kAttnMinChunk - 1u) / kAttnMinChunk);
+    p.chunk = (p.n + p.active - 1u) / p.active;
+    return p;
+}
+// attn_out matvec (EPI_RESIDUAL) whose x is merged from the attention partials.
+struct AttnOutLaunch {
+    MatvecLaunch mv;
+    const float *partials = nullptr;   // the AttnLaunch scratch (header + records)
+    float *attn_out = nullptr;         // nullable: also store the merged attention vector
+    const uint32_t *position = nullptr;
+    uint32_t context = 0, splits = 0, q_heads = 0, head_dim = 0;
+};
+int launch_attn_out(hipStream_t s, const AttnOutLaunch &a);
+// Partials only (k_attn_chunk), and partials + per-head merge (k_attn_combine).
+int launch_attn_partials(hipStream_t s, const AttnLaunch &a);
 int launch_attn_decode(hipStream_t s, const AttnLaunch &a);
 
 // Reference-granular kernels.
