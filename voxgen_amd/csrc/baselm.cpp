@@ -44,7 +44,7 @@ struct vx_baselm {
     vx_buf *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     vx_buf *attention = nullptr, *gate = nullptr, *branch = nullptr, *logits = nullptr;
     vx_buf *scores = nullptr, *kv_k = nullptr, *kv_v = nullptr, *position = nullptr;
-    vx_buf *tokens = nullptr, *attn_scratch = nullptr;
+    vx_buf *tokens = nullptr, *attn_scratch = nullptr, *rope_table = nullptr;
     std::vector<Layer> layers;
     uint32_t embd_offset = 0, embd_dtype = 1;
     WRef output;
@@ -158,7 +158,7 @@ void free_all(vx_baselm *e) {
             }
     vx_buf **bufs[] = {&e->hidden, &e->norm,   &e->q,      &e->k,        &e->v,
                        &e->attention, &e->gate, &e->branch, &e->logits, &e->scores,
-                       &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch};
+                       &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -180,11 +180,17 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
                                   U(e->tokens), U(e->position), c.vocab_size, e->embedding_alpha, F(e->hidden),
                                   c.active_context_length));
     }
+    {
+        ProfSpan sp(ctx, "baselm.rope_table");
+        VX_CHECK(launch_rope_table(s, e->rope_factors, U(e->position), c.head_dim, c.rope_theta, e->rope_scaling,
+                                   reinterpret_cast<float2 *>(e->rope_table->ptr)));
+    }
     for (uint32_t l = 0; l < c.block_count; ++l) {
         const Layer &L = e->layers[l];
         {
             ProfSpan sp(ctx, "baselm.qkv");
             QkvFusedLaunch a;
+            a.rope_cs = reinterpret_cast<const float2 *>(e->rope_table->ptr);
             a.q = L.q;
             a.k = L.k;
             a.v = L.v;
@@ -595,7 +601,8 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
         (st = alloc(ctx, (uint64_t)c.head_count * c.active_context_length * f, &e->scores)) ||
         (st = alloc(ctx, cache, &e->kv_k)) || (st = alloc(ctx, cache, &e->kv_v)) ||
         (st = alloc(ctx, 256, &e->position)) || (st = alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->tokens)) ||
-        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, splits), &e->attn_scratch)))
+        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, splits), &e->attn_scratch)) ||
+        (st = alloc(ctx, (uint64_t)c.head_dim * 4u, &e->rope_table)))
         return bail(st);
     // Zero state once (outside any graph). Cache contents are otherwise only ever
     // overwritten, as in the reference (reset leaves stale KV, baselm.rs:616-620).

@@ -39,6 +39,48 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// DPP reductions (no LDS round trips): quad swaps, row mirrors, then
+// row_bcast15/31 fold the four 16-lane rows into lane 63, read back as a
+// wave-uniform value.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                 0xf, false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_keep(float v) {  // lanes the control does not write keep v
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                 0xf, false));
+}
+__device__ __forceinline__ float uniform_lane63(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp<0xb1>(v);        // quad_perm [1,0,3,2]
+    v += dpp<0x4e>(v);        // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);       // row_half_mirror
+    v += dpp<0x140>(v);       // row_mirror
+    v += dpp<0x142, 0xa>(v);  // row_bcast:15
+    v += dpp<0x143, 0xc>(v);  // row_bcast:31
+    return uniform_lane63(v);
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_keep<0xb1>(v));
+    v = fmaxf(v, dpp_keep<0x4e>(v));
+    v = fmaxf(v, dpp_keep<0x141>(v));
+    v = fmaxf(v, dpp_keep<0x140>(v));
+    v = fmaxf(v, dpp_keep<0x142, 0xa>(v));
+    v = fmaxf(v, dpp_keep<0x143, 0xc>(v));
+    return uniform_lane63(v);
+}
+// Sum over each aligned quad of lanes, result in all four lanes.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp<0xb1>(v);  // quad_perm [1,0,3,2]
+    v += dpp<0x4e>(v);  // quad_perm [2,3,0,1]
+    return v;
+}
+
 struct AttnArgs {
     const float *q;
     const __half *kc, *vc;
@@ -64,7 +106,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     __shared__ float red[2][4];
     __shared__ float accs[256];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t s = blockIdx.x, h = blockIdx.y;
     const uint32_t kvh = h / (a.q_heads / a.kv_heads);
     const uint32_t kv_dim = a.kv_heads * HD;
@@ -110,12 +152,10 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
                 d1 = fmaf(qv[8 * i + 2 * t + 1], kf.y, d1);
             }
         }
-        float sc = d0 + d1;
-        sc += __shfl_xor(sc, 1, 64);
-        sc += __shfl_xor(sc, 2, 64);
+        float sc = quad_sum(d0 + d1);
         sc = valid ? sc * inv_sqrt : -FLT_MAX;
         // Tile max across the workgroup.
-        const float wm = wave_max(sc);
+        const float wm = wave_max_dpp(sc);
         if (lane == 0) red[0][wave] = wm;
         __syncthreads();
         const float tmax = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
@@ -125,7 +165,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < R / 8; ++i) *reinterpret_cast<uint4 *>(&vs[j][r * R + 8 * i]) = vw[i];
         if (r == 0) ps[j] = p;
-        const float ws = wave_sum(r == 0 ? p : 0.f);
+        const float ws = wave_sum_dpp(r == 0 ? p : 0.f);
         if (lane == 0) red[1][wave] = ws;
         __syncthreads();
         const float tsum = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);

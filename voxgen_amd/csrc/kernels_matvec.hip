@@ -5,7 +5,9 @@
 //     columns whose x values are float4 loads contiguous across the wave:
 //       Q8_0: columns 1024g + 256k + 4l + j      (k, j < 4; fragment index 4k + j)
 //       F16 : columns 1024g + 512h + 8l + j      (h < 2, j < 8; index 8h + j)
-//     The lane keeps these x values in registers for every row the wave streams.
+//     The workgroup stages x (with its rmsnorm where fused) in LDS once; each
+//     lane reads its x values from there and keeps them in registers for every
+//     row the wave streams.
 //   * Q8_0 rows come from the lane-interleaved repack (model.cpp): per lane and
 //     group one 16 B load of quants and one 8 B load of its four block scales,
 //     so every weight load instruction of a wave reads contiguous bytes. Bytes
@@ -13,7 +15,8 @@
 //     removed with the per-chunk sum of x: d*(sum (q+128)x - 128 sum x).
 //   * F16 rows: two 16 B loads per lane and group, straight from the GGUF layout.
 //   * All weight loads of the wave's rows are issued before any arithmetic, right
-//     after the x loads, so HBM latency is paid once per wave.
+//     after the x loads, so HBM latency is paid once per wave and the staging of
+//     x overlaps the weight streaming.
 //   * fp32 accumulation, DPP wave reduction, lane 0 runs the epilogue.
 // No MFMA: at batch 1 the arithmetic intensity is ~1 FLOP/byte.
 #include "vx_internal.h"
@@ -69,82 +72,6 @@ struct Frag {
     float v[NG][16];
 };
 
-// Loads are branch-free: an out-of-range element is read from a clamped, valid
-// address and replaced by zero with a select.
-
-// x fragment of a contiguous vector x[0..cols) (cols % 4 == 0, x 16-byte aligned):
-// load_frag_raw issues the loads (out-of-range columns read column 0), and
-// mask_frag zeroes those columns once the data is needed, so that no select
-// sits between these loads and the weight loads issued after them.
-template <int WT, int NG>
-__device__ __forceinline__ void load_frag_raw(Frag<NG> &f, const float *x, uint32_t cols, int lane) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            const uint32_t c = frag_col<WT>(g, lane, i);
-            const float4 v = *reinterpret_cast<const float4 *>(x + (c < cols ? c : 0u));
-            f.v[g][i] = v.x;
-            f.v[g][i + 1] = v.y;
-            f.v[g][i + 2] = v.z;
-            f.v[g][i + 3] = v.w;
-        }
-    }
-}
-
-template <int WT, int NG>
-__device__ __forceinline__ void mask_frag(Frag<NG> &f, uint32_t cols, int lane) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            const bool ok = frag_col<WT>(g, lane, i) < cols;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) f.v[g][i + t] = ok ? f.v[g][i + t] : 0.f;
-        }
-}
-
-template <int WT, int NG>
-__device__ __forceinline__ void load_frag(Frag<NG> &f, const float *x, uint32_t cols, int lane) {
-    load_frag_raw<WT, NG>(f, x, cols, lane);
-    mask_frag<WT, NG>(f, cols, lane);
-}
-
-// x fragment of x = xl[0..left) ++ xr[0..cols-left) (fusion_linear.comp:63).
-template <int WT, int NG>
-__device__ __forceinline__ void load_frag_concat(Frag<NG> &f, const float *xl, const float *xr,
-                                                 uint32_t left, uint32_t cols, int lane) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t c = frag_col<WT>(g, lane, i);
-            const bool ok = c < cols;
-            const uint32_t cc = ok ? c : 0u;
-            const float *p = cc < left ? xl + cc : xr + (cc - left);
-            const float v = *p;
-            f.v[g][i] = ok ? v : 0.f;
-        }
-    }
-}
-
-// x = rmsnorm(h) * w with the wave covering all of h (rmsnorm.comp:21-42 math).
-// f holds h and wf holds w on entry; f holds x on return.
-template <int NG>
-__device__ __forceinline__ void normalize_frag(Frag<NG> &f, const Frag<NG> &wf, uint32_t cols, float eps) {
-    float ss = 0.f;
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ss = fmaf(f.v[g][i], f.v[g][i], ss);
-    ss = wave_sum_dpp(ss);
-    const float inv_rms = 1.0f / sqrtf(ss / (float)cols + eps);
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) f.v[g][i] = f.v[g][i] * inv_rms * wf.v[g][i];
-}
-
 // Per-chunk sums of the x fragment (the Q8_0 bias correction): sx[g][k] is the
 // sum of the four x values lane-chunk k of group g multiplies.
 template <int NG>
@@ -158,6 +85,97 @@ __device__ __forceinline__ void frag_sums(const Frag<NG> &f, FragSums<NG> &sx) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             sx.s[g][k] = (f.v[g][4 * k] + f.v[g][4 * k + 1]) + (f.v[g][4 * k + 2] + f.v[g][4 * k + 3]);
+}
+
+// ------------------------------------------------------- x staged in LDS
+// The workgroup loads x once (thread t: float4 at 1024j + 4t, j < NG), optionally
+// applies rmsnorm(x)*w (rmsnorm.comp:21-42) with a block reduction, and stores it
+// to LDS; every wave then reads its fragment from there. stage_issue only issues
+// the loads, so a kernel can put its weight loads right behind them and
+// stage_finish (which waits for x alone) overlaps the weight streaming.
+template <int NG, bool NORM>
+struct XStage {
+    float4 v[NG];
+    float4 w[NORM ? NG : 1];
+};
+
+template <int NG, bool NORM>
+__device__ __forceinline__ void stage_issue(XStage<NG, NORM> &st, const float *x, const float *w, uint32_t cols) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        const uint32_t c = kGroupCols * j + 4u * t;
+        const uint32_t cc = c < cols ? c : 0u;
+        st.v[j] = *reinterpret_cast<const float4 *>(x + cc);
+        if constexpr (NORM) st.w[j] = *reinterpret_cast<const float4 *>(w + cc);
+    }
+}
+
+// x = xl[0..left) ++ xr[0..cols-left) (fusion_linear.comp:63), element by element.
+template <int NG>
+__device__ __forceinline__ void stage_issue_concat(XStage<NG, false> &st, const float *xl, const float *xr,
+                                                   uint32_t left, uint32_t cols) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        float e[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t c = kGroupCols * j + 4u * t + q;
+            const bool ok = c < cols;
+            const uint32_t cc = ok ? c : 0u;
+            const float v = cc < left ? xl[cc] : xr[cc - left];
+            e[q] = ok ? v : 0.f;
+        }
+        st.v[j] = make_float4(e[0], e[1], e[2], e[3]);
+    }
+}
+
+template <int NG, bool NORM>
+__device__ __forceinline__ void stage_finish(XStage<NG, NORM> &st, float *xs, float *red, uint32_t cols, float eps) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NG; ++j)
+        if (kGroupCols * j + 4u * t >= cols) st.v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            ss = fmaf(st.v[j].x, st.v[j].x, ss);
+            ss = fmaf(st.v[j].y, st.v[j].y, ss);
+            ss = fmaf(st.v[j].z, st.v[j].z, ss);
+            ss = fmaf(st.v[j].w, st.v[j].w, ss);
+        }
+        ss = wave_sum_dpp(ss);
+        if ((t & 63u) == 0u) red[t >> 6] = ss;
+        __syncthreads();
+        const float total = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv_rms = 1.0f / sqrtf(total / (float)cols + eps);
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            st.v[j].x = st.v[j].x * inv_rms * st.w[j].x;
+            st.v[j].y = st.v[j].y * inv_rms * st.w[j].y;
+            st.v[j].z = st.v[j].z * inv_rms * st.w[j].z;
+            st.v[j].w = st.v[j].w * inv_rms * st.w[j].w;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NG; ++j) *reinterpret_cast<float4 *>(xs + kGroupCols * j + 4u * t) = st.v[j];
+    __syncthreads();
+}
+
+template <int WT, int NG>
+__device__ __forceinline__ void frag_from_lds(Frag<NG> &f, const float *xs, int lane) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(xs + frag_col<WT>(g, lane, i));
+            f.v[g][i] = v.x;
+            f.v[g][i + 1] = v.y;
+            f.v[g][i + 2] = v.z;
+            f.v[g][i + 3] = v.w;
+        }
 }
 
 // ---------------------------------------------------------------- Q8_0 rows
@@ -257,7 +275,6 @@ struct MvArgs {
     uint32_t bias_dtype;
     float *y, *y2;
     float scale;
-    int concat;  // x is xl ++ xr rather than one aligned vector
 };
 
 // Epilogue variants are compile-time: each kernel instance has one
@@ -299,22 +316,25 @@ __device__ __forceinline__ void epilogue(const MvArgs &a, uint32_t row, float ac
     }
 }
 
-// Issue order per wave: x fragment (L2-resident) first, then the weight rows
-// (HBM), then the epilogue operands, so that vmcnt's in-order accounting lets
-// the x math proceed while the weights are in flight. Rows past the end are
-// clamped to a valid row and their results dropped, which keeps every load
-// unconditional.
+// Issue order: x (L2-resident) first, then the weight rows (HBM), then the
+// epilogue operands, so that vmcnt's in-order accounting lets the LDS staging of
+// x proceed while the weights are in flight. Rows past the end are clamped to a
+// valid row and their results dropped (no early exit: the staging has barriers).
 template <int WT, int NG, int RPW, int EP>
 __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
+    __shared__ __align__(16) float xs[NG * kGroupCols];
+    __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
     const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
-    if (row0 >= a.rows) return;
-    Frag<NG> f;
-    if (a.concat)
-        load_frag_concat<WT, NG>(f, a.xl, a.xr, a.left, a.cols, lane);
+    // Only fusion_linear reads a concatenated x (compile-time, so the plain path
+    // keeps its float4 loads).
+    constexpr bool CONCAT = EP == EP_FUSION_F32 || EP == EP_FUSION_F16;
+    XStage<NG, false> st;
+    if constexpr (CONCAT)
+        stage_issue_concat<NG>(st, a.xl, a.xr, a.left, a.cols);
     else
-        load_frag_raw<WT, NG>(f, a.xl, a.cols, lane);
+        stage_issue<NG, false>(st, a.xl, nullptr, a.cols);
     __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> r[RPW];
 #pragma unroll
@@ -323,7 +343,9 @@ __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < RPW; ++i) op[i] = epilogue_operand<EP>(a, min(row0 + i, a.rows - 1u));
     __builtin_amdgcn_sched_barrier(0);
-    if (!a.concat) mask_frag<WT, NG>(f, a.cols, lane);
+    stage_finish<NG, false>(st, xs, red, a.cols, 0.f);
+    Frag<NG> f;
+    frag_from_lds<WT, NG>(f, xs, lane);
     FragSums<NG> sx;
     frag_sums(f, sx);
     float acc[RPW];
@@ -354,9 +376,24 @@ template <int WT, int NG, int RPW, int HD, bool BRANCH>
 __global__ __launch_bounds__(kBlock) void k_attn_out(AttnOutArgs a) {
     constexpr int E = 4 * NG;  // outputs merged per thread
     __shared__ __align__(16) float xs[NG * kGroupCols];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const MvArgs &m = a.mv;
     const uint32_t row0 = (blockIdx.x * kWavesPerBlock + wave) * RPW;  // no early exit: barrier below
+    // Every split record of this thread's head is requested up front, whatever
+    // the position (records past the active splits get weight 0 by a select), so
+    // these loads do not wait for the position and go out ahead of the weights.
+    const uint32_t o0 = (uint32_t)(E * tid), hh = o0 / HD, d0 = o0 % HD;
+    float2 ml[kMaxFoldedSplits];
+    float4 av[kMaxFoldedSplits][E / 4];
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+        const float *rec = a.part + ((size_t)hh * a.splits + (s < a.splits ? s : 0u)) * (HD + 4);
+        ml[s] = *reinterpret_cast<const float2 *>(rec);
+#pragma unroll
+        for (int e = 0; e < E / 4; ++e) av[s][e] = *reinterpret_cast<const float4 *>(rec + 4 + d0 + 4 * e);
+    }
+    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
+    __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> r[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) load_row(r[i], m.w, min(row0 + i, m.rows - 1u), m.cols, lane);
@@ -365,17 +402,6 @@ __global__ __launch_bounds__(kBlock) void k_attn_out(AttnOutArgs a) {
     for (int i = 0; i < RPW; ++i) op[i] = m.y[min(row0 + i, m.rows - 1u)];
     __builtin_amdgcn_sched_barrier(0);
     // Merge of the partials (k_attn_combine's arithmetic).
-    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
-    const uint32_t o0 = (uint32_t)(E * tid), hh = o0 / HD, d0 = o0 % HD;
-    float2 ml[kMaxFoldedSplits];
-    float4 av[kMaxFoldedSplits][E / 4];
-#pragma unroll
-    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
-        const float *rec = a.part + ((size_t)hh * a.splits + (s < plan.active ? s : 0u)) * (HD + 4);
-        ml[s] = *reinterpret_cast<const float2 *>(rec);
-#pragma unroll
-        for (int e = 0; e < E / 4; ++e) av[s][e] = *reinterpret_cast<const float4 *>(rec + 4 + d0 + 4 * e);
-    }
     float mx = -3.402823466e+38f;
 #pragma unroll
     for (uint32_t s = 0; s < kMaxFoldedSplits; ++s)
@@ -385,14 +411,15 @@ __global__ __launch_bounds__(kBlock) void k_attn_out(AttnOutArgs a) {
     for (int e = 0; e < E; ++e) o[e] = 0.f;
 #pragma unroll
     for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
-        const float w = s < plan.active ? expf(ml[s].x - mx) : 0.f;
-        l = fmaf(ml[s].y, w, l);
+        const bool on = s < plan.active;
+        const float w = on ? expf(ml[s].x - mx) : 0.f;
+        l = on ? fmaf(ml[s].y, w, l) : l;
 #pragma unroll
         for (int e = 0; e < E / 4; ++e) {
-            o[4 * e] = fmaf(av[s][e].x, w, o[4 * e]);
-            o[4 * e + 1] = fmaf(av[s][e].y, w, o[4 * e + 1]);
-            o[4 * e + 2] = fmaf(av[s][e].z, w, o[4 * e + 2]);
-            o[4 * e + 3] = fmaf(av[s][e].w, w, o[4 * e + 3]);
+            o[4 * e] = on ? fmaf(av[s][e].x, w, o[4 * e]) : o[4 * e];
+            o[4 * e + 1] = on ? fmaf(av[s][e].y, w, o[4 * e + 1]) : o[4 * e + 1];
+            o[4 * e + 2] = on ? fmaf(av[s][e].z, w, o[4 * e + 2]) : o[4 * e + 2];
+            o[4 * e + 3] = on ? fmaf(av[s][e].w, w, o[4 * e + 3]) : o[4 * e + 3];
         }
     }
     const float inv_l = 1.0f / l;
@@ -487,13 +514,13 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 template <int WT, int NG, int RPW, bool NORM>
 __global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
+    __shared__ __align__(16) float xs[NG * kGroupCols];
+    __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
     const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
-    if (row0 >= a.rows) return;
-    Frag<NG> f, wf;
-    load_frag_raw<WT, NG>(f, a.x, a.cols, lane);
-    if constexpr (NORM) load_frag_raw<WT, NG>(wf, a.norm, a.cols, lane);
+    XStage<NG, NORM> st;
+    stage_issue<NG, NORM>(st, a.x, a.norm, a.cols);
     __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> rg[RPW], ru[RPW];
 #pragma unroll
@@ -503,8 +530,9 @@ __global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
         load_row(ru[i], a.u, row, a.cols, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
-    mask_frag<WT, NG>(f, a.cols, lane);
-    if constexpr (NORM) normalize_frag(f, wf, a.cols, a.eps);
+    stage_finish<NG, NORM>(st, xs, red, a.cols, a.eps);
+    Frag<NG> f;
+    frag_from_lds<WT, NG>(f, xs, lane);
     FragSums<NG> sx;
     frag_sums(f, sx);
     float gs[RPW], us[RPW];
@@ -557,6 +585,7 @@ struct QkvArgs {
     float *qo, *ko, *vo;
     __half *kc, *vc;
     const uint32_t *position;
+    const float2 *rope_cs;
 };
 
 // One wave per rotary pair: Q/K rows (i, i + head_dim/2) of a head, or two
@@ -565,11 +594,14 @@ struct QkvArgs {
 template <int WT, int NG>
 __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const uint32_t p = blockIdx.x * kWavesPerBlock + wave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
+    __shared__ __align__(16) float xs[NG * kGroupCols];
+    __shared__ float red[kWavesPerBlock];
     const uint32_t half_dim = a.head_dim >> 1;
     const uint32_t pq = a.q_rows >> 1, pk = a.kv_rows >> 1;
-    if (p >= pq + 2u * pk) return;
+    const uint32_t p_raw = blockIdx.x * kWavesPerBlock + wave;
+    const bool live = p_raw < pq + 2u * pk;  // no early exit: the staging has barriers
+    const uint32_t p = live ? p_raw : pq + 2u * pk - 1u;
     int seg;
     uint32_t r0, r1;
     if (p < pq + pk) {
@@ -583,31 +615,38 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
         r0 = 2u * (p - pq - pk);
         r1 = r0 + 1u;
     }
-    const WRef &w = seg == 0 ? a.q : (seg == 1 ? a.k : a.v);
-    Frag<NG> f, wf;
-    load_frag_raw<WT, NG>(f, a.hidden, a.cols, lane);
-    load_frag_raw<WT, NG>(wf, a.norm, a.cols, lane);
+    // Scalar selects of the segment's matrix (p and seg are wave-uniform).
+    WRef w;
+    w.ptr = seg == 0 ? a.q.ptr : (seg == 1 ? a.k.ptr : a.v.ptr);
+    w.d = seg == 0 ? a.q.d : (seg == 1 ? a.k.d : a.v.d);
+    XStage<NG, true> st;
+    stage_issue<NG, true>(st, a.hidden, a.norm, a.cols);
     __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> rr[2];
     load_row(rr[0], w, r0, a.cols, lane);
     load_row(rr[1], w, r1, a.cols, lane);
     const uint32_t pos = *a.position;
-    const float ext = seg < 2 ? a.factors[r0 % a.head_dim] : 1.f;
+    const uint32_t pair = r0 % a.head_dim;
+    const float ext = seg < 2 && !a.rope_cs ? a.factors[pair] : 1.f;
+    const float2 cs_tab = seg < 2 && a.rope_cs ? a.rope_cs[pair] : make_float2(1.f, 0.f);
     __builtin_amdgcn_sched_barrier(0);
-    mask_frag<WT, NG>(f, a.cols, lane);
-    normalize_frag(f, wf, a.cols, a.eps);
+    stage_finish<NG, true>(st, xs, red, a.cols, a.eps);
+    Frag<NG> f;
+    frag_from_lds<WT, NG>(f, xs, lane);
     FragSums<NG> sx;
     frag_sums(f, sx);
     float v0 = wave_sum_dpp(row_dot(rr[0], f, sx));
     float v1 = wave_sum_dpp(row_dot(rr[1], f, sx));
-    if (lane != 0) return;
+    if (lane != 0 || !live) return;
     if (seg < 2) {
-        const uint32_t i = r0 % a.head_dim;
-        const float exponent = (float)(i * 2u) / (float)a.head_dim;
-        const float inv_freq = 1.0f / powf(a.theta, exponent);
-        const float angle = (float)pos * inv_freq / ext;
-        const float c = cosf(angle) * a.scaling;
-        const float s = sinf(angle) * a.scaling;
+        float c = cs_tab.x, s = cs_tab.y;
+        if (!a.rope_cs) {  // rope.comp:28-41 inline
+            const float exponent = (float)(pair * 2u) / (float)a.head_dim;
+            const float inv_freq = 1.0f / powf(a.theta, exponent);
+            const float angle = (float)pos * inv_freq / ext;
+            c = cosf(angle) * a.scaling;
+            s = sinf(angle) * a.scaling;
+        }
         const float n0 = v0 * c - v1 * s;
         const float n1 = v1 * c + v0 * s;
         v0 = n0;
@@ -725,6 +764,8 @@ bool fast_weight_ok(const WRef &w, uint32_t cols) {
 
 int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
     if (l.rows <= l.row_base || l.cols == 0) return VX_OK;
+    if (l.xr && l.epi != EPI_FUSION)
+        return fail(VX_ERR_INVALID_ARG, "a concatenated x is only read by the fusion epilogue");
     MvArgs a{};
     a.w = l.w;
     a.xl = l.xl;
@@ -739,7 +780,6 @@ int launch_matvec(hipStream_t s, const MatvecLaunch &l) {
     a.y = l.y;
     a.y2 = l.y2;
     a.scale = l.scale;
-    a.concat = l.xr != nullptr;
     const uint32_t ng = (l.cols + kGroupCols - 1) / kGroupCols;
     const bool fast = fast_weight_ok(l.w, l.cols) && aligned16(l.xl);
     const bool has_bias = l.bias != nullptr && l.bias_dtype <= 1u;
@@ -811,7 +851,7 @@ int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &l) {
                     "column count and aligned buffers");
     QkvArgs a{l.q,      l.k,        l.v,       l.hidden,  l.norm,  l.eps,    l.q_rows, l.kv_rows,
               l.cols,   l.head_dim, l.factors, l.theta,   l.scaling, l.layer, l.context, l.qo,
-              l.ko,     l.vo,       l.kc,      l.vc,      l.position};
+              l.ko,     l.vo,       l.kc,      l.vc,      l.position, l.rope_cs};
     const uint32_t pairs = (l.q_rows + 2u * l.kv_rows) / 2u;
     const uint32_t grid = (pairs + kWavesPerBlock - 1) / kWavesPerBlock;
 #define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV><<<grid, kBlock, 0, s>>>(a)

@@ -134,6 +134,22 @@ __global__ __launch_bounds__(256) void k_embedding(const uint8_t *raw, uint32_t 
     hidden[i] = w * alpha;
 }
 
+// Per-step RoPE table: table[i] = (cos(angle)*scaling, sin(angle)*scaling) for
+// rotary pair i at the device decode position, with rope.comp's angle
+// pos * theta^(-2i/d) / ext[i] (rope.comp:28-41). Every layer's fused QKV kernel
+// reads its pair from here, so the transcendentals run once per step.
+__global__ __launch_bounds__(64) void k_rope_table(const float *factors, const uint32_t *position,
+                                                   uint32_t head_dim, float theta, float scaling,
+                                                   float2 *table) {
+    const uint32_t i = threadIdx.x;
+    if (i >= head_dim / 2u) return;
+    const uint32_t pos = *position;
+    const float exponent = (float)(i * 2u) / (float)head_dim;
+    const float inv_freq = 1.0f / powf(theta, exponent);
+    const float angle = (float)pos * inv_freq / factors[i];
+    table[i] = make_float2(cosf(angle) * scaling, sinf(angle) * scaling);
+}
+
 __global__ void k_set_step(uint32_t *tokens, uint32_t *position, uint32_t pos, uint32_t token,
                            int write_token) {
     if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -190,6 +206,15 @@ int launch_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, 
     k_embedding<<<(cols + 255u) / 256u, 256, 0, s>>>(raw, weight_offset, dtype, cols, token, dev_tokens,
                                                      dev_position, tokens_len, vocab, alpha, hidden);
     VX_LAUNCHED("k_embedding");
+    return VX_OK;
+}
+
+int launch_rope_table(hipStream_t s, const float *factors, const uint32_t *position, uint32_t head_dim,
+                      float theta, float scaling, float2 *table) {
+    if (head_dim == 0 || head_dim > 128u || (head_dim & 1u))
+        return fail(VX_ERR_UNSUPPORTED, "rope table: head_dim must be even and <= 128");
+    k_rope_table<<<1, 64, 0, s>>>(factors, position, head_dim, theta, scaling, table);
+    VX_LAUNCHED("k_rope_table");
     return VX_OK;
 }
 

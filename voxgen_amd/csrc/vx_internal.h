@@ -190,6 +190,7 @@ struct QkvFusedLaunch {
     float *qo = nullptr, *ko = nullptr, *vo = nullptr;
     __half *kc = nullptr, *vc = nullptr;
     const uint32_t *position = nullptr;
+    const float2 *rope_cs = nullptr;   // nullable: per-step (cos, sin) table from launch_rope_table
 };
 int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &a);
 
@@ -261,6 +262,9 @@ int launch_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, 
                      uint32_t cols, uint32_t token, const uint32_t *dev_tokens,
                      const uint32_t *dev_position, uint32_t vocab, float alpha, float *hidden,
                      uint32_t tokens_len = 0);
+// table[i] = (cos, sin)(angle_i) * scaling at the device position (i < head_dim/2).
+int launch_rope_table(hipStream_t s, const float *factors, const uint32_t *position, uint32_t head_dim,
+                      float theta, float scaling, float2 *table);
 int launch_set_step(hipStream_t s, uint32_t *tokens, uint32_t *position, uint32_t pos,
                     uint32_t token, int write_token);
 int launch_fill_u32(hipStream_t s, uint32_t *dst, uint32_t value, uint64_t count);
