@@ -7,15 +7,21 @@ decode steps at positions 256..256+K-1 with token ids uniform from the vocab;
 each step is one hipGraph replay of the fused decode step (LM head off, the
 *_gpu_only semantics). A "step" is one decoded token.
 
-Prints one JSON line: tok/s, the per-kernel roofline of the dominant kernel
-(the gate/up SwiGLU matvec) from HIP events on the engine stream, the whole
-matvec-family bandwidth, and the CPU oracle's throughput on a bounded sample.
+Prints one JSON line with:
+  value        tok/s over the K timed graph replays (inputs resident in HBM)
+  roofline     the dominant kernel (the gate/up SwiGLU matvec): algorithmic bytes
+               per launch / its average duration, measured with two HIP events on
+               the engine stream around back-to-back launches over all 28 layers
+  per_kernel   the same measurement for every kernel of the decode layer
+  cpu_baseline the CPU oracle's decode throughput on a bounded sample
+
+`--copy-calibration` instead runs one plain copy kernel of known size (the
+reference point for the FETCH_SIZE / WRITE_SIZE counters).
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -28,26 +34,32 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBPS = 8000.0
 METRIC = "Q8_0 BaseLM decode tok/s @ batch 1; matvec HBM GB/s (% of 8 TB/s peak)"
 
-# Algorithmic bytes per launch of each decode kernel at the benchmark shapes
-# (Q8_0: 34 B per 32 weights; activations f32; KV f16).
+# Decode geometry.
 H, KV, F, L, V = 2048, 256, 6144, 28, 73448
 
 
 def q8(rows, cols):
+    """GGUF Q8_0 bytes of a rows x cols matrix (34 B per 32 weights)."""
     return rows * cols // 32 * 34
 
 
+# Algorithmic HBM bytes per launch of each layer kernel (weights, activations in
+# and out, KV-cache traffic); attention depends on the position.
 KERNEL_BYTES = {
-    # weights + hidden + attn_norm in + q/k/v out + K/V cache row writes
-    "baselm.qkv": q8(H + 2 * KV, H) + 2 * H * 4 + (H + 2 * KV) * 4 + 2 * KV * 2,
-    "baselm.attn_out": q8(H, H) + H * 4 + 2 * H * 4,                 # weights + x + hidden rw
-    "baselm.swiglu": 2 * q8(F, H) + 2 * H * 4 + F * 4,               # gate+up + hidden,norm + out
-    "baselm.down": q8(H, F) + F * 4 + 2 * H * 4,                     # weights + x + hidden rw
+    # Wq|Wk|Wv + hidden + attn_norm + q/k/v out + K/V cache row writes
+    "qkv": q8(H + 2 * KV, H) + 2 * H * 4 + (H + 2 * KV) * 4 + 2 * KV * 2,
+    # Wo + attention vector + hidden read and write
+    "attn_out": q8(H, H) + H * 4 + 2 * H * 4,
+    # Wgate|Wup + hidden + ffn_norm + gate out
+    "swiglu": 2 * q8(F, H) + 2 * H * 4 + F * 4,
+    # Wdown + gate vector + hidden read and write
+    "down": q8(H, F) + F * 4 + 2 * H * 4,
 }
 
 
 def attention_bytes(pos):
-    return 2 * (pos + 1) * KV * 2 + H * 4 * 2  # K and V rows read + q in + out
+    """K and V rows 0..pos of the layer (f16) + q in + attention vector out."""
+    return 2 * (pos + 1) * KV * 2 + H * 4 * 2
 
 
 def step_bytes(pos, lm_head=False):
@@ -66,14 +78,33 @@ def parse():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prefill", type=int, default=256)
     ap.add_argument("--lm-head", action="store_true", help="include the tied F16 LM head per step")
-    ap.add_argument("--cpu-steps", type=int, default=-1, help="CPU oracle sample size (-1 = auto)")
+    ap.add_argument("--kernel-reps", type=int, default=8, help="passes over the 28 layers per kernel timing")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target length of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference"])
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one copy kernel of known size and exit (PMC calibration)")
     return ap.parse_args()
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def copy_calibration():
+    """One 256 MiB device-to-device copy through vx_diag_stream_copy: FETCH_SIZE
+    and WRITE_SIZE of this dispatch should read 256 MiB each."""
+    from voxgen_amd import abi
+    from voxgen_amd.runtime import Context
+    abi.load()
+    nbytes = 256 << 20
+    with Context(0) as ctx:
+        src, dst = ctx.zeros(nbytes), ctx.zeros(nbytes)
+        abi.call("vx_diag_stream_copy", ctx.handle, dst.handle, src.handle, nbytes, 4096)
+        ctx.sync()
+        src.free()
+        dst.free()
+    print(json.dumps({"copy_calibration_bytes": nbytes}), flush=True)
 
 
 def main():
@@ -82,6 +113,9 @@ def main():
         print(f"bench.py runs on one GPU only: the BaseLM decode path has no multi-GPU form "
               f"(got --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     from voxgen_amd import abi, synth
     from voxgen_amd.baselm import BaseLmEngine
     from voxgen_amd.runtime import Context, Model
@@ -113,7 +147,6 @@ def main():
     run_steps(P, tokens[P:P + W])                         # warmup (also captures the graph)
     ctx.sync()
     timed = tokens[P:P + K]
-    ctx.sync()
     t0 = time.perf_counter()
     run_steps(P, timed)
     ctx.sync()
@@ -121,37 +154,34 @@ def main():
     tok_s = K / elapsed
     log(f"timed {K} steps at positions {P}..{P + K - 1}: {elapsed * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
 
-    # Per-kernel durations from HIP events around each kernel on the engine stream,
-    # over the same K steps (positions P..P+K-1 again).
-    eng.set_position(P)
-    prof = eng.profile_steps(timed)
+    # Per-kernel durations: HIP events on the engine stream around back-to-back
+    # launches of one layer kernel over the 28 layers' weights (750 MB for the
+    # SwiGLU, beyond the 256 MB MALL), at the device position P+K.
+    pos_k = P + K
     per_kernel = {}
     fam_bytes = fam_ms = 0.0
-    for name, nbytes in KERNEL_BYTES.items():
-        e = prof.get(name)
-        if not e:
-            continue
-        gbps = nbytes / (e["avg_ms"] * 1e-3) / 1e9
-        per_kernel[name] = dict(avg_us=round(e["avg_ms"] * 1e3, 3), calls=e["calls"], bytes=nbytes,
-                                GBps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
-        fam_bytes += nbytes * e["calls"]
-        fam_ms += e["total_ms"]
-    for name in ("baselm.attention", "baselm.embedding", "baselm.output_norm", "baselm.logits"):
-        if name in prof:
-            per_kernel[name] = dict(avg_us=round(prof[name]["avg_ms"] * 1e3, 3), calls=prof[name]["calls"])
-    fam_gbps = fam_bytes / (fam_ms * 1e-3) / 1e9 if fam_ms else 0.0
-    dom = per_kernel["baselm.swiglu"]
-    mean_step_bytes = float(np.mean([step_bytes(p, args.lm_head) for p in range(P, P + K)]))
+    for name in eng.LAYER_KERNELS:
+        ms = eng.time_layer_kernel(name, args.kernel_reps)
+        nbytes = KERNEL_BYTES.get(name, attention_bytes(pos_k))
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        per_kernel[name] = dict(avg_us=round(ms * 1e3, 3), bytes=nbytes, GBps=round(gbps, 1),
+                                frac=round(gbps / HBM_PEAK_GBPS, 4))
+        if name in KERNEL_BYTES:
+            fam_bytes += nbytes
+            fam_ms += ms
+    fam_gbps = fam_bytes / (fam_ms * 1e-3) / 1e9
+    dom = per_kernel["swiglu"]
     traffic = None
-    tfile = ROOT / "profiles" / "traffic_swiglu.json"
+    tfile = ROOT / "profiles" / "traffic_k_swiglu_decode28.json"
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
-        except Exception:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
             traffic = None
     roofline = dict(bound="hbm", achieved=dom["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
-                    frac=dom["frac"], traffic=traffic, kernel="k_swiglu (gate+up Q8_0 matvec)",
+                    frac=dom["frac"], traffic=traffic, kernel="k_swiglu (rmsnorm + gate/up Q8_0 matvec + SiLU)",
                     bytes_per_launch=dom["bytes"], avg_us=dom["avg_us"])
+    mean_step_bytes = float(np.mean([step_bytes(p, args.lm_head) for p in range(P, P + K)]))
 
     cpu = None
     if not args.no_cpu:
@@ -171,7 +201,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "q8_0 x f32",
         "data": "synthetic",
         "config": {"workload": "baselm_q8_0_decode_28L_batch1", "layers": L, "hidden": H, "ffn": F,
                    "heads": "16q/2kv x 128", "vocab": V, "prefill": P,
@@ -179,7 +209,8 @@ def main():
                    "exec": args.mode, "parallelism": "single GPU"},
         "roofline": roofline,
         "matvec_family": {"achieved": round(fam_gbps, 1), "unit": "GB/s",
-                          "frac": round(fam_gbps / HBM_PEAK_GBPS, 4)},
+                          "frac": round(fam_gbps / HBM_PEAK_GBPS, 4),
+                          "kernels": ["qkv", "attn_out", "swiglu", "down"]},
         "step": {"bytes_mean": int(mean_step_bytes),
                  "achieved_GBps": round(mean_step_bytes * tok_s / 1e9, 1),
                  "frac": round(mean_step_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4)},
@@ -195,13 +226,14 @@ def cpu_baseline(cfg, m, eng, tokens, P, args):
     sys.path.insert(0, str(ROOT / "oracle"))
     import voxref
     o = voxref.BaseLm(m.data, {t.name: t for t in m.tensors}, cfg)
-    # KV cache of the prefill, from the GPU run.
+    # KV cache of the prefill (positions 0..P-1), from the GPU run.
     o.kv_k[:] = eng.buffer("kv_k").download(np.uint16, o.kv_k.size)
     o.kv_v[:] = eng.buffer("kv_v").download(np.uint16, o.kv_v.size)
     t0 = time.perf_counter()
     o.decode_token(int(tokens[P]), P, logits=args.lm_head)
     one = time.perf_counter() - t0
-    n = args.cpu_steps if args.cpu_steps > 0 else int(max(2, min(64, 15.0 // max(one, 1e-3))))
+    n = int(max(2, min(256, args.cpu_seconds // max(one, 1e-3))))
+    n = min(n, len(tokens) - P - 1)
     t0 = time.perf_counter()
     for i in range(n):
         o.decode_token(int(tokens[P + 1 + i]), P + 1 + i, logits=args.lm_head)
@@ -209,16 +241,17 @@ def cpu_baseline(cfg, m, eng, tokens, P, args):
     thr = voxref.threads()
     log(f"cpu oracle: {n} steps in {el:.2f}s on {thr} threads")
     return {"value": round(n / el, 3), "unit": "tok/s", "cores": thr, "kind": "port",
-            "sample": f"{n} decode steps at positions {P + 1}..{P + n} of the same 28-layer Q8_0 model "
-                      f"and tokens (KV cache from the GPU prefill), C oracle with OpenMP over rows",
+            "sample": f"{n} decode steps at positions {P + 1}..{P + n} of the same 28-layer Q8_0 model and "
+                      f"tokens (KV cache of the GPU prefill), C oracle (oracle/voxref.c) with OpenMP over rows; "
+                      f"the reference's own CPU path (Rust + GLSL on Mesa lavapipe) is not buildable here",
             "cpu": cpu_model()}
 
 
 def cpu_model():
     try:
-        for l in open("/proc/cpuinfo"):
-            if l.startswith("model name"):
-                return l.split(":", 1)[1].strip()
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
     except OSError:
         pass
     return "unknown"

@@ -197,6 +197,7 @@ PROTOTYPES = {
     "vx_baselm_benchmark": (i32, [ENGINE, u32, u32, u32, P(BenchmarkResult)]),
     "vx_baselm_buffer": (BUFP, [ENGINE, u32]),
     "vx_baselm_profile_steps": (i32, [ENGINE, P(u32), u32, P(ProfEntry), u32, P(u32)]),
+    "vx_baselm_time_layer_kernel": (i32, [ENGINE, u32, u32, P(C.c_double)]),
 }
 
 STRUCT_SIZES = {  # C name -> ctypes struct

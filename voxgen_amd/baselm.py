@@ -144,6 +144,16 @@ class BaseLmEngine:
         abi.call("vx_baselm_benchmark", self.handle, token_id, warmup, iterations, C.byref(b))
         return {k: getattr(b, k) for k, _ in b._fields_}
 
+    LAYER_KERNELS = ("qkv", "attention", "attn_out", "swiglu", "down")
+
+    def time_layer_kernel(self, name: str, reps: int = 4) -> float:
+        """Average duration (ms) of one fused layer kernel over `reps` back-to-back
+        passes across all layers, from two HIP events on the engine stream."""
+        out = C.c_double()
+        abi.call("vx_baselm_time_layer_kernel", self.handle, self.LAYER_KERNELS.index(name), reps,
+                 C.byref(out))
+        return out.value
+
     def profile_steps(self, tokens) -> dict:
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         n = C.c_uint32()

@@ -169,26 +169,31 @@ inline float *F(vx_buf *b) { return static_cast<float *>(b->ptr); }
 inline uint32_t *U(vx_buf *b) { return static_cast<uint32_t *>(b->ptr); }
 inline __half *H(vx_buf *b) { return static_cast<__half *>(b->ptr); }
 
-// The fused decode step, enqueued on the context stream.
-int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
-    vx_ctx *ctx = e->ctx;
-    hipStream_t s = ctx->stream;
+// Kernels of one layer of the fused decode step.
+enum LayerKernel : uint32_t { LK_QKV = 0, LK_ATTENTION = 1, LK_ATTN_OUT = 2, LK_SWIGLU = 3, LK_DOWN = 4, LK_COUNT = 5 };
+const char *const kLayerKernelNames[LK_COUNT] = {"baselm.qkv", "baselm.attention", "baselm.attn_out",
+                                                 "baselm.swiglu", "baselm.down"};
+
+// Enqueue one kernel of layer l (all read the decode position from device memory).
+int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l) {
+    hipStream_t s = e->ctx->stream;
     const vx_baselm_config &c = e->cfg;
-    if (with_embedding) {
-        ProfSpan sp(ctx, "baselm.embedding");
-        VX_CHECK(launch_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, c.embedding_length, 0,
-                                  U(e->tokens), U(e->position), c.vocab_size, e->embedding_alpha, F(e->hidden),
-                                  c.active_context_length));
-    }
-    {
-        ProfSpan sp(ctx, "baselm.rope_table");
-        VX_CHECK(launch_rope_table(s, e->rope_factors, U(e->position), c.head_dim, c.rope_theta, e->rope_scaling,
-                                   reinterpret_cast<float2 *>(e->rope_table->ptr)));
-    }
-    for (uint32_t l = 0; l < c.block_count; ++l) {
-        const Layer &L = e->layers[l];
-        {
-            ProfSpan sp(ctx, "baselm.qkv");
+    const Layer &L = e->layers[l];
+    AttnLaunch at;
+    at.q = F(e->q);
+    at.kc = H(e->kv_k);
+    at.vc = H(e->kv_v);
+    at.out = F(e->attention);
+    at.partials = F(e->attn_scratch);
+    at.position = U(e->position);
+    at.layer = l;
+    at.context = c.active_context_length;
+    at.head_dim = c.head_dim;
+    at.q_heads = c.head_count;
+    at.kv_heads = c.head_count_kv;
+    at.splits = e->splits;
+    switch (which) {
+        case LK_QKV: {
             QkvFusedLaunch a;
             a.rope_cs = reinterpret_cast<const float2 *>(e->rope_table->ptr);
             a.q = L.q;
@@ -212,35 +217,21 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
             a.kc = H(e->kv_k);
             a.vc = H(e->kv_v);
             a.position = U(e->position);
-            VX_CHECK(launch_qkv_fused(s, a));
+            return launch_qkv_fused(s, a);
         }
-        AttnLaunch at;
-        at.q = F(e->q);
-        at.kc = H(e->kv_k);
-        at.vc = H(e->kv_v);
-        at.out = F(e->attention);
-        at.partials = F(e->attn_scratch);
-        at.position = U(e->position);
-        at.layer = l;
-        at.context = c.active_context_length;
-        at.head_dim = c.head_dim;
-        at.q_heads = c.head_count;
-        at.kv_heads = c.head_count_kv;
-        at.splits = e->splits;
-        MatvecLaunch ao;
-        ao.w = L.o;
-        ao.xl = F(e->attention);
-        ao.rows = c.embedding_length;
-        ao.cols = c.embedding_length;
-        ao.epi = EPI_RESIDUAL;
-        ao.y = F(e->hidden);
-        ao.scale = e->residual_scale;
-        if (e->fold_attn_merge) {
-            {
-                ProfSpan sp(ctx, "baselm.attention");
-                VX_CHECK(launch_attn_partials(s, at));
-            }
-            ProfSpan sp(ctx, "baselm.attn_out");
+        case LK_ATTENTION:
+            // Partials only when attn_out merges them; else partials + merge.
+            return e->fold_attn_merge ? launch_attn_partials(s, at) : launch_attn_decode(s, at);
+        case LK_ATTN_OUT: {
+            MatvecLaunch ao;
+            ao.w = L.o;
+            ao.xl = F(e->attention);
+            ao.rows = c.embedding_length;
+            ao.cols = c.embedding_length;
+            ao.epi = EPI_RESIDUAL;
+            ao.y = F(e->hidden);
+            ao.scale = e->residual_scale;
+            if (!e->fold_attn_merge) return launch_matvec(s, ao);
             AttnOutLaunch a;
             a.mv = ao;
             a.partials = at.partials;
@@ -250,17 +241,9 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
             a.splits = at.splits;
             a.q_heads = at.q_heads;
             a.head_dim = at.head_dim;
-            VX_CHECK(launch_attn_out(s, a));
-        } else {
-            {
-                ProfSpan sp(ctx, "baselm.attention");
-                VX_CHECK(launch_attn_decode(s, at));
-            }
-            ProfSpan sp(ctx, "baselm.attn_out");
-            VX_CHECK(launch_matvec(s, ao));
+            return launch_attn_out(s, a);
         }
-        {
-            ProfSpan sp(ctx, "baselm.swiglu");
+        case LK_SWIGLU: {
             SwigluLaunch a;
             a.g = L.gate;
             a.u = L.up;
@@ -270,10 +253,9 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
             a.rows = c.feed_forward_length;
             a.cols = c.embedding_length;
             a.y = F(e->gate);
-            VX_CHECK(launch_swiglu(s, a));
+            return launch_swiglu(s, a);
         }
-        {
-            ProfSpan sp(ctx, "baselm.down");
+        case LK_DOWN: {
             MatvecLaunch a;
             a.w = L.down;
             a.xl = F(e->gate);
@@ -282,9 +264,33 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
             a.epi = EPI_RESIDUAL;
             a.y = F(e->hidden);
             a.scale = e->residual_scale;
-            VX_CHECK(launch_matvec(s, a));
+            return launch_matvec(s, a);
         }
+        default: return fail(VX_ERR_INVALID_ARG, "unknown layer kernel %u", which);
     }
+}
+
+// The fused decode step, enqueued on the context stream.
+int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_baselm_config &c = e->cfg;
+    if (with_embedding) {
+        ProfSpan sp(ctx, "baselm.embedding");
+        VX_CHECK(launch_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, c.embedding_length, 0,
+                                  U(e->tokens), U(e->position), c.vocab_size, e->embedding_alpha, F(e->hidden),
+                                  c.active_context_length));
+    }
+    {
+        ProfSpan sp(ctx, "baselm.rope_table");
+        VX_CHECK(launch_rope_table(s, e->rope_factors, U(e->position), c.head_dim, c.rope_theta, e->rope_scaling,
+                                   reinterpret_cast<float2 *>(e->rope_table->ptr)));
+    }
+    for (uint32_t l = 0; l < c.block_count; ++l)
+        for (uint32_t k = 0; k < LK_COUNT; ++k) {
+            ProfSpan sp(ctx, kLayerKernelNames[k]);
+            VX_CHECK(enqueue_layer_kernel(e, k, l));
+        }
     {
         ProfSpan sp(ctx, "baselm.output_norm");
         VX_CHECK(launch_rmsnorm(s, F(e->hidden), F(e->norm), e->output_norm, c.embedding_length, c.rms_epsilon,
@@ -810,6 +816,36 @@ int vx_baselm_profile_steps(vx_baselm *e, const uint32_t *tokens, uint32_t n, vx
     ctx->prof_enabled = was;
     VX_CHECK(st);
     return vx_prof_snapshot(ctx, out, cap, count);
+}
+
+int vx_baselm_time_layer_kernel(vx_baselm *e, uint32_t which, uint32_t reps, double *avg_ms) {
+    if (!e || !avg_ms) return fail(VX_ERR_INVALID_ARG, "vx_baselm_time_layer_kernel: null argument");
+    if (which >= LK_COUNT) return fail(VX_ERR_INVALID_ARG, "unknown layer kernel %u", which);
+    if (reps == 0) return fail(VX_ERR_INVALID_ARG, "reps must be > 0");
+    if (e->opt.exec_mode == VX_EXEC_REFERENCE)
+        return fail(VX_ERR_STATE, "kernel timing needs the fused decode kernels (graph or fused mode)");
+    vx_ctx *ctx = e->ctx;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    VX_HIP(hipEventCreate(&t0));
+    if (hipEventCreate(&t1) != hipSuccess) {
+        (void)hipEventDestroy(t0);
+        return fail(VX_ERR_HIP, "hipEventCreate failed");
+    }
+    int st = VX_OK;
+    // One warm pass over the layers, then `reps` timed passes, back to back.
+    for (uint32_t l = 0; l < e->cfg.block_count && st == VX_OK; ++l) st = enqueue_layer_kernel(e, which, l);
+    if (st == VX_OK && hipEventRecord(t0, ctx->stream) != hipSuccess) st = fail(VX_ERR_HIP, "hipEventRecord failed");
+    for (uint32_t r = 0; r < reps && st == VX_OK; ++r)
+        for (uint32_t l = 0; l < e->cfg.block_count && st == VX_OK; ++l) st = enqueue_layer_kernel(e, which, l);
+    if (st == VX_OK && hipEventRecord(t1, ctx->stream) != hipSuccess) st = fail(VX_ERR_HIP, "hipEventRecord failed");
+    float ms = 0.f;
+    if (st == VX_OK && hipEventSynchronize(t1) != hipSuccess) st = fail(VX_ERR_HIP, "hipEventSynchronize failed");
+    if (st == VX_OK && hipEventElapsedTime(&ms, t0, t1) != hipSuccess) st = fail(VX_ERR_HIP, "hipEventElapsedTime failed");
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    VX_CHECK(st);
+    *avg_ms = (double)ms / ((double)reps * e->cfg.block_count);
+    return VX_OK;
 }
 
 }  // extern "C"
