@@ -131,6 +131,52 @@ typedef struct vx_fusion_push {     /* FusionPush acoustic.rs:257-268 */
     uint32_t weight_dtype, bias_dtype, row_base;
 } vx_fusion_push;
 
+/* Token-batched ("seq") push structs of the LocEnc/LocDiT pipelines,
+ * identical to local.rs:183-212. */
+typedef struct vx_seq_linear_push {   /* SeqLinearPush local.rs:183-184 */
+    uint32_t weight_offset, bias_offset, rows, cols, weight_dtype, bias_dtype, tokens;
+    uint32_t input_stride, output_stride, input_base, output_base, has_bias;
+    float alpha;
+} vx_seq_linear_push;
+
+typedef struct vx_seq_rms_push {      /* SeqRmsPush local.rs:185-186 */
+    uint32_t weight_offset, n, tokens, input_stride, output_stride, input_base, output_base;
+    float eps;
+} vx_seq_rms_push;
+
+typedef struct vx_seq_residual_rms_push { /* SeqResidualRmsPush local.rs:187-188 */
+    uint32_t weight_offset, n, tokens, hidden_stride, branch_stride, output_stride;
+    uint32_t hidden_base, branch_base, output_base;
+    float eps, scale;
+} vx_seq_residual_rms_push;
+
+typedef struct vx_seq_qkv_push {      /* SeqQkvPush local.rs:189-190 */
+    uint32_t q_weight_offset, k_weight_offset, v_weight_offset, q_rows, kv_rows, cols, tokens;
+    uint32_t input_stride, q_stride, kv_stride, input_base;
+} vx_seq_qkv_push;
+
+typedef struct vx_seq_swiglu_push {   /* SeqSwigluPush local.rs:191-192 */
+    uint32_t gate_weight_offset, up_weight_offset, rows, cols, tokens;
+    uint32_t input_stride, output_stride, input_base, output_base;
+} vx_seq_swiglu_push;
+
+typedef struct vx_seq_rope_push {     /* SeqRopePush local.rs:193-194 */
+    uint32_t factor_offset, tokens, q_heads, kv_heads, head_dim, q_stride, k_stride;
+    float rope_theta, scaling_factor;
+} vx_seq_rope_push;
+
+typedef struct vx_dense_scores_push { /* DenseScoresPush local.rs:195-196 */
+    uint32_t tokens, q_heads, kv_heads, head_dim, q_stride, k_stride, score_stride;
+} vx_dense_scores_push;
+
+typedef struct vx_dense_softmax_push { /* DenseSoftmaxPush local.rs:197-198 */
+    uint32_t tokens, q_heads, score_stride;
+} vx_dense_softmax_push;
+
+typedef struct vx_dense_values_push { /* DenseValuesPush local.rs:199-200 */
+    uint32_t tokens, q_heads, kv_heads, head_dim, out_stride, v_stride, score_stride;
+} vx_dense_values_push;
+
 /* ------------------------------------------------------------------------- */
 /* Context, buffers, streams (replaces VulkanContext, vulkan.rs:96-113).      */
 /* ------------------------------------------------------------------------- */
@@ -279,6 +325,46 @@ int vx_linear_bias(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *
 /* fusion_linear.comp:56-78, dispatch acoustic.rs:941-966 (two identical outputs). */
 int vx_fusion_linear(vx_ctx *ctx, const vx_model *model, const vx_buf *left, const vx_buf *right,
                      vx_buf *y, vx_buf *snapshot, const vx_fusion_push *pc);
+
+/* ------------------------------------------------------------------------- */
+/* Token-batched per-op entry points (the seq_* / dense_* pipelines, dispatched */
+/* by local.rs:482-560). Buffers are f32 [tokens][stride] with the push's base */
+/* offsets (in floats). Projections run on MFMA (f16 hi/lo activations, exact  */
+/* weights, fp32 accumulation) when the weights are Q8_0 rows a multiple of    */
+/* 1024 wide or F16 rows a multiple of 128 and input rows are 16-byte aligned; */
+/* other shapes and F32 weights take a one-wave-per-output kernel.             */
+/* ------------------------------------------------------------------------- */
+/* seq_linear_bias.comp:22-30, record_linear local.rs:549-556:
+ * y[t][r] = alpha * (W[r] . x[t] + b[r]); weight dtype 0/1/8, bias 0/1. */
+int vx_seq_linear_bias(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y,
+                       const vx_seq_linear_push *pc);
+/* seq_qkv.comp:17-28, record_qkv local.rs:539-546. The reference shader reads
+ * F16 weights only; here each of q/k/v may be F16 or Q8_0 (from the tensor table). */
+int vx_seq_qkv(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *q, vx_buf *k, vx_buf *v,
+               const vx_seq_qkv_push *pc);
+/* seq_swiglu.comp:9, record_swiglu local.rs:560: y = silu(Wg.x) * (Wu.x); F16 or Q8_0. */
+int vx_seq_swiglu(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_seq_swiglu_push *pc);
+/* seq_silu_mul.comp:6: gate[i] = silu(gate[i]) * up[i], i < n. */
+int vx_seq_silu_mul(vx_ctx *ctx, vx_buf *gate, const vx_buf *up, uint32_t n);
+/* seq_rmsnorm.comp:9, record_rms local.rs:558. */
+int vx_seq_rmsnorm(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_seq_rms_push *pc);
+/* seq_residual_rmsnorm.comp:10, record_residual_rms local.rs:559. */
+int vx_seq_residual_rmsnorm(vx_ctx *ctx, const vx_model *model, vx_buf *hidden, const vx_buf *branch, vx_buf *y,
+                            const vx_seq_residual_rms_push *pc);
+/* seq_rope.comp:8 (position = token index, local.rs:498). */
+int vx_seq_rope(vx_ctx *ctx, const vx_model *model, vx_buf *q, vx_buf *k, const vx_seq_rope_push *pc);
+/* Same with token t at position position_base + t (the BaseLM prefill needs the
+ * decode position; the reference's seq_rope always starts at 0). */
+int vx_seq_rope_at(vx_ctx *ctx, const vx_model *model, vx_buf *q, vx_buf *k, uint32_t position_base,
+                   const vx_seq_rope_push *pc);
+/* dense_attn_scores.comp:8, dense_softmax.comp:5, dense_attn_values.comp:7
+ * (local.rs:500-504): full tokens x tokens attention, no causal mask. scores is
+ * f32 [tokens][q_heads][score_stride]. */
+int vx_dense_attn_scores(vx_ctx *ctx, const vx_buf *q, const vx_buf *k, vx_buf *scores,
+                         const vx_dense_scores_push *pc);
+int vx_dense_softmax(vx_ctx *ctx, vx_buf *scores, const vx_dense_softmax_push *pc);
+int vx_dense_attn_values(vx_ctx *ctx, const vx_buf *scores, const vx_buf *v, vx_buf *out,
+                         const vx_dense_values_push *pc);
 
 /* ------------------------------------------------------------------------- */
 /* Fused decode kernels used by the engine's graph (no single reference       */
@@ -461,6 +547,17 @@ int vx_baselm_decode_tokens_gpu_only(vx_baselm *eng, const uint32_t *tokens, uin
 /* prefill_tokens (baselm.rs:823-839): sequential decode of every token. */
 int vx_baselm_prefill_tokens(vx_baselm *eng, const uint32_t *tokens, uint32_t n, uint32_t top_k_last,
                              vx_step_result *res, vx_top_logit *top);
+/* Token-batched prefill: prefill_tokens (baselm.rs:823-839) with the n tokens
+ * run through the layer stack together -- MFMA projections over all tokens,
+ * causal attention over the KV cache, KV rows stored at positions
+ * position..position+n-1 -- instead of n sequential decode steps. Same engine
+ * state afterwards (KV cache, position, hidden/norm of the last token, its
+ * logits and top_k) to rounding. Needs Q8_0 row widths that are multiples of
+ * 1024 (F16: of 128), head_dim 64/128 and 1/2/4/8 query heads per KV head. */
+int vx_baselm_prefill_tokens_batched(vx_baselm *eng, const uint32_t *tokens, uint32_t n,
+                                     uint32_t top_k_last, vx_step_result *res, vx_top_logit *top);
+/* Same without the LM head, readback or host wait (the *_gpu_only semantics). */
+int vx_baselm_prefill_tokens_batched_gpu_only(vx_baselm *eng, const uint32_t *tokens, uint32_t n);
 typedef struct vx_baselm_benchmark_result { /* BaseLmBenchmark baselm.rs:413-421 */
     uint32_t iterations, token_id;
     double mean_ms, min_ms, max_ms, tokens_per_second;

@@ -61,6 +61,30 @@ LinearBiasPush = _struct("LinearBiasPush", [("weight_offset", u32), ("bias_offse
 FusionPush = _struct("FusionPush", [("weight_offset", u32), ("bias_offset", u32), ("rows", u32),
                                     ("left_cols", u32), ("right_cols", u32), ("weight_dtype", u32),
                                     ("bias_dtype", u32), ("row_base", u32)])
+# Token-batched push structs (local.rs:183-200).
+SeqLinearPush = _struct("SeqLinearPush", [(n, u32) for n in (
+    "weight_offset", "bias_offset", "rows", "cols", "weight_dtype", "bias_dtype", "tokens",
+    "input_stride", "output_stride", "input_base", "output_base", "has_bias")] + [("alpha", f32)])
+SeqRmsPush = _struct("SeqRmsPush", [(n, u32) for n in (
+    "weight_offset", "n", "tokens", "input_stride", "output_stride", "input_base",
+    "output_base")] + [("eps", f32)])
+SeqResidualRmsPush = _struct("SeqResidualRmsPush", [(n, u32) for n in (
+    "weight_offset", "n", "tokens", "hidden_stride", "branch_stride", "output_stride",
+    "hidden_base", "branch_base", "output_base")] + [("eps", f32), ("scale", f32)])
+SeqQkvPush = _struct("SeqQkvPush", [(n, u32) for n in (
+    "q_weight_offset", "k_weight_offset", "v_weight_offset", "q_rows", "kv_rows", "cols", "tokens",
+    "input_stride", "q_stride", "kv_stride", "input_base")])
+SeqSwigluPush = _struct("SeqSwigluPush", [(n, u32) for n in (
+    "gate_weight_offset", "up_weight_offset", "rows", "cols", "tokens", "input_stride",
+    "output_stride", "input_base", "output_base")])
+SeqRopePush = _struct("SeqRopePush", [(n, u32) for n in (
+    "factor_offset", "tokens", "q_heads", "kv_heads", "head_dim", "q_stride", "k_stride")] +
+    [("rope_theta", f32), ("scaling_factor", f32)])
+DenseScoresPush = _struct("DenseScoresPush", [(n, u32) for n in (
+    "tokens", "q_heads", "kv_heads", "head_dim", "q_stride", "k_stride", "score_stride")])
+DenseSoftmaxPush = _struct("DenseSoftmaxPush", [(n, u32) for n in ("tokens", "q_heads", "score_stride")])
+DenseValuesPush = _struct("DenseValuesPush", [(n, u32) for n in (
+    "tokens", "q_heads", "kv_heads", "head_dim", "out_stride", "v_stride", "score_stride")])
 DeviceInfo = _struct("DeviceInfo", [("name", C.c_char * 256), ("arch", C.c_char * 64),
                                     ("total_global_mem", u64), ("compute_units", u32),
                                     ("wavefront_size", u32), ("l2_cache_bytes", u32),
@@ -162,6 +186,17 @@ PROTOTYPES = {
     "vx_attn_values_devpos": (i32, [CTX, BUFP, BUFP, BUFP, BUFP, P(AttentionPush)]),
     "vx_linear_bias": (i32, [CTX, MODEL, BUFP, BUFP, P(LinearBiasPush)]),
     "vx_fusion_linear": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, BUFP, P(FusionPush)]),
+    "vx_seq_linear_bias": (i32, [CTX, MODEL, BUFP, BUFP, P(SeqLinearPush)]),
+    "vx_seq_qkv": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, BUFP, P(SeqQkvPush)]),
+    "vx_seq_swiglu": (i32, [CTX, MODEL, BUFP, BUFP, P(SeqSwigluPush)]),
+    "vx_seq_silu_mul": (i32, [CTX, BUFP, BUFP, u32]),
+    "vx_seq_rmsnorm": (i32, [CTX, MODEL, BUFP, BUFP, P(SeqRmsPush)]),
+    "vx_seq_residual_rmsnorm": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, P(SeqResidualRmsPush)]),
+    "vx_seq_rope": (i32, [CTX, MODEL, BUFP, BUFP, P(SeqRopePush)]),
+    "vx_seq_rope_at": (i32, [CTX, MODEL, BUFP, BUFP, u32, P(SeqRopePush)]),
+    "vx_dense_attn_scores": (i32, [CTX, BUFP, BUFP, BUFP, P(DenseScoresPush)]),
+    "vx_dense_softmax": (i32, [CTX, BUFP, P(DenseSoftmaxPush)]),
+    "vx_dense_attn_values": (i32, [CTX, BUFP, BUFP, BUFP, P(DenseValuesPush)]),
     "vx_fused_qkv_rope_store": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP,
                                       P(FusedQkvArgs)]),
     "vx_fused_attention_scratch_bytes": (u64, [P(FusedAttnArgs)]),
@@ -194,6 +229,8 @@ PROTOTYPES = {
     "vx_baselm_decode_embedding_from_gpu_only": (i32, [ENGINE, BUFP, P(u32)]),
     "vx_baselm_decode_tokens_gpu_only": (i32, [ENGINE, P(u32), u32]),
     "vx_baselm_prefill_tokens": (i32, [ENGINE, P(u32), u32, u32, P(StepResult), P(TopLogit)]),
+    "vx_baselm_prefill_tokens_batched": (i32, [ENGINE, P(u32), u32, u32, P(StepResult), P(TopLogit)]),
+    "vx_baselm_prefill_tokens_batched_gpu_only": (i32, [ENGINE, P(u32), u32]),
     "vx_baselm_benchmark": (i32, [ENGINE, u32, u32, u32, P(BenchmarkResult)]),
     "vx_baselm_buffer": (BUFP, [ENGINE, u32]),
     "vx_baselm_profile_steps": (i32, [ENGINE, P(u32), u32, P(ProfEntry), u32, P(u32)]),
@@ -206,6 +243,11 @@ STRUCT_SIZES = {  # C name -> ctypes struct
     "vx_attention_push": AttentionPush, "vx_softmax_push": SoftmaxPush, "vx_qkv_push": QkvPush,
     "vx_swiglu_push": SwigluPush, "vx_residual_rms_push": ResidualRmsPush,
     "vx_linear_bias_push": LinearBiasPush, "vx_fusion_push": FusionPush,
+    "vx_seq_linear_push": SeqLinearPush, "vx_seq_rms_push": SeqRmsPush,
+    "vx_seq_residual_rms_push": SeqResidualRmsPush, "vx_seq_qkv_push": SeqQkvPush,
+    "vx_seq_swiglu_push": SeqSwigluPush, "vx_seq_rope_push": SeqRopePush,
+    "vx_dense_scores_push": DenseScoresPush, "vx_dense_softmax_push": DenseSoftmaxPush,
+    "vx_dense_values_push": DenseValuesPush,
     "vx_device_info": DeviceInfo, "vx_prof_entry": ProfEntry, "vx_tensor_info": TensorInfo,
     "vx_fused_qkv_args": FusedQkvArgs, "vx_fused_attn_args": FusedAttnArgs,
     "vx_fused_residual_args": FusedResidualArgs, "vx_fused_swiglu_args": FusedSwigluArgs,

@@ -139,6 +139,21 @@ class BaseLmEngine:
                  t.size, top_k_last, C.byref(r), top)
         return self._result(r, top)
 
+    def prefill_tokens_batched(self, tokens, top_k_last: int = 0) -> StepResult:
+        """prefill_tokens with all tokens through the layer stack at once (MFMA
+        projections, causal attention over the cache)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        r = abi.StepResult()
+        top = (abi.TopLogit * max(top_k_last, 1))()
+        abi.call("vx_baselm_prefill_tokens_batched", self.handle, t.ctypes.data_as(C.POINTER(C.c_uint32)),
+                 t.size, top_k_last, C.byref(r), top)
+        return self._result(r, top)
+
+    def prefill_tokens_batched_gpu_only(self, tokens) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        abi.call("vx_baselm_prefill_tokens_batched_gpu_only", self.handle,
+                 t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size)
+
     def benchmark(self, token_id: int, warmup: int, iterations: int) -> dict:
         b = abi.BenchmarkResult()
         abi.call("vx_baselm_benchmark", self.handle, token_id, warmup, iterations, C.byref(b))

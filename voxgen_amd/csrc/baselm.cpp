@@ -54,6 +54,12 @@ struct vx_baselm {
     bool fold_attn_merge = false;  // attention merge folded into the attn_out matvec
     uint32_t pos = 0;
     vx_graph *graphs[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+    // Token-batched prefill workspace (allocated on first use): residual stream,
+    // hi/lo f16 planes of the GEMM inputs, q/k/v, roped q planes, token ids.
+    uint32_t pf_cap = 0;   // tokens per chunk
+    vx_buf *pf_h = nullptr, *pf_xh = nullptr, *pf_xl = nullptr, *pf_ah = nullptr, *pf_al = nullptr;
+    vx_buf *pf_qh = nullptr, *pf_ql = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    vx_buf *pf_tok = nullptr;
 };
 
 namespace {
@@ -158,11 +164,14 @@ void free_all(vx_baselm *e) {
             }
     vx_buf **bufs[] = {&e->hidden, &e->norm,   &e->q,      &e->k,        &e->v,
                        &e->attention, &e->gate, &e->branch, &e->logits, &e->scores,
-                       &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table};
+                       &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table,
+                       &e->pf_h, &e->pf_xh,    &e->pf_xl,  &e->pf_ah,    &e->pf_al,     &e->pf_qh,
+                       &e->pf_ql, &e->pf_q,    &e->pf_k,   &e->pf_v,     &e->pf_tok};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
     }
+    e->pf_cap = 0;
 }
 
 inline float *F(vx_buf *b) { return static_cast<float *>(b->ptr); }
@@ -270,6 +279,21 @@ int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l) {
     }
 }
 
+// LM head on the final normalised hidden state (baselm.rs:1040-1050).
+int enqueue_logits(vx_baselm *e) {
+    ProfSpan sp(e->ctx, "baselm.logits");
+    const vx_baselm_config &c = e->cfg;
+    MatvecLaunch a;
+    a.w = e->output;
+    a.xl = F(e->norm);
+    a.rows = c.vocab_size;
+    a.cols = c.embedding_length;
+    a.alpha = e->logit_alpha;
+    a.epi = EPI_STORE;
+    a.y = F(e->logits);
+    return launch_matvec(e->ctx->stream, a);
+}
+
 // The fused decode step, enqueued on the context stream.
 int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
     vx_ctx *ctx = e->ctx;
@@ -296,18 +320,7 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
         VX_CHECK(launch_rmsnorm(s, F(e->hidden), F(e->norm), e->output_norm, c.embedding_length, c.rms_epsilon,
                                 U(e->position)));
     }
-    if (logits) {
-        ProfSpan sp(ctx, "baselm.logits");
-        MatvecLaunch a;
-        a.w = e->output;
-        a.xl = F(e->norm);
-        a.rows = c.vocab_size;
-        a.cols = c.embedding_length;
-        a.alpha = e->logit_alpha;
-        a.epi = EPI_STORE;
-        a.y = F(e->logits);
-        VX_CHECK(launch_matvec(s, a));
-    }
+    if (logits) VX_CHECK(enqueue_logits(e));
     return VX_OK;
 }
 
@@ -427,6 +440,275 @@ int run_step(vx_baselm *e, bool with_embedding, uint32_t token, bool logits) {
         g = ng;
     }
     return vx_graph_launch(e->ctx, g);
+}
+
+// ------------------------------------------------------------------ prefill
+// Token-batched prefill (the seq_* op family of local.rs:482-527 applied to the
+// BaseLM stack, with Q8_0 projections, a causal mask and a position base):
+//   embedding rows -> per layer:
+//     rmsnorm(h)*attn_norm -> f16 hi/lo planes        (k_seq_rmsnorm)
+//     q|k|v = planes . Wq|Wk|Wv                       (k_gemm, split-K)
+//     RoPE at pos0+t, K/V rows -> f16 cache, q planes  (k_seq_rope_store)
+//     causal attention over cache keys 0..pos0+t       (k_prefill_attn)
+//     h += scale * Wo . attn                           (k_gemm residual)
+//     rmsnorm(h)*ffn_norm -> planes                    (k_seq_rmsnorm)
+//     act = silu(Wg . n) * (Wu . n) -> planes          (k_gemm swiglu)
+//     h += scale * Wdown . act                         (k_gemm residual)
+//   then the last token's rmsnorm(h)*output_norm into the engine's norm buffer.
+// This computes what prefill_tokens (baselm.rs:823-839) computes one token at a
+// time: the same KV-cache rows and the same final state, to rounding.
+constexpr uint32_t kPrefillChunk = 512;
+
+int ensure_prefill_work(vx_baselm *e) {
+    if (e->pf_cap) return VX_OK;
+    const vx_baselm_config &c = e->cfg;
+    const uint32_t cap = std::min<uint32_t>(kPrefillChunk, c.active_context_length);
+    const uint64_t H = c.embedding_length, F = c.feed_forward_length, KV = c.kv_dim, T = cap;
+    vx_ctx *ctx = e->ctx;
+    VX_CHECK(alloc(ctx, T * H * 4u, &e->pf_h));
+    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_xh));
+    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_xl));
+    VX_CHECK(alloc(ctx, T * F * 2u, &e->pf_ah));
+    VX_CHECK(alloc(ctx, T * F * 2u, &e->pf_al));
+    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_qh));
+    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_ql));
+    VX_CHECK(alloc(ctx, T * H * 4u, &e->pf_q));
+    VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_k));
+    VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_v));
+    VX_CHECK(alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->pf_tok));
+    e->pf_cap = cap;
+    return VX_OK;
+}
+
+GemmSeg gemm_seg(const WRef &w, uint32_t rows, float *out, uint32_t ldo) {
+    GemmSeg g;
+    if (w.wt == WT_Q8) {
+        g.qs = static_cast<const int8_t *>(w.ptr);
+        g.d = w.d;
+    } else {
+        g.w = static_cast<const __half *>(w.ptr);
+    }
+    g.rows = rows;
+    g.out = out;
+    g.ldo = ldo;
+    return g;
+}
+
+// Split-K factor that brings a projection to about one workgroup per CU.
+uint32_t pick_split(const vx_baselm *e, uint32_t n_tiles, uint32_t T, uint32_t K) {
+    const uint32_t tiles = n_tiles * ((T + 63u) / 64u);
+    const uint32_t cus = e->ctx->props.multiProcessorCount > 0 ? (uint32_t)e->ctx->props.multiProcessorCount : 256u;
+    uint32_t ks = (cus + tiles - 1u) / tiles;
+    ks = std::min<uint32_t>(ks, 4u);
+    ks = std::min<uint32_t>(ks, std::max<uint32_t>(1u, K / 128u / 4u));
+    return std::max<uint32_t>(ks, 1u);
+}
+
+int check_prefill_layout(const vx_baselm *e) {
+    for (uint32_t l = 0; l < e->cfg.block_count; ++l) {
+        const Layer &L = e->layers[l];
+        const WRef *ws[] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+        for (const WRef *w : ws) {
+            if (w->wt == WT_Q8 && !w->ptr)
+                return fail(VX_ERR_UNSUPPORTED,
+                            "batched prefill needs Q8_0 row widths that are multiples of 1024 (layer %u)", l);
+            if (w->wt == WT_F16 && (w->cols % 128u))
+                return fail(VX_ERR_UNSUPPORTED, "batched prefill needs F16 row widths that are multiples of 128");
+            if (w->wt == WT_F32) return fail(VX_ERR_UNSUPPORTED, "batched prefill has no F32 projection path");
+        }
+    }
+    if (e->cfg.head_dim != 64u && e->cfg.head_dim != 128u)
+        return fail(VX_ERR_UNSUPPORTED, "batched prefill attention needs head_dim 64 or 128");
+    const uint32_t qpk = e->cfg.head_count / e->cfg.head_count_kv;
+    if (qpk != 1u && qpk != 2u && qpk != 4u && qpk != 8u)
+        return fail(VX_ERR_UNSUPPORTED, "batched prefill attention needs 1, 2, 4 or 8 query heads per KV head");
+    return VX_OK;
+}
+
+// One chunk of T tokens at positions pos0..pos0+T-1, token ids at tok (device).
+int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint32_t T) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_baselm_config &c = e->cfg;
+    const uint32_t nH = c.embedding_length, nF = c.feed_forward_length, nKV = c.kv_dim;
+    {
+        ProfSpan sp(ctx, "prefill.embedding");
+        VX_CHECK(launch_seq_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, nH, tok, T, c.vocab_size,
+                                      e->embedding_alpha, F(e->pf_h), nH));
+    }
+    const uint32_t ks_qkv = pick_split(e, (nH + 127u) / 128u + 2u * ((nKV + 127u) / 128u), T, nH);
+    const uint32_t ks_o = pick_split(e, (nH + 127u) / 128u, T, nH);
+    const uint32_t ks_down = pick_split(e, (nH + 127u) / 128u, T, nF);
+    for (uint32_t l = 0; l < c.block_count; ++l) {
+        const Layer &L = e->layers[l];
+        {
+            ProfSpan sp(ctx, "prefill.norm");
+            SeqNormArgs n;
+            n.h = F(e->pf_h);
+            n.ldh = nH;
+            n.w = L.attn_norm;
+            n.n = nH;
+            n.eps = c.rms_epsilon;
+            n.yh = H(e->pf_xh);
+            n.yl = H(e->pf_xl);
+            n.ldp = nH;
+            if (ks_qkv > 1) {
+                n.zero[0] = F(e->pf_q);
+                n.zero_n[0] = nH;
+                n.zero[1] = F(e->pf_k);
+                n.zero_n[1] = nKV;
+                n.zero[2] = F(e->pf_v);
+                n.zero_n[2] = nKV;
+            }
+            VX_CHECK(launch_seq_rmsnorm(s, n, T));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.qkv");
+            GemmArgs g;
+            g.wk = L.q.wt;
+            g.epi = GEPI_STORE;
+            g.seg[0] = gemm_seg(L.q, nH, F(e->pf_q), nH);
+            g.seg[1] = gemm_seg(L.k, nKV, F(e->pf_k), nKV);
+            g.seg[2] = gemm_seg(L.v, nKV, F(e->pf_v), nKV);
+            g.nseg = 3;
+            g.K = nH;
+            g.T = T;
+            g.xh = H(e->pf_xh);
+            g.xl = H(e->pf_xl);
+            g.ldx = nH;
+            g.ksplit = ks_qkv;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.rope_store");
+            SeqRopeArgs r;
+            r.q = F(e->pf_q);
+            r.k = F(e->pf_k);
+            r.v = F(e->pf_v);
+            r.ldq = nH;
+            r.ldk = nKV;
+            r.factors = e->rope_factors;
+            r.pos_base = pos0;
+            r.q_heads = c.head_count;
+            r.kv_heads = c.head_count_kv;
+            r.head_dim = c.head_dim;
+            r.theta = c.rope_theta;
+            r.scaling = e->rope_scaling;
+            r.q_inplace = 0;
+            r.qh = H(e->pf_qh);
+            r.ql = H(e->pf_ql);
+            r.ldqp = nH;
+            r.kc = H(e->kv_k);
+            r.vc = H(e->kv_v);
+            r.layer = l;
+            r.context = c.active_context_length;
+            VX_CHECK(launch_seq_rope_store(s, r, T));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.attention");
+            PrefillAttnArgs a;
+            a.qh = H(e->pf_qh);
+            a.ql = H(e->pf_ql);
+            a.ldq = nH;
+            a.kc = H(e->kv_k);
+            a.vc = H(e->kv_v);
+            a.layer = l;
+            a.context = c.active_context_length;
+            a.pos_base = pos0;
+            a.T = T;
+            a.q_heads = c.head_count;
+            a.kv_heads = c.head_count_kv;
+            a.head_dim = c.head_dim;
+            a.oh = H(e->pf_xh);
+            a.ol = H(e->pf_xl);
+            a.ldo = nH;
+            VX_CHECK(launch_prefill_attn(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.attn_out");
+            GemmArgs g;
+            g.wk = L.o.wt;
+            g.epi = GEPI_RESIDUAL;
+            g.seg[0] = gemm_seg(L.o, nH, F(e->pf_h), nH);
+            g.K = nH;
+            g.T = T;
+            g.xh = H(e->pf_xh);
+            g.xl = H(e->pf_xl);
+            g.ldx = nH;
+            g.scale = e->residual_scale;
+            g.ksplit = ks_o;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.norm");
+            SeqNormArgs n;
+            n.h = F(e->pf_h);
+            n.ldh = nH;
+            n.w = L.ffn_norm;
+            n.n = nH;
+            n.eps = c.rms_epsilon;
+            n.yh = H(e->pf_xh);
+            n.yl = H(e->pf_xl);
+            n.ldp = nH;
+            VX_CHECK(launch_seq_rmsnorm(s, n, T));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.swiglu");
+            GemmArgs g;
+            g.wk = L.gate.wt;
+            g.epi = GEPI_SWIGLU;
+            g.seg[0] = gemm_seg(L.gate, nF, nullptr, 0);
+            g.seg[1] = gemm_seg(L.up, nF, nullptr, 0);
+            g.nseg = 2;
+            g.K = nH;
+            g.T = T;
+            g.xh = H(e->pf_xh);
+            g.xl = H(e->pf_xl);
+            g.ldx = nH;
+            g.oh = H(e->pf_ah);
+            g.ol = H(e->pf_al);
+            g.ldp = nF;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "prefill.down");
+            GemmArgs g;
+            g.wk = L.down.wt;
+            g.epi = GEPI_RESIDUAL;
+            g.seg[0] = gemm_seg(L.down, nH, F(e->pf_h), nH);
+            g.K = nF;
+            g.T = T;
+            g.xh = H(e->pf_ah);
+            g.xl = H(e->pf_al);
+            g.ldx = nF;
+            g.scale = e->residual_scale;
+            g.ksplit = ks_down;
+            VX_CHECK(launch_gemm(s, g));
+        }
+    }
+    // Engine state after the chunk: hidden = last token's residual stream, norm =
+    // its rmsnorm(h)*output_norm (record_transformer's final residual_rmsnorm).
+    ProfSpan sp(ctx, "prefill.output_norm");
+    const float *last = F(e->pf_h) + (size_t)(T - 1u) * nH;
+    VX_HIP(hipMemcpyAsync(e->hidden->ptr, last, (size_t)nH * 4u, hipMemcpyDeviceToDevice, s));
+    return launch_rmsnorm(s, last, F(e->norm), e->output_norm, nH, c.rms_epsilon, nullptr);
+}
+
+// Prefill n tokens at the engine position: upload the ids, run the chunks, leave
+// the device position at the next decode position.
+int enqueue_prefill(vx_baselm *e, const uint32_t *tokens, uint32_t n) {
+    VX_CHECK(check_prefill_layout(e));
+    VX_CHECK(ensure_prefill_work(e));
+    hipStream_t s = e->ctx->stream;
+    VX_HIP(hipMemcpyAsync(e->pf_tok->ptr, tokens, (size_t)n * 4u, hipMemcpyHostToDevice, s));
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t T = std::min<uint32_t>(e->pf_cap, n - done);
+        VX_CHECK(enqueue_prefill_chunk(e, U(e->pf_tok) + done, e->pos + done, T));
+        done += T;
+    }
+    VX_CHECK(launch_set_step(s, U(e->tokens), U(e->position), e->pos + n, 0, 0));
+    e->pos += n;
+    return VX_OK;
 }
 
 int ensure_context(const vx_baselm *e, uint32_t steps) {  // baselm.rs:882-890
@@ -743,6 +1025,28 @@ int vx_baselm_prefill_tokens(vx_baselm *e, const uint32_t *tokens, uint32_t n, u
     // logits are observable, so earlier steps skip the LM head.
     if (n > 1) VX_CHECK(vx_baselm_decode_tokens_gpu_only(e, tokens, n - 1));
     return vx_baselm_decode_token(e, tokens[n - 1], top_k_last, res, top);
+}
+
+int vx_baselm_prefill_tokens_batched(vx_baselm *e, const uint32_t *tokens, uint32_t n, uint32_t top_k_last,
+                                     vx_step_result *res, vx_top_logit *top) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_prefill_tokens_batched: null engine");
+    if (!tokens || n == 0) return fail(VX_ERR_INVALID_ARG, "prefill token list is empty");
+    for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
+    VX_CHECK(ensure_context(e, n));
+    const double t0 = now_ms();
+    VX_CHECK(enqueue_prefill(e, tokens, n));
+    VX_CHECK(enqueue_logits(e));  // decode_token of the last token computes logits
+    VX_CHECK(vx_sync(e->ctx));
+    const double elapsed = now_ms() - t0;
+    return collect_result(e, e->pos - 1u, elapsed, top_k_last, res, top);
+}
+
+int vx_baselm_prefill_tokens_batched_gpu_only(vx_baselm *e, const uint32_t *tokens, uint32_t n) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_prefill_tokens_batched_gpu_only: null engine");
+    if (!tokens || n == 0) return fail(VX_ERR_INVALID_ARG, "prefill token list is empty");
+    for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
+    VX_CHECK(ensure_context(e, n));
+    return enqueue_prefill(e, tokens, n);
 }
 
 int vx_baselm_benchmark(vx_baselm *e, uint32_t token_id, uint32_t warmup, uint32_t iterations,

@@ -1,0 +1,917 @@
+// Token-batched ("seq") kernels for gfx950: the prefill projections as MFMA
+// GEMMs, causal attention over the f16 KV cache on MFMA, and the per-token ops
+// around them (rmsnorm, RoPE, KV store).
+//
+// Projection GEMM  C[t][n] = sum_k X[t][k] * W[n][k]  (t: token, n: weight row)
+//   * v_mfma_f32_32x32x16_f16, fp32 accumulation. Workgroup tile 64 tokens x 128
+//     rows, 4 waves of 32 tokens x 64 rows (two 32x32 MFMA tiles each), k-stages
+//     of 128 columns staged through LDS, next stage prefetched into registers
+//     while the current one is multiplied. __launch_bounds__(256, 2): two
+//     workgroups per CU so one's MFMA chain overlaps the other's VALU work.
+//   * Q8_0 weights are read from the lane-interleaved repack the decode matvecs
+//     stream (model.cpp). Every 128-byte span of a repacked row holds four whole
+//     32-column blocks (block 32g + 8kk + m, kk < 4, for span m of 1024-column
+//     group g), so a k-stage is one span per row: its int8 quants are widened to
+//     f16 exactly (|q| <= 127) into LDS and the block scales d are applied in fp32
+//     after each block's MFMAs: acc += d[n][b] * (sum_{k in b} q*x). The weights
+//     enter the product exactly, as d*q does in matvec.comp:32-44.
+//   * Activations are carried as two f16 planes, hi = f16(x), lo = f16(x - hi),
+//     and both are multiplied (two MFMAs per k-step), so x enters the product
+//     with ~22 significant bits. Activations must stay inside the f16 range
+//     (|x| < 65504); the producers of the planes are the seq kernels below.
+//   * F16 weights (the LocEnc/LocDiT seq_* shaders) are staged as they are.
+//   * Workgroups are numbered XCD-major: consecutive ids of one XCD cover all
+//     token tiles of the same weight rows, so each weight tile is read from HBM
+//     once and reused from that XCD's L2.
+//   * Split-K over k-stages with fp32 atomic adds for the thin (N <= 2560)
+//     projections, so that a T = 384 prefill still fills 256 CUs.
+#include <cfloat>
+
+#include "vx_internal.h"
+
+namespace vx {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float acc16 __attribute__((ext_vector_type(16)));
+
+constexpr int GM = 64;      // tokens per workgroup tile
+constexpr int GN = 128;     // weight rows per workgroup tile
+constexpr int GK = 128;     // columns per k-stage
+constexpr int LROW = 136;   // f16 per LDS row: 128 + 8 pad (272 B; rows shift 4 banks)
+
+__device__ __forceinline__ acc16 mfma(h8 a, h8 b, acc16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float h2f(unsigned short bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// Four signed int8 quants (one dword) -> four exact f16 values: (q ^ 0x80) is
+// q + 128 in 0..255; the f16 with bits 0x6400 | u is 1024 + u, minus 1152 = q.
+__device__ __forceinline__ uint2 q8x4_to_f16(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2v a = __builtin_bit_cast(h2v, lo) - bias;
+    const h2v b = __builtin_bit_cast(h2v, hi) - bias;
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
+// hi/lo f16 split of four floats.
+__device__ __forceinline__ void split4(float4 v, uint2 &hi, uint2 &lo) {
+    const h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    const h4 l = {(_Float16)(v.x - (float)h[0]), (_Float16)(v.y - (float)h[1]), (_Float16)(v.z - (float)h[2]),
+                  (_Float16)(v.w - (float)h[3])};
+    hi = __builtin_bit_cast(uint2, h);
+    lo = __builtin_bit_cast(uint2, l);
+}
+
+// Column of element c of stage block kk of k-stage s.
+template <int WK>
+__device__ __forceinline__ uint32_t stage_col(uint32_t s, uint32_t kk) {
+    if constexpr (WK == WT_Q8)
+        return 1024u * (s >> 3) + 256u * kk + 32u * (s & 7u);
+    else
+        return 128u * s + 32u * kk;
+}
+
+struct RowMap {
+    const int8_t *qs;
+    const __half *d;
+    const __half *w;
+    uint32_t row;
+    bool valid;
+};
+
+template <int EPI>
+__device__ __forceinline__ RowMap map_row(const GemmArgs &a, uint32_t tn, uint32_t seg, uint32_t rho) {
+    RowMap r;
+    uint32_t mat, row;
+    if constexpr (EPI == GEPI_SWIGLU) {
+        mat = (rho >> 5) & 1u;
+        row = 64u * tn + 32u * (rho >> 6) + (rho & 31u);
+    } else {
+        mat = seg;
+        row = (tn - a.seg[seg].tile0) * GN + rho;
+    }
+    const GemmSeg &s = a.seg[mat];
+    r.valid = row < s.rows;
+    r.row = row;
+    r.qs = s.qs;
+    r.d = s.d;
+    r.w = s.w;
+    return r;
+}
+
+template <int WK, bool XF32>
+struct StageRegs {
+    uint4 w[WK == WT_Q8 ? 4 : 8];
+    uint2 d;
+    uint4 x[XF32 ? 8 : 8];   // planes: 4 hi + 4 lo chunks; f32: 8 float4 chunks
+};
+
+template <int WK, bool XF32, int EPI>
+__device__ __forceinline__ void load_stage(const GemmArgs &a, uint32_t tn, uint32_t seg, uint32_t m0, uint32_t s,
+                                           StageRegs<WK, XF32> &r) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t K = a.K;
+    if constexpr (WK == WT_Q8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = tid + 256u * i, rho = c >> 3, p = c & 7u;
+            const RowMap m = map_row<EPI>(a, tn, seg, rho);
+            const size_t off = (size_t)m.row * K + 1024u * (s >> 3) + 128u * (s & 7u) + 16u * p;
+            r.w[i] = m.valid ? *reinterpret_cast<const uint4 *>(m.qs + off) : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < (uint32_t)GN) {
+            const RowMap m = map_row<EPI>(a, tn, seg, tid);
+            const size_t off = (size_t)m.row * (K / 32u) + 32u * (s >> 3) + 4u * (s & 7u);
+            r.d = m.valid ? *reinterpret_cast<const uint2 *>(m.d + off) : make_uint2(0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = tid + 256u * i, rho = c >> 4, p = c & 15u;
+            const RowMap m = map_row<EPI>(a, tn, seg, rho);
+            const size_t off = (size_t)m.row * K + 128u * s + 8u * p;
+            r.w[i] = m.valid ? *reinterpret_cast<const uint4 *>(m.w + off) : make_uint4(0, 0, 0, 0);
+        }
+    }
+    if constexpr (XF32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = tid + 256u * i, t = c >> 5, kk = (c >> 3) & 3u, q = c & 7u;
+            const uint32_t tok = m0 + t;
+            const size_t off = (size_t)tok * a.ldx + stage_col<WK>(s, kk) + 4u * q;
+            r.x[i] = tok < a.T ? *reinterpret_cast<const uint4 *>(a.xf + off) : make_uint4(0, 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = tid + 256u * i, t = c >> 4, kk = (c >> 2) & 3u, q = c & 3u;
+            const uint32_t tok = m0 + t;
+            const size_t off = (size_t)tok * a.ldx + stage_col<WK>(s, kk) + 8u * q;
+            const bool ok = tok < a.T;
+            r.x[i] = ok ? *reinterpret_cast<const uint4 *>(a.xh + off) : make_uint4(0, 0, 0, 0);
+            r.x[4 + i] = ok ? *reinterpret_cast<const uint4 *>(a.xl + off) : make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+template <int WK, bool XF32>
+__device__ __forceinline__ void store_stage(const StageRegs<WK, XF32> &r, _Float16 *Wl, _Float16 *Xh, _Float16 *Xl,
+                                            float *Ds) {
+    const uint32_t tid = threadIdx.x;
+    if constexpr (WK == WT_Q8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = tid + 256u * i, rho = c >> 3, p = c & 7u;
+            _Float16 *dst = Wl + rho * LROW + 4u * p;
+            const uint32_t words[4] = {r.w[i].x, r.w[i].y, r.w[i].z, r.w[i].w};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) *reinterpret_cast<uint2 *>(dst + 32 * kk) = q8x4_to_f16(words[kk]);
+        }
+        if (tid < (uint32_t)GN) {
+            Ds[0 * GN + tid] = h2f((unsigned short)(r.d.x & 0xffffu));
+            Ds[1 * GN + tid] = h2f((unsigned short)(r.d.x >> 16));
+            Ds[2 * GN + tid] = h2f((unsigned short)(r.d.y & 0xffffu));
+            Ds[3 * GN + tid] = h2f((unsigned short)(r.d.y >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = tid + 256u * i, rho = c >> 4, p = c & 15u;
+            *reinterpret_cast<uint4 *>(Wl + rho * LROW + 8u * p) = r.w[i];
+        }
+    }
+    if constexpr (XF32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = tid + 256u * i, t = c >> 5, kk = (c >> 3) & 3u, q = c & 7u;
+            uint2 hi, lo;
+            split4(__builtin_bit_cast(float4, r.x[i]), hi, lo);
+            *reinterpret_cast<uint2 *>(Xh + t * LROW + 32u * kk + 4u * q) = hi;
+            *reinterpret_cast<uint2 *>(Xl + t * LROW + 32u * kk + 4u * q) = lo;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = tid + 256u * i, t = c >> 4, kk = (c >> 2) & 3u, q = c & 3u;
+            *reinterpret_cast<uint4 *>(Xh + t * LROW + 32u * kk + 8u * q) = r.x[i];
+            *reinterpret_cast<uint4 *>(Xl + t * LROW + 32u * kk + 8u * q) = r.x[4 + i];
+        }
+    }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+template <int WK, bool XF32, int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 Wl[GN * LROW];
+    __shared__ __attribute__((aligned(16))) _Float16 Xh[GM * LROW];
+    __shared__ __attribute__((aligned(16))) _Float16 Xl[GM * LROW];
+    __shared__ float Ds[WK == WT_Q8 ? 4 * GN : 1];
+
+    // XCD-major tile order: workgroup b runs on XCD b % 8.
+    const uint32_t b = blockIdx.x;
+    const uint32_t id = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
+    const uint32_t per_split = a.ntn * a.ntm;
+    if (id >= per_split * a.ksplit) return;
+    const uint32_t ks = id / per_split, rem = id - ks * per_split;
+    const uint32_t tn = rem / a.ntm, tm = rem - tn * a.ntm;
+    const uint32_t m0 = tm * GM;
+    uint32_t seg = 0;
+    if constexpr (EPI != GEPI_SWIGLU) {
+        while (seg + 1 < a.nseg && tn >= a.seg[seg + 1].tile0) ++seg;
+    }
+    const uint32_t S = a.K / GK;
+    const uint32_t s0 = ks * S / a.ksplit, s1 = (ks + 1) * S / a.ksplit;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wv & 1u, wn = wv >> 1;
+
+    acc16 acc0 = {}, acc1 = {};
+    StageRegs<WK, XF32> st;
+    if (s0 < s1) load_stage<WK, XF32, EPI>(a, tn, seg, m0, s0, st);
+    const _Float16 *xa = Xh + (32u * wm + l32) * LROW + 8u * hs;
+    const _Float16 *xb = Xl + (32u * wm + l32) * LROW + 8u * hs;
+    const _Float16 *wa = Wl + (64u * wn + l32) * LROW + 8u * hs;
+    const _Float16 *wb = wa + 32 * LROW;
+    for (uint32_t s = s0; s < s1; ++s) {
+        __syncthreads();
+        store_stage<WK, XF32>(st, Wl, Xh, Xl, Ds);
+        __syncthreads();
+        if (s + 1 < s1) load_stage<WK, XF32, EPI>(a, tn, seg, m0, s + 1, st);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            if constexpr (WK == WT_Q8) {
+                acc16 p0 = {}, p1 = {};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int off = 32 * kk + 16 * h;
+                    const h8 ah = *reinterpret_cast<const h8 *>(xa + off);
+                    const h8 al = *reinterpret_cast<const h8 *>(xb + off);
+                    const h8 b0 = *reinterpret_cast<const h8 *>(wa + off);
+                    const h8 b1 = *reinterpret_cast<const h8 *>(wb + off);
+                    p0 = mfma(ah, b0, p0);
+                    p1 = mfma(ah, b1, p1);
+                    p0 = mfma(al, b0, p0);
+                    p1 = mfma(al, b1, p1);
+                }
+                const float d0 = Ds[kk * GN + 64u * wn + l32];
+                const float d1 = Ds[kk * GN + 64u * wn + 32u + l32];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc0[r] = fmaf(d0, p0[r], acc0[r]);
+                    acc1[r] = fmaf(d1, p1[r], acc1[r]);
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int off = 32 * kk + 16 * h;
+                    const h8 ah = *reinterpret_cast<const h8 *>(xa + off);
+                    const h8 al = *reinterpret_cast<const h8 *>(xb + off);
+                    const h8 b0 = *reinterpret_cast<const h8 *>(wa + off);
+                    const h8 b1 = *reinterpret_cast<const h8 *>(wb + off);
+                    acc0 = mfma(ah, b0, acc0);
+                    acc1 = mfma(ah, b1, acc1);
+                    acc0 = mfma(al, b0, acc0);
+                    acc1 = mfma(al, b1, acc1);
+                }
+            }
+        }
+    }
+
+    // Epilogue. Lane (l32, hs) holds weight row rho = 64wn + 32*tile + l32 and
+    // tokens m0 + 32wm + 8(r/4) + 4hs + r%4 (r < 16) of each tile.
+    const uint32_t tbase = m0 + 32u * wm + 4u * hs;
+    if constexpr (EPI == GEPI_SWIGLU) {
+        const RowMap mg = map_row<EPI>(a, tn, 0, 64u * wn + l32);
+        if (!mg.valid) return;
+        const uint32_t row = mg.row;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t tok = tbase + 8u * (r >> 2) + (r & 3);
+            if (tok >= a.T) continue;
+            const float v = silu_mul(acc0[r], acc1[r]);
+            if (a.seg[0].out) a.seg[0].out[(size_t)tok * a.seg[0].ldo + row] = v;
+            if (a.oh) {
+                const _Float16 hv = (_Float16)v;
+                a.oh[(size_t)tok * a.ldp + row] = __builtin_bit_cast(__half, hv);
+                a.ol[(size_t)tok * a.ldp + row] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
+            }
+        }
+    } else {
+        const GemmSeg &sg = a.seg[seg];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const RowMap mr = map_row<EPI>(a, tn, seg, 64u * wn + 32u * t + l32);
+            if (!mr.valid) continue;
+            const uint32_t row = mr.row;
+            float bias = 0.f;
+            if (EPI == GEPI_STORE && sg.bias && ks == 0)
+                bias = sg.bias_dtype == 0 ? static_cast<const float *>(sg.bias)[row]
+                                          : h2f(static_cast<const unsigned short *>(sg.bias)[row]);
+            const acc16 &acc = t == 0 ? acc0 : acc1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t tok = tbase + 8u * (r >> 2) + (r & 3);
+                if (tok >= a.T) continue;
+                float *dst = sg.out + (size_t)tok * sg.ldo + row;
+                if constexpr (EPI == GEPI_STORE) {
+                    const float v = (acc[r] + bias) * a.alpha;
+                    if (a.ksplit > 1)
+                        unsafeAtomicAdd(dst, v);
+                    else
+                        *dst = v;
+                } else {  // GEPI_RESIDUAL: hidden += scale * (W . x)
+                    const float v = acc[r] * a.scale;
+                    if (a.ksplit > 1)
+                        unsafeAtomicAdd(dst, v);
+                    else
+                        *dst = *dst + v;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------
+// Per-token (residual +) rmsnorm: seq_rmsnorm.comp:9 / seq_residual_rmsnorm.comp:10.
+// One workgroup per token. If branch != nullptr, h += scale * branch first (and
+// h is written back). y = h * (1/sqrt(mean(h^2) + eps)) * w is written as f32
+// (y, nullable) and/or as hi/lo f16 planes (yh/yl, nullable). Optionally zeroes
+// `zero_n` floats of row t of up to three buffers (split-K accumulators).
+__global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x;
+    float *h = a.h + (size_t)t * a.ldh;
+    const float *br = a.branch ? a.branch + (size_t)t * a.ldb : nullptr;
+    float s = 0.f;
+    for (uint32_t i = threadIdx.x; i < a.n; i += 256u) {
+        float v = h[i];
+        if (br) {
+            v = v + br[i] * a.scale;
+            h[i] = v;
+        }
+        s += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    s = red[0] + red[1] + red[2] + red[3];
+    const float inv_rms = 1.0f / sqrtf(s / (float)a.n + a.eps);
+    for (uint32_t i = threadIdx.x; i < a.n; i += 256u) {
+        const float v = h[i] * inv_rms * a.w[i];
+        if (a.y) a.y[(size_t)t * a.ldy + i] = v;
+        if (a.yh) {
+            const _Float16 hv = (_Float16)v;
+            a.yh[(size_t)t * a.ldp + i] = __builtin_bit_cast(__half, hv);
+            a.yl[(size_t)t * a.ldp + i] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
+        }
+    }
+    for (int z = 0; z < 3; ++z)
+        if (a.zero[z])
+            for (uint32_t i = threadIdx.x; i < a.zero_n[z]; i += 256u) a.zero[z][(size_t)t * a.zero_n[z] + i] = 0.f;
+}
+
+// Per-token RoPE at position base + t (rope.comp:22-51 / seq_rope.comp:8 with a
+// position base), then the f16 KV store of token t at that position
+// (store_kv.comp:16-24), and q as hi/lo planes for the attention kernel.
+// The angle is computed exactly as the decode step's per-step table.
+__global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
+    __shared__ float2 cs[64];
+    const uint32_t t = blockIdx.x;
+    const uint32_t pos = a.pos_base + t;
+    const uint32_t half_dim = a.head_dim / 2u;
+    if (threadIdx.x < half_dim) {
+        const uint32_t i = threadIdx.x;
+        const float exponent = (float)(i * 2u) / (float)a.head_dim;
+        const float inv_freq = 1.0f / powf(a.theta, exponent);
+        const float angle = (float)pos * inv_freq / a.factors[i];
+        cs[i] = make_float2(cosf(angle) * a.scaling, sinf(angle) * a.scaling);
+    }
+    __syncthreads();
+    float *q = a.q + (size_t)t * a.ldq;
+    float *k = a.k + (size_t)t * a.ldk;
+    const uint32_t q_pairs = a.q_heads * half_dim, k_pairs = a.kv_heads * half_dim;
+    for (uint32_t p = threadIdx.x; p < q_pairs + k_pairs; p += 256u) {
+        const bool isq = p < q_pairs;
+        const uint32_t pp = isq ? p : p - q_pairs;
+        const uint32_t head = pp / half_dim, i = pp - head * half_dim;
+        float *buf = isq ? q : k;
+        const uint32_t base = head * a.head_dim;
+        const float x0 = buf[base + i], x1 = buf[base + i + half_dim];
+        const float c = cs[i].x, s = cs[i].y;
+        const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
+        if (isq) {
+            if (a.q_inplace) {
+                buf[base + i] = y0;
+                buf[base + i + half_dim] = y1;
+            }
+            if (a.qh) {
+                const size_t o = (size_t)t * a.ldqp + base + i;
+                const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+                a.qh[o] = __builtin_bit_cast(__half, h0);
+                a.ql[o] = __builtin_bit_cast(__half, (_Float16)(y0 - (float)h0));
+                a.qh[o + half_dim] = __builtin_bit_cast(__half, h1);
+                a.ql[o + half_dim] = __builtin_bit_cast(__half, (_Float16)(y1 - (float)h1));
+            }
+        } else {
+            buf[base + i] = y0;
+            buf[base + i + half_dim] = y1;
+        }
+    }
+    if (!a.kc) return;
+    __syncthreads();  // roped k visible to the store below
+    if (pos >= a.context) return;
+    const float *v = a.v + (size_t)t * a.ldk;
+    const uint32_t kv_dim = a.kv_heads * a.head_dim;
+    const size_t dst = ((size_t)a.layer * a.context + pos) * kv_dim;
+    for (uint32_t i = threadIdx.x; i < kv_dim; i += 256u) {
+        a.kc[dst + i] = __float2half_rn(k[i]);
+        a.vc[dst + i] = __float2half_rn(v[i]);
+    }
+}
+
+// ------------------------------------------------------------------------
+// Causal attention of a token block over the f16 KV cache on MFMA
+// (attn_scores.comp + softmax.comp + attn_values.comp for every query token
+// t at position pos_base + t over keys 0..pos_base + t, as the decode step would
+// compute them one token at a time).
+//
+// Workgroup: one KV head g and TPB = 32 / QPK consecutive query tokens, i.e. 32
+// query rows (token x the QPK query heads of g). Four waves split the key blocks
+// (32 keys each) round-robin, each keeping an online-softmax state, and merge at
+// the end through LDS.
+//   S^T (keys x rows) = K . Q^T   A = K block from LDS, B = q (hi and lo planes)
+//   O^T (dims x rows) += V^T . P^T A = V^T from LDS, B = p (hi/lo) from registers
+// Lane (l32, hs) holds query row l32 in both, so the softmax of a row is one
+// in-lane reduction and one exchange with lane ^ 32, and p feeds the second
+// product from the lane's own registers: its register r (key 8(r/4)+4hs+r%4)
+// is used in k-slot 8hs + r%8 of k-step r/8, and the V^T operand supplies the
+// same keys for those slots.
+template <int HD, int QPK>
+__global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
+    constexpr int TPB = 32 / QPK;
+    constexpr int KROW = HD + 8;   // K block row (f16)
+    constexpr int VROW = 40;       // V^T row: 32 keys + 8 pad (f16)
+    constexpr int ND = HD / 32;    // output tiles of 32 dims
+    constexpr int KS = HD / 16;    // k-steps over the head dim
+    constexpr int WAVE_LDS = 32 * KROW + HD * VROW;   // f16 per wave
+    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * WAVE_LDS];
+    static_assert(4 * WAVE_LDS * 2 >= 4 * (ND * 16 * 64 * 4 + 2 * 32 * 4), "merge area");
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = blockIdx.y;
+    const uint32_t t0 = blockIdx.x * TPB;
+    const uint32_t tq = t0 + l32 / QPK;
+    const uint32_t head = g * QPK + l32 % QPK;
+    const bool qvalid = tq < a.T;
+    const uint32_t qpos = a.pos_base + (qvalid ? tq : a.T - 1u);
+    const uint32_t tlast = min(t0 + (uint32_t)TPB, a.T) - 1u;
+    const uint32_t kmax = a.pos_base + tlast;   // last key any row of the block needs
+    const uint32_t nblocks = kmax / 32u + 1u;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const uint32_t kv_dim = a.kv_heads * HD;
+
+    h8 qh[KS], ql[KS];
+    {
+        const size_t qo = (size_t)(qvalid ? tq : 0u) * a.ldq + head * HD + 8u * hs;
+#pragma unroll
+        for (int ds = 0; ds < KS; ++ds) {
+            qh[ds] = qvalid ? *reinterpret_cast<const h8 *>(a.qh + qo + 16 * ds) : h8{};
+            ql[ds] = qvalid ? *reinterpret_cast<const h8 *>(a.ql + qo + 16 * ds) : h8{};
+        }
+    }
+    _Float16 *Ks = lds + w * WAVE_LDS;
+    _Float16 *Vt = Ks + 32 * KROW;
+
+    float m = -INFINITY, l = 0.f;
+    acc16 o[ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) o[dt] = acc16{};
+
+    for (uint32_t kb = w; kb < nblocks; kb += 4u) {
+        const uint32_t key0 = kb * 32u;
+        // Stage K (row per key) and V^T (row per dim) of keys key0..key0+31.
+        constexpr int CHUNKS = 32 * HD / 8;   // 16-byte chunks per block
+#pragma unroll
+        for (int i = 0; i < CHUNKS / 64; ++i) {
+            const uint32_t c = lane + 64u * i, key = c / (HD / 8), p = c % (HD / 8);
+            const uint32_t kp = key0 + key;
+            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+            if (kp <= kmax && kp < a.context) {
+                const size_t src = ((size_t)a.layer * a.context + kp) * kv_dim + g * HD + 8u * p;
+                kv = *reinterpret_cast<const uint4 *>(a.kc + src);
+                vv = *reinterpret_cast<const uint4 *>(a.vc + src);
+            }
+            *reinterpret_cast<uint4 *>(Ks + key * KROW + 8u * p) = kv;
+            const h8 vh = __builtin_bit_cast(h8, vv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Vt[(8u * p + j) * VROW + key] = vh[j];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        acc16 sc = {};
+#pragma unroll
+        for (int ds = 0; ds < KS; ++ds) {
+            const h8 kf = *reinterpret_cast<const h8 *>(Ks + l32 * KROW + 16 * ds + 8 * hs);
+            sc = mfma(kf, qh[ds], sc);
+            sc = mfma(kf, ql[ds], sc);
+        }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t key = key0 + 8u * (r >> 2) + 4u * hs + (r & 3);
+            sc[r] = key <= qpos ? sc[r] * scale : -INFINITY;
+            mloc = fmaxf(mloc, sc[r]);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float mnew = fmaxf(m, mloc);
+        float lsum = 0.f;
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = sc[r] == -INFINITY ? 0.f : expf(sc[r] - mnew);
+            lsum += p[r];
+        }
+        lsum += __shfl_xor(lsum, 32, 64);
+        const float alpha = m == -INFINITY ? 0.f : expf(m - mnew);
+        l = l * alpha + lsum;
+        m = mnew;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        h8 ph[2], pl[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float v = p[8 * kh + i];
+                const _Float16 hv = (_Float16)v;
+                ph[kh][i] = hv;
+                pl[kh][i] = (_Float16)(v - (float)hv);
+            }
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                const _Float16 *vr = Vt + (32u * dt + l32) * VROW + 16u * kh + 4u * hs;
+                const h4 v0 = *reinterpret_cast<const h4 *>(vr);
+                const h4 v1 = *reinterpret_cast<const h4 *>(vr + 8);
+                const h8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[dt] = mfma(vf, ph[kh], o[dt]);
+                o[dt] = mfma(vf, pl[kh], o[dt]);
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // Merge the four waves' states: wave w finalises output dims 32w..32w+31.
+    __syncthreads();
+    float *mo = reinterpret_cast<float *>(lds);            // [4 waves][ND][16][64]
+    float *ms = mo + 4 * ND * 16 * 64;                      // [4][32] max
+    float *ls = ms + 4 * 32;                                // [4][32] sum
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mo[((w * ND + dt) * 16 + r) * 64 + lane] = o[dt][r];
+    if (hs == 0) {
+        ms[w * 32 + l32] = m;
+        ls[w * 32 + l32] = l;
+    }
+    __syncthreads();
+    for (uint32_t dt = w; dt < (uint32_t)ND; dt += 4u) {
+        float mw[4], M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            mw[v] = ms[v * 32 + l32];
+            M = fmaxf(M, mw[v]);
+        }
+        float wt[4], L = 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            wt[v] = mw[v] == -INFINITY ? 0.f : expf(mw[v] - M);
+            L += wt[v] * ls[v * 32 + l32];
+        }
+        const float inv = 1.0f / L;
+        if (!qvalid) continue;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            float outv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 4 * r4 + j;
+                float acc = 0.f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc += wt[v] * mo[((v * ND + dt) * 16 + r) * 64 + lane];
+                outv[j] = acc * inv;
+            }
+            const uint32_t d = 32u * dt + 8u * r4 + 4u * hs;
+            const size_t oo = (size_t)tq * a.ldo + head * HD + d;
+            if (a.out) *reinterpret_cast<float4 *>(a.out + oo) = make_float4(outv[0], outv[1], outv[2], outv[3]);
+            if (a.oh) {
+                uint2 hi, lo;
+                split4(make_float4(outv[0], outv[1], outv[2], outv[3]), hi, lo);
+                *reinterpret_cast<uint2 *>(a.oh + oo) = hi;
+                *reinterpret_cast<uint2 *>(a.ol + oo) = lo;
+            }
+        }
+    }
+}
+
+// Embedding rows of T tokens (embedding.comp:28-48 per token): rows of the raw
+// GGUF table (F16 or Q8_0 blocks) widened to f32 and scaled, bit-exact. Ids
+// >= vocab give NaN rows; the host rejects them before launching.
+__global__ __launch_bounds__(256) void k_seq_embedding(const uint8_t *raw, uint32_t off, uint32_t dtype,
+                                                      uint32_t cols, const uint32_t *tokens, uint32_t vocab,
+                                                      float alpha, float *out, uint32_t ldo) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x, t = blockIdx.y;
+    if (i >= cols) return;
+    const uint32_t token = tokens[t];
+    float *dst = out + (size_t)t * ldo + i;
+    if (token >= vocab) {
+        *dst = __int_as_float(0x7fc00000);
+        return;
+    }
+    float w;
+    if (dtype == VX_DTYPE_F16) {
+        w = h2f(*reinterpret_cast<const unsigned short *>(raw + off + ((size_t)token * cols + i) * 2u));
+    } else {
+        const size_t block = (size_t)token * (cols / 32u) + i / 32u;
+        const uint8_t *b = raw + off + block * 34u;
+        w = h2f((unsigned short)(b[0] | (b[1] << 8))) * (float)(int)(int8_t)b[2 + (i & 31u)];
+    }
+    *dst = w * alpha;
+}
+
+// ------------------------------------------------------------------------
+// Reference-granular token-batched kernels for shapes the MFMA GEMM does not
+// take (F32 weights, Q8_0 rows not a multiple of 1024 wide, unaligned strides)
+// and the LocEnc/LocDiT dense attention (non-causal, f32).
+
+// Weight element (row r, column c) of a dtype 0/1/8 matrix in the raw GGUF
+// region (seq_linear_bias.comp:16-21).
+__device__ __forceinline__ float weight_at(const uint8_t *raw, uint32_t off, uint32_t dtype, uint32_t cols,
+                                           uint32_t r, uint32_t c) {
+    if (dtype == VX_DTYPE_F32) return reinterpret_cast<const float *>(raw + off)[(size_t)r * cols + c];
+    if (dtype == VX_DTYPE_F16) return h2f(reinterpret_cast<const unsigned short *>(raw + off)[(size_t)r * cols + c]);
+    const uint8_t *b = raw + off + ((size_t)r * (cols / 32u) + c / 32u) * 34u;
+    return h2f((unsigned short)(b[0] | (b[1] << 8))) * (float)(int)(int8_t)b[2u + (c & 31u)];
+}
+
+// One wave per (row, token): seq_linear_bias.comp:22-30 (mode 0) and
+// seq_swiglu.comp:9 (mode 1, gate at w_off, up at w2_off).
+__global__ __launch_bounds__(256) void k_seq_linear_generic(SeqGenericArgs a) {
+    const uint32_t idx = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (idx >= a.rows * a.tokens) return;
+    const uint32_t row = idx % a.rows, tok = idx / a.rows;
+    const float *x = a.x + a.in_base + (size_t)tok * a.in_stride;
+    float s = 0.f, s2 = 0.f;
+    for (uint32_t c = lane; c < a.cols; c += 64u) {
+        const float xv = x[c];
+        s += weight_at(a.raw, a.w_off, a.dtype, a.cols, row, c) * xv;
+        if (a.swiglu) s2 += weight_at(a.raw, a.w2_off, a.dtype, a.cols, row, c) * xv;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        s += __shfl_xor(s, o, 64);
+        s2 += __shfl_xor(s2, o, 64);
+    }
+    if (lane != 0) return;
+    float v;
+    if (a.swiglu) {
+        v = s / (1.0f + expf(-s)) * s2;
+    } else {
+        float b = 0.f;
+        if (a.has_bias)
+            b = a.bias_dtype == 0u ? reinterpret_cast<const float *>(a.raw + a.bias_off)[row]
+                                   : h2f(reinterpret_cast<const unsigned short *>(a.raw + a.bias_off)[row]);
+        v = (s + b) * a.alpha;
+    }
+    a.y[a.out_base + (size_t)tok * a.out_stride + row] = v;
+}
+
+// seq_silu_mul.comp:6: g = silu(g) * u.
+__global__ __launch_bounds__(256) void k_silu_mul(float *g, const float *u, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float x = g[i];
+    g[i] = x / (1.0f + expf(-x)) * u[i];
+}
+
+// dense_attn_scores.comp:8: s[(t*q_heads + h)*score_stride + key] = q_t,h . k_key,kv / sqrt(d),
+// for every key < tokens (no mask). Workgroup (query token, head), lane per key.
+__global__ __launch_bounds__(64) void k_dense_scores(DenseAttnArgs a) {
+    __shared__ float qs[256];
+    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const uint32_t kv = h / (a.q_heads / a.kv_heads);
+    const float *q = a.q + (size_t)t * a.q_stride + h * a.head_dim;
+    for (uint32_t i = threadIdx.x; i < a.head_dim; i += 64u) qs[i] = q[i];
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)a.head_dim);
+    for (uint32_t key = threadIdx.x; key < a.tokens; key += 64u) {
+        const float *k = a.k + (size_t)key * a.k_stride + kv * a.head_dim;
+        float s = 0.f;
+        for (uint32_t i = 0; i < a.head_dim; ++i) s += qs[i] * k[i];
+        a.s[((size_t)t * a.q_heads + h) * a.score_stride + key] = s * scale;
+    }
+}
+
+// dense_softmax.comp:5: max-subtracted softmax of each (token, head) row.
+__global__ __launch_bounds__(64) void k_dense_softmax(float *s, uint32_t tokens, uint32_t q_heads,
+                                                      uint32_t score_stride) {
+    const uint32_t h = blockIdx.x, t = blockIdx.y;
+    float *row = s + ((size_t)t * q_heads + h) * score_stride;
+    float m = -FLT_MAX;
+    for (uint32_t i = threadIdx.x; i < tokens; i += 64u) m = fmaxf(m, row[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float z = 0.f;
+    for (uint32_t i = threadIdx.x; i < tokens; i += 64u) {
+        const float e = expf(row[i] - m);
+        row[i] = e;
+        z += e;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o, 64);
+    for (uint32_t i = threadIdx.x; i < tokens; i += 64u) row[i] = row[i] / z;
+}
+
+// dense_attn_values.comp:7: o[t*out_stride + h*d + j] = sum_key s[...key] * v[key*v_stride + kv*d + j].
+__global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
+    const uint32_t j = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
+    if (j >= a.head_dim) return;
+    const uint32_t kv = h / (a.q_heads / a.kv_heads);
+    const float *row = a.s + ((size_t)t * a.q_heads + h) * a.score_stride;
+    float z = 0.f;
+    for (uint32_t key = 0; key < a.tokens; ++key) z += row[key] * a.v[(size_t)key * a.v_stride + kv * a.head_dim + j];
+    a.out[(size_t)t * a.out_stride + h * a.head_dim + j] = z;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+int launch_gemm(hipStream_t s, const GemmArgs &in) {
+    GemmArgs a = in;
+    if (a.T == 0) return VX_OK;
+    if (a.nseg == 0 || a.nseg > 3) return fail(VX_ERR_INVALID_ARG, "gemm: 1..3 weight segments");
+    if (a.wk == WT_Q8 ? (a.K % 1024u) : (a.K % (uint32_t)GK))
+        return fail(VX_ERR_UNSUPPORTED, "gemm: K=%u must be a multiple of %u for this weight type", a.K,
+                    a.wk == WT_Q8 ? 1024u : (uint32_t)GK);
+    if (a.xf32 ? (!a.xf || (a.ldx % 4u)) : (!a.xh || !a.xl || (a.ldx % 8u)))
+        return fail(VX_ERR_INVALID_ARG, "gemm: input rows must be 16-byte aligned");
+    uint32_t tiles = 0;
+    if (a.epi == GEPI_SWIGLU) {
+        if (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows)
+            return fail(VX_ERR_INVALID_ARG, "gemm swiglu: needs gate and up of equal rows");
+        tiles = (a.seg[0].rows + 63u) / 64u;
+        if (a.ksplit != 1) return fail(VX_ERR_INVALID_ARG, "gemm swiglu: no split-K");
+        if (a.oh && (!a.ol || !a.ldp)) return fail(VX_ERR_INVALID_ARG, "gemm swiglu: plane output incomplete");
+    } else {
+        for (uint32_t i = 0; i < a.nseg; ++i) {
+            a.seg[i].tile0 = tiles;
+            tiles += (a.seg[i].rows + GN - 1u) / GN;
+            if (!a.seg[i].out) return fail(VX_ERR_INVALID_ARG, "gemm: segment %u has no output", i);
+        }
+    }
+    for (uint32_t i = 0; i < a.nseg; ++i) {
+        const GemmSeg &g = a.seg[i];
+        if (a.wk == WT_Q8 ? (!g.qs || !g.d) : !g.w)
+            return fail(VX_ERR_INVALID_ARG, "gemm: segment %u weight pointers missing", i);
+    }
+    const uint32_t stages = a.K / GK;
+    if (a.ksplit == 0) a.ksplit = 1;
+    if (a.ksplit > stages) a.ksplit = stages;
+    a.ntn = tiles;
+    a.ntm = (a.T + GM - 1u) / GM;
+    const uint64_t total = (uint64_t)a.ntn * a.ntm * a.ksplit;
+    if (total == 0) return VX_OK;
+    const uint64_t grid = (total + 7u) / 8u * 8u;
+    if (grid > 0x7fffffffull) return fail(VX_ERR_UNSUPPORTED, "gemm: grid too large");
+    const dim3 g((unsigned)grid), blk(256);
+#define VX_GEMM_CASE(WKV, XF, EP)                                                                  \
+    if (a.wk == WKV && a.xf32 == XF && a.epi == EP) {                                              \
+        k_gemm<WKV, XF, EP><<<g, blk, 0, s>>>(a);                                                   \
+        VX_LAUNCHED("k_gemm");                                                                      \
+        return VX_OK;                                                                               \
+    }
+    VX_GEMM_CASE(WT_Q8, false, GEPI_STORE)
+    VX_GEMM_CASE(WT_Q8, false, GEPI_RESIDUAL)
+    VX_GEMM_CASE(WT_Q8, false, GEPI_SWIGLU)
+    VX_GEMM_CASE(WT_Q8, true, GEPI_STORE)
+    VX_GEMM_CASE(WT_Q8, true, GEPI_SWIGLU)
+    VX_GEMM_CASE(WT_F16, false, GEPI_STORE)
+    VX_GEMM_CASE(WT_F16, false, GEPI_RESIDUAL)
+    VX_GEMM_CASE(WT_F16, false, GEPI_SWIGLU)
+    VX_GEMM_CASE(WT_F16, true, GEPI_STORE)
+    VX_GEMM_CASE(WT_F16, true, GEPI_SWIGLU)
+#undef VX_GEMM_CASE
+    return fail(VX_ERR_UNSUPPORTED, "gemm: no kernel for weight type %u, f32 input %d, epilogue %u", a.wk,
+                (int)a.xf32, a.epi);
+}
+
+int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens) {
+    if (tokens == 0) return VX_OK;
+    if (a.yh && !a.yl) return fail(VX_ERR_INVALID_ARG, "seq rmsnorm: plane output incomplete");
+    k_seq_rmsnorm<<<tokens, 256, 0, s>>>(a);
+    VX_LAUNCHED("k_seq_rmsnorm");
+    return VX_OK;
+}
+
+int launch_seq_rope_store(hipStream_t s, const SeqRopeArgs &a, uint32_t tokens) {
+    if (tokens == 0) return VX_OK;
+    if (a.head_dim == 0 || a.head_dim > 128u || (a.head_dim & 1u))
+        return fail(VX_ERR_UNSUPPORTED, "seq rope: head_dim must be even and <= 128");
+    if (a.kc && (!a.vc || !a.v)) return fail(VX_ERR_INVALID_ARG, "seq rope: KV store needs v and both caches");
+    k_seq_rope_store<<<tokens, 256, 0, s>>>(a);
+    VX_LAUNCHED("k_seq_rope_store");
+    return VX_OK;
+}
+
+int launch_seq_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, uint32_t dtype,
+                         uint32_t cols, const uint32_t *tokens, uint32_t n, uint32_t vocab, float alpha,
+                         float *out, uint32_t ldo) {
+    if (!n || !cols) return VX_OK;
+    k_seq_embedding<<<dim3((cols + 255u) / 256u, n), 256, 0, s>>>(raw, weight_offset, dtype, cols, tokens, vocab,
+                                                                  alpha, out, ldo);
+    VX_LAUNCHED("k_seq_embedding");
+    return VX_OK;
+}
+
+int launch_seq_linear_generic(hipStream_t s, const SeqGenericArgs &a) {
+    const uint64_t waves = (uint64_t)a.rows * a.tokens;
+    if (!waves) return VX_OK;
+    if (waves > 0xffffffffull) return fail(VX_ERR_UNSUPPORTED, "seq linear: too many rows x tokens");
+    k_seq_linear_generic<<<(unsigned)((waves + 3u) / 4u), 256, 0, s>>>(a);
+    VX_LAUNCHED("k_seq_linear_generic");
+    return VX_OK;
+}
+
+int launch_silu_mul(hipStream_t s, float *g, const float *u, uint32_t n) {
+    if (!n) return VX_OK;
+    k_silu_mul<<<(n + 255u) / 256u, 256, 0, s>>>(g, u, n);
+    VX_LAUNCHED("k_silu_mul");
+    return VX_OK;
+}
+
+int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which) {
+    if (!a.tokens || !a.q_heads) return VX_OK;
+    if (!a.kv_heads || a.q_heads % a.kv_heads) return fail(VX_ERR_SHAPE, "dense attention: head counts");
+    if (which == 0) {
+        if (a.head_dim > 256u) return fail(VX_ERR_UNSUPPORTED, "dense attention: head_dim > 256");
+        k_dense_scores<<<dim3(a.tokens, a.q_heads), 64, 0, s>>>(a);
+        VX_LAUNCHED("k_dense_scores");
+    } else if (which == 1) {
+        k_dense_softmax<<<dim3(a.q_heads, a.tokens), 64, 0, s>>>(a.s, a.tokens, a.q_heads, a.score_stride);
+        VX_LAUNCHED("k_dense_softmax");
+    } else {
+        if (a.head_dim > 256u) return fail(VX_ERR_UNSUPPORTED, "dense attention: head_dim > 256");
+        k_dense_values<<<dim3(a.q_heads, a.tokens), 256, 0, s>>>(a);
+        VX_LAUNCHED("k_dense_values");
+    }
+    return VX_OK;
+}
+
+int launch_prefill_attn(hipStream_t s, const PrefillAttnArgs &a) {
+    if (a.T == 0) return VX_OK;
+    if (a.kv_heads == 0 || a.q_heads % a.kv_heads) return fail(VX_ERR_SHAPE, "prefill attention: head counts");
+    const uint32_t qpk = a.q_heads / a.kv_heads;
+    if ((uint64_t)a.pos_base + a.T > a.context)
+        return fail(VX_ERR_CONTEXT_FULL, "prefill attention: positions beyond the context");
+    if (a.oh && !a.ol) return fail(VX_ERR_INVALID_ARG, "prefill attention: plane output incomplete");
+    if (a.ldq % 8u || a.ldo % 4u) return fail(VX_ERR_INVALID_ARG, "prefill attention: row strides");
+#define VX_ATTN_CASE(HDV, QPKV)                                                                  \
+    if (a.head_dim == HDV && qpk == QPKV) {                                                      \
+        dim3 g((a.T + (32u / QPKV) - 1u) / (32u / QPKV), a.kv_heads);                            \
+        k_prefill_attn<HDV, QPKV><<<g, 256, 0, s>>>(a);                                          \
+        VX_LAUNCHED("k_prefill_attn");                                                           \
+        return VX_OK;                                                                            \
+    }
+    VX_ATTN_CASE(128, 8)
+    VX_ATTN_CASE(128, 4)
+    VX_ATTN_CASE(128, 2)
+    VX_ATTN_CASE(128, 1)
+    VX_ATTN_CASE(64, 8)
+    VX_ATTN_CASE(64, 4)
+    VX_ATTN_CASE(64, 2)
+    VX_ATTN_CASE(64, 1)
+#undef VX_ATTN_CASE
+    return fail(VX_ERR_UNSUPPORTED, "prefill attention: head_dim %u with %u query heads per KV head", a.head_dim,
+                qpk);
+}
+
+}  // namespace vx

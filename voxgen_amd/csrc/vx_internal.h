@@ -269,6 +269,114 @@ int launch_set_step(hipStream_t s, uint32_t *tokens, uint32_t *position, uint32_
                     uint32_t token, int write_token);
 int launch_fill_u32(hipStream_t s, uint32_t *dst, uint32_t value, uint64_t count);
 int launch_dequant(hipStream_t s, const WRef &w, uint32_t rows, uint32_t cols, float *out);
+
+// ------------------------------------------------- token-batched (seq) kernels
+// Projection GEMM C[t][n] = sum_k X[t][k] W[n][k] on MFMA (kernels_seq.hip).
+enum GemmEpilogue : uint32_t {
+    GEPI_STORE = 0,     // out[t][n] = alpha * (acc + bias[n])   (atomic add when split)
+    GEPI_RESIDUAL = 1,  // out[t][n] += scale * acc               (atomic add when split)
+    GEPI_SWIGLU = 2     // seg 0 = gate, seg 1 = up: silu(g) * u -> seg[0].out and/or planes
+};
+struct GemmSeg {                    // one weight matrix covering part of N
+    const int8_t *qs = nullptr;     // Q8_0: repacked quants (WRef::ptr) ...
+    const __half *d = nullptr;      // ... and scales (WRef::d)
+    const __half *w = nullptr;      // F16: [rows][K]
+    uint32_t rows = 0;
+    uint32_t tile0 = 0;             // set by launch_gemm
+    float *out = nullptr;           // [T][ldo] f32
+    uint32_t ldo = 0;
+    const void *bias = nullptr;     // GEPI_STORE: f32 (bias_dtype 0) or f16 (1), nullable
+    uint32_t bias_dtype = 0;
+};
+struct GemmArgs {
+    uint32_t wk = WT_Q8;            // WT_Q8 (repacked, K % 1024 == 0) or WT_F16 (K % 128 == 0)
+    uint32_t epi = GEPI_STORE;
+    uint32_t xf32 = 0;              // 1: X is f32 (xf), split to hi/lo in the kernel
+    GemmSeg seg[3];
+    uint32_t nseg = 1;
+    uint32_t K = 0, T = 0;
+    const __half *xh = nullptr, *xl = nullptr;  // X as hi/lo f16 planes [T][ldx]
+    const float *xf = nullptr;                  // X as f32 [T][ldx]
+    uint32_t ldx = 0;
+    float alpha = 1.f, scale = 1.f;
+    __half *oh = nullptr, *ol = nullptr;        // GEPI_SWIGLU plane output [T][ldp]
+    uint32_t ldp = 0;
+    uint32_t ksplit = 1;
+    uint32_t ntn = 0, ntm = 0;                  // set by launch_gemm
+};
+int launch_gemm(hipStream_t s, const GemmArgs &a);
+
+struct SeqNormArgs {
+    float *h = nullptr;             // [T][ldh] input (and residual stream when branch is set)
+    uint32_t ldh = 0;
+    const float *branch = nullptr;  // nullable: h += scale * branch first
+    uint32_t ldb = 0;
+    float scale = 1.f;
+    const float *w = nullptr;       // f32 gains [n]
+    uint32_t n = 0;
+    float eps = 0.f;
+    float *y = nullptr;             // nullable f32 output [T][ldy]
+    uint32_t ldy = 0;
+    __half *yh = nullptr, *yl = nullptr;   // nullable hi/lo planes [T][ldp]
+    uint32_t ldp = 0;
+    float *zero[3] = {nullptr, nullptr, nullptr};   // rows of split-K accumulators to clear
+    uint32_t zero_n[3] = {0, 0, 0};
+};
+int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens);
+
+struct SeqRopeArgs {
+    float *q = nullptr, *k = nullptr;   // [T][ldq], [T][ldk]
+    const float *v = nullptr;           // [T][ldk] (KV store)
+    uint32_t ldq = 0, ldk = 0;
+    const float *factors = nullptr;
+    uint32_t pos_base = 0, q_heads = 0, kv_heads = 0, head_dim = 0;
+    float theta = 10000.f, scaling = 1.f;
+    int q_inplace = 1;                  // write roped q back to q
+    __half *qh = nullptr, *ql = nullptr;   // nullable roped q planes [T][ldqp]
+    uint32_t ldqp = 0;
+    __half *kc = nullptr, *vc = nullptr;   // nullable: store K/V rows [layer][context][kv_dim]
+    uint32_t layer = 0, context = 0;
+};
+int launch_seq_rope_store(hipStream_t s, const SeqRopeArgs &a, uint32_t tokens);
+
+struct PrefillAttnArgs {
+    const __half *qh = nullptr, *ql = nullptr;  // roped q planes [T][ldq]
+    uint32_t ldq = 0;
+    const __half *kc = nullptr, *vc = nullptr;  // f16 caches [layer][context][kv_heads*head_dim]
+    uint32_t layer = 0, context = 0, pos_base = 0, T = 0;
+    uint32_t q_heads = 0, kv_heads = 0, head_dim = 0;
+    float *out = nullptr;                       // nullable f32 [T][ldo]
+    __half *oh = nullptr, *ol = nullptr;        // nullable planes [T][ldo]
+    uint32_t ldo = 0;
+};
+int launch_prefill_attn(hipStream_t s, const PrefillAttnArgs &a);
+// seq_linear_bias.comp / seq_swiglu.comp for any shape and dtype, one wave per
+// (row, token), reading the raw GGUF region.
+struct SeqGenericArgs {
+    const uint8_t *raw = nullptr;
+    uint32_t w_off = 0, w2_off = 0, dtype = 0, rows = 0, cols = 0, tokens = 0;
+    const float *x = nullptr;
+    uint32_t in_base = 0, in_stride = 0;
+    float *y = nullptr;
+    uint32_t out_base = 0, out_stride = 0;
+    uint32_t has_bias = 0, bias_off = 0, bias_dtype = 0;
+    float alpha = 1.f;
+    int swiglu = 0;
+};
+int launch_seq_linear_generic(hipStream_t s, const SeqGenericArgs &a);
+int launch_silu_mul(hipStream_t s, float *g, const float *u, uint32_t n);
+// dense_attn_scores / dense_softmax / dense_attn_values (which = 0 / 1 / 2).
+struct DenseAttnArgs {
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    float *s = nullptr, *out = nullptr;
+    uint32_t tokens = 0, q_heads = 0, kv_heads = 0, head_dim = 0;
+    uint32_t q_stride = 0, k_stride = 0, v_stride = 0, out_stride = 0, score_stride = 0;
+};
+int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
+// Embedding rows of n device token ids into out[t][ldo] (bit-exact gather).
+int launch_seq_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, uint32_t dtype,
+                         uint32_t cols, const uint32_t *tokens, uint32_t n, uint32_t vocab, float alpha,
+                         float *out, uint32_t ldo);
 int launch_repack_q8(hipStream_t s, const uint8_t *raw_tensor, uint32_t rows, uint32_t cols,
                      int8_t *qs, __half *d);
 
