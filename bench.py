@@ -14,6 +14,10 @@ Prints one JSON line with:
                the engine stream around back-to-back launches over all 28 layers
   per_kernel   the same measurement for every kernel of the decode layer
   cpu_baseline the CPU oracle's decode throughput on a bounded sample
+  prefill      the token-batched prefill of 384 tokens through the 28 layers
+               (MFMA projections, causal attention over the cache): wall time and
+               each kernel's HIP-event span, with the projection GEMMs' algorithmic
+               TFLOP/s against the 2.5 PFLOP/s dense f16 MFMA peak
 
 `--copy-calibration` instead runs one plain copy kernel of known size (the
 reference point for the FETCH_SIZE / WRITE_SIZE counters).
@@ -82,6 +86,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target length of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference"])
+    ap.add_argument("--prefill-tokens", type=int, default=384,
+                    help="tokens of the token-batched prefill leg (0 skips it)")
+    ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the token-batched prefill leg (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one copy kernel of known size and exit (PMC calibration)")
     return ap.parse_args()
@@ -107,6 +116,68 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": nbytes}), flush=True)
 
 
+F16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def prefill_flops(T):
+    """Algorithmic FLOP of each projection GEMM of one layer at T tokens."""
+    return {"prefill.qkv": 2 * T * (H + 2 * KV) * H, "prefill.attn_out": 2 * T * H * H,
+            "prefill.swiglu": 2 * T * 2 * F * H, "prefill.down": 2 * T * H * F}
+
+
+def prefill_leg(ctx, eng, cfg, T, reps):
+    """Token-batched prefill of T tokens through the 28 layers (positions 0..T-1):
+    whole-prefill wall time around the stream, then one run with a HIP-event span
+    around every kernel for the per-kernel breakdown."""
+    toks = synth_tokens(T, cfg)
+    eng.reset()
+    eng.prefill_tokens_batched_gpu_only(toks)   # warm (allocates the workspace)
+    ctx.sync()
+    times = []
+    for _ in range(reps):
+        eng.reset()
+        ctx.sync()
+        t0 = time.perf_counter()
+        eng.prefill_tokens_batched_gpu_only(toks)
+        ctx.sync()
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    eng.reset()
+    eng.prefill_tokens_batched_gpu_only(toks)
+    ctx.sync()
+    prof = ctx.prof_snapshot()
+    ctx.prof_enable(False)
+    fl = prefill_flops(T)
+    per = {}
+    gemm_ms = gemm_fl = 0.0
+    for name, v in prof.items():
+        e = dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"], total_ms=round(v["total_ms"], 4))
+        if name in fl:
+            tf = fl[name] / (v["avg_ms"] * 1e-3) / 1e12
+            e.update(tflops=round(tf, 1), mfma_frac=round(tf / F16_MFMA_PEAK_TFLOPS, 4))
+            gemm_ms += v["total_ms"]
+            gemm_fl += fl[name] * v["calls"]
+        per[name] = e
+    gemm_tf = gemm_fl / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
+    log(f"prefill T={T}: {ms:.3f} ms ({T / ms * 1e3:.0f} tok/s); GEMMs {gemm_ms:.3f} ms at "
+        f"{gemm_tf:.1f} TFLOP/s = {gemm_tf / F16_MFMA_PEAK_TFLOPS:.3f} of f16 MFMA peak")
+    return {"workload": f"baselm_q8_0_prefill_28L_T{T}", "tokens": T, "ms": round(ms, 3),
+            "tok_s": round(T / ms * 1e3, 1),
+            "gemm": {"ms": round(gemm_ms, 3), "flop": int(gemm_fl), "achieved": round(gemm_tf, 1),
+                     "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tf / F16_MFMA_PEAK_TFLOPS, 4),
+                     "precision": "Q8_0 weights exact (int8 as f16, block scale in fp32), activations as "
+                                  "f16 hi+lo (two MFMAs per k-step), fp32 accumulation"},
+            "per_kernel": per}
+
+
+def synth_tokens(n, cfg):
+    from voxgen_amd import synth
+    return synth.uniform_u32(n, 0x5EED0013, cfg["vocab_size"]).astype(np.uint32)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -122,7 +193,7 @@ def main():
 
     abi.load()
     K, W, P = args.steps, args.warmup, args.prefill
-    active = P + max(K, W) + 1
+    active = max(P + max(K, W) + 1, args.prefill_tokens)
     cfg = synth.baselm_config(active_context=max(active, 512))
     t0 = time.perf_counter()
     m = synth.build_baselm(cfg, seed=0x5EED0002)
@@ -134,6 +205,13 @@ def main():
     eng = BaseLmEngine(ctx, model, cfg, exec_mode=args.mode, strict_geometry=True)
     log(f"device {info['name']} {info['arch']} CUs={info['compute_units']}; model on device "
         f"{model.device_bytes / 1e9:.2f} GB")
+    if args.prefill_only:
+        pf = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
+        eng.close()
+        model.free()
+        ctx.close()
+        print(json.dumps({"prefill": pf}), flush=True)
+        return
 
     def run_steps(start, toks):
         eng.set_position(start)
@@ -186,6 +264,9 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, m, eng, tokens, P, args)
+    prefill = None
+    if args.prefill_tokens:
+        prefill = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
     eng.close()
     model.free()
     ctx.close()
@@ -216,6 +297,7 @@ def main():
                  "frac": round(mean_step_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4)},
         "per_kernel": per_kernel,
         "cpu_baseline": cpu,
+        "prefill": prefill,
         "device": f"{info['name']} ({info['arch']})",
     }
     print(json.dumps(line), flush=True)

@@ -80,85 +80,108 @@ __device__ __forceinline__ uint32_t stage_col(uint32_t s, uint32_t kk) {
         return 128u * s + 32u * kk;
 }
 
-struct RowMap {
-    const int8_t *qs;
-    const __half *d;
-    const __half *w;
-    uint32_t row;
-    bool valid;
+// Per-thread global row pointers of one workgroup tile, resolved once before
+// the k-loop (segment selection stays in registers; the k-loop only adds the
+// stage offset). Rows past a matrix and tokens past T are clamped to row 0 /
+// token 0: they are loaded and multiplied like the others, and the epilogue
+// never stores their results. Loads are therefore unconditional.
+template <int WK, bool XF32>
+struct TilePtrs {
+    const uint8_t *w[WK == WT_Q8 ? 4 : 8];   // weight row starts
+    const uint8_t *d;                         // Q8 scale row start
+    const uint8_t *x[XF32 ? 8 : 4];           // input row starts (hi plane / f32)
 };
 
+// Weight row of LDS row rho of tile tn: which matrix (0: seg, 1: the up matrix
+// of a SwiGLU tile) and its row index.
 template <int EPI>
-__device__ __forceinline__ RowMap map_row(const GemmArgs &a, uint32_t tn, uint32_t seg, uint32_t rho) {
-    RowMap r;
-    uint32_t mat, row;
+__device__ __forceinline__ void tile_row(uint32_t tn, uint32_t tile0, uint32_t rho, uint32_t &mat, uint32_t &row) {
     if constexpr (EPI == GEPI_SWIGLU) {
         mat = (rho >> 5) & 1u;
         row = 64u * tn + 32u * (rho >> 6) + (rho & 31u);
     } else {
-        mat = seg;
-        row = (tn - a.seg[seg].tile0) * GN + rho;
+        mat = 0;
+        row = (tn - tile0) * GN + rho;
     }
-    const GemmSeg &s = a.seg[mat];
-    r.valid = row < s.rows;
-    r.row = row;
-    r.qs = s.qs;
-    r.d = s.d;
-    r.w = s.w;
-    return r;
+}
+
+template <int WK, bool XF32, int EPI>
+__device__ __forceinline__ void tile_ptrs(const GemmSeg &s0, const GemmSeg &s1, const GemmArgs &a, uint32_t tn,
+                                          uint32_t m0, TilePtrs<WK, XF32> &p) {
+    const uint32_t tid = threadIdx.x;
+    const size_t K = a.K;
+    constexpr int NW = WK == WT_Q8 ? 4 : 8;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const uint32_t c = tid + 256u * i, rho = WK == WT_Q8 ? c >> 3 : c >> 4;
+        uint32_t mat, row;
+        tile_row<EPI>(tn, s0.tile0, rho, mat, row);
+        const uint32_t rows = mat ? s1.rows : s0.rows;
+        if (row >= rows) row = 0;
+        const uint8_t *base = WK == WT_Q8 ? reinterpret_cast<const uint8_t *>(mat ? s1.qs : s0.qs)
+                                          : reinterpret_cast<const uint8_t *>(mat ? s1.w : s0.w);
+        p.w[i] = base + (size_t)row * K * (WK == WT_Q8 ? 1u : 2u);
+    }
+    if constexpr (WK == WT_Q8) {
+        uint32_t mat, row;
+        tile_row<EPI>(tn, s0.tile0, tid & (GN - 1u), mat, row);
+        const uint32_t rows = mat ? s1.rows : s0.rows;
+        if (row >= rows) row = 0;
+        const uint8_t *base = reinterpret_cast<const uint8_t *>(mat ? s1.d : s0.d);
+        p.d = base + (size_t)row * (K / 32u) * 2u;
+    } else {
+        p.d = nullptr;
+    }
+    constexpr int NX = XF32 ? 8 : 4;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const uint32_t c = tid + 256u * i, t = XF32 ? c >> 5 : c >> 4;
+        uint32_t tok = m0 + t;
+        if (tok >= a.T) tok = 0;
+        const uint8_t *base = XF32 ? reinterpret_cast<const uint8_t *>(a.xf) : reinterpret_cast<const uint8_t *>(a.xh);
+        p.x[i] = base + (size_t)tok * a.ldx * (XF32 ? 4u : 2u);
+    }
 }
 
 template <int WK, bool XF32>
 struct StageRegs {
     uint4 w[WK == WT_Q8 ? 4 : 8];
     uint2 d;
-    uint4 x[XF32 ? 8 : 8];   // planes: 4 hi + 4 lo chunks; f32: 8 float4 chunks
+    uint4 x[8];   // planes: 4 hi + 4 lo chunks; f32: 8 float4 chunks
 };
 
-template <int WK, bool XF32, int EPI>
-__device__ __forceinline__ void load_stage(const GemmArgs &a, uint32_t tn, uint32_t seg, uint32_t m0, uint32_t s,
+template <int WK, bool XF32>
+__device__ __forceinline__ void load_stage(const TilePtrs<WK, XF32> &p, ptrdiff_t lo_delta, uint32_t s,
                                            StageRegs<WK, XF32> &r) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t K = a.K;
     if constexpr (WK == WT_Q8) {
+        const uint32_t so = 1024u * (s >> 3) + 128u * (s & 7u);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t c = tid + 256u * i, rho = c >> 3, p = c & 7u;
-            const RowMap m = map_row<EPI>(a, tn, seg, rho);
-            const size_t off = (size_t)m.row * K + 1024u * (s >> 3) + 128u * (s & 7u) + 16u * p;
-            r.w[i] = m.valid ? *reinterpret_cast<const uint4 *>(m.qs + off) : make_uint4(0, 0, 0, 0);
+            const uint32_t pp = (tid + 256u * i) & 7u;
+            r.w[i] = *reinterpret_cast<const uint4 *>(p.w[i] + so + 16u * pp);
         }
-        if (tid < (uint32_t)GN) {
-            const RowMap m = map_row<EPI>(a, tn, seg, tid);
-            const size_t off = (size_t)m.row * (K / 32u) + 32u * (s >> 3) + 4u * (s & 7u);
-            r.d = m.valid ? *reinterpret_cast<const uint2 *>(m.d + off) : make_uint2(0, 0);
-        }
+        r.d = *reinterpret_cast<const uint2 *>(p.d + 2u * (32u * (s >> 3) + 4u * (s & 7u)));
     } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t c = tid + 256u * i, rho = c >> 4, p = c & 15u;
-            const RowMap m = map_row<EPI>(a, tn, seg, rho);
-            const size_t off = (size_t)m.row * K + 128u * s + 8u * p;
-            r.w[i] = m.valid ? *reinterpret_cast<const uint4 *>(m.w + off) : make_uint4(0, 0, 0, 0);
+            const uint32_t pp = (tid + 256u * i) & 15u;
+            r.w[i] = *reinterpret_cast<const uint4 *>(p.w[i] + 2u * (128u * s + 8u * pp));
         }
     }
     if constexpr (XF32) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t c = tid + 256u * i, t = c >> 5, kk = (c >> 3) & 3u, q = c & 7u;
-            const uint32_t tok = m0 + t;
-            const size_t off = (size_t)tok * a.ldx + stage_col<WK>(s, kk) + 4u * q;
-            r.x[i] = tok < a.T ? *reinterpret_cast<const uint4 *>(a.xf + off) : make_uint4(0, 0, 0, 0);
+            const uint32_t c = tid + 256u * i, kk = (c >> 3) & 3u, q = c & 7u;
+            r.x[i] = *reinterpret_cast<const uint4 *>(p.x[i] + 4u * (stage_col<WK>(s, kk) + 4u * q));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t c = tid + 256u * i, t = c >> 4, kk = (c >> 2) & 3u, q = c & 3u;
-            const uint32_t tok = m0 + t;
-            const size_t off = (size_t)tok * a.ldx + stage_col<WK>(s, kk) + 8u * q;
-            const bool ok = tok < a.T;
-            r.x[i] = ok ? *reinterpret_cast<const uint4 *>(a.xh + off) : make_uint4(0, 0, 0, 0);
-            r.x[4 + i] = ok ? *reinterpret_cast<const uint4 *>(a.xl + off) : make_uint4(0, 0, 0, 0);
+            const uint32_t c = tid + 256u * i, kk = (c >> 2) & 3u, q = c & 3u;
+            const uint8_t *src = p.x[i] + 2u * (stage_col<WK>(s, kk) + 8u * q);
+            r.x[i] = *reinterpret_cast<const uint4 *>(src);
+            r.x[4 + i] = *reinterpret_cast<const uint4 *>(src + lo_delta);
         }
     }
 }
@@ -236,9 +259,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wv & 1u, wn = wv >> 1;
 
+    const GemmSeg &sg0 = a.seg[seg];
+    const GemmSeg &sg1 = a.seg[EPI == GEPI_SWIGLU ? 1u : seg];
+    TilePtrs<WK, XF32> tp;
+    tile_ptrs<WK, XF32, EPI>(sg0, sg1, a, tn, m0, tp);
+    const ptrdiff_t lo_delta = XF32 ? 0 : reinterpret_cast<const uint8_t *>(a.xl) - reinterpret_cast<const uint8_t *>(a.xh);
+
     acc16 acc0 = {}, acc1 = {};
     StageRegs<WK, XF32> st;
-    if (s0 < s1) load_stage<WK, XF32, EPI>(a, tn, seg, m0, s0, st);
+    if (s0 < s1) load_stage<WK, XF32>(tp, lo_delta, s0, st);
     const _Float16 *xa = Xh + (32u * wm + l32) * LROW + 8u * hs;
     const _Float16 *xb = Xl + (32u * wm + l32) * LROW + 8u * hs;
     const _Float16 *wa = Wl + (64u * wn + l32) * LROW + 8u * hs;
@@ -247,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         __syncthreads();
         store_stage<WK, XF32>(st, Wl, Xh, Xl, Ds);
         __syncthreads();
-        if (s + 1 < s1) load_stage<WK, XF32, EPI>(a, tn, seg, m0, s + 1, st);
+        if (s + 1 < s1) load_stage<WK, XF32>(tp, lo_delta, s + 1, st);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             if constexpr (WK == WT_Q8) {
@@ -292,9 +321,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     // tokens m0 + 32wm + 8(r/4) + 4hs + r%4 (r < 16) of each tile.
     const uint32_t tbase = m0 + 32u * wm + 4u * hs;
     if constexpr (EPI == GEPI_SWIGLU) {
-        const RowMap mg = map_row<EPI>(a, tn, 0, 64u * wn + l32);
-        if (!mg.valid) return;
-        const uint32_t row = mg.row;
+        uint32_t mat, row;
+        tile_row<EPI>(tn, 0, 64u * wn + l32, mat, row);
+        if (row >= sg0.rows) return;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t tok = tbase + 8u * (r >> 2) + (r & 3);
@@ -308,12 +337,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
             }
         }
     } else {
-        const GemmSeg &sg = a.seg[seg];
+        const GemmSeg &sg = sg0;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const RowMap mr = map_row<EPI>(a, tn, seg, 64u * wn + 32u * t + l32);
-            if (!mr.valid) continue;
-            const uint32_t row = mr.row;
+            uint32_t mat, row;
+            tile_row<EPI>(tn, sg.tile0, 64u * wn + 32u * t + l32, mat, row);
+            if (row >= sg.rows) continue;
             float bias = 0.f;
             if (EPI == GEPI_STORE && sg.bias && ks == 0)
                 bias = sg.bias_dtype == 0 ? static_cast<const float *>(sg.bias)[row]
