@@ -69,6 +69,7 @@ typedef struct vx_model vx_model;
 typedef struct vx_graph vx_graph;
 typedef struct vx_baselm vx_baselm;
 typedef struct vx_gguf vx_gguf;
+typedef struct vx_locdit vx_locdit;
 
 /* ------------------------------------------------------------------------- */
 /* Push structs: identical layout to the reference's #[repr(C)] structs.      */
@@ -176,6 +177,27 @@ typedef struct vx_dense_softmax_push { /* DenseSoftmaxPush local.rs:197-198 */
 typedef struct vx_dense_values_push { /* DenseValuesPush local.rs:199-200 */
     uint32_t tokens, q_heads, kv_heads, head_dim, out_stride, v_stride, score_stride;
 } vx_dense_values_push;
+
+/* CFM / LocDiT push structs, identical to local.rs:201-212. */
+typedef struct vx_cfm_noise_push {     /* CfmNoisePush local.rs:209-210 */
+    uint32_t n, seed_lo, seed_hi;
+    float temperature;
+} vx_cfm_noise_push;
+
+typedef struct vx_cfm_euler_push {     /* CfmEulerPush local.rs:211-212 */
+    uint32_t n;
+    float dt, cfg;
+    uint32_t use_zero_star;
+} vx_cfm_euler_push;
+
+typedef struct vx_time_push {          /* TimePush local.rs:207-208 */
+    uint32_t dim;
+    float t;
+} vx_time_push;
+
+typedef struct vx_pack_locdit_push {   /* PackLocDitPush local.rs:205-206 */
+    uint32_t hidden, patch_tokens, zero_mu;
+} vx_pack_locdit_push;
 
 /* ------------------------------------------------------------------------- */
 /* Context, buffers, streams (replaces VulkanContext, vulkan.rs:96-113).      */
@@ -599,6 +621,72 @@ int vx_baselm_profile_steps(vx_baselm *eng, const uint32_t *tokens, uint32_t n,
 #define VX_LAYER_KERNEL_SWIGLU 3u
 #define VX_LAYER_KERNEL_DOWN 4u
 int vx_baselm_time_layer_kernel(vx_baselm *eng, uint32_t which, uint32_t reps, double *avg_ms);
+
+/* ------------------------------------------------------------------------- */
+/* CFM shader entry points (UnifiedCFM pieces, local.rs:383-430).             */
+/* ------------------------------------------------------------------------- */
+/* cfm_noise.comp:25-37: x[i] = temperature * N(0,1) from the integer hash of
+ * (i/2, seed); dispatched at local.rs:404. */
+int vx_cfm_noise(vx_ctx *ctx, vx_buf *x, const vx_cfm_noise_push *pc);
+/* cfm_cfg_euler.comp:15-36 (CFG-Zero* scale, Euler step), local.rs:423. */
+int vx_cfm_cfg_euler(vx_ctx *ctx, vx_buf *x, const vx_buf *positive, const vx_buf *negative,
+                     const vx_cfm_euler_push *pc);
+/* time_sinusoidal.comp:5, local.rs:471. */
+int vx_time_sinusoidal(vx_ctx *ctx, vx_buf *out, const vx_time_push *pc);
+/* pack_locdit.comp:10: [mu1, mu2, time, cond x patch, x x patch] rows, local.rs:465. */
+int vx_pack_locdit(vx_ctx *ctx, const vx_buf *mu1, const vx_buf *mu2, const vx_buf *time, const vx_buf *cond,
+                   const vx_buf *x, vx_buf *hidden, const vx_pack_locdit_push *pc);
+/* silu_inplace.comp:5 and add_vectors.comp:6. */
+int vx_silu_inplace(vx_ctx *ctx, vx_buf *x, uint32_t n);
+int vx_add_vectors(vx_ctx *ctx, vx_buf *a, const vx_buf *b, uint32_t n);
+
+/* ------------------------------------------------------------------------- */
+/* LocDiT estimator + UnifiedCFM solve (LocalEngine, local.rs:264-537).       */
+/* ------------------------------------------------------------------------- */
+typedef struct vx_locdit_config {   /* LocalConfig local.rs:51-70, LocDiT part */
+    uint32_t hidden, layers, q_heads, kv_heads, head_dim, ffn;
+    uint32_t feat_dim, patch;       /* latent patch: patch tokens x feat_dim (4 x 64) */
+    uint32_t n_mu;                  /* mu tokens ahead of the time token (VoxCPM2: 2) */
+    uint32_t n_cond;                /* condition tokens after the time token */
+    uint32_t cond_raw;              /* 0: condition = patch x feat_dim latent through locdit.cond_proj
+                                       (n_cond == patch, the reference); 1: n_cond x hidden rows given */
+    uint32_t uncond_zero_cond;      /* 1: the unconditional CFG pass also zeroes the condition rows
+                                       (the reference zeroes only the mu tokens) */
+    float rms_epsilon, rope_theta, rope_scaling;
+} vx_locdit_config;
+
+typedef struct vx_cfm_options {     /* CfmOptions local.rs:244-252 */
+    uint32_t n_timesteps;
+    float cfg_value, temperature, sway_sampling_coef;
+    uint64_t seed;
+    uint32_t use_cfg_zero_star;
+} vx_cfm_options;
+
+typedef struct vx_cfm_result {      /* CfmResult local.rs:253-261 (scalar part) */
+    double elapsed_ms;
+    uint32_t n_timesteps, estimator_calls, zero_init_steps;
+    double output_checksum, output_l2;
+    float output_min, output_max;
+} vx_cfm_result;
+
+/* LocalEngine::new (local.rs:276-339), LocDiT half: validates the locdit.*
+ * tensors of `model` (F16 matrices, F32 norms; validate_tensors local.rs:127-168)
+ * and allocates a CFG batch of two sequences. RoPE factors are the BaseLM's
+ * (rope_model, rope_factor_offset; local.rs:336-337). strict_geometry enforces
+ * the VoxCPM2 contract (12 x 1024, 16/2 x 128, ffn 4096, 4 x 64, two mu tokens). */
+int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_model, uint32_t rope_factor_offset,
+                     const vx_locdit_config *cfg, uint32_t strict_geometry, vx_locdit **out);
+int vx_locdit_destroy(vx_locdit *loc);
+/* locdit_from_cpu_mu (local.rs:352-355): one estimator pass on host inputs
+ * x [patch x feat_dim], cond (see cond_raw), mu [n_mu x hidden]; out [patch x feat_dim]. */
+int vx_locdit_estimate(vx_locdit *loc, const float *x, const float *cond, const float *mu, float t, float dt,
+                       float *out);
+/* cfm_from_cpu_mu (local.rs:359-363, cfm_solve 383-430): noise (or initial_x),
+ * then every Euler step's conditional and unconditional estimate as one batch
+ * of two and the CFG-Zero* update; the whole solve is one hipGraph replay.
+ * out_patch receives the final x [patch x feat_dim]. */
+int vx_locdit_cfm_solve(vx_locdit *loc, const float *cond, const float *mu, const vx_cfm_options *opt,
+                        const float *initial_x, float *out_patch, vx_cfm_result *res);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,19 @@
  *                                  the closed forms above (not this file's code).
  *   vr_rope_scaling_factor,         reference unit tests baselm.rs:1319-1358 and
  *   vr_effective_scale              closed forms.
+ *   vr_mix32                        the published inverse of this finaliser
+ *                                  (lowbias32 family) undoes it on 10^5
+ *                                  values; mix32(0) = 0.
+ *   vr_cfm_noise                    the hash words bit-exact against vr_mix32;
+ *                                  Box-Muller pairs against f64 numpy; the
+ *                                  sample mean/variance of 2^16 draws.
+ *   vr_cfm_cfg_euler                f64 numpy closed form of the CFG-Zero*
+ *                                  update; zero_star off = plain CFG; cfg = 1
+ *                                  reduces to the positive estimate.
+ *   vr_time_sinusoidal              f64 numpy closed form; t = 0 gives 0 / 1.
+ *   vr_pack_locdit                  numpy concatenation; zero_mu rows are 0.
+ *   vr_cfm_time_span                closed form; endpoints 1 and 0; sway = 0
+ *                                  gives the linear grid; descending check.
  * Parity unpinned at the bit level (inside the float tolerances): the
  * driver's rounding of exp/sin/cos/pow/inversesqrt and FMA contraction.
  */
@@ -516,6 +529,99 @@ void vr_baselm_decode_token(const uint8_t *blob, const vr_baselm *m, vr_state *s
                             vr_effective_scale(m->cfg.embedding_scale)};
     vr_embedding(blob, s->hidden, &ep); /* baselm.rs:634-647 */
     vr_baselm_record(blob, m, s, position, compute_logits);
+}
+
+/* ------------------------------------------------------------- CFM pieces */
+/* cfm_noise.comp:11-18: integer finaliser. */
+uint32_t vr_mix32(uint32_t v) {
+    v ^= v >> 16;
+    v *= 0x7feb352du;
+    v ^= v >> 15;
+    v *= 0x846ca68bu;
+    v ^= v >> 16;
+    return v;
+}
+
+/* cfm_noise.comp:25-37, one invocation per element i < n. */
+void vr_cfm_noise(float *x, const vx_cfm_noise_push *pc) {
+    for (uint32_t i = 0; i < pc->n; ++i) {
+        uint32_t pair = i >> 1;
+        uint32_t a = vr_mix32(pair ^ pc->seed_lo ^ 0x9e3779b9u);
+        uint32_t b = vr_mix32(pair ^ pc->seed_hi ^ 0x85ebca6bu);
+        float u1 = ((float)a + 0.5f) * (1.0f / 4294967296.0f);
+        if (u1 < 1.0e-7f) u1 = 1.0e-7f;
+        float u2 = ((float)b + 0.5f) * (1.0f / 4294967296.0f);
+        float r = sqrtf(-2.0f * logf(u1));
+        float theta = 6.28318530717958647692f * u2;
+        float z = (i & 1u) == 0u ? r * cosf(theta) : r * sinf(theta);
+        x[i] = z * pc->temperature;
+    }
+}
+
+/* cfm_cfg_euler.comp:15-36: 256-lane tree reduction of <p,n> and |n|^2, then
+ * x -= dt * (n*s + cfg*(p - n*s)) with s the CFG-Zero* scale (or 1). */
+void vr_cfm_cfg_euler(float *x, const float *pos, const float *neg, const vx_cfm_euler_push *pc) {
+    float dot[256], nrm[256];
+    for (uint32_t i = 0; i < 256u; ++i) {
+        float p = 0.0f, n = 0.0f;
+        for (uint32_t j = i; j < pc->n; j += 256u) { /* the shader's one element per lane, strided for n > 256 */
+            p += pos[j] * neg[j];
+            n += neg[j] * neg[j];
+        }
+        dot[i] = p;
+        nrm[i] = n;
+    }
+    for (uint32_t stride = 128u; stride > 0u; stride >>= 1u)
+        for (uint32_t i = 0; i < stride; ++i) {
+            dot[i] += dot[i + stride];
+            nrm[i] += nrm[i + stride];
+        }
+    float scale = pc->use_zero_star ? dot[0] / (nrm[0] + 1.0e-8f) : 1.0f;
+    for (uint32_t i = 0; i < pc->n; ++i) {
+        float g = neg[i] * scale + pc->cfg * (pos[i] - neg[i] * scale);
+        x[i] -= pc->dt * g;
+    }
+}
+
+/* time_sinusoidal.comp:5. */
+void vr_time_sinusoidal(float *out, const vx_time_push *pc) {
+    uint32_t half = pc->dim / 2u;
+    float denom = (float)(half > 1u ? half - 1u : 1u);
+    for (uint32_t i = 0; i < pc->dim; ++i) {
+        uint32_t j = i % half;
+        float freq = expf((float)j * (-logf(10000.0f) / denom));
+        float a = 1000.0f * pc->t * freq;
+        out[i] = i < half ? sinf(a) : cosf(a);
+    }
+}
+
+/* pack_locdit.comp:10: rows [mu1, mu2, time, cond x P, x x P]. */
+void vr_pack_locdit(const float *mu1, const float *mu2, const float *time, const float *cond, const float *x,
+                    float *hidden, const vx_pack_locdit_push *pc) {
+    uint32_t H = pc->hidden, P = pc->patch_tokens;
+    for (uint32_t i = 0; i < (3u + 2u * P) * H; ++i) {
+        uint32_t tok = i / H, d = i % H;
+        float v;
+        if (tok == 0u) v = pc->zero_mu ? 0.0f : mu1[d];
+        else if (tok == 1u) v = pc->zero_mu ? 0.0f : mu2[d];
+        else if (tok == 2u) v = time[d];
+        else if (tok < 3u + P) v = cond[(tok - 3u) * H + d];
+        else v = x[(tok - 3u - P) * H + d];
+        hidden[i] = v;
+    }
+}
+
+/* cfm_time_span (local.rs:531-537); returns 0 or -1 when the schedule is not
+ * descending (the reference's bail). out holds n + 1 values. */
+int vr_cfm_time_span(uint32_t n, float sway, float *out) {
+    if (n == 0u) return -1;
+    for (uint32_t i = 0; i <= n; ++i) {
+        float t = 1.0f - (float)i / (float)n;
+        out[i] = t + sway * (cosf(1.57079632679489661923f * t) - 1.0f + t);
+    }
+    for (uint32_t i = 1; i <= n; ++i)
+        if (out[i] > out[i - 1] + 1.0e-6f) return -1;
+    return 0;
 }
 
 void vr_set_threads(int n) {

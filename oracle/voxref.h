@@ -88,6 +88,15 @@ float vr_rope_scaling_factor(const vx_baselm_config *cfg);
 /* effective_scale (baselm.rs:1262-1264). */
 float vr_effective_scale(float v);
 
+/* CFM pieces of the LocDiT solve (local.rs:383-430). */
+uint32_t vr_mix32(uint32_t v);
+void vr_cfm_noise(float *x, const vx_cfm_noise_push *pc);
+void vr_cfm_cfg_euler(float *x, const float *pos, const float *neg, const vx_cfm_euler_push *pc);
+void vr_time_sinusoidal(float *out, const vx_time_push *pc);
+void vr_pack_locdit(const float *mu1, const float *mu2, const float *time, const float *cond, const float *x,
+                    float *hidden, const vx_pack_locdit_push *pc);
+int vr_cfm_time_span(uint32_t n, float sway, float *out);
+
 /* Threads used by the OpenMP loops (0 = runtime default). */
 void vr_set_threads(int n);
 int vr_get_threads(void);

@@ -59,6 +59,14 @@ def lib() -> C.CDLL:
         L.vr_rope_scaling_factor.argtypes = [P(abi.BaseLmConfig)]
         L.vr_effective_scale.restype = f32
         L.vr_effective_scale.argtypes = [f32]
+        L.vr_mix32.restype = u32
+        L.vr_mix32.argtypes = [u32]
+        L.vr_cfm_noise.argtypes = [vp, P(abi.CfmNoisePush)]
+        L.vr_cfm_cfg_euler.argtypes = [vp, vp, vp, P(abi.CfmEulerPush)]
+        L.vr_time_sinusoidal.argtypes = [vp, P(abi.TimePush)]
+        L.vr_pack_locdit.argtypes = [vp, vp, vp, vp, vp, vp, P(abi.PackLocDitPush)]
+        L.vr_cfm_time_span.restype = C.c_int
+        L.vr_cfm_time_span.argtypes = [u32, f32, vp]
         L.vr_set_threads.argtypes = [C.c_int]
         L.vr_get_threads.restype = C.c_int
         _lib = L
@@ -110,34 +118,39 @@ def embedding(blob, push: abi.EmbeddingPush) -> np.ndarray:
 
 def rmsnorm(blob, x, push: abi.RmsPush) -> np.ndarray:
     y = f32(push.n)
-    lib().vr_rmsnorm(_p(blob), _p(np.ascontiguousarray(x, np.float32)), _p(y), C.byref(push))
+    x_c = np.ascontiguousarray(x, np.float32)  # held across the call
+    lib().vr_rmsnorm(_p(blob), _p(x_c), _p(y), C.byref(push))
     return y
 
 
 def residual_rmsnorm(blob, hidden, branch, push: abi.ResidualRmsPush):
     h = np.array(hidden, np.float32, copy=True)
     y = f32(push.n)
-    lib().vr_residual_rmsnorm(_p(blob), _p(h), _p(np.ascontiguousarray(branch, np.float32)), _p(y),
+    branch_c = np.ascontiguousarray(branch, np.float32)  # held across the call
+    lib().vr_residual_rmsnorm(_p(blob), _p(h), _p(branch_c), _p(y),
                               C.byref(push))
     return h, y
 
 
 def matvec(blob, x, push: abi.MatvecPush, y=None) -> np.ndarray:
     y = f32(push.rows) if y is None else y
-    lib().vr_matvec(_p(blob), _p(np.ascontiguousarray(x, np.float32)), _p(y), C.byref(push))
+    x_c = np.ascontiguousarray(x, np.float32)  # held across the call
+    lib().vr_matvec(_p(blob), _p(x_c), _p(y), C.byref(push))
     return y
 
 
 def qkv_matvec(blob, x, push: abi.QkvPush):
     q, k, v = f32(push.q_rows), f32(push.kv_rows), f32(push.kv_rows)
-    lib().vr_qkv_matvec(_p(blob), _p(np.ascontiguousarray(x, np.float32)), _p(q), _p(k), _p(v),
+    x_c = np.ascontiguousarray(x, np.float32)  # held across the call
+    lib().vr_qkv_matvec(_p(blob), _p(x_c), _p(q), _p(k), _p(v),
                         C.byref(push))
     return q, k, v
 
 
 def matvec_swiglu(blob, x, push: abi.SwigluPush) -> np.ndarray:
     y = f32(push.rows)
-    lib().vr_matvec_swiglu(_p(blob), _p(np.ascontiguousarray(x, np.float32)), _p(y), C.byref(push))
+    x_c = np.ascontiguousarray(x, np.float32)  # held across the call
+    lib().vr_matvec_swiglu(_p(blob), _p(x_c), _p(y), C.byref(push))
     return y
 
 
@@ -150,13 +163,16 @@ def rope(blob, q, k, push: abi.RopePush):
 
 def store_kv(k, v, k_cache: np.ndarray, v_cache: np.ndarray, push: abi.StoreKvPush) -> None:
     """k_cache/v_cache: uint16 (f16 bits) arrays updated in place."""
-    lib().vr_store_kv(_p(np.ascontiguousarray(k, np.float32)), _p(np.ascontiguousarray(v, np.float32)),
+    k_c = np.ascontiguousarray(k, np.float32)  # held across the call
+    v_c = np.ascontiguousarray(v, np.float32)  # held across the call
+    lib().vr_store_kv(_p(k_c), _p(v_c),
                       _p(k_cache), _p(v_cache), C.byref(push))
 
 
 def attn_scores(q, k_cache, q_heads: int, push: abi.AttentionPush) -> np.ndarray:
     s = f32(q_heads * push.context)
-    lib().vr_attn_scores(_p(np.ascontiguousarray(q, np.float32)), _p(k_cache), _p(s), q_heads, C.byref(push))
+    q_c = np.ascontiguousarray(q, np.float32)  # held across the call
+    lib().vr_attn_scores(_p(q_c), _p(k_cache), _p(s), q_heads, C.byref(push))
     return s
 
 
@@ -168,21 +184,24 @@ def softmax(scores, heads: int, push: abi.SoftmaxPush) -> np.ndarray:
 
 def attn_values(scores, v_cache, q_heads: int, push: abi.AttentionPush) -> np.ndarray:
     o = f32(q_heads * push.head_dim)
-    lib().vr_attn_values(_p(np.ascontiguousarray(scores, np.float32)), _p(v_cache), _p(o), q_heads,
+    scores_c = np.ascontiguousarray(scores, np.float32)  # held across the call
+    lib().vr_attn_values(_p(scores_c), _p(v_cache), _p(o), q_heads,
                          C.byref(push))
     return o
 
 
 def linear_bias(blob, x, push: abi.LinearBiasPush) -> np.ndarray:
     y = f32(push.rows)
-    lib().vr_linear_bias(_p(blob), _p(np.ascontiguousarray(x, np.float32)), _p(y), C.byref(push))
+    x_c = np.ascontiguousarray(x, np.float32)  # held across the call
+    lib().vr_linear_bias(_p(blob), _p(x_c), _p(y), C.byref(push))
     return y
 
 
 def fusion_linear(blob, left, right, push: abi.FusionPush):
     y, s = f32(push.rows), f32(push.rows)
     r = np.ascontiguousarray(right if right is not None else np.zeros(1), np.float32)
-    lib().vr_fusion_linear(_p(blob), _p(np.ascontiguousarray(left, np.float32)), _p(r), _p(y), _p(s),
+    left_c = np.ascontiguousarray(left, np.float32)  # held across the call
+    lib().vr_fusion_linear(_p(blob), _p(left_c), _p(r), _p(y), _p(s),
                            C.byref(push))
     return y, s
 
@@ -270,3 +289,184 @@ class BaseLm:
         lib().vr_baselm_record(_p(self.blob), C.byref(self._m), C.byref(self._s), position,
                                1 if logits else 0)
         return self.norm.copy()
+
+
+# ------------------------------------------------------------- CFM pieces
+def mix32(v: int) -> int:
+    return lib().vr_mix32(v & 0xFFFFFFFF)
+
+
+def cfm_noise(push: abi.CfmNoisePush) -> np.ndarray:
+    x = f32(push.n)
+    lib().vr_cfm_noise(_p(x), C.byref(push))
+    return x
+
+
+def cfm_cfg_euler(x, pos, neg, push: abi.CfmEulerPush) -> np.ndarray:
+    y = np.array(x, np.float32, copy=True)
+    pos_c = np.ascontiguousarray(pos, np.float32)  # held across the call
+    neg_c = np.ascontiguousarray(neg, np.float32)  # held across the call
+    lib().vr_cfm_cfg_euler(_p(y), _p(pos_c), _p(neg_c),
+                           C.byref(push))
+    return y
+
+
+def time_sinusoidal(push: abi.TimePush) -> np.ndarray:
+    y = f32(push.dim)
+    lib().vr_time_sinusoidal(_p(y), C.byref(push))
+    return y
+
+
+def pack_locdit(mu1, mu2, time, cond, x, push: abi.PackLocDitPush) -> np.ndarray:
+    h = f32((3 + 2 * push.patch_tokens) * push.hidden)
+    a = [np.ascontiguousarray(v, np.float32) for v in (mu1, mu2, time, cond, x)]
+    lib().vr_pack_locdit(*[_p(v) for v in a], _p(h), C.byref(push))
+    return h
+
+
+def cfm_time_span(n: int, sway: float):
+    out = f32(n + 1)
+    st = lib().vr_cfm_time_span(n, sway, _p(out))
+    return out if st == 0 else None
+
+
+class LocDit:
+    """LocDiT estimator and UnifiedCFM solve (local.rs:383-537) in float64 numpy:
+    record_locdit_common + record_locdit_body (local.rs:445-468), record_time
+    (470-480), record_transformer (482-527) with the seq_* / dense_* shader
+    semantics, and cfm_solve (383-430). The token layout, mu zeroing of the
+    unconditional pass and the condition modes follow vx_locdit_config."""
+
+    def __init__(self, data: np.ndarray, tensors: dict, cfg: dict, rope_factors=None):
+        self.blob = np.ascontiguousarray(data, dtype=np.uint8)
+        self.c = dict(cfg)
+        self.t = tensors
+        c = self.c
+        self.H, self.QD, self.KD = c["hidden"], c["q_heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
+        self.S = c["n_mu"] + 1 + c["n_cond"] + c["patch"]
+        if rope_factors is None:
+            rf = tensors["rope_factors_short.weight"]
+            rope_factors = self.blob[rf.offset:rf.offset + rf.nbytes].view(np.float32)
+        self.rope_factors = np.asarray(rope_factors, np.float64)
+        self._cache = {}
+
+    def _mat(self, name):
+        w = self._cache.get(name)
+        if w is None:
+            t = self.t[name]
+            cols, rows = t.dims[0], t.dims[1]
+            w = self._cache[name] = dequant(self.blob, t.offset, t.ggml_type, rows, cols).astype(np.float64)
+        return w
+
+    def _vec(self, name):
+        t = self.t[name]
+        n = int(np.prod(t.dims))
+        raw = self.blob[t.offset:t.offset + t.nbytes]
+        return (raw.view(np.float32) if t.ggml_type == abi.DTYPE_F32 else raw.view(np.float16)).astype(np.float64)[:n]
+
+    def _lin(self, prefix, x):
+        return x @ self._mat(prefix + ".weight").T + self._vec(prefix + ".bias")
+
+    def _rms(self, x, w):
+        return x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + self.c["rms_epsilon"]) * w
+
+    @staticmethod
+    def _silu(x):
+        return x / (1.0 + np.exp(-x))
+
+    def time_embed(self, t, dt):
+        """record_time: time_mlp(sin(t)) + delta_time_mlp(sin(dt)) (f64 sinusoid)."""
+        H = self.H
+        half = H // 2
+        j = np.arange(H) % half
+        freq = np.exp(j * (-np.log(10000.0) / max(half - 1, 1)))
+
+        def sinus(v):
+            a = 1000.0 * v * freq
+            return np.where(np.arange(H) < half, np.sin(a), np.cos(a))
+
+        tv = self._lin("locdit.time_mlp.linear_2", self._silu(self._lin("locdit.time_mlp.linear_1", sinus(t))))
+        dv = self._lin("locdit.delta_time_mlp.linear_2",
+                       self._silu(self._lin("locdit.delta_time_mlp.linear_1", sinus(dt))))
+        return tv + dv
+
+    def _rope(self, x, heads):
+        c = self.c
+        hd, half = c["head_dim"], c["head_dim"] // 2
+        S = x.shape[0]
+        pos = np.arange(S, dtype=np.float64)[:, None]
+        i = np.arange(half, dtype=np.float64)
+        ang = pos / (c["rope_theta"] ** (2.0 * i / hd) * self.rope_factors[:half])
+        cs, sn = np.cos(ang) * c["rope_scaling"], np.sin(ang) * c["rope_scaling"]
+        y = x.reshape(S, heads, hd).copy()
+        a, b = y[..., :half].copy(), y[..., half:].copy()
+        y[..., :half] = a * cs[:, None, :] - b * sn[:, None, :]
+        y[..., half:] = b * cs[:, None, :] + a * sn[:, None, :]
+        return y.reshape(S, heads * hd)
+
+    def transformer(self, h):
+        """record_transformer over one sequence h [S][H]; returns the final norm."""
+        c = self.c
+        L, hd, qh, kh = c["layers"], c["head_dim"], c["q_heads"], c["kv_heads"]
+        S = h.shape[0]
+        h = h.copy()
+        norm = self._rms(h, self._vec("locdit.blk.0.attn_norm.weight"))
+        for l in range(L):
+            p = f"locdit.blk.{l}."
+            q = self._rope(norm @ self._mat(p + "attn_q.weight").T, qh)
+            k = self._rope(norm @ self._mat(p + "attn_k.weight").T, kh)
+            v = norm @ self._mat(p + "attn_v.weight").T
+            Q = q.reshape(S, qh, hd)
+            K = k.reshape(S, kh, hd)[:, np.arange(qh) // (qh // kh), :]
+            V = v.reshape(S, kh, hd)[:, np.arange(qh) // (qh // kh), :]
+            sc = np.einsum("thd,shd->hts", Q, K) / np.sqrt(hd)
+            pr = np.exp(sc - sc.max(axis=2, keepdims=True))
+            pr /= pr.sum(axis=2, keepdims=True)
+            att = np.einsum("hts,shd->thd", pr, V).reshape(S, qh * hd)
+            h = h + att @ self._mat(p + "attn_output.weight").T
+            norm = self._rms(h, self._vec(p + "ffn_norm.weight"))
+            act = self._silu(norm @ self._mat(p + "ffn_gate.weight").T) * (norm @ self._mat(p + "ffn_up.weight").T)
+            h = h + act @ self._mat(p + "ffn_down.weight").T
+            nxt = f"locdit.blk.{l + 1}.attn_norm.weight" if l + 1 < L else "locdit.norm.weight"
+            norm = self._rms(h, self._vec(nxt))
+        return norm
+
+    def estimate(self, x, cond, mu, t, dt, zero_mu=False):
+        """One estimator pass: out [patch][feat] (flattened)."""
+        c = self.c
+        H, P, FD = self.H, c["patch"], c["feat_dim"]
+        xt = self._lin("locdit.in_proj", np.asarray(x, np.float64).reshape(P, FD))
+        if c["cond_raw"]:
+            ct = np.asarray(cond, np.float64).reshape(c["n_cond"], H)
+        else:
+            ct = self._lin("locdit.cond_proj", np.asarray(cond, np.float64).reshape(P, FD))
+        if zero_mu and c["uncond_zero_cond"]:
+            ct = np.zeros_like(ct)
+        rows = []
+        if c["n_mu"]:
+            m = np.asarray(mu, np.float64).reshape(c["n_mu"], H)
+            rows.append(np.zeros_like(m) if zero_mu else m)
+        rows += [self.time_embed(t, dt)[None, :], ct, xt]
+        norm = self.transformer(np.concatenate(rows, axis=0))
+        return self._lin("locdit.out_proj", norm[self.S - P:]).reshape(-1)
+
+    def cfm_solve(self, cond, mu, n_timesteps=10, cfg_value=2.0, temperature=1.0, sway=1.0, seed=42,
+                  zero_star=True, initial_x=None):
+        c = self.c
+        n = c["patch"] * c["feat_dim"]
+        if initial_x is None:
+            x = cfm_noise(abi.CfmNoisePush(n, seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF, temperature))
+            x = x.astype(np.float64)
+        else:
+            x = np.asarray(initial_x, np.float64).copy()
+        span = cfm_time_span(n_timesteps, sway).astype(np.float64)
+        zi = max(1, int(np.floor(len(span) * 0.04))) if zero_star else 0
+        for step in range(1, len(span)):
+            if step <= zi:
+                continue
+            t, dt = float(np.float32(span[step - 1])), float(np.float32(span[step - 1]) - np.float32(span[step]))
+            pos = self.estimate(x, cond, mu, t, 0.0)
+            neg = self.estimate(x, cond, mu, t, 0.0, zero_mu=True)
+            s = (pos @ neg) / (neg @ neg + 1e-8) if zero_star else 1.0
+            x = x - dt * (neg * s + cfg_value * (pos - neg * s))
+        return x

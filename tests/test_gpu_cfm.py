@@ -1,0 +1,162 @@
+"""LocDiT estimator, UnifiedCFM solve and the CFM shader entry points on the GPU
+against the oracle (voxref.LocDit in float64, voxref CFM functions).
+
+The solve batches each Euler step's conditional and unconditional passes into
+one sequence batch of two and replays the whole solve as one hipGraph; the
+oracle runs the reference's order (positive pass, negative pass, update).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import voxref
+from conftest import rel_l2
+from voxgen_amd import abi, synth
+from voxgen_amd.locdit import CfmOptions, LocDit
+from voxgen_amd.runtime import Model
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_of(m, cfg):
+    return voxref.LocDit(m.data, {t.name: t for t in m.tensors}, cfg)
+
+
+@pytest.fixture(scope="module")
+def ref_shape(ctx):
+    """The VoxCPM2 LocDiT layout (mu1, mu2, time, 4 condition, 4 latent tokens;
+    16/2 x 128, hidden 1024, ffn 4096) with 2 layers."""
+    cfg = synth.locdit_config(layers=2)
+    m = synth.build_locdit(cfg, seed=0x5EED0201)
+    model = Model(ctx, m.data, m.tensors)
+    yield cfg, m, model, oracle_of(m, cfg)
+    model.free()
+
+
+def inputs(cfg, seed):
+    x = synth.normal_f32(cfg["patch"] * cfg["feat_dim"], seed)
+    cond_n = cfg["n_cond"] * cfg["hidden"] if cfg["cond_raw"] else cfg["patch"] * cfg["feat_dim"]
+    cond = synth.normal_f32(cond_n, seed + 1)
+    mu = synth.normal_f32(max(cfg["n_mu"], 1) * cfg["hidden"], seed + 2)
+    return x, cond, mu
+
+
+def test_estimate_matches_oracle(ctx, ref_shape):
+    cfg, m, model, o = ref_shape
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    x, cond, mu = inputs(cfg, 0x5EED0202)
+    for t, dt in ((0.9, 0.0), (0.3, 0.05)):
+        got = loc.estimate(x, cond, mu, t, dt)
+        assert rel_l2(got, o.estimate(x, cond, mu, t, dt)) < 1e-4, (t, dt)
+    loc.close()
+
+
+@pytest.mark.parametrize("zero_star", [True, False])
+def test_cfm_solve_matches_oracle(ctx, ref_shape, zero_star):
+    cfg, m, model, o = ref_shape
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, mu = inputs(cfg, 0x5EED0203)
+    opt = CfmOptions(n_timesteps=4, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0, seed=1234,
+                     use_cfg_zero_star=zero_star)
+    got, res = loc.cfm_solve(cond, mu, opt)
+    want = o.cfm_solve(cond, mu, n_timesteps=4, cfg_value=2.0, temperature=1.0, sway=1.0, seed=1234,
+                       zero_star=zero_star)
+    assert rel_l2(got, want) < 1e-4
+    assert res["estimator_calls"] == (6 if zero_star else 8)
+    assert res["zero_init_steps"] == (1 if zero_star else 0)
+    assert abs(res["output_checksum"] - float(np.sum(got, dtype=np.float64))) < 1e-3
+    loc.close()
+
+
+def test_cfm_solve_graph_replay_seeds_and_initial_x(ctx, ref_shape):
+    cfg, m, model, o = ref_shape
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, mu = inputs(cfg, 0x5EED0204)
+    opt = CfmOptions(n_timesteps=3, seed=7)
+    a1, _ = loc.cfm_solve(cond, mu, opt)
+    b1, _ = loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=3, seed=8))   # same graph, new seed
+    a2, _ = loc.cfm_solve(cond, mu, opt)
+    assert np.array_equal(a1, a2) and not np.allclose(a1, b1)
+    assert rel_l2(b1, o.cfm_solve(cond, mu, n_timesteps=3, seed=8)) < 1e-4
+    x0 = synth.normal_f32(256, 99)
+    c1, _ = loc.cfm_solve(cond, mu, opt, initial_x=x0)
+    assert rel_l2(c1, o.cfm_solve(cond, mu, n_timesteps=3, initial_x=x0)) < 1e-4
+    loc.close()
+
+
+def test_baseline_shape_cfm_solve(ctx):
+    """The benchmark's LocDiT shape: 8 layers, 16 x 64 MHA, 32 given condition rows
+    zeroed in the unconditional pass, no mu tokens; 10 timesteps, cfg 2.0."""
+    cfg = synth.locdit_config(layers=8, q_heads=16, kv_heads=16, head_dim=64, n_mu=0, n_cond=32, cond_raw=1,
+                              uncond_zero_cond=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0205)
+    model = Model(ctx, m.data, m.tensors)
+    o = oracle_of(m, cfg)
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, _ = inputs(cfg, 0x5EED0206)
+    got, res = loc.cfm_solve(cond, None, CfmOptions(seed=42))
+    want = o.cfm_solve(cond, None, seed=42)
+    assert res["estimator_calls"] == 18
+    assert rel_l2(got, want) < 1e-4
+    loc.close()
+    model.free()
+
+
+def test_strict_geometry_and_errors(ctx, ref_shape):
+    cfg, m, model, o = ref_shape
+    with pytest.raises(abi.VxError) as e:
+        LocDit(ctx, model, cfg, strict_geometry=True)   # 2 layers != 12
+    assert e.value.name == "VX_ERR_UNSUPPORTED"
+    with pytest.raises(abi.VxError) as e:
+        LocDit(ctx, model, dict(cfg, layers=3), strict_geometry=False)
+    assert e.value.name == "VX_ERR_NOT_FOUND"
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    x, cond, mu = inputs(cfg, 5)
+    bad = cond.copy()
+    bad[3] = np.nan
+    with pytest.raises(abi.VxError) as e:
+        loc.cfm_solve(bad, mu)
+    assert e.value.name == "VX_ERR_INVALID_ARG"
+    with pytest.raises(abi.VxError) as e:
+        loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=0))
+    assert e.value.name == "VX_ERR_INVALID_ARG"
+    with pytest.raises(abi.VxError) as e:
+        loc.cfm_solve(cond, mu, CfmOptions(temperature=-1.0))
+    assert e.value.name == "VX_ERR_INVALID_ARG"
+    with pytest.raises(abi.VxError) as e:
+        loc.estimate(x, cond, mu, float("inf"), 0.0)
+    assert e.value.name == "VX_ERR_INVALID_ARG"
+    loc.close()
+
+
+def test_cfm_shader_entry_points(ctx):
+    n = 256
+    xb = ctx.zeros(n * 4)
+    push = abi.CfmNoisePush(n, 0x89ABCDEF, 0x01234567, 0.8)
+    abi.call("vx_cfm_noise", ctx.handle, xb.handle, C.byref(push))
+    assert rel_l2(xb.download(np.float32, n), voxref.cfm_noise(push)) < 1e-6
+    x, p, q = synth.normal_f32(n, 1), synth.normal_f32(n, 2), synth.normal_f32(n, 3)
+    xb2, pb, qb = ctx.array(x), ctx.array(p), ctx.array(q)
+    ep = abi.CfmEulerPush(n, 0.1, 2.0, 1)
+    abi.call("vx_cfm_cfg_euler", ctx.handle, xb2.handle, pb.handle, qb.handle, C.byref(ep))
+    assert rel_l2(xb2.download(np.float32, n), voxref.cfm_cfg_euler(x, p, q, ep)) < 1e-6
+    tb = ctx.zeros(1024 * 4)
+    tp = abi.TimePush(1024, 0.42)
+    abi.call("vx_time_sinusoidal", ctx.handle, tb.handle, C.byref(tp))
+    assert np.max(np.abs(tb.download(np.float32, 1024) - voxref.time_sinusoidal(tp))) < 1e-3
+    H, P = 1024, 4
+    parts = [synth.normal_f32(k, s) for k, s in ((H, 11), (H, 12), (H, 13), (P * H, 14), (P * H, 15))]
+    bufs = [ctx.array(v) for v in parts]
+    hb = ctx.zeros((3 + 2 * P) * H * 4)
+    for zero in (0, 1):
+        pp = abi.PackLocDitPush(H, P, zero)
+        abi.call("vx_pack_locdit", ctx.handle, *[b.handle for b in bufs], hb.handle, C.byref(pp))
+        assert np.array_equal(hb.download(np.float32, (3 + 2 * P) * H), voxref.pack_locdit(*parts, pp))
+    sb = ctx.array(p * 3)
+    abi.call("vx_silu_inplace", ctx.handle, sb.handle, n)
+    pd = p.astype(np.float64) * 3
+    assert rel_l2(sb.download(np.float32, n), pd / (1 + np.exp(-pd))) < 1e-6
+    ab = ctx.array(x)
+    abi.call("vx_add_vectors", ctx.handle, ab.handle, pb.handle, n)
+    assert np.array_equal(ab.download(np.float32, n), x + p)

@@ -85,6 +85,18 @@ DenseScoresPush = _struct("DenseScoresPush", [(n, u32) for n in (
 DenseSoftmaxPush = _struct("DenseSoftmaxPush", [(n, u32) for n in ("tokens", "q_heads", "score_stride")])
 DenseValuesPush = _struct("DenseValuesPush", [(n, u32) for n in (
     "tokens", "q_heads", "kv_heads", "head_dim", "out_stride", "v_stride", "score_stride")])
+CfmNoisePush = _struct("CfmNoisePush", [("n", u32), ("seed_lo", u32), ("seed_hi", u32), ("temperature", f32)])
+CfmEulerPush = _struct("CfmEulerPush", [("n", u32), ("dt", f32), ("cfg", f32), ("use_zero_star", u32)])
+TimePush = _struct("TimePush", [("dim", u32), ("t", f32)])
+PackLocDitPush = _struct("PackLocDitPush", [("hidden", u32), ("patch_tokens", u32), ("zero_mu", u32)])
+LocDitConfig = _struct("LocDitConfig", [(n, u32) for n in (
+    "hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "feat_dim", "patch", "n_mu", "n_cond",
+    "cond_raw", "uncond_zero_cond")] + [("rms_epsilon", f32), ("rope_theta", f32), ("rope_scaling", f32)])
+CfmOptions = _struct("CfmOptions", [("n_timesteps", u32), ("cfg_value", f32), ("temperature", f32),
+                                    ("sway_sampling_coef", f32), ("seed", u64), ("use_cfg_zero_star", u32)])
+CfmResult = _struct("CfmResult", [("elapsed_ms", f64), ("n_timesteps", u32), ("estimator_calls", u32),
+                                  ("zero_init_steps", u32), ("output_checksum", f64), ("output_l2", f64),
+                                  ("output_min", f32), ("output_max", f32)])
 DeviceInfo = _struct("DeviceInfo", [("name", C.c_char * 256), ("arch", C.c_char * 64),
                                     ("total_global_mem", u64), ("compute_units", u32),
                                     ("wavefront_size", u32), ("l2_cache_bytes", u32),
@@ -136,6 +148,7 @@ MODEL = vp
 GRAPH = vp
 ENGINE = vp
 GGUF = vp
+LOCDIT = vp
 
 # name -> (restype, argtypes)
 PROTOTYPES = {
@@ -197,6 +210,16 @@ PROTOTYPES = {
     "vx_dense_attn_scores": (i32, [CTX, BUFP, BUFP, BUFP, P(DenseScoresPush)]),
     "vx_dense_softmax": (i32, [CTX, BUFP, P(DenseSoftmaxPush)]),
     "vx_dense_attn_values": (i32, [CTX, BUFP, BUFP, BUFP, P(DenseValuesPush)]),
+    "vx_cfm_noise": (i32, [CTX, BUFP, P(CfmNoisePush)]),
+    "vx_cfm_cfg_euler": (i32, [CTX, BUFP, BUFP, BUFP, P(CfmEulerPush)]),
+    "vx_time_sinusoidal": (i32, [CTX, BUFP, P(TimePush)]),
+    "vx_pack_locdit": (i32, [CTX, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP, P(PackLocDitPush)]),
+    "vx_silu_inplace": (i32, [CTX, BUFP, u32]),
+    "vx_add_vectors": (i32, [CTX, BUFP, BUFP, u32]),
+    "vx_locdit_create": (i32, [CTX, MODEL, MODEL, u32, P(LocDitConfig), u32, P(LOCDIT)]),
+    "vx_locdit_destroy": (i32, [LOCDIT]),
+    "vx_locdit_estimate": (i32, [LOCDIT, P(f32), P(f32), P(f32), f32, f32, P(f32)]),
+    "vx_locdit_cfm_solve": (i32, [LOCDIT, P(f32), P(f32), P(CfmOptions), P(f32), P(f32), P(CfmResult)]),
     "vx_fused_qkv_rope_store": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP,
                                       P(FusedQkvArgs)]),
     "vx_fused_attention_scratch_bytes": (u64, [P(FusedAttnArgs)]),
@@ -247,7 +270,9 @@ STRUCT_SIZES = {  # C name -> ctypes struct
     "vx_seq_residual_rms_push": SeqResidualRmsPush, "vx_seq_qkv_push": SeqQkvPush,
     "vx_seq_swiglu_push": SeqSwigluPush, "vx_seq_rope_push": SeqRopePush,
     "vx_dense_scores_push": DenseScoresPush, "vx_dense_softmax_push": DenseSoftmaxPush,
-    "vx_dense_values_push": DenseValuesPush,
+    "vx_dense_values_push": DenseValuesPush, "vx_cfm_noise_push": CfmNoisePush,
+    "vx_cfm_euler_push": CfmEulerPush, "vx_time_push": TimePush, "vx_pack_locdit_push": PackLocDitPush,
+    "vx_locdit_config": LocDitConfig, "vx_cfm_options": CfmOptions, "vx_cfm_result": CfmResult,
     "vx_device_info": DeviceInfo, "vx_prof_entry": ProfEntry, "vx_tensor_info": TensorInfo,
     "vx_fused_qkv_args": FusedQkvArgs, "vx_fused_attn_args": FusedAttnArgs,
     "vx_fused_residual_args": FusedResidualArgs, "vx_fused_swiglu_args": FusedSwigluArgs,

@@ -1,0 +1,172 @@
+// Kernels of the LocDiT flow-matching solve (UnifiedCFM, local.rs:383-430):
+// seeded Gaussian noise, the CFG-Zero* Euler update, the sinusoidal time
+// embedding, LocDiT token packing, and small elementwise ops. All fp32; the
+// noise hash is exact integer arithmetic.
+#include "vx_internal.h"
+
+namespace vx {
+namespace {
+
+// Integer finaliser of cfm_noise.comp:11-18 (xorshift-multiply, two rounds).
+__device__ __forceinline__ uint32_t mix32(uint32_t v) {
+    v ^= v >> 16;
+    v *= 0x7feb352du;
+    v ^= v >> 15;
+    v *= 0x846ca68bu;
+    v ^= v >> 16;
+    return v;
+}
+
+// cfm_noise.comp:25-37: x[i] = temperature * Box-Muller(u(a), u(b)) for the pair
+// i/2, with a, b hashes of the pair index and the 64-bit seed. The seed is read
+// from device memory (seed[0] = low word, seed[1] = high word) when `seed` is set,
+// so that a captured solve replays with new seeds.
+__global__ __launch_bounds__(256) void k_cfm_noise(float *x, uint32_t n, const uint32_t *seed, uint32_t seed_lo,
+                                                   uint32_t seed_hi, float temperature) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t lo = seed ? seed[0] : seed_lo, hi = seed ? seed[1] : seed_hi;
+    const uint32_t pair = i >> 1;
+    const uint32_t a = mix32(pair ^ lo ^ 0x9e3779b9u);
+    const uint32_t b = mix32(pair ^ hi ^ 0x85ebca6bu);
+    const float u1 = fmaxf(((float)a + 0.5f) * (1.0f / 4294967296.0f), 1.0e-7f);
+    const float u2 = ((float)b + 0.5f) * (1.0f / 4294967296.0f);
+    const float r = sqrtf(-2.0f * logf(u1));
+    const float theta = 6.28318530717958647692f * u2;
+    const float z = (i & 1u) == 0u ? r * cosf(theta) : r * sinf(theta);
+    x[i] = z * temperature;
+}
+
+// cfm_cfg_euler.comp:15-36 with the conditional and unconditional estimates
+// read from `pos` and `neg` (rows of the CFG batch): s = <p,n>/(|n|^2 + 1e-8)
+// under CFG-Zero* (else 1); x -= dt * (n*s + cfg*(p - n*s)). One workgroup; the
+// dot products are block reductions over n <= 1024 elements.
+__global__ __launch_bounds__(256) void k_cfm_cfg_euler(float *x, const float *pos, const float *neg, uint32_t n,
+                                                       float dt, float cfg, uint32_t zero_star) {
+    __shared__ float red[2][4];
+    float pn = 0.f, nn = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256u) {
+        const float p = pos[i], q = neg[i];
+        pn += p * q;
+        nn += q * q;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        pn += __shfl_xor(pn, o, 64);
+        nn += __shfl_xor(nn, o, 64);
+    }
+    if ((threadIdx.x & 63u) == 0) {
+        red[0][threadIdx.x >> 6] = pn;
+        red[1][threadIdx.x >> 6] = nn;
+    }
+    __syncthreads();
+    pn = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    nn = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    const float scale = zero_star ? pn / (nn + 1.0e-8f) : 1.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256u) {
+        const float p = pos[i], q = neg[i];
+        const float guided = q * scale + cfg * (p - q * scale);
+        x[i] -= dt * guided;
+    }
+}
+
+// time_sinusoidal.comp:5: out[i] = sin(a) for i < dim/2, cos(a) after, with
+// a = 1000 t exp(-j ln(1e4)/(dim/2 - 1)), j = i mod dim/2. t from device memory
+// (t_dev[t_index]) when t_dev is set, so a captured solve can step through t.
+__global__ __launch_bounds__(256) void k_time_sinusoidal(float *out, uint32_t dim, float t_in, const float *t_dev,
+                                                         uint32_t t_index) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= dim) return;
+    const float t = t_dev ? t_dev[t_index] : t_in;
+    const uint32_t half_dim = dim / 2u;
+    const uint32_t j = i % half_dim;
+    const float denom = (float)max(half_dim - 1u, 1u);
+    const float freq = expf((float)j * (-logf(10000.0f) / denom));
+    const float a = 1000.0f * t * freq;
+    out[i] = i < half_dim ? sinf(a) : cosf(a);
+}
+
+// pack_locdit.comp:10 generalised to n_mu mu tokens, one time token, n_cond
+// condition rows and n_x latent rows, for `batch` sequences laid out back to
+// back; sequence b zeroes its mu tokens when bit b of zero_mu_mask is set and
+// its condition rows when bit b of zero_cond_mask is set.
+__global__ __launch_bounds__(256) void k_pack_locdit(PackLocditArgs a) {
+    const uint32_t seq_tokens = a.n_mu + 1u + a.n_cond + a.n_x;
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t per = seq_tokens * a.hidden;
+    if (i >= per * a.batch) return;
+    const uint32_t b = i / per, r = i - b * per;
+    const uint32_t tok = r / a.hidden, d = r - tok * a.hidden;
+    float v;
+    if (tok < a.n_mu) {
+        v = (a.zero_mu_mask >> b) & 1u ? 0.f : a.mu[tok][d];
+    } else if (tok == a.n_mu) {
+        v = a.time[d];
+    } else if (tok < a.n_mu + 1u + a.n_cond) {
+        v = (a.zero_cond_mask >> b) & 1u ? 0.f : a.cond[(tok - a.n_mu - 1u) * a.hidden + d];
+    } else {
+        v = a.x[(tok - a.n_mu - 1u - a.n_cond) * a.hidden + d];
+    }
+    a.out[i] = v;
+}
+
+// silu_inplace.comp:5 and add_vectors.comp:6.
+__global__ __launch_bounds__(256) void k_silu_inplace(float *x, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    x[i] = v / (1.0f + expf(-v));
+}
+
+__global__ __launch_bounds__(256) void k_add_vectors(float *a, const float *b, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) a[i] += b[i];
+}
+
+}  // namespace
+
+int launch_cfm_noise(hipStream_t s, float *x, uint32_t n, const uint32_t *dev_seed, uint64_t seed, float temperature) {
+    if (!n) return VX_OK;
+    k_cfm_noise<<<(n + 255u) / 256u, 256, 0, s>>>(x, n, dev_seed, (uint32_t)seed, (uint32_t)(seed >> 32), temperature);
+    VX_LAUNCHED("k_cfm_noise");
+    return VX_OK;
+}
+
+int launch_cfm_cfg_euler(hipStream_t s, float *x, const float *pos, const float *neg, uint32_t n, float dt, float cfg,
+                         uint32_t zero_star) {
+    if (!n) return VX_OK;
+    k_cfm_cfg_euler<<<1, 256, 0, s>>>(x, pos, neg, n, dt, cfg, zero_star);
+    VX_LAUNCHED("k_cfm_cfg_euler");
+    return VX_OK;
+}
+
+int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index) {
+    if (!dim) return VX_OK;
+    k_time_sinusoidal<<<(dim + 255u) / 256u, 256, 0, s>>>(out, dim, t, t_dev, t_index);
+    VX_LAUNCHED("k_time_sinusoidal");
+    return VX_OK;
+}
+
+int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a) {
+    const uint64_t n = (uint64_t)(a.n_mu + 1u + a.n_cond + a.n_x) * a.hidden * a.batch;
+    if (!n) return VX_OK;
+    k_pack_locdit<<<(unsigned)((n + 255u) / 256u), 256, 0, s>>>(a);
+    VX_LAUNCHED("k_pack_locdit");
+    return VX_OK;
+}
+
+int launch_silu_inplace(hipStream_t s, float *x, uint32_t n) {
+    if (!n) return VX_OK;
+    k_silu_inplace<<<(n + 255u) / 256u, 256, 0, s>>>(x, n);
+    VX_LAUNCHED("k_silu_inplace");
+    return VX_OK;
+}
+
+int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n) {
+    if (!n) return VX_OK;
+    k_add_vectors<<<(n + 255u) / 256u, 256, 0, s>>>(a, b, n);
+    VX_LAUNCHED("k_add_vectors");
+    return VX_OK;
+}
+
+}  // namespace vx

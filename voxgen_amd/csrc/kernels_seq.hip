@@ -418,7 +418,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
 __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
     __shared__ float2 cs[64];
     const uint32_t t = blockIdx.x;
-    const uint32_t pos = a.pos_base + t;
+    const uint32_t pos = a.pos_base + (a.pos_period ? t % a.pos_period : t);
     const uint32_t half_dim = a.head_dim / 2u;
     if (threadIdx.x < half_dim) {
         const uint32_t i = threadIdx.x;
@@ -726,9 +726,9 @@ __global__ __launch_bounds__(256) void k_seq_linear_generic(SeqGenericArgs a) {
         v = s / (1.0f + expf(-s)) * s2;
     } else {
         float b = 0.f;
-        if (a.has_bias)
-            b = a.bias_dtype == 0u ? reinterpret_cast<const float *>(a.raw + a.bias_off)[row]
-                                   : h2f(reinterpret_cast<const unsigned short *>(a.raw + a.bias_off)[row]);
+        if (a.bias)
+            b = a.bias_dtype == 0u ? static_cast<const float *>(a.bias)[row]
+                                   : h2f(static_cast<const unsigned short *>(a.bias)[row]);
         v = (s + b) * a.alpha;
     }
     a.y[a.out_base + (size_t)tok * a.out_stride + row] = v;
@@ -746,7 +746,10 @@ __global__ __launch_bounds__(256) void k_silu_mul(float *g, const float *u, uint
 // for every key < tokens (no mask). Workgroup (query token, head), lane per key.
 __global__ __launch_bounds__(64) void k_dense_scores(DenseAttnArgs a) {
     __shared__ float qs[256];
-    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const uint32_t t = blockIdx.x, h = blockIdx.y, bz = blockIdx.z;
+    a.q += (size_t)bz * a.tokens * a.q_stride;
+    a.k += (size_t)bz * a.tokens * a.k_stride;
+    a.s += (size_t)bz * a.tokens * a.q_heads * a.score_stride;
     const uint32_t kv = h / (a.q_heads / a.kv_heads);
     const float *q = a.q + (size_t)t * a.q_stride + h * a.head_dim;
     for (uint32_t i = threadIdx.x; i < a.head_dim; i += 64u) qs[i] = q[i];
@@ -763,7 +766,7 @@ __global__ __launch_bounds__(64) void k_dense_scores(DenseAttnArgs a) {
 // dense_softmax.comp:5: max-subtracted softmax of each (token, head) row.
 __global__ __launch_bounds__(64) void k_dense_softmax(float *s, uint32_t tokens, uint32_t q_heads,
                                                       uint32_t score_stride) {
-    const uint32_t h = blockIdx.x, t = blockIdx.y;
+    const uint32_t h = blockIdx.x, t = blockIdx.y + blockIdx.z * tokens;
     float *row = s + ((size_t)t * q_heads + h) * score_stride;
     float m = -FLT_MAX;
     for (uint32_t i = threadIdx.x; i < tokens; i += 64u) m = fmaxf(m, row[i]);
@@ -782,8 +785,11 @@ __global__ __launch_bounds__(64) void k_dense_softmax(float *s, uint32_t tokens,
 
 // dense_attn_values.comp:7: o[t*out_stride + h*d + j] = sum_key s[...key] * v[key*v_stride + kv*d + j].
 __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
-    const uint32_t j = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
+    const uint32_t j = threadIdx.x, h = blockIdx.x, t = blockIdx.y, bz = blockIdx.z;
     if (j >= a.head_dim) return;
+    a.v += (size_t)bz * a.tokens * a.v_stride;
+    a.out += (size_t)bz * a.tokens * a.out_stride;
+    a.s += (size_t)bz * a.tokens * a.q_heads * a.score_stride;
     const uint32_t kv = h / (a.q_heads / a.kv_heads);
     const float *row = a.s + ((size_t)t * a.q_heads + h) * a.score_stride;
     float z = 0.f;
@@ -898,18 +904,18 @@ int launch_silu_mul(hipStream_t s, float *g, const float *u, uint32_t n) {
 }
 
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which) {
-    if (!a.tokens || !a.q_heads) return VX_OK;
+    if (!a.tokens || !a.q_heads || !a.batch) return VX_OK;
     if (!a.kv_heads || a.q_heads % a.kv_heads) return fail(VX_ERR_SHAPE, "dense attention: head counts");
     if (which == 0) {
         if (a.head_dim > 256u) return fail(VX_ERR_UNSUPPORTED, "dense attention: head_dim > 256");
-        k_dense_scores<<<dim3(a.tokens, a.q_heads), 64, 0, s>>>(a);
+        k_dense_scores<<<dim3(a.tokens, a.q_heads, a.batch), 64, 0, s>>>(a);
         VX_LAUNCHED("k_dense_scores");
     } else if (which == 1) {
-        k_dense_softmax<<<dim3(a.q_heads, a.tokens), 64, 0, s>>>(a.s, a.tokens, a.q_heads, a.score_stride);
+        k_dense_softmax<<<dim3(a.q_heads, a.tokens, a.batch), 64, 0, s>>>(a.s, a.tokens, a.q_heads, a.score_stride);
         VX_LAUNCHED("k_dense_softmax");
     } else {
         if (a.head_dim > 256u) return fail(VX_ERR_UNSUPPORTED, "dense attention: head_dim > 256");
-        k_dense_values<<<dim3(a.q_heads, a.tokens), 256, 0, s>>>(a);
+        k_dense_values<<<dim3(a.q_heads, a.tokens, a.batch), 256, 0, s>>>(a);
         VX_LAUNCHED("k_dense_values");
     }
     return VX_OK;

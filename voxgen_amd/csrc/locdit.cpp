@@ -1,0 +1,637 @@
+// LocDiT estimator and the UnifiedCFM solve (LocalEngine, local.rs:264-537) over
+// HIP, plus the per-op entry points of the CFM shaders.
+//
+// One estimator pass (record_locdit_common + record_locdit_body,
+// local.rs:445-468):
+//   x tokens    = in_proj(x patch) + b          [patch][hidden]
+//   cond tokens = cond_proj(cond patch) + b     [patch][hidden] (or given rows)
+//   time token  = time_mlp(sin(t)) + delta_time_mlp(sin(dt))
+//   hidden      = [mu tokens | time | cond tokens | x tokens]   (pack_locdit)
+//   transformer: rmsnorm, per layer q/k/v -> RoPE (position = token index) ->
+//                dense attention -> attn_output -> residual rmsnorm -> SwiGLU ->
+//                down -> residual rmsnorm (record_transformer, local.rs:482-527)
+//   out         = out_proj(norm of the x tokens) + b  [patch][feat]
+// The solve (cfm_solve, local.rs:383-430) runs the conditional and the
+// unconditional pass of every Euler step as ONE batch of two sequences: the
+// projections see 2 x tokens rows (each weight is streamed once per step, not
+// twice), the attention stays per sequence, and the CFG-Zero* update reads both
+// outputs. The whole solve is captured as one hipGraph and replayed while the
+// options are unchanged; the noise seed is read from device memory.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "vx_internal.h"
+
+using namespace vx;
+
+namespace {
+
+struct LocLayer {
+    WRef q, k, v, o, gate, up, down;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+
+struct Lin {
+    WRef w;
+    const void *b = nullptr;
+    uint32_t bt = 0;
+};
+
+inline float *F(vx_buf *b) { return static_cast<float *>(b->ptr); }
+
+}  // namespace
+
+struct vx_locdit {
+    vx_ctx *ctx = nullptr;
+    const vx_model *model = nullptr;
+    vx_locdit_config cfg{};
+    uint32_t S = 0;   // tokens per sequence
+    Lin in_proj, cond_proj, out_proj, t1, t2, d1, d2;
+    const float *norm_w = nullptr, *rope_factors = nullptr;
+    std::vector<LocLayer> layers;
+    // State and activations (two sequences: conditional, unconditional).
+    vx_buf *x = nullptr, *cond_in = nullptr, *mu = nullptr, *patch_proj = nullptr, *cond_proj_out = nullptr;
+    vx_buf *tsin = nullptr, *ttmp = nullptr, *tvec = nullptr, *dsin = nullptr, *dtmp = nullptr, *dvec = nullptr;
+    vx_buf *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    vx_buf *gate = nullptr, *branch = nullptr, *scores = nullptr, *out = nullptr, *seed = nullptr;
+    vx_graph *graph = nullptr;
+    vx_cfm_options graph_opt{};
+    int graph_initial_x = -1;
+};
+
+namespace {
+
+int find(const vx_model *m, const std::string &name, const vx_tensor_info **out) {
+    auto it = m->by_name.find(name);
+    if (it == m->by_name.end())
+        return fail(VX_ERR_NOT_FOUND, "required GGUF tensor \"%s\" is missing", name.c_str());
+    *out = &m->tensors[it->second];
+    return VX_OK;
+}
+
+// require_matrix (local.rs:170-174): dims [cols, rows], F16.
+int matrix(const vx_model *m, const std::string &name, uint32_t cols, uint32_t rows, WRef *w) {
+    const vx_tensor_info *t;
+    VX_CHECK(find(m, name, &t));
+    if (t->n_dims != 2 || t->dims[0] != cols || t->dims[1] != rows)
+        return fail(VX_ERR_SHAPE, "%s has dimensions [%llu, %llu], expected [%u, %u]", name.c_str(),
+                    (unsigned long long)t->dims[0], (unsigned long long)(t->n_dims > 1 ? t->dims[1] : 1), cols,
+                    rows);
+    if (t->ggml_type != VX_DTYPE_F16)
+        return fail(VX_ERR_SHAPE, "%s is type %u, expected F16 acoustic weight", name.c_str(), t->ggml_type);
+    return resolve_matrix(m, (uint32_t)t->offset, VX_DTYPE_F16, rows, cols, w, name.c_str());
+}
+
+// require_vector (local.rs:175-180).
+int vector(const vx_model *m, const std::string &name, uint32_t n, bool f32_only, const void **p, uint32_t *dtype) {
+    const vx_tensor_info *t;
+    VX_CHECK(find(m, name, &t));
+    if (t->n_dims != 1 || t->dims[0] != n)
+        return fail(VX_ERR_SHAPE, "%s has dimensions [%llu], expected [%u]", name.c_str(),
+                    (unsigned long long)t->dims[0], n);
+    if (f32_only && t->ggml_type != VX_DTYPE_F32)
+        return fail(VX_ERR_SHAPE, "%s is type %u, expected F32 norm", name.c_str(), t->ggml_type);
+    if (t->ggml_type != VX_DTYPE_F32 && t->ggml_type != VX_DTYPE_F16)
+        return fail(VX_ERR_SHAPE, "%s has unsupported type %u", name.c_str(), t->ggml_type);
+    if (dtype) *dtype = t->ggml_type == VX_DTYPE_F32 ? 0u : 1u;
+    return resolve_vector(m, (uint32_t)t->offset, t->ggml_type, n, p, name.c_str());
+}
+
+int linear(const vx_model *m, const std::string &prefix, uint32_t cols, uint32_t rows, Lin *l) {
+    VX_CHECK(matrix(m, prefix + ".weight", cols, rows, &l->w));
+    return vector(m, prefix + ".bias", rows, false, &l->b, &l->bt);
+}
+
+int validate(const vx_locdit_config &c, bool strict) {
+    if (!c.hidden || !c.layers || !c.q_heads || !c.kv_heads || !c.head_dim || !c.ffn || !c.feat_dim || !c.patch)
+        return fail(VX_ERR_INVALID_ARG, "LocDiT config has a zero dimension");
+    if (c.n_mu > 2) return fail(VX_ERR_UNSUPPORTED, "LocDiT takes at most two mu tokens");
+    if (!c.cond_raw && c.n_cond != c.patch)
+        return fail(VX_ERR_SHAPE, "projected condition has patch=%u tokens, config says %u", c.patch, c.n_cond);
+    if (c.q_heads % c.kv_heads) return fail(VX_ERR_SHAPE, "q_heads %u not a multiple of kv_heads %u", c.q_heads, c.kv_heads);
+    if (c.head_dim > 128u || (c.head_dim & 1u)) return fail(VX_ERR_UNSUPPORTED, "head_dim %u (even, <= 128)", c.head_dim);
+    if (strict && (c.hidden != 1024u || c.layers != 12u || c.q_heads != 16u || c.kv_heads != 2u || c.head_dim != 128u ||
+                   c.ffn != 4096u || c.patch != 4u || c.feat_dim != 64u || c.n_mu != 2u || c.cond_raw))
+        // LocalConfig::from_gguf (local.rs:85-92) and the 16q/2kv x 128 geometry check.
+        return fail(VX_ERR_UNSUPPORTED,
+                    "unsupported VoxCPM2 local contract: LocDiT=%ux%u, heads %u/%u x %u, ffn %u, patch %u x %u; "
+                    "expected 12x1024, 16/2 x 128, 4096, 4 x 64",
+                    c.layers, c.hidden, c.q_heads, c.kv_heads, c.head_dim, c.ffn, c.patch, c.feat_dim);
+    const uint64_t S = (uint64_t)c.n_mu + 1u + c.n_cond + c.patch;
+    if (S > 4096u) return fail(VX_ERR_UNSUPPORTED, "LocDiT sequence of %llu tokens", (unsigned long long)S);
+    return VX_OK;
+}
+
+void free_all(vx_locdit *e) {
+    if (e->graph) {
+        vx_graph_free(e->ctx, e->graph);
+        e->graph = nullptr;
+    }
+    vx_buf **bufs[] = {&e->x,      &e->cond_in, &e->mu,   &e->patch_proj, &e->cond_proj_out, &e->tsin,
+                       &e->ttmp,   &e->tvec,    &e->dsin, &e->dtmp,       &e->dvec,          &e->hidden,
+                       &e->norm,   &e->q,       &e->k,    &e->v,          &e->attn,          &e->gate,
+                       &e->branch, &e->scores,  &e->out,  &e->seed};
+    for (vx_buf **b : bufs) {
+        vx_free(e->ctx, *b);
+        *b = nullptr;
+    }
+}
+
+// Time embedding (record_time, local.rs:470-480): tvec = time_mlp(sin(t)) +
+// delta_time_mlp(sin(dt)), each MLP linear -> SiLU -> linear.
+int enqueue_time(vx_locdit *e, float t, float dt) {
+    hipStream_t s = e->ctx->stream;
+    const uint32_t H = e->cfg.hidden;
+    ProfSpan sp(e->ctx, "local.time");
+    VX_CHECK(launch_time_sinusoidal(s, F(e->tsin), H, t, nullptr, 0));
+    VX_CHECK(launch_time_sinusoidal(s, F(e->dsin), H, dt, nullptr, 0));
+    VX_CHECK(enqueue_seq_linear(s, e->t1.w, e->t1.b, e->t1.bt, H, H, 1, F(e->tsin), 0, H, F(e->ttmp), 0, H, 1.f));
+    VX_CHECK(enqueue_seq_linear(s, e->d1.w, e->d1.b, e->d1.bt, H, H, 1, F(e->dsin), 0, H, F(e->dtmp), 0, H, 1.f));
+    VX_CHECK(launch_silu_inplace(s, F(e->ttmp), H));
+    VX_CHECK(launch_silu_inplace(s, F(e->dtmp), H));
+    VX_CHECK(enqueue_seq_linear(s, e->t2.w, e->t2.b, e->t2.bt, H, H, 1, F(e->ttmp), 0, H, F(e->tvec), 0, H, 1.f));
+    VX_CHECK(enqueue_seq_linear(s, e->d2.w, e->d2.b, e->d2.bt, H, H, 1, F(e->dtmp), 0, H, F(e->dvec), 0, H, 1.f));
+    return launch_add_vectors(s, F(e->tvec), F(e->dvec), H);
+}
+
+// in_proj / cond_proj (record_locdit_common, local.rs:445-449).
+int enqueue_inputs(vx_locdit *e) {
+    hipStream_t s = e->ctx->stream;
+    const vx_locdit_config &c = e->cfg;
+    ProfSpan sp(e->ctx, "local.locdit_in");
+    VX_CHECK(enqueue_seq_linear(s, e->in_proj.w, e->in_proj.b, e->in_proj.bt, c.hidden, c.feat_dim, c.patch, F(e->x),
+                                0, c.feat_dim, F(e->patch_proj), 0, c.hidden, 1.f));
+    if (!c.cond_raw)
+        VX_CHECK(enqueue_seq_linear(s, e->cond_proj.w, e->cond_proj.b, e->cond_proj.bt, c.hidden, c.feat_dim, c.patch,
+                                    F(e->cond_in), 0, c.feat_dim, F(e->cond_proj_out), 0, c.hidden, 1.f));
+    return VX_OK;
+}
+
+// pack_locdit + record_transformer + out_proj for `batch` sequences (1: the
+// conditional pass; 2: conditional then unconditional).
+int enqueue_body(vx_locdit *e, uint32_t batch) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_locdit_config &c = e->cfg;
+    const uint32_t H = c.hidden, S = e->S, M = S * batch;
+    const uint32_t QD = c.q_heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    {
+        ProfSpan sp(ctx, "local.pack_locdit");
+        PackLocditArgs p;
+        p.mu[0] = F(e->mu);
+        p.mu[1] = F(e->mu) + H;
+        p.time = F(e->tvec);
+        p.cond = c.cond_raw ? F(e->cond_in) : F(e->cond_proj_out);
+        p.x = F(e->patch_proj);
+        p.out = F(e->hidden);
+        p.hidden = H;
+        p.n_mu = c.n_mu;
+        p.n_cond = c.n_cond;
+        p.n_x = c.patch;
+        p.batch = batch;
+        p.zero_mu_mask = 0x2u;                               // the unconditional sequence (local.rs:413-421)
+        p.zero_cond_mask = c.uncond_zero_cond ? 0x2u : 0u;
+        VX_CHECK(launch_pack_locdit(s, p));
+    }
+    SeqNormArgs n;
+    n.h = F(e->hidden);
+    n.ldh = H;
+    n.w = e->layers[0].attn_norm;
+    n.n = H;
+    n.eps = c.rms_epsilon;
+    n.y = F(e->norm);
+    n.ldy = H;
+    {
+        ProfSpan sp(ctx, "local.seq_rmsnorm");
+        VX_CHECK(launch_seq_rmsnorm(s, n, M));
+    }
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const LocLayer &L = e->layers[l];
+        {
+            ProfSpan sp(ctx, "local.seq_qkv");
+            const WRef w[3] = {L.q, L.k, L.v};
+            const uint32_t rows[3] = {QD, KD, KD}, strides[3] = {QD, KD, KD};
+            float *const o[3] = {F(e->q), F(e->k), F(e->v)};
+            VX_CHECK(enqueue_seq_qkv(s, w, rows, H, M, F(e->norm), 0, H, o, strides));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_rope");
+            SeqRopeArgs r;
+            r.q = F(e->q);
+            r.k = F(e->k);
+            r.ldq = QD;
+            r.ldk = KD;
+            r.factors = e->rope_factors;
+            r.q_heads = c.q_heads;
+            r.kv_heads = c.kv_heads;
+            r.head_dim = c.head_dim;
+            r.pos_period = S;   // seq_rope.comp:8: position = token index within the sequence
+            r.theta = c.rope_theta;
+            r.scaling = c.rope_scaling;
+            VX_CHECK(launch_seq_rope_store(s, r, M));
+        }
+        {
+            ProfSpan sp(ctx, "local.attention");
+            DenseAttnArgs a;
+            a.q = F(e->q);
+            a.k = F(e->k);
+            a.v = F(e->v);
+            a.s = F(e->scores);
+            a.out = F(e->attn);
+            a.tokens = S;
+            a.q_heads = c.q_heads;
+            a.kv_heads = c.kv_heads;
+            a.head_dim = c.head_dim;
+            a.q_stride = QD;
+            a.k_stride = KD;
+            a.v_stride = KD;
+            a.out_stride = QD;
+            a.score_stride = S;
+            a.batch = batch;
+            VX_CHECK(launch_dense_attn(s, a, 0));
+            VX_CHECK(launch_dense_attn(s, a, 1));
+            VX_CHECK(launch_dense_attn(s, a, 2));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_linear");
+            VX_CHECK(enqueue_seq_linear(s, L.o, nullptr, 0, H, QD, M, F(e->attn), 0, QD, F(e->branch), 0, H, 1.f));
+        }
+        SeqNormArgs r;
+        r.h = F(e->hidden);
+        r.ldh = H;
+        r.branch = F(e->branch);
+        r.ldb = H;
+        r.scale = 1.f;
+        r.n = H;
+        r.eps = c.rms_epsilon;
+        r.y = F(e->norm);
+        r.ldy = H;
+        {
+            ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
+            r.w = L.ffn_norm;
+            VX_CHECK(launch_seq_rmsnorm(s, r, M));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_swiglu");
+            VX_CHECK(enqueue_seq_swiglu(s, L.gate, L.up, c.ffn, H, M, F(e->norm), 0, H, F(e->gate), 0, c.ffn));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_linear");
+            VX_CHECK(enqueue_seq_linear(s, L.down, nullptr, 0, H, c.ffn, M, F(e->gate), 0, c.ffn, F(e->branch), 0, H,
+                                        1.f));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
+            r.w = l + 1 < c.layers ? e->layers[l + 1].attn_norm : e->norm_w;
+            VX_CHECK(launch_seq_rmsnorm(s, r, M));
+        }
+    }
+    ProfSpan sp(ctx, "local.locdit_out");
+    const uint32_t x0 = c.n_mu + 1u + c.n_cond;   // first x token of a sequence
+    for (uint32_t b = 0; b < batch; ++b)
+        VX_CHECK(enqueue_seq_linear(s, e->out_proj.w, e->out_proj.b, e->out_proj.bt, c.feat_dim, H, c.patch,
+                                    F(e->norm), (b * S + x0) * H, H, F(e->out), b * c.patch * c.feat_dim, c.feat_dim,
+                                    1.f));
+    return VX_OK;
+}
+
+// cfm_time_span (local.rs:531-537): t_i = 1 - i/n, w = t + sway (cos(pi t / 2) - 1 + t).
+int time_span(uint32_t n, float sway, std::vector<float> &out) {
+    if (n == 0) return fail(VX_ERR_INVALID_ARG, "CFM n_timesteps must be >= 1");
+    out.clear();
+    for (uint32_t i = 0; i <= n; ++i) {
+        const float t = 1.0f - (float)i / (float)n;
+        const float w = t + sway * (std::cos(1.57079632679489661923f * t) - 1.0f + t);
+        if (!std::isfinite(w)) return fail(VX_ERR_INVALID_ARG, "non-finite CFM time grid at %u", i);
+        out.push_back(w);
+    }
+    for (size_t i = 1; i < out.size(); ++i)
+        if (out[i] > out[i - 1] + 1.0e-6f)
+            return fail(VX_ERR_INVALID_ARG, "CFM sway schedule is not descending at %zu: %g -> %g", i, out[i - 1],
+                        out[i]);
+    return VX_OK;
+}
+
+int validate_options(const vx_cfm_options &o) {  // CfmOptions::validate (local.rs:262-268)
+    if (o.n_timesteps == 0) return fail(VX_ERR_INVALID_ARG, "CFM n_timesteps must be >= 1");
+    if (!std::isfinite(o.cfg_value) || !std::isfinite(o.temperature) || !std::isfinite(o.sway_sampling_coef))
+        return fail(VX_ERR_INVALID_ARG, "CFM options must be finite");
+    if (o.temperature < 0.0f) return fail(VX_ERR_INVALID_ARG, "CFM temperature must be >= 0");
+    return VX_OK;
+}
+
+uint32_t zero_init_steps(const vx_cfm_options &o, size_t span_len) {
+    return o.use_cfg_zero_star ? std::max<uint32_t>(1u, (uint32_t)std::floor((float)span_len * 0.04f)) : 0u;
+}
+
+// The solve after the inputs are in place (cfm_solve, local.rs:383-430).
+int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_t *calls) {
+    hipStream_t s = e->ctx->stream;
+    const vx_locdit_config &c = e->cfg;
+    const uint32_t n = c.patch * c.feat_dim;
+    std::vector<float> span;
+    VX_CHECK(time_span(o.n_timesteps, o.sway_sampling_coef, span));
+    if (!initial_x) {
+        ProfSpan sp(e->ctx, "local.cfm_noise");
+        VX_CHECK(launch_cfm_noise(s, F(e->x), n, static_cast<const uint32_t *>(e->seed->ptr), 0, o.temperature));
+    }
+    const uint32_t zi = zero_init_steps(o, span.size());
+    uint32_t est = 0;
+    for (size_t step = 1; step < span.size(); ++step) {
+        if (step <= zi) continue;
+        const float t = span[step - 1], dt = t - span[step];
+        VX_CHECK(enqueue_inputs(e));
+        VX_CHECK(enqueue_time(e, t, 0.0f));   // mean_mode = false: estimator dt is zero
+        VX_CHECK(enqueue_body(e, 2));
+        ProfSpan sp(e->ctx, "local.cfm_cfg_euler");
+        VX_CHECK(launch_cfm_cfg_euler(s, F(e->x), F(e->out), F(e->out) + n, n, dt, o.cfg_value,
+                                      o.use_cfg_zero_star ? 1u : 0u));
+        est += 2;
+    }
+    if (calls) *calls = est;
+    return VX_OK;
+}
+
+int check_finite(const float *v, uint64_t n, const char *what) {
+    for (uint64_t i = 0; i < n; ++i)
+        if (!std::isfinite(v[i]))
+            return fail(VX_ERR_INVALID_ARG, "%s contains non-finite value at index %llu: %g", what,
+                        (unsigned long long)i, v[i]);
+    return VX_OK;
+}
+
+int upload_inputs(vx_locdit *e, const float *cond, const float *mu) {
+    const vx_locdit_config &c = e->cfg;
+    const uint64_t cn = c.cond_raw ? (uint64_t)c.n_cond * c.hidden : (uint64_t)c.patch * c.feat_dim;
+    if (!cond) return fail(VX_ERR_INVALID_ARG, "LocDiT condition is null");
+    VX_CHECK(check_finite(cond, cn, "CFM condition"));
+    VX_CHECK(vx_upload(e->ctx, e->cond_in, 0, cond, cn * 4u));
+    if (c.n_mu) {
+        if (!mu) return fail(VX_ERR_INVALID_ARG, "LocDiT mu is null");
+        VX_CHECK(check_finite(mu, (uint64_t)c.n_mu * c.hidden, "CFM mu"));
+        VX_CHECK(vx_upload(e->ctx, e->mu, 0, mu, (uint64_t)c.n_mu * c.hidden * 4u));
+    }
+    return VX_OK;
+}
+
+double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+bool same_options(const vx_cfm_options &a, const vx_cfm_options &b) {
+    return a.n_timesteps == b.n_timesteps && a.cfg_value == b.cfg_value && a.temperature == b.temperature &&
+           a.sway_sampling_coef == b.sway_sampling_coef && a.use_cfg_zero_star == b.use_cfg_zero_star;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_model, uint32_t rope_factor_offset,
+                     const vx_locdit_config *cfg, uint32_t strict_geometry, vx_locdit **out) {
+    if (!ctx || !model || !rope_model || !cfg || !out) return fail(VX_ERR_INVALID_ARG, "vx_locdit_create: null argument");
+    *out = nullptr;
+    VX_CHECK(validate(*cfg, strict_geometry != 0));
+    vx_locdit *e = new vx_locdit();
+    e->ctx = ctx;
+    e->model = model;
+    e->cfg = *cfg;
+    const vx_locdit_config &c = e->cfg;
+    e->S = c.n_mu + 1u + c.n_cond + c.patch;
+    auto bail = [&](int st) {
+        free_all(e);
+        delete e;
+        return st;
+    };
+    const uint32_t H = c.hidden, QD = c.q_heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    // validate_tensors (local.rs:127-145) for the LocDiT half.
+    int st;
+    if ((st = linear(model, "locdit.in_proj", c.feat_dim, H, &e->in_proj))) return bail(st);
+    if (!c.cond_raw && (st = linear(model, "locdit.cond_proj", c.feat_dim, H, &e->cond_proj))) return bail(st);
+    if ((st = linear(model, "locdit.out_proj", H, c.feat_dim, &e->out_proj))) return bail(st);
+    const void *p;
+    if ((st = vector(model, "locdit.norm.weight", H, true, &p, nullptr))) return bail(st);
+    e->norm_w = static_cast<const float *>(p);
+    if ((st = linear(model, "locdit.time_mlp.linear_1", H, H, &e->t1)) ||
+        (st = linear(model, "locdit.time_mlp.linear_2", H, H, &e->t2)) ||
+        (st = linear(model, "locdit.delta_time_mlp.linear_1", H, H, &e->d1)) ||
+        (st = linear(model, "locdit.delta_time_mlp.linear_2", H, H, &e->d2)))
+        return bail(st);
+    e->layers.resize(c.layers);
+    for (uint32_t l = 0; l < c.layers; ++l) {  // validate_local_layers (local.rs:150-168)
+        LocLayer &L = e->layers[l];
+        const std::string pre = "locdit.blk." + std::to_string(l) + ".";
+        if ((st = vector(model, pre + "attn_norm.weight", H, true, &p, nullptr))) return bail(st);
+        L.attn_norm = static_cast<const float *>(p);
+        if ((st = vector(model, pre + "ffn_norm.weight", H, true, &p, nullptr))) return bail(st);
+        L.ffn_norm = static_cast<const float *>(p);
+        if ((st = matrix(model, pre + "attn_q.weight", H, QD, &L.q)) || (st = matrix(model, pre + "attn_k.weight", H, KD, &L.k)) ||
+            (st = matrix(model, pre + "attn_v.weight", H, KD, &L.v)) ||
+            (st = matrix(model, pre + "attn_output.weight", QD, H, &L.o)) ||
+            (st = matrix(model, pre + "ffn_gate.weight", H, c.ffn, &L.gate)) ||
+            (st = matrix(model, pre + "ffn_up.weight", H, c.ffn, &L.up)) ||
+            (st = matrix(model, pre + "ffn_down.weight", c.ffn, H, &L.down)))
+            return bail(st);
+    }
+    if ((st = resolve_vector(rope_model, rope_factor_offset, VX_DTYPE_F32, c.head_dim / 2u, &p, "LocDiT rope factors")))
+        return bail(st);
+    e->rope_factors = static_cast<const float *>(p);
+    // Buffers (LocalEngine::new, local.rs:285-297), sized for the CFG batch of two.
+    const uint64_t f = 4, S2 = 2ull * e->S;
+    const uint64_t cond_n = c.cond_raw ? (uint64_t)c.n_cond * H : (uint64_t)c.patch * c.feat_dim;
+    struct {
+        vx_buf **b;
+        uint64_t n;
+    } bufs[] = {{&e->x, (uint64_t)c.patch * c.feat_dim},
+                {&e->cond_in, cond_n},
+                {&e->mu, 2ull * H},
+                {&e->patch_proj, (uint64_t)c.patch * H},
+                {&e->cond_proj_out, (uint64_t)c.patch * H},
+                {&e->tsin, H},
+                {&e->ttmp, H},
+                {&e->tvec, H},
+                {&e->dsin, H},
+                {&e->dtmp, H},
+                {&e->dvec, H},
+                {&e->hidden, S2 * H},
+                {&e->norm, S2 * H},
+                {&e->q, S2 * QD},
+                {&e->k, S2 * KD},
+                {&e->v, S2 * KD},
+                {&e->attn, S2 * QD},
+                {&e->gate, S2 * c.ffn},
+                {&e->branch, S2 * H},
+                {&e->scores, S2 * c.q_heads * e->S},
+                {&e->out, 2ull * c.patch * c.feat_dim},
+                {&e->seed, 2}};
+    for (auto &b : bufs)
+        if ((st = vx_alloc(ctx, std::max<uint64_t>(b.n * f, 16u), b.b))) return bail(st);
+    for (auto &b : bufs)
+        if (hipMemsetAsync((*b.b)->ptr, 0, (*b.b)->bytes, ctx->stream) != hipSuccess)
+            return bail(fail(VX_ERR_HIP, "hipMemsetAsync of LocDiT state failed"));
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return bail(fail(VX_ERR_HIP, "LocDiT init sync failed"));
+    *out = e;
+    return VX_OK;
+}
+
+int vx_locdit_destroy(vx_locdit *e) {
+    if (!e) return VX_OK;
+    (void)hipStreamSynchronize(e->ctx->stream);
+    free_all(e);
+    delete e;
+    return VX_OK;
+}
+
+int vx_locdit_estimate(vx_locdit *e, const float *x, const float *cond, const float *mu, float t, float dt,
+                       float *out) {
+    if (!e || !x || !out) return fail(VX_ERR_INVALID_ARG, "vx_locdit_estimate: null argument");
+    const vx_locdit_config &c = e->cfg;
+    const uint64_t n = (uint64_t)c.patch * c.feat_dim;
+    if (!std::isfinite(t) || !std::isfinite(dt))  // check_time (local.rs:563)
+        return fail(VX_ERR_INVALID_ARG, "LocDiT t/dt must be finite, got t=%g, dt=%g", t, dt);
+    VX_CHECK(check_finite(x, n, "LocDiT x"));
+    VX_CHECK(upload_inputs(e, cond, mu));
+    VX_CHECK(vx_upload(e->ctx, e->x, 0, x, n * 4u));
+    VX_CHECK(enqueue_inputs(e));
+    VX_CHECK(enqueue_time(e, t, dt));
+    VX_CHECK(enqueue_body(e, 1));
+    return vx_download(e->ctx, e->out, 0, out, n * 4u);
+}
+
+int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const vx_cfm_options *opt,
+                        const float *initial_x, float *out_patch, vx_cfm_result *res) {
+    if (!e || !opt || !out_patch) return fail(VX_ERR_INVALID_ARG, "vx_locdit_cfm_solve: null argument");
+    VX_CHECK(validate_options(*opt));
+    const vx_locdit_config &c = e->cfg;
+    const uint64_t n = (uint64_t)c.patch * c.feat_dim;
+    vx_ctx *ctx = e->ctx;
+    const double t0 = now_ms();
+    VX_CHECK(upload_inputs(e, cond, mu));
+    if (initial_x) {
+        VX_CHECK(check_finite(initial_x, n, "CFM initial x"));
+        VX_CHECK(vx_upload(ctx, e->x, 0, initial_x, n * 4u));
+    }
+    const uint32_t seed[2] = {(uint32_t)opt->seed, (uint32_t)(opt->seed >> 32)};
+    VX_CHECK(vx_upload(ctx, e->seed, 0, seed, 8u));
+    uint32_t calls = 0;
+    if (ctx->prof_enabled) {
+        VX_CHECK(enqueue_solve(e, *opt, initial_x != nullptr, &calls));
+    } else {
+        const int ix = initial_x ? 1 : 0;
+        if (!e->graph || !same_options(e->graph_opt, *opt) || e->graph_initial_x != ix) {
+            if (e->graph) {
+                vx_graph_free(ctx, e->graph);
+                e->graph = nullptr;
+            }
+            VX_CHECK(vx_graph_begin(ctx));
+            const int st = enqueue_solve(e, *opt, initial_x != nullptr, &calls);
+            vx_graph *g = nullptr;
+            const int st2 = vx_graph_end(ctx, &g);
+            if (st != VX_OK) {
+                if (g) vx_graph_free(ctx, g);
+                return st;
+            }
+            VX_CHECK(st2);
+            e->graph = g;
+            e->graph_opt = *opt;
+            e->graph_initial_x = ix;
+        }
+        std::vector<float> span;
+        VX_CHECK(time_span(opt->n_timesteps, opt->sway_sampling_coef, span));
+        calls = 2u * (uint32_t)(span.size() - 1u - std::min<size_t>(zero_init_steps(*opt, span.size()), span.size() - 1u));
+        VX_CHECK(vx_graph_launch(ctx, e->graph));
+    }
+    VX_CHECK(vx_download(ctx, e->x, 0, out_patch, n * 4u));
+    if (res) {
+        std::vector<float> span;
+        VX_CHECK(time_span(opt->n_timesteps, opt->sway_sampling_coef, span));
+        double sum = 0, sq = 0;
+        float mn = INFINITY, mx = -INFINITY;
+        for (uint64_t i = 0; i < n; ++i) {
+            sum += out_patch[i];
+            sq += (double)out_patch[i] * out_patch[i];
+            mn = std::min(mn, out_patch[i]);
+            mx = std::max(mx, out_patch[i]);
+        }
+        res->elapsed_ms = now_ms() - t0;
+        res->n_timesteps = opt->n_timesteps;
+        res->estimator_calls = calls;
+        res->zero_init_steps = zero_init_steps(*opt, span.size());
+        res->output_checksum = sum;
+        res->output_l2 = std::sqrt(sq);
+        res->output_min = mn;
+        res->output_max = mx;
+    }
+    return VX_OK;
+}
+
+// ------------------------------------------------------- CFM shader entry points
+int vx_cfm_noise(vx_ctx *ctx, vx_buf *x, const vx_cfm_noise_push *pc) {
+    if (!ctx || !pc) return fail(VX_ERR_INVALID_ARG, "vx_cfm_noise: null argument");
+    VX_CHECK(need_buf(x, (uint64_t)pc->n * 4u, "vx_cfm_noise x"));
+    ProfSpan sp(ctx, "local.cfm_noise");
+    return launch_cfm_noise(ctx->stream, F(x), pc->n, nullptr, ((uint64_t)pc->seed_hi << 32) | pc->seed_lo,
+                            pc->temperature);
+}
+
+int vx_cfm_cfg_euler(vx_ctx *ctx, vx_buf *x, const vx_buf *positive, const vx_buf *negative,
+                     const vx_cfm_euler_push *pc) {
+    if (!ctx || !pc) return fail(VX_ERR_INVALID_ARG, "vx_cfm_cfg_euler: null argument");
+    VX_CHECK(need_buf(x, (uint64_t)pc->n * 4u, "vx_cfm_cfg_euler x"));
+    VX_CHECK(need_buf(positive, (uint64_t)pc->n * 4u, "vx_cfm_cfg_euler positive"));
+    VX_CHECK(need_buf(negative, (uint64_t)pc->n * 4u, "vx_cfm_cfg_euler negative"));
+    ProfSpan sp(ctx, "local.cfm_cfg_euler");
+    return launch_cfm_cfg_euler(ctx->stream, F(x), static_cast<const float *>(positive->ptr),
+                                static_cast<const float *>(negative->ptr), pc->n, pc->dt, pc->cfg, pc->use_zero_star);
+}
+
+int vx_time_sinusoidal(vx_ctx *ctx, vx_buf *out, const vx_time_push *pc) {
+    if (!ctx || !pc) return fail(VX_ERR_INVALID_ARG, "vx_time_sinusoidal: null argument");
+    VX_CHECK(need_buf(out, (uint64_t)pc->dim * 4u, "vx_time_sinusoidal out"));
+    ProfSpan sp(ctx, "local.time_sinusoidal");
+    return launch_time_sinusoidal(ctx->stream, F(out), pc->dim, pc->t, nullptr, 0);
+}
+
+int vx_pack_locdit(vx_ctx *ctx, const vx_buf *mu1, const vx_buf *mu2, const vx_buf *time, const vx_buf *cond,
+                   const vx_buf *x, vx_buf *hidden, const vx_pack_locdit_push *pc) {
+    if (!ctx || !pc) return fail(VX_ERR_INVALID_ARG, "vx_pack_locdit: null argument");
+    const uint64_t H = pc->hidden, P = pc->patch_tokens;
+    VX_CHECK(need_buf(mu1, H * 4u, "vx_pack_locdit mu1"));
+    VX_CHECK(need_buf(mu2, H * 4u, "vx_pack_locdit mu2"));
+    VX_CHECK(need_buf(time, H * 4u, "vx_pack_locdit time"));
+    VX_CHECK(need_buf(cond, P * H * 4u, "vx_pack_locdit cond"));
+    VX_CHECK(need_buf(x, P * H * 4u, "vx_pack_locdit x"));
+    VX_CHECK(need_buf(hidden, (3u + 2u * P) * H * 4u, "vx_pack_locdit hidden"));
+    ProfSpan sp(ctx, "local.pack_locdit");
+    PackLocditArgs a;
+    a.mu[0] = static_cast<const float *>(mu1->ptr);
+    a.mu[1] = static_cast<const float *>(mu2->ptr);
+    a.time = static_cast<const float *>(time->ptr);
+    a.cond = static_cast<const float *>(cond->ptr);
+    a.x = static_cast<const float *>(x->ptr);
+    a.out = F(hidden);
+    a.hidden = pc->hidden;
+    a.n_mu = 2;
+    a.n_cond = pc->patch_tokens;
+    a.n_x = pc->patch_tokens;
+    a.zero_mu_mask = pc->zero_mu ? 1u : 0u;
+    return launch_pack_locdit(ctx->stream, a);
+}
+
+int vx_silu_inplace(vx_ctx *ctx, vx_buf *x, uint32_t n) {
+    if (!ctx) return fail(VX_ERR_INVALID_ARG, "vx_silu_inplace: null context");
+    VX_CHECK(need_buf(x, (uint64_t)n * 4u, "vx_silu_inplace x"));
+    return launch_silu_inplace(ctx->stream, F(x), n);
+}
+
+int vx_add_vectors(vx_ctx *ctx, vx_buf *a, const vx_buf *b, uint32_t n) {
+    if (!ctx) return fail(VX_ERR_INVALID_ARG, "vx_add_vectors: null context");
+    VX_CHECK(need_buf(a, (uint64_t)n * 4u, "vx_add_vectors a"));
+    VX_CHECK(need_buf(b, (uint64_t)n * 4u, "vx_add_vectors b"));
+    return launch_add_vectors(ctx->stream, F(a), static_cast<const float *>(b->ptr), n);
+}
+
+}  // extern "C"

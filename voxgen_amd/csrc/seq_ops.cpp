@@ -55,6 +55,132 @@ GemmSeg seg_of(const WRef &w, uint32_t rows, float *out, uint32_t ldo) {
 
 }  // namespace
 
+namespace vx {
+
+int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t bias_dtype, uint32_t rows,
+                       uint32_t cols, uint32_t tokens, const float *x, uint32_t in_base, uint32_t in_stride,
+                       float *y, uint32_t out_base, uint32_t out_stride, float alpha) {
+    if (!tokens || !rows) return VX_OK;
+    if (tokens == 1) {  // one token: the batch-1 matvec (matvec.comp / linear_bias.comp)
+        MatvecLaunch m;
+        m.w = w;
+        m.xl = x + in_base;
+        m.rows = rows;
+        m.cols = cols;
+        m.alpha = alpha;
+        m.epi = bias ? EPI_BIAS : EPI_STORE;
+        m.bias = bias;
+        m.bias_dtype = bias_dtype;
+        m.y = y + out_base;
+        return launch_matvec(s, m);
+    }
+    if (gemm_ok(w, cols, in_base, in_stride, tokens)) {
+        GemmArgs g;
+        g.wk = w.wt;
+        g.epi = GEPI_STORE;
+        g.xf32 = 1;
+        g.seg[0] = seg_of(w, rows, y + out_base, out_stride);
+        g.seg[0].bias = bias;
+        g.seg[0].bias_dtype = bias_dtype;
+        g.K = cols;
+        g.T = tokens;
+        g.xf = x + in_base;
+        g.ldx = in_stride;
+        g.alpha = alpha;
+        return launch_gemm(s, g);
+    }
+    SeqGenericArgs a;
+    a.raw = w.raw;
+    a.w_off = w.raw_offset;
+    a.dtype = w.dtype;
+    a.rows = rows;
+    a.cols = cols;
+    a.tokens = tokens;
+    a.x = x;
+    a.in_base = in_base;
+    a.in_stride = in_stride;
+    a.y = y;
+    a.out_base = out_base;
+    a.out_stride = out_stride;
+    a.bias = bias;
+    a.bias_dtype = bias_dtype;
+    a.alpha = alpha;
+    return launch_seq_linear_generic(s, a);
+}
+
+int enqueue_seq_qkv(hipStream_t s, const WRef w[3], const uint32_t rows[3], uint32_t cols, uint32_t tokens,
+                    const float *x, uint32_t in_base, uint32_t in_stride, float *const out[3],
+                    const uint32_t strides[3]) {
+    if (!tokens) return VX_OK;
+    bool all = tokens > 1 && w[0].wt == w[1].wt && w[0].wt == w[2].wt;
+    for (int i = 0; i < 3; ++i) all = all && gemm_ok(w[i], cols, in_base, in_stride, tokens);
+    if (all) {
+        GemmArgs g;
+        g.wk = w[0].wt;
+        g.epi = GEPI_STORE;
+        g.xf32 = 1;
+        for (int i = 0; i < 3; ++i) g.seg[i] = seg_of(w[i], rows[i], out[i], strides[i]);
+        g.nseg = 3;
+        g.K = cols;
+        g.T = tokens;
+        g.xf = x + in_base;
+        g.ldx = in_stride;
+        return launch_gemm(s, g);
+    }
+    for (int i = 0; i < 3; ++i)
+        VX_CHECK(enqueue_seq_linear(s, w[i], nullptr, 0, rows[i], cols, tokens, x, in_base, in_stride, out[i], 0,
+                                    strides[i], 1.f));
+    return VX_OK;
+}
+
+int enqueue_seq_swiglu(hipStream_t s, const WRef &g, const WRef &u, uint32_t rows, uint32_t cols, uint32_t tokens,
+                       const float *x, uint32_t in_base, uint32_t in_stride, float *y, uint32_t out_base,
+                       uint32_t out_stride) {
+    if (!tokens || !rows) return VX_OK;
+    if (tokens == 1) {
+        SwigluLaunch a;
+        a.g = g;
+        a.u = u;
+        a.x = x + in_base;
+        a.rows = rows;
+        a.cols = cols;
+        a.y = y + out_base;
+        return launch_swiglu(s, a);
+    }
+    if (g.wt == u.wt && gemm_ok(g, cols, in_base, in_stride, tokens) && gemm_ok(u, cols, in_base, in_stride, tokens)) {
+        GemmArgs a;
+        a.wk = g.wt;
+        a.epi = GEPI_SWIGLU;
+        a.xf32 = 1;
+        a.seg[0] = seg_of(g, rows, y + out_base, out_stride);
+        a.seg[1] = seg_of(u, rows, nullptr, 0);
+        a.nseg = 2;
+        a.K = cols;
+        a.T = tokens;
+        a.xf = x + in_base;
+        a.ldx = in_stride;
+        return launch_gemm(s, a);
+    }
+    SeqGenericArgs a;
+    a.raw = g.raw;
+    a.w_off = g.raw_offset;
+    a.w2_off = u.raw_offset;
+    a.dtype = g.dtype;
+    a.rows = rows;
+    a.cols = cols;
+    a.tokens = tokens;
+    a.x = x;
+    a.in_base = in_base;
+    a.in_stride = in_stride;
+    a.y = y;
+    a.out_base = out_base;
+    a.out_stride = out_stride;
+    a.swiglu = 1;
+    return launch_seq_linear_generic(s, a);
+}
+
+}  // namespace vx
+
 extern "C" {
 
 int vx_seq_linear_bias(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y,
@@ -71,41 +197,10 @@ int vx_seq_linear_bias(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_b
     }
     VX_CHECK(need_buf(x, span(pc->input_base, pc->tokens, pc->input_stride, pc->cols) * 4u, "vx_seq_linear_bias x"));
     VX_CHECK(need_buf(y, span(pc->output_base, pc->tokens, pc->output_stride, pc->rows) * 4u, "vx_seq_linear_bias y"));
-    if (!pc->tokens || !pc->rows) return VX_OK;
     ProfSpan sp(ctx, "local.seq_linear");
-    if (gemm_ok(w, pc->cols, pc->input_base, pc->input_stride, pc->tokens)) {
-        GemmArgs g;
-        g.wk = w.wt;
-        g.epi = GEPI_STORE;
-        g.xf32 = 1;
-        g.seg[0] = seg_of(w, pc->rows, F(y) + pc->output_base, pc->output_stride);
-        g.seg[0].bias = bias;
-        g.seg[0].bias_dtype = pc->bias_dtype;
-        g.K = pc->cols;
-        g.T = pc->tokens;
-        g.xf = CF(x) + pc->input_base;
-        g.ldx = pc->input_stride;
-        g.alpha = pc->alpha;
-        return launch_gemm(ctx->stream, g);
-    }
-    SeqGenericArgs a;
-    a.raw = model->raw;
-    a.w_off = pc->weight_offset;
-    a.dtype = pc->weight_dtype;
-    a.rows = pc->rows;
-    a.cols = pc->cols;
-    a.tokens = pc->tokens;
-    a.x = CF(x);
-    a.in_base = pc->input_base;
-    a.in_stride = pc->input_stride;
-    a.y = F(y);
-    a.out_base = pc->output_base;
-    a.out_stride = pc->output_stride;
-    a.has_bias = pc->has_bias;
-    a.bias_off = pc->bias_offset;
-    a.bias_dtype = pc->bias_dtype;
-    a.alpha = pc->alpha;
-    return launch_seq_linear_generic(ctx->stream, a);
+    return enqueue_seq_linear(ctx->stream, w, pc->has_bias ? bias : nullptr, pc->bias_dtype, pc->rows, pc->cols,
+                              pc->tokens, CF(x), pc->input_base, pc->input_stride, F(y), pc->output_base,
+                              pc->output_stride, pc->alpha);
 }
 
 int vx_seq_qkv(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *q, vx_buf *k, vx_buf *v,
@@ -126,39 +221,10 @@ int vx_seq_qkv(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *q, v
         VX_CHECK(need_buf(outs[i], span(0, pc->tokens, strides[i], rows[i]) * 4u, names[i]));
     }
     VX_CHECK(need_buf(x, span(pc->input_base, pc->tokens, pc->input_stride, pc->cols) * 4u, "vx_seq_qkv x"));
-    if (!pc->tokens) return VX_OK;
     ProfSpan sp(ctx, "local.seq_qkv");
-    bool all = w[0].wt == w[1].wt && w[0].wt == w[2].wt;
-    for (int i = 0; i < 3; ++i) all = all && gemm_ok(w[i], pc->cols, pc->input_base, pc->input_stride, pc->tokens);
-    if (all) {
-        GemmArgs g;
-        g.wk = w[0].wt;
-        g.epi = GEPI_STORE;
-        g.xf32 = 1;
-        for (int i = 0; i < 3; ++i) g.seg[i] = seg_of(w[i], rows[i], F(outs[i]), strides[i]);
-        g.nseg = 3;
-        g.K = pc->cols;
-        g.T = pc->tokens;
-        g.xf = CF(x) + pc->input_base;
-        g.ldx = pc->input_stride;
-        return launch_gemm(ctx->stream, g);
-    }
-    for (int i = 0; i < 3; ++i) {
-        SeqGenericArgs a;
-        a.raw = model->raw;
-        a.w_off = offs[i];
-        a.dtype = w[i].dtype;
-        a.rows = rows[i];
-        a.cols = pc->cols;
-        a.tokens = pc->tokens;
-        a.x = CF(x);
-        a.in_base = pc->input_base;
-        a.in_stride = pc->input_stride;
-        a.y = F(outs[i]);
-        a.out_stride = strides[i];
-        VX_CHECK(launch_seq_linear_generic(ctx->stream, a));
-    }
-    return VX_OK;
+    float *const o[3] = {F(q), F(k), F(v)};
+    return enqueue_seq_qkv(ctx->stream, w, rows, pc->cols, pc->tokens, CF(x), pc->input_base, pc->input_stride, o,
+                           strides);
 }
 
 int vx_seq_swiglu(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_seq_swiglu_push *pc) {
@@ -173,39 +239,9 @@ int vx_seq_swiglu(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y
     VX_CHECK(resolve_matrix(model, pc->up_weight_offset, du, pc->rows, pc->cols, &wu, "vx_seq_swiglu up"));
     VX_CHECK(need_buf(x, span(pc->input_base, pc->tokens, pc->input_stride, pc->cols) * 4u, "vx_seq_swiglu x"));
     VX_CHECK(need_buf(y, span(pc->output_base, pc->tokens, pc->output_stride, pc->rows) * 4u, "vx_seq_swiglu y"));
-    if (!pc->tokens || !pc->rows) return VX_OK;
     ProfSpan sp(ctx, "local.seq_swiglu");
-    if (gemm_ok(wg, pc->cols, pc->input_base, pc->input_stride, pc->tokens) &&
-        gemm_ok(wu, pc->cols, pc->input_base, pc->input_stride, pc->tokens)) {
-        GemmArgs g;
-        g.wk = wg.wt;
-        g.epi = GEPI_SWIGLU;
-        g.xf32 = 1;
-        g.seg[0] = seg_of(wg, pc->rows, F(y) + pc->output_base, pc->output_stride);
-        g.seg[1] = seg_of(wu, pc->rows, nullptr, 0);
-        g.nseg = 2;
-        g.K = pc->cols;
-        g.T = pc->tokens;
-        g.xf = CF(x) + pc->input_base;
-        g.ldx = pc->input_stride;
-        return launch_gemm(ctx->stream, g);
-    }
-    SeqGenericArgs a;
-    a.raw = model->raw;
-    a.w_off = pc->gate_weight_offset;
-    a.w2_off = pc->up_weight_offset;
-    a.dtype = dg;
-    a.rows = pc->rows;
-    a.cols = pc->cols;
-    a.tokens = pc->tokens;
-    a.x = CF(x);
-    a.in_base = pc->input_base;
-    a.in_stride = pc->input_stride;
-    a.y = F(y);
-    a.out_base = pc->output_base;
-    a.out_stride = pc->output_stride;
-    a.swiglu = 1;
-    return launch_seq_linear_generic(ctx->stream, a);
+    return enqueue_seq_swiglu(ctx->stream, wg, wu, pc->rows, pc->cols, pc->tokens, CF(x), pc->input_base,
+                              pc->input_stride, F(y), pc->output_base, pc->output_stride);
 }
 
 int vx_seq_silu_mul(vx_ctx *ctx, vx_buf *gate, const vx_buf *up, uint32_t n) {

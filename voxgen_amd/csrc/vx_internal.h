@@ -330,6 +330,7 @@ struct SeqRopeArgs {
     uint32_t ldq = 0, ldk = 0;
     const float *factors = nullptr;
     uint32_t pos_base = 0, q_heads = 0, kv_heads = 0, head_dim = 0;
+    uint32_t pos_period = 0;            // nonzero: row t is at position pos_base + t % pos_period
     float theta = 10000.f, scaling = 1.f;
     int q_inplace = 1;                  // write roped q back to q
     __half *qh = nullptr, *ql = nullptr;   // nullable roped q planes [T][ldqp]
@@ -359,11 +360,28 @@ struct SeqGenericArgs {
     uint32_t in_base = 0, in_stride = 0;
     float *y = nullptr;
     uint32_t out_base = 0, out_stride = 0;
-    uint32_t has_bias = 0, bias_off = 0, bias_dtype = 0;
+    const void *bias = nullptr;     // device pointer, nullable; f32 (bias_dtype 0) or f16 (1)
+    uint32_t bias_dtype = 0;
     float alpha = 1.f;
     int swiglu = 0;
 };
 int launch_seq_linear_generic(hipStream_t s, const SeqGenericArgs &a);
+
+// Token-batched projections (seq_ops.cpp) over resolved weights, choosing the
+// MFMA GEMM (f32 input split to hi/lo in the kernel), the decode matvec for a
+// single token, or the generic kernel. Strides and bases are in floats.
+// y[t][r] = alpha * (W[r] . x[t] + b[r])                     seq_linear_bias.comp
+int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t bias_dtype, uint32_t rows,
+                       uint32_t cols, uint32_t tokens, const float *x, uint32_t in_base, uint32_t in_stride,
+                       float *y, uint32_t out_base, uint32_t out_stride, float alpha);
+// q|k|v[t] = Wq|Wk|Wv . x[t]                                  seq_qkv.comp
+int enqueue_seq_qkv(hipStream_t s, const WRef w[3], const uint32_t rows[3], uint32_t cols, uint32_t tokens,
+                    const float *x, uint32_t in_base, uint32_t in_stride, float *const out[3],
+                    const uint32_t strides[3]);
+// y[t][r] = silu(Wg[r] . x[t]) * (Wu[r] . x[t])                 seq_swiglu.comp
+int enqueue_seq_swiglu(hipStream_t s, const WRef &g, const WRef &u, uint32_t rows, uint32_t cols, uint32_t tokens,
+                       const float *x, uint32_t in_base, uint32_t in_stride, float *y, uint32_t out_base,
+                       uint32_t out_stride);
 int launch_silu_mul(hipStream_t s, float *g, const float *u, uint32_t n);
 // dense_attn_scores / dense_softmax / dense_attn_values (which = 0 / 1 / 2).
 struct DenseAttnArgs {
@@ -371,8 +389,30 @@ struct DenseAttnArgs {
     float *s = nullptr, *out = nullptr;
     uint32_t tokens = 0, q_heads = 0, kv_heads = 0, head_dim = 0;
     uint32_t q_stride = 0, k_stride = 0, v_stride = 0, out_stride = 0, score_stride = 0;
+    // Independent sequences of `tokens` rows each (the CFG batch): sequence b
+    // starts b*tokens rows into q/k/v/out and b*tokens*q_heads score rows in.
+    uint32_t batch = 1;
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
+// ---------------------------------------------- CFM / LocDiT (kernels_cfm.hip)
+// Noise seed from dev_seed[0..1] (low, high word) when set, else from `seed`.
+int launch_cfm_noise(hipStream_t s, float *x, uint32_t n, const uint32_t *dev_seed, uint64_t seed, float temperature);
+int launch_cfm_cfg_euler(hipStream_t s, float *x, const float *pos, const float *neg, uint32_t n, float dt, float cfg,
+                         uint32_t zero_star);
+// t from t_dev[t_index] when t_dev is set.
+int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index);
+struct PackLocditArgs {
+    const float *mu[2] = {nullptr, nullptr};   // mu tokens (n_mu <= 2), [hidden] each
+    const float *time = nullptr;    // [hidden]
+    const float *cond = nullptr;    // [n_cond][hidden]
+    const float *x = nullptr;       // [n_x][hidden]
+    float *out = nullptr;           // [batch][n_mu + 1 + n_cond + n_x][hidden]
+    uint32_t hidden = 0, n_mu = 0, n_cond = 0, n_x = 0, batch = 1;
+    uint32_t zero_mu_mask = 0, zero_cond_mask = 0;
+};
+int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a);
+int launch_silu_inplace(hipStream_t s, float *x, uint32_t n);
+int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n);
 // Embedding rows of n device token ids into out[t][ldo] (bit-exact gather).
 int launch_seq_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, uint32_t dtype,
                          uint32_t cols, const uint32_t *tokens, uint32_t n, uint32_t vocab, float alpha,

@@ -206,3 +206,63 @@ def kv_cache_fill(layers: int, context: int, kv_dim: int, filled: int, seed: int
         v = normal_f16(layers * filled * kv_dim, seed).reshape(layers, filled, kv_dim)
         c[:, :filled, :] = v
     return c
+
+
+def locdit_config(layers=12, hidden=1024, q_heads=16, kv_heads=2, head_dim=128, ffn=4096, feat_dim=64,
+                  patch=4, n_mu=2, n_cond=None, cond_raw=0, uncond_zero_cond=0, eps=1e-6, theta=10000.0,
+                  rope_scaling=1.0) -> dict:
+    """vx_locdit_config fields. Defaults are the VoxCPM2 LocDiT contract
+    (LocalConfig::from_gguf, local.rs:85-92): 12 x 1024, 16/2 x 128, ffn 4096,
+    patch 4 x 64, mu1 + mu2 + time + 4 condition + 4 latent tokens."""
+    return dict(hidden=hidden, layers=layers, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, ffn=ffn,
+                feat_dim=feat_dim, patch=patch, n_mu=n_mu, n_cond=patch if n_cond is None else n_cond,
+                cond_raw=cond_raw, uncond_zero_cond=uncond_zero_cond, rms_epsilon=eps, rope_theta=theta,
+                rope_scaling=rope_scaling)
+
+
+def build_locdit(cfg: dict, seed: int = 0x5EED0040, std: float = 0.02) -> SynthModel:
+    """Synthetic LocDiT tensors with the names and shapes validate_tensors checks
+    (local.rs:127-168): F16 matrices N(0, std), F32 biases N(0, std), F32 norm
+    gains N(1, 0.02), plus rope_factors_short.weight (ones) so the same region
+    can serve as the RoPE-factor model."""
+    H, F, hd = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QD, KD, FD = cfg["q_heads"] * hd, cfg["kv_heads"] * hd, cfg["feat_dim"]
+    reg = Region()
+    reg.add("rope_factors_short.weight", abi.DTYPE_F32, (hd // 2,))
+
+    def lin(name, cols, rows):
+        reg.add(name + ".weight", abi.DTYPE_F16, (cols, rows))
+        reg.add(name + ".bias", abi.DTYPE_F32, (rows,))
+
+    lin("locdit.in_proj", FD, H)
+    if not cfg["cond_raw"]:
+        lin("locdit.cond_proj", FD, H)
+    lin("locdit.out_proj", H, FD)
+    reg.add("locdit.norm.weight", abi.DTYPE_F32, (H,))
+    for p in ("locdit.time_mlp", "locdit.delta_time_mlp"):
+        lin(p + ".linear_1", H, H)
+        lin(p + ".linear_2", H, H)
+    for l in range(cfg["layers"]):
+        p = f"locdit.blk.{l}."
+        reg.add(p + "attn_norm.weight", abi.DTYPE_F32, (H,))
+        reg.add(p + "attn_q.weight", abi.DTYPE_F16, (H, QD))
+        reg.add(p + "attn_k.weight", abi.DTYPE_F16, (H, KD))
+        reg.add(p + "attn_v.weight", abi.DTYPE_F16, (H, KD))
+        reg.add(p + "attn_output.weight", abi.DTYPE_F16, (QD, H))
+        reg.add(p + "ffn_norm.weight", abi.DTYPE_F32, (H,))
+        reg.add(p + "ffn_gate.weight", abi.DTYPE_F16, (H, F))
+        reg.add(p + "ffn_up.weight", abi.DTYPE_F16, (H, F))
+        reg.add(p + "ffn_down.weight", abi.DTYPE_F16, (F, H))
+    data = np.zeros((reg.size + 255) // 256 * 256, np.uint8)
+    for i, t in enumerate(reg.tensors):
+        s = derive_seed(seed, i)
+        n = int(np.prod(t.dims))
+        if t.name.startswith("rope_factors"):
+            data[t.offset:t.offset + t.nbytes].view(np.float32)[:] = 1.0
+        elif t.ggml_type == abi.DTYPE_F16:
+            lib().vs_fill_normal_f16(_ptr(data, t.offset), n, s, 0.0, std)
+        elif t.name.endswith("norm.weight"):
+            lib().vs_fill_normal_f32(_ptr(data, t.offset), n, s, 1.0, 0.02)
+        else:
+            lib().vs_fill_normal_f32(_ptr(data, t.offset), n, s, 0.0, std)
+    return SynthModel(data, reg.tensors, dict(cfg), {})
