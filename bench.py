@@ -18,6 +18,8 @@ Prints one JSON line with:
                (MFMA projections, causal attention over the cache): wall time and
                each kernel's HIP-event span, with the projection GEMMs' algorithmic
                TFLOP/s against the 2.5 PFLOP/s dense f16 MFMA peak
+  cfm          the LocDiT flow-matching solve (8 layers, hidden 1024, CFG batch
+               2, 10 timesteps): solve time and weight-streaming GB/s
 
 `--copy-calibration` instead runs one plain copy kernel of known size (the
 reference point for the FETCH_SIZE / WRITE_SIZE counters).
@@ -85,10 +87,12 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=8, help="passes over the 28 layers per kernel timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target length of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference"])
+    ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference", "persistent"])
     ap.add_argument("--prefill-tokens", type=int, default=384,
                     help="tokens of the token-batched prefill leg (0 skips it)")
     ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--cfm-reps", type=int, default=5, help="CFM solves timed (0 skips the CFM leg)")
+    ap.add_argument("--cfm-only", action="store_true", help="run only the LocDiT CFM leg (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the token-batched prefill leg (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -173,6 +177,53 @@ def prefill_leg(ctx, eng, cfg, T, reps):
             "per_kernel": per}
 
 
+def cfm_leg(ctx, reps):
+    """The LocDiT flow-matching solve at the benchmark shape: hidden 1024, 8 layers,
+    16 x 64 heads, FFN 4096, F16 weights N(0, 0.02); 32 condition rows N(0,1) +
+    the time token + 4 latent rows of 64; CFG batch 2 (the unconditional pass
+    zeroes the condition rows); 10 timesteps, cfg 2.0, CFG-Zero*, seeded noise.
+    Each Euler step runs both passes as one batch, so the step streams the
+    weights once."""
+    from voxgen_amd import synth
+    from voxgen_amd.locdit import CfmOptions, LocDit
+    from voxgen_amd.runtime import Model
+    cfg = synth.locdit_config(layers=8, q_heads=16, kv_heads=16, head_dim=64, n_mu=0, n_cond=32, cond_raw=1,
+                              uncond_zero_cond=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0014)
+    model = Model(ctx, m.data, m.tensors)
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    cond = synth.normal_f32(32 * 1024, 0x5EED0015)
+    opt = CfmOptions(n_timesteps=10, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0, seed=42,
+                     use_cfg_zero_star=True)
+    out, res = loc.cfm_solve(cond, None, opt)            # captures the graph
+    times = []
+    for i in range(reps):
+        t0 = time.perf_counter()
+        out, res = loc.cfm_solve(cond, None, CfmOptions(seed=42 + i))
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    loc.cfm_solve(cond, None, opt)
+    prof = ctx.prof_snapshot()
+    ctx.prof_enable(False)
+    loc.close()
+    model.free()
+    steps = res["estimator_calls"] // 2
+    per_layer = 4 * 1024 * 1024 * 2 + 3 * 1024 * 4096 * 2          # q,k,v,o + gate,up,down (F16)
+    step_bytes = 8 * per_layer + 4 * 1024 * 1024 * 2 + 2 * 64 * 1024 * 2   # + time MLPs, in/out proj
+    solve_bytes = steps * step_bytes
+    gbps = solve_bytes / (ms * 1e-3) / 1e9
+    log(f"cfm solve: {ms:.3f} ms for {steps} Euler steps x 2 passes; {solve_bytes / 1e9:.2f} GB of weights "
+        f"-> {gbps:.0f} GB/s")
+    per = {k: dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"], total_ms=round(v["total_ms"], 4))
+           for k, v in prof.items()}
+    return {"workload": "locdit_f16_cfm_8L_h1024_16x64_cond32_cfg2_batch2_10steps", "ms": round(ms, 3),
+            "euler_steps": steps, "estimator_calls": res["estimator_calls"],
+            "weight_bytes_per_solve": int(solve_bytes), "achieved_GBps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "per_kernel_eager": per}
+
+
 def synth_tokens(n, cfg):
     from voxgen_amd import synth
     return synth.uniform_u32(n, 0x5EED0013, cfg["vocab_size"]).astype(np.uint32)
@@ -205,6 +256,13 @@ def main():
     eng = BaseLmEngine(ctx, model, cfg, exec_mode=args.mode, strict_geometry=True)
     log(f"device {info['name']} {info['arch']} CUs={info['compute_units']}; model on device "
         f"{model.device_bytes / 1e9:.2f} GB")
+    if args.cfm_only:
+        cf = cfm_leg(ctx, args.cfm_reps)
+        eng.close()
+        model.free()
+        ctx.close()
+        print(json.dumps({"cfm": cf}), flush=True)
+        return
     if args.prefill_only:
         pf = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
         eng.close()
@@ -269,6 +327,7 @@ def main():
         prefill = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
     eng.close()
     model.free()
+    cfm = cfm_leg(ctx, args.cfm_reps) if args.cfm_reps else None
     ctx.close()
 
     line = {
@@ -298,6 +357,7 @@ def main():
         "per_kernel": per_kernel,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "cfm": cfm,
         "device": f"{info['name']} ({info['arch']})",
     }
     print(json.dumps(line), flush=True)

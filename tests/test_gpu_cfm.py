@@ -77,7 +77,8 @@ def test_cfm_solve_graph_replay_seeds_and_initial_x(ctx, ref_shape):
     a1, _ = loc.cfm_solve(cond, mu, opt)
     b1, _ = loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=3, seed=8))   # same graph, new seed
     a2, _ = loc.cfm_solve(cond, mu, opt)
-    assert np.array_equal(a1, a2) and not np.allclose(a1, b1)
+    # Replays agree to float rounding (split-K projections accumulate with atomics).
+    assert rel_l2(a2, a1) < 1e-5 and rel_l2(b1, a1) > 0.1
     assert rel_l2(b1, o.cfm_solve(cond, mu, n_timesteps=3, seed=8)) < 1e-4
     x0 = synth.normal_f32(256, 99)
     c1, _ = loc.cfm_solve(cond, mu, opt, initial_x=x0)

@@ -1,4 +1,5 @@
-"""BaseLM engine parity (graph, fused-eager and reference op order) against the oracle.
+"""BaseLM engine parity (graph, fused-eager, reference op order and the persistent
+one-kernel step) against the oracle.
 
 One decoder layer at context 512 (the single-layer benchmark workload), short
 multi-layer sequences from position 0 through every decode entry point, error
@@ -14,7 +15,7 @@ from voxgen_amd.baselm import BaseLmEngine
 from voxgen_amd.runtime import Model
 
 pytestmark = pytest.mark.gpu
-MODES = ["graph", "fused", "reference"]
+MODES = ["graph", "fused", "reference", "persistent"]
 
 
 def kv_bits(layers, ctxlen, filled, seed):
@@ -189,15 +190,18 @@ def full_model(ctx):
 
 def test_full_stack_from_position_zero(ctx, full_model):
     cfg, m, model, o = full_model
-    eng = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=True)
     toks = [int(t) for t in synth.uniform_u32(3, 0x5EED0006, cfg["vocab_size"])]
+    wants, tops = [], []
     for pos, t in enumerate(toks):
-        r = eng.decode_token(t, top_k=5)
-        want = o.decode_token(t, pos, logits=True)
-        assert rel_l2(eng.output(), want) < 5e-3, pos
-        top_want = list(np.argsort(-o.logits, kind="stable")[:5])
-        assert [t for t, _ in r.top_logits][:3] == top_want[:3]
-    eng.close()
+        wants.append(o.decode_token(t, pos, logits=True))
+        tops.append(list(np.argsort(-o.logits, kind="stable")[:5]))
+    for mode in ("graph", "persistent"):
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=True)
+        for pos, t in enumerate(toks):
+            r = eng.decode_token(t, top_k=5)
+            assert rel_l2(eng.output(), wants[pos]) < 5e-3, (mode, pos)
+            assert [t for t, _ in r.top_logits][:3] == tops[pos][:3], mode
+        eng.close()
 
 
 def test_full_stack_decode_at_position_256(ctx, full_model):
@@ -208,7 +212,7 @@ def test_full_stack_decode_at_position_256(ctx, full_model):
     o.kv_k[:] = kk
     o.kv_v[:] = vv
     wants = [o.decode_token(t, 256 + i) for i, t in enumerate(toks)]
-    for mode in ("graph", "reference"):
+    for mode in ("graph", "reference", "persistent"):
         eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=True)
         eng.buffer("kv_k").upload(kk)
         eng.buffer("kv_v").upload(vv)
@@ -217,3 +221,39 @@ def test_full_stack_decode_at_position_256(ctx, full_model):
             eng.decode_token_gpu_only(t)
             assert rel_l2(eng.output(), w) < 5e-3, mode
         eng.close()
+
+
+def test_persistent_mode_matches_graph_over_a_sequence(ctx, two_layers):
+    """Graph and persistent modes through every decode entry point, step for step."""
+    cfg, m, model = two_layers
+    toks = [int(t) for t in synth.uniform_u32(10, 0x5EED0009, 2048)]
+    outs = {}
+    for mode in ("graph", "persistent"):
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=False)
+        got = []
+        eng.decode_tokens_gpu_only(toks[:5])
+        got.append(eng.output())
+        for t in toks[5:8]:
+            eng.decode_token_gpu_only(t)
+            got.append(eng.output())
+        r = eng.prefill_tokens(toks[8:], top_k_last=4)
+        got.append(eng.output())
+        got.append(eng.buffer("kv_k").download(np.uint16, 2 * 64 * 256).view(np.float16)[: 2 * 64 * 256])
+        outs[mode] = (got, [t for t, _ in r.top_logits])
+        prof = eng.profile_steps([1, 2]) if mode == "persistent" else None
+        if prof is not None:
+            assert prof["baselm.layers"]["calls"] == 2 and "baselm.qkv" not in prof
+        eng.close()
+    for a, b in zip(outs["graph"][0], outs["persistent"][0]):
+        assert rel_l2(b.astype(np.float32), a.astype(np.float32)) < 1e-3
+    assert outs["graph"][1] == outs["persistent"][1]
+
+
+def test_persistent_mode_rejects_other_geometry(ctx):
+    cfg = synth.baselm_config(layers=1, hidden=1024, ffn=3072, vocab=512, q_heads=8, active_context=32)
+    m = synth.build_baselm(cfg, seed=0x5EED000A)
+    model = Model(ctx, m.data, m.tensors)
+    with pytest.raises(abi.VxError) as e:
+        BaseLmEngine(ctx, model, cfg, exec_mode="persistent", strict_geometry=False)
+    assert e.value.name == "VX_ERR_UNSUPPORTED"
+    model.free()

@@ -25,7 +25,7 @@ STATUS = {
 STATUS_CODE = {v: k for k, v in STATUS.items()}
 
 DTYPE_F32, DTYPE_F16, DTYPE_Q8_0 = 0, 1, 8
-EXEC_GRAPH, EXEC_FUSED, EXEC_REFERENCE = 0, 1, 2
+EXEC_GRAPH, EXEC_FUSED, EXEC_REFERENCE, EXEC_PERSISTENT = 0, 1, 2, 3
 BUF = dict(HIDDEN=0, NORM=1, Q=2, K=3, V=4, ATTENTION=5, GATE=6, BRANCH=7, LOGITS=8,
            SCORES=9, KV_K=10, KV_V=11, POSITION=12)
 

@@ -14,7 +14,8 @@ import numpy as np
 from . import abi
 from .runtime import Buffer, Context, Model
 
-EXEC_MODES = {"graph": abi.EXEC_GRAPH, "fused": abi.EXEC_FUSED, "reference": abi.EXEC_REFERENCE}
+EXEC_MODES = {"graph": abi.EXEC_GRAPH, "fused": abi.EXEC_FUSED, "reference": abi.EXEC_REFERENCE,
+              "persistent": abi.EXEC_PERSISTENT}
 
 
 def config_struct(cfg: dict) -> abi.BaseLmConfig:
@@ -59,11 +60,12 @@ class BaseLmEngine:
         abi.call("vx_baselm_create", ctx.handle, model.handle, C.byref(config_struct(config)),
                  C.byref(opt), C.byref(h))
         self.handle = h.value
+        ctx.register(self)
 
     def close(self) -> None:
-        if self.handle:
+        if self.handle and self.ctx.handle:   # a closed context already released the device
             abi.load().vx_baselm_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:

@@ -5,6 +5,8 @@
 // F16 rows a multiple of 128, 16-byte aligned input rows -- and on the generic
 // one-wave-per-output kernel otherwise. Every entry point checks the push
 // extents against the model's tensor table and the bound buffers first.
+#include <algorithm>
+
 #include "vx_internal.h"
 
 using namespace vx;
@@ -37,6 +39,31 @@ bool gemm_ok(const WRef &w, uint32_t cols, uint32_t in_base, uint32_t in_stride,
     const bool layout = (w.wt == WT_Q8 && w.ptr && cols % 1024u == 0) || (w.wt == WT_F16 && cols % 128u == 0);
     const bool aligned = in_base % 4u == 0 && (tokens <= 1 || in_stride % 4u == 0);
     return layout && aligned;
+}
+
+// Compute units of the current device (cached per device).
+uint32_t device_cus() {
+    static uint32_t cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = (uint32_t)n;
+    }
+    return cus[dev];
+}
+
+// Split-K factor that brings a projection of `n_tiles` x ceil(T/64) tiles to
+// about one workgroup per CU (k-stages of 128 columns; at most 8 splits).
+uint32_t split_for(uint32_t n_tiles, uint32_t tokens, uint32_t K) {
+    const uint32_t tiles = n_tiles * ((tokens + 63u) / 64u);
+    const uint32_t cus = device_cus();
+    if (tiles >= cus) return 1u;
+    uint32_t ks = (cus + tiles - 1u) / tiles;
+    ks = std::min<uint32_t>(ks, 8u);
+    ks = std::min<uint32_t>(ks, std::max<uint32_t>(1u, K / 128u));
+    return ks;
 }
 
 GemmSeg seg_of(const WRef &w, uint32_t rows, float *out, uint32_t ldo) {
@@ -87,6 +114,11 @@ int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t 
         g.xf = x + in_base;
         g.ldx = in_stride;
         g.alpha = alpha;
+        // Few tiles (a short token batch): split K and accumulate with atomics into a
+        // zeroed output, when the output rows are dense so they can be cleared whole.
+        if (out_stride == rows) g.ksplit = split_for((rows + 127u) / 128u, tokens, cols);
+        if (g.ksplit > 1)
+            VX_CHECK(launch_fill_u32(s, reinterpret_cast<uint32_t *>(y + out_base), 0u, (uint64_t)tokens * rows));
         return launch_gemm(s, g);
     }
     SeqGenericArgs a;
@@ -125,6 +157,13 @@ int enqueue_seq_qkv(hipStream_t s, const WRef w[3], const uint32_t rows[3], uint
         g.T = tokens;
         g.xf = x + in_base;
         g.ldx = in_stride;
+        if (strides[0] == rows[0] && strides[1] == rows[1] && strides[2] == rows[2]) {
+            const uint32_t nt = (rows[0] + 127u) / 128u + (rows[1] + 127u) / 128u + (rows[2] + 127u) / 128u;
+            g.ksplit = split_for(nt, tokens, cols);
+        }
+        if (g.ksplit > 1)
+            for (int i = 0; i < 3; ++i)
+                VX_CHECK(launch_fill_u32(s, reinterpret_cast<uint32_t *>(out[i]), 0u, (uint64_t)tokens * rows[i]));
         return launch_gemm(s, g);
     }
     for (int i = 0; i < 3; ++i)

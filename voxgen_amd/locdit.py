@@ -51,11 +51,12 @@ class LocDit:
                  1 if strict_geometry else 0, C.byref(h))
         self.handle = h.value
         self._keep = (model, rm)
+        ctx.register(self)
 
     def close(self) -> None:
-        if self.handle:
+        if self.handle and self.ctx.handle:   # a closed context already released the device
             abi.load().vx_locdit_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:

@@ -10,6 +10,8 @@ import ctypes as C
 from dataclasses import dataclass
 from typing import Iterable, Sequence
 
+import weakref
+
 import numpy as np
 
 from . import abi
@@ -112,13 +114,21 @@ class Context:
 
     def __init__(self, device: int = 0):
         self.handle = None
+        # Engines created on this context (BaseLmEngine, LocDit): closed before the
+        # context itself, whatever order the interpreter finalises objects in.
+        self._engines = weakref.WeakSet()
         h = abi.CTX()
         abi.call("vx_init", device, C.byref(h))
         self.handle = h.value
         self.device = device
 
+    def register(self, engine) -> None:
+        self._engines.add(engine)
+
     def close(self) -> None:
         if self.handle:
+            for e in list(self._engines):
+                e.close()
             abi.load().vx_destroy(self.handle)
             self.handle = None
 
