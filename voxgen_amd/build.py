@@ -40,11 +40,19 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
+# Per-file device flags. The prefill GEMM keeps its MFMA accumulators in
+# VGPRs: its per-block scale FMAs read them, and accumulators in AGPRs would cost
+# a v_accvgpr_read per element.
+FILE_FLAGS = {
+    "kernels_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path) -> Path:
     OBJ.mkdir(parents=True, exist_ok=True)
     obj = OBJ / (src.name + ".o")
     # hipcc treats .cpp as HIP source too; both get the gfx950 device flags.
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     _run(cmd)
     return obj
 

@@ -60,6 +60,15 @@ struct vx_baselm {
     vx_buf *pf_h = nullptr, *pf_xh = nullptr, *pf_xl = nullptr, *pf_ah = nullptr, *pf_al = nullptr;
     vx_buf *pf_qh = nullptr, *pf_ql = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
     vx_buf *pf_tok = nullptr;
+    vx_buf *pf_ws = nullptr;   // split-K partials of the residual projections [kPrefillMaxSplit][cap][H]
+    // Q8_0 weights in the prefill-GEMM layout (built by the first batched prefill
+    // that can use them; empty when some projection is not Q8_0).
+    struct PrefillLayer {
+        PrefillMatrix q, k, v, o, gu, down;
+    };
+    std::vector<PrefillLayer> pw;
+    vx_buf *pw_arena = nullptr;
+    bool pw_tried = false;
     // Persistent decode step: per-layer weight table, phase counters, sticky
     // error word, attention partials.
     vx_buf *ps_layers = nullptr, *ps_cnt = nullptr, *ps_err = nullptr, *ps_part = nullptr;
@@ -172,12 +181,14 @@ void free_all(vx_baselm *e) {
                        &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table,
                        &e->pf_h, &e->pf_xh,    &e->pf_xl,  &e->pf_ah,    &e->pf_al,     &e->pf_qh,
                        &e->pf_ql, &e->pf_q,    &e->pf_k,   &e->pf_v,     &e->pf_tok,    &e->ps_layers,
-                       &e->ps_cnt, &e->ps_err, &e->ps_part, &e->ps_trace};
+                       &e->ps_cnt, &e->ps_err, &e->ps_part, &e->ps_trace, &e->pw_arena, &e->pf_ws};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
     }
     e->pf_cap = 0;
+    e->pw.clear();
+    e->pw_tried = false;
 }
 
 inline float *F(vx_buf *b) { return static_cast<float *>(b->ptr); }
@@ -381,7 +392,7 @@ int enqueue_persistent(vx_baselm *e, bool with_embedding, bool logits) {
         a.head_cnt = U(e->ps_cnt) + (uint64_t)c.block_count * kPersistPhases * kPersistCntStride;
         a.err = U(e->ps_err);
         if (ctx->prof_enabled && !ctx->capturing) {
-            const uint64_t bytes = (uint64_t)e->ps_grid * c.block_count * kPersistPhases * 4u * 8u;
+            const uint64_t bytes = (uint64_t)kPersistGroups * e->ps_grid * c.block_count * kPersistPhases * 4u * 8u;
             if (!e->ps_trace) VX_CHECK(alloc(ctx, bytes, &e->ps_trace));
             a.trace = static_cast<unsigned long long *>(e->ps_trace->ptr);
         }
@@ -397,13 +408,14 @@ int enqueue_persistent(vx_baselm *e, bool with_embedding, bool logits) {
 }
 
 // Profile entries of one persistent step from its phase timeline (after a sync):
-// per phase, the mean over workgroups of the wait and of the work after it, and
+// per phase, the mean over the workgroups that ran it of the wait and of the work
+// after it, and
 // the whole kernel from the first phase start to the last completion.
 int collect_persistent_trace(vx_baselm *e) {
     if (!e->ps_trace) return VX_OK;
     vx_ctx *ctx = e->ctx;
     const uint32_t G = e->ps_grid, P = e->cfg.block_count * kPersistPhases;
-    std::vector<unsigned long long> t((size_t)G * P * 4u);
+    std::vector<unsigned long long> t((size_t)kPersistGroups * G * P * 4u);
     VX_CHECK(vx_download(ctx, e->ps_trace, 0, t.data(), t.size() * 8u));
     int khz = 0;
     VX_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device));
@@ -421,7 +433,8 @@ int collect_persistent_trace(vx_baselm *e) {
     unsigned long long first = ~0ull, last = 0;
     for (uint32_t p = 0; p < P; ++p) {
         double wait = 0.0, work = 0.0;
-        for (uint32_t g = 0; g < G; ++g) {
+        const uint32_t g0 = (p % kPersistGroups) * G;   // the group that ran phase p
+        for (uint32_t g = g0; g < g0 + G; ++g) {
             const unsigned long long *r = &t[((size_t)g * P + p) * 4u];
             wait += (double)(long long)(r[1] - r[0]);
             work += (double)(long long)(r[2] - r[1]);
@@ -459,7 +472,9 @@ int setup_persistent(vx_baselm *e) {
                     c.embedding_length, c.feed_forward_length, c.head_dim, cus);
     int per_cu = 0;
     VX_CHECK(persistent_occupancy(&per_cu));
-    if (per_cu < 1) return fail(VX_ERR_UNSUPPORTED, "persistent decode kernel does not fit on a CU");
+    if (per_cu < (int)kPersistGroups)
+        return fail(VX_ERR_UNSUPPORTED, "persistent decode kernel: %d workgroups fit on a CU, %u needed", per_cu,
+                    kPersistGroups);
     std::vector<PLayer> table(c.block_count);
     for (uint32_t l = 0; l < c.block_count; ++l) {
         const Layer &L = e->layers[l];
@@ -634,24 +649,27 @@ int run_step(vx_baselm *e, bool with_embedding, uint32_t token, bool logits) {
 // This computes what prefill_tokens (baselm.rs:823-839) computes one token at a
 // time: the same KV-cache rows and the same final state, to rounding.
 constexpr uint32_t kPrefillChunk = 512;
+constexpr uint32_t kPrefillMaxSplit = 8;   // split-K factor bound (pick_split)
 
 int ensure_prefill_work(vx_baselm *e) {
     if (e->pf_cap) return VX_OK;
     const vx_baselm_config &c = e->cfg;
     const uint32_t cap = std::min<uint32_t>(kPrefillChunk, c.active_context_length);
     const uint64_t H = c.embedding_length, F = c.feed_forward_length, KV = c.kv_dim, T = cap;
+    const uint64_t Tp = (T + 127u) / 128u * 128u;   // GEMM input planes: whole 128-token tiles
     vx_ctx *ctx = e->ctx;
     VX_CHECK(alloc(ctx, T * H * 4u, &e->pf_h));
-    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_xh));
-    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_xl));
-    VX_CHECK(alloc(ctx, T * F * 2u, &e->pf_ah));
-    VX_CHECK(alloc(ctx, T * F * 2u, &e->pf_al));
+    VX_CHECK(alloc(ctx, Tp * H * 2u, &e->pf_xh));
+    VX_CHECK(alloc(ctx, Tp * H * 2u, &e->pf_xl));
+    VX_CHECK(alloc(ctx, Tp * F * 2u, &e->pf_ah));
+    VX_CHECK(alloc(ctx, Tp * F * 2u, &e->pf_al));
     VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_qh));
     VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_ql));
     VX_CHECK(alloc(ctx, T * H * 4u, &e->pf_q));
     VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_k));
     VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_v));
     VX_CHECK(alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->pf_tok));
+    VX_CHECK(alloc(ctx, (uint64_t)kPrefillMaxSplit * T * H * 4u, &e->pf_ws));
     e->pf_cap = cap;
     return VX_OK;
 }
@@ -671,12 +689,58 @@ GemmSeg gemm_seg(const WRef &w, uint32_t rows, float *out, uint32_t ldo) {
 }
 
 // Split-K factor that brings a projection to about one workgroup per CU.
-uint32_t pick_split(const vx_baselm *e, uint32_t n_tiles, uint32_t T, uint32_t K) {
-    const uint32_t tiles = n_tiles * ((T + 63u) / 64u);
+// Repack every layer's Q8_0 projections into the prefill-GEMM layout (once;
+// about 53 MB per layer at the VoxCPM2 geometry). Left empty, so that prefill
+// uses the general GEMM, when a projection is not Q8_0.
+int ensure_prefill_weights(vx_baselm *e) {
+    if (e->pw_tried) return VX_OK;
+    e->pw_tried = true;
+    const vx_baselm_config &c = e->cfg;
+    const uint32_t nH = c.embedding_length, nF = c.feed_forward_length, nKV = c.kv_dim;
+    for (const Layer &L : e->layers) {
+        const WRef *m[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+        for (const WRef *w : m)
+            if (w->dtype != VX_DTYPE_Q8_0 || !w->raw) return VX_OK;
+    }
+    if (nH % 32u || nF % 32u) return VX_OK;
+    const uint64_t per_layer = prefill_matrix_bytes(nH, nH) + 2u * prefill_matrix_bytes(nKV, nH) +
+                               prefill_matrix_bytes(nH, nH) + prefill_matrix_bytes(2u * nF, nH) +
+                               prefill_matrix_bytes(nH, nF) + 6u * 256u;
+    VX_CHECK(alloc(e->ctx, per_layer * c.block_count, &e->pw_arena));
+    uint8_t *cur = static_cast<uint8_t *>(e->pw_arena->ptr);
+    hipStream_t s = e->ctx->stream;
+    auto place = [&](PrefillMatrix &pm, const WRef &w0, const WRef *w1, uint32_t rows, uint32_t K) {
+        const uint32_t rows_out = w1 ? 2u * rows : rows;
+        pm.rows_pad = (rows_out + 127u) / 128u * 128u;
+        pm.q = reinterpret_cast<int8_t *>(cur);
+        pm.d = reinterpret_cast<float *>(cur + (uint64_t)pm.rows_pad * K);
+        cur += (prefill_matrix_bytes(rows_out, K) + 255u) / 256u * 256u;
+        return launch_repack_prefill(s, w0.raw, w0.raw_offset, w1 ? w1->raw_offset : 0u, rows, K, w1 ? 1 : 0, pm.q,
+                                     pm.d);
+    };
+    e->pw.resize(c.block_count);
+    for (uint32_t l = 0; l < c.block_count; ++l) {
+        const Layer &L = e->layers[l];
+        vx_baselm::PrefillLayer &P = e->pw[l];
+        int st = VX_OK;
+        if ((st = place(P.q, L.q, nullptr, nH, nH)) || (st = place(P.k, L.k, nullptr, nKV, nH)) ||
+            (st = place(P.v, L.v, nullptr, nKV, nH)) || (st = place(P.o, L.o, nullptr, nH, nH)) ||
+            (st = place(P.gu, L.gate, &L.up, nF, nH)) || (st = place(P.down, L.down, nullptr, nH, nF))) {
+            e->pw.clear();
+            return st;
+        }
+    }
+    return VX_OK;
+}
+
+// Split-K factor for a projection of n_tiles 128-row tiles and tt-token tiles:
+// enough workgroups to cover the CUs, at least four 32-column blocks per split.
+uint32_t pick_split(const vx_baselm *e, uint32_t tt, uint32_t n_tiles, uint32_t T, uint32_t K) {
+    const uint32_t tiles = n_tiles * ((T + tt - 1u) / tt);
     const uint32_t cus = e->ctx->props.multiProcessorCount > 0 ? (uint32_t)e->ctx->props.multiProcessorCount : 256u;
     uint32_t ks = (cus + tiles - 1u) / tiles;
-    ks = std::min<uint32_t>(ks, 4u);
-    ks = std::min<uint32_t>(ks, std::max<uint32_t>(1u, K / 128u / 4u));
+    ks = std::min<uint32_t>(ks, tt > 64u ? 8u : 4u);
+    ks = std::min<uint32_t>(ks, std::max<uint32_t>(1u, K / 128u));
     return std::max<uint32_t>(ks, 1u);
 }
 
@@ -712,9 +776,17 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
         VX_CHECK(launch_seq_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, nH, tok, T, c.vocab_size,
                                       e->embedding_alpha, F(e->pf_h), nH));
     }
-    const uint32_t ks_qkv = pick_split(e, (nH + 127u) / 128u + 2u * ((nKV + 127u) / 128u), T, nH);
-    const uint32_t ks_o = pick_split(e, (nH + 127u) / 128u, T, nH);
-    const uint32_t ks_down = pick_split(e, (nH + 127u) / 128u, T, nF);
+    // The deep-pipelined GEMM takes the prefill-layout weights and tiled planes,
+    // from one full 128-token tile up.
+    const bool tiled = !e->pw.empty() && T >= gemm_q8p_tile_tokens();
+    const uint32_t tt = tiled ? gemm_q8p_tile_tokens() : 64u;
+    const uint32_t ks_qkv = pick_split(e, tt, (nH + 127u) / 128u + 2u * ((nKV + 127u) / 128u), T, nH);
+    const uint32_t ks_o = pick_split(e, tt, (nH + 127u) / 128u, T, nH);
+    const uint32_t ks_down = pick_split(e, tt, (nH + 127u) / 128u, T, nF);
+    // Split residual projections on the tiled path leave their partials in
+    // pf_ws; the next rmsnorm adds them to h (no atomics in the GEMM epilogue).
+    const uint64_t ws_stride = (uint64_t)e->pf_cap * nH;
+    const bool ws_o = tiled && ks_o > 1, ws_down = tiled && ks_down > 1;
     for (uint32_t l = 0; l < c.block_count; ++l) {
         const Layer &L = e->layers[l];
         {
@@ -723,11 +795,18 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             n.h = F(e->pf_h);
             n.ldh = nH;
             n.w = L.attn_norm;
+            if (l > 0 && ws_down) {
+                n.branch = F(e->pf_ws);
+                n.ldb = nH;
+                n.nbranch = ks_down;
+                n.branch_stride = ws_stride;
+            }
             n.n = nH;
             n.eps = c.rms_epsilon;
             n.yh = H(e->pf_xh);
             n.yl = H(e->pf_xl);
             n.ldp = nH;
+            n.tiled = tiled ? 1u : 0u;
             if (ks_qkv > 1) {
                 n.zero[0] = F(e->pf_q);
                 n.zero_n[0] = nH;
@@ -746,6 +825,16 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.seg[0] = gemm_seg(L.q, nH, F(e->pf_q), nH);
             g.seg[1] = gemm_seg(L.k, nKV, F(e->pf_k), nKV);
             g.seg[2] = gemm_seg(L.v, nKV, F(e->pf_v), nKV);
+            if (tiled) {
+                const vx_baselm::PrefillLayer &P = e->pw[l];
+                g.seg[0].pq = P.q.q;
+                g.seg[0].pd = P.q.d;
+                g.seg[1].pq = P.k.q;
+                g.seg[1].pd = P.k.d;
+                g.seg[2].pq = P.v.q;
+                g.seg[2].pd = P.v.d;
+                g.x_tiled = 1;
+            }
             g.nseg = 3;
             g.K = nH;
             g.T = T;
@@ -798,6 +887,7 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             a.oh = H(e->pf_xh);
             a.ol = H(e->pf_xl);
             a.ldo = nH;
+            a.tiled = tiled ? 1u : 0u;
             VX_CHECK(launch_prefill_attn(s, a));
         }
         {
@@ -806,6 +896,11 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.wk = L.o.wt;
             g.epi = GEPI_RESIDUAL;
             g.seg[0] = gemm_seg(L.o, nH, F(e->pf_h), nH);
+            if (tiled) {
+                g.seg[0].pq = e->pw[l].o.q;
+                g.seg[0].pd = e->pw[l].o.d;
+                g.x_tiled = 1;
+            }
             g.K = nH;
             g.T = T;
             g.xh = H(e->pf_xh);
@@ -813,6 +908,10 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.ldx = nH;
             g.scale = e->residual_scale;
             g.ksplit = ks_o;
+            if (ws_o) {
+                g.ws = F(e->pf_ws);
+                g.ws_stride = ws_stride;
+            }
             VX_CHECK(launch_gemm(s, g));
         }
         {
@@ -821,11 +920,18 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             n.h = F(e->pf_h);
             n.ldh = nH;
             n.w = L.ffn_norm;
+            if (ws_o) {
+                n.branch = F(e->pf_ws);
+                n.ldb = nH;
+                n.nbranch = ks_o;
+                n.branch_stride = ws_stride;
+            }
             n.n = nH;
             n.eps = c.rms_epsilon;
             n.yh = H(e->pf_xh);
             n.yl = H(e->pf_xl);
             n.ldp = nH;
+            n.tiled = tiled ? 1u : 0u;
             VX_CHECK(launch_seq_rmsnorm(s, n, T));
         }
         {
@@ -835,6 +941,12 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.epi = GEPI_SWIGLU;
             g.seg[0] = gemm_seg(L.gate, nF, nullptr, 0);
             g.seg[1] = gemm_seg(L.up, nF, nullptr, 0);
+            if (tiled) {
+                g.seg[0].pq = e->pw[l].gu.q;   // gate and up interleaved
+                g.seg[0].pd = e->pw[l].gu.d;
+                g.x_tiled = 1;
+                g.o_tiled = 1;
+            }
             g.nseg = 2;
             g.K = nH;
             g.T = T;
@@ -852,6 +964,11 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.wk = L.down.wt;
             g.epi = GEPI_RESIDUAL;
             g.seg[0] = gemm_seg(L.down, nH, F(e->pf_h), nH);
+            if (tiled) {
+                g.seg[0].pq = e->pw[l].down.q;
+                g.seg[0].pd = e->pw[l].down.d;
+                g.x_tiled = 1;
+            }
             g.K = nF;
             g.T = T;
             g.xh = H(e->pf_ah);
@@ -859,8 +976,24 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.ldx = nF;
             g.scale = e->residual_scale;
             g.ksplit = ks_down;
+            if (ws_down) {
+                g.ws = F(e->pf_ws);
+                g.ws_stride = ws_stride;
+            }
             VX_CHECK(launch_gemm(s, g));
         }
+    }
+    if (ws_down) {   // the last layer's down partials
+        ProfSpan sp(ctx, "prefill.norm");
+        SeqNormArgs n;
+        n.h = F(e->pf_h);
+        n.ldh = nH;
+        n.n = nH;
+        n.branch = F(e->pf_ws);
+        n.ldb = nH;
+        n.nbranch = ks_down;
+        n.branch_stride = ws_stride;
+        VX_CHECK(launch_seq_rmsnorm(s, n, T));
     }
     // Engine state after the chunk: hidden = last token's residual stream, norm =
     // its rmsnorm(h)*output_norm (record_transformer's final residual_rmsnorm).
@@ -875,6 +1008,7 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
 int enqueue_prefill(vx_baselm *e, const uint32_t *tokens, uint32_t n) {
     VX_CHECK(check_prefill_layout(e));
     VX_CHECK(ensure_prefill_work(e));
+    VX_CHECK(ensure_prefill_weights(e));
     hipStream_t s = e->ctx->stream;
     VX_HIP(hipMemcpyAsync(e->pf_tok->ptr, tokens, (size_t)n * 4u, hipMemcpyHostToDevice, s));
     for (uint32_t done = 0; done < n;) {

@@ -1,0 +1,399 @@
+// Prefill projection GEMM for Q8_0 weights on gfx950, token-batched (T >= 128):
+//   C[t][n] = sum_k X[t][k] * W[n][k],   X as hi/lo f16 planes, W = d * q (Q8_0).
+//
+// Same arithmetic as k_gemm (kernels_seq.hip): the int8 quants enter the MFMA as
+// exact f16, each 32-column block's partial product is scaled by its f32 block
+// scale afterwards (acc += d[n][b] * sum_{k in b} q*x, matvec.comp:32-44), and X
+// enters as hi + lo planes through two MFMAs. The kernel is organised around
+// keeping the matrix cores fed at small token counts:
+//   * workgroup tile 128 tokens x 128 weight rows, four waves of 64 x 64 (2 x 2
+//     v_mfma_f32_32x32x16_f16 tiles per plane), two workgroups per CU, so each
+//     SIMD holds two waves and one's VALU work (quant widening, scale FMAs)
+//     runs under the other's MFMAs;
+//   * both operands are stored for this kernel: the weights in the prefill
+//     layout (PrefillMatrix, repacked once per model) and X in the tiled plane
+//     layout (tiled_plane_index, written so by the producers). A k-stage is one
+//     32-column Q8_0 block, and its operands are contiguous pieces: 8 KB per X
+//     plane, 4 KB of quants, 512 B of scales. Each wave copies six pieces per
+//     stage global -> LDS by the DMA path (global_load_lds: no registers, no
+//     VALU, every fetched byte used) into a ring of kStages LDS slots,
+//     kStages - 1 stages ahead of the one being multiplied;
+//   * the quants stay int8 in LDS (a quarter of the f16 footprint, which is
+//     what fits two workgroups per CU) and are widened when a wave reads its B
+//     fragment;
+//   * both layouts carry a permutation so every fragment read from LDS is free
+//     of bank conflicts (for 32 and for 64 banks) after a verbatim copy.
+// Measured alternatives, slower on MI355X at T = 384: 16-column stages, one
+// workgroup per CU with a deeper ring, f16 quants in LDS, and weights as exact
+// hi/lo f16 pairs of d*q (three MFMAs per k-step, no scale step).
+#include <type_traits>
+
+#include "vx_internal.h"
+
+namespace vx {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float acc16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128;                       // tokens per workgroup tile
+constexpr int kBN = 128;                       // weight rows per workgroup tile
+constexpr int kStages = 3;                     // LDS ring slots (61.5 KB: two workgroups per CU)
+constexpr int kXBytes = kBM * 32 * 2;          // one plane of a stage: f16 [token][32]
+constexpr int kWBytes = kBN * 32;              // int8 quants [row][32]
+constexpr int kDBytes = kBN * 4;               // f32 scales [row]
+constexpr int kXOff = 0, kWOff = 2 * kXBytes, kDOff = kWOff + kWBytes;
+constexpr int kStageBytes = kDOff + kDBytes;   // 20992
+constexpr int kOpsPerStage = 6;                // DMA instructions per wave per stage
+
+// Chunk permutations of the stored layouts: X rows of 64 bytes in 16-byte
+// chunks (tiled_plane_index), quant rows of 32 bytes in 8-byte chunks
+// (PrefillMatrix); both conflict-free for 32 and for 64 LDS banks.
+__device__ __forceinline__ uint32_t xperm(uint32_t t) { return ((t >> 1) ^ (t >> 3)) & 3u; }
+__device__ __forceinline__ uint32_t wperm(uint32_t n) { return ((n >> 2) ^ (n >> 4)) & 3u; }
+
+// Four signed int8 quants (one dword) -> four exact f16 values: (q ^ 0x80) is
+// q + 128 in 0..255; the f16 with bits 0x6400 | u is 1024 + u, minus 1152 = q.
+__device__ __forceinline__ uint2 q8x4_to_f16(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2v a = __builtin_bit_cast(h2v, lo) - bias;
+    const h2v b = __builtin_bit_cast(h2v, hi) - bias;
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
+__device__ __forceinline__ acc16 mfma(h8 a, h8 b, acc16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Weight row of tile row rho (as k_gemm's tile_row): SwiGLU tiles interleave 32
+// gate rows and the same 32 up rows, so one lane holds g and u of one row.
+template <int EPI>
+__device__ __forceinline__ uint32_t tile_row(uint32_t tn, uint32_t tile0, uint32_t rho) {
+    if constexpr (EPI == GEPI_SWIGLU)
+        return 64u * tn + 32u * (rho >> 6) + (rho & 31u);
+    else
+        return (tn - tile0) * kBN + rho;
+}
+
+// s_waitcnt vmcnt(N) (expcnt at its maximum; lgkmcnt 0 when LGKM0, else at its
+// maximum), gfx9 encoding.
+template <int N, bool LGKM0 = false>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | ((LGKM0 ? 0 : 15) << 8));
+}
+
+// LDS DMA, issued from asm: the compiler then does not model these as LDS
+// writes, so it adds no waits of its own before LDS reads (it cannot tell ring
+// slots apart reliably and would drain every DMA in flight). The ring protocol
+// orders them instead: a slot is read only after wait_vm<> has retired its DMA
+// and a barrier, and refilled only after a barrier that follows its last read.
+// `lds` is the LDS byte address of lane 0's destination (wave-uniform, in M0);
+// lane i writes at lds + i * size.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// (An LDS DMA may not read M0 in the instruction right after the write: one
+// wait state between them.)
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+
+// Stage b (32-column block) of the tile: wave w copies X pieces 4w .. 4w + 3
+// (1 KB each, plane = piece / 8), quant piece w (1 KB), and one 256 B half of
+// the scales (waves 2 and 3 repeat what waves 0 and 1 copy).
+struct Src {
+    const uint8_t *x[4];   // X plane piece + 16 * lane
+    const uint8_t *w;      // quants + 1024 * wave + 16 * lane
+    const uint8_t *d;      // scales + 256 * (wave & 1) + 4 * lane
+};
+
+__device__ __forceinline__ void issue_stage(const Src &src, uint32_t blk, uint32_t slot, uint32_t wave) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t u = 4u * wave + (uint32_t)j;
+        dma16(src.x[j] + (size_t)blk * kXBytes, slot + kXOff + (u >> 3) * kXBytes + (u & 7u) * 1024u);
+    }
+    dma16(src.w + (size_t)blk * kWBytes, slot + kWOff + wave * 1024u);
+    dma4(src.d + (size_t)blk * kDBytes, slot + kDOff + (wave & 1u) * 256u);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kStageBytes];
+    const uint32_t ring_lds = lds_addr(ring);
+
+    // XCD-major order: workgroup b runs on XCD b % 8; consecutive ids of one XCD
+    // cover the token tiles of the same weight rows.
+    const uint32_t b = blockIdx.x;
+    const uint32_t id = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
+    const uint32_t per_split = a.ntn * a.ntm;
+    if (id >= per_split * a.ksplit) return;
+    const uint32_t ks = id / per_split, rem = id - ks * per_split;
+    const uint32_t tn = rem / a.ntm, tm = rem - tn * a.ntm;
+    const uint32_t m0 = tm * kBM;
+    uint32_t seg = 0;
+    if constexpr (EPI != GEPI_SWIGLU) {
+        while (seg + 1 < a.nseg && tn >= a.seg[seg + 1].tile0) ++seg;
+    }
+    const GemmSeg &sg = a.seg[seg];
+    const uint32_t nblk = a.K / 32u;
+    const uint32_t kb0 = ks * nblk / a.ksplit, kb1 = (ks + 1u) * nblk / a.ksplit;
+    if (kb1 == kb0) return;   // nothing to add (ksplit is clamped to the block count)
+    const uint32_t nkb = kb1 - kb0;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave & 1u, wn = wave >> 1;
+
+    // ---- DMA sources of this tile at block 0
+    Src src;
+    {
+        const uint32_t lt = EPI == GEPI_SWIGLU ? tn : tn - sg.tile0;   // tile within the matrix
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t u = 4u * wave + (uint32_t)j;
+            const uint8_t *plane = reinterpret_cast<const uint8_t *>((u >> 3) ? a.xl : a.xh);
+            src.x[j] = plane + ((size_t)tm * nblk) * kXBytes + (u & 7u) * 1024u + 16u * lane;
+        }
+        src.w = reinterpret_cast<const uint8_t *>(sg.pq) + ((size_t)lt * nblk) * kWBytes + 1024u * wave + 16u * lane;
+        src.d = reinterpret_cast<const uint8_t *>(sg.pd) + ((size_t)lt * nblk) * kDBytes + 256u * (wave & 1u) +
+                4u * lane;
+    }
+
+    // ---- fragment addresses inside a stage slot: k-step e covers columns
+    // 16e .. 16e + 15 of the block; this lane takes 8 of them, chunk 2e + hs.
+    uint32_t xa[2][2];   // [mt][e] (plane hi; lo is + kXBytes)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const uint32_t t = 64u * wm + 32u * (uint32_t)mt + l32;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) xa[mt][e] = kXOff + t * 64u + (((2u * (uint32_t)e + hs) ^ xperm(t)) * 16u);
+    }
+    uint32_t wa[2][2], da[2];   // [nt][e] quant dword pair, [nt] scale
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const uint32_t n = 64u * wn + 32u * (uint32_t)nt + l32;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) wa[nt][e] = kWOff + n * 32u + (((2u * (uint32_t)e + hs) ^ wperm(n)) * 8u);
+        da[nt] = kDOff + n * 4u;
+    }
+
+    // ---- prologue: blocks 0 .. kStages-2 (indices clamped: always the same
+    // number of DMA instructions per stage, which the vmcnt waits count on)
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s)
+        issue_stage(src, kb0 + ((uint32_t)s < nkb ? (uint32_t)s : nkb - 1u), ring_lds + (uint32_t)s * kStageBytes, wave);
+
+    acc16 acc[2][2], p[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = acc16{};
+
+    // One block: wait for its slot, refill the slot consumed last, two MFMA
+    // k-steps per plane into p, then acc += d * p. The wait also drains this
+    // wave's LDS reads of the slot about to be refilled.
+    for (uint32_t it = 0; it < nkb; ++it) {
+        wait_vm<kOpsPerStage * (kStages - 2), true>();
+        __builtin_amdgcn_s_barrier();
+        const uint32_t nxt = it + kStages - 1u;
+        issue_stage(src, kb0 + (nxt < nkb ? nxt : nkb - 1u), ring_lds + (nxt % kStages) * kStageBytes, wave);
+        const uint8_t *slot = ring + (it % kStages) * kStageBytes;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) p[i][j] = acc16{};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            h8 bf[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint2 q = *reinterpret_cast<const uint2 *>(slot + wa[nt][e]);
+                const uint2 f0 = q8x4_to_f16(q.x), f1 = q8x4_to_f16(q.y);
+                bf[nt] = __builtin_bit_cast(h8, make_uint4(f0.x, f0.y, f1.x, f1.y));
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const h8 ah = *reinterpret_cast<const h8 *>(slot + xa[mt][e]);
+                const h8 al = *reinterpret_cast<const h8 *>(slot + xa[mt][e] + kXBytes);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    p[mt][nt] = mfma(ah, bf[nt], p[mt][nt]);
+                    p[mt][nt] = mfma(al, bf[nt], p[mt][nt]);
+                }
+            }
+        }
+        float d[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) d[nt] = *reinterpret_cast<const float *>(slot + da[nt]);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[mt][nt][r] = fmaf(d[nt], p[mt][nt][r], acc[mt][nt][r]);
+    }
+    // Drain the DMA of the clamped trailing stages before the workgroup ends.
+    wait_vm<0>();
+
+    float *const out0 = sg.out;
+    const uint32_t ldo0 = sg.ldo, rows0 = sg.rows;
+    // ---- epilogue. Lane (l32, hs) of wave (wm, wn) holds, for tile (mt, nt),
+    // weight row rho = 64wn + 32nt + l32 and tokens m0 + 64wm + 32mt + 8(r/4) + 4hs + r%4.
+    // It issues stores and atomics only (no loads): a load here would make every
+    // element wait for the stores before it. Residual adds are atomic adds, which
+    // with one contributor (no split) give exactly h + v; split residual
+    // products go to the partial workspace when one is given.
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const uint32_t tbase = m0 + 64u * wm + 32u * (uint32_t)mt + 4u * hs;
+        if constexpr (EPI == GEPI_SWIGLU) {
+            const uint32_t row = tile_row<EPI>(tn, 0, 64u * wn + l32);
+            if (row < rows0) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t tok = tbase + 8u * (uint32_t)(r >> 2) + (uint32_t)(r & 3);
+                    if (tok >= a.T) continue;
+                    const float g = acc[mt][0][r], u = acc[mt][1][r];
+                    const float v = g / (1.0f + expf(-g)) * u;   // matvec_swiglu.comp:67
+                    if (out0) out0[(size_t)tok * ldo0 + row] = v;
+                    if (a.oh) {
+                        const size_t o = a.o_tiled ? tiled_plane_index(tok, row, a.ldp) : (size_t)tok * a.ldp + row;
+                        const _Float16 hv = (_Float16)v;
+                        a.oh[o] = __builtin_bit_cast(__half, hv);
+                        a.ol[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t row = tile_row<EPI>(tn, sg.tile0, 64u * wn + 32u * (uint32_t)nt + l32);
+                if (row >= rows0) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t tok = tbase + 8u * (uint32_t)(r >> 2) + (uint32_t)(r & 3);
+                    if (tok >= a.T) continue;
+                    float *dst = out0 + (size_t)tok * ldo0 + row;
+                    if constexpr (EPI == GEPI_STORE) {
+                        const float v = acc[mt][nt][r] * a.alpha;
+                        if (a.ksplit > 1)
+                            unsafeAtomicAdd(dst, v);
+                        else
+                            *dst = v;
+                    } else if (a.ws && a.ksplit > 1) {
+                        a.ws[ks * a.ws_stride + (size_t)tok * ldo0 + row] = acc[mt][nt][r] * a.scale;
+                    } else {
+                        unsafeAtomicAdd(dst, acc[mt][nt][r] * a.scale);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// One thread per 32-byte quant row piece (tile, block b, row n) of the output.
+__global__ __launch_bounds__(256) void k_repack_prefill(const uint8_t *raw, uint32_t off0, uint32_t off1,
+                                                        uint32_t rows, uint32_t K, int interleave, uint64_t total,
+                                                        int8_t *q, float *d) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= total) return;
+    const uint32_t nb = K / 32u;
+    const uint32_t n = (uint32_t)(i & 127u), blk = (uint32_t)((i >> 7) % nb), tile = (uint32_t)((i >> 7) / nb);
+    const uint32_t r_out = 128u * tile + n;
+    uint32_t mat = 0, row = r_out;
+    if (interleave) {
+        mat = (r_out >> 5) & 1u;
+        row = 32u * (r_out >> 6) + (r_out & 31u);
+    }
+    const bool live = row < rows;
+    const uint8_t *b = raw + (mat ? off1 : off0) + ((size_t)(live ? row : 0u) * nb + blk) * 34u;
+    const uint32_t g = wperm(n);
+    uint32_t w[8];   // stored chunk sc holds source chunk sc ^ g
+#pragma unroll
+    for (int sc = 0; sc < 4; ++sc) {
+        const uint32_t src = 2u + 8u * ((uint32_t)sc ^ g);
+        w[2 * sc] = live ? (b[src] | (b[src + 1] << 8) | (b[src + 2] << 16) | ((uint32_t)b[src + 3] << 24)) : 0u;
+        w[2 * sc + 1] =
+            live ? (b[src + 4] | (b[src + 5] << 8) | (b[src + 6] << 16) | ((uint32_t)b[src + 7] << 24)) : 0u;
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(q + i * 32u);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    d[((size_t)tile * nb + blk) * 128u + n] =
+        live ? (float)__builtin_bit_cast(_Float16, (unsigned short)(b[0] | (b[1] << 8))) : 0.f;
+}
+
+}  // namespace
+
+uint32_t gemm_q8p_tile_tokens() { return kBM; }
+
+bool gemm_q8p_eligible(const GemmArgs &a) {
+    if (a.wk != WT_Q8 || a.xf32 || !a.x_tiled || a.T == 0 || a.K % 32u) return false;
+    const uint32_t nseg = a.epi == GEPI_SWIGLU ? 1u : a.nseg;
+    for (uint32_t i = 0; i < nseg; ++i)
+        if (!a.seg[i].pq || !a.seg[i].pd || a.seg[i].bias) return false;   // no bias epilogue here
+    return true;
+}
+
+uint64_t prefill_matrix_bytes(uint32_t rows_out, uint32_t K) {
+    const uint64_t rp = (rows_out + 127u) / 128u * 128u;
+    return rp * K + rp * (K / 32u) * 4u;
+}
+
+int launch_repack_prefill(hipStream_t s, const uint8_t *raw, uint32_t off0, uint32_t off1, uint32_t rows,
+                          uint32_t K, int interleave, int8_t *q, float *d) {
+    if (K % 32u || !raw || !q || !d) return fail(VX_ERR_INVALID_ARG, "prefill repack: K %% 32 and buffers");
+    if (interleave && rows % 32u) return fail(VX_ERR_INVALID_ARG, "prefill repack: interleaved rows %% 32");
+    const uint32_t rows_out = interleave ? 2u * rows : rows;
+    const uint64_t rp = (rows_out + 127u) / 128u * 128u;
+    const uint64_t total = rp * (K / 32u);
+    k_repack_prefill<<<(unsigned)((total + 255u) / 256u), 256, 0, s>>>(raw, off0, off1, rows, K, interleave, total, q,
+                                                                        d);
+    VX_LAUNCHED("k_repack_prefill");
+    return VX_OK;
+}
+
+// Called by launch_gemm with validated arguments; sets the tiling fields.
+// For GEPI_SWIGLU, seg[0].pq/pd hold the interleaved gate/up matrix.
+int launch_gemm_q8p(hipStream_t s, GemmArgs a) {
+    uint32_t tiles = 0;
+    if (a.epi == GEPI_SWIGLU) {
+        tiles = (a.seg[0].rows + 63u) / 64u;
+        if (a.oh && a.o_tiled && a.ldp % 32u) return fail(VX_ERR_INVALID_ARG, "gemm: tiled output width %% 32");
+    } else {
+        for (uint32_t i = 0; i < a.nseg; ++i) {
+            a.seg[i].tile0 = tiles;
+            tiles += (a.seg[i].rows + kBN - 1u) / kBN;
+        }
+    }
+    const uint32_t nblk = a.K / 32u;
+    if (a.ksplit == 0) a.ksplit = 1;
+    if (a.ksplit > nblk) a.ksplit = nblk;
+    a.ntn = tiles;
+    a.ntm = (a.T + kBM - 1u) / kBM;
+    const uint64_t total = (uint64_t)a.ntn * a.ntm * a.ksplit;
+    if (total == 0) return VX_OK;
+    const uint64_t grid = (total + 7u) / 8u * 8u;
+    if (grid > 0x7fffffffull) return fail(VX_ERR_UNSUPPORTED, "gemm: grid too large");
+    switch (a.epi) {
+        case GEPI_STORE: k_gemm_q8p<GEPI_STORE><<<(unsigned)grid, 256, 0, s>>>(a); break;
+        case GEPI_RESIDUAL: k_gemm_q8p<GEPI_RESIDUAL><<<(unsigned)grid, 256, 0, s>>>(a); break;
+        case GEPI_SWIGLU: k_gemm_q8p<GEPI_SWIGLU><<<(unsigned)grid, 256, 0, s>>>(a); break;
+        default: return fail(VX_ERR_UNSUPPORTED, "gemm: epilogue %u", a.epi);
+    }
+    VX_LAUNCHED("k_gemm_q8p");
+    return VX_OK;
+}
+
+}  // namespace vx

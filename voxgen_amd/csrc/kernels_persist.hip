@@ -1,6 +1,6 @@
 // Persistent decode step: every layer of record_transformer (baselm.rs:922-1039)
-// in ONE kernel of G workgroups (one per CU), so that the weight streaming of a
-// phase overlaps the dependency on the phase before it.
+// in ONE kernel, so that the weight streaming of a phase overlaps the work of the
+// phase before it.
 //
 // Per layer, five phases (the five kernels of the per-kernel step):
 //   A  rmsnorm(h)*attn_norm -> Q/K/V rows -> RoPE -> q, k, v and the f16 KV row
@@ -9,18 +9,25 @@
 //   C  h += scale * Wo . attention
 //   D  act = silu(Wg . n) * (Wu . n), n = rmsnorm(h)*ffn_norm
 //   E  h += scale * Wdown . act
-// A workgroup first issues the loads of its weight rows for the phase (they do
-// not depend on anything computed in the step), then waits until every
-// workgroup has finished the previous phase, then reads that phase's outputs and
-// computes. Phase completion is counted on eight per-XCD counters (one cache
-// line each) with device-scope atomic adds; no memory fence is issued: every
-// value one workgroup hands to another inside the step (h, q/k/v, the KV row,
-// partials, attention, act) is written with device-scope stores and read with
-// device-scope loads, which the hardware keeps coherent across XCDs, and a
-// workgroup waits for its own stores to complete before it counts itself done.
-// Every wait is bounded: on timeout the kernel records an error word and all
-// later waits fall through, so a fault of the protocol ends the step with an
-// error instead of hanging the device.
+// The grid is kPersistGroups groups of one workgroup per CU. Phases are numbered
+// p = 5*layer + k and group p % kPersistGroups runs phase p. A workgroup first
+// issues the loads of its weight rows for its next phase (they do not depend on
+// anything computed in the step), then waits until the phase before is finished,
+// then reads that phase's outputs and computes. With two groups the weights of
+// phase p stream in while phase p-1 runs on the other group (each wave's load
+// counter retires in order, so that overlap needs a second group); measured on
+// MI355X this is slower than one group, because the streaming raises the latency
+// of the coherent hand-offs between phases, so one group is compiled.
+// Phase completion is counted on eight per-XCD counters (one cache line each)
+// with device-scope atomic adds; no memory fence is issued: every value one
+// workgroup hands to another inside the step (h, q/k/v, the KV row, partials,
+// attention, act) is written with device-scope stores and read with device-scope
+// loads, which the hardware keeps coherent across XCDs, and a workgroup waits
+// for its own stores to complete before it counts itself done. Every wait is
+// bounded: on timeout the kernel records an error word and all later waits fall
+// through, so a fault of the protocol ends the step with an error instead of
+// hanging the device. All workgroups must be resident at once (checked against
+// the occupancy before the first launch).
 #include <cfloat>
 
 #include "decode_dev.h"
@@ -308,7 +315,7 @@ __device__ __forceinline__ void mark(const PersistArgs &a, uint32_t idx, uint32_
 
 // ---------------------------------------------------------------- the kernel
 template <int NGH, int NGF, int RPWC, int RPWD>
-__global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
+__global__ __launch_bounds__(256, kPersistGroups) void k_decode_persistent(PersistArgs a) {
     __shared__ __align__(16) float xs[(NGF > NGH ? NGF : NGH) * kGroupCols];
     __shared__ float red[kWavesPerBlock];
     __shared__ __align__(16) __half vs[64][128];
@@ -318,7 +325,9 @@ __global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
     __shared__ uint32_t flag;
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t G = gridDim.x, gw = blockIdx.x * kWavesPerBlock + wave, NW = G * kWavesPerBlock;
+    // G workgroups per group; lb = index within the group.
+    const uint32_t G = gridDim.x / kPersistGroups, grp = blockIdx.x / G, lb = blockIdx.x % G;
+    const uint32_t gw = lb * kWavesPerBlock + wave, NW = G * kWavesPerBlock;
     const uint32_t H = a.H, F = a.F, KV = a.KV, HD = 128u, half_dim = 64u;
     const uint32_t pq = H / 2u, pk = KV / 2u, NP = pq + 2u * pk;
     const uint32_t pos = *a.position;
@@ -329,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
     for (uint32_t l = 0; l < a.n_layers; ++l) {
         const PLayer &L = a.layers[l];
         // ------------------------------------------------ A: QKV + RoPE + KV row
-        {
+        if ((l * 5u + 0u) % kPersistGroups == grp) {
             mark(a, l * 5u + 0u, 0);
             Q8Row<NGH> rr[2][2];
             uint32_t r0s[2], r1s[2];
@@ -400,11 +409,11 @@ __global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
             mark(a, l * 5u + 0u, 2);
         }
         // ------------------------------------------------ B: attention
-        {
+        if ((l * 5u + 1u) % kPersistGroups == grp) {
             mark(a, l * 5u + 1u, 0);
             phase_wait(a.cnt, l * 5u + 0u, G, a.err);
             mark(a, l * 5u + 1u, 1);
-            for (uint32_t u = blockIdx.x; u < nunits; u += G) {
+            for (uint32_t u = lb; u < nunits; u += G) {
                 const uint32_t s = u % a.splits, h = u / a.splits;
                 if (s < plan.active) attn_unit<128>(a, l, s, h, pos, plan, vs, ps, red2, accs, &flag);
             }
@@ -412,7 +421,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
             mark(a, l * 5u + 1u, 2);
         }
         // ------------------------------------------------ C: attn_out + residual
-        {
+        if ((l * 5u + 2u) % kPersistGroups == grp) {
             mark(a, l * 5u + 2u, 0);
             const uint32_t row0 = gw * RPWC;
             Q8Row<NGH> r[RPWC];
@@ -442,7 +451,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
             mark(a, l * 5u + 2u, 2);
         }
         // ------------------------------------------------ D: rmsnorm + SwiGLU
-        {
+        if ((l * 5u + 3u) % kPersistGroups == grp) {
             mark(a, l * 5u + 3u, 0);
             const uint32_t row0 = gw * RPWD;
             Q8Row<NGH> rg[RPWD], ru[RPWD];
@@ -473,7 +482,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_persistent(PersistArgs a) {
             mark(a, l * 5u + 3u, 2);
         }
         // ------------------------------------------------ E: down + residual
-        {
+        if ((l * 5u + 4u) % kPersistGroups == grp) {
             mark(a, l * 5u + 4u, 0);
             const uint32_t row0 = gw * RPWC;
             Q8Row<NGF> r[RPWC];
@@ -505,22 +514,22 @@ uint64_t persist_counter_words(uint32_t n_layers, uint32_t q_heads) {
 }
 
 // Compiled instance: H = 2048 (two 1024-column groups), F = 6144, head_dim 128,
-// 2 rows per wave in attn_out/down (H = 2 * 4 * grid) and 6 gate/up row pairs
-// per wave in SwiGLU (F = 6 * 4 * grid), at most two rotary pairs per wave in
-// the QKV phase.
-bool persistent_supported(uint32_t H, uint32_t F, uint32_t KV, uint32_t q_heads, uint32_t head_dim, uint32_t grid) {
-    const uint32_t waves = grid * kWavesPerBlock;
+// 2 rows per wave in attn_out/down (H = 2 * 4 * cus) and 6 gate/up row pairs
+// per wave in SwiGLU (F = 6 * 4 * cus), at most two rotary pairs per wave in
+// the QKV phase; `cus` workgroups per group.
+bool persistent_supported(uint32_t H, uint32_t F, uint32_t KV, uint32_t q_heads, uint32_t head_dim, uint32_t cus) {
+    const uint32_t waves = cus * kWavesPerBlock;
     return H == 2048u && F == 6144u && head_dim == 128u && q_heads * head_dim == H && KV % 2u == 0u &&
            H == 2u * waves && F == 6u * waves && H / 2u + KV <= 2u * waves;
 }
 
-int launch_decode_persistent(hipStream_t s, const PersistArgs &a, uint32_t grid) {
-    if (!persistent_supported(a.H, a.F, a.KV, a.q_heads, a.H / (a.q_heads ? a.q_heads : 1u), grid) ||
+int launch_decode_persistent(hipStream_t s, const PersistArgs &a, uint32_t cus) {
+    if (!persistent_supported(a.H, a.F, a.KV, a.q_heads, a.H / (a.q_heads ? a.q_heads : 1u), cus) ||
         a.kv_heads == 0 || a.q_heads % a.kv_heads || a.KV != a.kv_heads * 128u || a.splits == 0 ||
         a.splits > kPersistMaxSplits)
-        return fail(VX_ERR_UNSUPPORTED, "persistent decode step: geometry H=%u F=%u KV=%u on %u workgroups not compiled",
-                    a.H, a.F, a.KV, grid);
-    k_decode_persistent<2, 6, 2, 6><<<grid, 256, 0, s>>>(a);
+        return fail(VX_ERR_UNSUPPORTED, "persistent decode step: geometry H=%u F=%u KV=%u on %u CUs not compiled",
+                    a.H, a.F, a.KV, cus);
+    k_decode_persistent<2, 6, 2, 6><<<kPersistGroups * cus, 256, 0, s>>>(a);
     VX_LAUNCHED("k_decode_persistent");
     return VX_OK;
 }

@@ -331,9 +331,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
             const float v = silu_mul(acc0[r], acc1[r]);
             if (a.seg[0].out) a.seg[0].out[(size_t)tok * a.seg[0].ldo + row] = v;
             if (a.oh) {
+                const size_t o = a.o_tiled ? tiled_plane_index(tok, row, a.ldp) : (size_t)tok * a.ldp + row;
                 const _Float16 hv = (_Float16)v;
-                a.oh[(size_t)tok * a.ldp + row] = __builtin_bit_cast(__half, hv);
-                a.ol[(size_t)tok * a.ldp + row] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
+                a.oh[o] = __builtin_bit_cast(__half, hv);
+                a.ol[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
             }
         }
     } else {
@@ -347,6 +348,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
             if (EPI == GEPI_STORE && sg.bias && ks == 0)
                 bias = sg.bias_dtype == 0 ? static_cast<const float *>(sg.bias)[row]
                                           : h2f(static_cast<const unsigned short *>(sg.bias)[row]);
+            // Take the bias now: used first inside the branchy loop below, its
+            // wait would drain every store issued before it.
+            asm volatile("" : "+v"(bias));
             const acc16 &acc = t == 0 ? acc0 : acc1;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -359,12 +363,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
                         unsafeAtomicAdd(dst, v);
                     else
                         *dst = v;
-                } else {  // GEPI_RESIDUAL: hidden += scale * (W . x)
-                    const float v = acc[r] * a.scale;
-                    if (a.ksplit > 1)
-                        unsafeAtomicAdd(dst, v);
-                    else
-                        *dst = *dst + v;
+                } else {  // GEPI_RESIDUAL: hidden += scale * (W . x), an atomic add (no load to wait for;
+                          // with one contributor it is exactly h + v)
+                    unsafeAtomicAdd(dst, acc[r] * a.scale);
                 }
             }
         }
@@ -386,11 +387,14 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
     for (uint32_t i = threadIdx.x; i < a.n; i += 256u) {
         float v = h[i];
         if (br) {
-            v = v + br[i] * a.scale;
+            float add = br[i];
+            for (uint32_t b = 1; b < a.nbranch; ++b) add += br[(size_t)b * a.branch_stride + i];
+            v = v + add * a.scale;
             h[i] = v;
         }
         s += v * v;
     }
+    if (!a.w) return;   // residual update only
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
     if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = s;
@@ -401,14 +405,83 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
         const float v = h[i] * inv_rms * a.w[i];
         if (a.y) a.y[(size_t)t * a.ldy + i] = v;
         if (a.yh) {
+            const size_t o = a.tiled ? tiled_plane_index(t, i, a.n) : (size_t)t * a.ldp + i;
             const _Float16 hv = (_Float16)v;
-            a.yh[(size_t)t * a.ldp + i] = __builtin_bit_cast(__half, hv);
-            a.yl[(size_t)t * a.ldp + i] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
+            a.yh[o] = __builtin_bit_cast(__half, hv);
+            a.yl[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
         }
     }
     for (int z = 0; z < 3; ++z)
         if (a.zero[z])
             for (uint32_t i = threadIdx.x; i < a.zero_n[z]; i += 256u) a.zero[z][(size_t)t * a.zero_n[z] + i] = 0.f;
+}
+
+// k_seq_rmsnorm for n = 1024 * NV: thread t holds the float4 chunks t + 256j of
+// the token's row in registers across the reduction; the branch rows of a chunk
+// are all requested before they are summed. Same arithmetic, summation order
+// h + scale * (b0 + b1 + ...) as k_seq_rmsnorm.
+template <int NV>
+__global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    float *h = a.h + (size_t)t * a.ldh;
+    float4 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4 *>(h + 4u * (tid + 256u * j));
+    if (a.branch) {
+        const float *br = a.branch + (size_t)t * a.ldb;
+        float4 bv[NV][kSeqNormMaxBranch];
+#pragma unroll
+        for (int b = 0; b < (int)kSeqNormMaxBranch; ++b)
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                bv[j][b] = (uint32_t)b < a.nbranch
+                               ? *reinterpret_cast<const float4 *>(br + (size_t)b * a.branch_stride + 4u * (tid + 256u * j))
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            float4 add = bv[j][0];
+#pragma unroll
+            for (int b = 1; b < (int)kSeqNormMaxBranch; ++b)
+                if ((uint32_t)b < a.nbranch) {
+                    add.x += bv[j][b].x;
+                    add.y += bv[j][b].y;
+                    add.z += bv[j][b].z;
+                    add.w += bv[j][b].w;
+                }
+            v[j] = make_float4(v[j].x + add.x * a.scale, v[j].y + add.y * a.scale, v[j].z + add.z * a.scale,
+                               v[j].w + add.w * a.scale);
+            *reinterpret_cast<float4 *>(h + 4u * (tid + 256u * j)) = v[j];
+        }
+    }
+    if (!a.w) return;   // residual update only
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63u) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    const float inv_rms = 1.0f / sqrtf(ss / (float)a.n + a.eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t c = 4u * (tid + 256u * j);
+        const float4 w = *reinterpret_cast<const float4 *>(a.w + c);
+        const float o[4] = {v[j].x * inv_rms * w.x, v[j].y * inv_rms * w.y, v[j].z * inv_rms * w.z, v[j].w * inv_rms * w.w};
+        if (a.y) *reinterpret_cast<float4 *>(a.y + (size_t)t * a.ldy + c) = make_float4(o[0], o[1], o[2], o[3]);
+        if (a.yh) {
+            // Four columns from a multiple of 4 stay inside one 8-column chunk.
+            const size_t po = a.tiled ? tiled_plane_index(t, c, a.n) : (size_t)t * a.ldp + c;
+            uint2 hi, lo;
+            split4(make_float4(o[0], o[1], o[2], o[3]), hi, lo);
+            *reinterpret_cast<uint2 *>(a.yh + po) = hi;
+            *reinterpret_cast<uint2 *>(a.yl + po) = lo;
+        }
+    }
+    for (int z = 0; z < 3; ++z)
+        if (a.zero[z])
+            for (uint32_t i = tid; i < a.zero_n[z]; i += 256u) a.zero[z][(size_t)t * a.zero_n[z] + i] = 0.f;
 }
 
 // Per-token RoPE at position base + t (rope.comp:22-51 / seq_rope.comp:8 with a
@@ -655,8 +728,10 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
             if (a.oh) {
                 uint2 hi, lo;
                 split4(make_float4(outv[0], outv[1], outv[2], outv[3]), hi, lo);
-                *reinterpret_cast<uint2 *>(a.oh + oo) = hi;
-                *reinterpret_cast<uint2 *>(a.ol + oo) = lo;
+                // Four columns from a multiple of 4 stay inside one 8-column half.
+                const size_t po = a.tiled ? tiled_plane_index(tq, head * HD + d, a.ldo) : oo;
+                *reinterpret_cast<uint2 *>(a.oh + po) = hi;
+                *reinterpret_cast<uint2 *>(a.ol + po) = lo;
             }
         }
     }
@@ -800,6 +875,8 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
+uint32_t gemm_tile_tokens(const GemmArgs &a) { return gemm_q8p_eligible(a) ? gemm_q8p_tile_tokens() : (uint32_t)GM; }
+
 int launch_gemm(hipStream_t s, const GemmArgs &in) {
     GemmArgs a = in;
     if (a.T == 0) return VX_OK;
@@ -828,6 +905,7 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
         if (a.wk == WT_Q8 ? (!g.qs || !g.d) : !g.w)
             return fail(VX_ERR_INVALID_ARG, "gemm: segment %u weight pointers missing", i);
     }
+    if (gemm_q8p_eligible(a)) return launch_gemm_q8p(s, a);
     const uint32_t stages = a.K / GK;
     if (a.ksplit == 0) a.ksplit = 1;
     if (a.ksplit > stages) a.ksplit = stages;
@@ -862,6 +940,21 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
 int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens) {
     if (tokens == 0) return VX_OK;
     if (a.yh && !a.yl) return fail(VX_ERR_INVALID_ARG, "seq rmsnorm: plane output incomplete");
+    if (a.yh && a.tiled && a.n % 32u) return fail(VX_ERR_INVALID_ARG, "seq rmsnorm: tiled planes need n %% 32");
+    if (a.nbranch == 0 || a.nbranch > kSeqNormMaxBranch)
+        return fail(VX_ERR_INVALID_ARG, "seq rmsnorm: 1..%u branches", kSeqNormMaxBranch);
+    const bool vec = a.n % 1024u == 0 && a.n <= 4096u && a.ldh % 4u == 0 && (!a.branch || (a.ldb % 4u == 0 && a.branch_stride % 4u == 0)) &&
+                     (!a.y || a.ldy % 4u == 0) && (!a.yh || a.tiled || a.ldp % 4u == 0);
+    if (vec) {
+        switch (a.n / 1024u) {
+            case 1: k_seq_rmsnorm4<1><<<tokens, 256, 0, s>>>(a); break;
+            case 2: k_seq_rmsnorm4<2><<<tokens, 256, 0, s>>>(a); break;
+            case 3: k_seq_rmsnorm4<3><<<tokens, 256, 0, s>>>(a); break;
+            default: k_seq_rmsnorm4<4><<<tokens, 256, 0, s>>>(a); break;
+        }
+        VX_LAUNCHED("k_seq_rmsnorm4");
+        return VX_OK;
+    }
     k_seq_rmsnorm<<<tokens, 256, 0, s>>>(a);
     VX_LAUNCHED("k_seq_rmsnorm");
     return VX_OK;
@@ -929,6 +1022,7 @@ int launch_prefill_attn(hipStream_t s, const PrefillAttnArgs &a) {
         return fail(VX_ERR_CONTEXT_FULL, "prefill attention: positions beyond the context");
     if (a.oh && !a.ol) return fail(VX_ERR_INVALID_ARG, "prefill attention: plane output incomplete");
     if (a.ldq % 8u || a.ldo % 4u) return fail(VX_ERR_INVALID_ARG, "prefill attention: row strides");
+    if (a.oh && a.tiled && a.ldo % 32u) return fail(VX_ERR_INVALID_ARG, "prefill attention: tiled planes need width %% 32");
 #define VX_ATTN_CASE(HDV, QPKV)                                                                  \
     if (a.head_dim == HDV && qpk == QPKV) {                                                      \
         dim3 g((a.T + (32u / QPKV) - 1u) / (32u / QPKV), a.kv_heads);                            \

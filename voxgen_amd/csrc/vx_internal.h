@@ -280,6 +280,8 @@ enum GemmEpilogue : uint32_t {
 struct GemmSeg {                    // one weight matrix covering part of N
     const int8_t *qs = nullptr;     // Q8_0: repacked quants (WRef::ptr) ...
     const __half *d = nullptr;      // ... and scales (WRef::d)
+    const int8_t *pq = nullptr;     // Q8_0 in the prefill-GEMM layout (PrefillMatrix), nullable ...
+    const float *pd = nullptr;      // ... and its f32 scales
     const __half *w = nullptr;      // F16: [rows][K]
     uint32_t rows = 0;
     uint32_t tile0 = 0;             // set by launch_gemm
@@ -303,8 +305,47 @@ struct GemmArgs {
     uint32_t ldp = 0;
     uint32_t ksplit = 1;
     uint32_t ntn = 0, ntm = 0;                  // set by launch_gemm
+    uint32_t x_tiled = 0;           // 1: xh/xl are in the tiled plane layout (tiled_plane_index)
+    uint32_t o_tiled = 0;           // 1: GEPI_SWIGLU writes oh/ol in the tiled plane layout
+    // GEPI_RESIDUAL with ksplit > 1 on the prefill-layout kernel: when set, split
+    // s stores scale * (its partial product) to ws + s * ws_stride ([T][ldo]) with
+    // plain stores instead of adding to out; the consumer adds the partials.
+    float *ws = nullptr;
+    uint64_t ws_stride = 0;
 };
 int launch_gemm(hipStream_t s, const GemmArgs &a);
+// Tiled hi/lo plane layout read by the prefill GEMM (kernels_gemm.hip):
+// f16 [T/128][K/32][128][32], i.e. one contiguous 8 KB piece per (128-token
+// tile, 32-column block); the four 8-column chunks of a token's 32 values are
+// permuted by the token's index in the tile (chunk c stored at c ^ f(t),
+// f(t) = ((t >> 1) ^ (t >> 3)) & 3), which makes the GEMM's fragment reads
+// conflict-free once the piece is copied to LDS. T is padded to a multiple of 128.
+__host__ __device__ __forceinline__ size_t tiled_plane_index(uint32_t t, uint32_t c, uint32_t K) {
+    const uint32_t ti = t & 127u, f = ((ti >> 1) ^ (ti >> 3)) & 3u;
+    return ((((size_t)(t >> 7) * (K >> 5) + (c >> 5)) << 7) + ti) * 32u + 8u * (((c >> 3) & 3u) ^ f) + (c & 7u);
+}
+// Q8_0 matrix in the prefill-GEMM layout: quants int8 [rows_pad/128][K/32][128][32]
+// (one contiguous 4 KB piece per 128-row tile and 32-column block; the four
+// 8-byte chunks of a row permuted as chunk c at c ^ g(n), g(n) = ((n >> 2) ^
+// (n >> 4)) & 3 for row n of the tile), scales f32 [rows_pad/128][K/32][128].
+// With interleave, rows come from two matrices (gate, up) as 32 of the first,
+// the same 32 of the second, and so on, the row order of a SwiGLU tile.
+// Padding rows are zero.
+struct PrefillMatrix {
+    int8_t *q = nullptr;
+    float *d = nullptr;
+    uint32_t rows_pad = 0;
+};
+uint64_t prefill_matrix_bytes(uint32_t rows_out, uint32_t K);   // q + d, rows padded to 128
+int launch_repack_prefill(hipStream_t s, const uint8_t *raw, uint32_t off0, uint32_t off1, uint32_t rows,
+                          uint32_t K, int interleave, int8_t *q, float *d);
+// The deep-pipelined Q8_0 x hi/lo-plane GEMM (kernels_gemm.hip), which
+// launch_gemm picks when the weights have the prefill layout and X is tiled.
+bool gemm_q8p_eligible(const GemmArgs &a);
+uint32_t gemm_q8p_tile_tokens();
+int launch_gemm_q8p(hipStream_t s, GemmArgs a);
+// Tokens per workgroup tile of the kernel launch_gemm picks for these arguments.
+uint32_t gemm_tile_tokens(const GemmArgs &a);
 
 struct SeqNormArgs {
     float *h = nullptr;             // [T][ldh] input (and residual stream when branch is set)
@@ -312,16 +353,20 @@ struct SeqNormArgs {
     const float *branch = nullptr;  // nullable: h += scale * branch first
     uint32_t ldb = 0;
     float scale = 1.f;
-    const float *w = nullptr;       // f32 gains [n]
+    uint32_t nbranch = 1;           // branches added (at branch + i * branch_stride), when branch is set
+    uint64_t branch_stride = 0;
+    const float *w = nullptr;       // f32 gains [n], nullable: only the residual update
     uint32_t n = 0;
     float eps = 0.f;
     float *y = nullptr;             // nullable f32 output [T][ldy]
     uint32_t ldy = 0;
     __half *yh = nullptr, *yl = nullptr;   // nullable hi/lo planes [T][ldp]
     uint32_t ldp = 0;
+    uint32_t tiled = 0;             // 1: planes in the tiled layout of width n (ldp unused)
     float *zero[3] = {nullptr, nullptr, nullptr};   // rows of split-K accumulators to clear
     uint32_t zero_n[3] = {0, 0, 0};
 };
+constexpr uint32_t kSeqNormMaxBranch = 8;
 int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens);
 
 struct SeqRopeArgs {
@@ -349,6 +394,7 @@ struct PrefillAttnArgs {
     float *out = nullptr;                       // nullable f32 [T][ldo]
     __half *oh = nullptr, *ol = nullptr;        // nullable planes [T][ldo]
     uint32_t ldo = 0;
+    uint32_t tiled = 0;                         // 1: planes in the tiled layout of width ldo
 };
 int launch_prefill_attn(hipStream_t s, const PrefillAttnArgs &a);
 // seq_linear_bias.comp / seq_swiglu.comp for any shape and dtype, one wave per
@@ -421,10 +467,12 @@ int launch_repack_q8(hipStream_t s, const uint8_t *raw_tensor, uint32_t rows, ui
                      int8_t *qs, __half *d);
 
 // ------------------------------------- persistent decode step (kernels_persist.hip)
-// Every layer of one decode step in one launch of one workgroup per CU. Phase
-// completion is counted on 8 per-XCD counters per phase, 128 bytes apart.
+// Every layer of one decode step in one launch of kPersistGroups workgroups per CU
+// (groups take phases in turn). Phase completion is counted on 8 per-XCD
+// counters per phase, 128 bytes apart.
 constexpr uint32_t kPersistCntStride = 256;   // uints per phase
 constexpr uint32_t kPersistPhases = 5;        // per layer: qkv, attention, attn_out, swiglu, down
+constexpr uint32_t kPersistGroups = 1;        // workgroup groups (one workgroup per CU each)
 struct PLayer {                               // repacked Q8_0 matrices of one layer
     const void *q, *k, *v, *o, *g, *u, *dn;
     const __half *qd, *kd, *vd, *od, *gd, *ud, *dnd;
@@ -445,12 +493,13 @@ struct PersistArgs {
     unsigned *err = nullptr;                  // sticky: nonzero after a wait timed out
     // Nullable phase timeline for profiling: per workgroup and phase, the 100 MHz
     // device clock at phase start, after its wait and after its completion count.
-    unsigned long long *trace = nullptr;      // [grid][n_layers * 5][4]
+    unsigned long long *trace = nullptr;      // [grid][n_layers * 5][4] (the running group's rows)
 };
 uint64_t persist_counter_words(uint32_t n_layers, uint32_t q_heads);
-// Whether the persistent step is compiled for this geometry on `grid` workgroups.
-bool persistent_supported(uint32_t H, uint32_t F, uint32_t KV, uint32_t q_heads, uint32_t head_dim, uint32_t grid);
-int launch_decode_persistent(hipStream_t s, const PersistArgs &a, uint32_t grid);
+// Whether the persistent step is compiled for this geometry with `cus` workgroups
+// per group; the launch grid is kPersistGroups * cus.
+bool persistent_supported(uint32_t H, uint32_t F, uint32_t KV, uint32_t q_heads, uint32_t head_dim, uint32_t cus);
+int launch_decode_persistent(hipStream_t s, const PersistArgs &a, uint32_t cus);
 int persistent_occupancy(int *blocks_per_cu);
 
 }  // namespace vx
