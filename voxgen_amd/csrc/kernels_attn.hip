@@ -3,9 +3,10 @@
 // k_attn_chunk: grid = splits x q_heads. Each workgroup takes one query head and
 // one contiguous slice of the context [0, position] and runs an online softmax
 // over 64-key tiles of it: the 256 threads are 64 keys x 4 quarters of the head
-// dimension for the scores (a quad reduction per key), then head_dim dims x
-// 256/head_dim key groups for P.V out of LDS. It writes one (max, sum, acc)
-// partial per (head, slice). Every load a tile needs (q, K and V rows) is issued
+// dimension for the scores (a quad reduction per key; lane r of a quad holds dims
+// 8(r + 4i)..+7, so each load of the quad reads 64 contiguous bytes), then
+// head_dim dims x 256/head_dim key groups for P.V out of LDS. It writes one
+// (max, sum, acc) partial per (head, slice). Every load a tile needs (q, K and V rows) is issued
 // before any of it is used. The GQA map is attn_scores.comp's kvh = qh / q_per_kv.
 // k_attn_combine merges the slices of each head; the engine's decode step folds
 // that merge into the attn_out matvec instead (k_attn_out in kernels_matvec.hip).
@@ -113,10 +114,12 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const int j = tid >> 2, r = tid & 3;
 
     // q quarter (independent of the position) and the position, issued together.
+    // Element 8k + e of quarter r is dimension 8(r + 4k) + e, so the four lanes of
+    // a key read 64 contiguous bytes of its row per load.
     float qv[R];
 #pragma unroll
     for (int i = 0; i < R; i += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + r * R + i);
+        const float4 v = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * (r + 4 * (i >> 3)) + (i & 7));
         qv[i] = v.x;
         qv[i + 1] = v.y;
         qv[i + 2] = v.z;
@@ -133,12 +136,12 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     for (uint32_t tb = t0; tb < t1; tb += kTile) {
         const uint32_t key = tb + (uint32_t)j;
         const bool valid = key < t1;
-        const size_t row = (layer_base + (valid ? key : t0)) * kv_dim + (size_t)kvh * HD + (size_t)r * R;
+        const size_t row = (layer_base + (valid ? key : t0)) * kv_dim + (size_t)kvh * HD + (size_t)r * 8;
         uint4 kw[R / 8], vw[R / 8];
 #pragma unroll
         for (int i = 0; i < R / 8; ++i) {
-            kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 8 * i);
-            vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 8 * i);
+            kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
+            vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
         }
         // Score of key j: quarter dot product, then a quad reduction.
         float d0 = 0.f, d1 = 0.f;
@@ -163,7 +166,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         const float p = valid ? expf(sc - m_new) : 0.f;
         // V rows of the tile and p to LDS; each key's p counted once (quarter 0).
 #pragma unroll
-        for (int i = 0; i < R / 8; ++i) *reinterpret_cast<uint4 *>(&vs[j][r * R + 8 * i]) = vw[i];
+        for (int i = 0; i < R / 8; ++i) lds_st16(&vs[j][8 * (r + 4 * i)], vw[i]);
         if (r == 0) ps[j] = p;
         const float ws = wave_sum_dpp(r == 0 ? p : 0.f);
         if (lane == 0) red[1][wave] = ws;

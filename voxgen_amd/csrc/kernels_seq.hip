@@ -209,7 +209,7 @@ __device__ __forceinline__ void store_stage(const StageRegs<WK, XF32> &r, _Float
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t c = tid + 256u * i, rho = c >> 4, p = c & 15u;
-            *reinterpret_cast<uint4 *>(Wl + rho * LROW + 8u * p) = r.w[i];
+            lds_st16(Wl + rho * LROW + 8u * p, r.w[i]);
         }
     }
     if constexpr (XF32) {
@@ -225,8 +225,8 @@ __device__ __forceinline__ void store_stage(const StageRegs<WK, XF32> &r, _Float
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t c = tid + 256u * i, t = c >> 4, kk = (c >> 2) & 3u, q = c & 3u;
-            *reinterpret_cast<uint4 *>(Xh + t * LROW + 32u * kk + 8u * q) = r.x[i];
-            *reinterpret_cast<uint4 *>(Xl + t * LROW + 32u * kk + 8u * q) = r.x[4 + i];
+            lds_st16(Xh + t * LROW + 32u * kk + 8u * q, r.x[i]);
+            lds_st16(Xl + t * LROW + 32u * kk + 8u * q, r.x[4 + i]);
         }
     }
 }

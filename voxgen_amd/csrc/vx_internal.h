@@ -194,6 +194,17 @@ struct QkvFusedLaunch {
 };
 int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &a);
 
+// 16-byte store to LDS written as four dwords (the compiler still emits one
+// ds_write_b128). Assigning a HIP uint4 through a reinterpret_cast pointer into an
+// f16 LDS array kept the source registers in scratch memory.
+__device__ __forceinline__ void lds_st16(void *p, const uint4 &v) {
+    uint32_t *d = static_cast<uint32_t *>(p);
+    d[0] = v.x;
+    d[1] = v.y;
+    d[2] = v.z;
+    d[3] = v.w;
+}
+
 struct AttnLaunch {
     const float *q = nullptr;
     const __half *kc = nullptr, *vc = nullptr;
