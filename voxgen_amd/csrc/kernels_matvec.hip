@@ -488,7 +488,7 @@ int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
             break;
         case 3: VX_MV(3, 2); break;
         case 4: VX_MV(4, 2); break;
-        case 6: VX_MV(6, 2); break;
+        case 6: VX_MV(6, 1); break;   // one row per wave: 512 workgroups for 2048 rows
         default: VX_MV(8, 1); break;
     }
 #undef VX_MV
@@ -582,7 +582,7 @@ int launch_swiglu(hipStream_t s, const SwigluLaunch &l) {
 #define VX_SW_NG(WTV)                          \
     switch (ng) {                              \
         case 1: VX_SW(WTV, 1, 2); break;       \
-        case 2: VX_SW(WTV, 2, 2); break;       \
+        case 2: VX_SW(WTV, 2, 1); break;       \
         case 3: VX_SW(WTV, 3, 2); break;       \
         case 4: VX_SW(WTV, 4, 2); break;       \
         case 6: VX_SW(WTV, 6, 1); break;       \
