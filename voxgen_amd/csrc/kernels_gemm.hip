@@ -18,14 +18,21 @@
 //     stage global -> LDS by the DMA path (global_load_lds: no registers, no
 //     VALU, every fetched byte used) into a ring of kStages LDS slots,
 //     kStages - 1 stages ahead of the one being multiplied;
-//   * the quants stay int8 in LDS (a quarter of the f16 footprint, which is
-//     what fits two workgroups per CU) and are widened when a wave reads its B
-//     fragment;
+//   * the quants stay 8-bit in LDS (stored as q + 128; a quarter of the f16
+//     footprint, which is what fits two workgroups per CU) and are widened when
+//     a wave reads its B fragment;
 //   * both layouts carry a permutation so every fragment read from LDS is free
-//     of bank conflicts (for 32 and for 64 banks) after a verbatim copy.
+//     of bank conflicts (for 32 and for 64 banks) after a verbatim copy;
+//   * the VALU work of a block (64 scale FMAs and the quant widening per lane)
+//     is as long as its 16 MFMAs and a wave issues both in order, so the block
+//     loop is unrolled over the ring slots (constant LDS offsets, no address
+//     VALU), the DMA addresses are scalar, and the block is split by output
+//     half so that scale FMAs and widening issue between MFMAs.
 // Measured alternatives, slower on MI355X at T = 384: 16-column stages, one
-// workgroup per CU with a deeper ring, f16 quants in LDS, and weights as exact
-// hi/lo f16 pairs of d*q (three MFMAs per k-step, no scale step).
+// workgroup per CU with a deeper ring (up to 7 slots), f16 quants in LDS,
+// weights as exact hi/lo f16 pairs of d*q (three MFMAs per k-step, no scale
+// step), fragments prefetched a block ahead, double-buffered block products,
+// and split K to put two workgroups on every CU.
 #include <type_traits>
 
 #include "vx_internal.h"
@@ -53,10 +60,9 @@ constexpr int kOpsPerStage = 6;                // DMA instructions per wave per 
 __device__ __forceinline__ uint32_t xperm(uint32_t t) { return ((t >> 1) ^ (t >> 3)) & 3u; }
 __device__ __forceinline__ uint32_t wperm(uint32_t n) { return ((n >> 2) ^ (n >> 4)) & 3u; }
 
-// Four signed int8 quants (one dword) -> four exact f16 values: (q ^ 0x80) is
-// q + 128 in 0..255; the f16 with bits 0x6400 | u is 1024 + u, minus 1152 = q.
-__device__ __forceinline__ uint2 q8x4_to_f16(uint32_t w) {
-    const uint32_t u = w ^ 0x80808080u;
+// Four stored quants u = q + 128 (one dword) -> four exact f16 values q: the f16
+// with bits 0x6400 | u is 1024 + u, minus 1152 = q.
+__device__ __forceinline__ uint2 q8x4_to_f16(uint32_t u) {
     const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
     const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
     const h2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
@@ -97,34 +103,45 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
-// (An LDS DMA may not read M0 in the instruction right after the write: one
-// wait state between them.)
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+// The global address is a wave-uniform base in an SGPR pair plus a per-lane
+// 32-bit offset, so advancing a stream by one block is scalar arithmetic. (An
+// LDS DMA may not read M0 in the instruction right after the write: one wait
+// state between them.)
+__device__ __forceinline__ void dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds)
+__device__ __forceinline__ void dma4(const uint8_t *base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                  : "memory", "m0");
+}
+// A pointer that is the same in every lane, made explicitly wave-uniform.
+__device__ __forceinline__ const uint8_t *uniform_ptr(const void *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
 }
 
 // Stage b (32-column block) of the tile: wave w copies X pieces 4w .. 4w + 3
 // (1 KB each, plane = piece / 8), quant piece w (1 KB), and one 256 B half of
-// the scales (waves 2 and 3 repeat what waves 0 and 1 copy).
+// the scales (waves 2 and 3 repeat what waves 0 and 1 copy). Bases are the
+// wave's pieces at block 0; lane i adds 16 i (4 i for the scales).
 struct Src {
-    const uint8_t *x[4];   // X plane piece + 16 * lane
-    const uint8_t *w;      // quants + 1024 * wave + 16 * lane
-    const uint8_t *d;      // scales + 256 * (wave & 1) + 4 * lane
+    const uint8_t *x[4];   // X plane piece
+    const uint8_t *w;      // quants + 1024 * wave
+    const uint8_t *d;      // scales + 256 * (wave & 1)
 };
 
-__device__ __forceinline__ void issue_stage(const Src &src, uint32_t blk, uint32_t slot, uint32_t wave) {
+__device__ __forceinline__ void issue_stage(const Src &src, uint32_t blk, uint32_t slot, uint32_t wave,
+                                            uint32_t lane) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t u = 4u * wave + (uint32_t)j;
-        dma16(src.x[j] + (size_t)blk * kXBytes, slot + kXOff + (u >> 3) * kXBytes + (u & 7u) * 1024u);
+        dma16(src.x[j] + (size_t)blk * kXBytes, 16u * lane, slot + kXOff + (u >> 3) * kXBytes + (u & 7u) * 1024u);
     }
-    dma16(src.w + (size_t)blk * kWBytes, slot + kWOff + wave * 1024u);
-    dma4(src.d + (size_t)blk * kDBytes, slot + kDOff + (wave & 1u) * 256u);
+    dma16(src.w + (size_t)blk * kWBytes, 16u * lane, slot + kWOff + wave * 1024u);
+    dma4(src.d + (size_t)blk * kDBytes, 4u * lane, slot + kDOff + (wave & 1u) * 256u);
 }
 
 template <int EPI>
@@ -155,7 +172,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave & 1u, wn = wave >> 1;
 
-    // ---- DMA sources of this tile at block 0
+    // ---- DMA sources of this tile at block 0 (wave-uniform bases)
     Src src;
     {
         const uint32_t lt = EPI == GEPI_SWIGLU ? tn : tn - sg.tile0;   // tile within the matrix
@@ -163,11 +180,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
         for (int j = 0; j < 4; ++j) {
             const uint32_t u = 4u * wave + (uint32_t)j;
             const uint8_t *plane = reinterpret_cast<const uint8_t *>((u >> 3) ? a.xl : a.xh);
-            src.x[j] = plane + ((size_t)tm * nblk) * kXBytes + (u & 7u) * 1024u + 16u * lane;
+            src.x[j] = uniform_ptr(plane + ((size_t)tm * nblk) * kXBytes + (u & 7u) * 1024u);
         }
-        src.w = reinterpret_cast<const uint8_t *>(sg.pq) + ((size_t)lt * nblk) * kWBytes + 1024u * wave + 16u * lane;
-        src.d = reinterpret_cast<const uint8_t *>(sg.pd) + ((size_t)lt * nblk) * kDBytes + 256u * (wave & 1u) +
-                4u * lane;
+        src.w = uniform_ptr(reinterpret_cast<const uint8_t *>(sg.pq) + ((size_t)lt * nblk) * kWBytes + 1024u * wave);
+        src.d = uniform_ptr(reinterpret_cast<const uint8_t *>(sg.pd) + ((size_t)lt * nblk) * kDBytes +
+                            256u * (wave & 1u));
     }
 
     // ---- fragment addresses inside a stage slot: k-step e covers columns
@@ -192,57 +209,105 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
     // number of DMA instructions per stage, which the vmcnt waits count on)
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s)
-        issue_stage(src, kb0 + ((uint32_t)s < nkb ? (uint32_t)s : nkb - 1u), ring_lds + (uint32_t)s * kStageBytes, wave);
+        issue_stage(src, kb0 + ((uint32_t)s < nkb ? (uint32_t)s : nkb - 1u), ring_lds + (uint32_t)s * kStageBytes, wave,
+                    lane);
 
     acc16 acc[2][2], p[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = acc16{};
+        for (int j = 0; j < 2; ++j) acc[i][j] = p[i][j] = acc16{};
+    float dprev1 = 0.f;   // scale of the previous block's second output half
 
-    // One block: wait for its slot, refill the slot consumed last, two MFMA
-    // k-steps per plane into p, then acc += d * p. The wait also drains this
-    // wave's LDS reads of the slot about to be refilled.
-    for (uint32_t it = 0; it < nkb; ++it) {
+    // One block in ring slot SL (compile-time, so every LDS address is a base
+    // register plus an immediate): wait for its DMA, refill the slot consumed
+    // last, read the fragments, then
+    //   widen the quants of output half 0;
+    //   MFMAs of half 0, interleaved with the previous block's half-1 scale FMAs
+    //   (acc += d * p) and the widening of half 1;
+    //   MFMAs of half 1, interleaved with this block's half-0 scale FMAs.
+    // A wave issues VALU and MFMA work in order, so this keeps its VALU work in
+    // the gaps between matrix instructions; half 1's scale FMAs wait for the
+    // next block (or the end of the loop).
+    auto block = [&](uint32_t it, auto slot_c) {
+        constexpr uint32_t SL = decltype(slot_c)::value;
+        __builtin_amdgcn_sched_barrier(0);
         wait_vm<kOpsPerStage * (kStages - 2), true>();
         __builtin_amdgcn_s_barrier();
         const uint32_t nxt = it + kStages - 1u;
-        issue_stage(src, kb0 + (nxt < nkb ? nxt : nkb - 1u), ring_lds + (nxt % kStages) * kStageBytes, wave);
-        const uint8_t *slot = ring + (it % kStages) * kStageBytes;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) p[i][j] = acc16{};
+        issue_stage(src, kb0 + (nxt < nkb ? nxt : nkb - 1u), ring_lds + ((SL + kStages - 1u) % kStages) * kStageBytes,
+                    wave, lane);
+        const uint8_t *slot = ring + SL * kStageBytes;
+        uint2 q[2][2];
+        h8 ah[2][2], al[2][2], bf[2][2];   // [e][nt], [e][mt], [e][mt], [e][nt]
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            h8 bf[2];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const uint2 q = *reinterpret_cast<const uint2 *>(slot + wa[nt][e]);
-                const uint2 f0 = q8x4_to_f16(q.x), f1 = q8x4_to_f16(q.y);
-                bf[nt] = __builtin_bit_cast(h8, make_uint4(f0.x, f0.y, f1.x, f1.y));
-            }
+            for (int nt = 0; nt < 2; ++nt) q[e][nt] = *reinterpret_cast<const uint2 *>(slot + wa[nt][e]);
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
-                const h8 ah = *reinterpret_cast<const h8 *>(slot + xa[mt][e]);
-                const h8 al = *reinterpret_cast<const h8 *>(slot + xa[mt][e] + kXBytes);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    p[mt][nt] = mfma(ah, bf[nt], p[mt][nt]);
-                    p[mt][nt] = mfma(al, bf[nt], p[mt][nt]);
-                }
+                ah[e][mt] = *reinterpret_cast<const h8 *>(slot + xa[mt][e]);
+                al[e][mt] = *reinterpret_cast<const h8 *>(slot + xa[mt][e] + kXBytes);
             }
         }
-        float d[2];
+        const float d0 = *reinterpret_cast<const float *>(slot + da[0]);
+        const float d1 = *reinterpret_cast<const float *>(slot + da[1]);
+        auto widen = [&](int nt) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) d[nt] = *reinterpret_cast<const float *>(slot + da[nt]);
+            for (int e = 0; e < 2; ++e) {
+                const uint2 f0 = q8x4_to_f16(q[e][nt].x), f1 = q8x4_to_f16(q[e][nt].y);
+                bf[e][nt] = __builtin_bit_cast(h8, make_uint4(f0.x, f0.y, f1.x, f1.y));
+            }
+        };
+        auto mfmas = [&](int nt) {   // no two dependent MFMAs adjacent
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+            for (int e = 0; e < 2; ++e) {
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+                for (int mt = 0; mt < 2; ++mt) p[mt][nt] = mfma(ah[e][mt], bf[e][nt], e == 0 ? acc16{} : p[mt][nt]);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[mt][nt][r] = fmaf(d[nt], p[mt][nt][r], acc[mt][nt][r]);
+                for (int mt = 0; mt < 2; ++mt) p[mt][nt] = mfma(al[e][mt], bf[e][nt], p[mt][nt]);
+            }
+        };
+        auto scale = [&](int nt, float d) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[mt][nt][r] = fmaf(d, p[mt][nt][r], acc[mt][nt][r]);
+        };
+        widen(0);
+        __builtin_amdgcn_sched_barrier(0);
+        scale(1, dprev1);   // reads p[.][1] before this block's half-1 MFMAs rewrite it
+        widen(1);
+        mfmas(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // then six VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        scale(0, d0);
+        mfmas(1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+        dprev1 = d1;
+    };
+    static_assert(kStages == 3, "the block loop is unrolled over three ring slots");
+    uint32_t it = 0;
+    for (; it + 3u <= nkb; it += 3u) {
+        block(it, std::integral_constant<uint32_t, 0>{});
+        block(it + 1u, std::integral_constant<uint32_t, 1>{});
+        block(it + 2u, std::integral_constant<uint32_t, 2>{});
     }
+    if (it < nkb) block(it, std::integral_constant<uint32_t, 0>{});
+    if (it + 1u < nkb) block(it + 1u, std::integral_constant<uint32_t, 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mt][1][r] = fmaf(dprev1, p[mt][1][r], acc[mt][1][r]);
     // Drain the DMA of the clamped trailing stages before the workgroup ends.
     wait_vm<0>();
 
@@ -319,13 +384,14 @@ __global__ __launch_bounds__(256) void k_repack_prefill(const uint8_t *raw, uint
     const bool live = row < rows;
     const uint8_t *b = raw + (mat ? off1 : off0) + ((size_t)(live ? row : 0u) * nb + blk) * 34u;
     const uint32_t g = wperm(n);
-    uint32_t w[8];   // stored chunk sc holds source chunk sc ^ g
+    uint32_t w[8];   // stored chunk sc holds source chunk sc ^ g, each byte q + 128
 #pragma unroll
     for (int sc = 0; sc < 4; ++sc) {
         const uint32_t src = 2u + 8u * ((uint32_t)sc ^ g);
-        w[2 * sc] = live ? (b[src] | (b[src + 1] << 8) | (b[src + 2] << 16) | ((uint32_t)b[src + 3] << 24)) : 0u;
-        w[2 * sc + 1] =
-            live ? (b[src + 4] | (b[src + 5] << 8) | (b[src + 6] << 16) | ((uint32_t)b[src + 7] << 24)) : 0u;
+        const uint32_t lo = b[src] | (b[src + 1] << 8) | (b[src + 2] << 16) | ((uint32_t)b[src + 3] << 24);
+        const uint32_t hi = b[src + 4] | (b[src + 5] << 8) | (b[src + 6] << 16) | ((uint32_t)b[src + 7] << 24);
+        w[2 * sc] = (live ? lo : 0u) ^ 0x80808080u;
+        w[2 * sc + 1] = (live ? hi : 0u) ^ 0x80808080u;
     }
     uint4 *dst = reinterpret_cast<uint4 *>(q + i * 32u);
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);

@@ -335,13 +335,14 @@ __host__ __device__ __forceinline__ size_t tiled_plane_index(uint32_t t, uint32_
     const uint32_t ti = t & 127u, f = ((ti >> 1) ^ (ti >> 3)) & 3u;
     return ((((size_t)(t >> 7) * (K >> 5) + (c >> 5)) << 7) + ti) * 32u + 8u * (((c >> 3) & 3u) ^ f) + (c & 7u);
 }
-// Q8_0 matrix in the prefill-GEMM layout: quants int8 [rows_pad/128][K/32][128][32]
+// Q8_0 matrix in the prefill-GEMM layout: quants stored as q + 128 (uint8, the
+// sign bit flipped) [rows_pad/128][K/32][128][32]
 // (one contiguous 4 KB piece per 128-row tile and 32-column block; the four
 // 8-byte chunks of a row permuted as chunk c at c ^ g(n), g(n) = ((n >> 2) ^
 // (n >> 4)) & 3 for row n of the tile), scales f32 [rows_pad/128][K/32][128].
 // With interleave, rows come from two matrices (gate, up) as 32 of the first,
 // the same 32 of the second, and so on, the row order of a SwiGLU tile.
-// Padding rows are zero.
+// Padding rows hold q = 0 (byte 0x80) with scale 0.
 struct PrefillMatrix {
     int8_t *q = nullptr;
     float *d = nullptr;
