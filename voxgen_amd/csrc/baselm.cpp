@@ -60,7 +60,7 @@ struct vx_baselm {
     vx_buf *pf_h = nullptr, *pf_xh = nullptr, *pf_xl = nullptr, *pf_ah = nullptr, *pf_al = nullptr;
     vx_buf *pf_qh = nullptr, *pf_ql = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
     vx_buf *pf_tok = nullptr;
-    vx_buf *pf_ws = nullptr;   // split-K partials of the residual projections [kPrefillMaxSplit][cap][H]
+    vx_buf *pf_ws = nullptr;   // split-K partials of the projections [kPrefillMaxSplit][cap][H + 2 KV]
     // Q8_0 weights in the prefill-GEMM layout (built by the first batched prefill
     // that can use them; empty when some projection is not Q8_0).
     struct PrefillLayer {
@@ -669,7 +669,9 @@ int ensure_prefill_work(vx_baselm *e) {
     VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_k));
     VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_v));
     VX_CHECK(alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->pf_tok));
-    VX_CHECK(alloc(ctx, (uint64_t)kPrefillMaxSplit * T * H * 4u, &e->pf_ws));
+    // Split-K partials: of the residual projections ([split][T][H]) and of QKV
+    // ([split][T][H + 2 KV]); the two uses never overlap in time.
+    VX_CHECK(alloc(ctx, (uint64_t)kPrefillMaxSplit * T * (H + 2u * e->cfg.kv_dim) * 4u, &e->pf_ws));
     e->pf_cap = cap;
     return VX_OK;
 }
@@ -787,6 +789,11 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
     // pf_ws; the next rmsnorm adds them to h (no atomics in the GEMM epilogue).
     const uint64_t ws_stride = (uint64_t)e->pf_cap * nH;
     const bool ws_o = tiled && ks_o > 1, ws_down = tiled && ks_down > 1;
+    // Split QKV on the tiled path stores its partials to pf_ws as well (q, k, v
+    // regions of one split, ws_qkv floats per split); the RoPE kernel sums them.
+    const bool ws_qkv = tiled && ks_qkv > 1;
+    const uint64_t ws_qkv_stride = (uint64_t)e->pf_cap * (nH + 2u * nKV);
+    float *const wq = F(e->pf_ws), *const wk = wq + (size_t)e->pf_cap * nH, *const wv = wk + (size_t)e->pf_cap * nKV;
     for (uint32_t l = 0; l < c.block_count; ++l) {
         const Layer &L = e->layers[l];
         {
@@ -807,7 +814,7 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             n.yl = H(e->pf_xl);
             n.ldp = nH;
             n.tiled = tiled ? 1u : 0u;
-            if (ks_qkv > 1) {
+            if (ks_qkv > 1 && !ws_qkv) {
                 n.zero[0] = F(e->pf_q);
                 n.zero_n[0] = nH;
                 n.zero[1] = F(e->pf_k);
@@ -842,14 +849,25 @@ int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint
             g.xl = H(e->pf_xl);
             g.ldx = nH;
             g.ksplit = ks_qkv;
+            if (ws_qkv) {
+                g.seg[0].out = wq;
+                g.seg[1].out = wk;
+                g.seg[2].out = wv;
+                g.split_store = 1;
+                g.ws_stride = ws_qkv_stride;
+            }
             VX_CHECK(launch_gemm(s, g));
         }
         {
             ProfSpan sp(ctx, "prefill.rope_store");
             SeqRopeArgs r;
-            r.q = F(e->pf_q);
-            r.k = F(e->pf_k);
-            r.v = F(e->pf_v);
+            r.q = ws_qkv ? wq : F(e->pf_q);
+            r.k = ws_qkv ? wk : F(e->pf_k);
+            r.v = ws_qkv ? wv : F(e->pf_v);
+            if (ws_qkv) {
+                r.nsplit = ks_qkv;
+                r.split_stride = ws_qkv_stride;
+            }
             r.ldq = nH;
             r.ldk = nKV;
             r.factors = e->rope_factors;

@@ -352,10 +352,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
                     float *dst = out0 + (size_t)tok * ldo0 + row;
                     if constexpr (EPI == GEPI_STORE) {
                         const float v = acc[mt][nt][r] * a.alpha;
-                        if (a.ksplit > 1)
-                            unsafeAtomicAdd(dst, v);
-                        else
+                        if (a.ksplit == 1)
                             *dst = v;
+                        else if (a.split_store)
+                            dst[ks * a.ws_stride] = v;
+                        else
+                            unsafeAtomicAdd(dst, v);
                     } else if (a.ws && a.ksplit > 1) {
                         a.ws[ks * a.ws_stride + (size_t)tok * ldo0 + row] = acc[mt][nt][r] * a.scale;
                     } else {

@@ -504,13 +504,28 @@ __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
     float *q = a.q + (size_t)t * a.ldq;
     float *k = a.k + (size_t)t * a.ldk;
     const uint32_t q_pairs = a.q_heads * half_dim, k_pairs = a.kv_heads * half_dim;
+    const uint32_t ns = a.nsplit ? a.nsplit : 1u;
     for (uint32_t p = threadIdx.x; p < q_pairs + k_pairs; p += 256u) {
         const bool isq = p < q_pairs;
         const uint32_t pp = isq ? p : p - q_pairs;
         const uint32_t head = pp / half_dim, i = pp - head * half_dim;
         float *buf = isq ? q : k;
         const uint32_t base = head * a.head_dim;
-        const float x0 = buf[base + i], x1 = buf[base + i + half_dim];
+        // split-K partials (at most kSeqRopeMaxSplit), all loads issued together,
+        // summed in split order
+        float p0[kSeqRopeMaxSplit], p1[kSeqRopeMaxSplit];
+#pragma unroll
+        for (uint32_t sp = 0; sp < kSeqRopeMaxSplit; ++sp) {
+            const size_t o = (size_t)(sp < ns ? sp : 0u) * a.split_stride + base + i;
+            p0[sp] = buf[o];
+            p1[sp] = buf[o + half_dim];
+        }
+        float x0 = p0[0], x1 = p1[0];
+#pragma unroll
+        for (uint32_t sp = 1; sp < kSeqRopeMaxSplit; ++sp) {
+            x0 += sp < ns ? p0[sp] : 0.f;
+            x1 += sp < ns ? p1[sp] : 0.f;
+        }
         const float c = cs[i].x, s = cs[i].y;
         const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
         if (isq) {
@@ -538,8 +553,14 @@ __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
     const uint32_t kv_dim = a.kv_heads * a.head_dim;
     const size_t dst = ((size_t)a.layer * a.context + pos) * kv_dim;
     for (uint32_t i = threadIdx.x; i < kv_dim; i += 256u) {
+        float pv[kSeqRopeMaxSplit];
+#pragma unroll
+        for (uint32_t sp = 0; sp < kSeqRopeMaxSplit; ++sp) pv[sp] = v[(size_t)(sp < ns ? sp : 0u) * a.split_stride + i];
+        float vv = pv[0];
+#pragma unroll
+        for (uint32_t sp = 1; sp < kSeqRopeMaxSplit; ++sp) vv += sp < ns ? pv[sp] : 0.f;
         a.kc[dst + i] = __float2half_rn(k[i]);
-        a.vc[dst + i] = __float2half_rn(v[i]);
+        a.vc[dst + i] = __float2half_rn(vv);
     }
 }
 
@@ -906,6 +927,8 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
             return fail(VX_ERR_INVALID_ARG, "gemm: segment %u weight pointers missing", i);
     }
     if (gemm_q8p_eligible(a)) return launch_gemm_q8p(s, a);
+    if (a.split_store && a.ksplit > 1)
+        return fail(VX_ERR_INVALID_ARG, "gemm: split partial stores need the prefill-layout Q8_0 kernel");
     const uint32_t stages = a.K / GK;
     if (a.ksplit == 0) a.ksplit = 1;
     if (a.ksplit > stages) a.ksplit = stages;
@@ -962,6 +985,8 @@ int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens) {
 
 int launch_seq_rope_store(hipStream_t s, const SeqRopeArgs &a, uint32_t tokens) {
     if (tokens == 0) return VX_OK;
+    if (a.nsplit > kSeqRopeMaxSplit)
+        return fail(VX_ERR_INVALID_ARG, "seq rope: at most %u split partials", kSeqRopeMaxSplit);
     if (a.head_dim == 0 || a.head_dim > 128u || (a.head_dim & 1u))
         return fail(VX_ERR_UNSUPPORTED, "seq rope: head_dim must be even and <= 128");
     if (a.kc && (!a.vc || !a.v)) return fail(VX_ERR_INVALID_ARG, "seq rope: KV store needs v and both caches");

@@ -323,6 +323,10 @@ struct GemmArgs {
     // plain stores instead of adding to out; the consumer adds the partials.
     float *ws = nullptr;
     uint64_t ws_stride = 0;
+    // GEPI_STORE with ksplit > 1 on the prefill-layout kernel: when set, split s
+    // stores alpha * (its partial product) to out + s * ws_stride (each segment's
+    // [T][ldo]) with plain stores instead of atomic adds; the consumer sums them.
+    uint32_t split_store = 0;
 };
 int launch_gemm(hipStream_t s, const GemmArgs &a);
 // Tiled hi/lo plane layout read by the prefill GEMM (kernels_gemm.hip):
@@ -394,7 +398,12 @@ struct SeqRopeArgs {
     uint32_t ldqp = 0;
     __half *kc = nullptr, *vc = nullptr;   // nullable: store K/V rows [layer][context][kv_dim]
     uint32_t layer = 0, context = 0;
+    // q, k and v hold nsplit partial products split_stride floats apart (split-K
+    // GEMM output); the kernel reads their sums and writes roped k to split 0.
+    uint32_t nsplit = 1;
+    uint64_t split_stride = 0;
 };
+constexpr uint32_t kSeqRopeMaxSplit = 8;
 int launch_seq_rope_store(hipStream_t s, const SeqRopeArgs &a, uint32_t tokens);
 
 struct PrefillAttnArgs {
