@@ -32,7 +32,8 @@
 // workgroup per CU with a deeper ring (up to 7 slots), f16 quants in LDS,
 // weights as exact hi/lo f16 pairs of d*q (three MFMAs per k-step, no scale
 // step), fragments prefetched a block ahead, double-buffered block products,
-// and split K to put two workgroups on every CU.
+// split K to put two workgroups on every CU, and a stream-K schedule of the
+// SwiGLU tiles (equal block ranges over two workgroups per CU).
 #include <type_traits>
 
 #include "vx_internal.h"
