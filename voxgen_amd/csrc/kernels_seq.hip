@@ -377,7 +377,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
 // One workgroup per token. If branch != nullptr, h += scale * branch first (and
 // h is written back). y = h * (1/sqrt(mean(h^2) + eps)) * w is written as f32
 // (y, nullable) and/or as hi/lo f16 planes (yh/yl, nullable). Optionally zeroes
-// `zero_n` floats of row t of up to three buffers (split-K accumulators).
+// `zero_n` floats of row t of up to four buffers, and the branch rows after they
+// are read (split-K accumulators of the next GEMMs).
 __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
@@ -391,6 +392,8 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
             for (uint32_t b = 1; b < a.nbranch; ++b) add += br[(size_t)b * a.branch_stride + i];
             v = v + add * a.scale;
             h[i] = v;
+            if (a.clear_branch)
+                for (uint32_t b = 0; b < a.nbranch; ++b) const_cast<float *>(br)[(size_t)b * a.branch_stride + i] = 0.f;
         }
         s += v * v;
     }
@@ -411,7 +414,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
             a.yl[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
         }
     }
-    for (int z = 0; z < 3; ++z)
+    for (int z = 0; z < 4; ++z)
         if (a.zero[z])
             for (uint32_t i = threadIdx.x; i < a.zero_n[z]; i += 256u) a.zero[z][(size_t)t * a.zero_n[z] + i] = 0.f;
 }
@@ -453,6 +456,12 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
                                v[j].w + add.w * a.scale);
             *reinterpret_cast<float4 *>(h + 4u * (tid + 256u * j)) = v[j];
         }
+        if (a.clear_branch)
+            for (uint32_t b = 0; b < a.nbranch; ++b)
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    *reinterpret_cast<float4 *>(const_cast<float *>(br) + (size_t)b * a.branch_stride +
+                                                4u * (tid + 256u * j)) = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (!a.w) return;   // residual update only
     float ss = 0.f;
@@ -479,7 +488,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
             *reinterpret_cast<uint2 *>(a.yl + po) = lo;
         }
     }
-    for (int z = 0; z < 3; ++z)
+    for (int z = 0; z < 4; ++z)
         if (a.zero[z])
             for (uint32_t i = tid; i < a.zero_n[z]; i += 256u) a.zero[z][(size_t)t * a.zero_n[z] + i] = 0.f;
 }
@@ -893,6 +902,63 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
     a.out[(size_t)t * a.out_stride + h * a.head_dim + j] = z;
 }
 
+// dense_attn_scores.comp -> dense_softmax.comp -> dense_attn_values.comp for
+// kDenseFusedRows query tokens of one head of one sequence in a workgroup: their q
+// rows, the head's k and v rows (each padded by one float) and the rows x tokens
+// probabilities live in LDS. Scores are thread per (row, key), the softmax a wave
+// per row (lane per key), the values thread per (row, dim); each dot product and
+// sum runs in the order of the three-kernel path.
+constexpr uint32_t kDenseFusedRows = 8;
+__global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
+    extern __shared__ float sm[];
+    const uint32_t h = blockIdx.x, bz = blockIdx.y, t0 = blockIdx.z * kDenseFusedRows;
+    const uint32_t S = a.tokens, D = a.head_dim, DP = D + 1u;
+    const uint32_t R = min(kDenseFusedRows, S - t0);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t kv = h / (a.q_heads / a.kv_heads);
+    const float *q = a.q + ((size_t)bz * S + t0) * a.q_stride + (size_t)h * D;
+    const float *k = a.k + (size_t)bz * S * a.k_stride + (size_t)kv * D;
+    const float *v = a.v + (size_t)bz * S * a.v_stride + (size_t)kv * D;
+    float *out = a.out + ((size_t)bz * S + t0) * a.out_stride + (size_t)h * D;
+    float *ks = sm, *vs = ks + S * DP, *qs = vs + S * DP, *ps = qs + kDenseFusedRows * DP;
+    for (uint32_t i = tid; i < S * D; i += 256u) {
+        const uint32_t t = i / D, d = i - t * D;
+        ks[t * DP + d] = k[(size_t)t * a.k_stride + d];
+        vs[t * DP + d] = v[(size_t)t * a.v_stride + d];
+    }
+    for (uint32_t i = tid; i < R * D; i += 256u) {
+        const uint32_t t = i / D, d = i - t * D;
+        qs[t * DP + d] = q[(size_t)t * a.q_stride + d];
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)D);
+    for (uint32_t e = tid; e < R * S; e += 256u) {
+        const uint32_t t = e / S, key = e - t * S;
+        float s = 0.f;
+        for (uint32_t d = 0; d < D; ++d) s += qs[t * DP + d] * ks[key * DP + d];
+        ps[e] = s * scale;
+    }
+    __syncthreads();
+    for (uint32_t t = wave; t < R; t += 4u) {
+        const float x = lane < S ? ps[t * S + lane] : -FLT_MAX;
+        float m = x;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float ex = lane < S ? expf(x - m) : 0.f;
+        float z = ex;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o, 64);
+        if (lane < S) ps[t * S + lane] = ex / z;
+    }
+    __syncthreads();
+    for (uint32_t o = tid; o < R * D; o += 256u) {
+        const uint32_t t = o / D, d = o - t * D;
+        float z = 0.f;
+        for (uint32_t key = 0; key < S; ++key) z += ps[t * S + key] * vs[key * DP + d];
+        out[(size_t)t * a.out_stride + d] = z;
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
@@ -1036,6 +1102,23 @@ int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which) {
         k_dense_values<<<dim3(a.q_heads, a.tokens, a.batch), 256, 0, s>>>(a);
         VX_LAUNCHED("k_dense_values");
     }
+    return VX_OK;
+}
+
+uint64_t dense_fused_lds(uint32_t tokens, uint32_t head_dim) {
+    return ((2ull * tokens + kDenseFusedRows) * (head_dim + 1u) + (uint64_t)kDenseFusedRows * tokens) * 4u;
+}
+
+int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a) {
+    if (!a.tokens || !a.q_heads || !a.batch) return VX_OK;
+    if (!a.kv_heads || a.q_heads % a.kv_heads) return fail(VX_ERR_SHAPE, "dense attention: head counts");
+    const uint64_t lds = dense_fused_lds(a.tokens, a.head_dim);
+    if (a.tokens > kDenseFusedMaxTokens || a.head_dim == 0 || lds > 65536u)
+        return fail(VX_ERR_UNSUPPORTED, "fused dense attention: %u tokens x head_dim %u do not fit", a.tokens,
+                    a.head_dim);
+    k_dense_attn_fused<<<dim3(a.q_heads, a.batch, (a.tokens + kDenseFusedRows - 1u) / kDenseFusedRows), 256,
+                         (size_t)lds, s>>>(a);
+    VX_LAUNCHED("k_dense_attn_fused");
     return VX_OK;
 }
 

@@ -49,6 +49,7 @@ struct vx_locdit {
     const vx_model *model = nullptr;
     vx_locdit_config cfg{};
     uint32_t S = 0;   // tokens per sequence
+    bool dense_fused = false;   // attention of a sequence fits the one-kernel path
     Lin in_proj, cond_proj, out_proj, t1, t2, d1, d2;
     const float *norm_w = nullptr, *rope_factors = nullptr;
     std::vector<LocLayer> layers;
@@ -196,6 +197,10 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
         p.zero_cond_mask = c.uncond_zero_cond ? 0x2u : 0u;
         VX_CHECK(launch_pack_locdit(s, p));
     }
+    // Split-K projections add into outputs that the rmsnorm kernels clear on the
+    // way: the first norm clears q, k, v and the branch; the residual norm after
+    // attn_out clears the branch (the down projection's accumulator) once it has
+    // read it, and the one after down clears the branch and the next layer's q, k, v.
     SeqNormArgs n;
     n.h = F(e->hidden);
     n.ldh = H;
@@ -204,6 +209,14 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
     n.eps = c.rms_epsilon;
     n.y = F(e->norm);
     n.ldy = H;
+    n.zero[0] = F(e->q);
+    n.zero_n[0] = QD;
+    n.zero[1] = F(e->k);
+    n.zero_n[1] = KD;
+    n.zero[2] = F(e->v);
+    n.zero_n[2] = KD;
+    n.zero[3] = F(e->branch);
+    n.zero_n[3] = H;
     {
         ProfSpan sp(ctx, "local.seq_rmsnorm");
         VX_CHECK(launch_seq_rmsnorm(s, n, M));
@@ -215,7 +228,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
             const WRef w[3] = {L.q, L.k, L.v};
             const uint32_t rows[3] = {QD, KD, KD}, strides[3] = {QD, KD, KD};
             float *const o[3] = {F(e->q), F(e->k), F(e->v)};
-            VX_CHECK(enqueue_seq_qkv(s, w, rows, H, M, F(e->norm), 0, H, o, strides));
+            VX_CHECK(enqueue_seq_qkv(s, w, rows, H, M, F(e->norm), 0, H, o, strides, true));
         }
         {
             ProfSpan sp(ctx, "local.seq_rope");
@@ -251,13 +264,18 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
             a.out_stride = QD;
             a.score_stride = S;
             a.batch = batch;
-            VX_CHECK(launch_dense_attn(s, a, 0));
-            VX_CHECK(launch_dense_attn(s, a, 1));
-            VX_CHECK(launch_dense_attn(s, a, 2));
+            if (e->dense_fused) {
+                VX_CHECK(launch_dense_attn_fused(s, a));
+            } else {
+                VX_CHECK(launch_dense_attn(s, a, 0));
+                VX_CHECK(launch_dense_attn(s, a, 1));
+                VX_CHECK(launch_dense_attn(s, a, 2));
+            }
         }
         {
             ProfSpan sp(ctx, "local.seq_linear");
-            VX_CHECK(enqueue_seq_linear(s, L.o, nullptr, 0, H, QD, M, F(e->attn), 0, QD, F(e->branch), 0, H, 1.f));
+            VX_CHECK(
+                enqueue_seq_linear(s, L.o, nullptr, 0, H, QD, M, F(e->attn), 0, QD, F(e->branch), 0, H, 1.f, true));
         }
         SeqNormArgs r;
         r.h = F(e->hidden);
@@ -269,6 +287,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
         r.eps = c.rms_epsilon;
         r.y = F(e->norm);
         r.ldy = H;
+        r.clear_branch = 1;
         {
             ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
             r.w = L.ffn_norm;
@@ -281,12 +300,17 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
         {
             ProfSpan sp(ctx, "local.seq_linear");
             VX_CHECK(enqueue_seq_linear(s, L.down, nullptr, 0, H, c.ffn, M, F(e->gate), 0, c.ffn, F(e->branch), 0, H,
-                                        1.f));
+                                        1.f, true));
         }
         {
             ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
             r.w = l + 1 < c.layers ? e->layers[l + 1].attn_norm : e->norm_w;
+            for (int z = 0; z < 3; ++z) {
+                r.zero[z] = n.zero[z];
+                r.zero_n[z] = n.zero_n[z];
+            }
             VX_CHECK(launch_seq_rmsnorm(s, r, M));
+            for (int z = 0; z < 3; ++z) r.zero[z] = nullptr;
         }
     }
     ProfSpan sp(ctx, "local.locdit_out");
@@ -401,6 +425,7 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
     e->cfg = *cfg;
     const vx_locdit_config &c = e->cfg;
     e->S = c.n_mu + 1u + c.n_cond + c.patch;
+    e->dense_fused = e->S <= kDenseFusedMaxTokens && dense_fused_lds(e->S, c.head_dim) <= 65536u;
     auto bail = [&](int st) {
         free_all(e);
         delete e;

@@ -86,7 +86,7 @@ namespace vx {
 
 int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t bias_dtype, uint32_t rows,
                        uint32_t cols, uint32_t tokens, const float *x, uint32_t in_base, uint32_t in_stride,
-                       float *y, uint32_t out_base, uint32_t out_stride, float alpha) {
+                       float *y, uint32_t out_base, uint32_t out_stride, float alpha, bool out_zeroed) {
     if (!tokens || !rows) return VX_OK;
     if (tokens == 1) {  // one token: the batch-1 matvec (matvec.comp / linear_bias.comp)
         MatvecLaunch m;
@@ -117,7 +117,7 @@ int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t 
         // Few tiles (a short token batch): split K and accumulate with atomics into a
         // zeroed output, when the output rows are dense so they can be cleared whole.
         if (out_stride == rows) g.ksplit = split_for((rows + 127u) / 128u, tokens, cols);
-        if (g.ksplit > 1)
+        if (g.ksplit > 1 && !out_zeroed)
             VX_CHECK(launch_fill_u32(s, reinterpret_cast<uint32_t *>(y + out_base), 0u, (uint64_t)tokens * rows));
         return launch_gemm(s, g);
     }
@@ -142,7 +142,7 @@ int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t 
 
 int enqueue_seq_qkv(hipStream_t s, const WRef w[3], const uint32_t rows[3], uint32_t cols, uint32_t tokens,
                     const float *x, uint32_t in_base, uint32_t in_stride, float *const out[3],
-                    const uint32_t strides[3]) {
+                    const uint32_t strides[3], bool out_zeroed) {
     if (!tokens) return VX_OK;
     bool all = tokens > 1 && w[0].wt == w[1].wt && w[0].wt == w[2].wt;
     for (int i = 0; i < 3; ++i) all = all && gemm_ok(w[i], cols, in_base, in_stride, tokens);
@@ -161,14 +161,14 @@ int enqueue_seq_qkv(hipStream_t s, const WRef w[3], const uint32_t rows[3], uint
             const uint32_t nt = (rows[0] + 127u) / 128u + (rows[1] + 127u) / 128u + (rows[2] + 127u) / 128u;
             g.ksplit = split_for(nt, tokens, cols);
         }
-        if (g.ksplit > 1)
+        if (g.ksplit > 1 && !out_zeroed)
             for (int i = 0; i < 3; ++i)
                 VX_CHECK(launch_fill_u32(s, reinterpret_cast<uint32_t *>(out[i]), 0u, (uint64_t)tokens * rows[i]));
         return launch_gemm(s, g);
     }
     for (int i = 0; i < 3; ++i)
         VX_CHECK(enqueue_seq_linear(s, w[i], nullptr, 0, rows[i], cols, tokens, x, in_base, in_stride, out[i], 0,
-                                    strides[i], 1.f));
+                                    strides[i], 1.f, out_zeroed));
     return VX_OK;
 }
 

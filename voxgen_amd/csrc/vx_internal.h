@@ -379,8 +379,11 @@ struct SeqNormArgs {
     __half *yh = nullptr, *yl = nullptr;   // nullable hi/lo planes [T][ldp]
     uint32_t ldp = 0;
     uint32_t tiled = 0;             // 1: planes in the tiled layout of width n (ldp unused)
-    float *zero[3] = {nullptr, nullptr, nullptr};   // rows of split-K accumulators to clear
-    uint32_t zero_n[3] = {0, 0, 0};
+    float *zero[4] = {nullptr, nullptr, nullptr, nullptr};   // rows of split-K accumulators to clear
+    uint32_t zero_n[4] = {0, 0, 0, 0};
+    // 1: zero the branch rows (every split) after reading them, so the buffer is the
+    // cleared accumulator of the next split-K GEMM; the branch memory must be writable.
+    uint32_t clear_branch = 0;
 };
 constexpr uint32_t kSeqNormMaxBranch = 8;
 int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens);
@@ -437,14 +440,17 @@ int launch_seq_linear_generic(hipStream_t s, const SeqGenericArgs &a);
 // Token-batched projections (seq_ops.cpp) over resolved weights, choosing the
 // MFMA GEMM (f32 input split to hi/lo in the kernel), the decode matvec for a
 // single token, or the generic kernel. Strides and bases are in floats.
+// When a split-K GEMM adds into its output, the output is cleared first unless
+// out_zeroed says the caller already left it zero (e.g. cleared by the rmsnorm
+// kernel that runs before).
 // y[t][r] = alpha * (W[r] . x[t] + b[r])                     seq_linear_bias.comp
 int enqueue_seq_linear(hipStream_t s, const WRef &w, const void *bias, uint32_t bias_dtype, uint32_t rows,
                        uint32_t cols, uint32_t tokens, const float *x, uint32_t in_base, uint32_t in_stride,
-                       float *y, uint32_t out_base, uint32_t out_stride, float alpha);
+                       float *y, uint32_t out_base, uint32_t out_stride, float alpha, bool out_zeroed = false);
 // q|k|v[t] = Wq|Wk|Wv . x[t]                                  seq_qkv.comp
 int enqueue_seq_qkv(hipStream_t s, const WRef w[3], const uint32_t rows[3], uint32_t cols, uint32_t tokens,
                     const float *x, uint32_t in_base, uint32_t in_stride, float *const out[3],
-                    const uint32_t strides[3]);
+                    const uint32_t strides[3], bool out_zeroed = false);
 // y[t][r] = silu(Wg[r] . x[t]) * (Wu[r] . x[t])                 seq_swiglu.comp
 int enqueue_seq_swiglu(hipStream_t s, const WRef &g, const WRef &u, uint32_t rows, uint32_t cols, uint32_t tokens,
                        const float *x, uint32_t in_base, uint32_t in_stride, float *y, uint32_t out_base,
@@ -461,6 +467,12 @@ struct DenseAttnArgs {
     uint32_t batch = 1;
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
+// The three phases in one kernel (one workgroup per head, sequence and eight query
+// tokens, everything in LDS) for sequences of at most kDenseFusedMaxTokens tokens whose q, k, v and
+// scores fit 64 KB of LDS; VX_ERR_UNSUPPORTED otherwise. The scores are not stored.
+constexpr uint32_t kDenseFusedMaxTokens = 64;
+uint64_t dense_fused_lds(uint32_t tokens, uint32_t head_dim);   // bytes of LDS the fused kernel needs
+int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a);
 // ---------------------------------------------- CFM / LocDiT (kernels_cfm.hip)
 // Noise seed from dev_seed[0..1] (low, high word) when set, else from `seed`.
 int launch_cfm_noise(hipStream_t s, float *x, uint32_t n, const uint32_t *dev_seed, uint64_t seed, float temperature);
