@@ -70,6 +70,7 @@ typedef struct vx_graph vx_graph;
 typedef struct vx_baselm vx_baselm;
 typedef struct vx_gguf vx_gguf;
 typedef struct vx_locdit vx_locdit;
+typedef struct vx_residual vx_residual;
 
 /* ------------------------------------------------------------------------- */
 /* Push structs: identical layout to the reference's #[repr(C)] structs.      */
@@ -642,6 +643,13 @@ int vx_pack_locdit(vx_ctx *ctx, const vx_buf *mu1, const vx_buf *mu2, const vx_b
                    const vx_buf *x, vx_buf *hidden, const vx_pack_locdit_push *pc);
 /* silu_inplace.comp:5 and add_vectors.comp:6. */
 int vx_silu_inplace(vx_ctx *ctx, vx_buf *x, uint32_t n);
+typedef struct vx_fsq_push {        /* FsqPush acoustic.rs:249-255 */
+    uint32_t n;
+    float scale;
+} vx_fsq_push;
+/* fsq_quantize.comp: latent[i] = round(tanh(latent[i]) * scale) / scale, in place
+ * (record_fsq, acoustic.rs:922-928). Ties round away from zero. */
+int vx_fsq_quantize(vx_ctx *ctx, vx_buf *latent, const vx_fsq_push *pc);
 int vx_add_vectors(vx_ctx *ctx, vx_buf *a, const vx_buf *b, uint32_t n);
 
 /* ------------------------------------------------------------------------- */
@@ -691,6 +699,124 @@ int vx_locdit_estimate(vx_locdit *loc, const float *x, const float *cond, const 
  * out_patch receives the final x [patch x feat_dim]. */
 int vx_locdit_cfm_solve(vx_locdit *loc, const float *cond, const float *mu, const vx_cfm_options *opt,
                         const float *initial_x, float *out_patch, vx_cfm_result *res);
+
+/* ------------------------------------------------------------------------- */
+/* ResidualLM + FSQ + fusion + stop head (ResidualFsqEngine, acoustic.rs:400-1035). */
+/* ------------------------------------------------------------------------- */
+typedef struct vx_acoustic_config { /* AcousticConfig acoustic.rs:39-56 (numeric part) */
+    float model_version;
+    uint32_t residual_block_count;
+    uint32_t embedding_length;
+    uint32_t feed_forward_length;
+    uint32_t head_count;
+    uint32_t head_count_kv;
+    uint32_t head_dim;
+    uint32_t kv_dim;
+    uint32_t no_rope;
+    uint32_t active_context_length;
+    float rms_epsilon;
+    float residual_scale;           /* already effective_scale()d, acoustic.rs:117 */
+    uint32_t fsq_latent_dim;
+    float fsq_scale;
+    uint32_t fusion_input_dim;
+} vx_acoustic_config;
+
+/* AcousticConfig::from_gguf (acoustic.rs:59-125): architecture, version and the
+ * 8/2048/512/no-RoPE contract, BaseLM geometry compatibility, every tensor
+ * (validate_tensors acoustic.rs:127-174) and GgufSummary::validate_acoustic_f16
+ * (gguf.rs:150-160). */
+int vx_acoustic_config_from_gguf(const vx_gguf *g, const vx_baselm_config *base, uint32_t active_context_length,
+                                 vx_acoustic_config *out);
+/* AcousticConfig::kv_cache_bytes / per_cache_bytes (acoustic.rs:176-187). */
+uint64_t vx_acoustic_kv_cache_bytes(const vx_acoustic_config *cfg);
+
+typedef struct vx_residual_options {
+    uint32_t exec_mode;             /* VX_EXEC_GRAPH, VX_EXEC_FUSED or VX_EXEC_REFERENCE */
+    uint32_t strict_geometry;       /* 1: the VoxCPM2 contract; 0: other sizes for harnesses */
+} vx_residual_options;
+
+typedef struct vx_fsq_result {      /* FsqResult acoustic.rs:359-366 */
+    double elapsed_ms;
+    double output_checksum, output_l2;
+    double latent_checksum, latent_l2;
+} vx_fsq_result;
+
+typedef struct vx_residual_step_result {   /* ResidualStepResult acoustic.rs:368-379 */
+    uint32_t position;
+    uint32_t fsq_applied;
+    double elapsed_ms;
+    double fsq_checksum, fsq_l2;    /* 0 when fsq_applied == 0 (None) */
+    double fused_input_checksum, fused_input_l2;
+    double residual_hidden_checksum, residual_hidden_l2;
+} vx_residual_step_result;
+
+typedef struct vx_residual_gpu_step {      /* ResidualGpuStep acoustic.rs:381 */
+    uint32_t position;
+    uint32_t fsq_applied;
+    double elapsed_ms;
+} vx_residual_gpu_step;
+
+typedef struct vx_residual_benchmark {     /* ResidualBenchmark acoustic.rs:384-391 */
+    uint32_t iterations;
+    double mean_ms, min_ms, max_ms, steps_per_second;
+} vx_residual_benchmark_result;
+
+typedef struct vx_stop_prediction {        /* StopPrediction acoustic.rs:393-398 */
+    uint32_t stop;                  /* stop_logit > continue_logit */
+    float continue_logit, stop_logit;
+    double elapsed_ms;
+} vx_stop_prediction;
+
+/* ResidualFsqEngine::new (acoustic.rs:432-583): resolves every tensor, allocates
+ * the activations and the f16 ResidualLM KV caches. */
+int vx_residual_create(vx_ctx *ctx, const vx_model *acoustic, const vx_acoustic_config *cfg,
+                       const vx_residual_options *opt, vx_residual **out);
+int vx_residual_destroy(vx_residual *eng);
+uint32_t vx_residual_position(const vx_residual *eng);          /* acoustic.rs:585 */
+int vx_residual_reset(vx_residual *eng);                        /* acoustic.rs:589 */
+uint64_t vx_residual_allocated_bytes(const vx_residual *eng);   /* acoustic.rs:591-613 */
+
+#define VX_RESIDUAL_BUF_OUTPUT 0u        /* norm: the normalised ResidualLM output (output_buffer) */
+#define VX_RESIDUAL_BUF_CURRENT_LM 1u    /* current_lm_buffer (acoustic.rs:588) */
+#define VX_RESIDUAL_BUF_FSQ_LATENT 2u
+#define VX_RESIDUAL_BUF_FSQ_OUTPUT 3u
+#define VX_RESIDUAL_BUF_FUSION_SNAPSHOT 4u
+#define VX_RESIDUAL_BUF_HIDDEN 5u
+#define VX_RESIDUAL_BUF_KV_K 6u
+#define VX_RESIDUAL_BUF_KV_V 7u
+#define VX_RESIDUAL_BUF_STOP_LOGITS 8u
+vx_buf *vx_residual_buffer(vx_residual *eng, uint32_t which);
+
+/* fsq_only (acoustic.rs:654-676): FSQ of a host hidden state; no position change. */
+int vx_residual_fsq_only(vx_residual *eng, const float *base_hidden, uint32_t n, vx_fsq_result *out);
+/* step (acoustic.rs:678-692): FSQ(base) -> current_lm, fusion with the current
+ * acoustic embedding, one ResidualLM position. Host inputs of n floats each. */
+int vx_residual_step(vx_residual *eng, const float *base_hidden, const float *current_embedding, uint32_t n,
+                     vx_residual_step_result *out);
+/* step_from_gpu_base (acoustic.rs:694-710). */
+int vx_residual_step_from_gpu_base(vx_residual *eng, const vx_buf *base_hidden, const float *current_embedding,
+                                   uint32_t n, vx_residual_step_result *out);
+/* step_from_gpu_base_and_embedding (acoustic.rs:712-726). */
+int vx_residual_step_from_gpu_base_and_embedding(vx_residual *eng, const vx_buf *base_hidden,
+                                                 const vx_buf *current_embedding, vx_residual_step_result *out);
+/* step_from_gpu_base_and_embedding_gpu_only (acoustic.rs:728-731): enqueue only. */
+int vx_residual_step_from_gpu_base_and_embedding_gpu_only(vx_residual *eng, const vx_buf *base_hidden,
+                                                          const vx_buf *current_embedding,
+                                                          vx_residual_gpu_step *out);
+/* step_text_prefix_from_gpu_base (acoustic.rs:740-757): no FSQ, raw BaseLM
+ * hidden -> current_lm, zero acoustic half of the fusion input. */
+int vx_residual_step_text_prefix_from_gpu_base(vx_residual *eng, const vx_buf *base_hidden,
+                                               vx_residual_step_result *out);
+/* step_text_prefix_from_gpu_base_gpu_only (acoustic.rs:733-736): enqueue only. */
+int vx_residual_step_text_prefix_from_gpu_base_gpu_only(vx_residual *eng, const vx_buf *base_hidden,
+                                                        vx_residual_gpu_step *out);
+/* benchmark (acoustic.rs:759-793): reset, warmup + iterations host steps. */
+int vx_residual_benchmark(vx_residual *eng, const float *base_hidden, const float *current_embedding, uint32_t n,
+                          uint32_t warmup, uint32_t iterations, vx_residual_benchmark_result *out);
+/* predict_stop_from_gpu_base (acoustic.rs:619-634): Linear+SiLU+Linear(->2). */
+int vx_residual_predict_stop_from_gpu_base(vx_residual *eng, const vx_buf *base_hidden, vx_stop_prediction *out);
+/* predict_stop_from_current_lm (acoustic.rs:638-652). */
+int vx_residual_predict_stop_from_current_lm(vx_residual *eng, vx_stop_prediction *out);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,14 @@
  *   vr_pack_locdit                  numpy concatenation; zero_mu rows are 0.
  *   vr_cfm_time_span                closed form; endpoints 1 and 0; sway = 0
  *                                  gives the linear grid; descending check.
+ *   vr_fsq_quantize                 the known answer of acoustic.rs:1266-1271
+ *                                  (0.42 at scale 9 -> 4/9); f64 numpy
+ *                                  round-half-away(tanh(x)*s)/s; outputs on the
+ *                                  grid k/s with |k| <= s; odd symmetry.
+ *   vr_silu_inplace                 f64 x/(1+e^-x); silu(0) = 0.
+ *   vr_residual_lm_record           f64 numpy re-derivation of one layer
+ *                                  without RoPE; equals vr_baselm_record at
+ *                                  position 0, where RoPE is the identity.
  * Parity unpinned at the bit level (inside the float tolerances): the
  * driver's rounding of exp/sin/cos/pow/inversesqrt and FMA contraction.
  */
@@ -481,9 +489,11 @@ float vr_rope_scaling_factor(const vx_baselm_config *c) {
     return sqrtf(1.0f + logf(max / original) / logf(original));
 }
 
-void vr_baselm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint32_t position,
-                      int compute_logits) {
-    const vx_baselm_config *c = &m->cfg; /* record_transformer, baselm.rs:892-1052 */
+/* record_transformer (baselm.rs:892-1052), or record_residual_lm
+ * (acoustic.rs:968-1035) when rotate == 0: the same op order without RoPE. */
+static void record_stack(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint32_t position,
+                         int compute_logits, int rotate) {
+    const vx_baselm_config *c = &m->cfg;
     float residual_scale = vr_effective_scale(c->residual_scale);
     uint32_t q_per_kv = c->head_count / c->head_count_kv;
     vx_rms_push rp = {m->layers[0].attn_norm, c->embedding_length, c->rms_epsilon};
@@ -493,9 +503,11 @@ void vr_baselm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint
         vx_qkv_push qp = {L->q, L->k, L->v, c->embedding_length, c->kv_dim, c->embedding_length,
                           L->q_dtype, L->k_dtype, L->v_dtype, 0u};
         vr_qkv_matvec(blob, s->norm, s->q, s->k, s->v, &qp);
-        vx_rope_push ro = {m->rope_factors, position, c->head_count, c->head_count_kv, c->head_dim,
-                           c->rope_theta, vr_rope_scaling_factor(c)};
-        vr_rope(blob, s->q, s->k, &ro);
+        if (rotate) {
+            vx_rope_push ro = {m->rope_factors, position, c->head_count, c->head_count_kv, c->head_dim,
+                               c->rope_theta, vr_rope_scaling_factor(c)};
+            vr_rope(blob, s->q, s->k, &ro);
+        }
         vx_store_kv_push sk = {layer, position, c->active_context_length, c->kv_dim};
         vr_store_kv(s->k, s->v, s->kv_k, s->kv_v, &sk);
         vx_attention_push ap = {layer, c->active_context_length, position, c->head_dim, q_per_kv,
@@ -521,6 +533,26 @@ void vr_baselm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint
                              vr_effective_scale(c->logit_scale)};
         vr_matvec(blob, s->norm, s->logits, &lp);
     }
+}
+
+void vr_baselm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint32_t position,
+                      int compute_logits) {
+    record_stack(blob, m, s, position, compute_logits, 1);
+}
+
+void vr_residual_lm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint32_t position) {
+    record_stack(blob, m, s, position, 0, 0);
+}
+
+/* fsq_quantize.comp; ties of v * scale round away from zero (f32::round, the
+ * known answer of acoustic.rs:1266-1271). */
+void vr_fsq_quantize(float *x, uint32_t n, float scale) {
+    for (uint32_t i = 0; i < n; ++i) x[i] = roundf(tanhf(x[i]) * scale) / scale;
+}
+
+/* silu_inplace.comp. */
+void vr_silu_inplace(float *x, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) x[i] = x[i] / (1.0f + expf(-x[i]));
 }
 
 void vr_baselm_decode_token(const uint8_t *blob, const vr_baselm *m, vr_state *s,

@@ -80,6 +80,13 @@ typedef struct vr_state {
 /* record_transformer (baselm.rs:892-1052) at `position`. */
 void vr_baselm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint32_t position,
                       int compute_logits);
+/* record_residual_lm (acoustic.rs:968-1035): record_transformer's order without
+ * RoPE and without logits; m->cfg carries the ResidualLM geometry. */
+void vr_residual_lm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s, uint32_t position);
+/* fsq_quantize.comp (in place). */
+void vr_fsq_quantize(float *x, uint32_t n, float scale);
+/* silu_inplace.comp (in place). */
+void vr_silu_inplace(float *x, uint32_t n);
 /* Embedding dispatch (baselm.rs:634-647) then record_transformer. */
 void vr_baselm_decode_token(const uint8_t *blob, const vr_baselm *m, vr_state *s,
                             uint32_t token_id, uint32_t position, int compute_logits);

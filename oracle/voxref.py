@@ -67,6 +67,9 @@ def lib() -> C.CDLL:
         L.vr_pack_locdit.argtypes = [vp, vp, vp, vp, vp, vp, P(abi.PackLocDitPush)]
         L.vr_cfm_time_span.restype = C.c_int
         L.vr_cfm_time_span.argtypes = [u32, f32, vp]
+        L.vr_residual_lm_record.argtypes = [vp, vp, vp, u32]
+        L.vr_fsq_quantize.argtypes = [vp, u32, f32]
+        L.vr_silu_inplace.argtypes = [vp, u32]
         L.vr_set_threads.argtypes = [C.c_int]
         L.vr_get_threads.restype = C.c_int
         _lib = L
@@ -289,6 +292,112 @@ class BaseLm:
         lib().vr_baselm_record(_p(self.blob), C.byref(self._m), C.byref(self._s), position,
                                1 if logits else 0)
         return self.norm.copy()
+
+
+def fsq_quantize(x, scale: float) -> np.ndarray:
+    """fsq_quantize.comp."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().vr_fsq_quantize(_p(y), y.size, scale)
+    return y
+
+
+def silu_inplace(x) -> np.ndarray:
+    """silu_inplace.comp."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().vr_silu_inplace(_p(y), y.size)
+    return y
+
+
+class ResidualFsq:
+    """ResidualFsqEngine (acoustic.rs:400-1035) on the CPU over a SynthModel-like
+    (data, tensors, acoustic config): FSQ, fusion, record_residual_lm and the stop
+    predictor from the per-op functions, with its own f16 KV cache."""
+
+    def __init__(self, data: np.ndarray, tensors: dict, acfg: dict):
+        self.blob = np.ascontiguousarray(data, dtype=np.uint8)
+        if self.blob.size % 4:
+            self.blob = np.concatenate([self.blob, np.zeros(4 - self.blob.size % 4, np.uint8)])
+        self.cfg, self.t = dict(acfg), tensors
+        L, H = acfg["residual_block_count"], acfg["embedding_length"]
+        KV, F, ctx = acfg["kv_dim"], acfg["feed_forward_length"], acfg["active_context_length"]
+        self._layers = (_Layer * L)()
+        for l in range(L):
+            p = f"residual_lm.blk.{l}."
+            ly = self._layers[l]
+            for fld, name in (("attn_norm", "attn_norm"), ("ffn_norm", "ffn_norm"), ("q", "attn_q"),
+                              ("k", "attn_k"), ("v", "attn_v"), ("o", "attn_output"),
+                              ("gate", "ffn_gate"), ("up", "ffn_up"), ("down", "ffn_down")):
+                tt = tensors[p + name + ".weight"]
+                setattr(ly, fld, tt.offset)
+                if fld not in ("attn_norm", "ffn_norm"):
+                    setattr(ly, fld + "_dtype", tt.ggml_type)
+        m = _BaseLm()
+        c = m.cfg
+        c.context_length = c.active_context_length = ctx
+        c.embedding_length, c.block_count, c.feed_forward_length = H, L, F
+        c.head_count, c.head_count_kv = acfg["head_count"], acfg["head_count_kv"]
+        c.head_dim, c.kv_dim = acfg["head_dim"], KV
+        c.rms_epsilon, c.residual_scale = acfg["rms_epsilon"], acfg["residual_scale"]
+        m.output_norm = tensors["residual_lm.output_norm.weight"].offset
+        m.layers = C.cast(self._layers, C.POINTER(_Layer))
+        self._m = m
+        self.hidden, self.norm, self.q = f32(H), f32(H), f32(H)
+        self.k, self.v, self.attention = f32(KV), f32(KV), f32(H)
+        self.gate, self.branch, self.logits = f32(F), f32(H), f32(1)
+        self.scores = f32(acfg["head_count"] * ctx)
+        self.kv_k = np.zeros(L * ctx * KV, np.uint16)
+        self.kv_v = np.zeros(L * ctx * KV, np.uint16)
+        st = _State()
+        for n, _ in _State._fields_:
+            setattr(st, n, _p(getattr(self, n)))
+        self._s = st
+        self.current_lm = f32(H)
+
+    def _lin(self, prefix, x, rows, cols):
+        w, b = self.t[prefix + ".weight"], self.t[prefix + ".bias"]
+        return linear_bias(self.blob, x, abi.LinearBiasPush(w.offset, b.offset, rows, cols, w.ggml_type,
+                                                            b.ggml_type, 0, 1.0))
+
+    def fsq(self, base):
+        """record_fsq (acoustic.rs:909-939): (quantized latent, output)."""
+        H, Ld = self.cfg["embedding_length"], self.cfg["fsq_latent_dim"]
+        latent = fsq_quantize(self._lin("fsq.in_proj", base, Ld, H), self.cfg["fsq_scale"])
+        return latent, self._lin("fsq.out_proj", latent, H, Ld)
+
+    def step(self, base, embedding, position: int, fsq: bool = True) -> dict:
+        """step_record_submit (acoustic.rs:847-893): FSQ (or the raw text-prefix
+        state), current_lm, fusion, record_residual_lm at `position`."""
+        H = self.cfg["embedding_length"]
+        base = np.ascontiguousarray(base, dtype=np.float32)
+        out = {}
+        if fsq:
+            out["latent"], left = self.fsq(base)
+            out["fsq"] = left
+            right = np.ascontiguousarray(embedding, dtype=np.float32)
+        else:
+            left, right = base, np.zeros(H, np.float32)
+        self.current_lm = left.copy()
+        w, b = self.t["projections.res_fusion_proj.weight"], self.t["projections.res_fusion_proj.bias"]
+        fused, _ = fusion_linear(self.blob, left, right, abi.FusionPush(w.offset, b.offset, H, H, H, w.ggml_type,
+                                                                     b.ggml_type, 0))
+        out["fused"] = fused.copy()
+        self.hidden[:] = fused
+        lib().vr_residual_lm_record(_p(self.blob), C.byref(self._m), C.byref(self._s), position)
+        out["norm"] = self.norm.copy()
+        return out
+
+    def stop(self, x):
+        """predict_stop_* (acoustic.rs:619-652): the two logits (continue, stop)."""
+        H = self.cfg["embedding_length"]
+        h = silu_inplace(self._lin("stop_predictor.linear1", x, H, H))
+        w = self.t["stop_predictor.linear2.weight"]
+        return matvec(self.blob, h, abi.MatvecPush(w.offset, 2, H, w.ggml_type, 0, 1.0))
+
+
+def stats(v) -> tuple:
+    """stats (acoustic.rs:1248-1257): position-weighted checksum and L2."""
+    x = np.asarray(v, dtype=np.float64)
+    return float(np.sum(x * (np.arange(x.size) % 251 + 1))), float(np.sqrt(np.sum(x * x)))
 
 
 # ------------------------------------------------------------- CFM pieces

@@ -170,3 +170,90 @@ def test_writer_layout_is_gguf_v3():
     magic, ver, nt, nm = struct.unpack_from("<IIQQ", hdr)
     assert (magic, ver, nt, nm) == (0x46554747, 3, 1, 1)
     assert len(hdr) % 32 == 0
+
+
+# ----------------------------------------------- AcousticConfig::from_gguf
+def acoustic_file(tmp_path, mutate=None, drop=None, meta_over=None):
+    acfg = synth.acoustic_config()
+    m = synth.build_acoustic(acfg, with_data=False)
+    tensors = [t for t in m.tensors if t.name != drop]
+    if mutate:
+        tensors = [mutate(t) for t in tensors]
+    meta = dict(m.metadata)
+    meta.update(meta_over or {})
+    size = max(t.offset + t.nbytes for t in tensors)
+    return gguf.write(tmp_path / "a.gguf", meta, tensors, None, data_bytes=size)
+
+
+def test_acoustic_config_from_gguf(tmp_path):
+    base = synth.baselm_config(context_length=32768, residual_scale=0.0)
+    c = Gguf(acoustic_file(tmp_path)).acoustic_config(base, 4096)
+    want = synth.acoustic_config(active_context=4096)
+    for k, v in want.items():
+        assert c[k] == pytest.approx(v), k
+    base["residual_scale"] = 0.25
+    assert Gguf(acoustic_file(tmp_path)).acoustic_config(base, 1)["residual_scale"] == 0.25
+
+
+def _retype(name, ty):
+    def mutate(t):
+        return synth.TensorDesc(t.name, ty, t.dims, t.offset) if t.name == name else t
+    return mutate
+
+
+@pytest.mark.parametrize("case,code", [
+    ("arch", "VX_ERR_UNSUPPORTED"), ("version", "VX_ERR_UNSUPPORTED"), ("ctx0", "VX_ERR_INVALID_ARG"),
+    ("ctx_big", "VX_ERR_INVALID_ARG"), ("layers7", "VX_ERR_UNSUPPORTED"), ("rope", "VX_ERR_UNSUPPORTED"),
+    ("bool", "VX_ERR_GGUF"), ("scale0", "VX_ERR_INVALID_ARG"), ("base", "VX_ERR_UNSUPPORTED"),
+    ("missing", "VX_ERR_NOT_FOUND"), ("fsq_bias_f32", "VX_ERR_SHAPE"), ("q8", "VX_ERR_UNSUPPORTED"),
+    ("norm_f16", "VX_ERR_SHAPE"), ("stop_dims", "VX_ERR_SHAPE"), ("missing_meta", "VX_ERR_NOT_FOUND"),
+])
+def test_acoustic_config_errors(tmp_path, case, code):
+    base = synth.baselm_config(context_length=32768)
+    active, kw = 512, {}
+    if case == "arch":
+        kw["meta_over"] = {"general.architecture": (8, "minicpm4")}
+    elif case == "version":
+        kw["meta_over"] = {"voxcpm.model_version": (6, 1.5)}
+    elif case == "ctx0":
+        active = 0
+    elif case == "ctx_big":
+        active = 8193
+    elif case == "layers7":
+        kw["meta_over"] = {"voxcpm.residual_lm.n_layer": (4, 7)}
+    elif case == "rope":
+        kw["meta_over"] = {"voxcpm.residual_lm.no_rope": (7, False)}
+    elif case == "bool":
+        kw["meta_over"] = {"voxcpm.residual_lm.no_rope": (8, "yes")}
+    elif case == "scale0":
+        kw["meta_over"] = {"voxcpm.fsq.scale": (6, 0.0)}
+    elif case == "base":
+        base["feed_forward_length"] = 4096
+    elif case == "missing":
+        kw["drop"] = "residual_lm.blk.5.ffn_down.weight"
+    elif case == "fsq_bias_f32":   # require_vector(.., allow_f32 = false)
+        kw["mutate"] = _retype("fsq.in_proj.bias", abi.DTYPE_F32)
+    elif case == "q8":             # validate_acoustic_f16
+        kw["mutate"] = _retype("residual_lm.blk.0.attn_q.weight", abi.DTYPE_Q8_0)
+    elif case == "norm_f16":
+        kw["mutate"] = _retype("residual_lm.blk.2.ffn_norm.weight", abi.DTYPE_F16)
+    elif case == "stop_dims":
+        def mutate(t):
+            if t.name == "stop_predictor.linear2.weight":
+                t = synth.TensorDesc(t.name, t.ggml_type, (2048, 3), t.offset)
+            return t
+        kw["mutate"] = mutate
+    elif case == "missing_meta":
+        acfg = synth.acoustic_config()
+        m = synth.build_acoustic(acfg, with_data=False)
+        meta = dict(m.metadata)
+        del meta["voxcpm.fsq.latent_dim"]
+        size = max(t.offset + t.nbytes for t in m.tensors)
+        path = gguf.write(tmp_path / "b.gguf", meta, m.tensors, None, data_bytes=size)
+        with pytest.raises(abi.VxError) as e:
+            Gguf(path).acoustic_config(base, active)
+        assert e.value.name == code
+        return
+    with pytest.raises(abi.VxError) as e:
+        Gguf(acoustic_file(tmp_path, **kw)).acoustic_config(base, active)
+    assert e.value.name == code

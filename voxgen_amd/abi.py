@@ -140,6 +140,26 @@ StepResult = _struct("StepResult", [("position", u32), ("elapsed_ms", f64),
 BenchmarkResult = _struct("BenchmarkResult", [("iterations", u32), ("token_id", u32),
                                               ("mean_ms", f64), ("min_ms", f64), ("max_ms", f64),
                                               ("tokens_per_second", f64)])
+FsqPush = _struct("FsqPush", [("n", u32), ("scale", f32)])
+AcousticConfig = _struct("AcousticConfig", [
+    ("model_version", f32), ("residual_block_count", u32), ("embedding_length", u32),
+    ("feed_forward_length", u32), ("head_count", u32), ("head_count_kv", u32), ("head_dim", u32),
+    ("kv_dim", u32), ("no_rope", u32), ("active_context_length", u32), ("rms_epsilon", f32),
+    ("residual_scale", f32), ("fsq_latent_dim", u32), ("fsq_scale", f32), ("fusion_input_dim", u32)])
+ResidualOptions = _struct("ResidualOptions", [("exec_mode", u32), ("strict_geometry", u32)])
+FsqResult = _struct("FsqResult", [("elapsed_ms", f64), ("output_checksum", f64), ("output_l2", f64),
+                                  ("latent_checksum", f64), ("latent_l2", f64)])
+ResidualStepResult = _struct("ResidualStepResult", [
+    ("position", u32), ("fsq_applied", u32), ("elapsed_ms", f64), ("fsq_checksum", f64), ("fsq_l2", f64),
+    ("fused_input_checksum", f64), ("fused_input_l2", f64), ("residual_hidden_checksum", f64),
+    ("residual_hidden_l2", f64)])
+ResidualGpuStep = _struct("ResidualGpuStep", [("position", u32), ("fsq_applied", u32), ("elapsed_ms", f64)])
+ResidualBenchmark = _struct("ResidualBenchmark", [("iterations", u32), ("mean_ms", f64), ("min_ms", f64),
+                                                  ("max_ms", f64), ("steps_per_second", f64)])
+StopPrediction = _struct("StopPrediction", [("stop", u32), ("continue_logit", f32), ("stop_logit", f32),
+                                            ("elapsed_ms", f64)])
+RESIDUAL_BUF = dict(OUTPUT=0, CURRENT_LM=1, FSQ_LATENT=2, FSQ_OUTPUT=3, FUSION_SNAPSHOT=4, HIDDEN=5,
+                    KV_K=6, KV_V=7, STOP_LOGITS=8)
 
 P = C.POINTER
 CTX = vp   # vx_ctx*
@@ -149,6 +169,7 @@ GRAPH = vp
 ENGINE = vp
 GGUF = vp
 LOCDIT = vp
+RESIDUAL = vp
 
 # name -> (restype, argtypes)
 PROTOTYPES = {
@@ -258,6 +279,25 @@ PROTOTYPES = {
     "vx_baselm_buffer": (BUFP, [ENGINE, u32]),
     "vx_baselm_profile_steps": (i32, [ENGINE, P(u32), u32, P(ProfEntry), u32, P(u32)]),
     "vx_baselm_time_layer_kernel": (i32, [ENGINE, u32, u32, P(C.c_double)]),
+    "vx_fsq_quantize": (i32, [CTX, BUFP, P(FsqPush)]),
+    "vx_acoustic_config_from_gguf": (i32, [GGUF, P(BaseLmConfig), u32, P(AcousticConfig)]),
+    "vx_acoustic_kv_cache_bytes": (u64, [P(AcousticConfig)]),
+    "vx_residual_create": (i32, [CTX, MODEL, P(AcousticConfig), P(ResidualOptions), P(RESIDUAL)]),
+    "vx_residual_destroy": (i32, [RESIDUAL]),
+    "vx_residual_position": (u32, [RESIDUAL]),
+    "vx_residual_reset": (i32, [RESIDUAL]),
+    "vx_residual_allocated_bytes": (u64, [RESIDUAL]),
+    "vx_residual_buffer": (BUFP, [RESIDUAL, u32]),
+    "vx_residual_fsq_only": (i32, [RESIDUAL, P(f32), u32, P(FsqResult)]),
+    "vx_residual_step": (i32, [RESIDUAL, P(f32), P(f32), u32, P(ResidualStepResult)]),
+    "vx_residual_step_from_gpu_base": (i32, [RESIDUAL, BUFP, P(f32), u32, P(ResidualStepResult)]),
+    "vx_residual_step_from_gpu_base_and_embedding": (i32, [RESIDUAL, BUFP, BUFP, P(ResidualStepResult)]),
+    "vx_residual_step_from_gpu_base_and_embedding_gpu_only": (i32, [RESIDUAL, BUFP, BUFP, P(ResidualGpuStep)]),
+    "vx_residual_step_text_prefix_from_gpu_base": (i32, [RESIDUAL, BUFP, P(ResidualStepResult)]),
+    "vx_residual_step_text_prefix_from_gpu_base_gpu_only": (i32, [RESIDUAL, BUFP, P(ResidualGpuStep)]),
+    "vx_residual_benchmark": (i32, [RESIDUAL, P(f32), P(f32), u32, u32, u32, P(ResidualBenchmark)]),
+    "vx_residual_predict_stop_from_gpu_base": (i32, [RESIDUAL, BUFP, P(StopPrediction)]),
+    "vx_residual_predict_stop_from_current_lm": (i32, [RESIDUAL, P(StopPrediction)]),
 }
 
 STRUCT_SIZES = {  # C name -> ctypes struct
@@ -278,7 +318,11 @@ STRUCT_SIZES = {  # C name -> ctypes struct
     "vx_fused_residual_args": FusedResidualArgs, "vx_fused_swiglu_args": FusedSwigluArgs,
     "vx_gguf_summary": GgufSummary, "vx_baselm_config": BaseLmConfig,
     "vx_baselm_options": BaseLmOptions, "vx_top_logit": TopLogit, "vx_step_result": StepResult,
-    "vx_baselm_benchmark_result": BenchmarkResult,
+    "vx_baselm_benchmark_result": BenchmarkResult, "vx_fsq_push": FsqPush,
+    "vx_acoustic_config": AcousticConfig, "vx_residual_options": ResidualOptions,
+    "vx_fsq_result": FsqResult, "vx_residual_step_result": ResidualStepResult,
+    "vx_residual_gpu_step": ResidualGpuStep, "vx_residual_benchmark_result": ResidualBenchmark,
+    "vx_stop_prediction": StopPrediction,
 }
 
 

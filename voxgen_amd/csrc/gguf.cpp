@@ -501,4 +501,108 @@ int vx_baselm_config_from_gguf(const vx_gguf *g, uint32_t active_context_length,
     return VX_OK;
 }
 
+// AcousticConfig::from_gguf (acoustic.rs:59-125) with GgufSummary::validate_acoustic_f16
+// (gguf.rs:150-160) and validate_tensors (acoustic.rs:127-174).
+int vx_acoustic_config_from_gguf(const vx_gguf *g, const vx_baselm_config *base, uint32_t active_context_length,
+                                 vx_acoustic_config *out) {
+    if (!g || !base || !out) return fail(VX_ERR_INVALID_ARG, "vx_acoustic_config_from_gguf: null argument");
+    bool any_f16 = false;
+    for (const vx_tensor_info &t : g->tensors) {
+        if (t.ggml_type != 0 && t.ggml_type != 1)
+            return fail(VX_ERR_UNSUPPORTED, "Unsupported acoustic tensor type %u in %s; the F16 acoustic GGUF is required",
+                        t.ggml_type, t.name);
+        uint64_t elements = 1;
+        for (uint32_t d = 0; d < t.n_dims; ++d) elements *= t.dims[d];
+        if (t.ggml_type == 1 && elements >= 4096) any_f16 = true;
+    }
+    if (!any_f16) return fail(VX_ERR_GGUF, "acoustic GGUF does not contain expected F16 weight tensors");
+    std::string arch, no_rope;
+    if (!meta_string(g, "general.architecture", &arch))
+        return fail(VX_ERR_NOT_FOUND, "required GGUF metadata key \"general.architecture\" is missing");
+    if (arch != "voxcpm-acoustic")
+        return fail(VX_ERR_UNSUPPORTED, "expected general.architecture=voxcpm-acoustic for the acoustic GGUF, got \"%s\"",
+                    arch.c_str());
+    vx_acoustic_config c{};
+    if (!meta_f32(g, {"voxcpm.model_version"}, &c.model_version))
+        return fail(VX_ERR_NOT_FOUND, "missing required metadata: voxcpm.model_version");
+    if (std::fabs(c.model_version - 2.0f) > 0.01f)
+        return fail(VX_ERR_UNSUPPORTED, "specialized for VoxCPM2 acoustic v2.0, got model_version=%g", c.model_version);
+    if (active_context_length == 0 || active_context_length > 8192u)  // VOXCPM2_MAX_GENERATION_CONTEXT
+        return fail(VX_ERR_INVALID_ARG, "ResidualLM --max-context must be in 1..=8192; got %u", active_context_length);
+    if (!meta_u32(g, {"voxcpm.residual_lm.n_layer"}, &c.residual_block_count) ||
+        !meta_u32(g, {"voxcpm.residual_lm.n_embd"}, &c.embedding_length) ||
+        !meta_u32(g, {"voxcpm.fsq.latent_dim"}, &c.fsq_latent_dim) || !meta_f32(g, {"voxcpm.fsq.scale"}, &c.fsq_scale) ||
+        !meta_string(g, "voxcpm.residual_lm.no_rope", &no_rope))
+        return fail(VX_ERR_NOT_FOUND, "missing required voxcpm.residual_lm / voxcpm.fsq metadata");
+    if (no_rope == "true" || no_rope == "1")  // metadata_bool gguf.rs:104-110
+        c.no_rope = 1;
+    else if (no_rope == "false" || no_rope == "0")
+        c.no_rope = 0;
+    else
+        return fail(VX_ERR_GGUF, "GGUF metadata \"voxcpm.residual_lm.no_rope\" is not a bool");
+    if (c.residual_block_count != 8 || c.embedding_length != 2048 || c.fsq_latent_dim != 512 || !c.no_rope)
+        return fail(VX_ERR_UNSUPPORTED,
+                    "unsupported VoxCPM2 acoustic contract: residual_layers=%u, embd=%u, fsq_latent=%u, no_rope=%u; "
+                    "expected 8/2048/512/true",
+                    c.residual_block_count, c.embedding_length, c.fsq_latent_dim, c.no_rope);
+    if (base->embedding_length != c.embedding_length || base->feed_forward_length != 6144 || base->head_count != 16 ||
+        base->head_count_kv != 2 || base->head_dim != 128)
+        return fail(VX_ERR_UNSUPPORTED, "BaseLM geometry is incompatible with VoxCPM2 ResidualLM");
+    if (!std::isfinite(c.fsq_scale) || c.fsq_scale <= 0.f)
+        return fail(VX_ERR_INVALID_ARG, "invalid FSQ scale %g", c.fsq_scale);
+    c.feed_forward_length = base->feed_forward_length;
+    c.head_count = base->head_count;
+    c.head_count_kv = base->head_count_kv;
+    c.head_dim = base->head_dim;
+    c.kv_dim = base->kv_dim;
+    c.active_context_length = active_context_length;
+    c.rms_epsilon = base->rms_epsilon;
+    c.residual_scale = base->residual_scale == 0.f ? 1.f : base->residual_scale;
+    c.fusion_input_dim = c.embedding_length * 2u;
+    const uint64_t H = c.embedding_length, L = c.fsq_latent_dim, KV = c.kv_dim, FF = c.feed_forward_length;
+    const vx_tensor_info *t;
+    auto f16_matrix = [&](const std::string &name, uint64_t cols, uint64_t rows) -> int {  // require_matrix(.., true)
+        VX_CHECK(need_tensor(g, name, &t));
+        VX_CHECK(dims_eq(t, {cols, rows}));
+        if (t->ggml_type != 1)
+            return fail(VX_ERR_SHAPE, "tensor %s is type %u, expected F16 from VoxCPM2-Acoustic-F16.gguf", t->name,
+                        t->ggml_type);
+        return VX_OK;
+    };
+    auto vector = [&](const std::string &name, uint64_t n, bool allow_f32) -> int {  // require_vector
+        VX_CHECK(need_tensor(g, name, &t));
+        VX_CHECK(dims_eq(t, {n}));
+        if (!(t->ggml_type == 1 || (allow_f32 && t->ggml_type == 0)))
+            return fail(VX_ERR_SHAPE, "tensor %s uses unsupported vector type %u", t->name, t->ggml_type);
+        return VX_OK;
+    };
+    VX_CHECK(f16_matrix("fsq.in_proj.weight", H, L));
+    VX_CHECK(vector("fsq.in_proj.bias", L, false));
+    VX_CHECK(f16_matrix("fsq.out_proj.weight", L, H));
+    VX_CHECK(vector("fsq.out_proj.bias", H, false));
+    VX_CHECK(f16_matrix("projections.res_fusion_proj.weight", c.fusion_input_dim, H));
+    VX_CHECK(vector("projections.res_fusion_proj.bias", H, false));
+    VX_CHECK(vector("residual_lm.output_norm.weight", H, true));
+    VX_CHECK(is_f32(t));
+    for (uint32_t l = 0; l < c.residual_block_count; ++l) {
+        const std::string p = "residual_lm.blk." + std::to_string(l) + ".";
+        for (const char *n : {"attn_norm.weight", "ffn_norm.weight"}) {
+            VX_CHECK(vector(p + n, H, true));
+            VX_CHECK(is_f32(t));
+        }
+        const struct {
+            const char *n;
+            uint64_t cols, rows;
+        } mats[] = {{"attn_q.weight", H, H},       {"attn_k.weight", H, KV},   {"attn_v.weight", H, KV},
+                    {"attn_output.weight", H, H},  {"ffn_gate.weight", H, FF}, {"ffn_up.weight", H, FF},
+                    {"ffn_down.weight", FF, H}};
+        for (const auto &m : mats) VX_CHECK(f16_matrix(p + m.n, m.cols, m.rows));
+    }
+    VX_CHECK(f16_matrix("stop_predictor.linear1.weight", H, H));
+    VX_CHECK(vector("stop_predictor.linear1.bias", H, true));
+    VX_CHECK(f16_matrix("stop_predictor.linear2.weight", H, 2));
+    *out = c;
+    return VX_OK;
+}
+
 }  // extern "C"

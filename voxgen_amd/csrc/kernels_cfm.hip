@@ -118,6 +118,15 @@ __global__ __launch_bounds__(256) void k_silu_inplace(float *x, uint32_t n) {
     x[i] = v / (1.0f + expf(-v));
 }
 
+// fsq_quantize.comp: the latent of the finite scalar quantizer, in place. Ties of
+// v * scale round away from zero (f32::round of acoustic.rs:1266-1271).
+__global__ __launch_bounds__(256) void k_fsq_quantize(float *x, uint32_t n, float scale) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float v = tanhf(x[i]);
+    x[i] = roundf(v * scale) / scale;
+}
+
 __global__ __launch_bounds__(256) void k_add_vectors(float *a, const float *b, uint32_t n) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i < n) a[i] += b[i];
@@ -159,6 +168,13 @@ int launch_silu_inplace(hipStream_t s, float *x, uint32_t n) {
     if (!n) return VX_OK;
     k_silu_inplace<<<(n + 255u) / 256u, 256, 0, s>>>(x, n);
     VX_LAUNCHED("k_silu_inplace");
+    return VX_OK;
+}
+
+int launch_fsq_quantize(hipStream_t s, float *x, uint32_t n, float scale) {
+    if (!n) return VX_OK;
+    k_fsq_quantize<<<(n + 255u) / 256u, 256, 0, s>>>(x, n, scale);
+    VX_LAUNCHED("k_fsq_quantize");
     return VX_OK;
 }
 

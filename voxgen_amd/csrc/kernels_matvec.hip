@@ -345,6 +345,7 @@ struct QkvArgs {
     __half *kc, *vc;
     const uint32_t *position;
     const float2 *rope_cs;
+    uint32_t no_rope;
 };
 
 // One wave per rotary pair: Q/K rows (i, i + head_dim/2) of a head, or two
@@ -386,8 +387,9 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
     load_row(rr[1], w, r1, a.cols, lane);
     const uint32_t pos = *a.position;
     const uint32_t pair = r0 % a.head_dim;
-    const float ext = seg < 2 && !a.rope_cs ? a.factors[pair] : 1.f;
-    const float2 cs_tab = seg < 2 && a.rope_cs ? a.rope_cs[pair] : make_float2(1.f, 0.f);
+    const bool rotate = seg < 2 && !a.no_rope;   // q/k rotated unless the stack runs without RoPE
+    const float ext = rotate && !a.rope_cs ? a.factors[pair] : 1.f;
+    const float2 cs_tab = rotate && a.rope_cs ? a.rope_cs[pair] : make_float2(1.f, 0.f);
     __builtin_amdgcn_sched_barrier(0);
     stage_finish<NG, true>(st, xs, red, a.cols, a.eps);
     Frag<NG> f;
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
     float v0 = wave_sum_dpp(row_dot(rr[0], f, sx));
     float v1 = wave_sum_dpp(row_dot(rr[1], f, sx));
     if (lane != 0 || !live) return;
-    if (seg < 2) {
+    if (rotate) {
         float c = cs_tab.x, s = cs_tab.y;
         if (!a.rope_cs) {  // rope.comp:28-41 inline
             const float exponent = (float)(pair * 2u) / (float)a.head_dim;
@@ -610,7 +612,7 @@ int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &l) {
                     "column count and aligned buffers");
     QkvArgs a{l.q,      l.k,        l.v,       l.hidden,  l.norm,  l.eps,    l.q_rows, l.kv_rows,
               l.cols,   l.head_dim, l.factors, l.theta,   l.scaling, l.layer, l.context, l.qo,
-              l.ko,     l.vo,       l.kc,      l.vc,      l.position, l.rope_cs};
+              l.ko,     l.vo,       l.kc,      l.vc,      l.position, l.rope_cs, l.no_rope ? 1u : 0u};
     const uint32_t pairs = (l.q_rows + 2u * l.kv_rows) / 2u;
     const uint32_t grid = (pairs + kWavesPerBlock - 1) / kWavesPerBlock;
 #define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV><<<grid, kBlock, 0, s>>>(a)

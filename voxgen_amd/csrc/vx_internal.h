@@ -191,6 +191,7 @@ struct QkvFusedLaunch {
     __half *kc = nullptr, *vc = nullptr;
     const uint32_t *position = nullptr;
     const float2 *rope_cs = nullptr;   // nullable: per-step (cos, sin) table from launch_rope_table
+    bool no_rope = false;              // q/k stored unrotated (a stack without RoPE)
 };
 int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &a);
 
@@ -491,6 +492,8 @@ struct PackLocditArgs {
 };
 int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a);
 int launch_silu_inplace(hipStream_t s, float *x, uint32_t n);
+// x[i] = round(tanh(x[i]) * scale) / scale (fsq_quantize.comp), i < n.
+int launch_fsq_quantize(hipStream_t s, float *x, uint32_t n, float scale);
 int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n);
 // Embedding rows of n device token ids into out[t][ldo] (bit-exact gather).
 int launch_seq_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, uint32_t dtype,

@@ -111,3 +111,12 @@ class Gguf:
         c = abi.BaseLmConfig()
         abi.call("vx_baselm_config_from_gguf", self.handle, active_context, C.byref(c))
         return {k: getattr(c, k) for k, _ in c._fields_}
+
+    def acoustic_config(self, base_config: dict, active_context: int) -> dict:
+        """AcousticConfig::from_gguf (acoustic.rs:59-125) against the BaseLM config."""
+        b = abi.BaseLmConfig()
+        for k, _ in b._fields_:
+            setattr(b, k, base_config[k])
+        c = abi.AcousticConfig()
+        abi.call("vx_acoustic_config_from_gguf", self.handle, C.byref(b), active_context, C.byref(c))
+        return {k: getattr(c, k) for k, _ in c._fields_}

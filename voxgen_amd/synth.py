@@ -266,3 +266,74 @@ def build_locdit(cfg: dict, seed: int = 0x5EED0040, std: float = 0.02) -> SynthM
         else:
             lib().vs_fill_normal_f32(_ptr(data, t.offset), n, s, 0.0, std)
     return SynthModel(data, reg.tensors, dict(cfg), {})
+
+
+def acoustic_config(layers=8, hidden=2048, ffn=6144, q_heads=16, kv_heads=2, head_dim=128, latent=512,
+                    fsq_scale=9.0, active_context=512, eps=1e-6, residual_scale=1.0) -> dict:
+    """vx_acoustic_config fields. Defaults are the VoxCPM2 contract
+    (AcousticConfig::from_gguf, acoustic.rs:83-103): 8 residual layers over the
+    2048/6144/16/2/128 BaseLM geometry, FSQ latent 512, no RoPE."""
+    return dict(model_version=2.0, residual_block_count=layers, embedding_length=hidden, feed_forward_length=ffn,
+                head_count=q_heads, head_count_kv=kv_heads, head_dim=head_dim, kv_dim=kv_heads * head_dim,
+                no_rope=1, active_context_length=active_context, rms_epsilon=eps, residual_scale=residual_scale,
+                fsq_latent_dim=latent, fsq_scale=fsq_scale, fusion_input_dim=2 * hidden)
+
+
+def build_acoustic(cfg: dict, seed: int = 0x5EED0060, std: float = 0.02, bias_f32_stop: bool = True,
+                   with_data: bool = True) -> SynthModel:
+    """Synthetic ResidualLM / FSQ / fusion / stop-predictor tensors with the names,
+    shapes and dtypes validate_tensors checks (acoustic.rs:127-174): F16 matrices
+    N(0, std), F16 biases N(0, std) (the stop predictor's linear1 bias F32 when
+    bias_f32_stop), F32 norm gains N(1, 0.02)."""
+    H, F, L = cfg["embedding_length"], cfg["feed_forward_length"], cfg["fsq_latent_dim"]
+    KV = cfg["kv_dim"]
+    reg = Region()
+    f16, f32 = abi.DTYPE_F16, abi.DTYPE_F32
+    reg.add("fsq.in_proj.weight", f16, (H, L))
+    reg.add("fsq.in_proj.bias", f16, (L,))
+    reg.add("fsq.out_proj.weight", f16, (L, H))
+    reg.add("fsq.out_proj.bias", f16, (H,))
+    reg.add("projections.res_fusion_proj.weight", f16, (2 * H, H))
+    reg.add("projections.res_fusion_proj.bias", f16, (H,))
+    reg.add("residual_lm.output_norm.weight", f32, (H,))
+    for l in range(cfg["residual_block_count"]):
+        p = f"residual_lm.blk.{l}."
+        reg.add(p + "attn_norm.weight", f32, (H,))
+        reg.add(p + "attn_q.weight", f16, (H, H))
+        reg.add(p + "attn_k.weight", f16, (H, KV))
+        reg.add(p + "attn_v.weight", f16, (H, KV))
+        reg.add(p + "attn_output.weight", f16, (H, H))
+        reg.add(p + "ffn_norm.weight", f32, (H,))
+        reg.add(p + "ffn_gate.weight", f16, (H, F))
+        reg.add(p + "ffn_up.weight", f16, (H, F))
+        reg.add(p + "ffn_down.weight", f16, (F, H))
+    reg.add("stop_predictor.linear1.weight", f16, (H, H))
+    reg.add("stop_predictor.linear1.bias", f32 if bias_f32_stop else f16, (H,))
+    reg.add("stop_predictor.linear2.weight", f16, (H, 2))
+    data = np.zeros((reg.size + 255) // 256 * 256 if with_data else 0, np.uint8)
+    if with_data:
+        for i, t in enumerate(reg.tensors):
+            s = derive_seed(seed, i)
+            n = int(np.prod(t.dims))
+            if t.name.endswith("norm.weight"):
+                lib().vs_fill_normal_f32(_ptr(data, t.offset), n, s, 1.0, 0.02)
+            elif t.ggml_type == f16:
+                lib().vs_fill_normal_f16(_ptr(data, t.offset), n, s, 0.0, std)
+            else:
+                lib().vs_fill_normal_f32(_ptr(data, t.offset), n, s, 0.0, std)
+    return SynthModel(data, reg.tensors, dict(cfg), acoustic_metadata(cfg))
+
+
+def acoustic_metadata(cfg: dict) -> dict:
+    """Metadata AcousticConfig::from_gguf reads (acoustic.rs:64-82)."""
+    U32, F32, STR, BOOL = 4, 6, 8, 7
+    return {
+        "general.architecture": (STR, "voxcpm-acoustic"),
+        "general.alignment": (U32, ALIGN),
+        "voxcpm.model_version": (F32, cfg["model_version"]),
+        "voxcpm.residual_lm.n_layer": (U32, cfg["residual_block_count"]),
+        "voxcpm.residual_lm.n_embd": (U32, cfg["embedding_length"]),
+        "voxcpm.residual_lm.no_rope": (BOOL, bool(cfg["no_rope"])),
+        "voxcpm.fsq.latent_dim": (U32, cfg["fsq_latent_dim"]),
+        "voxcpm.fsq.scale": (F32, cfg["fsq_scale"]),
+    }
