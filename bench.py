@@ -20,6 +20,8 @@ Prints one JSON line with:
                TFLOP/s against the 2.5 PFLOP/s dense f16 MFMA peak
   cfm          the LocDiT flow-matching solve (8 layers, hidden 1024, CFG batch
                2, 10 timesteps): solve time and weight-streaming GB/s
+  residual     the ResidualLM step (FSQ + fusion + 8 F16 layers without RoPE,
+               hidden 2048): steps/s and weight-streaming GB/s
 
 `--copy-calibration` instead runs one plain copy kernel of known size (the
 reference point for the FETCH_SIZE / WRITE_SIZE counters).
@@ -93,6 +95,9 @@ def parse():
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--cfm-reps", type=int, default=5, help="CFM solves timed (0 skips the CFM leg)")
     ap.add_argument("--cfm-only", action="store_true", help="run only the LocDiT CFM leg (for profiling)")
+    ap.add_argument("--residual-steps", type=int, default=64,
+                    help="ResidualLM steps timed (0 skips the ResidualLM leg)")
+    ap.add_argument("--residual-only", action="store_true", help="run only the ResidualLM leg (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the token-batched prefill leg (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -224,6 +229,59 @@ def cfm_leg(ctx, reps):
             "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "per_kernel_eager": per}
 
 
+def residual_step_bytes(pos):
+    """Algorithmic bytes of one FSQ ResidualLM step at position pos: F16 weights
+    and biases of fsq.in/out, the fusion projection and 8 layers, the f32 norm
+    gains, and the f16 K/V rows read by the attention (positions 0..pos)."""
+    Hr, Lr, Fr, KVr, Lat = 2048, 8, 6144, 256, 512
+    fsq = 2 * (Lat * Hr + Lat) + 2 * (Hr * Lat + Hr)
+    fusion = 2 * (Hr * 2 * Hr + Hr)
+    layer = 2 * (Hr * (Hr + 2 * KVr) + Hr * Hr + 3 * Fr * Hr) + 2 * Hr * 4 + 2 * (pos + 1) * KVr * 2
+    return fsq + fusion + Lr * layer + Hr * 4
+
+
+def residual_leg(ctx, steps, warmup=8):
+    """The ResidualLM step of the VoxCPM2 acoustic model (acoustic.rs:830-1035):
+    FSQ of the BaseLM hidden, fusion with the acoustic embedding, 8 F16 layers
+    (hidden 2048, FFN 6144, 16/2 x 128, no RoPE), F16 weights N(0, 0.02); inputs
+    resident in device buffers, one graph replay per step with the reference's
+    wait per step (step_from_gpu_base_and_embedding_gpu_only)."""
+    from voxgen_amd import synth
+    from voxgen_amd.residual import ResidualFsqEngine
+    from voxgen_amd.runtime import Model
+    acfg = synth.acoustic_config(active_context=512)
+    m = synth.build_acoustic(acfg, seed=0x5EED0016)
+    model = Model(ctx, m.data, m.tensors)
+    eng = ResidualFsqEngine(ctx, model, acfg, exec_mode="graph", strict_geometry=True)
+    base = ctx.array(synth.normal_f32(2048, 0x5EED0017))
+    emb = ctx.array(synth.normal_f32(2048, 0x5EED0018))
+    for _ in range(warmup):
+        eng.step_from_gpu_base_and_embedding_gpu_only(base, emb)
+    ctx.sync()
+    p0 = eng.position
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.step_from_gpu_base_and_embedding_gpu_only(base, emb)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / steps
+    nbytes = float(np.mean([residual_step_bytes(p) for p in range(p0, p0 + steps)]))
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    eng.step_from_gpu_base_and_embedding_gpu_only(base, emb)
+    prof = ctx.prof_snapshot()
+    ctx.prof_enable(False)
+    eng.close()
+    model.free()
+    log(f"residual step: {ms * 1e3:.1f} us ({1e3 / ms:.0f} steps/s); {nbytes / 1e6:.1f} MB -> {gbps:.0f} GB/s")
+    per = {k: dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"]) for k, v in prof.items()}
+    return {"workload": "residual_lm_f16_fsq_fusion_8L_h2048_ffn6144_16q2kv", "us_per_step": round(ms * 1e3, 2),
+            "steps_per_second": round(1e3 / ms, 1), "positions": f"{p0}..{p0 + steps - 1}",
+            "bytes_per_step": int(nbytes), "achieved_GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "per_kernel_eager": per}
+
+
 def synth_tokens(n, cfg):
     from voxgen_amd import synth
     return synth.uniform_u32(n, 0x5EED0013, cfg["vocab_size"]).astype(np.uint32)
@@ -256,6 +314,13 @@ def main():
     eng = BaseLmEngine(ctx, model, cfg, exec_mode=args.mode, strict_geometry=True)
     log(f"device {info['name']} {info['arch']} CUs={info['compute_units']}; model on device "
         f"{model.device_bytes / 1e9:.2f} GB")
+    if args.residual_only:
+        rs = residual_leg(ctx, args.residual_steps)
+        eng.close()
+        model.free()
+        ctx.close()
+        print(json.dumps({"residual": rs}), flush=True)
+        return
     if args.cfm_only:
         cf = cfm_leg(ctx, args.cfm_reps)
         eng.close()
@@ -328,6 +393,7 @@ def main():
     eng.close()
     model.free()
     cfm = cfm_leg(ctx, args.cfm_reps) if args.cfm_reps else None
+    residual = residual_leg(ctx, args.residual_steps) if args.residual_steps else None
     ctx.close()
 
     line = {
@@ -358,6 +424,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "cfm": cfm,
+        "residual": residual,
         "device": f"{info['name']} ({info['arch']})",
     }
     print(json.dumps(line), flush=True)
