@@ -817,6 +817,17 @@ int vx_residual_benchmark(vx_residual *eng, const float *base_hidden, const floa
 int vx_residual_predict_stop_from_gpu_base(vx_residual *eng, const vx_buf *base_hidden, vx_stop_prediction *out);
 /* predict_stop_from_current_lm (acoustic.rs:638-652). */
 int vx_residual_predict_stop_from_current_lm(vx_residual *eng, vx_stop_prediction *out);
+/* n text-prefix positions (step_text_prefix_from_gpu_base_gpu_only each,
+ * acoustic.rs:733-736) from n BaseLM output rows [n][hidden] f32 at once: one
+ * batched fusion projection and a token-batched ResidualLM stack. Enqueue only;
+ * graph or fused exec mode. */
+int vx_residual_prefill_text_from_gpu_rows(vx_residual *eng, const vx_buf *rows, uint32_t n);
+/* The text runs of prefill_conditioning_plan (runtime.rs:483-566): for each token,
+ * a BaseLM decode then a ResidualLM text-prefix step from its output, computed as
+ * a batched BaseLM prefill (every position's output row kept) followed by the
+ * batched ResidualLM text prefix, in chunks of up to 512 positions. Both engines
+ * advance by n and end in the state of the last position. Enqueue only. */
+int vx_prefill_text_cross_engine(vx_baselm *base, vx_residual *eng, const uint32_t *tokens, uint32_t n);
 
 #ifdef __cplusplus
 }

@@ -233,3 +233,103 @@ def test_full_contract_steps(ctx):
     assert rel_l2([st.continue_logit, st.stop_logit], o.stop(o.current_lm)) < 1e-3
     eng.close()
     model.free()
+
+
+# ------------------------------------------------------- batched text prefix
+def _kv(eng, acfg, which, n):
+    L, ctxlen, kv = acfg["residual_block_count"], acfg["active_context_length"], acfg["kv_dim"]
+    c = eng.buffer(which).download(np.float16, L * ctxlen * kv).reshape(L, ctxlen, kv)
+    return c[:, :n].astype(np.float32)
+
+
+def test_prefill_from_rows_matches_per_position_steps(ctx):
+    """600 text-prefix positions from given rows (two chunks, a partial 128-row
+    tile) against the per-position text-prefix step, which the tests above pin to
+    the oracle; then one FSQ step on top of each cache."""
+    acfg = synth.acoustic_config(layers=2, active_context=640)
+    m = synth.build_acoustic(acfg, seed=0x5EED0405)
+    model = Model(ctx, m.data, m.tensors)
+    H, n = acfg["embedding_length"], 600
+    rows = synth.normal_f32(n * H, 0x700).reshape(n, H)
+    rbuf = ctx.array(rows)
+    one = ctx.array(np.zeros(H, np.float32))
+    seq = ResidualFsqEngine(ctx, model, acfg, exec_mode="graph", strict_geometry=False)
+    for t in range(n):
+        one.upload(rows[t])
+        seq.step_text_prefix_from_gpu_base_gpu_only(one)
+    bat = ResidualFsqEngine(ctx, model, acfg, exec_mode="fused", strict_geometry=False)
+    bat.prefill_text_from_gpu_rows(rbuf, n)
+    ctx.sync()
+    assert bat.position == n
+    for name in ("output", "hidden", "fusion_snapshot", "current_lm"):
+        a, b = bat.buffer(name).download(np.float32, H), seq.buffer(name).download(np.float32, H)
+        assert rel_l2(a, b) < 1e-3, name
+    for which in ("kv_k", "kv_v"):
+        a, b = _kv(bat, acfg, which, n), _kv(seq, acfg, which, n)
+        for l in range(2):
+            assert rel_l2(a[l], b[l]) < 1e-3, (which, l)
+    base, emb = ctx.array(synth.normal_f32(H, 0x701)), ctx.array(synth.normal_f32(H, 0x702))
+    seq.step_from_gpu_base_and_embedding(base, emb)
+    bat.step_from_gpu_base_and_embedding(base, emb)
+    assert rel_l2(bat.output(), seq.output()) < 1e-3
+    with pytest.raises(abi.VxError) as e:
+        bat.prefill_text_from_gpu_rows(rbuf, 40)
+    assert e.value.name == "VX_ERR_CONTEXT_FULL"
+    ref = ResidualFsqEngine(ctx, model, acfg, exec_mode="reference", strict_geometry=False)
+    with pytest.raises(abi.VxError) as e:
+        ref.prefill_text_from_gpu_rows(rbuf, 4)
+    assert e.value.name == "VX_ERR_STATE"
+    for x in (seq, bat, ref):
+        x.close()
+    model.free()
+
+
+def test_cross_engine_text_prefill_matches_sequential_and_oracle(ctx):
+    """BaseLM (2 Q8_0 layers) + ResidualLM (2 F16 layers) text prefix of 37
+    tokens: batched per engine vs one decode + one text-prefix step per token, and
+    the last ResidualLM output vs the oracles chained the same way."""
+    from voxgen_amd.baselm import BaseLmEngine
+    from voxgen_amd.residual import prefill_text_cross_engine
+    bcfg = synth.baselm_config(layers=2, vocab=512, context_length=256, active_context=256)
+    bm = synth.build_baselm(bcfg, seed=0x5EED0406)
+    bmodel = Model(ctx, bm.data, bm.tensors)
+    acfg = synth.acoustic_config(layers=2, active_context=256)
+    am = synth.build_acoustic(acfg, seed=0x5EED0407)
+    amodel = Model(ctx, am.data, am.tensors)
+    tokens = synth.uniform_u32(37, 0x703, 512)
+    H = acfg["embedding_length"]
+    b1 = BaseLmEngine(ctx, bmodel, bcfg, strict_geometry=False)
+    r1 = ResidualFsqEngine(ctx, amodel, acfg, strict_geometry=False)
+    for t in tokens:
+        b1.decode_token_gpu_only(int(t))
+        r1.step_text_prefix_from_gpu_base_gpu_only(b1.buffer("norm"))
+    b2 = BaseLmEngine(ctx, bmodel, bcfg, strict_geometry=False)
+    r2 = ResidualFsqEngine(ctx, amodel, acfg, strict_geometry=False)
+    prefill_text_cross_engine(b2, r2, tokens)
+    ctx.sync()
+    assert b2.position == 37 and r2.position == 37
+    assert rel_l2(b2.output(), b1.output()) < 1e-3
+    for name in ("output", "current_lm", "fusion_snapshot"):
+        assert rel_l2(r2.buffer(name).download(np.float32, H), r1.buffer(name).download(np.float32, H)) < 1e-3, name
+    for which in ("kv_k", "kv_v"):
+        a, b = _kv(r2, acfg, which, 37), _kv(r1, acfg, which, 37)
+        assert rel_l2(a, b) < 1e-3, which
+    ob = voxref.BaseLm(bm.data, {t.name: t for t in bm.tensors}, bcfg)
+    orr = oracle_of(am, acfg)
+    for pos, t in enumerate(tokens):
+        row = ob.decode_token(int(t), pos)
+        want = orr.step(row, None, pos, fsq=False)
+    assert rel_l2(r2.output(), want["norm"]) < 5e-3
+    r3 = ResidualFsqEngine(ctx, amodel, dict(acfg, embedding_length=H), strict_geometry=False)
+    small = synth.baselm_config(layers=1, hidden=256, ffn=512, vocab=64, q_heads=2, kv_heads=1, context_length=64,
+                                active_context=64)
+    sm = synth.build_baselm(small, seed=3)
+    smodel = Model(ctx, sm.data, sm.tensors)
+    b3 = BaseLmEngine(ctx, smodel, small, strict_geometry=False)
+    with pytest.raises(abi.VxError) as e:
+        prefill_text_cross_engine(b3, r3, tokens[:4])
+    assert e.value.name == "VX_ERR_SHAPE"
+    for x in (b1, r1, b2, r2, r3, b3):
+        x.close()
+    for x in (bmodel, amodel, smodel):
+        x.free()

@@ -298,6 +298,8 @@ PROTOTYPES = {
     "vx_residual_benchmark": (i32, [RESIDUAL, P(f32), P(f32), u32, u32, u32, P(ResidualBenchmark)]),
     "vx_residual_predict_stop_from_gpu_base": (i32, [RESIDUAL, BUFP, P(StopPrediction)]),
     "vx_residual_predict_stop_from_current_lm": (i32, [RESIDUAL, P(StopPrediction)]),
+    "vx_residual_prefill_text_from_gpu_rows": (i32, [RESIDUAL, BUFP, u32]),
+    "vx_prefill_text_cross_engine": (i32, [ENGINE, RESIDUAL, P(u32), u32]),
 }
 
 STRUCT_SIZES = {  # C name -> ctypes struct

@@ -27,10 +27,7 @@ using namespace vx;
 
 namespace {
 
-struct Layer {
-    WRef q, k, v, o, gate, up, down;
-    const float *attn_norm = nullptr, *ffn_norm = nullptr;
-};
+using Layer = StackLayer;
 
 float effective_scale(float v) { return v == 0.0f ? 1.0f : v; }  // baselm.rs:1262-1264
 
@@ -56,17 +53,11 @@ struct vx_baselm {
     vx_graph *graphs[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
     // Token-batched prefill workspace (allocated on first use): residual stream,
     // hi/lo f16 planes of the GEMM inputs, q/k/v, roped q planes, token ids.
-    uint32_t pf_cap = 0;   // tokens per chunk
-    vx_buf *pf_h = nullptr, *pf_xh = nullptr, *pf_xl = nullptr, *pf_ah = nullptr, *pf_al = nullptr;
-    vx_buf *pf_qh = nullptr, *pf_ql = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    StackWork pf;
     vx_buf *pf_tok = nullptr;
-    vx_buf *pf_ws = nullptr;   // split-K partials of the projections [kPrefillMaxSplit][cap][H + 2 KV]
     // Q8_0 weights in the prefill-GEMM layout (built by the first batched prefill
     // that can use them; empty when some projection is not Q8_0).
-    struct PrefillLayer {
-        PrefillMatrix q, k, v, o, gu, down;
-    };
-    std::vector<PrefillLayer> pw;
+    std::vector<StackPrefillWeights> pw;
     vx_buf *pw_arena = nullptr;
     bool pw_tried = false;
     // Persistent decode step: per-layer weight table, phase counters, sticky
@@ -179,14 +170,13 @@ void free_all(vx_baselm *e) {
     vx_buf **bufs[] = {&e->hidden, &e->norm,   &e->q,      &e->k,        &e->v,
                        &e->attention, &e->gate, &e->branch, &e->logits, &e->scores,
                        &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table,
-                       &e->pf_h, &e->pf_xh,    &e->pf_xl,  &e->pf_ah,    &e->pf_al,     &e->pf_qh,
-                       &e->pf_ql, &e->pf_q,    &e->pf_k,   &e->pf_v,     &e->pf_tok,    &e->ps_layers,
-                       &e->ps_cnt, &e->ps_err, &e->ps_part, &e->ps_trace, &e->pw_arena, &e->pf_ws};
+                       &e->pf_tok, &e->ps_layers, &e->ps_cnt, &e->ps_err, &e->ps_part, &e->ps_trace,
+                       &e->pw_arena};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
     }
-    e->pf_cap = 0;
+    prefill_stack_free(e->ctx, &e->pf);
     e->pw.clear();
     e->pw_tried = false;
 }
@@ -648,46 +638,39 @@ int run_step(vx_baselm *e, bool with_embedding, uint32_t token, bool logits) {
 //   then the last token's rmsnorm(h)*output_norm into the engine's norm buffer.
 // This computes what prefill_tokens (baselm.rs:823-839) computes one token at a
 // time: the same KV-cache rows and the same final state, to rounding.
-constexpr uint32_t kPrefillChunk = 512;
-constexpr uint32_t kPrefillMaxSplit = 8;   // split-K factor bound (pick_split)
-
 int ensure_prefill_work(vx_baselm *e) {
-    if (e->pf_cap) return VX_OK;
+    if (e->pf.cap) return VX_OK;
     const vx_baselm_config &c = e->cfg;
     const uint32_t cap = std::min<uint32_t>(kPrefillChunk, c.active_context_length);
-    const uint64_t H = c.embedding_length, F = c.feed_forward_length, KV = c.kv_dim, T = cap;
-    const uint64_t Tp = (T + 127u) / 128u * 128u;   // GEMM input planes: whole 128-token tiles
-    vx_ctx *ctx = e->ctx;
-    VX_CHECK(alloc(ctx, T * H * 4u, &e->pf_h));
-    VX_CHECK(alloc(ctx, Tp * H * 2u, &e->pf_xh));
-    VX_CHECK(alloc(ctx, Tp * H * 2u, &e->pf_xl));
-    VX_CHECK(alloc(ctx, Tp * F * 2u, &e->pf_ah));
-    VX_CHECK(alloc(ctx, Tp * F * 2u, &e->pf_al));
-    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_qh));
-    VX_CHECK(alloc(ctx, T * H * 2u, &e->pf_ql));
-    VX_CHECK(alloc(ctx, T * H * 4u, &e->pf_q));
-    VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_k));
-    VX_CHECK(alloc(ctx, T * KV * 4u, &e->pf_v));
-    VX_CHECK(alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->pf_tok));
-    // Split-K partials: of the residual projections ([split][T][H]) and of QKV
-    // ([split][T][H + 2 KV]); the two uses never overlap in time.
-    VX_CHECK(alloc(ctx, (uint64_t)kPrefillMaxSplit * T * (H + 2u * e->cfg.kv_dim) * 4u, &e->pf_ws));
-    e->pf_cap = cap;
-    return VX_OK;
+    VX_CHECK(prefill_stack_alloc(e->ctx, cap, c.embedding_length, c.feed_forward_length, c.kv_dim, &e->pf));
+    return alloc(e->ctx, (uint64_t)c.active_context_length * 4u, &e->pf_tok);
 }
 
-GemmSeg gemm_seg(const WRef &w, uint32_t rows, float *out, uint32_t ldo) {
-    GemmSeg g;
-    if (w.wt == WT_Q8) {
-        g.qs = static_cast<const int8_t *>(w.ptr);
-        g.d = w.d;
-    } else {
-        g.w = static_cast<const __half *>(w.ptr);
-    }
-    g.rows = rows;
-    g.out = out;
-    g.ldo = ldo;
-    return g;
+// The BaseLM layers as a token-batched stack (RoPE on, the engine's KV caches).
+PrefillStack make_stack(vx_baselm *e) {
+    const vx_baselm_config &c = e->cfg;
+    PrefillStack p;
+    p.ctx = e->ctx;
+    p.nH = c.embedding_length;
+    p.nF = c.feed_forward_length;
+    p.nKV = c.kv_dim;
+    p.q_heads = c.head_count;
+    p.kv_heads = c.head_count_kv;
+    p.head_dim = c.head_dim;
+    p.context = c.active_context_length;
+    p.n_layers = c.block_count;
+    p.eps = c.rms_epsilon;
+    p.residual_scale = e->residual_scale;
+    p.layers = e->layers.data();
+    p.pw = e->pw.empty() ? nullptr : e->pw.data();
+    p.rope = true;
+    p.rope_factors = e->rope_factors;
+    p.theta = c.rope_theta;
+    p.rope_scaling = e->rope_scaling;
+    p.kc = H(e->kv_k);
+    p.vc = H(e->kv_v);
+    p.work = &e->pf;
+    return p;
 }
 
 // Split-K factor that brings a projection to about one workgroup per CU.
@@ -723,7 +706,7 @@ int ensure_prefill_weights(vx_baselm *e) {
     e->pw.resize(c.block_count);
     for (uint32_t l = 0; l < c.block_count; ++l) {
         const Layer &L = e->layers[l];
-        vx_baselm::PrefillLayer &P = e->pw[l];
+        StackPrefillWeights &P = e->pw[l];
         int st = VX_OK;
         if ((st = place(P.q, L.q, nullptr, nH, nH)) || (st = place(P.k, L.k, nullptr, nKV, nH)) ||
             (st = place(P.v, L.v, nullptr, nKV, nH)) || (st = place(P.o, L.o, nullptr, nH, nH)) ||
@@ -735,303 +718,50 @@ int ensure_prefill_weights(vx_baselm *e) {
     return VX_OK;
 }
 
-// Split-K factor for a projection of n_tiles 128-row tiles and tt-token tiles:
-// enough workgroups to cover the CUs, at least four 32-column blocks per split.
-uint32_t pick_split(const vx_baselm *e, uint32_t tt, uint32_t n_tiles, uint32_t T, uint32_t K) {
-    const uint32_t tiles = n_tiles * ((T + tt - 1u) / tt);
-    const uint32_t cus = e->ctx->props.multiProcessorCount > 0 ? (uint32_t)e->ctx->props.multiProcessorCount : 256u;
-    uint32_t ks = (cus + tiles - 1u) / tiles;
-    ks = std::min<uint32_t>(ks, tt > 64u ? 8u : 4u);
-    ks = std::min<uint32_t>(ks, std::max<uint32_t>(1u, K / 128u));
-    return std::max<uint32_t>(ks, 1u);
-}
-
-int check_prefill_layout(const vx_baselm *e) {
-    for (uint32_t l = 0; l < e->cfg.block_count; ++l) {
-        const Layer &L = e->layers[l];
-        const WRef *ws[] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
-        for (const WRef *w : ws) {
-            if (w->wt == WT_Q8 && !w->ptr)
-                return fail(VX_ERR_UNSUPPORTED,
-                            "batched prefill needs Q8_0 row widths that are multiples of 1024 (layer %u)", l);
-            if (w->wt == WT_F16 && (w->cols % 128u))
-                return fail(VX_ERR_UNSUPPORTED, "batched prefill needs F16 row widths that are multiples of 128");
-            if (w->wt == WT_F32) return fail(VX_ERR_UNSUPPORTED, "batched prefill has no F32 projection path");
-        }
-    }
-    if (e->cfg.head_dim != 64u && e->cfg.head_dim != 128u)
-        return fail(VX_ERR_UNSUPPORTED, "batched prefill attention needs head_dim 64 or 128");
-    const uint32_t qpk = e->cfg.head_count / e->cfg.head_count_kv;
-    if (qpk != 1u && qpk != 2u && qpk != 4u && qpk != 8u)
-        return fail(VX_ERR_UNSUPPORTED, "batched prefill attention needs 1, 2, 4 or 8 query heads per KV head");
-    return VX_OK;
-}
-
 // One chunk of T tokens at positions pos0..pos0+T-1, token ids at tok (device).
-int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint32_t T) {
+int enqueue_prefill_chunk(vx_baselm *e, const uint32_t *tok, uint32_t pos0, uint32_t T, float *rows) {
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_baselm_config &c = e->cfg;
-    const uint32_t nH = c.embedding_length, nF = c.feed_forward_length, nKV = c.kv_dim;
+    const uint32_t nH = c.embedding_length;
     {
         ProfSpan sp(ctx, "prefill.embedding");
         VX_CHECK(launch_seq_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, nH, tok, T, c.vocab_size,
-                                      e->embedding_alpha, F(e->pf_h), nH));
+                                      e->embedding_alpha, F(e->pf.h), nH));
     }
-    // The deep-pipelined GEMM takes the prefill-layout weights and tiled planes,
-    // from one full 128-token tile up.
-    const bool tiled = !e->pw.empty() && T >= gemm_q8p_tile_tokens();
-    const uint32_t tt = tiled ? gemm_q8p_tile_tokens() : 64u;
-    const uint32_t ks_qkv = pick_split(e, tt, (nH + 127u) / 128u + 2u * ((nKV + 127u) / 128u), T, nH);
-    const uint32_t ks_o = pick_split(e, tt, (nH + 127u) / 128u, T, nH);
-    const uint32_t ks_down = pick_split(e, tt, (nH + 127u) / 128u, T, nF);
-    // Split residual projections on the tiled path leave their partials in
-    // pf_ws; the next rmsnorm adds them to h (no atomics in the GEMM epilogue).
-    const uint64_t ws_stride = (uint64_t)e->pf_cap * nH;
-    const bool ws_o = tiled && ks_o > 1, ws_down = tiled && ks_down > 1;
-    // Split QKV on the tiled path stores its partials to pf_ws as well (q, k, v
-    // regions of one split, ws_qkv floats per split); the RoPE kernel sums them.
-    const bool ws_qkv = tiled && ks_qkv > 1;
-    const uint64_t ws_qkv_stride = (uint64_t)e->pf_cap * (nH + 2u * nKV);
-    float *const wq = F(e->pf_ws), *const wk = wq + (size_t)e->pf_cap * nH, *const wv = wk + (size_t)e->pf_cap * nKV;
-    for (uint32_t l = 0; l < c.block_count; ++l) {
-        const Layer &L = e->layers[l];
-        {
-            ProfSpan sp(ctx, "prefill.norm");
-            SeqNormArgs n;
-            n.h = F(e->pf_h);
-            n.ldh = nH;
-            n.w = L.attn_norm;
-            if (l > 0 && ws_down) {
-                n.branch = F(e->pf_ws);
-                n.ldb = nH;
-                n.nbranch = ks_down;
-                n.branch_stride = ws_stride;
-            }
-            n.n = nH;
-            n.eps = c.rms_epsilon;
-            n.yh = H(e->pf_xh);
-            n.yl = H(e->pf_xl);
-            n.ldp = nH;
-            n.tiled = tiled ? 1u : 0u;
-            if (ks_qkv > 1 && !ws_qkv) {
-                n.zero[0] = F(e->pf_q);
-                n.zero_n[0] = nH;
-                n.zero[1] = F(e->pf_k);
-                n.zero_n[1] = nKV;
-                n.zero[2] = F(e->pf_v);
-                n.zero_n[2] = nKV;
-            }
-            VX_CHECK(launch_seq_rmsnorm(s, n, T));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.qkv");
-            GemmArgs g;
-            g.wk = L.q.wt;
-            g.epi = GEPI_STORE;
-            g.seg[0] = gemm_seg(L.q, nH, F(e->pf_q), nH);
-            g.seg[1] = gemm_seg(L.k, nKV, F(e->pf_k), nKV);
-            g.seg[2] = gemm_seg(L.v, nKV, F(e->pf_v), nKV);
-            if (tiled) {
-                const vx_baselm::PrefillLayer &P = e->pw[l];
-                g.seg[0].pq = P.q.q;
-                g.seg[0].pd = P.q.d;
-                g.seg[1].pq = P.k.q;
-                g.seg[1].pd = P.k.d;
-                g.seg[2].pq = P.v.q;
-                g.seg[2].pd = P.v.d;
-                g.x_tiled = 1;
-            }
-            g.nseg = 3;
-            g.K = nH;
-            g.T = T;
-            g.xh = H(e->pf_xh);
-            g.xl = H(e->pf_xl);
-            g.ldx = nH;
-            g.ksplit = ks_qkv;
-            if (ws_qkv) {
-                g.seg[0].out = wq;
-                g.seg[1].out = wk;
-                g.seg[2].out = wv;
-                g.split_store = 1;
-                g.ws_stride = ws_qkv_stride;
-            }
-            VX_CHECK(launch_gemm(s, g));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.rope_store");
-            SeqRopeArgs r;
-            r.q = ws_qkv ? wq : F(e->pf_q);
-            r.k = ws_qkv ? wk : F(e->pf_k);
-            r.v = ws_qkv ? wv : F(e->pf_v);
-            if (ws_qkv) {
-                r.nsplit = ks_qkv;
-                r.split_stride = ws_qkv_stride;
-            }
-            r.ldq = nH;
-            r.ldk = nKV;
-            r.factors = e->rope_factors;
-            r.pos_base = pos0;
-            r.q_heads = c.head_count;
-            r.kv_heads = c.head_count_kv;
-            r.head_dim = c.head_dim;
-            r.theta = c.rope_theta;
-            r.scaling = e->rope_scaling;
-            r.q_inplace = 0;
-            r.qh = H(e->pf_qh);
-            r.ql = H(e->pf_ql);
-            r.ldqp = nH;
-            r.kc = H(e->kv_k);
-            r.vc = H(e->kv_v);
-            r.layer = l;
-            r.context = c.active_context_length;
-            VX_CHECK(launch_seq_rope_store(s, r, T));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.attention");
-            PrefillAttnArgs a;
-            a.qh = H(e->pf_qh);
-            a.ql = H(e->pf_ql);
-            a.ldq = nH;
-            a.kc = H(e->kv_k);
-            a.vc = H(e->kv_v);
-            a.layer = l;
-            a.context = c.active_context_length;
-            a.pos_base = pos0;
-            a.T = T;
-            a.q_heads = c.head_count;
-            a.kv_heads = c.head_count_kv;
-            a.head_dim = c.head_dim;
-            a.oh = H(e->pf_xh);
-            a.ol = H(e->pf_xl);
-            a.ldo = nH;
-            a.tiled = tiled ? 1u : 0u;
-            VX_CHECK(launch_prefill_attn(s, a));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.attn_out");
-            GemmArgs g;
-            g.wk = L.o.wt;
-            g.epi = GEPI_RESIDUAL;
-            g.seg[0] = gemm_seg(L.o, nH, F(e->pf_h), nH);
-            if (tiled) {
-                g.seg[0].pq = e->pw[l].o.q;
-                g.seg[0].pd = e->pw[l].o.d;
-                g.x_tiled = 1;
-            }
-            g.K = nH;
-            g.T = T;
-            g.xh = H(e->pf_xh);
-            g.xl = H(e->pf_xl);
-            g.ldx = nH;
-            g.scale = e->residual_scale;
-            g.ksplit = ks_o;
-            if (ws_o) {
-                g.ws = F(e->pf_ws);
-                g.ws_stride = ws_stride;
-            }
-            VX_CHECK(launch_gemm(s, g));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.norm");
-            SeqNormArgs n;
-            n.h = F(e->pf_h);
-            n.ldh = nH;
-            n.w = L.ffn_norm;
-            if (ws_o) {
-                n.branch = F(e->pf_ws);
-                n.ldb = nH;
-                n.nbranch = ks_o;
-                n.branch_stride = ws_stride;
-            }
-            n.n = nH;
-            n.eps = c.rms_epsilon;
-            n.yh = H(e->pf_xh);
-            n.yl = H(e->pf_xl);
-            n.ldp = nH;
-            n.tiled = tiled ? 1u : 0u;
-            VX_CHECK(launch_seq_rmsnorm(s, n, T));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.swiglu");
-            GemmArgs g;
-            g.wk = L.gate.wt;
-            g.epi = GEPI_SWIGLU;
-            g.seg[0] = gemm_seg(L.gate, nF, nullptr, 0);
-            g.seg[1] = gemm_seg(L.up, nF, nullptr, 0);
-            if (tiled) {
-                g.seg[0].pq = e->pw[l].gu.q;   // gate and up interleaved
-                g.seg[0].pd = e->pw[l].gu.d;
-                g.x_tiled = 1;
-                g.o_tiled = 1;
-            }
-            g.nseg = 2;
-            g.K = nH;
-            g.T = T;
-            g.xh = H(e->pf_xh);
-            g.xl = H(e->pf_xl);
-            g.ldx = nH;
-            g.oh = H(e->pf_ah);
-            g.ol = H(e->pf_al);
-            g.ldp = nF;
-            VX_CHECK(launch_gemm(s, g));
-        }
-        {
-            ProfSpan sp(ctx, "prefill.down");
-            GemmArgs g;
-            g.wk = L.down.wt;
-            g.epi = GEPI_RESIDUAL;
-            g.seg[0] = gemm_seg(L.down, nH, F(e->pf_h), nH);
-            if (tiled) {
-                g.seg[0].pq = e->pw[l].down.q;
-                g.seg[0].pd = e->pw[l].down.d;
-                g.x_tiled = 1;
-            }
-            g.K = nF;
-            g.T = T;
-            g.xh = H(e->pf_ah);
-            g.xl = H(e->pf_al);
-            g.ldx = nF;
-            g.scale = e->residual_scale;
-            g.ksplit = ks_down;
-            if (ws_down) {
-                g.ws = F(e->pf_ws);
-                g.ws_stride = ws_stride;
-            }
-            VX_CHECK(launch_gemm(s, g));
-        }
-    }
-    if (ws_down) {   // the last layer's down partials
-        ProfSpan sp(ctx, "prefill.norm");
+    VX_CHECK(enqueue_prefill_stack(make_stack(e), pos0, T));
+    if (rows) {   // every token's output_buffer (rmsnorm(h)*output_norm), as the decode step leaves it
+        ProfSpan sp(ctx, "prefill.output_rows");
         SeqNormArgs n;
-        n.h = F(e->pf_h);
+        n.h = F(e->pf.h);
         n.ldh = nH;
+        n.w = e->output_norm;
         n.n = nH;
-        n.branch = F(e->pf_ws);
-        n.ldb = nH;
-        n.nbranch = ks_down;
-        n.branch_stride = ws_stride;
+        n.eps = c.rms_epsilon;
+        n.y = rows;
+        n.ldy = nH;
         VX_CHECK(launch_seq_rmsnorm(s, n, T));
     }
     // Engine state after the chunk: hidden = last token's residual stream, norm =
     // its rmsnorm(h)*output_norm (record_transformer's final residual_rmsnorm).
     ProfSpan sp(ctx, "prefill.output_norm");
-    const float *last = F(e->pf_h) + (size_t)(T - 1u) * nH;
+    const float *last = F(e->pf.h) + (size_t)(T - 1u) * nH;
     VX_HIP(hipMemcpyAsync(e->hidden->ptr, last, (size_t)nH * 4u, hipMemcpyDeviceToDevice, s));
     return launch_rmsnorm(s, last, F(e->norm), e->output_norm, nH, c.rms_epsilon, nullptr);
 }
 
 // Prefill n tokens at the engine position: upload the ids, run the chunks, leave
 // the device position at the next decode position.
-int enqueue_prefill(vx_baselm *e, const uint32_t *tokens, uint32_t n) {
-    VX_CHECK(check_prefill_layout(e));
+int enqueue_prefill(vx_baselm *e, const uint32_t *tokens, uint32_t n, float *rows = nullptr) {
+    VX_CHECK(prefill_stack_check(make_stack(e)));
     VX_CHECK(ensure_prefill_work(e));
     VX_CHECK(ensure_prefill_weights(e));
     hipStream_t s = e->ctx->stream;
     VX_HIP(hipMemcpyAsync(e->pf_tok->ptr, tokens, (size_t)n * 4u, hipMemcpyHostToDevice, s));
     for (uint32_t done = 0; done < n;) {
-        const uint32_t T = std::min<uint32_t>(e->pf_cap, n - done);
-        VX_CHECK(enqueue_prefill_chunk(e, U(e->pf_tok) + done, e->pos + done, T));
+        const uint32_t T = std::min<uint32_t>(e->pf.cap, n - done);
+        VX_CHECK(enqueue_prefill_chunk(e, U(e->pf_tok) + done, e->pos + done, T,
+                                       rows ? rows + (size_t)done * e->cfg.embedding_length : nullptr));
         done += T;
     }
     VX_CHECK(launch_set_step(s, U(e->tokens), U(e->position), e->pos + n, 0, 0));
@@ -1096,6 +826,21 @@ int upload_embedding(vx_baselm *e, const float *emb, uint32_t n) {
 }
 
 }  // namespace
+
+namespace vx {
+
+vx_ctx *baselm_context(const vx_baselm *e) { return e->ctx; }
+
+uint32_t baselm_hidden_size(const vx_baselm *e) { return e->cfg.embedding_length; }
+
+int baselm_prefill_rows(vx_baselm *e, const uint32_t *tokens, uint32_t n, float *rows) {
+    if (!tokens || n == 0) return fail(VX_ERR_INVALID_ARG, "prefill token list is empty");
+    for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
+    VX_CHECK(ensure_context(e, n));
+    return enqueue_prefill(e, tokens, n, rows);
+}
+
+}  // namespace vx
 
 extern "C" {
 

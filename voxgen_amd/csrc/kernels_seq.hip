@@ -502,7 +502,7 @@ __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
     const uint32_t t = blockIdx.x;
     const uint32_t pos = a.pos_base + (a.pos_period ? t % a.pos_period : t);
     const uint32_t half_dim = a.head_dim / 2u;
-    if (threadIdx.x < half_dim) {
+    if (threadIdx.x < half_dim && !a.no_rope) {
         const uint32_t i = threadIdx.x;
         const float exponent = (float)(i * 2u) / (float)a.head_dim;
         const float inv_freq = 1.0f / powf(a.theta, exponent);
@@ -535,8 +535,12 @@ __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
             x0 += sp < ns ? p0[sp] : 0.f;
             x1 += sp < ns ? p1[sp] : 0.f;
         }
-        const float c = cs[i].x, s = cs[i].y;
-        const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
+        float y0 = x0, y1 = x1;
+        if (!a.no_rope) {
+            const float c = cs[i].x, s = cs[i].y;
+            y0 = x0 * c - x1 * s;
+            y1 = x1 * c + x0 * s;
+        }
         if (isq) {
             if (a.q_inplace) {
                 buf[base + i] = y0;

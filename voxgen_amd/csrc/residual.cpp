@@ -30,10 +30,7 @@ using namespace vx;
 
 namespace {
 
-struct RLayer {
-    WRef q, k, v, o, gate, up, down;
-    const float *attn_norm = nullptr, *ffn_norm = nullptr;
-};
+using RLayer = StackLayer;
 
 struct Lin {
     WRef w;
@@ -74,6 +71,11 @@ struct vx_residual {
     bool fold_attn_merge = false;
     uint32_t pos = 0;
     std::vector<CachedGraph> graphs;
+    // Token-batched text prefix (allocated on first use): the layer stack's
+    // activations, the fusion input [cap][2H] (right half kept zero) and the
+    // BaseLM output rows of a cross-engine chunk [cap][H].
+    StackWork pf;
+    vx_buf *fuse_x = nullptr, *rows = nullptr;
 };
 
 namespace {
@@ -157,6 +159,12 @@ void free_all(vx_residual *e) {
     for (CachedGraph &g : e->graphs)
         if (g.g) vx_graph_free(e->ctx, g.g);
     e->graphs.clear();
+    prefill_stack_free(e->ctx, &e->pf);
+    for (vx_buf **b : {&e->fuse_x, &e->rows})
+        if (*b) {
+            vx_free(e->ctx, *b);
+            *b = nullptr;
+        }
     vx_buf **bufs[] = {&e->base_input, &e->current_embed, &e->zero_embed, &e->fsq_latent, &e->fsq_output,
                        &e->current_lm, &e->hidden,        &e->fusion_snapshot, &e->norm,  &e->q,
                        &e->k,          &e->v,             &e->attention, &e->gate,        &e->branch,
@@ -554,9 +562,118 @@ int predict_stop(vx_residual *e, const float *x, vx_stop_prediction *out) {
     return VX_OK;
 }
 
+// ------------------------------------------------------------- batched text prefix
+// The text-prefix positions of a conditioning prefill (runtime.rs:483-566 runs
+// them one BaseLM decode + one ResidualLM text-prefix step at a time) as one
+// token batch per engine: the BaseLM batched prefill leaves every position's
+// output row, the fusion projection takes [row | 0] for all rows at once, and the
+// ResidualLM layers run as a token-batched stack without RoPE over its own cache.
+// The engine state afterwards is the last position's, as after the per-position
+// steps: hidden, norm (output), fusion snapshot and current_lm (the raw row).
+int ensure_prefill_work(vx_residual *e) {
+    if (e->pf.cap) return VX_OK;
+    const vx_acoustic_config &c = e->cfg;
+    const uint32_t cap = std::min<uint32_t>(kPrefillChunk, c.active_context_length);
+    VX_CHECK(prefill_stack_alloc(e->ctx, cap, c.embedding_length, c.feed_forward_length, c.kv_dim, &e->pf));
+    VX_CHECK(vx_alloc(e->ctx, (uint64_t)cap * c.fusion_input_dim * 4u, &e->fuse_x));
+    VX_CHECK(vx_alloc(e->ctx, (uint64_t)cap * c.embedding_length * 4u, &e->rows));
+    VX_HIP(hipMemsetAsync(e->fuse_x->ptr, 0, e->fuse_x->bytes, e->ctx->stream));
+    return VX_OK;
+}
+
+PrefillStack make_stack(vx_residual *e) {
+    const vx_acoustic_config &c = e->cfg;
+    PrefillStack p;
+    p.ctx = e->ctx;
+    p.nH = c.embedding_length;
+    p.nF = c.feed_forward_length;
+    p.nKV = c.kv_dim;
+    p.q_heads = c.head_count;
+    p.kv_heads = c.head_count_kv;
+    p.head_dim = c.head_dim;
+    p.context = c.active_context_length;
+    p.n_layers = c.residual_block_count;
+    p.eps = c.rms_epsilon;
+    p.residual_scale = c.residual_scale;
+    p.layers = e->layers.data();
+    p.rope = false;
+    p.kc = H(e->kv_k);
+    p.vc = H(e->kv_v);
+    p.work = &e->pf;
+    return p;
+}
+
+int check_prefill(vx_residual *e, uint32_t n) {
+    if (n == 0) return fail(VX_ERR_INVALID_ARG, "text prefix of zero positions");
+    if ((uint64_t)e->pos + n > e->cfg.active_context_length)
+        return fail(VX_ERR_CONTEXT_FULL, "ResidualLM KV cache is full at %u positions", e->cfg.active_context_length);
+    if (e->opt.exec_mode == VX_EXEC_REFERENCE)
+        return fail(VX_ERR_STATE, "the batched text prefix needs the graph or fused exec mode");
+    VX_CHECK(prefill_stack_check(make_stack(e)));
+    return ensure_prefill_work(e);
+}
+
+// T <= cap text-prefix positions from BaseLM output rows [T][H] (device).
+int enqueue_prefill_rows(vx_residual *e, const float *rows, uint32_t T) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_acoustic_config &c = e->cfg;
+    const uint32_t nH = c.embedding_length;
+    {
+        ProfSpan sp(ctx, "residual.prefix_fusion");
+        VX_HIP(hipMemcpy2DAsync(e->fuse_x->ptr, (size_t)c.fusion_input_dim * 4u, rows, (size_t)nH * 4u,
+                                (size_t)nH * 4u, T, hipMemcpyDeviceToDevice, s));
+        VX_CHECK(enqueue_seq_linear(s, e->fusion.w, e->fusion.b, e->fusion.bt, nH, c.fusion_input_dim, T,
+                                    F(e->fuse_x), 0, c.fusion_input_dim, F(e->pf.h), 0, nH, 1.f));
+    }
+    const float *last_fused = F(e->pf.h) + (size_t)(T - 1u) * nH;
+    VX_HIP(hipMemcpyAsync(e->fusion_snapshot->ptr, last_fused, (size_t)nH * 4u, hipMemcpyDeviceToDevice, s));
+    VX_HIP(hipMemcpyAsync(e->current_lm->ptr, rows + (size_t)(T - 1u) * nH, (size_t)nH * 4u,
+                          hipMemcpyDeviceToDevice, s));
+    VX_CHECK(enqueue_prefill_stack(make_stack(e), e->pos, T));
+    ProfSpan sp(ctx, "residual.prefix_output_norm");
+    const float *last = F(e->pf.h) + (size_t)(T - 1u) * nH;
+    VX_HIP(hipMemcpyAsync(e->hidden->ptr, last, (size_t)nH * 4u, hipMemcpyDeviceToDevice, s));
+    VX_CHECK(launch_rmsnorm(s, last, F(e->norm), e->output_norm, nH, c.rms_epsilon, nullptr));
+    e->pos += T;
+    return launch_set_step(s, nullptr, U(e->position), e->pos, 0, 0);
+}
+
 }  // namespace
 
 extern "C" {
+
+int vx_residual_prefill_text_from_gpu_rows(vx_residual *e, const vx_buf *rows, uint32_t n) {
+    if (!e) return fail(VX_ERR_INVALID_ARG, "vx_residual_prefill_text_from_gpu_rows: null engine");
+    if (!rows || rows->bytes < (uint64_t)n * e->cfg.embedding_length * 4u)
+        return fail(VX_ERR_BOUNDS, "BaseLM output rows buffer is too small for %u x %u f32 values", n,
+                    e->cfg.embedding_length);
+    VX_CHECK(check_prefill(e, n));
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t T = std::min<uint32_t>(e->pf.cap, n - done);
+        VX_CHECK(enqueue_prefill_rows(e, F(rows) + (size_t)done * e->cfg.embedding_length, T));
+        done += T;
+    }
+    return VX_OK;
+}
+
+int vx_prefill_text_cross_engine(vx_baselm *base, vx_residual *e, const uint32_t *tokens, uint32_t n) {
+    if (!base || !e) return fail(VX_ERR_INVALID_ARG, "vx_prefill_text_cross_engine: null engine");
+    if (baselm_context(base) != e->ctx)
+        return fail(VX_ERR_INVALID_ARG, "the BaseLM and ResidualLM engines must share one context");
+    if (baselm_hidden_size(base) != e->cfg.embedding_length)
+        return fail(VX_ERR_SHAPE, "BaseLM hidden %u != ResidualLM hidden %u", baselm_hidden_size(base),
+                    e->cfg.embedding_length);
+    if (!tokens) return fail(VX_ERR_INVALID_ARG, "prefill token list is empty");
+    VX_CHECK(check_prefill(e, n));
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t T = std::min<uint32_t>(e->pf.cap, n - done);
+        VX_CHECK(baselm_prefill_rows(base, tokens + done, T, F(e->rows)));
+        VX_CHECK(enqueue_prefill_rows(e, F(e->rows), T));
+        done += T;
+    }
+    return VX_OK;
+}
 
 uint64_t vx_acoustic_kv_cache_bytes(const vx_acoustic_config *c) {
     if (!c) return 0;

@@ -406,9 +406,52 @@ struct SeqRopeArgs {
     // GEMM output); the kernel reads their sums and writes roped k to split 0.
     uint32_t nsplit = 1;
     uint64_t split_stride = 0;
+    uint32_t no_rope = 0;               // 1: q/k pass through unrotated (factors unused)
 };
 constexpr uint32_t kSeqRopeMaxSplit = 8;
 int launch_seq_rope_store(hipStream_t s, const SeqRopeArgs &a, uint32_t tokens);
+
+// ------------------------------------------- token-batched decoder stack (prefill)
+struct StackLayer {
+    WRef q, k, v, o, gate, up, down;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+struct StackPrefillWeights {        // Q8_0 projections in the prefill-GEMM layout
+    PrefillMatrix q, k, v, o, gu, down;
+};
+struct StackWork {                  // activations of one chunk of rows (cap rows)
+    uint32_t cap = 0;
+    vx_buf *h = nullptr;            // residual stream [cap][nH] f32: the input rows, then the output
+    vx_buf *xh = nullptr, *xl = nullptr, *ah = nullptr, *al = nullptr, *qh = nullptr, *ql = nullptr;
+    vx_buf *q = nullptr, *k = nullptr, *v = nullptr, *ws = nullptr;
+};
+constexpr uint32_t kPrefillChunk = 512;     // rows per chunk
+constexpr uint32_t kPrefillMaxSplit = 8;    // split-K factor bound
+struct PrefillStack {
+    vx_ctx *ctx = nullptr;
+    uint32_t nH = 0, nF = 0, nKV = 0, q_heads = 0, kv_heads = 0, head_dim = 0, context = 0, n_layers = 0;
+    float eps = 0.f, residual_scale = 1.f;
+    const StackLayer *layers = nullptr;
+    const StackPrefillWeights *pw = nullptr;   // nullable: per-layer prefill-layout Q8_0 weights
+    bool rope = true;
+    const float *rope_factors = nullptr;
+    float theta = 10000.f, rope_scaling = 1.f;
+    __half *kc = nullptr, *vc = nullptr;       // f16 caches [layer][context][nKV]
+    const StackWork *work = nullptr;
+};
+int prefill_stack_check(const PrefillStack &p);
+int prefill_stack_alloc(vx_ctx *ctx, uint32_t cap, uint32_t nH, uint32_t nF, uint32_t nKV, StackWork *w);
+void prefill_stack_free(vx_ctx *ctx, StackWork *w);
+// The layers over rows 0..T-1 of work->h at positions pos0..pos0+T-1 (K/V rows
+// stored at those positions); work->h then holds every row's residual stream.
+int enqueue_prefill_stack(const PrefillStack &p, uint32_t pos0, uint32_t T);
+
+// Engine hooks of the cross-engine text prefill (baselm.cpp). baselm_prefill_rows
+// runs the batched prefill of n tokens at the engine position and, when rows is
+// set, stores every token's rmsnorm(h)*output_norm there ([n][hidden] f32).
+vx_ctx *baselm_context(const vx_baselm *e);
+uint32_t baselm_hidden_size(const vx_baselm *e);
+int baselm_prefill_rows(vx_baselm *e, const uint32_t *tokens, uint32_t n, float *rows);
 
 struct PrefillAttnArgs {
     const __half *qh = nullptr, *ql = nullptr;  // roped q planes [T][ldq]

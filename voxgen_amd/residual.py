@@ -203,3 +203,15 @@ class ResidualFsqEngine:
         r = abi.StopPrediction()
         abi.call("vx_residual_predict_stop_from_current_lm", self.handle, C.byref(r))
         return self._stop(r)
+
+    def prefill_text_from_gpu_rows(self, rows: Buffer, n: int) -> None:
+        """n text-prefix positions from n BaseLM output rows at once (enqueue only)."""
+        abi.call("vx_residual_prefill_text_from_gpu_rows", self.handle, rows.handle, n)
+
+
+def prefill_text_cross_engine(base, residual: ResidualFsqEngine, tokens) -> None:
+    """The text runs of prefill_conditioning_plan (runtime.rs:483-566): BaseLM then
+    ResidualLM text prefix for every token, batched per engine (enqueue only)."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    abi.call("vx_prefill_text_cross_engine", base.handle, residual.handle,
+             t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size)
