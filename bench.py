@@ -240,7 +240,7 @@ def residual_step_bytes(pos):
     return fsq + fusion + Lr * layer + Hr * 4
 
 
-def residual_leg(ctx, steps, warmup=8):
+def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384):
     """The ResidualLM step of the VoxCPM2 acoustic model (acoustic.rs:830-1035):
     FSQ of the BaseLM hidden, fusion with the acoustic embedding, 8 F16 layers
     (hidden 2048, FFN 6144, 16/2 x 128, no RoPE), F16 weights N(0, 0.02); inputs
@@ -272,14 +272,59 @@ def residual_leg(ctx, steps, warmup=8):
     eng.step_from_gpu_base_and_embedding_gpu_only(base, emb)
     prof = ctx.prof_snapshot()
     ctx.prof_enable(False)
+    log(f"residual step: {ms * 1e3:.1f} us ({1e3 / ms:.0f} steps/s); {nbytes / 1e6:.1f} MB -> {gbps:.0f} GB/s")
+    text = None
+    if baselm is not None and prefix:
+        text = text_prefill(ctx, baselm, bcfg, model, acfg, prefix)
     eng.close()
     model.free()
-    log(f"residual step: {ms * 1e3:.1f} us ({1e3 / ms:.0f} steps/s); {nbytes / 1e6:.1f} MB -> {gbps:.0f} GB/s")
     per = {k: dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"]) for k, v in prof.items()}
     return {"workload": "residual_lm_f16_fsq_fusion_8L_h2048_ffn6144_16q2kv", "us_per_step": round(ms * 1e3, 2),
             "steps_per_second": round(1e3 / ms, 1), "positions": f"{p0}..{p0 + steps - 1}",
             "bytes_per_step": int(nbytes), "achieved_GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "per_kernel_eager": per}
+            "per_kernel_eager": per, "text_prefill": text}
+
+
+def text_prefill(ctx, base, bcfg, amodel, acfg, T, reps=3, seq_positions=32):
+    """The text-prefix run of a conditioning prefill (runtime.rs:483-566): T text
+    tokens through the 28-layer BaseLM and the 8-layer ResidualLM. Batched: one
+    cross-engine call (enqueue) + sync per rep, fresh positions. Per position:
+    BaseLM decode + ResidualLM text-prefix step per token, timed over
+    seq_positions tokens and reported per token."""
+    from voxgen_amd import synth
+    from voxgen_amd.residual import ResidualFsqEngine, prefill_text_cross_engine
+    res = ResidualFsqEngine(ctx, amodel, acfg, exec_mode="graph", strict_geometry=True)
+    tokens = synth.uniform_u32(T, 0x5EED0019, bcfg["vocab_size"]).astype(np.uint32)
+    times = []
+    for _ in range(reps + 1):
+        base.reset()
+        res.reset()
+        ctx.sync()
+        t0 = time.perf_counter()
+        prefill_text_cross_engine(base, res, tokens)
+        ctx.sync()
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times[1:])) * 1e3
+    base.reset()
+    res.reset()
+    norm = base.buffer("norm")
+    for t in tokens[:4]:                                   # captures both graphs
+        base.decode_token_gpu_only(int(t))
+        res.step_text_prefix_from_gpu_base_gpu_only(norm)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for t in tokens[4:4 + seq_positions]:
+        base.decode_token_gpu_only(int(t))
+        res.step_text_prefix_from_gpu_base_gpu_only(norm)
+    ctx.sync()
+    per_pos_ms = (time.perf_counter() - t0) * 1e3 / seq_positions
+    res.close()
+    base.reset()
+    log(f"text prefill of {T} tokens (BaseLM + ResidualLM): batched {ms:.2f} ms; per position "
+        f"{per_pos_ms:.3f} ms/token -> {per_pos_ms * T:.1f} ms")
+    return {"tokens": T, "batched_ms": round(ms, 3), "batched_tok_s": round(T / ms * 1e3, 1),
+            "per_position_ms_per_token": round(per_pos_ms, 4), "per_position_ms_est": round(per_pos_ms * T, 2),
+            "speedup": round(per_pos_ms * T / ms, 1)}
 
 
 def synth_tokens(n, cfg):
@@ -315,7 +360,7 @@ def main():
     log(f"device {info['name']} {info['arch']} CUs={info['compute_units']}; model on device "
         f"{model.device_bytes / 1e9:.2f} GB")
     if args.residual_only:
-        rs = residual_leg(ctx, args.residual_steps)
+        rs = residual_leg(ctx, args.residual_steps, baselm=eng, bcfg=cfg)
         eng.close()
         model.free()
         ctx.close()
@@ -390,10 +435,10 @@ def main():
     prefill = None
     if args.prefill_tokens:
         prefill = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
+    residual = residual_leg(ctx, args.residual_steps, baselm=eng, bcfg=cfg) if args.residual_steps else None
     eng.close()
     model.free()
     cfm = cfm_leg(ctx, args.cfm_reps) if args.cfm_reps else None
-    residual = residual_leg(ctx, args.residual_steps) if args.residual_steps else None
     ctx.close()
 
     line = {
