@@ -71,6 +71,7 @@ typedef struct vx_baselm vx_baselm;
 typedef struct vx_gguf vx_gguf;
 typedef struct vx_locdit vx_locdit;
 typedef struct vx_residual vx_residual;
+typedef struct vx_audiovae vx_audiovae;
 
 /* ------------------------------------------------------------------------- */
 /* Push structs: identical layout to the reference's #[repr(C)] structs.      */
@@ -828,6 +829,76 @@ int vx_residual_prefill_text_from_gpu_rows(vx_residual *eng, const vx_buf *rows,
  * batched ResidualLM text prefix, in chunks of up to 512 positions. Both engines
  * advance by n and end in the state of the last position. Enqueue only. */
 int vx_prefill_text_cross_engine(vx_baselm *base, vx_residual *eng, const uint32_t *tokens, uint32_t n);
+
+/* ------------------------------------------------------------------------- */
+/* AudioVAE decoder (AudioVaeEngine::decode_latents, audiovae.rs:330-372).     */
+/* ------------------------------------------------------------------------- */
+typedef struct vx_vae_conv_push {   /* ConvPush audiovae.rs:198-202 */
+    uint32_t weight_offset, bias_offset, in_channels, out_channels, in_length, out_length;
+    uint32_t kernel, stride, dilation, groups, left_pad, weight_dtype, bias_dtype, has_bias;
+} vx_vae_conv_push;
+typedef struct vx_vae_convt_push {  /* ConvTPush audiovae.rs:203-204 */
+    uint32_t weight_offset, bias_offset, in_channels, out_channels, in_length, out_length;
+    uint32_t kernel, stride, groups, weight_dtype, bias_dtype, has_bias;
+} vx_vae_convt_push;
+typedef struct vx_vae_snake_push {  /* SnakePush audiovae.rs:205-206 */
+    uint32_t alpha_offset, channels, length, dtype;
+} vx_vae_snake_push;
+typedef struct vx_vae_scale_push {  /* ScalePush audiovae.rs:207-208 */
+    uint32_t scale_offset, bias_offset, channels, length, bucket, buckets, scale_dtype, bias_dtype;
+} vx_vae_scale_push;
+typedef struct vx_vae_grid_push {   /* GridPush audiovae.rs:210 */
+    uint32_t channels, length;
+} vx_vae_grid_push;
+/* The shaders over channel-major [C][L] f32 buffers, model scalars from the model
+ * region: vae_conv1d.comp, vae_convtranspose1d.comp, vae_snake.comp (x -> y),
+ * vae_scale_bias.comp (in place), vae_add.comp (a += b), vae_tanh.comp. */
+int vx_vae_conv1d(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_vae_conv_push *pc);
+int vx_vae_convtranspose1d(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y,
+                           const vx_vae_convt_push *pc);
+int vx_vae_snake(vx_ctx *ctx, const vx_model *model, const vx_buf *x, vx_buf *y, const vx_vae_snake_push *pc);
+int vx_vae_scale_bias(vx_ctx *ctx, const vx_model *model, vx_buf *x, const vx_vae_scale_push *pc);
+int vx_vae_add(vx_ctx *ctx, vx_buf *a, const vx_buf *b, const vx_vae_grid_push *pc);
+int vx_vae_tanh(vx_ctx *ctx, vx_buf *x, uint32_t n);
+
+typedef struct vx_audiovae_config { /* AudioVaeConfig audiovae.rs:29-47 (numeric part) */
+    uint32_t encoder_dim, latent_dim, decoder_dim, sample_rate, out_sample_rate;
+    uint32_t encoder_rates[4];
+    uint32_t decoder_rates[6];
+    uint32_t encoder_hop, decoder_hop, patch_size;
+    uint32_t input_samples_per_patch, output_samples_per_patch;
+    uint32_t sr_bin_boundaries[3];
+    uint32_t decoder_sr_bucket;
+    uint32_t depthwise;
+} vx_audiovae_config;
+/* AudioVaeConfig::from_gguf (audiovae.rs:49-79) with validate_tensors
+ * (audiovae.rs:81-128): the V2 geometry, cond_type scale_bias, every encoder and
+ * decoder tensor. */
+int vx_audiovae_config_from_gguf(const vx_gguf *g, vx_audiovae_config *out);
+
+typedef struct vx_audio_decode_stats {   /* AudioDecodeStats audiovae.rs:179-191 */
+    uint32_t latent_frames, latent_patches, output_samples, output_sample_rate;
+    double duration_seconds, checksum, l2;
+    float peak;
+    double decode_ms;
+    uint64_t scratch_bytes;
+} vx_audio_decode_stats;
+
+/* AudioVaeEngine::new (audiovae.rs:256-260): resolves the decoder tensors and
+ * repacks the transposed-convolution weights for the GEMM form. strict_geometry
+ * 0 admits other decoder widths (harnesses). */
+int vx_audiovae_create(vx_ctx *ctx, const vx_model *model, const vx_audiovae_config *cfg, uint32_t strict_geometry,
+                       vx_audiovae **out);
+int vx_audiovae_destroy(vx_audiovae *vae);
+uint64_t vx_audiovae_scratch_bytes(const vx_audiovae *vae);   /* audiovae.rs:261 */
+/* decode_latents (audiovae.rs:330-372): frame-major latents [frames][latent_dim]
+ * (frames a multiple of patch_size) -> mono wave of frames * decoder_hop samples
+ * at out_sample_rate into wave (wave_cap floats). */
+int vx_audiovae_decode_latents(vx_audiovae *vae, const float *frame_major, uint64_t n_values, float *wave,
+                               uint64_t wave_cap, vx_audio_decode_stats *out);
+/* The same decode from and to device buffers, enqueue only (no checks of the
+ * values; frames a multiple of patch_size). */
+int vx_audiovae_decode_latents_gpu(vx_audiovae *vae, const vx_buf *frame_major, uint32_t frames, vx_buf *wave);
 
 #ifdef __cplusplus
 }

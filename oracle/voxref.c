@@ -43,6 +43,11 @@
  *                                  round-half-away(tanh(x)*s)/s; outputs on the
  *                                  grid k/s with |k| <= s; odd symmetry.
  *   vr_silu_inplace                 f64 x/(1+e^-x); silu(0) = 0.
+ *   vr_vae_conv1d                   f64 numpy gather over shifted slices
+ *                                  (groups, stride, dilation, causal pad).
+ *   vr_vae_convt1d                  f64 numpy scatter form out[ti s + k] +=
+ *                                  x[ti] w[k] (PyTorch ConvTranspose1d), cropped.
+ *   vr_vae_snake / scale_bias / add / tanh  f64 closed forms.
  *   vr_residual_lm_record           f64 numpy re-derivation of one layer
  *                                  without RoPE; equals vr_baselm_record at
  *                                  position 0, where RoPE is the identity.
@@ -561,6 +566,92 @@ void vr_baselm_decode_token(const uint8_t *blob, const vr_baselm *m, vr_state *s
                             vr_effective_scale(m->cfg.embedding_scale)};
     vr_embedding(blob, s->hidden, &ep); /* baselm.rs:634-647 */
     vr_baselm_record(blob, m, s, position, compute_logits);
+}
+
+/* --------------------------------------------------------------- AudioVAE */
+/* The vae_*.comp shaders over channel-major [C][L] buffers. */
+static inline float vae_scalar(const uint8_t *blob, uint32_t base, uint32_t i, uint32_t dtype) {
+    return dtype == 1u ? load_f16(blob, base + i * 2u) : load_f32(blob, base + i * 4u);
+}
+
+void vr_vae_conv1d(const uint8_t *blob, const float *x, float *y, const vx_vae_conv_push *pc) {
+    ensure_lut();
+    const uint32_t out_pg = pc->out_channels / pc->groups, in_pg = pc->in_channels / pc->groups;
+#pragma omp parallel for schedule(static)
+    for (uint32_t oc = 0; oc < pc->out_channels; ++oc) { /* vae_conv1d.comp:33-57 */
+        const uint32_t in_base = (oc / out_pg) * in_pg;
+        for (uint32_t t = 0; t < pc->out_length; ++t) {
+            float sum = pc->has_bias ? vae_scalar(blob, pc->bias_offset, oc, pc->bias_dtype) : 0.0f;
+            for (uint32_t icg = 0; icg < in_pg; ++icg) {
+                const uint32_t ic = in_base + icg;
+                for (uint32_t k = 0; k < pc->kernel; ++k) {
+                    const int64_t ti = (int64_t)t * pc->stride + (int64_t)k * pc->dilation - (int64_t)pc->left_pad;
+                    if (ti < 0 || ti >= (int64_t)pc->in_length) continue;
+                    const float w = vae_scalar(blob, pc->weight_offset, (oc * in_pg + icg) * pc->kernel + k,
+                                               pc->weight_dtype);
+                    sum += x[(size_t)ic * pc->in_length + (size_t)ti] * w;
+                }
+            }
+            y[(size_t)oc * pc->out_length + t] = sum;
+        }
+    }
+}
+
+void vr_vae_convt1d(const uint8_t *blob, const float *x, float *y, const vx_vae_convt_push *pc) {
+    ensure_lut();
+    const uint32_t out_pg = pc->out_channels / pc->groups, in_pg = pc->in_channels / pc->groups;
+#pragma omp parallel for schedule(static)
+    for (uint32_t oc = 0; oc < pc->out_channels; ++oc) { /* vae_convtranspose1d.comp:23-48 */
+        const uint32_t group = oc / out_pg, ocg = oc - group * out_pg, in_base = group * in_pg;
+        for (uint32_t t = 0; t < pc->out_length; ++t) {
+            float sum = pc->has_bias ? vae_scalar(blob, pc->bias_offset, oc, pc->bias_dtype) : 0.0f;
+            for (uint32_t icg = 0; icg < in_pg; ++icg) {
+                const uint32_t ic = in_base + icg;
+                for (uint32_t k = t % pc->stride; k < pc->kernel; k += pc->stride) {
+                    if (t < k) continue;
+                    const uint32_t ti = (t - k) / pc->stride;
+                    if (ti >= pc->in_length) continue;
+                    sum += x[(size_t)ic * pc->in_length + ti] *
+                           vae_scalar(blob, pc->weight_offset, (ic * out_pg + ocg) * pc->kernel + k, pc->weight_dtype);
+                }
+            }
+            y[(size_t)oc * pc->out_length + t] = sum;
+        }
+    }
+}
+
+void vr_vae_snake(const uint8_t *blob, const float *x, float *y, const vx_vae_snake_push *pc) {
+    ensure_lut();
+    for (uint32_t c = 0; c < pc->channels; ++c) { /* vae_snake.comp:9-17 */
+        const float a = vae_scalar(blob, pc->alpha_offset, c, pc->dtype);
+        for (uint32_t t = 0; t < pc->length; ++t) {
+            const size_t i = (size_t)c * pc->length + t;
+            const float s = sinf(a * x[i]);
+            y[i] = x[i] + (s * s) / (a + 1e-9f);
+        }
+    }
+}
+
+void vr_vae_scale_bias(const uint8_t *blob, float *x, const vx_vae_scale_push *pc) {
+    ensure_lut();
+    for (uint32_t c = 0; c < pc->channels; ++c) { /* vae_scale_bias.comp:9-17 */
+        const uint32_t idx = pc->bucket * pc->channels + c;
+        const float sc = vae_scalar(blob, pc->scale_offset, idx, pc->scale_dtype);
+        const float bi = vae_scalar(blob, pc->bias_offset, idx, pc->bias_dtype);
+        for (uint32_t t = 0; t < pc->length; ++t) {
+            const size_t i = (size_t)c * pc->length + t;
+            x[i] = x[i] * sc + bi;
+        }
+    }
+}
+
+void vr_vae_add(float *a, const float *b, const vx_vae_grid_push *pc) {
+    const size_t n = (size_t)pc->channels * pc->length;
+    for (size_t i = 0; i < n; ++i) a[i] += b[i];
+}
+
+void vr_vae_tanh(float *x, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) x[i] = tanhf(x[i]);
 }
 
 /* ------------------------------------------------------------- CFM pieces */

@@ -87,6 +87,13 @@ void vr_residual_lm_record(const uint8_t *blob, const vr_baselm *m, vr_state *s,
 void vr_fsq_quantize(float *x, uint32_t n, float scale);
 /* silu_inplace.comp (in place). */
 void vr_silu_inplace(float *x, uint32_t n);
+/* vae_*.comp over channel-major [C][L] f32 buffers. */
+void vr_vae_conv1d(const uint8_t *blob, const float *x, float *y, const vx_vae_conv_push *pc);
+void vr_vae_convt1d(const uint8_t *blob, const float *x, float *y, const vx_vae_convt_push *pc);
+void vr_vae_snake(const uint8_t *blob, const float *x, float *y, const vx_vae_snake_push *pc);
+void vr_vae_scale_bias(const uint8_t *blob, float *x, const vx_vae_scale_push *pc);
+void vr_vae_add(float *a, const float *b, const vx_vae_grid_push *pc);
+void vr_vae_tanh(float *x, uint32_t n);
 /* Embedding dispatch (baselm.rs:634-647) then record_transformer. */
 void vr_baselm_decode_token(const uint8_t *blob, const vr_baselm *m, vr_state *s,
                             uint32_t token_id, uint32_t position, int compute_logits);

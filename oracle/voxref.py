@@ -70,6 +70,12 @@ def lib() -> C.CDLL:
         L.vr_residual_lm_record.argtypes = [vp, vp, vp, u32]
         L.vr_fsq_quantize.argtypes = [vp, u32, f32]
         L.vr_silu_inplace.argtypes = [vp, u32]
+        L.vr_vae_conv1d.argtypes = [vp, vp, vp, P(abi.VaeConvPush)]
+        L.vr_vae_convt1d.argtypes = [vp, vp, vp, P(abi.VaeConvTPush)]
+        L.vr_vae_snake.argtypes = [vp, vp, vp, P(abi.VaeSnakePush)]
+        L.vr_vae_scale_bias.argtypes = [vp, vp, P(abi.VaeScalePush)]
+        L.vr_vae_add.argtypes = [vp, vp, P(abi.VaeGridPush)]
+        L.vr_vae_tanh.argtypes = [vp, u32]
         L.vr_set_threads.argtypes = [C.c_int]
         L.vr_get_threads.restype = C.c_int
         _lib = L
@@ -392,6 +398,97 @@ class ResidualFsq:
         h = silu_inplace(self._lin("stop_predictor.linear1", x, H, H))
         w = self.t["stop_predictor.linear2.weight"]
         return matvec(self.blob, h, abi.MatvecPush(w.offset, 2, H, w.ggml_type, 0, 1.0))
+
+
+def _dt(t) -> int:
+    return 1 if t.ggml_type == abi.DTYPE_F16 else 0
+
+
+def vae_conv1d(blob, x, push: abi.VaeConvPush) -> np.ndarray:
+    xc = np.ascontiguousarray(x, np.float32)
+    y = f32(push.out_channels * push.out_length)
+    lib().vr_vae_conv1d(_p(blob), _p(xc), _p(y), C.byref(push))
+    return y
+
+
+def vae_convt1d(blob, x, push: abi.VaeConvTPush) -> np.ndarray:
+    xc = np.ascontiguousarray(x, np.float32)
+    y = f32(push.out_channels * push.out_length)
+    lib().vr_vae_convt1d(_p(blob), _p(xc), _p(y), C.byref(push))
+    return y
+
+
+def vae_snake(blob, x, push: abi.VaeSnakePush) -> np.ndarray:
+    xc = np.ascontiguousarray(x, np.float32)
+    y = f32(xc.size)
+    lib().vr_vae_snake(_p(blob), _p(xc), _p(y), C.byref(push))
+    return y
+
+
+def vae_scale_bias(blob, x, push: abi.VaeScalePush) -> np.ndarray:
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().vr_vae_scale_bias(_p(blob), _p(y), C.byref(push))
+    return y
+
+
+def vae_tanh(x) -> np.ndarray:
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().vr_vae_tanh(_p(y), y.size)
+    return y
+
+
+class AudioVae:
+    """AudioVaeEngine::decode_latents (audiovae.rs:330-372) on the CPU: the
+    record_* sequence over channel-major buffers, with the reference's
+    snapshot/residual order (record_residual, audiovae.rs:400-407)."""
+
+    def __init__(self, data: np.ndarray, tensors: dict, cfg: dict):
+        self.blob = np.ascontiguousarray(data, dtype=np.uint8)
+        if self.blob.size % 4:
+            self.blob = np.concatenate([self.blob, np.zeros(4 - self.blob.size % 4, np.uint8)])
+        self.t, self.cfg = tensors, dict(cfg)
+
+    def _conv(self, x, base, in_c, out_c, in_len, out_len, k, stride, dil, groups, pad):
+        w, b = self.t[base], self.t[base + ".bias"]
+        return vae_conv1d(self.blob, x, abi.VaeConvPush(w.offset, b.offset, in_c, out_c, in_len, out_len, k, stride,
+                                                         dil, groups, pad, _dt(w), _dt(b), 1))
+
+    def _snake(self, x, name, c, n):
+        a = self.t[name]
+        return vae_snake(self.blob, x, abi.VaeSnakePush(a.offset, c, n, _dt(a)))
+
+    def decode(self, frame_major) -> np.ndarray:
+        cfg = self.cfg
+        ld = cfg["latent_dim"]
+        fm = np.asarray(frame_major, np.float32).reshape(-1, ld)
+        frames = fm.shape[0]
+        x = np.ascontiguousarray(fm.T).ravel()             # frame_to_channel_major
+        n, c = frames, ld
+        x = self._conv(x, "audio_vae.decoder.model.0", c, c, n, n, 7, 1, 1, c, 6)
+        x = self._conv(x, "audio_vae.decoder.model.1", c, cfg["decoder_dim"], n, n, 1, 1, 1, 1, 0)
+        c = cfg["decoder_dim"]
+        for i, s in enumerate(cfg["decoder_rates"]):
+            mi, co = i + 2, c // 2
+            sw = self.t[f"audio_vae.decoder.sr_cond_model.{mi}.scale_embed"]
+            bw = self.t[f"audio_vae.decoder.sr_cond_model.{mi}.bias_embed"]
+            x = vae_scale_bias(self.blob, x, abi.VaeScalePush(sw.offset, bw.offset, c, n, cfg["decoder_sr_bucket"],
+                                                               4, _dt(sw), _dt(bw)))
+            y = self._snake(x, f"audio_vae.decoder.model.{mi}.block.0.alpha", c, n)
+            w, b = self.t[f"audio_vae.decoder.model.{mi}.block.1"], self.t[f"audio_vae.decoder.model.{mi}.block.1.bias"]
+            x = vae_convt1d(self.blob, y, abi.VaeConvTPush(w.offset, b.offset, c, co, n, n * s, 2 * s, s, 1, _dt(w),
+                                                            _dt(b), 1))
+            c, n = co, n * s
+            for rj, dil in enumerate((1, 3, 9)):
+                p = f"audio_vae.decoder.model.{mi}.block.{rj + 2}.block"
+                snap = x.copy()
+                y = self._snake(x, p + ".0.alpha", c, n)
+                x = self._conv(y, p + ".1", c, c, n, n, 7, 1, dil, c, 6 * dil)
+                y = self._snake(x, p + ".2.alpha", c, n)
+                x = self._conv(y, p + ".3", c, c, n, n, 1, 1, 1, 1, 0)
+                lib().vr_vae_add(_p(x), _p(snap), C.byref(abi.VaeGridPush(c, n)))
+        y = self._snake(x, "audio_vae.decoder.model.8.alpha", c, n)
+        x = self._conv(y, "audio_vae.decoder.model.9", c, 1, n, n, 7, 1, 1, 1, 6)
+        return vae_tanh(x)
 
 
 def stats(v) -> tuple:

@@ -257,3 +257,72 @@ def test_acoustic_config_errors(tmp_path, case, code):
     with pytest.raises(abi.VxError) as e:
         Gguf(acoustic_file(tmp_path, **kw)).acoustic_config(base, active)
     assert e.value.name == code
+
+
+# --------------------------------------------- AudioVaeConfig::from_gguf
+def vae_file(tmp_path, mutate=None, drop=None, meta_over=None):
+    cfg = synth.audiovae_config()
+    m = synth.build_audiovae(cfg, encoder=True, with_data=False)
+    tensors = [t for t in m.tensors if t.name != drop]
+    if mutate:
+        tensors = [mutate(t) for t in tensors]
+    meta = dict(m.metadata)
+    meta.update(meta_over or {})
+    size = max(t.offset + t.nbytes for t in tensors)
+    return gguf.write(tmp_path / "v.gguf", meta, tensors, None, data_bytes=size)
+
+
+def test_audiovae_config_from_gguf(tmp_path):
+    c = Gguf(vae_file(tmp_path)).audiovae_config()
+    want = synth.audiovae_config()
+    for k, v in want.items():
+        assert c[k] == v, k
+    assert c["decoder_hop"] == 1920 and c["encoder_hop"] == 640 and c["decoder_sr_bucket"] == 3
+
+
+@pytest.mark.parametrize("case,code", [
+    ("version", "VX_ERR_UNSUPPORTED"), ("dec", "VX_ERR_UNSUPPORTED"), ("cond", "VX_ERR_UNSUPPORTED"),
+    ("missing_enc", "VX_ERR_NOT_FOUND"), ("missing_dec", "VX_ERR_NOT_FOUND"), ("f32_alpha", "VX_ERR_SHAPE"),
+    ("convt_dims", "VX_ERR_SHAPE"), ("embed_dims", "VX_ERR_SHAPE"), ("no_meta", "VX_ERR_NOT_FOUND"),
+])
+def test_audiovae_config_errors(tmp_path, case, code):
+    kw = {}
+    if case == "version":
+        kw["meta_over"] = {"voxcpm.model_version": (6, 1.0)}
+    elif case == "dec":
+        kw["meta_over"] = {"voxcpm.audiovae.decoder_dim": (4, 1024)}
+    elif case == "cond":
+        kw["meta_over"] = {"voxcpm.audiovae.cond_type": (8, "film")}
+    elif case == "missing_enc":
+        kw["drop"] = "audio_vae.encoder.fc_logvar"
+    elif case == "missing_dec":
+        kw["drop"] = "audio_vae.decoder.model.5.block.3.block.2.alpha"
+    elif case == "f32_alpha":
+        kw["mutate"] = _retype("audio_vae.decoder.model.8.alpha", abi.DTYPE_F32)
+    elif case == "convt_dims":
+        def mutate(t):
+            if t.name == "audio_vae.decoder.model.3.block.1":
+                t = synth.TensorDesc(t.name, t.ggml_type, (12, 1024, 512), t.offset)
+            return t
+        kw["mutate"] = mutate
+    elif case == "embed_dims":
+        def mutate(t):
+            if t.name == "audio_vae.decoder.sr_cond_model.4.bias_embed":
+                t = synth.TensorDesc(t.name, t.ggml_type, (512, 3), t.offset)
+            return t
+        kw["mutate"] = mutate
+    elif case == "no_meta":
+        kw["meta_over"] = {}
+        cfg = synth.audiovae_config()
+        m = synth.build_audiovae(cfg, encoder=True, with_data=False)
+        meta = dict(m.metadata)
+        del meta["voxcpm.audiovae.out_sample_rate"]
+        size = max(t.offset + t.nbytes for t in m.tensors)
+        path = gguf.write(tmp_path / "w.gguf", meta, m.tensors, None, data_bytes=size)
+        with pytest.raises(abi.VxError) as e:
+            Gguf(path).audiovae_config()
+        assert e.value.name == code
+        return
+    with pytest.raises(abi.VxError) as e:
+        Gguf(vae_file(tmp_path, **kw)).audiovae_config()
+    assert e.value.name == code

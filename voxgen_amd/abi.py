@@ -158,6 +158,26 @@ ResidualBenchmark = _struct("ResidualBenchmark", [("iterations", u32), ("mean_ms
                                                   ("max_ms", f64), ("steps_per_second", f64)])
 StopPrediction = _struct("StopPrediction", [("stop", u32), ("continue_logit", f32), ("stop_logit", f32),
                                             ("elapsed_ms", f64)])
+VaeConvPush = _struct("VaeConvPush", [(n, u32) for n in (
+    "weight_offset", "bias_offset", "in_channels", "out_channels", "in_length", "out_length", "kernel", "stride",
+    "dilation", "groups", "left_pad", "weight_dtype", "bias_dtype", "has_bias")])
+VaeConvTPush = _struct("VaeConvTPush", [(n, u32) for n in (
+    "weight_offset", "bias_offset", "in_channels", "out_channels", "in_length", "out_length", "kernel", "stride",
+    "groups", "weight_dtype", "bias_dtype", "has_bias")])
+VaeSnakePush = _struct("VaeSnakePush", [(n, u32) for n in ("alpha_offset", "channels", "length", "dtype")])
+VaeScalePush = _struct("VaeScalePush", [(n, u32) for n in (
+    "scale_offset", "bias_offset", "channels", "length", "bucket", "buckets", "scale_dtype", "bias_dtype")])
+VaeGridPush = _struct("VaeGridPush", [("channels", u32), ("length", u32)])
+AudioVaeConfig = _struct("AudioVaeConfig", [
+    ("encoder_dim", u32), ("latent_dim", u32), ("decoder_dim", u32), ("sample_rate", u32),
+    ("out_sample_rate", u32), ("encoder_rates", u32 * 4), ("decoder_rates", u32 * 6), ("encoder_hop", u32),
+    ("decoder_hop", u32), ("patch_size", u32), ("input_samples_per_patch", u32),
+    ("output_samples_per_patch", u32), ("sr_bin_boundaries", u32 * 3), ("decoder_sr_bucket", u32),
+    ("depthwise", u32)])
+AudioDecodeStats = _struct("AudioDecodeStats", [
+    ("latent_frames", u32), ("latent_patches", u32), ("output_samples", u32), ("output_sample_rate", u32),
+    ("duration_seconds", f64), ("checksum", f64), ("l2", f64), ("peak", f32), ("decode_ms", f64),
+    ("scratch_bytes", u64)])
 RESIDUAL_BUF = dict(OUTPUT=0, CURRENT_LM=1, FSQ_LATENT=2, FSQ_OUTPUT=3, FUSION_SNAPSHOT=4, HIDDEN=5,
                     KV_K=6, KV_V=7, STOP_LOGITS=8)
 
@@ -170,6 +190,7 @@ ENGINE = vp
 GGUF = vp
 LOCDIT = vp
 RESIDUAL = vp
+AUDIOVAE = vp
 
 # name -> (restype, argtypes)
 PROTOTYPES = {
@@ -300,6 +321,18 @@ PROTOTYPES = {
     "vx_residual_predict_stop_from_current_lm": (i32, [RESIDUAL, P(StopPrediction)]),
     "vx_residual_prefill_text_from_gpu_rows": (i32, [RESIDUAL, BUFP, u32]),
     "vx_prefill_text_cross_engine": (i32, [ENGINE, RESIDUAL, P(u32), u32]),
+    "vx_vae_conv1d": (i32, [CTX, MODEL, BUFP, BUFP, P(VaeConvPush)]),
+    "vx_vae_convtranspose1d": (i32, [CTX, MODEL, BUFP, BUFP, P(VaeConvTPush)]),
+    "vx_vae_snake": (i32, [CTX, MODEL, BUFP, BUFP, P(VaeSnakePush)]),
+    "vx_vae_scale_bias": (i32, [CTX, MODEL, BUFP, P(VaeScalePush)]),
+    "vx_vae_add": (i32, [CTX, BUFP, BUFP, P(VaeGridPush)]),
+    "vx_vae_tanh": (i32, [CTX, BUFP, u32]),
+    "vx_audiovae_config_from_gguf": (i32, [GGUF, P(AudioVaeConfig)]),
+    "vx_audiovae_create": (i32, [CTX, MODEL, P(AudioVaeConfig), u32, P(AUDIOVAE)]),
+    "vx_audiovae_destroy": (i32, [AUDIOVAE]),
+    "vx_audiovae_scratch_bytes": (u64, [AUDIOVAE]),
+    "vx_audiovae_decode_latents": (i32, [AUDIOVAE, P(f32), u64, P(f32), u64, P(AudioDecodeStats)]),
+    "vx_audiovae_decode_latents_gpu": (i32, [AUDIOVAE, BUFP, u32, BUFP]),
 }
 
 STRUCT_SIZES = {  # C name -> ctypes struct
@@ -324,7 +357,9 @@ STRUCT_SIZES = {  # C name -> ctypes struct
     "vx_acoustic_config": AcousticConfig, "vx_residual_options": ResidualOptions,
     "vx_fsq_result": FsqResult, "vx_residual_step_result": ResidualStepResult,
     "vx_residual_gpu_step": ResidualGpuStep, "vx_residual_benchmark_result": ResidualBenchmark,
-    "vx_stop_prediction": StopPrediction,
+    "vx_stop_prediction": StopPrediction, "vx_vae_conv_push": VaeConvPush, "vx_vae_convt_push": VaeConvTPush,
+    "vx_vae_snake_push": VaeSnakePush, "vx_vae_scale_push": VaeScalePush, "vx_vae_grid_push": VaeGridPush,
+    "vx_audiovae_config": AudioVaeConfig, "vx_audio_decode_stats": AudioDecodeStats,
 }
 
 

@@ -605,4 +605,111 @@ int vx_acoustic_config_from_gguf(const vx_gguf *g, const vx_baselm_config *base,
     return VX_OK;
 }
 
+// AudioVaeConfig::from_gguf (audiovae.rs:49-79) and validate_tensors
+// (audiovae.rs:81-128).
+int vx_audiovae_config_from_gguf(const vx_gguf *g, vx_audiovae_config *out) {
+    if (!g || !out) return fail(VX_ERR_INVALID_ARG, "vx_audiovae_config_from_gguf: null argument");
+    vx_audiovae_config c{};
+    float version = 0.f;
+    if (!meta_f32(g, {"voxcpm.model_version"}, &version))
+        return fail(VX_ERR_NOT_FOUND, "missing required metadata: voxcpm.model_version");
+    if (std::fabs(version - 2.0f) > 0.01f)
+        return fail(VX_ERR_UNSUPPORTED, "AudioVAE V2 requires VoxCPM2 acoustic model_version=2.0, got %g", version);
+    std::string cond;
+    if (!meta_u32(g, {"voxcpm.audiovae.encoder_dim"}, &c.encoder_dim) ||
+        !meta_u32(g, {"voxcpm.audiovae.latent_dim"}, &c.latent_dim) ||
+        !meta_u32(g, {"voxcpm.audiovae.decoder_dim"}, &c.decoder_dim) ||
+        !meta_u32(g, {"voxcpm.audiovae.sample_rate"}, &c.sample_rate) ||
+        !meta_u32(g, {"voxcpm.audiovae.out_sample_rate"}, &c.out_sample_rate) ||
+        !meta_string(g, "voxcpm.audiovae.cond_type", &cond) || !meta_u32(g, {"voxcpm.patch_size"}, &c.patch_size))
+        return fail(VX_ERR_NOT_FOUND, "missing required voxcpm.audiovae / voxcpm.patch_size metadata");
+    if (c.encoder_dim != 128 || c.latent_dim != 64 || c.decoder_dim != 2048 || c.sample_rate != 16000 ||
+        c.out_sample_rate != 48000 || c.patch_size != 4)
+        return fail(VX_ERR_UNSUPPORTED, "unsupported VoxCPM2 AudioVAE geometry: enc=%u, latent=%u, dec=%u, sr=%u, "
+                    "out_sr=%u, patch=%u", c.encoder_dim, c.latent_dim, c.decoder_dim, c.sample_rate,
+                    c.out_sample_rate, c.patch_size);
+    if (cond != "scale_bias")
+        return fail(VX_ERR_UNSUPPORTED, "AudioVAE cond_type must be scale_bias, got \"%s\"", cond.c_str());
+    static const uint32_t enc[4] = {2, 5, 8, 8}, dec[6] = {8, 6, 5, 2, 2, 2}, bins[3] = {20000, 30000, 40000};
+    c.encoder_hop = c.decoder_hop = 1;
+    for (uint32_t i = 0; i < 4; ++i) c.encoder_hop *= (c.encoder_rates[i] = enc[i]);
+    for (uint32_t i = 0; i < 6; ++i) c.decoder_hop *= (c.decoder_rates[i] = dec[i]);
+    c.input_samples_per_patch = c.encoder_hop * c.patch_size;
+    c.output_samples_per_patch = c.decoder_hop * c.patch_size;
+    for (uint32_t i = 0; i < 3; ++i) {
+        c.sr_bin_boundaries[i] = bins[i];
+        if (c.out_sample_rate > bins[i] && c.decoder_sr_bucket == i) c.decoder_sr_bucket = i + 1;
+    }
+    c.depthwise = 1;
+    const vx_tensor_info *t;
+    auto f16 = [&](const std::string &name) -> int {   // require_f16
+        VX_CHECK(need_tensor(g, name, &t));
+        if (t->ggml_type != 1) return fail(VX_ERR_SHAPE, "AudioVAE tensor %s is type %u, expected F16", t->name,
+                                           t->ggml_type);
+        return VX_OK;
+    };
+    auto elements = [&]() {
+        uint64_t n = 1;
+        for (uint32_t d = 0; d < t->n_dims; ++d) n *= t->dims[d];
+        return n;
+    };
+    auto alpha = [&](const std::string &name, uint64_t ch) -> int {   // require_alpha
+        VX_CHECK(f16(name));
+        if (elements() != ch) return fail(VX_ERR_SHAPE, "AudioVAE alpha %s has %llu values, expected %llu", t->name,
+                                          (unsigned long long)elements(), (unsigned long long)ch);
+        return VX_OK;
+    };
+    auto conv = [&](const std::string &base, uint64_t in_c, uint64_t out_c, uint64_t k, uint64_t groups,
+                    bool transpose) -> int {   // require_conv
+        VX_CHECK(f16(base));
+        VX_CHECK(dims_eq(t, {k, transpose ? out_c / groups : in_c / groups, transpose ? in_c : out_c}));
+        VX_CHECK(f16(base + ".bias"));
+        if (elements() != out_c) return fail(VX_ERR_SHAPE, "AudioVAE bias %s has %llu values, expected %llu", t->name,
+                                             (unsigned long long)elements(), (unsigned long long)out_c);
+        return VX_OK;
+    };
+    VX_CHECK(conv("audio_vae.encoder.block.0", 1, 128, 7, 1, false));
+    uint64_t ch = c.encoder_dim;
+    for (uint32_t stage = 0; stage < 4; ++stage) {
+        const std::string b = "audio_vae.encoder.block." + std::to_string(stage + 1);
+        for (uint32_t ri = 0; ri < 3; ++ri) {
+            const std::string p = b + ".block." + std::to_string(ri) + ".block";
+            VX_CHECK(alpha(p + ".0.alpha", ch));
+            VX_CHECK(conv(p + ".1", ch, ch, 7, ch, false));
+            VX_CHECK(alpha(p + ".2.alpha", ch));
+            VX_CHECK(conv(p + ".3", ch, ch, 1, 1, false));
+        }
+        VX_CHECK(alpha(b + ".block.3.alpha", ch));
+        VX_CHECK(conv(b + ".block.4", ch, ch * 2, enc[stage] * 2u, 1, false));
+        ch *= 2;
+    }
+    VX_CHECK(conv("audio_vae.encoder.fc_mu", ch, c.latent_dim, 3, 1, false));
+    VX_CHECK(conv("audio_vae.encoder.fc_logvar", ch, c.latent_dim, 3, 1, false));
+    VX_CHECK(conv("audio_vae.decoder.model.0", c.latent_dim, c.latent_dim, 7, c.latent_dim, false));
+    VX_CHECK(conv("audio_vae.decoder.model.1", c.latent_dim, c.decoder_dim, 1, 1, false));
+    uint64_t din = c.decoder_dim;
+    for (uint32_t i = 0; i < 6; ++i) {
+        const std::string mi = std::to_string(i + 2), p = "audio_vae.decoder.model." + mi;
+        const uint64_t dout = din / 2;
+        for (const char *kind : {"scale_embed", "bias_embed"}) {   // require_sr_embed
+            VX_CHECK(f16("audio_vae.decoder.sr_cond_model." + mi + "." + kind));
+            VX_CHECK(dims_eq(t, {din, 4}));
+        }
+        VX_CHECK(alpha(p + ".block.0.alpha", din));
+        VX_CHECK(conv(p + ".block.1", din, dout, dec[i] * 2u, 1, true));
+        for (uint32_t rj = 0; rj < 3; ++rj) {
+            const std::string q = p + ".block." + std::to_string(rj + 2) + ".block";
+            VX_CHECK(alpha(q + ".0.alpha", dout));
+            VX_CHECK(conv(q + ".1", dout, dout, 7, dout, false));
+            VX_CHECK(alpha(q + ".2.alpha", dout));
+            VX_CHECK(conv(q + ".3", dout, dout, 1, 1, false));
+        }
+        din = dout;
+    }
+    VX_CHECK(alpha("audio_vae.decoder.model.8.alpha", din));
+    VX_CHECK(conv("audio_vae.decoder.model.9", din, 1, 7, 1, false));
+    *out = c;
+    return VX_OK;
+}
+
 }  // extern "C"

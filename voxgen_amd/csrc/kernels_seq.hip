@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
             tile_row<EPI>(tn, sg.tile0, 64u * wn + 32u * t + l32, mat, row);
             if (row >= sg.rows) continue;
             float bias = 0.f;
-            if (EPI == GEPI_STORE && sg.bias && ks == 0)
+            if ((EPI == GEPI_STORE || EPI == GEPI_RESIDUAL) && sg.bias && ks == 0)
                 bias = sg.bias_dtype == 0 ? static_cast<const float *>(sg.bias)[row]
                                           : h2f(static_cast<const unsigned short *>(sg.bias)[row]);
             // Take the bias now: used first inside the branchy loop below, its
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
                         *dst = v;
                 } else {  // GEPI_RESIDUAL: hidden += scale * (W . x), an atomic add (no load to wait for;
                           // with one contributor it is exactly h + v)
-                    unsafeAtomicAdd(dst, acc[r] * a.scale);
+                    unsafeAtomicAdd(dst, (sg.bias ? acc[r] + bias : acc[r]) * a.scale);
                 }
             }
         }
@@ -1024,6 +1024,7 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
     VX_GEMM_CASE(WT_F16, false, GEPI_RESIDUAL)
     VX_GEMM_CASE(WT_F16, false, GEPI_SWIGLU)
     VX_GEMM_CASE(WT_F16, true, GEPI_STORE)
+    VX_GEMM_CASE(WT_F16, true, GEPI_RESIDUAL)
     VX_GEMM_CASE(WT_F16, true, GEPI_SWIGLU)
 #undef VX_GEMM_CASE
     return fail(VX_ERR_UNSUPPORTED, "gemm: no kernel for weight type %u, f32 input %d, epilogue %u", a.wk,

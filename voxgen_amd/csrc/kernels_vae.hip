@@ -1,0 +1,271 @@
+// AudioVAE decoder kernels (vae_*.comp).
+//
+// Two families:
+//  * channel-major [C][L] kernels with the reference shaders' semantics, behind
+//    the per-op entry points (vae_conv1d.comp, vae_convtranspose1d.comp,
+//    vae_snake.comp, vae_scale_bias.comp, vae_add.comp, vae_tanh.comp);
+//  * frame-major [L][C] kernels of the decode engine, where the 1x1 convolutions
+//    and the transposed convolutions are GEMMs on MFMA (k_gemm) and the
+//    elementwise work (scale/bias, snake) is fused into the passes around them.
+// Snake: x + sin(a x)^2 / (a + 1e-9) (vae_snake.comp:13-16).
+#include "vx_internal.h"
+
+namespace vx {
+namespace {
+
+__device__ __forceinline__ float hf(__half v) { return __half2float(v); }
+
+// A model scalar of GGML dtype 1 (F16) or 0 (F32).
+__device__ __forceinline__ float ldw(const void *p, uint32_t i, uint32_t dtype) {
+    return dtype == 1u ? hf(static_cast<const __half *>(p)[i]) : static_cast<const float *>(p)[i];
+}
+
+__device__ __forceinline__ float snake(float x, float a) {
+    const float s = sinf(a * x);
+    return x + (s * s) / (a + 1e-9f);
+}
+
+// ------------------------------------------------------------ channel-major
+__global__ __launch_bounds__(256) void k_vae_conv1d_cm(VaeConvArgs a) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x, oc = blockIdx.y;
+    if (t >= a.out_length || oc >= a.out_channels) return;
+    const uint32_t out_pg = a.out_channels / a.groups, in_pg = a.in_channels / a.groups;
+    const uint32_t in_base = (oc / out_pg) * in_pg;
+    float sum = a.bias ? ldw(a.bias, oc, a.bias_dtype) : 0.f;
+    for (uint32_t icg = 0; icg < in_pg; ++icg) {
+        const uint32_t ic = in_base + icg;
+        for (uint32_t k = 0; k < a.kernel; ++k) {
+            const int ti = (int)(t * a.stride + k * a.dilation) - (int)a.left_pad;
+            if (ti < 0 || ti >= (int)a.in_length) continue;
+            const float w = ldw(a.w, (oc * in_pg + icg) * a.kernel + k, a.w_dtype);
+            sum += a.x[(size_t)ic * a.in_length + (uint32_t)ti] * w;
+        }
+    }
+    a.y[(size_t)oc * a.out_length + t] = sum;
+}
+
+__global__ __launch_bounds__(256) void k_vae_convt1d_cm(VaeConvArgs a) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x, oc = blockIdx.y;
+    if (t >= a.out_length || oc >= a.out_channels) return;
+    const uint32_t out_pg = a.out_channels / a.groups, in_pg = a.in_channels / a.groups;
+    const uint32_t group = oc / out_pg, ocg = oc - group * out_pg, in_base = group * in_pg;
+    float sum = a.bias ? ldw(a.bias, oc, a.bias_dtype) : 0.f;
+    const uint32_t first_k = t % a.stride;
+    for (uint32_t icg = 0; icg < in_pg; ++icg) {
+        const uint32_t ic = in_base + icg;
+        for (uint32_t k = first_k; k < a.kernel; k += a.stride) {
+            if (t < k) continue;
+            const uint32_t ti = (t - k) / a.stride;
+            if (ti >= a.in_length) continue;
+            sum += a.x[(size_t)ic * a.in_length + ti] * ldw(a.w, (ic * out_pg + ocg) * a.kernel + k, a.w_dtype);
+        }
+    }
+    a.y[(size_t)oc * a.out_length + t] = sum;
+}
+
+__global__ __launch_bounds__(256) void k_vae_snake_cm(const float *x, float *y, const void *alpha, uint32_t dtype,
+                                                      uint32_t channels, uint32_t length) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x, c = blockIdx.y;
+    if (t >= length || c >= channels) return;
+    const size_t i = (size_t)c * length + t;
+    y[i] = snake(x[i], ldw(alpha, c, dtype));
+}
+
+__global__ __launch_bounds__(256) void k_vae_scale_bias_cm(float *x, const void *scale, const void *bias,
+                                                           uint32_t sdt, uint32_t bdt, uint32_t channels,
+                                                           uint32_t length, uint32_t bucket) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x, c = blockIdx.y;
+    if (t >= length || c >= channels) return;
+    const size_t i = (size_t)c * length + t;
+    const uint32_t idx = bucket * channels + c;
+    x[i] = x[i] * ldw(scale, idx, sdt) + ldw(bias, idx, bdt);
+}
+
+__global__ __launch_bounds__(256) void k_vae_add_cm(float *a, const float *b, uint32_t channels, uint32_t length) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x, c = blockIdx.y;
+    if (t >= length || c >= channels) return;
+    const size_t i = (size_t)c * length + t;
+    a[i] += b[i];
+}
+
+__global__ __launch_bounds__(256) void k_vae_tanh(float *x, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) x[i] = tanhf(x[i]);
+}
+
+// -------------------------------------------------------------- frame-major
+// Depthwise k-tap convolution over [L][C] rows, stride 1, dilation d, left pad
+// (causal): y[t][c] = post(b[c] + sum_k w[c][k] pre(x[t + k d - pad][c])), where
+// pre / post are the snake of alpha_in / alpha_out when given. One thread per
+// (t, c), c fastest.
+__global__ __launch_bounds__(256) void k_vae_dwconv_fm(VaeDwArgs a) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= (uint64_t)a.length * a.channels) return;
+    const uint32_t t = (uint32_t)(i / a.channels), c = (uint32_t)(i - (uint64_t)t * a.channels);
+    const float ain = a.alpha_in ? hf(a.alpha_in[c]) : 0.f;
+    float sum = hf(a.b[c]);
+    for (uint32_t k = 0; k < a.kernel; ++k) {
+        const int ti = (int)(t + k * a.dilation) - (int)a.left_pad;
+        if (ti < 0) continue;
+        float v = a.x[(size_t)ti * a.channels + c];
+        if (a.alpha_in) v = snake(v, ain);
+        sum += v * hf(a.w[c * a.kernel + k]);
+    }
+    if (a.alpha_out) sum = snake(sum, hf(a.alpha_out[c]));
+    a.y[i] = sum;
+}
+
+// Input of a stride-s transposed convolution as a GEMM: row j of X2 is
+// [pre(x[j]) | pre(x[j-1])] (zeros for j = 0), pre = snake(alpha)(x * scale + bias)
+// with the per-channel scale/bias of the sample-rate bucket.
+__global__ __launch_bounds__(256) void k_vae_convt_input_fm(VaeConvtInArgs a) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const uint32_t C = a.channels;
+    if (i >= (uint64_t)a.length * 2u * C) return;
+    const uint32_t j = (uint32_t)(i / (2u * C)), r = (uint32_t)(i - (uint64_t)j * 2u * C);
+    const uint32_t tap = r >= C ? 1u : 0u, c = r - tap * C;
+    float v = 0.f;
+    if (j >= tap) {
+        const float x = a.x[(size_t)(j - tap) * C + c];
+        const float pre = a.scale ? x * hf(a.scale[c]) + hf(a.bias[c]) : x;
+        v = snake(pre, hf(a.alpha[c]));
+    }
+    a.x2[i] = v;
+}
+
+// Repack of a ConvTranspose1d weight [Cin][Cout][2s] (kernel 2s, stride s) for
+// the GEMM form: W'[(r Cout + oc)][tap Cin + ic] = W[ic][oc][r + tap s], and the
+// bias tiled over the s phases, b'[r Cout + oc] = b[oc].
+__global__ __launch_bounds__(256) void k_vae_repack_convt(const __half *w, const __half *b, uint32_t cin,
+                                                          uint32_t cout, uint32_t s, __half *wp, float *bp) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const uint64_t n = (uint64_t)s * cout * 2u * cin;
+    if (i < n) {
+        const uint32_t row = (uint32_t)(i / (2u * cin)), col = (uint32_t)(i - (uint64_t)row * 2u * cin);
+        const uint32_t r = row / cout, oc = row - r * cout, tap = col / cin, ic = col - tap * cin;
+        wp[i] = w[((size_t)ic * cout + oc) * (2u * s) + r + tap * s];
+    }
+    if (i < (uint64_t)s * cout) bp[i] = hf(b[i % cout]);
+}
+
+// y[t][n] (+)= b[n] + sum_k x[t][k] W[n][k] for short K (the GEMM takes K % 128
+// == 0): one thread per (t, n), x row in LDS.
+__global__ __launch_bounds__(256) void k_vae_linear_fm(VaeLinearArgs a) {
+    extern __shared__ float xs[];
+    const uint32_t t = blockIdx.y;
+    for (uint32_t k = threadIdx.x; k < a.K; k += 256u) xs[k] = a.x[(size_t)t * a.ldx + k];
+    __syncthreads();
+    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
+    if (n >= a.N) return;
+    float sum = 0.f;
+    const __half *w = a.w + (size_t)n * a.K;
+    for (uint32_t k = 0; k < a.K; ++k) sum += xs[k] * __half2float(w[k]);
+    const float v = sum + (a.bias_f32 ? a.bias_f32[n] : (a.bias ? __half2float(a.bias[n]) : 0.f));
+    float *dst = a.y + (size_t)t * a.ldy + n;
+    *dst = a.residual ? *dst + v : v;
+}
+
+// Decoder head: wave[t] = tanh(b + sum_c sum_k w[c][k] snake(x[t + k - pad][c])),
+// one output channel (model.8 snake, model.9 conv, vae_tanh.comp).
+__global__ __launch_bounds__(256) void k_vae_head_fm(VaeHeadArgs a) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= a.length) return;
+    float sum = hf(a.b[0]);
+    for (uint32_t c = 0; c < a.channels; ++c) {
+        const float al = hf(a.alpha[c]);
+        for (uint32_t k = 0; k < a.kernel; ++k) {
+            const int ti = (int)(t + k) - (int)a.left_pad;
+            if (ti < 0) continue;
+            sum += snake(a.x[(size_t)ti * a.channels + c], al) * hf(a.w[c * a.kernel + k]);
+        }
+    }
+    a.y[t] = tanhf(sum);
+}
+
+unsigned grid1(uint64_t n) { return (unsigned)((n + 255u) / 256u); }
+
+}  // namespace
+
+int launch_vae_conv1d_cm(hipStream_t s, const VaeConvArgs &a, bool transpose) {
+    if (!a.out_length || !a.out_channels) return VX_OK;
+    const dim3 g(grid1(a.out_length), a.out_channels);
+    if (transpose) {
+        k_vae_convt1d_cm<<<g, 256, 0, s>>>(a);
+        VX_LAUNCHED("k_vae_convt1d_cm");
+    } else {
+        k_vae_conv1d_cm<<<g, 256, 0, s>>>(a);
+        VX_LAUNCHED("k_vae_conv1d_cm");
+    }
+    return VX_OK;
+}
+
+int launch_vae_snake_cm(hipStream_t s, const float *x, float *y, const void *alpha, uint32_t dtype, uint32_t c,
+                        uint32_t len) {
+    if (!c || !len) return VX_OK;
+    k_vae_snake_cm<<<dim3(grid1(len), c), 256, 0, s>>>(x, y, alpha, dtype, c, len);
+    VX_LAUNCHED("k_vae_snake_cm");
+    return VX_OK;
+}
+
+int launch_vae_scale_bias_cm(hipStream_t s, float *x, const void *scale, const void *bias, uint32_t sdt,
+                             uint32_t bdt, uint32_t c, uint32_t len, uint32_t bucket) {
+    if (!c || !len) return VX_OK;
+    k_vae_scale_bias_cm<<<dim3(grid1(len), c), 256, 0, s>>>(x, scale, bias, sdt, bdt, c, len, bucket);
+    VX_LAUNCHED("k_vae_scale_bias_cm");
+    return VX_OK;
+}
+
+int launch_vae_add_cm(hipStream_t s, float *a, const float *b, uint32_t c, uint32_t len) {
+    if (!c || !len) return VX_OK;
+    k_vae_add_cm<<<dim3(grid1(len), c), 256, 0, s>>>(a, b, c, len);
+    VX_LAUNCHED("k_vae_add_cm");
+    return VX_OK;
+}
+
+int launch_vae_tanh(hipStream_t s, float *x, uint32_t n) {
+    if (!n) return VX_OK;
+    k_vae_tanh<<<grid1(n), 256, 0, s>>>(x, n);
+    VX_LAUNCHED("k_vae_tanh");
+    return VX_OK;
+}
+
+int launch_vae_dwconv_fm(hipStream_t s, const VaeDwArgs &a) {
+    const uint64_t n = (uint64_t)a.length * a.channels;
+    if (!n) return VX_OK;
+    k_vae_dwconv_fm<<<grid1(n), 256, 0, s>>>(a);
+    VX_LAUNCHED("k_vae_dwconv_fm");
+    return VX_OK;
+}
+
+int launch_vae_convt_input_fm(hipStream_t s, const VaeConvtInArgs &a) {
+    const uint64_t n = (uint64_t)a.length * 2u * a.channels;
+    if (!n) return VX_OK;
+    k_vae_convt_input_fm<<<grid1(n), 256, 0, s>>>(a);
+    VX_LAUNCHED("k_vae_convt_input_fm");
+    return VX_OK;
+}
+
+int launch_vae_repack_convt(hipStream_t s, const __half *w, const __half *b, uint32_t cin, uint32_t cout,
+                            uint32_t stride, __half *wp, float *bp) {
+    const uint64_t n = (uint64_t)stride * cout * 2u * cin;
+    k_vae_repack_convt<<<grid1(n), 256, 0, s>>>(w, b, cin, cout, stride, wp, bp);
+    VX_LAUNCHED("k_vae_repack_convt");
+    return VX_OK;
+}
+
+int launch_vae_linear_fm(hipStream_t s, const VaeLinearArgs &a) {
+    if (!a.T || !a.N) return VX_OK;
+    if (a.K > 4096u) return fail(VX_ERR_UNSUPPORTED, "vae linear: K %u > 4096", a.K);
+    k_vae_linear_fm<<<dim3(grid1(a.N), a.T), 256, (size_t)a.K * 4u, s>>>(a);
+    VX_LAUNCHED("k_vae_linear_fm");
+    return VX_OK;
+}
+
+int launch_vae_head_fm(hipStream_t s, const VaeHeadArgs &a) {
+    if (!a.length) return VX_OK;
+    k_vae_head_fm<<<grid1(a.length), 256, 0, s>>>(a);
+    VX_LAUNCHED("k_vae_head_fm");
+    return VX_OK;
+}
+
+}  // namespace vx

@@ -286,7 +286,7 @@ int launch_dequant(hipStream_t s, const WRef &w, uint32_t rows, uint32_t cols, f
 // Projection GEMM C[t][n] = sum_k X[t][k] W[n][k] on MFMA (kernels_seq.hip).
 enum GemmEpilogue : uint32_t {
     GEPI_STORE = 0,     // out[t][n] = alpha * (acc + bias[n])   (atomic add when split)
-    GEPI_RESIDUAL = 1,  // out[t][n] += scale * acc               (atomic add when split)
+    GEPI_RESIDUAL = 1,  // out[t][n] += scale * (acc [+ bias[n]]) (atomic add when split)
     GEPI_SWIGLU = 2     // seg 0 = gate, seg 1 = up: silu(g) * u -> seg[0].out and/or planes
 };
 struct GemmSeg {                    // one weight matrix covering part of N
@@ -445,6 +445,60 @@ void prefill_stack_free(vx_ctx *ctx, StackWork *w);
 // The layers over rows 0..T-1 of work->h at positions pos0..pos0+T-1 (K/V rows
 // stored at those positions); work->h then holds every row's residual stream.
 int enqueue_prefill_stack(const PrefillStack &p, uint32_t pos0, uint32_t T);
+
+// ------------------------------------------------------------ AudioVAE (kernels_vae.hip)
+struct VaeConvArgs {                // vae_conv1d.comp / vae_convtranspose1d.comp, channel-major
+    const float *x = nullptr;
+    float *y = nullptr;
+    const void *w = nullptr, *bias = nullptr;   // model scalars (dtype 0 = f32, 1 = f16); bias nullable
+    uint32_t w_dtype = 1, bias_dtype = 1;
+    uint32_t in_channels = 0, out_channels = 0, in_length = 0, out_length = 0;
+    uint32_t kernel = 1, stride = 1, dilation = 1, groups = 1, left_pad = 0;
+};
+int launch_vae_conv1d_cm(hipStream_t s, const VaeConvArgs &a, bool transpose);
+int launch_vae_snake_cm(hipStream_t s, const float *x, float *y, const void *alpha, uint32_t dtype, uint32_t c,
+                        uint32_t len);
+int launch_vae_scale_bias_cm(hipStream_t s, float *x, const void *scale, const void *bias, uint32_t sdt,
+                             uint32_t bdt, uint32_t c, uint32_t len, uint32_t bucket);
+int launch_vae_add_cm(hipStream_t s, float *a, const float *b, uint32_t c, uint32_t len);
+int launch_vae_tanh(hipStream_t s, float *x, uint32_t n);
+struct VaeDwArgs {                  // depthwise conv over frame-major rows
+    const float *x = nullptr;
+    float *y = nullptr;
+    const __half *w = nullptr, *b = nullptr;            // [C][kernel], [C]
+    const __half *alpha_in = nullptr, *alpha_out = nullptr;   // nullable snakes
+    uint32_t channels = 0, length = 0, kernel = 7, dilation = 1, left_pad = 0;
+};
+int launch_vae_dwconv_fm(hipStream_t s, const VaeDwArgs &a);
+struct VaeConvtInArgs {             // [pre(x[j]) | pre(x[j-1])] rows for the transposed-conv GEMM
+    const float *x = nullptr;
+    float *x2 = nullptr;
+    const __half *scale = nullptr, *bias = nullptr;     // nullable: the sample-rate bucket's rows
+    const __half *alpha = nullptr;
+    uint32_t channels = 0, length = 0;
+};
+int launch_vae_convt_input_fm(hipStream_t s, const VaeConvtInArgs &a);
+int launch_vae_repack_convt(hipStream_t s, const __half *w, const __half *b, uint32_t cin, uint32_t cout,
+                            uint32_t stride, __half *wp, float *bp);
+struct VaeLinearArgs {              // y[t][n] (+)= b[n] + x[t] . W[n], short K
+    const float *x = nullptr;
+    uint32_t ldx = 0;
+    const __half *w = nullptr;      // [N][K]
+    const __half *bias = nullptr;
+    const float *bias_f32 = nullptr;
+    float *y = nullptr;
+    uint32_t ldy = 0;
+    uint32_t T = 0, N = 0, K = 0;
+    uint32_t residual = 0;
+};
+int launch_vae_linear_fm(hipStream_t s, const VaeLinearArgs &a);
+struct VaeHeadArgs {                // snake -> k-tap conv to one channel -> tanh
+    const float *x = nullptr;
+    float *y = nullptr;
+    const __half *alpha = nullptr, *w = nullptr, *b = nullptr;
+    uint32_t channels = 0, length = 0, kernel = 7, left_pad = 6;
+};
+int launch_vae_head_fm(hipStream_t s, const VaeHeadArgs &a);
 
 // Engine hooks of the cross-engine text prefill (baselm.cpp). baselm_prefill_rows
 // runs the batched prefill of n tokens at the engine position and, when rows is

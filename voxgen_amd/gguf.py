@@ -120,3 +120,13 @@ class Gguf:
         c = abi.AcousticConfig()
         abi.call("vx_acoustic_config_from_gguf", self.handle, C.byref(b), active_context, C.byref(c))
         return {k: getattr(c, k) for k, _ in c._fields_}
+
+    def audiovae_config(self) -> dict:
+        """AudioVaeConfig::from_gguf (audiovae.rs:49-128)."""
+        c = abi.AudioVaeConfig()
+        abi.call("vx_audiovae_config_from_gguf", self.handle, C.byref(c))
+        out = {}
+        for k, _ in c._fields_:
+            v = getattr(c, k)
+            out[k] = list(v) if hasattr(v, "__len__") else v
+        return out

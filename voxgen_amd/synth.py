@@ -337,3 +337,93 @@ def acoustic_metadata(cfg: dict) -> dict:
         "voxcpm.fsq.latent_dim": (U32, cfg["fsq_latent_dim"]),
         "voxcpm.fsq.scale": (F32, cfg["fsq_scale"]),
     }
+
+
+def audiovae_config(decoder_dim=2048, latent=64, encoder_dim=128, bucket=3) -> dict:
+    """vx_audiovae_config fields. Defaults are the VoxCPM2 AudioVAE V2 contract
+    (AudioVaeConfig::from_gguf, audiovae.rs:49-79)."""
+    enc, dec = [2, 5, 8, 8], [8, 6, 5, 2, 2, 2]
+    return dict(encoder_dim=encoder_dim, latent_dim=latent, decoder_dim=decoder_dim, sample_rate=16000,
+                out_sample_rate=48000, encoder_rates=enc, decoder_rates=dec, encoder_hop=640, decoder_hop=1920,
+                patch_size=4, input_samples_per_patch=2560, output_samples_per_patch=7680,
+                sr_bin_boundaries=[20000, 30000, 40000], decoder_sr_bucket=bucket, depthwise=1)
+
+
+def build_audiovae(cfg: dict, seed: int = 0x5EED0080, encoder: bool = False, with_data: bool = True) -> SynthModel:
+    """Synthetic AudioVAE tensors with the names, shapes and F16 dtype that
+    validate_tensors checks (audiovae.rs:81-128); the encoder's only with
+    `encoder`. Conv weights N(0, 1/sqrt(fan-in)) (x0.3 for the residual units'
+    1x1 convolutions, x0.1 for the output convolution, so the decoder's
+    activations stay O(1) and tanh unsaturated), biases N(0, 0.02), snake alphas
+    N(1, 0.1), sample-rate scale N(1, 0.05) and bias N(0, 0.02)."""
+    f16 = abi.DTYPE_F16
+    reg = Region()
+    std = {}
+
+    def conv(base, in_c, out_c, k, groups, transpose=False, gain=1.0):
+        dims = (k, out_c // groups, in_c) if transpose else (k, in_c // groups, out_c)
+        reg.add(base, f16, dims)
+        std[base] = (0.0, gain / np.sqrt(2.0 * in_c if transpose else (in_c // groups) * k))
+        reg.add(base + ".bias", f16, (out_c,))
+        std[base + ".bias"] = (0.0, 0.02)
+
+    def alpha(name, c):
+        reg.add(name, f16, (1, c, 1))
+        std[name] = (1.0, 0.1)
+
+    if encoder:
+        conv("audio_vae.encoder.block.0", 1, cfg["encoder_dim"], 7, 1)
+        c = cfg["encoder_dim"]
+        for stage, s in enumerate(cfg["encoder_rates"]):
+            b = f"audio_vae.encoder.block.{stage + 1}"
+            for ri in range(3):
+                p = f"{b}.block.{ri}.block"
+                alpha(p + ".0.alpha", c)
+                conv(p + ".1", c, c, 7, c)
+                alpha(p + ".2.alpha", c)
+                conv(p + ".3", c, c, 1, 1)
+            alpha(b + ".block.3.alpha", c)
+            conv(b + ".block.4", c, 2 * c, 2 * s, 1)
+            c *= 2
+        conv("audio_vae.encoder.fc_mu", c, cfg["latent_dim"], 3, 1)
+        conv("audio_vae.encoder.fc_logvar", c, cfg["latent_dim"], 3, 1)
+    L = cfg["latent_dim"]
+    conv("audio_vae.decoder.model.0", L, L, 7, L)
+    conv("audio_vae.decoder.model.1", L, cfg["decoder_dim"], 1, 1)
+    din = cfg["decoder_dim"]
+    for i, s in enumerate(cfg["decoder_rates"]):
+        mi, dout = i + 2, din // 2
+        for kind, ms in (("scale_embed", (1.0, 0.05)), ("bias_embed", (0.0, 0.02))):
+            name = f"audio_vae.decoder.sr_cond_model.{mi}.{kind}"
+            reg.add(name, f16, (din, 4))
+            std[name] = ms
+        p = f"audio_vae.decoder.model.{mi}"
+        alpha(p + ".block.0.alpha", din)
+        conv(p + ".block.1", din, dout, 2 * s, 1, transpose=True)
+        for rj in range(3):
+            q = f"{p}.block.{rj + 2}.block"
+            alpha(q + ".0.alpha", dout)
+            conv(q + ".1", dout, dout, 7, dout)
+            alpha(q + ".2.alpha", dout)
+            conv(q + ".3", dout, dout, 1, 1, gain=0.3)
+        din = dout
+    alpha("audio_vae.decoder.model.8.alpha", din)
+    conv("audio_vae.decoder.model.9", din, 1, 7, 1, gain=0.1)
+    data = np.zeros((reg.size + 255) // 256 * 256 if with_data else 0, np.uint8)
+    if with_data:
+        for i, t in enumerate(reg.tensors):
+            mean, sd = std[t.name]
+            lib().vs_fill_normal_f16(_ptr(data, t.offset), int(np.prod(t.dims)), derive_seed(seed, i), mean, sd)
+    meta = {
+        "general.architecture": (8, "voxcpm-acoustic"),
+        "general.alignment": (4, ALIGN),
+        "voxcpm.model_version": (6, 2.0),
+        "voxcpm.patch_size": (4, cfg["patch_size"]),
+        "voxcpm.audiovae.encoder_dim": (4, cfg["encoder_dim"]),
+        "voxcpm.audiovae.latent_dim": (4, cfg["latent_dim"]),
+        "voxcpm.audiovae.decoder_dim": (4, cfg["decoder_dim"]),
+        "voxcpm.audiovae.sample_rate": (4, cfg["sample_rate"]),
+        "voxcpm.audiovae.out_sample_rate": (4, cfg["out_sample_rate"]),
+        "voxcpm.audiovae.cond_type": (8, "scale_bias"),
+    }
+    return SynthModel(data, reg.tensors, dict(cfg), meta)
