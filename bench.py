@@ -22,6 +22,8 @@ Prints one JSON line with:
                2, 10 timesteps): solve time and weight-streaming GB/s
   residual     the ResidualLM step (FSQ + fusion + 8 F16 layers without RoPE,
                hidden 2048): steps/s and weight-streaming GB/s
+  audiovae     the AudioVAE decode of 40 latent frames (1.6 s of 48 kHz audio):
+               time, real-time factor and GEMM-form TFLOP/s
 
 `--copy-calibration` instead runs one plain copy kernel of known size (the
 reference point for the FETCH_SIZE / WRITE_SIZE counters).
@@ -98,6 +100,8 @@ def parse():
     ap.add_argument("--residual-steps", type=int, default=64,
                     help="ResidualLM steps timed (0 skips the ResidualLM leg)")
     ap.add_argument("--residual-only", action="store_true", help="run only the ResidualLM leg (for profiling)")
+    ap.add_argument("--vae-frames", type=int, default=40, help="latent frames of the AudioVAE leg (0 skips it)")
+    ap.add_argument("--vae-only", action="store_true", help="run only the AudioVAE leg (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the token-batched prefill leg (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -327,6 +331,60 @@ def text_prefill(ctx, base, bcfg, amodel, acfg, T, reps=3, seq_positions=32):
             "speedup": round(per_pos_ms * T / ms, 1)}
 
 
+def vae_flops(frames):
+    """Multiply-adds x 2 of one AudioVAE decode of `frames` latent frames at the
+    VoxCPM2 geometry (latent 64, decoder 2048, rates 8,6,5,2,2,2)."""
+    L, c = frames, 2048
+    f = 2 * (64 * 7 * L + 64 * 2048 * L)
+    for s in (8, 6, 5, 2, 2, 2):
+        co, lo = c // 2, L * s
+        f += 2 * lo * co * c * 2                       # transposed conv: 2 taps per input channel
+        f += 3 * 2 * (lo * co * 7 + lo * co * co)      # residual units: depthwise k=7 + 1x1
+        c, L = co, lo
+    return f + 2 * L * c * 7
+
+
+def vae_leg(ctx, frames, reps=5):
+    """AudioVAE decode (audiovae.rs:330-372) of `frames` latent frames at the VoxCPM2
+    geometry, F16 weights (synthetic, activations O(1)), latents N(0,1) resident
+    on the device (decode_latents_gpu), timed with a sync per decode."""
+    from voxgen_amd import synth
+    from voxgen_amd.audiovae import AudioVaeEngine
+    from voxgen_amd.runtime import Model
+    cfg = synth.audiovae_config()
+    m = synth.build_audiovae(cfg, seed=0x5EED001A)
+    model = Model(ctx, m.data, m.tensors)
+    vae = AudioVaeEngine(ctx, model, cfg, strict_geometry=True)
+    lat = ctx.array(synth.normal_f32(frames * 64, 0x5EED001B))
+    wave = ctx.alloc(frames * 1920 * 4)
+    vae.decode_latents_gpu(lat, frames, wave)
+    ctx.sync()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        vae.decode_latents_gpu(lat, frames, wave)
+        ctx.sync()
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    vae.decode_latents_gpu(lat, frames, wave)
+    prof = ctx.prof_snapshot()
+    ctx.prof_enable(False)
+    vae.close()
+    model.free()
+    flops = vae_flops(frames)
+    audio_s = frames * 1920 / 48000
+    log(f"audiovae decode of {frames} frames ({audio_s:.2f} s audio): {ms:.2f} ms -> {audio_s * 1e3 / ms:.0f}x "
+        f"real time, {flops / ms / 1e9:.1f} TFLOP/s")
+    per = {k: dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"], total_ms=round(v["total_ms"], 4))
+           for k, v in prof.items()}
+    return {"workload": f"audiovae_v2_decode_{frames}frames_dec2048", "ms": round(ms, 3),
+            "audio_seconds": audio_s, "realtime_factor": round(audio_s * 1e3 / ms, 1),
+            "flops": int(flops), "TFLOPs": round(flops / ms / 1e9, 2),
+            "mfma_frac": round(flops / ms / 1e9 / 2500.0, 4), "per_span_eager": per}
+
+
 def synth_tokens(n, cfg):
     from voxgen_amd import synth
     return synth.uniform_u32(n, 0x5EED0013, cfg["vocab_size"]).astype(np.uint32)
@@ -359,6 +417,13 @@ def main():
     eng = BaseLmEngine(ctx, model, cfg, exec_mode=args.mode, strict_geometry=True)
     log(f"device {info['name']} {info['arch']} CUs={info['compute_units']}; model on device "
         f"{model.device_bytes / 1e9:.2f} GB")
+    if args.vae_only:
+        va = vae_leg(ctx, args.vae_frames)
+        eng.close()
+        model.free()
+        ctx.close()
+        print(json.dumps({"audiovae": va}), flush=True)
+        return
     if args.residual_only:
         rs = residual_leg(ctx, args.residual_steps, baselm=eng, bcfg=cfg)
         eng.close()
@@ -439,6 +504,7 @@ def main():
     eng.close()
     model.free()
     cfm = cfm_leg(ctx, args.cfm_reps) if args.cfm_reps else None
+    audiovae = vae_leg(ctx, args.vae_frames) if args.vae_frames else None
     ctx.close()
 
     line = {
@@ -470,6 +536,7 @@ def main():
         "prefill": prefill,
         "cfm": cfm,
         "residual": residual,
+        "audiovae": audiovae,
         "device": f"{info['name']} ({info['arch']})",
     }
     print(json.dumps(line), flush=True)
