@@ -115,6 +115,35 @@ __global__ __launch_bounds__(256) void k_vae_dwconv_fm(VaeDwArgs a) {
     a.y[i] = sum;
 }
 
+// The same convolution when left_pad = (kernel - 1) * dilation (the causal
+// layers), tiled: a workgroup covers TB = 2048 / CB rows of CB channels, stages
+// pre(x) for its rows and their left halo in LDS once (pre(0) = 0, so the zero
+// padding stays zero), then takes the taps from LDS.
+__global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32_t CB) {
+    __shared__ float xs[2048 + 64 * 54];
+    const uint32_t TB = 2048u / CB, halo = a.left_pad;
+    const uint32_t t0 = blockIdx.x * TB, c0 = blockIdx.y * CB, C = a.channels, tid = threadIdx.x;
+    for (uint32_t idx = tid; idx < (TB + halo) * CB; idx += 256u) {
+        const uint32_t r = idx / CB, cc = idx - r * CB, c = c0 + cc;
+        const int ti = (int)(t0 + r) - (int)halo;
+        float v = 0.f;
+        if (ti >= 0 && (uint32_t)ti < a.length && c < C) {
+            v = a.x[(size_t)ti * C + c];
+            if (a.alpha_in) v = snake(v, hf(a.alpha_in[c]));
+        }
+        xs[idx] = v;
+    }
+    __syncthreads();
+    for (uint32_t o = tid; o < TB * CB; o += 256u) {
+        const uint32_t r = o / CB, cc = o - r * CB, t = t0 + r, c = c0 + cc;
+        if (t >= a.length || c >= C) continue;
+        float sum = hf(a.b[c]);
+        for (uint32_t k = 0; k < a.kernel; ++k) sum += xs[(r + k * a.dilation) * CB + cc] * hf(a.w[c * a.kernel + k]);
+        if (a.alpha_out) sum = snake(sum, hf(a.alpha_out[c]));
+        a.y[(size_t)t * C + c] = sum;
+    }
+}
+
 // Input of a stride-s transposed convolution as a GEMM: row j of X2 is
 // [pre(x[j]) | pre(x[j-1])] (zeros for j = 0), pre = snake(alpha)(x * scale + bias)
 // with the per-channel scale/bias of the sample-rate bucket.
@@ -149,20 +178,27 @@ __global__ __launch_bounds__(256) void k_vae_repack_convt(const __half *w, const
 }
 
 // y[t][n] (+)= b[n] + sum_k x[t][k] W[n][k] for short K (the GEMM takes K % 128
-// == 0): one thread per (t, n), x row in LDS.
-__global__ __launch_bounds__(256) void k_vae_linear_fm(VaeLinearArgs a) {
+// == 0): a workgroup covers NB = min(N, 256) outputs of RB rows, the rows staged
+// in LDS; thread (g, n) computes rows g, g + G, ... (G = 256 / NB).
+__global__ __launch_bounds__(256) void k_vae_linear_fm(VaeLinearArgs a, uint32_t NB, uint32_t RB) {
     extern __shared__ float xs[];
-    const uint32_t t = blockIdx.y;
-    for (uint32_t k = threadIdx.x; k < a.K; k += 256u) xs[k] = a.x[(size_t)t * a.ldx + k];
+    const uint32_t tid = threadIdx.x, G = 256u / NB, n = blockIdx.x * NB + tid % NB, g = tid / NB;
+    const uint32_t r0 = blockIdx.y * RB;
+    for (uint32_t idx = tid; idx < RB * a.K; idx += 256u) {
+        const uint32_t r = idx / a.K, k = idx - r * a.K;
+        xs[idx] = r0 + r < a.T ? a.x[(size_t)(r0 + r) * a.ldx + k] : 0.f;
+    }
     __syncthreads();
-    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
-    if (n >= a.N) return;
-    float sum = 0.f;
+    if (n >= a.N || g >= G) return;
     const __half *w = a.w + (size_t)n * a.K;
-    for (uint32_t k = 0; k < a.K; ++k) sum += xs[k] * __half2float(w[k]);
-    const float v = sum + (a.bias_f32 ? a.bias_f32[n] : (a.bias ? __half2float(a.bias[n]) : 0.f));
-    float *dst = a.y + (size_t)t * a.ldy + n;
-    *dst = a.residual ? *dst + v : v;
+    const float b = a.bias_f32 ? a.bias_f32[n] : (a.bias ? hf(a.bias[n]) : 0.f);
+    for (uint32_t r = g; r < RB && r0 + r < a.T; r += G) {
+        float sum = 0.f;
+        for (uint32_t k = 0; k < a.K; ++k) sum += xs[r * a.K + k] * hf(w[k]);
+        const float v = sum + b;
+        float *dst = a.y + (size_t)(r0 + r) * a.ldy + n;
+        *dst = a.residual ? *dst + v : v;
+    }
 }
 
 // Decoder head: wave[t] = tanh(b + sum_c sum_k w[c][k] snake(x[t + k - pad][c])),
@@ -179,6 +215,25 @@ __global__ __launch_bounds__(256) void k_vae_head_fm(VaeHeadArgs a) {
             sum += snake(a.x[(size_t)ti * a.channels + c], al) * hf(a.w[c * a.kernel + k]);
         }
     }
+    a.y[t] = tanhf(sum);
+}
+
+// The head tiled over 256 output rows: snake(x) of the rows and the left halo
+// staged once in LDS (row stride C + 1), C <= 48.
+__global__ __launch_bounds__(256) void k_vae_head_tiled_fm(VaeHeadArgs a) {
+    __shared__ float xs[(256 + 6) * 49];
+    const uint32_t C = a.channels, S = C + 1u, t0 = blockIdx.x * 256u, halo = a.left_pad;
+    for (uint32_t idx = threadIdx.x; idx < (256u + halo) * C; idx += 256u) {
+        const uint32_t r = idx / C, c = idx - r * C;
+        const int ti = (int)(t0 + r) - (int)halo;
+        xs[r * S + c] = ti >= 0 && (uint32_t)ti < a.length ? snake(a.x[(size_t)ti * C + c], hf(a.alpha[c])) : 0.f;
+    }
+    __syncthreads();
+    const uint32_t t = t0 + threadIdx.x;
+    if (t >= a.length) return;
+    float sum = hf(a.b[0]);
+    for (uint32_t c = 0; c < C; ++c)
+        for (uint32_t k = 0; k < a.kernel; ++k) sum += xs[(threadIdx.x + k) * S + c] * hf(a.w[c * a.kernel + k]);
     a.y[t] = tanhf(sum);
 }
 
@@ -232,6 +287,15 @@ int launch_vae_tanh(hipStream_t s, float *x, uint32_t n) {
 int launch_vae_dwconv_fm(hipStream_t s, const VaeDwArgs &a) {
     const uint64_t n = (uint64_t)a.length * a.channels;
     if (!n) return VX_OK;
+    if (a.kernel >= 1u && a.left_pad == (a.kernel - 1u) * a.dilation && a.left_pad <= 54u) {
+        const uint32_t CB = a.channels < 64u ? a.channels : 64u;   // >= 1; 2048 / CB rows per workgroup
+        if (2048u % CB == 0) {
+            const uint32_t TB = 2048u / CB;
+            k_vae_dwconv_tiled_fm<<<dim3((a.length + TB - 1u) / TB, (a.channels + CB - 1u) / CB), 256, 0, s>>>(a, CB);
+            VX_LAUNCHED("k_vae_dwconv_tiled_fm");
+            return VX_OK;
+        }
+    }
     k_vae_dwconv_fm<<<grid1(n), 256, 0, s>>>(a);
     VX_LAUNCHED("k_vae_dwconv_fm");
     return VX_OK;
@@ -256,13 +320,24 @@ int launch_vae_repack_convt(hipStream_t s, const __half *w, const __half *b, uin
 int launch_vae_linear_fm(hipStream_t s, const VaeLinearArgs &a) {
     if (!a.T || !a.N) return VX_OK;
     if (a.K > 4096u) return fail(VX_ERR_UNSUPPORTED, "vae linear: K %u > 4096", a.K);
-    k_vae_linear_fm<<<dim3(grid1(a.N), a.T), 256, (size_t)a.K * 4u, s>>>(a);
+    const uint32_t NB = a.N < 256u ? a.N : 256u, G = 256u / NB;
+    uint32_t rpt = 8192u / (G * a.K);
+    rpt = rpt < 1u ? 1u : (rpt > 8u ? 8u : rpt);
+    const uint32_t RB = G * rpt;   // RB * K <= max(8192, G * K) floats
+    if ((uint64_t)RB * a.K * 4u > 65536u)
+        return fail(VX_ERR_UNSUPPORTED, "vae linear: %u rows x K %u exceed the LDS tile", RB, a.K);
+    k_vae_linear_fm<<<dim3((a.N + NB - 1u) / NB, (a.T + RB - 1u) / RB), 256, (size_t)RB * a.K * 4u, s>>>(a, NB, RB);
     VX_LAUNCHED("k_vae_linear_fm");
     return VX_OK;
 }
 
 int launch_vae_head_fm(hipStream_t s, const VaeHeadArgs &a) {
     if (!a.length) return VX_OK;
+    if (a.channels <= 48u && a.left_pad <= 6u && a.kernel == a.left_pad + 1u) {
+        k_vae_head_tiled_fm<<<grid1(a.length), 256, 0, s>>>(a);
+        VX_LAUNCHED("k_vae_head_tiled_fm");
+        return VX_OK;
+    }
     k_vae_head_fm<<<grid1(a.length), 256, 0, s>>>(a);
     VX_LAUNCHED("k_vae_head_fm");
     return VX_OK;
