@@ -244,7 +244,7 @@ def residual_step_bytes(pos):
     return fsq + fusion + Lr * layer + Hr * 4
 
 
-def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384):
+def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384, cpu_steps=0):
     """The ResidualLM step of the VoxCPM2 acoustic model (acoustic.rs:830-1035):
     FSQ of the BaseLM hidden, fusion with the acoustic embedding, 8 F16 layers
     (hidden 2048, FFN 6144, 16/2 x 128, no RoPE), F16 weights N(0, 0.02); inputs
@@ -282,11 +282,25 @@ def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384):
         text = text_prefill(ctx, baselm, bcfg, model, acfg, prefix)
     eng.close()
     model.free()
+    cpu = None
+    if cpu_steps:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import voxref
+        o = voxref.ResidualFsq(m.data, {t.name: t for t in m.tensors}, acfg)
+        b, e = synth.normal_f32(2048, 0x5EED0017), synth.normal_f32(2048, 0x5EED0018)
+        t0 = time.perf_counter()
+        for p in range(cpu_steps):
+            o.step(b, e, p, fsq=True)
+        el = time.perf_counter() - t0
+        cpu = {"value": round(cpu_steps / el, 3), "unit": "steps/s", "cores": voxref.threads(), "kind": "port",
+               "sample": f"{cpu_steps} FSQ ResidualLM steps at positions 0..{cpu_steps - 1}, same model, C oracle "
+                         f"(oracle/voxref.c) with OpenMP over rows"}
+        log(f"cpu oracle residual: {cpu_steps} steps in {el:.2f}s")
     per = {k: dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"]) for k, v in prof.items()}
     return {"workload": "residual_lm_f16_fsq_fusion_8L_h2048_ffn6144_16q2kv", "us_per_step": round(ms * 1e3, 2),
             "steps_per_second": round(1e3 / ms, 1), "positions": f"{p0}..{p0 + steps - 1}",
             "bytes_per_step": int(nbytes), "achieved_GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "per_kernel_eager": per, "text_prefill": text}
+            "per_kernel_eager": per, "text_prefill": text, "cpu_baseline": cpu}
 
 
 def text_prefill(ctx, base, bcfg, amodel, acfg, T, reps=3, seq_positions=32):
@@ -344,7 +358,7 @@ def vae_flops(frames):
     return f + 2 * L * c * 7
 
 
-def vae_leg(ctx, frames, reps=5):
+def vae_leg(ctx, frames, reps=5, cpu_frames=0):
     """AudioVAE decode (audiovae.rs:330-372) of `frames` latent frames at the VoxCPM2
     geometry, F16 weights (synthetic, activations O(1)), latents N(0,1) resident
     on the device (decode_latents_gpu), timed with a sync per decode."""
@@ -373,6 +387,19 @@ def vae_leg(ctx, frames, reps=5):
     ctx.prof_enable(False)
     vae.close()
     model.free()
+    cpu = None
+    if cpu_frames:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import voxref
+        o = voxref.AudioVae(m.data, {t.name: t for t in m.tensors}, cfg)
+        lat_h = synth.normal_f32(cpu_frames * 64, 0x5EED001B)
+        t0 = time.perf_counter()
+        o.decode(lat_h)
+        el = time.perf_counter() - t0
+        cpu = {"value": round(cpu_frames * 1920 / 48000 / el, 3), "unit": "audio s per s", "cores": voxref.threads(),
+               "kind": "port", "sample": f"one decode of {cpu_frames} latent frames, same model, C oracle of the "
+                                         f"vae_*.comp shaders (channel-major, OpenMP over output channels)"}
+        log(f"cpu oracle audiovae: {cpu_frames} frames in {el:.2f}s")
     flops = vae_flops(frames)
     audio_s = frames * 1920 / 48000
     log(f"audiovae decode of {frames} frames ({audio_s:.2f} s audio): {ms:.2f} ms -> {audio_s * 1e3 / ms:.0f}x "
@@ -382,7 +409,7 @@ def vae_leg(ctx, frames, reps=5):
     return {"workload": f"audiovae_v2_decode_{frames}frames_dec2048", "ms": round(ms, 3),
             "audio_seconds": audio_s, "realtime_factor": round(audio_s * 1e3 / ms, 1),
             "flops": int(flops), "TFLOPs": round(flops / ms / 1e9, 2),
-            "mfma_frac": round(flops / ms / 1e9 / 2500.0, 4), "per_span_eager": per}
+            "mfma_frac": round(flops / ms / 1e9 / 2500.0, 4), "per_span_eager": per, "cpu_baseline": cpu}
 
 
 def synth_tokens(n, cfg):
@@ -500,11 +527,12 @@ def main():
     prefill = None
     if args.prefill_tokens:
         prefill = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
-    residual = residual_leg(ctx, args.residual_steps, baselm=eng, bcfg=cfg) if args.residual_steps else None
+    residual = (residual_leg(ctx, args.residual_steps, baselm=eng, bcfg=cfg, cpu_steps=0 if args.no_cpu else 128)
+                if args.residual_steps else None)
     eng.close()
     model.free()
     cfm = cfm_leg(ctx, args.cfm_reps) if args.cfm_reps else None
-    audiovae = vae_leg(ctx, args.vae_frames) if args.vae_frames else None
+    audiovae = vae_leg(ctx, args.vae_frames, cpu_frames=0 if args.no_cpu else args.vae_frames) if args.vae_frames else None
     ctx.close()
 
     line = {
