@@ -114,7 +114,10 @@ uint64_t decoder_max_elements(const vx_audiovae_config &c, uint64_t frames, uint
 
 int grow(vx_ctx *ctx, vx_buf **b, uint64_t *cap, uint64_t floats) {
     if (*cap >= floats) return VX_OK;
-    if (*b) vx_free(ctx, *b);
+    if (*b) {   // an earlier enqueued decode may still read or write it
+        VX_HIP(hipStreamSynchronize(ctx->stream));
+        vx_free(ctx, *b);
+    }
     *b = nullptr;
     *cap = 0;
     VX_CHECK(vx_alloc(ctx, std::max<uint64_t>(floats, 64u) * 4u, b));
