@@ -925,14 +925,23 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     const float *v = a.v + (size_t)bz * S * a.v_stride + (size_t)kv * D;
     float *out = a.out + ((size_t)bz * S + t0) * a.out_stride + (size_t)h * D;
     float *ks = sm, *vs = ks + S * DP, *qs = vs + S * DP, *ps = qs + kDenseFusedRows * DP;
+    const uint32_t half = D >> 1;
+    // Element d of a row, rotated for the row's position pos when a table is given.
+    auto staged = [&](const float *row, uint32_t pos, uint32_t d) -> float {
+        if (!a.rope) return row[d];
+        const uint32_t i = d < half ? d : d - half;
+        const float x0 = row[i], x1 = row[i + half];
+        const float2 cs = a.rope[pos * half + i];
+        return d < half ? x0 * cs.x - x1 * cs.y : x1 * cs.x + x0 * cs.y;
+    };
     for (uint32_t i = tid; i < S * D; i += 256u) {
         const uint32_t t = i / D, d = i - t * D;
-        ks[t * DP + d] = k[(size_t)t * a.k_stride + d];
+        ks[t * DP + d] = staged(k + (size_t)t * a.k_stride, t, d);
         vs[t * DP + d] = v[(size_t)t * a.v_stride + d];
     }
     for (uint32_t i = tid; i < R * D; i += 256u) {
         const uint32_t t = i / D, d = i - t * D;
-        qs[t * DP + d] = q[(size_t)t * a.q_stride + d];
+        qs[t * DP + d] = staged(q + (size_t)t * a.q_stride, t0 + t, d);
     }
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)D);
@@ -1107,6 +1116,29 @@ int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which) {
         k_dense_values<<<dim3(a.q_heads, a.tokens, a.batch), 256, 0, s>>>(a);
         VX_LAUNCHED("k_dense_values");
     }
+    return VX_OK;
+}
+
+namespace {
+__global__ __launch_bounds__(256) void k_rope_pos_table(float2 *tab, const float *factors, uint32_t tokens,
+                                                        uint32_t head_dim, float theta, float scaling) {
+    const uint32_t half = head_dim / 2u, n = tokens * half;
+    const uint32_t j = blockIdx.x * 256u + threadIdx.x;
+    if (j >= n) return;
+    const uint32_t pos = j / half, i = j - pos * half;
+    const float exponent = (float)(i * 2u) / (float)head_dim;   // as k_seq_rope_store
+    const float inv_freq = 1.0f / powf(theta, exponent);
+    const float angle = (float)pos * inv_freq / factors[i];
+    tab[j] = make_float2(cosf(angle) * scaling, sinf(angle) * scaling);
+}
+}  // namespace
+
+int launch_rope_pos_table(hipStream_t s, float2 *table, const float *factors, uint32_t tokens, uint32_t head_dim,
+                          float theta, float scaling) {
+    const uint32_t n = tokens * (head_dim / 2u);
+    if (!n) return VX_OK;
+    k_rope_pos_table<<<(n + 255u) / 256u, 256, 0, s>>>(table, factors, tokens, head_dim, theta, scaling);
+    VX_LAUNCHED("k_rope_pos_table");
     return VX_OK;
 }
 

@@ -58,6 +58,7 @@ struct vx_locdit {
     vx_buf *tsin = nullptr, *ttmp = nullptr, *tvec = nullptr, *dsin = nullptr, *dtmp = nullptr, *dvec = nullptr;
     vx_buf *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     vx_buf *gate = nullptr, *branch = nullptr, *scores = nullptr, *out = nullptr, *seed = nullptr;
+    vx_buf *rope_tab = nullptr;   // (cos, sin) per position of a sequence, for the fused attention
     vx_graph *graph = nullptr;
     vx_cfm_options graph_opt{};
     int graph_initial_x = -1;
@@ -134,7 +135,7 @@ void free_all(vx_locdit *e) {
     vx_buf **bufs[] = {&e->x,      &e->cond_in, &e->mu,   &e->patch_proj, &e->cond_proj_out, &e->tsin,
                        &e->ttmp,   &e->tvec,    &e->dsin, &e->dtmp,       &e->dvec,          &e->hidden,
                        &e->norm,   &e->q,       &e->k,    &e->v,          &e->attn,          &e->gate,
-                       &e->branch, &e->scores,  &e->out,  &e->seed};
+                       &e->branch, &e->scores,  &e->out,  &e->seed,       &e->rope_tab};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -230,7 +231,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
             float *const o[3] = {F(e->q), F(e->k), F(e->v)};
             VX_CHECK(enqueue_seq_qkv(s, w, rows, H, M, F(e->norm), 0, H, o, strides, true));
         }
-        {
+        if (!e->dense_fused) {
             ProfSpan sp(ctx, "local.seq_rope");
             SeqRopeArgs r;
             r.q = F(e->q);
@@ -265,6 +266,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
             a.score_stride = S;
             a.batch = batch;
             if (e->dense_fused) {
+                a.rope = reinterpret_cast<const float2 *>(e->rope_tab->ptr);   // RoPE applied while staging q, k
                 VX_CHECK(launch_dense_attn_fused(s, a));
             } else {
                 VX_CHECK(launch_dense_attn(s, a, 0));
@@ -491,12 +493,17 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
                 {&e->branch, S2 * H},
                 {&e->scores, S2 * c.q_heads * e->S},
                 {&e->out, 2ull * c.patch * c.feat_dim},
-                {&e->seed, 2}};
+                {&e->seed, 2},
+                {&e->rope_tab, (uint64_t)e->S * c.head_dim}};
     for (auto &b : bufs)
         if ((st = vx_alloc(ctx, std::max<uint64_t>(b.n * f, 16u), b.b))) return bail(st);
     for (auto &b : bufs)
         if (hipMemsetAsync((*b.b)->ptr, 0, (*b.b)->bytes, ctx->stream) != hipSuccess)
             return bail(fail(VX_ERR_HIP, "hipMemsetAsync of LocDiT state failed"));
+    if (e->dense_fused && (st = launch_rope_pos_table(ctx->stream, reinterpret_cast<float2 *>(e->rope_tab->ptr),
+                                                      e->rope_factors, e->S, c.head_dim, c.rope_theta,
+                                                      c.rope_scaling)))
+        return bail(st);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return bail(fail(VX_ERR_HIP, "LocDiT init sync failed"));
     *out = e;
     return VX_OK;

@@ -563,8 +563,16 @@ struct DenseAttnArgs {
     // Independent sequences of `tokens` rows each (the CFG batch): sequence b
     // starts b*tokens rows into q/k/v/out and b*tokens*q_heads score rows in.
     uint32_t batch = 1;
+    // Fused kernel only, nullable: (cos, sin) [tokens][head_dim / 2] of each token's
+    // position within its sequence; q and k rows are then rotated (NeoX pairs d,
+    // d + head_dim / 2) as they are staged, in place of a separate RoPE pass.
+    const float2 *rope = nullptr;
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
+// table[p][i] = (cos, sin)(p * theta^(-2i/head_dim) / factors[i]) * scaling for
+// positions p < tokens (the angle of k_seq_rope_store).
+int launch_rope_pos_table(hipStream_t s, float2 *table, const float *factors, uint32_t tokens, uint32_t head_dim,
+                          float theta, float scaling);
 // The three phases in one kernel (one workgroup per head, sequence and eight query
 // tokens, everything in LDS) for sequences of at most kDenseFusedMaxTokens tokens whose q, k, v and
 // scores fit 64 KB of LDS; VX_ERR_UNSUPPORTED otherwise. The scores are not stored.
