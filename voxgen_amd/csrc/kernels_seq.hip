@@ -925,23 +925,30 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     const float *v = a.v + (size_t)bz * S * a.v_stride + (size_t)kv * D;
     float *out = a.out + ((size_t)bz * S + t0) * a.out_stride + (size_t)h * D;
     float *ks = sm, *vs = ks + S * DP, *qs = vs + S * DP, *ps = qs + kDenseFusedRows * DP;
-    const uint32_t half = D >> 1;
-    // Element d of a row, rotated for the row's position pos when a table is given.
-    auto staged = [&](const float *row, uint32_t pos, uint32_t d) -> float {
-        if (!a.rope) return row[d];
-        const uint32_t i = d < half ? d : d - half;
-        const float x0 = row[i], x1 = row[i + half];
-        const float2 cs = a.rope[pos * half + i];
-        return d < half ? x0 * cs.x - x1 * cs.y : x1 * cs.x + x0 * cs.y;
-    };
     for (uint32_t i = tid; i < S * D; i += 256u) {
         const uint32_t t = i / D, d = i - t * D;
-        ks[t * DP + d] = staged(k + (size_t)t * a.k_stride, t, d);
         vs[t * DP + d] = v[(size_t)t * a.v_stride + d];
+        if (!a.rope) ks[t * DP + d] = k[(size_t)t * a.k_stride + d];
     }
-    for (uint32_t i = tid; i < R * D; i += 256u) {
-        const uint32_t t = i / D, d = i - t * D;
-        qs[t * DP + d] = staged(q + (size_t)t * a.q_stride, t0 + t, d);
+    if (!a.rope) {
+        for (uint32_t i = tid; i < R * D; i += 256u) {
+            const uint32_t t = i / D, d = i - t * D;
+            qs[t * DP + d] = q[(size_t)t * a.q_stride + d];
+        }
+    } else {
+        // Rotated pairs (d, d + D/2) at the row's position within its sequence.
+        const uint32_t half = D >> 1;
+        for (uint32_t i = tid; i < (S + R) * half; i += 256u) {
+            const uint32_t r = i / half, d = i - r * half;
+            const bool isk = r < S;
+            const uint32_t t = isk ? r : r - S, pos = isk ? t : t0 + t;
+            const float *row = isk ? k + (size_t)t * a.k_stride : q + (size_t)t * a.q_stride;
+            float *dst = (isk ? ks : qs) + t * DP;
+            const float x0 = row[d], x1 = row[d + half];
+            const float2 cs = a.rope[pos * half + d];
+            dst[d] = x0 * cs.x - x1 * cs.y;
+            dst[d + half] = x1 * cs.x + x0 * cs.y;
+        }
     }
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)D);
