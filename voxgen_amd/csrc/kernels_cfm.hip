@@ -77,7 +77,8 @@ __global__ __launch_bounds__(256) void k_time_sinusoidal(float *out, uint32_t di
                                                          uint32_t t_index) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= dim) return;
-    const float t = t_dev ? t_dev[t_index] : t_in;
+    const float t = t_dev ? t_dev[t_index + blockIdx.y] : t_in;   // row blockIdx.y of a batch
+    out += (size_t)blockIdx.y * dim;
     const uint32_t half_dim = dim / 2u;
     const uint32_t j = i % half_dim;
     const float denom = (float)max(half_dim - 1u, 1u);
@@ -127,9 +128,10 @@ __global__ __launch_bounds__(256) void k_fsq_quantize(float *x, uint32_t n, floa
     x[i] = roundf(v * scale) / scale;
 }
 
+// a[r][i] += b[i] for each of gridDim.y rows r of n values.
 __global__ __launch_bounds__(256) void k_add_vectors(float *a, const float *b, uint32_t n) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i < n) a[i] += b[i];
+    if (i < n) a[(size_t)blockIdx.y * n + i] += b[i];
 }
 
 }  // namespace
@@ -149,9 +151,11 @@ int launch_cfm_cfg_euler(hipStream_t s, float *x, const float *pos, const float 
     return VX_OK;
 }
 
-int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index) {
-    if (!dim) return VX_OK;
-    k_time_sinusoidal<<<(dim + 255u) / 256u, 256, 0, s>>>(out, dim, t, t_dev, t_index);
+int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index,
+                           uint32_t rows) {
+    if (!dim || !rows) return VX_OK;
+    if (rows > 1 && !t_dev) return fail(VX_ERR_INVALID_ARG, "time_sinusoidal: several rows need device t values");
+    k_time_sinusoidal<<<dim3((dim + 255u) / 256u, rows), 256, 0, s>>>(out, dim, t, t_dev, t_index);
     VX_LAUNCHED("k_time_sinusoidal");
     return VX_OK;
 }
@@ -178,9 +182,9 @@ int launch_fsq_quantize(hipStream_t s, float *x, uint32_t n, float scale) {
     return VX_OK;
 }
 
-int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n) {
-    if (!n) return VX_OK;
-    k_add_vectors<<<(n + 255u) / 256u, 256, 0, s>>>(a, b, n);
+int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n, uint32_t rows) {
+    if (!n || !rows) return VX_OK;
+    k_add_vectors<<<dim3((n + 255u) / 256u, rows), 256, 0, s>>>(a, b, n);
     VX_LAUNCHED("k_add_vectors");
     return VX_OK;
 }

@@ -59,6 +59,10 @@ struct vx_locdit {
     vx_buf *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     vx_buf *gate = nullptr, *branch = nullptr, *scores = nullptr, *out = nullptr, *seed = nullptr;
     vx_buf *rope_tab = nullptr;   // (cos, sin) per position of a sequence, for the fused attention
+    // Time embeddings of every estimator call of a solve, computed as one batch:
+    // t values, sinusoid rows, MLP hidden rows, embeddings ([steps][hidden]).
+    vx_buf *tvals = nullptr, *trows = nullptr, *tmid = nullptr, *temb = nullptr;
+    uint32_t trows_cap = 0;
     vx_graph *graph = nullptr;
     vx_cfm_options graph_opt{};
     int graph_initial_x = -1;
@@ -135,7 +139,8 @@ void free_all(vx_locdit *e) {
     vx_buf **bufs[] = {&e->x,      &e->cond_in, &e->mu,   &e->patch_proj, &e->cond_proj_out, &e->tsin,
                        &e->ttmp,   &e->tvec,    &e->dsin, &e->dtmp,       &e->dvec,          &e->hidden,
                        &e->norm,   &e->q,       &e->k,    &e->v,          &e->attn,          &e->gate,
-                       &e->branch, &e->scores,  &e->out,  &e->seed,       &e->rope_tab};
+                       &e->branch, &e->scores,  &e->out,  &e->seed,       &e->rope_tab,
+                       &e->tvals,  &e->trows,   &e->tmid, &e->temb};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -159,6 +164,24 @@ int enqueue_time(vx_locdit *e, float t, float dt) {
     return launch_add_vectors(s, F(e->tvec), F(e->dvec), H);
 }
 
+// record_time for the n estimator calls of a solve at once: row i of temb is
+// time_mlp(sin(t_i)) + delta_time_mlp(sin(0)) (the solve's estimator dt is zero),
+// t_i read from the device t values.
+int enqueue_time_rows(vx_locdit *e, uint32_t n) {
+    hipStream_t s = e->ctx->stream;
+    const uint32_t H = e->cfg.hidden;
+    ProfSpan sp(e->ctx, "local.time");
+    VX_CHECK(launch_time_sinusoidal(s, F(e->trows), H, 0.0f, static_cast<const float *>(e->tvals->ptr), 0, n));
+    VX_CHECK(enqueue_seq_linear(s, e->t1.w, e->t1.b, e->t1.bt, H, H, n, F(e->trows), 0, H, F(e->tmid), 0, H, 1.f));
+    VX_CHECK(launch_silu_inplace(s, F(e->tmid), n * H));
+    VX_CHECK(enqueue_seq_linear(s, e->t2.w, e->t2.b, e->t2.bt, H, H, n, F(e->tmid), 0, H, F(e->temb), 0, H, 1.f));
+    VX_CHECK(launch_time_sinusoidal(s, F(e->dsin), H, 0.0f, nullptr, 0));
+    VX_CHECK(enqueue_seq_linear(s, e->d1.w, e->d1.b, e->d1.bt, H, H, 1, F(e->dsin), 0, H, F(e->dtmp), 0, H, 1.f));
+    VX_CHECK(launch_silu_inplace(s, F(e->dtmp), H));
+    VX_CHECK(enqueue_seq_linear(s, e->d2.w, e->d2.b, e->d2.bt, H, H, 1, F(e->dtmp), 0, H, F(e->dvec), 0, H, 1.f));
+    return launch_add_vectors(s, F(e->temb), F(e->dvec), H, n);
+}
+
 // in_proj / cond_proj (record_locdit_common, local.rs:445-449).
 int enqueue_inputs(vx_locdit *e) {
     hipStream_t s = e->ctx->stream;
@@ -174,7 +197,7 @@ int enqueue_inputs(vx_locdit *e) {
 
 // pack_locdit + record_transformer + out_proj for `batch` sequences (1: the
 // conditional pass; 2: conditional then unconditional).
-int enqueue_body(vx_locdit *e, uint32_t batch) {
+int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) {
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_locdit_config &c = e->cfg;
@@ -185,7 +208,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch) {
         PackLocditArgs p;
         p.mu[0] = F(e->mu);
         p.mu[1] = F(e->mu) + H;
-        p.time = F(e->tvec);
+        p.time = time_row ? time_row : F(e->tvec);
         p.cond = c.cond_raw ? F(e->cond_in) : F(e->cond_proj_out);
         p.x = F(e->patch_proj);
         p.out = F(e->hidden);
@@ -365,13 +388,17 @@ int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_
         VX_CHECK(launch_cfm_noise(s, F(e->x), n, static_cast<const uint32_t *>(e->seed->ptr), 0, o.temperature));
     }
     const uint32_t zi = zero_init_steps(o, span.size());
-    uint32_t est = 0;
+    uint32_t est = 0, k = 0;
+    uint32_t active = 0;
+    for (size_t step = 1; step < span.size(); ++step) active += step > zi ? 1u : 0u;
+    if (active > e->trows_cap) return fail(VX_ERR_STATE, "CFM time rows were not prepared for %u steps", active);
+    if (active) VX_CHECK(enqueue_time_rows(e, active));   // mean_mode = false: estimator dt is zero
     for (size_t step = 1; step < span.size(); ++step) {
         if (step <= zi) continue;
         const float t = span[step - 1], dt = t - span[step];
+        (void)t;
         VX_CHECK(enqueue_inputs(e));
-        VX_CHECK(enqueue_time(e, t, 0.0f));   // mean_mode = false: estimator dt is zero
-        VX_CHECK(enqueue_body(e, 2));
+        VX_CHECK(enqueue_body(e, 2, F(e->temb) + (size_t)k++ * e->cfg.hidden));
         ProfSpan sp(e->ctx, "local.cfm_cfg_euler");
         VX_CHECK(launch_cfm_cfg_euler(s, F(e->x), F(e->out), F(e->out) + n, n, dt, o.cfg_value,
                                       o.use_cfg_zero_star ? 1u : 0u));
@@ -379,6 +406,40 @@ int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_
     }
     if (calls) *calls = est;
     return VX_OK;
+}
+
+// The t values of the solve's estimator calls, on the device before the solve is
+// enqueued (or captured); the row buffers grow with the step count, and a cached
+// graph that addresses replaced buffers is dropped.
+int prepare_time_rows(vx_locdit *e, const vx_cfm_options &o) {
+    std::vector<float> span;
+    VX_CHECK(time_span(o.n_timesteps, o.sway_sampling_coef, span));
+    const uint32_t zi = zero_init_steps(o, span.size());
+    std::vector<float> ts;
+    for (size_t step = 1; step < span.size(); ++step)
+        if (step > zi) ts.push_back(span[step - 1]);
+    if (ts.empty()) return VX_OK;
+    vx_ctx *ctx = e->ctx;
+    const uint32_t n = (uint32_t)ts.size(), H = e->cfg.hidden;
+    if (n > e->trows_cap) {
+        VX_HIP(hipStreamSynchronize(ctx->stream));
+        if (e->graph) {
+            vx_graph_free(ctx, e->graph);
+            e->graph = nullptr;
+        }
+        for (vx_buf **b : {&e->tvals, &e->trows, &e->tmid, &e->temb})
+            if (*b) {
+                vx_free(ctx, *b);
+                *b = nullptr;
+            }
+        e->trows_cap = 0;
+        VX_CHECK(vx_alloc(ctx, (uint64_t)n * 4u, &e->tvals));
+        VX_CHECK(vx_alloc(ctx, (uint64_t)n * H * 4u, &e->trows));
+        VX_CHECK(vx_alloc(ctx, (uint64_t)n * H * 4u, &e->tmid));
+        VX_CHECK(vx_alloc(ctx, (uint64_t)n * H * 4u, &e->temb));
+        e->trows_cap = n;
+    }
+    return vx_upload(ctx, e->tvals, 0, ts.data(), (uint64_t)n * 4u);
 }
 
 int check_finite(const float *v, uint64_t n, const char *what) {
@@ -548,6 +609,7 @@ int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const 
     }
     const uint32_t seed[2] = {(uint32_t)opt->seed, (uint32_t)(opt->seed >> 32)};
     VX_CHECK(vx_upload(ctx, e->seed, 0, seed, 8u));
+    VX_CHECK(prepare_time_rows(e, *opt));
     uint32_t calls = 0;
     if (ctx->prof_enabled) {
         VX_CHECK(enqueue_solve(e, *opt, initial_x != nullptr, &calls));

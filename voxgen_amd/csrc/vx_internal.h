@@ -585,7 +585,9 @@ int launch_cfm_noise(hipStream_t s, float *x, uint32_t n, const uint32_t *dev_se
 int launch_cfm_cfg_euler(hipStream_t s, float *x, const float *pos, const float *neg, uint32_t n, float dt, float cfg,
                          uint32_t zero_star);
 // t from t_dev[t_index] when t_dev is set.
-int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index);
+// rows > 1: row r from t_dev[t_index + r] into out + r * dim.
+int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index,
+                           uint32_t rows = 1);
 struct PackLocditArgs {
     const float *mu[2] = {nullptr, nullptr};   // mu tokens (n_mu <= 2), [hidden] each
     const float *time = nullptr;    // [hidden]
@@ -599,7 +601,8 @@ int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a);
 int launch_silu_inplace(hipStream_t s, float *x, uint32_t n);
 // x[i] = round(tanh(x[i]) * scale) / scale (fsq_quantize.comp), i < n.
 int launch_fsq_quantize(hipStream_t s, float *x, uint32_t n, float scale);
-int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n);
+// a[r][i] += b[i] for rows r < rows of n values.
+int launch_add_vectors(hipStream_t s, float *a, const float *b, uint32_t n, uint32_t rows = 1);
 // Embedding rows of n device token ids into out[t][ldo] (bit-exact gather).
 int launch_seq_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offset, uint32_t dtype,
                          uint32_t cols, const uint32_t *tokens, uint32_t n, uint32_t vocab, float alpha,
