@@ -913,10 +913,11 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 // per row (lane per key), the values thread per (row, dim); each dot product and
 // sum runs in the order of the three-kernel path.
 constexpr uint32_t kDenseFusedRows = 8;
+template <int HD>   // head_dim when known at compile time (the dot loops unroll), 0: a.head_dim
 __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     extern __shared__ float sm[];
     const uint32_t h = blockIdx.x, bz = blockIdx.y, t0 = blockIdx.z * kDenseFusedRows;
-    const uint32_t S = a.tokens, D = a.head_dim, DP = D + 1u;
+    const uint32_t S = a.tokens, D = HD ? (uint32_t)HD : a.head_dim, DP = D + 1u;
     const uint32_t R = min(kDenseFusedRows, S - t0);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t kv = h / (a.q_heads / a.kv_heads);
@@ -955,6 +956,7 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     for (uint32_t e = tid; e < R * S; e += 256u) {
         const uint32_t t = e / S, key = e - t * S;
         float s = 0.f;
+#pragma unroll 16
         for (uint32_t d = 0; d < D; ++d) s += qs[t * DP + d] * ks[key * DP + d];
         ps[e] = s * scale;
     }
@@ -974,6 +976,7 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     for (uint32_t o = tid; o < R * D; o += 256u) {
         const uint32_t t = o / D, d = o - t * D;
         float z = 0.f;
+#pragma unroll 8
         for (uint32_t key = 0; key < S; ++key) z += ps[t * S + key] * vs[key * DP + d];
         out[(size_t)t * a.out_stride + d] = z;
     }
@@ -1160,8 +1163,13 @@ int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a) {
     if (a.tokens > kDenseFusedMaxTokens || a.head_dim == 0 || lds > 65536u)
         return fail(VX_ERR_UNSUPPORTED, "fused dense attention: %u tokens x head_dim %u do not fit", a.tokens,
                     a.head_dim);
-    k_dense_attn_fused<<<dim3(a.q_heads, a.batch, (a.tokens + kDenseFusedRows - 1u) / kDenseFusedRows), 256,
-                         (size_t)lds, s>>>(a);
+    const dim3 grid(a.q_heads, a.batch, (a.tokens + kDenseFusedRows - 1u) / kDenseFusedRows);
+    if (a.head_dim == 64u)
+        k_dense_attn_fused<64><<<grid, 256, (size_t)lds, s>>>(a);
+    else if (a.head_dim == 128u)
+        k_dense_attn_fused<128><<<grid, 256, (size_t)lds, s>>>(a);
+    else
+        k_dense_attn_fused<0><<<grid, 256, (size_t)lds, s>>>(a);
     VX_LAUNCHED("k_dense_attn_fused");
     return VX_OK;
 }
