@@ -86,7 +86,7 @@ def test_cfm_solve_graph_replay_seeds_and_initial_x(ctx, ref_shape):
     loc.close()
 
 
-def test_baseline_shape_cfm_solve(ctx):
+def test_cfm_solve_8_layers_16x64_cond32(ctx):
     """The benchmark's LocDiT shape: 8 layers, 16 x 64 MHA, 32 given condition rows
     zeroed in the unconditional pass, no mu tokens; 10 timesteps, cfg 2.0."""
     cfg = synth.locdit_config(layers=8, q_heads=16, kv_heads=16, head_dim=64, n_mu=0, n_cond=32, cond_raw=1,
