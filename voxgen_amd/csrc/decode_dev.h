@@ -153,6 +153,60 @@ __device__ __forceinline__ void stage_finish(XStage<NG, NORM> &st, float *xs, fl
     __syncthreads();
 }
 
+// Staging for workgroups of any wave count: the first 256 threads load x (and
+// the norm weight w), store x (or x*w) to LDS and their per-wave partial sums of
+// x^2 to red[0..3]; one barrier; every wave then reads its fragment. With NORM
+// the rmsnorm's scalar 1/rms is returned instead of being applied to x, so the
+// caller multiplies its reduced dot products by it: rmsnorm(x)*w . W[r] =
+// (1/rms) * ((x*w) . W[r]). A scheduling barrier ends the staging, so the
+// compiler cannot hoist weight arithmetic (which waits for the weight loads)
+// above the LDS stores that other waves are waiting for at the barrier.
+template <int NG, bool NORM>
+__device__ __forceinline__ void stage_issue_first256(XStage<NG, NORM> &st, const float *x, const float *w,
+                                                     uint32_t cols) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        st.v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (NORM) st.w[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (t < (uint32_t)kBlock) stage_issue<NG, NORM>(st, x, w, cols);
+}
+
+template <int NG, bool NORM>
+__device__ __forceinline__ float stage_finish_first256(XStage<NG, NORM> &st, float *xs, float *red, uint32_t cols,
+                                                       float eps) {
+    const uint32_t t = threadIdx.x;
+    if (t < (uint32_t)kBlock) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            float4 v = st.v[j];
+            if (kGroupCols * j + 4u * t >= cols) v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (NORM) {
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+                v = make_float4(v.x * st.w[j].x, v.y * st.w[j].y, v.z * st.w[j].z, v.w * st.w[j].w);
+            }
+            *reinterpret_cast<float4 *>(xs + kGroupCols * j + 4u * t) = v;
+        }
+        if constexpr (NORM) {
+            ss = wave_sum_dpp(ss);
+            if ((t & 63u) == 0u) red[t >> 6] = ss;
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        const float total = (red[0] + red[1]) + (red[2] + red[3]);
+        return 1.0f / sqrtf(total / (float)cols + eps);  // rmsnorm.comp:36-38
+    } else {
+        return 1.f;
+    }
+}
+
 template <int WT, int NG>
 __device__ __forceinline__ void frag_from_lds(Frag<NG> &f, const float *xs, int lane) {
 #pragma unroll

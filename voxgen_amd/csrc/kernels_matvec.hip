@@ -79,21 +79,28 @@ __device__ __forceinline__ void epilogue(const MvArgs &a, uint32_t row, float ac
 // epilogue operands, so that vmcnt's in-order accounting lets the LDS staging of
 // x proceed while the weights are in flight. Rows past the end are clamped to a
 // valid row and their results dropped (no early exit: the staging has barriers).
-template <int WT, int NG, int RPW, int EP>
-__global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
+// WPB waves share one staging of x: the staging reads are per workgroup, and
+// under a full weight stream they compete with it for the L2 and the CU's load
+// path, so the large shapes use 8-wave workgroups (measured on MI355X: down
+// 5.28 -> 4.90 us, attn_out-shaped 3.03 -> 2.74 us against 4-wave groups).
+template <int WT, int NG, int RPW, int EP, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_matvec(MvArgs a) {
     __shared__ __align__(16) float xs[NG * kGroupCols];
     __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
-    const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
+    const uint32_t row0 = a.row_base + (blockIdx.x * WPB + wave) * RPW;
     // Only fusion_linear reads a concatenated x (compile-time, so the plain path
     // keeps its float4 loads).
     constexpr bool CONCAT = EP == EP_FUSION_F32 || EP == EP_FUSION_F16;
     XStage<NG, false> st;
-    if constexpr (CONCAT)
-        stage_issue_concat<NG>(st, a.xl, a.xr, a.left, a.cols);
-    else
-        stage_issue<NG, false>(st, a.xl, nullptr, a.cols);
+    if constexpr (CONCAT) {
+#pragma unroll
+        for (int j = 0; j < NG; ++j) st.v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (threadIdx.x < (unsigned)kBlock) stage_issue_concat<NG>(st, a.xl, a.xr, a.left, a.cols);
+    } else {
+        stage_issue_first256<NG, false>(st, a.xl, nullptr, a.cols);
+    }
     __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> r[RPW];
 #pragma unroll
@@ -102,7 +109,7 @@ __global__ __launch_bounds__(kBlock) void k_matvec(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < RPW; ++i) op[i] = epilogue_operand<EP>(a, min(row0 + i, a.rows - 1u));
     __builtin_amdgcn_sched_barrier(0);
-    stage_finish<NG, false>(st, xs, red, a.cols, 0.f);
+    stage_finish_first256<NG, false>(st, xs, red, a.cols, 0.f);
     Frag<NG> f;
     frag_from_lds<WT, NG>(f, xs, lane);
     FragSums<NG> sx;
@@ -131,13 +138,14 @@ struct AttnOutArgs {
     uint32_t context, splits;
 };
 
-template <int WT, int NG, int RPW, int HD, bool BRANCH>
-__global__ __launch_bounds__(kBlock) void k_attn_out(AttnOutArgs a) {
-    constexpr int E = 4 * NG;  // outputs merged per thread
+template <int WT, int NG, int RPW, int HD, bool BRANCH, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
+    constexpr int E = 16 * NG / WPB;  // outputs merged per thread (all 64*WPB threads merge)
+    static_assert(E >= 4 && E % 4 == 0, "merge works in float4 units");
     __shared__ __align__(16) float xs[NG * kGroupCols];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const MvArgs &m = a.mv;
-    const uint32_t row0 = (blockIdx.x * kWavesPerBlock + wave) * RPW;  // no early exit: barrier below
+    const uint32_t row0 = (blockIdx.x * WPB + wave) * RPW;  // no early exit: barrier below
     // Every split record of this thread's head is requested up front, whatever
     // the position (records past the active splits get weight 0 by a select), so
     // these loads do not wait for the position and go out ahead of the weights.
@@ -190,6 +198,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_out(AttnOutArgs a) {
         if (a.attn && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.attn + o0 + e) = v;
     }
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     Frag<NG> f;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
@@ -271,15 +280,17 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;  // matvec_swiglu.comp:67
 }
 
-template <int WT, int NG, int RPW, bool NORM>
-__global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
+// With the rmsnorm fused (ffn_norm), x*w is staged and 1/rms scales the two
+// reduced dot products: silu(g/rms) * (u/rms).
+template <int WT, int NG, int RPW, bool NORM, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_swiglu(SwArgs a) {
     __shared__ __align__(16) float xs[NG * kGroupCols];
     __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
-    const uint32_t row0 = a.row_base + (blockIdx.x * kWavesPerBlock + wave) * RPW;
+    const uint32_t row0 = a.row_base + (blockIdx.x * WPB + wave) * RPW;
     XStage<NG, NORM> st;
-    stage_issue<NG, NORM>(st, a.x, a.norm, a.cols);
+    stage_issue_first256<NG, NORM>(st, a.x, a.norm, a.cols);
     __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> rg[RPW], ru[RPW];
 #pragma unroll
@@ -289,7 +300,7 @@ __global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
         load_row(ru[i], a.u, row, a.cols, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
-    stage_finish<NG, NORM>(st, xs, red, a.cols, a.eps);
+    const float inv = stage_finish_first256<NG, NORM>(st, xs, red, a.cols, a.eps);
     Frag<NG> f;
     frag_from_lds<WT, NG>(f, xs, lane);
     FragSums<NG> sx;
@@ -297,8 +308,8 @@ __global__ __launch_bounds__(kBlock) void k_swiglu(SwArgs a) {
     float gs[RPW], us[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        gs[i] = wave_sum_dpp(row_dot(rg[i], f, sx));
-        us[i] = wave_sum_dpp(row_dot(ru[i], f, sx));
+        gs[i] = wave_sum_dpp(row_dot(rg[i], f, sx)) * inv;
+        us[i] = wave_sum_dpp(row_dot(ru[i], f, sx)) * inv;
     }
     if (lane == 0) {
 #pragma unroll
@@ -351,15 +362,15 @@ struct QkvArgs {
 // One wave per rotary pair: Q/K rows (i, i + head_dim/2) of a head, or two
 // adjacent V rows. RoPE (rope.comp:28-49) and the f16 cache store
 // (store_kv.comp:21-23) run on the reduced pair in lane 0.
-template <int WT, int NG>
-__global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
+template <int WT, int NG, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_qkv_fused(QkvArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
     __shared__ __align__(16) float xs[NG * kGroupCols];
     __shared__ float red[kWavesPerBlock];
     const uint32_t half_dim = a.head_dim >> 1;
     const uint32_t pq = a.q_rows >> 1, pk = a.kv_rows >> 1;
-    const uint32_t p_raw = blockIdx.x * kWavesPerBlock + wave;
+    const uint32_t p_raw = blockIdx.x * WPB + wave;
     const bool live = p_raw < pq + 2u * pk;  // no early exit: the staging has barriers
     const uint32_t p = live ? p_raw : pq + 2u * pk - 1u;
     int seg;
@@ -380,7 +391,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
     w.ptr = seg == 0 ? a.q.ptr : (seg == 1 ? a.k.ptr : a.v.ptr);
     w.d = seg == 0 ? a.q.d : (seg == 1 ? a.k.d : a.v.d);
     XStage<NG, true> st;
-    stage_issue<NG, true>(st, a.hidden, a.norm, a.cols);
+    stage_issue_first256<NG, true>(st, a.hidden, a.norm, a.cols);
     __builtin_amdgcn_sched_barrier(0);
     RowT<WT, NG> rr[2];
     load_row(rr[0], w, r0, a.cols, lane);
@@ -391,13 +402,13 @@ __global__ __launch_bounds__(kBlock) void k_qkv_fused(QkvArgs a) {
     const float ext = rotate && !a.rope_cs ? a.factors[pair] : 1.f;
     const float2 cs_tab = rotate && a.rope_cs ? a.rope_cs[pair] : make_float2(1.f, 0.f);
     __builtin_amdgcn_sched_barrier(0);
-    stage_finish<NG, true>(st, xs, red, a.cols, a.eps);
+    const float inv = stage_finish_first256<NG, true>(st, xs, red, a.cols, a.eps);
     Frag<NG> f;
     frag_from_lds<WT, NG>(f, xs, lane);
     FragSums<NG> sx;
     frag_sums(f, sx);
-    float v0 = wave_sum_dpp(row_dot(rr[0], f, sx));
-    float v1 = wave_sum_dpp(row_dot(rr[1], f, sx));
+    float v0 = wave_sum_dpp(row_dot(rr[0], f, sx)) * inv;
+    float v1 = wave_sum_dpp(row_dot(rr[1], f, sx)) * inv;
     if (lane != 0 || !live) return;
     if (rotate) {
         float c = cs_tab.x, s = cs_tab.y;
@@ -476,22 +487,22 @@ template <int WT, int EP>
 int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
     const uint32_t n = a.rows - a.row_base;
     const bool big = n > 8192u && ng <= 2u;
-#define VX_MV(NGV, RPWV)                                                                    \
-    do {                                                                                    \
-        const uint32_t per_block = kWavesPerBlock * (RPWV);                                \
-        k_matvec<WT, NGV, RPWV, EP><<<(n + per_block - 1) / per_block, kBlock, 0, s>>>(a);  \
+#define VX_MV(NGV, RPWV, WPBV)                                                                       \
+    do {                                                                                             \
+        const uint32_t per_block = (WPBV) * (RPWV);                                                  \
+        k_matvec<WT, NGV, RPWV, EP, WPBV><<<(n + per_block - 1) / per_block, 64 * (WPBV), 0, s>>>(a); \
     } while (0)
     switch (ng) {
         case 1:
-            if (big) VX_MV(1, 4); else VX_MV(1, 2);
+            if (big) VX_MV(1, 4, 4); else VX_MV(1, 2, 4);
             break;
         case 2:
-            if (big) VX_MV(2, 4); else VX_MV(2, 2);
+            if (big) VX_MV(2, 4, 4); else VX_MV(2, 1, 8);   // 2048 rows: 256 workgroups of 8 waves
             break;
-        case 3: VX_MV(3, 2); break;
-        case 4: VX_MV(4, 2); break;
-        case 6: VX_MV(6, 1); break;   // one row per wave: 512 workgroups for 2048 rows
-        default: VX_MV(8, 1); break;
+        case 3: VX_MV(3, 2, 4); break;
+        case 4: VX_MV(4, 2, 4); break;
+        case 6: VX_MV(6, 1, 8); break;   // one row per wave, 8 waves: 256 workgroups for 2048 rows
+        default: VX_MV(8, 1, 4); break;
     }
 #undef VX_MV
     VX_LAUNCHED("k_matvec");
@@ -573,22 +584,22 @@ int launch_swiglu(hipStream_t s, const SwigluLaunch &l) {
         VX_LAUNCHED("k_swiglu_generic");
         return VX_OK;
     }
-#define VX_SW(WTV, NGV, RPWV)                                                                           \
+#define VX_SW(WTV, NGV, RPWV, WPBV)                                                                     \
     do {                                                                                                \
-        const uint32_t grid = (n + kWavesPerBlock * (RPWV) - 1) / (kWavesPerBlock * (RPWV));            \
+        const uint32_t grid = (n + (WPBV) * (RPWV) - 1) / ((WPBV) * (RPWV));                           \
         if (l.norm)                                                                                     \
-            k_swiglu<WTV, NGV, RPWV, true><<<grid, kBlock, 0, s>>>(a);                                  \
+            k_swiglu<WTV, NGV, RPWV, true, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                       \
         else                                                                                            \
-            k_swiglu<WTV, NGV, RPWV, false><<<grid, kBlock, 0, s>>>(a);                                 \
+            k_swiglu<WTV, NGV, RPWV, false, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                      \
     } while (0)
-#define VX_SW_NG(WTV)                          \
-    switch (ng) {                              \
-        case 1: VX_SW(WTV, 1, 2); break;       \
-        case 2: VX_SW(WTV, 2, 1); break;       \
-        case 3: VX_SW(WTV, 3, 2); break;       \
-        case 4: VX_SW(WTV, 4, 2); break;       \
-        case 6: VX_SW(WTV, 6, 1); break;       \
-        default: VX_SW(WTV, 8, 1); break;      \
+#define VX_SW_NG(WTV)                             \
+    switch (ng) {                                 \
+        case 1: VX_SW(WTV, 1, 2, 4); break;       \
+        case 2: VX_SW(WTV, 2, 1, 8); break;       \
+        case 3: VX_SW(WTV, 3, 2, 4); break;       \
+        case 4: VX_SW(WTV, 4, 2, 4); break;       \
+        case 6: VX_SW(WTV, 6, 1, 4); break;       \
+        default: VX_SW(WTV, 8, 1, 4); break;      \
     }
     if (l.g.wt == WT_Q8) {
         VX_SW_NG(WT_Q8)
@@ -614,8 +625,10 @@ int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &l) {
               l.cols,   l.head_dim, l.factors, l.theta,   l.scaling, l.layer, l.context, l.qo,
               l.ko,     l.vo,       l.kc,      l.vc,      l.position, l.rope_cs, l.no_rope ? 1u : 0u};
     const uint32_t pairs = (l.q_rows + 2u * l.kv_rows) / 2u;
-    const uint32_t grid = (pairs + kWavesPerBlock - 1) / kWavesPerBlock;
-#define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV><<<grid, kBlock, 0, s>>>(a)
+    // 8-wave workgroups (one staging of x per 8 rotary pairs).
+    constexpr uint32_t WPB = 8;
+    const uint32_t grid = (pairs + WPB - 1) / WPB;
+#define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV, WPB><<<grid, 64 * WPB, 0, s>>>(a)
 #define VX_QKV_NG(WTV)                      \
     switch (ng) {                           \
         case 1: VX_QKV(WTV, 1); break;      \
@@ -656,20 +669,20 @@ int launch_attn_out(hipStream_t s, const AttnOutLaunch &l) {
     a.position = l.position;
     a.context = l.context;
     a.splits = l.splits;
-    constexpr uint32_t RPW = 2;
-    const uint32_t grid = (l.mv.rows + kWavesPerBlock * RPW - 1) / (kWavesPerBlock * RPW);
-#define VX_AO(WTV, NGV, HDV)                                                                   \
-    do {                                                                                       \
-        if (l.mv.y2)                                                                           \
-            k_attn_out<WTV, NGV, RPW, HDV, true><<<grid, kBlock, 0, s>>>(a);                  \
-        else                                                                                   \
-            k_attn_out<WTV, NGV, RPW, HDV, false><<<grid, kBlock, 0, s>>>(a);                 \
+    // 2048 columns: 8 waves of one row (256 workgroups for 2048 rows); 1024: 4 waves of two.
+#define VX_AO(WTV, NGV, HDV, RPWV, WPBV)                                                                   \
+    do {                                                                                                   \
+        const uint32_t grid = (l.mv.rows + (WPBV) * (RPWV) - 1) / ((WPBV) * (RPWV));                      \
+        if (l.mv.y2)                                                                                       \
+            k_attn_out<WTV, NGV, RPWV, HDV, true, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                 \
+        else                                                                                               \
+            k_attn_out<WTV, NGV, RPWV, HDV, false, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                \
     } while (0)
-#define VX_AO_WT(WTV)                                          \
-    if (ng == 2u) {                                            \
-        if (l.head_dim == 128u) VX_AO(WTV, 2, 128); else VX_AO(WTV, 2, 64); \
-    } else {                                                   \
-        if (l.head_dim == 128u) VX_AO(WTV, 1, 128); else VX_AO(WTV, 1, 64); \
+#define VX_AO_WT(WTV)                                                                \
+    if (ng == 2u) {                                                                  \
+        if (l.head_dim == 128u) VX_AO(WTV, 2, 128, 1, 8); else VX_AO(WTV, 2, 64, 1, 8); \
+    } else {                                                                         \
+        if (l.head_dim == 128u) VX_AO(WTV, 1, 128, 2, 4); else VX_AO(WTV, 1, 64, 2, 4); \
     }
     if (l.mv.w.wt == WT_Q8) {
         VX_AO_WT(WT_Q8)
