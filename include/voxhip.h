@@ -270,7 +270,9 @@ typedef struct vx_tensor_info {     /* TensorInfo gguf.rs:51-59 */
     char name[96];
     uint32_t ggml_type;             /* VX_DTYPE_* */
     uint32_t n_dims;
-    uint64_t dims[4];               /* GGUF order: dims[0] is the contiguous axis */
+    uint64_t dims[4];               /* GGUF order: dims[0] is the contiguous axis; a GGUF
+                                       tensor of rank 5..8 is listed with n_dims 4 and its
+                                       dims 3.. folded into dims[3] */
     uint64_t offset;                /* byte offset into the data region */
     uint64_t bytes;
 } vx_tensor_info;
@@ -278,7 +280,10 @@ typedef struct vx_tensor_info {     /* TensorInfo gguf.rs:51-59 */
 /* Upload `bytes` of GGUF data region plus its tensor table. Rank-2 Q8_0 tensors
  * are additionally repacked on the device into the coalesced layout the matvec
  * and GEMM kernels read; the original bytes stay resident for bit-exact gathers.
- * Fails with VX_ERR_OFFSET if the region is >= 4 GiB (u32 push offsets). */
+ * Fails with VX_ERR_OFFSET if the region is >= 4 GiB (u32 push offsets). The
+ * tensor table is validated first, with checked size arithmetic (element counts,
+ * byte sizes and extents that overflow are VX_ERR_GGUF or VX_ERR_SHAPE), before
+ * the context is used or any device memory is touched. */
 int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes,
                     const vx_tensor_info *tensors, uint32_t n_tensors, vx_model **out);
 int vx_model_free(vx_ctx *ctx, vx_model *model);

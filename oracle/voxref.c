@@ -682,7 +682,12 @@ void vr_cfm_noise(float *x, const vx_cfm_noise_push *pc) {
 }
 
 /* cfm_cfg_euler.comp:15-36: 256-lane tree reduction of <p,n> and |n|^2, then
- * x -= dt * (n*s + cfg*(p - n*s)) with s the CFG-Zero* scale (or 1). */
+ * x -= dt * (n*s + cfg*(p - n*s)) with s the CFG-Zero* scale (or 1).
+ * For n <= 256 this is the shader exactly (one element per lane). The strided
+ * loop for n > 256 is NOT the reference's behaviour (its single workgroup only
+ * covers x[0..256)): it restates the engine solve's generalisation for latent
+ * sizes above 256, which only non-reference geometries have; the per-op entry
+ * point refuses n > 256. */
 void vr_cfm_cfg_euler(float *x, const float *pos, const float *neg, const vx_cfm_euler_push *pc) {
     float dot[256], nrm[256];
     for (uint32_t i = 0; i < 256u; ++i) {

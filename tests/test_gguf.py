@@ -3,6 +3,7 @@
 Files are written by voxgen_amd.gguf; full-geometry models use a sparse data
 region so the 28-layer table can be validated without 1.7 GB of disk.
 """
+import ctypes as C
 import struct
 
 import numpy as np
@@ -135,7 +136,8 @@ def test_rope_original_context_and_long_factor_scaling(tmp_path):
 
 
 @pytest.mark.parametrize("how", ["magic", "version1", "version4", "truncated_header", "tensor_past_eof",
-                                 "bad_type", "rank0", "q8_not_div32"])
+                                 "bad_type", "rank0", "q8_not_div32", "f32_size_overflow",
+                                 "q8_size_overflow", "offset_overflow"])
 def test_parse_errors(tmp_path, how):
     cfg = synth.baselm_config(layers=1, hidden=256, ffn=512, vocab=64, q_heads=2, kv_heads=1)
     m = synth.build_baselm(cfg, seed=1)
@@ -151,6 +153,19 @@ def test_parse_errors(tmp_path, how):
     if how == "q8_not_div32":
         t = tensors[-1]
         tensors[-1] = synth.TensorDesc(t.name, 8, (40, 2), t.offset, 102)
+    # Sizes that wrap 64 bits (gguf.rs:37-48 checked_mul): 2^62 f32 elements are
+    # 2^64 bytes, and 1024 x 16954728008924221 Q8_0 weights are 34/32 of a count
+    # that fits 64 bits but whose byte size does not.
+    if how == "f32_size_overflow":
+        t = tensors[-1]
+        tensors[-1] = synth.TensorDesc(t.name, 0, (1 << 62, 1), t.offset, 1)
+    if how == "q8_size_overflow":
+        t = tensors[-1]
+        tensors[-1] = synth.TensorDesc(t.name, 8, (1024, 16954728008924221), t.offset, 1)
+    # data_offset + offset + bytes wraps (gguf.rs:281 checked_add).
+    if how == "offset_overflow":
+        t = tensors[-1]
+        tensors[-1] = synth.TensorDesc(t.name, t.ggml_type, t.dims, (1 << 64) - 64, t.nbytes)
     p = gguf.write(tmp_path / "e.gguf", m.metadata, tensors, data, version=version)
     raw = bytearray(p.read_bytes())
     if how == "magic":
@@ -326,3 +341,77 @@ def test_audiovae_config_errors(tmp_path, case, code):
     with pytest.raises(abi.VxError) as e:
         Gguf(vae_file(tmp_path, **kw)).audiovae_config()
     assert e.value.name == code
+
+
+@pytest.mark.parametrize("dims,ty,code", [
+    ((1 << 62, 1), 0, "VX_ERR_GGUF"),                   # f32 byte size wraps
+    ((1024, 16954728008924221), 8, "VX_ERR_GGUF"),      # Q8_0 byte size wraps
+    ((1 << 33, 1 << 32), 1, "VX_ERR_GGUF"),             # element count wraps
+])
+def test_model_upload_refuses_overflowing_tables_before_device_work(dims, ty, code):
+    """The upload validates its tensor table with checked arithmetic before it uses
+    the context, so these tables are refused here without a GPU (a null context)."""
+    data = np.zeros(4096, dtype=np.uint8)
+    arr = (abi.TensorInfo * 1)(synth.TensorDesc("w", ty, dims, 0, 1).to_c())
+    h = abi.MODEL()
+    with pytest.raises(abi.VxError) as e:
+        abi.call("vx_model_upload", None, data.ctypes.data_as(C.c_void_p), data.nbytes, arr, 1, C.byref(h))
+    assert e.value.name == code
+
+
+# ------------------------------------- parse rules shared with gguf.rs / baselm.rs
+def test_invalid_utf8_string_is_refused(tmp_path):
+    """gguf.rs:182 reads strings with std::str::from_utf8: a metadata key or value
+    that is not UTF-8 fails the load."""
+    p = full_model(tmp_path)
+    raw = bytearray(p.read_bytes())
+    i = raw.find(b"general.architecture")
+    assert i > 0
+    raw[i + 3] = 0xFF  # a lone continuation-less byte
+    p.write_bytes(bytes(raw))
+    with pytest.raises(abi.VxError) as e:
+        Gguf(p)
+    assert e.value.name == "VX_ERR_GGUF"
+
+
+def test_rank_up_to_8_is_accepted(tmp_path):
+    """gguf.rs:253-256 accepts n_dims <= 8; an unused rank-6 tensor does not stop
+    the model from loading, and is listed with its upper dims folded into dims[3]."""
+    extra = synth.TensorDesc("unused.rank6", 0, (2, 3, 4, 5, 6, 7), 0)
+    cfg = synth.baselm_config(context_length=32768)
+    m = synth.build_baselm(cfg, with_data=False)
+    tensors = list(m.tensors) + [extra]
+    size = max(t.offset + t.nbytes for t in tensors)
+    p = gguf.write(tmp_path / "r.gguf", m.metadata, tensors, None, data_bytes=size)
+    g = Gguf(p)
+    t = {x.name: x for x in g.tensors()}["unused.rank6"]
+    assert t.dims == (2, 3, 4, 5 * 6 * 7)
+    assert g.baselm_config(4096)["block_count"] == 28
+
+
+@pytest.mark.parametrize("text,ok", [("28", True), ("+28", True), (" 28", False), ("28 ", False),
+                                     ("0x1c", False), ("-28", False), ("2.8e1", False), ("", False)])
+def test_string_metadata_parses_like_rust_u32(tmp_path, text, ok):
+    """baselm.rs:275 parses metadata text with str::parse::<u32>: digits with an
+    optional '+', nothing else. A value that does not parse counts as missing."""
+    p = full_model(tmp_path, meta_over={"minicpm4.block_count": (8, text)})
+    if ok:
+        assert Gguf(p).baselm_config(4096)["block_count"] == 28
+    else:
+        with pytest.raises(abi.VxError) as e:
+            Gguf(p).baselm_config(4096)
+        assert e.value.name == "VX_ERR_NOT_FOUND"  # "missing required metadata"
+
+
+@pytest.mark.parametrize("text,want", [("1e-6", 1e-6), ("+1e-6", 1e-6), ("0.000001", 1e-6),
+                                       (" 1e-6", None), ("0x1p-20", None), ("1e-6\n", None)])
+def test_string_metadata_parses_like_rust_f32(tmp_path, text, want):
+    """baselm.rs:281 parses metadata text with str::parse::<f32>: no surrounding
+    whitespace and no hexadecimal floats (which strtof alone would accept)."""
+    p = full_model(tmp_path, meta_over={"minicpm4.attention.layer_norm_rms_epsilon": (8, text)})
+    if want is not None:
+        assert Gguf(p).baselm_config(4096)["rms_epsilon"] == pytest.approx(want)
+    else:
+        with pytest.raises(abi.VxError) as e:
+            Gguf(p).baselm_config(4096)
+        assert e.value.name == "VX_ERR_NOT_FOUND"  # "missing required metadata"

@@ -142,6 +142,12 @@ def test_cfm_shader_entry_points(ctx):
     ep = abi.CfmEulerPush(n, 0.1, 2.0, 1)
     abi.call("vx_cfm_cfg_euler", ctx.handle, xb2.handle, pb.handle, qb.handle, C.byref(ep))
     assert rel_l2(xb2.download(np.float32, n), voxref.cfm_cfg_euler(x, p, q, ep)) < 1e-6
+    # The shader is one 256-lane workgroup: the entry point refuses a longer latent.
+    big = ctx.zeros(257 * 4)
+    with pytest.raises(abi.VxError) as e:
+        abi.call("vx_cfm_cfg_euler", ctx.handle, big.handle, big.handle, big.handle,
+                 C.byref(abi.CfmEulerPush(257, 0.1, 2.0, 1)))
+    assert e.value.name == "VX_ERR_UNSUPPORTED"
     tb = ctx.zeros(1024 * 4)
     tp = abi.TimePush(1024, 0.42)
     abi.call("vx_time_sinusoidal", ctx.handle, tb.handle, C.byref(tp))

@@ -110,6 +110,12 @@ def test_decode_errors(ctx):
     with pytest.raises(abi.VxError) as e:
         eng.decode_latents_gpu(ctx.array(lat), 4, ctx.alloc(1024))
     assert e.value.name == "VX_ERR_BOUNDS"
+    # A frame count whose activations pass the 32-bit index range is refused by
+    # the device-buffer entry as by the host one, before any buffer check or launch.
+    patch = cfg["patch_size"]
+    with pytest.raises(abi.VxError) as e:
+        eng.decode_latents_gpu(ctx.array(lat), (0xFFFFFFFF // patch) * patch, ctx.alloc(1024))
+    assert e.value.name == "VX_ERR_UNSUPPORTED"
     with pytest.raises(abi.VxError) as e:
         AudioVaeEngine(ctx, model, cfg, strict_geometry=True)
     assert e.value.name == "VX_ERR_UNSUPPORTED"

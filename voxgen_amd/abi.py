@@ -376,11 +376,14 @@ _LIB = None
 
 
 def load(path: str | os.PathLike | None = None) -> C.CDLL:
-    """Load libvoxhip.so (once). Raises if the library has not been built."""
+    """Load libvoxhip.so (once). Raises if the library has not been built.
+
+    VOXHIP_LIBRARY, when set, names another build of the same library to load
+    (the sanitizer build the CPU tests run under)."""
     global _LIB
     if _LIB is not None:
         return _LIB
-    p = Path(path) if path else LIB_PATH
+    p = Path(path) if path else Path(os.environ.get("VOXHIP_LIBRARY") or LIB_PATH)
     if not p.exists():
         raise ImportError(f"{p} is missing: build it with `python voxgen_amd/build.py` "
                           "(or __graft_entry__.build()) before using voxgen_amd")

@@ -48,26 +48,50 @@ FILE_FLAGS = {
 }
 
 
-def _compile(src: Path) -> Path:
-    OBJ.mkdir(parents=True, exist_ok=True)
-    obj = OBJ / (src.name + ".o")
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build, for the CPU
+# tests of the host code (GGUF parsing, argument checks). Each sanitizer flag is
+# scoped to the host pass with -Xarch_host; the device code is built as usual.
+SANITIZE_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                 "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+                 "-Xarch_host", "-shared-libasan"]
+ASAN_DIR = ROOT / "_build" / "asan"
+
+
+def _compile(src: Path, sanitize: bool = False) -> Path:
+    odir = ASAN_DIR / "obj" if sanitize else OBJ
+    odir.mkdir(parents=True, exist_ok=True)
+    obj = odir / (src.name + ".o")
     # hipcc treats .cpp as HIP source too; both get the gfx950 device flags.
-    cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), *(SANITIZE_HOST if sanitize else []),
+           "-c", str(src), "-o", str(obj)]
     _run(cmd)
     return obj
 
 
-def build_voxhip(jobs: int | None = None) -> Path:
+def build_voxhip(jobs: int | None = None, sanitize: bool = False) -> Path:
+    """Build libvoxhip.so in the package, or with sanitize=True the host-sanitized
+    variant at _build/asan/libvoxhip.so (load it with VOXHIP_LIBRARY and the ASan
+    runtime preloaded)."""
     sources = sorted(CSRC.glob("*.hip")) + sorted(
         p for p in CSRC.glob("*.cpp"))
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    out = PKG / "libvoxhip.so"
-    tmp = PKG / "libvoxhip.so.tmp"
-    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)])
+        objs = list(ex.map(lambda src: _compile(src, sanitize), sources))
+    out = (ASAN_DIR if sanitize else PKG) / "libvoxhip.so"
+    tmp = out.with_name("libvoxhip.so.tmp")
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *(SANITIZE_HOST if sanitize else []),
+          "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, out)
     return out
+
+
+def asan_runtime() -> str:
+    """Path of the clang ASan runtime that a sanitized build needs preloaded."""
+    clang = Path(HIPCC).resolve().parent.parent / "lib" / "llvm" / "bin" / "clang"
+    if not clang.exists():
+        clang = Path(shutil.which("clang") or "/opt/rocm/lib/llvm/bin/clang")
+    return subprocess.run([str(clang), "-print-file-name=libclang_rt.asan-x86_64.so"], check=True,
+                          stdout=subprocess.PIPE, text=True).stdout.strip()
 
 
 def build_synth() -> Path:

@@ -180,6 +180,9 @@ int enqueue_decode(vx_audiovae *e, const float *in, uint32_t frames, float *wave
     const vx_audiovae_config &c = e->cfg;
     uint64_t x2_max = 0;
     const uint64_t act = decoder_max_elements(c, frames, &x2_max);
+    // Every stage indexes its activations (and the output length) in 32 bits.
+    if (act > 0xffffffffull || x2_max > 0xffffffffull)
+        return fail(VX_ERR_UNSUPPORTED, "AudioVAE decoder activation exceeds the 32-bit index range");
     VX_CHECK(grow(ctx, &e->cur, &e->act_cap, act));
     VX_CHECK(grow(ctx, &e->tmp, &e->tmp_cap, act));
     VX_CHECK(grow(ctx, &e->x2, &e->x2_cap, x2_max));
@@ -392,6 +395,9 @@ int vx_audiovae_decode_latents_gpu(vx_audiovae *e, const vx_buf *frame_major, ui
     if (frames == 0 || frames % c.patch_size)
         return fail(VX_ERR_SHAPE, "VoxCPM2 AudioVAE decode expects latent frames in groups of %u, got %u",
                     c.patch_size, frames);
+    uint64_t x2_max = 0;
+    if (decoder_max_elements(c, frames, &x2_max) > 0xffffffffull || x2_max > 0xffffffffull)
+        return fail(VX_ERR_UNSUPPORTED, "AudioVAE decoder activation exceeds the 32-bit index range");
     VX_CHECK(need_buf(frame_major, (uint64_t)frames * c.latent_dim * 4u, "AudioVAE latents"));
     VX_CHECK(need_buf(wave, (uint64_t)frames * c.decoder_hop * 4u, "AudioVAE wave"));
     return enqueue_decode(e, static_cast<const float *>(frame_major->ptr), frames, F(wave));
@@ -411,7 +417,8 @@ int vx_audiovae_decode_latents(vx_audiovae *e, const float *frame_major, uint64_
         return fail(VX_ERR_SHAPE, "VoxCPM2 AudioVAE decode expects latent frames in groups of %u, got %llu",
                     c.patch_size, (unsigned long long)frames);
     uint64_t x2_max = 0;
-    if (decoder_max_elements(c, frames, &x2_max) > 0xffffffffull || x2_max > 0xffffffffull)
+    if (frames > 0xffffffffull || decoder_max_elements(c, frames, &x2_max) > 0xffffffffull ||
+        x2_max > 0xffffffffull)
         return fail(VX_ERR_UNSUPPORTED, "AudioVAE decoder activation exceeds the 32-bit index range");
     const uint64_t samples = frames * c.decoder_hop;
     if (!wave || wave_cap < samples)

@@ -59,7 +59,38 @@ struct Reader {
     std::string str() {
         const uint64_t len = get<uint64_t>();
         const uint8_t *b = take(len);
-        return b ? std::string(reinterpret_cast<const char *>(b), len) : std::string();
+        if (!b) return std::string();
+        if (!valid_utf8(b, len)) {  // gguf.rs:182 (std::str::from_utf8)
+            ok = false;
+            err = "invalid UTF-8 in GGUF string";
+            return std::string();
+        }
+        return std::string(reinterpret_cast<const char *>(b), len);
+    }
+    // Well-formed UTF-8 as Rust's from_utf8 checks it: no overlong forms, no
+    // surrogates, nothing above U+10FFFF.
+    static bool valid_utf8(const uint8_t *s, uint64_t n) {
+        uint64_t i = 0;
+        while (i < n) {
+            const uint8_t c = s[i];
+            if (c < 0x80) { ++i; continue; }
+            uint32_t need, cp;
+            if (c >= 0xC2 && c <= 0xDF) { need = 1; cp = c & 0x1Fu; }
+            else if (c >= 0xE0 && c <= 0xEF) { need = 2; cp = c & 0x0Fu; }
+            else if (c >= 0xF0 && c <= 0xF4) { need = 3; cp = c & 0x07u; }
+            else return false;
+            if (need > n - i - 1) return false;
+            for (uint32_t k = 1; k <= need; ++k) {
+                const uint8_t d = s[i + k];
+                if ((d & 0xC0u) != 0x80u) return false;
+                cp = (cp << 6) | (d & 0x3Fu);
+            }
+            if ((need == 2 && (cp < 0x800 || (cp >= 0xD800 && cp <= 0xDFFF))) ||
+                (need == 3 && (cp < 0x10000 || cp > 0x10FFFF)))
+                return false;
+            i += need + 1;
+        }
+        return true;
     }
 };
 
@@ -101,19 +132,29 @@ bool read_value(Reader &r, uint32_t ty, int depth, MetaValue &out, std::vector<s
     return r.ok;
 }
 
+// Byte size of a tensor, with the multiplications checked (gguf.rs:37-48 uses
+// checked_mul and fails on overflow).
 bool storage_bytes(uint32_t type, uint64_t elements, uint64_t *out, std::string *err) {
+    uint64_t units = elements, per = 0;
     switch (type) {  // GgmlType::storage_bytes gguf.rs:37-48
-        case 0: *out = elements * 4u; return true;
-        case 1: *out = elements * 2u; return true;
+        case 0: per = 4u; break;
+        case 1: per = 2u; break;
         case 8:
             if (elements % 32u) {
                 *err = "Q8_0 tensor has " + std::to_string(elements) + " elements, not divisible by 32";
                 return false;
             }
-            *out = elements / 32u * 34u;
-            return true;
+            units = elements / 32u;
+            per = 34u;
+            break;
         default: *err = "unsupported GGML tensor type " + std::to_string(type); return false;
     }
+    if (units > UINT64_MAX / per) {
+        *err = "tensor size overflow";
+        return false;
+    }
+    *out = units * per;
+    return true;
 }
 
 }  // namespace
@@ -143,13 +184,23 @@ bool meta_u32(const vx_gguf *g, std::initializer_list<const char *> keys, uint32
             *out = (uint32_t)v.f;
             return true;
         }
-        if (v.kind == META_STRING && !v.s.empty()) {
-            char *end = nullptr;
-            errno = 0;
-            const unsigned long long x = strtoull(v.s.c_str(), &end, 10);
-            if (errno == 0 && *end == '\0' && v.s[0] != '-' && v.s[0] != '+' && x <= 0xffffffffull) {
-                *out = (uint32_t)x;
-                return true;
+        if (v.kind == META_STRING) {
+            // str::parse::<u32> (baselm.rs:275): an optional '+', then decimal
+            // digits only; no whitespace, no other sign, no base prefix.
+            const std::string &t = v.s;
+            size_t i = !t.empty() && t[0] == '+' ? 1u : 0u;
+            if (i < t.size()) {
+                uint64_t x = 0;
+                bool good = true;
+                for (; i < t.size() && good; ++i) {
+                    if (t[i] < '0' || t[i] > '9') good = false;
+                    else x = x * 10u + (uint64_t)(t[i] - '0');
+                    if (x > 0xffffffffull) good = false;
+                }
+                if (good) {
+                    *out = (uint32_t)x;
+                    return true;
+                }
             }
         }
     }
@@ -166,9 +217,14 @@ bool meta_f32(const vx_gguf *g, std::initializer_list<const char *> keys, float 
         if (v.kind == META_INT) { *out = (float)v.i; return true; }
         if (v.kind == META_FLOAT) { *out = (float)v.f; return true; }
         if (v.kind == META_STRING && !v.s.empty()) {
+            // str::parse::<f32> (baselm.rs:281): decimal or exponent forms and
+            // inf/infinity/nan, no surrounding whitespace, no hexadecimal forms,
+            // which strtof would also take.
+            const std::string &t = v.s;
+            const bool plain = t.find_first_of(" \t\n\r\v\fxXpP()") == std::string::npos;
             char *end = nullptr;
-            const float x = strtof(v.s.c_str(), &end);
-            if (*end == '\0') { *out = x; return true; }
+            const float x = plain ? strtof(t.c_str(), &end) : 0.f;
+            if (plain && end && *end == '\0') { *out = x; return true; }
         }
     }
     return false;
@@ -311,11 +367,18 @@ int vx_gguf_open(const char *path, vx_gguf **out) {
         t.ggml_type = r.get<uint32_t>();
         t.offset = r.get<uint64_t>();
         if (!r.ok) break;
-        if (n_dims > 4) return bail(VX_ERR_UNSUPPORTED, "tensor " + name + " has rank > 4");
         if (name.size() >= sizeof(t.name)) return bail(VX_ERR_UNSUPPORTED, "tensor name too long: " + name);
         snprintf(t.name, sizeof(t.name), "%s", name.c_str());
-        t.n_dims = n_dims;
-        for (uint32_t d = 0; d < n_dims; ++d) t.dims[d] = dims[d];
+        // Ranks up to 8 are read as gguf.rs:253-256 reads them. The table keeps four
+        // dims: a rank 5..8 tensor is listed with its dims 3.. folded into dims[3]
+        // (same element count and memory order). No engine reads such a tensor.
+        t.n_dims = n_dims < 4u ? n_dims : 4u;
+        for (uint32_t d = 0; d < t.n_dims; ++d) t.dims[d] = dims[d];
+        for (uint32_t d = 4; d < n_dims; ++d) {
+            if (dims[d] && t.dims[3] > UINT64_MAX / dims[d])
+                return bail(VX_ERR_GGUF, "element-count overflow for " + name);
+            t.dims[3] *= dims[d];
+        }
         std::string err;
         if (!storage_bytes(t.ggml_type, elements, &t.bytes, &err)) return bail(VX_ERR_GGUF, "tensor " + name + ": " + err);
         g->summary.tensor_bytes += t.bytes;
@@ -324,8 +387,8 @@ int vx_gguf_open(const char *path, vx_gguf **out) {
     if (!r.ok) return bail(VX_ERR_GGUF, r.err);
     const uint64_t data_offset = (r.pos + alignment - 1) / alignment * alignment;  // gguf.rs:278-279
     for (const vx_tensor_info &t : g->tensors) {
-        const uint64_t end = data_offset + t.offset + t.bytes;
-        if (end < data_offset || end > size)
+        // data_offset + offset + bytes <= size, without wrapping (gguf.rs:281 checked_add).
+        if (data_offset > size || t.offset > size - data_offset || t.bytes > size - data_offset - t.offset)
             return bail(VX_ERR_GGUF, std::string("tensor ") + t.name + " extends beyond end of " + path);
     }
     g->summary.version = version;

@@ -674,6 +674,11 @@ int vx_cfm_noise(vx_ctx *ctx, vx_buf *x, const vx_cfm_noise_push *pc) {
 int vx_cfm_cfg_euler(vx_ctx *ctx, vx_buf *x, const vx_buf *positive, const vx_buf *negative,
                      const vx_cfm_euler_push *pc) {
     if (!ctx || !pc) return fail(VX_ERR_INVALID_ARG, "vx_cfm_cfg_euler: null argument");
+    // cfm_cfg_euler.comp runs one 256-lane workgroup: it reduces over and updates
+    // x[0..256) only. Larger n would have another meaning here, so it is refused.
+    if (pc->n > 256u)
+        return fail(VX_ERR_UNSUPPORTED, "vx_cfm_cfg_euler: n = %u, but cfm_cfg_euler.comp covers at most 256 "
+                    "elements (one 256-lane workgroup)", pc->n);
     VX_CHECK(need_buf(x, (uint64_t)pc->n * 4u, "vx_cfm_cfg_euler x"));
     VX_CHECK(need_buf(positive, (uint64_t)pc->n * 4u, "vx_cfm_cfg_euler positive"));
     VX_CHECK(need_buf(negative, (uint64_t)pc->n * 4u, "vx_cfm_cfg_euler negative"));

@@ -13,16 +13,34 @@
 
 namespace vx {
 
+// GgmlType::storage_bytes (gguf.rs:37-48), checked: *ok is false for an unknown
+// type, a Q8_0 count not divisible by 32, or a size that does not fit 64 bits.
 static uint64_t ggml_bytes(uint32_t type, uint64_t elements, bool *ok) {
     *ok = true;
-    switch (type) {  // GgmlType::storage_bytes (gguf.rs:37-48)
-        case VX_DTYPE_F32: return elements * 4u;
-        case VX_DTYPE_F16: return elements * 2u;
+    uint64_t units = elements, per = 0;
+    switch (type) {
+        case VX_DTYPE_F32: per = 4u; break;
+        case VX_DTYPE_F16: per = 2u; break;
         case VX_DTYPE_Q8_0:
             if (elements % 32u) { *ok = false; return 0; }
-            return elements / 32u * 34u;
+            units = elements / 32u;
+            per = 34u;
+            break;
         default: *ok = false; return 0;
     }
+    if (units > UINT64_MAX / per) { *ok = false; return 0; }
+    return units * per;
+}
+
+// Element count of a tensor's dims, false on overflow.
+static bool element_count(const vx_tensor_info &t, uint64_t *out) {
+    uint64_t elems = 1;
+    for (uint32_t k = 0; k < t.n_dims; ++k) {
+        if (t.dims[k] && elems > UINT64_MAX / t.dims[k]) return false;
+        elems *= t.dims[k];
+    }
+    *out = elems;
+    return true;
 }
 
 int find_tensor_at(const vx_model *m, uint32_t offset, const vx_tensor_info **out) {
@@ -100,9 +118,11 @@ using namespace vx;
 
 extern "C" {
 
+// The tensor table is validated before the context is used, so a bad table is
+// refused without any device work (and is reported even without a context).
 int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes, const vx_tensor_info *tensors,
                     uint32_t n_tensors, vx_model **out) {
-    if (!ctx || !data || !out || (!tensors && n_tensors))
+    if (!data || !out || (!tensors && n_tensors))
         return fail(VX_ERR_INVALID_ARG, "vx_model_upload: null argument");
     *out = nullptr;
     if (bytes == 0) return fail(VX_ERR_INVALID_ARG, "vx_model_upload: empty data region");
@@ -117,16 +137,23 @@ int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes, const vx_tens
         if (t.n_dims == 0 || t.n_dims > 4)
             return fail(VX_ERR_GGUF, "tensor %u has rank %u", i, t.n_dims);
         uint64_t elems = 1;
-        for (uint32_t k = 0; k < t.n_dims; ++k) elems *= t.dims[k];
+        if (!element_count(t, &elems)) return fail(VX_ERR_GGUF, "tensor %.96s: element-count overflow", t.name);
         bool ok = true;
         uint64_t tb = ggml_bytes(t.ggml_type, elems, &ok);
-        if (!ok)
+        if (!ok) {
+            if (t.ggml_type == VX_DTYPE_F32 || t.ggml_type == VX_DTYPE_F16 ||
+                (t.ggml_type == VX_DTYPE_Q8_0 && elems % 32u == 0))
+                return fail(VX_ERR_GGUF, "tensor %.96s: tensor size overflow", t.name);
             return fail(VX_ERR_UNSUPPORTED, "tensor %.96s: unsupported type %u or size", t.name,
                         t.ggml_type);
+        }
         if (t.offset > bytes || tb > bytes - t.offset)
             return fail(VX_ERR_GGUF, "tensor %.96s extends beyond the data region", t.name);
         if (t.ggml_type == VX_DTYPE_Q8_0 && t.n_dims == 2) {
             uint64_t rows = t.dims[1], cols = t.dims[0];
+            if (rows > UINT32_MAX || cols > UINT32_MAX)  // the repack kernel takes 32-bit extents
+                return fail(VX_ERR_SHAPE, "Q8_0 matrix %.96s is [%llu, %llu], beyond 32-bit extents", t.name,
+                            (unsigned long long)cols, (unsigned long long)rows);
             if (cols % 32u)
                 return fail(VX_ERR_SHAPE, "Q8_0 matrix %.96s has row width %llu, not divisible by 32",
                             t.name, (unsigned long long)cols);
@@ -139,6 +166,7 @@ int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes, const vx_tens
             packed_total += (rows * (cols / 32u) * 2u + 255u) & ~255ull;
         }
     }
+    if (!ctx) return fail(VX_ERR_INVALID_ARG, "vx_model_upload: null context");
     VX_HIP(hipSetDevice(ctx->device));
     vx_model *m = new vx_model();
     m->ctx = ctx;
@@ -173,7 +201,7 @@ int vx_model_upload(vx_ctx *ctx, const void *data, uint64_t bytes, const vx_tens
     for (uint32_t i = 0; i < n_tensors; ++i) {
         m->tensors[i].name[sizeof(m->tensors[i].name) - 1] = '\0';
         uint64_t elems = 1;
-        for (uint32_t k = 0; k < m->tensors[i].n_dims; ++k) elems *= m->tensors[i].dims[k];
+        (void)element_count(m->tensors[i], &elems);  // validated above
         bool ok = true;
         m->tensors[i].bytes = ggml_bytes(m->tensors[i].ggml_type, elems, &ok);
         m->by_offset.emplace(m->tensors[i].offset, i);  // first tensor at an offset wins
