@@ -430,6 +430,21 @@ int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, cons
                        vx_buf *out, vx_buf *scratch, const vx_buf *position,
                        const vx_fused_attn_args *a);
 
+/* Bytes of device scratch each GPU holds (from vx_init until the process ends)
+ * for the entry points that allocate nothing. */
+#define VX_NOALLOC_SCRATCH_BYTES (2u * 1024u * 1024u)
+/* vx_fused_attention without the scratch argument, for callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. It has no counterpart in the reference. It calls no
+ * hipMalloc, hipFree, hipMemset or other allocating routine: the partials go to
+ * a fixed per-GPU scratch of VX_NOALLOC_SCRATCH_BYTES, so a call needing more
+ * than that (vx_fused_attention_scratch_bytes(a)) fails with VX_ERR_BOUNDS.
+ * Every call on one GPU shares that scratch: calls that overlap on one GPU (on
+ * different streams or contexts) race; calls in one stream are ordered. */
+int vx_fused_attention_noalloc(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache,
+                               const vx_buf *v_cache, vx_buf *out, const vx_buf *position,
+                               const vx_fused_attn_args *a);
+
 typedef struct vx_fused_residual_args {
     uint32_t weight_offset, rows, cols, dtype;
     float scale;                    /* residual_scale (effective) */

@@ -266,6 +266,7 @@ PROTOTYPES = {
                                       P(FusedQkvArgs)]),
     "vx_fused_attention_scratch_bytes": (u64, [P(FusedAttnArgs)]),
     "vx_fused_attention": (i32, [CTX, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP, P(FusedAttnArgs)]),
+    "vx_fused_attention_noalloc": (i32, [CTX, BUFP, BUFP, BUFP, BUFP, BUFP, P(FusedAttnArgs)]),
     "vx_fused_matvec_residual": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, P(FusedResidualArgs)]),
     "vx_fused_rms_swiglu": (i32, [CTX, MODEL, BUFP, BUFP, P(FusedSwigluArgs)]),
     "vx_diag_stream_read": (i32, [CTX, BUFP, u64, u64, BUFP, u32, u32]),
@@ -371,6 +372,8 @@ class VxError(RuntimeError):
         self.name = STATUS.get(status, str(status))
         super().__init__(f"{func}: {self.name}: {message}")
 
+
+NOALLOC_SCRATCH_BYTES = 2 * 1024 * 1024  # VX_NOALLOC_SCRATCH_BYTES
 
 _LIB = None
 

@@ -417,9 +417,11 @@ uint64_t vx_fused_attention_scratch_bytes(const vx_fused_attn_args *a) {
     return attn_scratch_bytes(a->head_dim, a->q_heads, a->kv_heads, a->splits);
 }
 
-int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, const vx_buf *v_cache, vx_buf *out,
-                       vx_buf *scratch, const vx_buf *position, const vx_fused_attn_args *a) {
-    VX_CHECK(need_ctx(ctx, a, "vx_fused_attention"));
+namespace {
+// Checks and launch description shared by the two fused attention entry points;
+// the caller supplies the partials buffer.
+int fused_attention_launch(const vx_buf *q, const vx_buf *k_cache, const vx_buf *v_cache, vx_buf *out,
+                           const vx_buf *position, const vx_fused_attn_args *a, AttnLaunch *l) {
     if (a->kv_heads == 0 || a->q_heads % a->kv_heads)
         return fail(VX_ERR_SHAPE, "fused attention: q_heads must be a multiple of kv_heads");
     const uint32_t kv_dim = a->kv_heads * a->head_dim;
@@ -428,22 +430,51 @@ int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, cons
     VX_CHECK(need_buf(k_cache, cache, "fused attention k_cache"));
     VX_CHECK(need_buf(v_cache, cache, "fused attention v_cache"));
     VX_CHECK(need_buf(out, (uint64_t)a->q_heads * a->head_dim * 4u, "fused attention out"));
-    VX_CHECK(need_buf(scratch, vx_fused_attention_scratch_bytes(a), "fused attention scratch"));
     VX_CHECK(need_buf(position, 4u, "fused attention position"));
+    l->q = CF(q);
+    l->kc = static_cast<const __half *>(k_cache->ptr);
+    l->vc = static_cast<const __half *>(v_cache->ptr);
+    l->out = F(out);
+    l->position = CU(position);
+    l->layer = a->layer;
+    l->context = a->context;
+    l->head_dim = a->head_dim;
+    l->q_heads = a->q_heads;
+    l->kv_heads = a->kv_heads;
+    l->splits = a->splits;
+    return VX_OK;
+}
+}  // namespace
+
+int vx_fused_attention(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, const vx_buf *v_cache, vx_buf *out,
+                       vx_buf *scratch, const vx_buf *position, const vx_fused_attn_args *a) {
+    VX_CHECK(need_ctx(ctx, a, "vx_fused_attention"));
     AttnLaunch l;
-    l.q = CF(q);
-    l.kc = static_cast<const __half *>(k_cache->ptr);
-    l.vc = static_cast<const __half *>(v_cache->ptr);
-    l.out = F(out);
+    VX_CHECK(fused_attention_launch(q, k_cache, v_cache, out, position, a, &l));
+    VX_CHECK(need_buf(scratch, vx_fused_attention_scratch_bytes(a), "fused attention scratch"));
     l.partials = F(scratch);
-    l.position = CU(position);
-    l.layer = a->layer;
-    l.context = a->context;
-    l.head_dim = a->head_dim;
-    l.q_heads = a->q_heads;
-    l.kv_heads = a->kv_heads;
-    l.splits = a->splits;
     ProfSpan span(ctx, "baselm.attention");
+    return launch_attn_decode(ctx->stream, l);
+}
+
+// The partials go to this GPU's no-allocation scratch (runtime.cpp), resolved at
+// vx_init. Nothing here allocates, frees or clears memory: the split records are
+// written by the partials kernel before the combine kernel reads them, so
+// nothing in the scratch needs to start at zero.
+int vx_fused_attention_noalloc(vx_ctx *ctx, const vx_buf *q, const vx_buf *k_cache, const vx_buf *v_cache,
+                               vx_buf *out, const vx_buf *position, const vx_fused_attn_args *a) {
+    VX_CHECK(need_ctx(ctx, a, "vx_fused_attention_noalloc"));
+    AttnLaunch l;
+    VX_CHECK(fused_attention_launch(q, k_cache, v_cache, out, position, a, &l));
+    const uint64_t need = vx_fused_attention_scratch_bytes(a);
+    if (need > VX_NOALLOC_SCRATCH_BYTES)
+        return fail(VX_ERR_BOUNDS,
+                    "vx_fused_attention_noalloc: %u heads x %u splits need %llu bytes of partials; the "
+                    "no-allocation scratch holds %u",
+                    a->q_heads, a->splits, (unsigned long long)need, (unsigned)VX_NOALLOC_SCRATCH_BYTES);
+    if (!ctx->noalloc_scratch)
+        return fail(VX_ERR_STATE, "vx_fused_attention_noalloc: the context has no scratch address");
+    l.partials = static_cast<float *>(ctx->noalloc_scratch);
     return launch_attn_decode(ctx->stream, l);
 }
 

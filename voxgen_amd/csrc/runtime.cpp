@@ -89,6 +89,13 @@ int collect_profile(vx_ctx *ctx) {
 
 using namespace vx;
 
+// Device scratch of the entry points that allocate nothing
+// (vx_fused_attention_noalloc): VX_NOALLOC_SCRATCH_BYTES per GPU, held until the
+// process ends. Host code never passes this array's name to a kernel or a copy:
+// vx_init resolves the device address of this GPU's copy once (with the device
+// current) and keeps it in the context.
+static __device__ __align__(256) uint8_t scratch[VX_NOALLOC_SCRATCH_BYTES];
+
 extern "C" {
 
 int vx_abi_version(void) { return VX_ABI_VERSION; }
@@ -116,6 +123,15 @@ int vx_init(int device_index, vx_ctx **out) {
         delete ctx;
         return fail(VX_ERR_HIP, "hipStreamCreate failed");
     }
+    void *sp = nullptr;
+    e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !sp) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return fail(VX_ERR_HIP, "hipGetSymbolAddress of the no-allocation scratch failed: %s",
+                    hipGetErrorString(e));
+    }
+    ctx->noalloc_scratch = sp;
     *out = ctx;
     return VX_OK;
 }

@@ -97,6 +97,7 @@ struct vx_ctx {
     std::unordered_map<std::string, vx::ProfTotal> prof_totals;
     std::vector<std::string> prof_order;
     hipDeviceProp_t props{};
+    void *noalloc_scratch = nullptr;  // device address of this GPU's no-allocation scratch
 };
 
 struct vx_model {
