@@ -257,3 +257,32 @@ def test_persistent_mode_rejects_other_geometry(ctx):
         BaseLmEngine(ctx, model, cfg, exec_mode="persistent", strict_geometry=False)
     assert e.value.name == "VX_ERR_UNSUPPORTED"
     model.free()
+
+
+def test_gguf_file_through_the_loader_decodes_like_the_oracle(ctx, full_model, tmp_path):
+    """The real load path: the 28-layer model written as a GGUF v3 file, parsed by
+    vx_gguf_open (load_summary, gguf.rs:222-286), configured by
+    vx_baselm_config_from_gguf (BaseLmConfig::from_gguf, baselm.rs:60-180),
+    uploaded by vx_model_upload_gguf (data region + Q8_0 repack) and decoded."""
+    from voxgen_amd import gguf
+    from voxgen_amd.gguf import Gguf
+    cfg, m, _, o = full_model
+    p = gguf.write(tmp_path / "baselm.gguf", m.metadata, m.tensors, m.data)
+    g = Gguf(p)
+    fcfg = g.baselm_config(cfg["active_context_length"])
+    for k in ("embedding_length", "block_count", "feed_forward_length", "head_count", "head_count_kv",
+              "head_dim", "vocab_size", "context_length"):
+        assert fcfg[k] == cfg[k], k
+    model = Model.from_gguf(ctx, g)
+    try:
+        eng = BaseLmEngine(ctx, model, fcfg, exec_mode="graph", strict_geometry=True)
+        toks = [int(t) for t in synth.uniform_u32(2, 0x5EED000A, cfg["vocab_size"])]
+        for pos, t in enumerate(toks):
+            want = o.decode_token(t, pos, logits=True)
+            r = eng.decode_token(t, top_k=3)
+            assert rel_l2(eng.output(), want) < 5e-3, pos
+            assert [i for i, _ in r.top_logits][:3] == list(np.argsort(-o.logits, kind="stable")[:3])
+        eng.close()
+    finally:
+        model.free()
+        g.close()

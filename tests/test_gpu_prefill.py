@@ -154,10 +154,17 @@ def test_full_stack_prefill_32_tokens_against_oracle(ctx, full):
 
 
 def test_full_stack_prefill_384_matches_sequential_decode(ctx, full):
-    """The T = 384 prefill workload: batched prefill against the same engine's
-    sequential decode (itself pinned to the oracle by the decode tests)."""
+    """The T = 384 prefill workload: batched prefill against the oracle's
+    sequential decode of the same 384 tokens (prefill_tokens, baselm.rs:823-839:
+    final hidden, every layer's K/V rows, the last token's top logits), and
+    against the same engine's sequential decode."""
     cfg, m, model = full
     toks = [int(t) for t in synth.uniform_u32(384, 0x5EED0108, cfg["vocab_size"])]
+    o = oracle_of(m, cfg)
+    for p, t in enumerate(toks):
+        o.decode_token(t, p, logits=(p == 383))
+    okv_k = o.kv_k.reshape(28, 512, 256)[:, :384]
+    okv_v = o.kv_v.reshape(28, 512, 256)[:, :384]
     seq = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=True)
     seq.prefill_tokens(toks)
     want_out = seq.output()
@@ -165,9 +172,16 @@ def test_full_stack_prefill_384_matches_sequential_decode(ctx, full):
     want_v = kv_rows(seq, "kv_v", 28, 512)[:, :384]
     seq.close()
     eng = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=True)
-    eng.prefill_tokens_batched_gpu_only(toks)
-    ctx.sync()
+    r = eng.prefill_tokens_batched(toks, top_k_last=5)
     assert eng.position == 384
+    # against the oracle
+    assert rel_l2(eng.output(), o.norm) < 5e-3
+    assert [t for t, _ in r.top_logits][:3] == list(np.argsort(-o.logits, kind="stable")[:3])
+    gk, gv = kv_rows(eng, "kv_k", 28, 512)[:, :384], kv_rows(eng, "kv_v", 28, 512)[:, :384]
+    for l in range(28):
+        assert rel_l2(f16(gk[l]), f16(okv_k[l])) < 5e-3, l
+        assert rel_l2(f16(gv[l]), f16(okv_v[l])) < 5e-3, l
+    # and against the engine's own sequential decode
     assert rel_l2(eng.output(), want_out) < 5e-3
     got_k = kv_rows(eng, "kv_k", 28, 512)[:, :384]
     got_v = kv_rows(eng, "kv_v", 28, 512)[:, :384]

@@ -56,7 +56,7 @@ def write(path, metadata: dict, tensors, data: np.ndarray | None, data_bytes: in
     with open(path, "wb") as f:
         f.write(hdr)
         if data is not None:
-            f.write(np.ascontiguousarray(data, dtype=np.uint8).tobytes())
+            f.write(memoryview(np.ascontiguousarray(data, dtype=np.uint8)))
         else:
             f.truncate(len(hdr) + int(data_bytes))
     return path
