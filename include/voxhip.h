@@ -720,6 +720,18 @@ int vx_locdit_estimate(vx_locdit *loc, const float *x, const float *cond, const 
  * out_patch receives the final x [patch x feat_dim]. */
 int vx_locdit_cfm_solve(vx_locdit *loc, const float *cond, const float *mu, const vx_cfm_options *opt,
                         const float *initial_x, float *out_patch, vx_cfm_result *res);
+/* cfm_from_model_hiddens (local.rs:379-381; record_project_mu 459-462): the same
+ * solve with the two mu tokens projected on the device, inside the solve's graph,
+ * from the ResidualLM engine's buffers the reference binds to the local engine
+ * (runtime.rs:239-243): mu1 = projections.lm_to_dit_proj . current_lm + b
+ * (VX_RESIDUAL_BUF_CURRENT_LM), mu2 = projections.res_to_dit_proj . output + b
+ * (VX_RESIDUAL_BUF_OUTPUT); each buffer holds the projections' input width
+ * (2048) of f32. No host round trip. VX_ERR_NOT_FOUND if the model lacks the
+ * projections (they are required only under strict geometry). */
+int vx_locdit_cfm_solve_from_model_hiddens(vx_locdit *loc, const vx_buf *current_lm,
+                                           const vx_buf *residual_output, const float *cond,
+                                           const vx_cfm_options *opt, const float *initial_x,
+                                           float *out_patch, vx_cfm_result *res);
 
 /* ------------------------------------------------------------------------- */
 /* ResidualLM + FSQ + fusion + stop head (ResidualFsqEngine, acoustic.rs:400-1035). */

@@ -656,6 +656,14 @@ class LocDit:
         norm = self.transformer(np.concatenate(rows, axis=0))
         return self._lin("locdit.out_proj", norm[self.S - P:]).reshape(-1)
 
+    def project_mu(self, current_lm, residual_output):
+        """record_project_mu (local.rs:459-462): seq_linear_bias with one token,
+        mu1 = lm_to_dit_proj . current_lm + b, mu2 = res_to_dit_proj . residual + b."""
+        out = []
+        for name, x in (("projections.lm_to_dit_proj", current_lm), ("projections.res_to_dit_proj", residual_output)):
+            out.append(self._mat(name + ".weight") @ np.asarray(x, np.float64) + self._vec(name + ".bias"))
+        return np.concatenate(out)
+
     def cfm_solve(self, cond, mu, n_timesteps=10, cfg_value=2.0, temperature=1.0, sway=1.0, seed=42,
                   zero_star=True, initial_x=None):
         c = self.c

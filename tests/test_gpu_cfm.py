@@ -167,3 +167,111 @@ def test_cfm_shader_entry_points(ctx):
     ab = ctx.array(x)
     abi.call("vx_add_vectors", ctx.handle, ab.handle, pb.handle, n)
     assert np.array_equal(ab.download(np.float32, n), x + p)
+
+
+def test_cfm_from_model_hiddens_matches_chained_oracles(ctx, ref_shape):
+    """cfm_from_model_hiddens (local.rs:379-381): the mu tokens are projected on
+    the device from the ResidualLM engine's current_lm and output buffers
+    (runtime.rs:239-243) inside the solve's graph. BaseLM (2 Q8_0 layers) ->
+    ResidualLM (2 F16 layers, an FSQ step after a text-prefix step) -> LocDiT
+    (reference layout, 2 layers), against the oracles chained the same way."""
+    from voxgen_amd.baselm import BaseLmEngine
+    from voxgen_amd.residual import ResidualFsqEngine
+    cfg, m, model, o = ref_shape
+    bcfg = synth.baselm_config(layers=2, vocab=512, context_length=256, active_context=256)
+    bm = synth.build_baselm(bcfg, seed=0x5EED0240)
+    acfg = synth.acoustic_config(layers=2, active_context=64)
+    am = synth.build_acoustic(acfg, seed=0x5EED0241)
+    bmodel, amodel = Model(ctx, bm.data, bm.tensors), Model(ctx, am.data, am.tensors)
+    base = BaseLmEngine(ctx, bmodel, bcfg, strict_geometry=False)
+    res = ResidualFsqEngine(ctx, amodel, acfg, strict_geometry=False)
+    ob = voxref.BaseLm(bm.data, {t.name: t for t in bm.tensors}, bcfg)
+    orr = voxref.ResidualFsq(am.data, {t.name: t for t in am.tensors}, acfg)
+    toks = [int(t) for t in synth.uniform_u32(2, 0x5EED0242, 512)]
+    emb = synth.normal_f32(2048, 0x5EED0243)
+    # The chain up to the LocDiT inputs: each engine against its oracle, the
+    # ResidualLM oracle fed the GPU's BaseLM rows (FSQ is a rounding: identical
+    # inputs keep the latent exact instead of letting a tie flip it).
+    base.decode_token_gpu_only(toks[0])
+    b0 = base.buffer("norm").download(np.float32, 2048)
+    assert rel_l2(b0, ob.decode_token(toks[0], 0)) < 5e-3
+    res.step_text_prefix_from_gpu_base_gpu_only(base.buffer("norm"))
+    orr.step(b0, None, 0, fsq=False)
+    base.decode_token_gpu_only(toks[1])
+    b1 = base.buffer("norm").download(np.float32, 2048)
+    assert rel_l2(b1, ob.decode_token(toks[1], 1)) < 5e-3
+    res.step_from_gpu_base(base.buffer("norm"), emb)
+    want_step = orr.step(b1, emb, 1, fsq=True)
+    ctx.sync()
+    lm = res.current_lm_buffer().download(np.float32, 2048)
+    out = res.output_buffer().download(np.float32, 2048)
+    assert rel_l2(lm, want_step["fsq"]) < 1e-4
+    assert rel_l2(out, want_step["norm"]) < 1e-3
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, _ = inputs(cfg, 0x5EED0244)
+    opt = CfmOptions(n_timesteps=4, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0, seed=77,
+                     use_cfg_zero_star=True)
+    got, info = loc.cfm_from_model_hiddens(res.current_lm_buffer(), res.output_buffer(), cond, opt)
+    mu = o.project_mu(lm, out)                           # the projection of the same device vectors, f64
+    want = o.cfm_solve(cond, mu, n_timesteps=4, cfg_value=2.0, temperature=1.0, sway=1.0, seed=77,
+                       zero_star=True)
+    assert rel_l2(got, want) < 1e-3
+    assert info["estimator_calls"] == 6
+    host, _ = loc.cfm_solve(cond, mu.astype(np.float32), opt)  # the host-mu entry on the same mu
+    assert rel_l2(got, host) < 1e-4
+    # A replay reads the buffers' current contents: another step changes mu and the result.
+    base.decode_token_gpu_only(toks[0])
+    res.step_from_gpu_base(base.buffer("norm"), emb)
+    ctx.sync()
+    got2, _ = loc.cfm_from_model_hiddens(res.current_lm_buffer(), res.output_buffer(), cond, opt)
+    mu2 = o.project_mu(res.current_lm_buffer().download(np.float32, 2048), res.output_buffer().download(np.float32, 2048))
+    want2 = o.cfm_solve(cond, mu2, n_timesteps=4, cfg_value=2.0, temperature=1.0, sway=1.0, seed=77, zero_star=True)
+    assert rel_l2(got2, want2) < 1e-3 and rel_l2(got2, got) > 1e-3
+    with pytest.raises(abi.VxError) as e:
+        loc.cfm_from_model_hiddens(res.current_lm_buffer(), ctx.zeros(1024), cond, opt)
+    assert e.value.name in ("VX_ERR_BOUNDS", "VX_ERR_SHAPE")
+    for x in (loc, res, base):
+        x.close()
+    bmodel.free()
+    amodel.free()
+
+
+def test_cfm_from_model_hiddens_needs_the_projections(ctx):
+    cfg = synth.locdit_config(layers=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0250, with_mu_proj=False)
+    model = Model(ctx, m.data, m.tensors)
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, _ = inputs(cfg, 0x5EED0251)
+    with pytest.raises(abi.VxError) as e:
+        loc.cfm_from_model_hiddens(ctx.zeros(8192), ctx.zeros(8192), cond)
+    assert e.value.name == "VX_ERR_NOT_FOUND"
+    loc.close()
+    with pytest.raises(abi.VxError) as e:  # the reference's contract requires them (local.rs:141-144)
+        LocDit(ctx, model, synth.locdit_config(layers=1), strict_geometry=True)
+    assert e.value.name in ("VX_ERR_NOT_FOUND", "VX_ERR_UNSUPPORTED")
+    model.free()
+
+
+def test_cfm_solve_at_the_reference_contract_strict(ctx):
+    """The reference's enforced LocDiT geometry (LocalConfig::from_gguf,
+    local.rs:37-48,85-92): 12 layers x 1024, 16/2 x 128, ffn 4096, mu1 + mu2 +
+    time + 4 condition + 4 latent tokens, strict geometry on, against the oracle
+    (host mu and model-hidden mu)."""
+    cfg = synth.locdit_config()
+    m = synth.build_locdit(cfg, seed=0x5EED0260)
+    model = Model(ctx, m.data, m.tensors)
+    o = oracle_of(m, cfg)
+    loc = LocDit(ctx, model, cfg, strict_geometry=True)
+    _, cond, mu = inputs(cfg, 0x5EED0261)
+    opt = CfmOptions(n_timesteps=4, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0, seed=9,
+                     use_cfg_zero_star=True)
+    got, info = loc.cfm_solve(cond, mu, opt)
+    want = o.cfm_solve(cond, mu, n_timesteps=4, cfg_value=2.0, temperature=1.0, sway=1.0, seed=9, zero_star=True)
+    assert rel_l2(got, want) < 1e-3 and info["estimator_calls"] == 6
+    h1, h2 = ctx.array(synth.normal_f32(2048, 0x5EED0262)), ctx.array(synth.normal_f32(2048, 0x5EED0263))
+    got_h, _ = loc.cfm_from_model_hiddens(h1, h2, cond, opt)
+    mu_h = o.project_mu(h1.download(np.float32, 2048), h2.download(np.float32, 2048))
+    want_h = o.cfm_solve(cond, mu_h, n_timesteps=4, cfg_value=2.0, temperature=1.0, sway=1.0, seed=9, zero_star=True)
+    assert rel_l2(got_h, want_h) < 1e-3
+    loc.close()
+    model.free()

@@ -209,3 +209,26 @@ def test_locdit_oracle_matches_loop_restatement():
         want = naive_locdit(m, cfg, x.astype(np.float64), cond.astype(np.float64), mu.astype(np.float64), 0.63, 0.0,
                             zero_mu=zero_mu)
         assert rel_l2(got, want) < 1e-10, zero_mu
+
+
+def test_project_mu_matches_the_linear_bias_restatement():
+    """LocDit.project_mu (record_project_mu, local.rs:459-462) against the C
+    restatement of linear_bias.comp on the same F16 projection tensors, and a
+    one-hot input recovers a weight column plus the bias."""
+    cfg = synth.locdit_config(layers=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0901)
+    ts = {t.name: t for t in m.tensors}
+    o = voxref.LocDit(m.data, ts, cfg)
+    x1, x2 = synth.normal_f32(2048, 0x5EED0902), synth.normal_f32(2048, 0x5EED0903)
+    got = o.project_mu(x1, x2)
+    for i, (name, x) in enumerate((("projections.lm_to_dit_proj", x1), ("projections.res_to_dit_proj", x2))):
+        w, b = ts[name + ".weight"], ts[name + ".bias"]
+        push = abi.LinearBiasPush(w.offset, b.offset, cfg["hidden"], 2048, abi.DTYPE_F16, 0, 0, 1.0)
+        want = voxref.linear_bias(m.data, x, push)
+        assert rel_l2(got[i * cfg["hidden"]:(i + 1) * cfg["hidden"]], want) < 1e-6, name
+    onehot = np.zeros(2048, np.float32)
+    onehot[77] = 1.0
+    w = ts["projections.lm_to_dit_proj.weight"]
+    col = m.data[w.offset:w.offset + w.nbytes].view(np.float16).reshape(cfg["hidden"], 2048)[:, 77]
+    bias = m.data[ts["projections.lm_to_dit_proj.bias"].offset:][:cfg["hidden"] * 4].view(np.float32)
+    assert np.allclose(o.project_mu(onehot, onehot)[:cfg["hidden"]], col.astype(np.float64) + bias, rtol=0, atol=1e-7)

@@ -262,6 +262,8 @@ PROTOTYPES = {
     "vx_locdit_destroy": (i32, [LOCDIT]),
     "vx_locdit_estimate": (i32, [LOCDIT, P(f32), P(f32), P(f32), f32, f32, P(f32)]),
     "vx_locdit_cfm_solve": (i32, [LOCDIT, P(f32), P(f32), P(CfmOptions), P(f32), P(f32), P(CfmResult)]),
+    "vx_locdit_cfm_solve_from_model_hiddens": (i32, [LOCDIT, BUFP, BUFP, P(f32), P(CfmOptions), P(f32), P(f32),
+                                                     P(CfmResult)]),
     "vx_fused_qkv_rope_store": (i32, [CTX, MODEL, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP, BUFP,
                                       P(FusedQkvArgs)]),
     "vx_fused_attention_scratch_bytes": (u64, [P(FusedAttnArgs)]),

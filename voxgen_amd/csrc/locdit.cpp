@@ -51,6 +51,11 @@ struct vx_locdit {
     uint32_t S = 0;   // tokens per sequence
     bool dense_fused = false;   // attention of a sequence fits the one-kernel path
     Lin in_proj, cond_proj, out_proj, t1, t2, d1, d2;
+    // projections.lm_to_dit_proj / res_to_dit_proj (local.rs:141-144): the mu
+    // tokens from the ResidualLM engine's current_lm and output buffers.
+    Lin lm_to_dit, res_to_dit;
+    bool has_mu_proj = false;
+    uint32_t lm_hidden = 0;   // their input width (the BaseLM embedding length)
     const float *norm_w = nullptr, *rope_factors = nullptr;
     std::vector<LocLayer> layers;
     // State and activations (two sequences: conditional, unconditional).
@@ -66,6 +71,7 @@ struct vx_locdit {
     vx_graph *graph = nullptr;
     vx_cfm_options graph_opt{};
     int graph_initial_x = -1;
+    const float *graph_mu_src[2] = {nullptr, nullptr};   // model-hidden sources the graph projects, or null
 };
 
 namespace {
@@ -376,11 +382,40 @@ uint32_t zero_init_steps(const vx_cfm_options &o, size_t span_len) {
     return o.use_cfg_zero_star ? std::max<uint32_t>(1u, (uint32_t)std::floor((float)span_len * 0.04f)) : 0u;
 }
 
-// The solve after the inputs are in place (cfm_solve, local.rs:383-430).
-int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_t *calls) {
+// record_project_mu (local.rs:459-462): mu1 = lm_to_dit_proj . current_lm + b and
+// mu2 = res_to_dit_proj . residual + b (seq_linear_bias with one token), written
+// into the two mu tokens of the solve.
+int enqueue_project_mu(vx_locdit *e, const float *current_lm, const float *residual) {
+    hipStream_t s = e->ctx->stream;
+    const uint32_t H = e->cfg.hidden;
+    const Lin *proj[2] = {&e->lm_to_dit, &e->res_to_dit};
+    const float *src[2] = {current_lm, residual};
+    for (int i = 0; i < 2; ++i) {
+        ProfSpan sp(e->ctx, "local.seq_linear");
+        MatvecLaunch a;
+        a.w = proj[i]->w;
+        a.xl = src[i];
+        a.rows = H;
+        a.cols = e->lm_hidden;
+        a.epi = EPI_BIAS;
+        a.bias = proj[i]->b;
+        a.bias_dtype = proj[i]->bt;
+        a.alpha = 1.f;
+        a.y = F(e->mu) + (size_t)i * H;
+        VX_CHECK(launch_matvec(s, a));
+    }
+    return VX_OK;
+}
+
+// The solve after the inputs are in place (cfm_solve, local.rs:383-430). With
+// mu_src set, the mu tokens are first projected from those device vectors
+// (cfm_from_model_hiddens, local.rs:379-381,399-401).
+int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_t *calls,
+                  const float *const *mu_src = nullptr) {
     hipStream_t s = e->ctx->stream;
     const vx_locdit_config &c = e->cfg;
     const uint32_t n = c.patch * c.feat_dim;
+    if (mu_src) VX_CHECK(enqueue_project_mu(e, mu_src[0], mu_src[1]));
     std::vector<float> span;
     VX_CHECK(time_span(o.n_timesteps, o.sway_sampling_coef, span));
     if (!initial_x) {
@@ -524,6 +559,23 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
             (st = matrix(model, pre + "ffn_down.weight", c.ffn, H, &L.down)))
             return bail(st);
     }
+    // The mu projections are required by the reference's contract (local.rs:141-144);
+    // outside it they are optional and only the model-hidden solve needs them.
+    {
+        const bool have = model->by_name.count("projections.lm_to_dit_proj.weight") != 0;
+        if (have || strict_geometry) {
+            const vx_tensor_info *t;
+            if ((st = find(model, "projections.lm_to_dit_proj.weight", &t))) return bail(st);
+            const uint32_t in = t->n_dims == 2 ? (uint32_t)t->dims[0] : 0u;
+            if (strict_geometry && in != 2048u)
+                return bail(fail(VX_ERR_SHAPE, "projections.lm_to_dit_proj.weight has %u columns, expected 2048", in));
+            if ((st = linear(model, "projections.lm_to_dit_proj", in, H, &e->lm_to_dit)) ||
+                (st = linear(model, "projections.res_to_dit_proj", in, H, &e->res_to_dit)))
+                return bail(st);
+            e->has_mu_proj = true;
+            e->lm_hidden = in;
+        }
+    }
     if ((st = resolve_vector(rope_model, rope_factor_offset, VX_DTYPE_F32, c.head_dim / 2u, &p, "LocDiT rope factors")))
         return bail(st);
     e->rope_factors = static_cast<const float *>(p);
@@ -594,15 +646,25 @@ int vx_locdit_estimate(vx_locdit *e, const float *x, const float *cond, const fl
     return vx_download(e->ctx, e->out, 0, out, n * 4u);
 }
 
-int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const vx_cfm_options *opt,
-                        const float *initial_x, float *out_patch, vx_cfm_result *res) {
-    if (!e || !opt || !out_patch) return fail(VX_ERR_INVALID_ARG, "vx_locdit_cfm_solve: null argument");
+}  // extern "C"
+
+namespace {
+// cfm_solve (local.rs:383-430) from host mu (mu_src null) or from model hiddens.
+int solve(vx_locdit *e, const float *cond, const float *mu, const float *const *mu_src, const vx_cfm_options *opt,
+          const float *initial_x, float *out_patch, vx_cfm_result *res) {
     VX_CHECK(validate_options(*opt));
     const vx_locdit_config &c = e->cfg;
     const uint64_t n = (uint64_t)c.patch * c.feat_dim;
     vx_ctx *ctx = e->ctx;
     const double t0 = now_ms();
-    VX_CHECK(upload_inputs(e, cond, mu));
+    if (mu_src) {
+        const uint64_t cn = c.cond_raw ? (uint64_t)c.n_cond * c.hidden : (uint64_t)c.patch * c.feat_dim;
+        if (!cond) return fail(VX_ERR_INVALID_ARG, "LocDiT condition is null");
+        VX_CHECK(check_finite(cond, cn, "CFM condition"));
+        VX_CHECK(vx_upload(ctx, e->cond_in, 0, cond, cn * 4u));
+    } else {
+        VX_CHECK(upload_inputs(e, cond, mu));
+    }
     if (initial_x) {
         VX_CHECK(check_finite(initial_x, n, "CFM initial x"));
         VX_CHECK(vx_upload(ctx, e->x, 0, initial_x, n * 4u));
@@ -612,16 +674,18 @@ int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const 
     VX_CHECK(prepare_time_rows(e, *opt));
     uint32_t calls = 0;
     if (ctx->prof_enabled) {
-        VX_CHECK(enqueue_solve(e, *opt, initial_x != nullptr, &calls));
+        VX_CHECK(enqueue_solve(e, *opt, initial_x != nullptr, &calls, mu_src));
     } else {
         const int ix = initial_x ? 1 : 0;
-        if (!e->graph || !same_options(e->graph_opt, *opt) || e->graph_initial_x != ix) {
+        const float *src0 = mu_src ? mu_src[0] : nullptr, *src1 = mu_src ? mu_src[1] : nullptr;
+        if (!e->graph || !same_options(e->graph_opt, *opt) || e->graph_initial_x != ix ||
+            e->graph_mu_src[0] != src0 || e->graph_mu_src[1] != src1) {
             if (e->graph) {
                 vx_graph_free(ctx, e->graph);
                 e->graph = nullptr;
             }
             VX_CHECK(vx_graph_begin(ctx));
-            const int st = enqueue_solve(e, *opt, initial_x != nullptr, &calls);
+            const int st = enqueue_solve(e, *opt, initial_x != nullptr, &calls, mu_src);
             vx_graph *g = nullptr;
             const int st2 = vx_graph_end(ctx, &g);
             if (st != VX_OK) {
@@ -632,6 +696,8 @@ int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const 
             e->graph = g;
             e->graph_opt = *opt;
             e->graph_initial_x = ix;
+            e->graph_mu_src[0] = src0;
+            e->graph_mu_src[1] = src1;
         }
         std::vector<float> span;
         VX_CHECK(time_span(opt->n_timesteps, opt->sway_sampling_coef, span));
@@ -660,6 +726,30 @@ int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const 
         res->output_max = mx;
     }
     return VX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const vx_cfm_options *opt,
+                        const float *initial_x, float *out_patch, vx_cfm_result *res) {
+    if (!e || !opt || !out_patch) return fail(VX_ERR_INVALID_ARG, "vx_locdit_cfm_solve: null argument");
+    return solve(e, cond, mu, nullptr, opt, initial_x, out_patch, res);
+}
+
+int vx_locdit_cfm_solve_from_model_hiddens(vx_locdit *e, const vx_buf *current_lm, const vx_buf *residual_output,
+                                           const float *cond, const vx_cfm_options *opt, const float *initial_x,
+                                           float *out_patch, vx_cfm_result *res) {
+    if (!e || !opt || !out_patch)
+        return fail(VX_ERR_INVALID_ARG, "vx_locdit_cfm_solve_from_model_hiddens: null argument");
+    if (!e->has_mu_proj)
+        return fail(VX_ERR_NOT_FOUND, "required GGUF tensor \"projections.lm_to_dit_proj.weight\" is missing");
+    if (e->cfg.n_mu != 2u)
+        return fail(VX_ERR_UNSUPPORTED, "the model-hidden solve projects two mu tokens; the config has %u", e->cfg.n_mu);
+    VX_CHECK(need_buf(current_lm, (uint64_t)e->lm_hidden * 4u, "CFM current_lm"));
+    VX_CHECK(need_buf(residual_output, (uint64_t)e->lm_hidden * 4u, "CFM residual output"));
+    const float *src[2] = {static_cast<const float *>(current_lm->ptr), static_cast<const float *>(residual_output->ptr)};
+    return solve(e, cond, nullptr, src, opt, initial_x, out_patch, res);
 }
 
 // ------------------------------------------------------- CFM shader entry points

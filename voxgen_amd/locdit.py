@@ -91,3 +91,17 @@ class LocDit:
         abi.call("vx_locdit_cfm_solve", self.handle, _f32p(cond), _f32p(mu), C.byref(options.to_c()),
                  _f32p(ix) if ix is not None else None, _f32p(out), C.byref(res))
         return out, {k: getattr(res, k) for k, _ in res._fields_}
+
+    def cfm_from_model_hiddens(self, current_lm, residual_output, cond, options: CfmOptions | None = None,
+                               initial_x=None):
+        """cfm_from_model_hiddens (local.rs:379-381): mu projected on the device from
+        the ResidualLM engine's current_lm and output buffers (runtime.Buffer)."""
+        options = options or CfmOptions()
+        cond = np.ascontiguousarray(cond, np.float32)
+        out = np.empty(self.patch_floats, np.float32)
+        res = abi.CfmResult()
+        ix = None if initial_x is None else np.ascontiguousarray(initial_x, np.float32)
+        abi.call("vx_locdit_cfm_solve_from_model_hiddens", self.handle, current_lm.handle, residual_output.handle,
+                 _f32p(cond), C.byref(options.to_c()), _f32p(ix) if ix is not None else None, _f32p(out),
+                 C.byref(res))
+        return out, {k: getattr(res, k) for k, _ in res._fields_}

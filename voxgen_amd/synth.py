@@ -220,7 +220,7 @@ def locdit_config(layers=12, hidden=1024, q_heads=16, kv_heads=2, head_dim=128, 
                 rope_scaling=rope_scaling)
 
 
-def build_locdit(cfg: dict, seed: int = 0x5EED0040, std: float = 0.02) -> SynthModel:
+def build_locdit(cfg: dict, seed: int = 0x5EED0040, std: float = 0.02, with_mu_proj: bool = True) -> SynthModel:
     """Synthetic LocDiT tensors with the names and shapes validate_tensors checks
     (local.rs:127-168): F16 matrices N(0, std), F32 biases N(0, std), F32 norm
     gains N(1, 0.02), plus rope_factors_short.weight (ones) so the same region
@@ -253,6 +253,11 @@ def build_locdit(cfg: dict, seed: int = 0x5EED0040, std: float = 0.02) -> SynthM
         reg.add(p + "ffn_gate.weight", abi.DTYPE_F16, (H, F))
         reg.add(p + "ffn_up.weight", abi.DTYPE_F16, (H, F))
         reg.add(p + "ffn_down.weight", abi.DTYPE_F16, (F, H))
+    # The mu projections from the ResidualLM engine's buffers (local.rs:141-144),
+    # appended so that the tensors above keep their seeds.
+    if with_mu_proj:
+        lin("projections.lm_to_dit_proj", cfg.get("lm_hidden", 2048), H)
+        lin("projections.res_to_dit_proj", cfg.get("lm_hidden", 2048), H)
     data = np.zeros((reg.size + 255) // 256 * 256, np.uint8)
     for i, t in enumerate(reg.tensors):
         s = derive_seed(seed, i)
