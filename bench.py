@@ -13,6 +13,13 @@ Prints one JSON line with:
                per launch / its average duration, measured with two HIP events on
                the engine stream around back-to-back launches over all 28 layers
   per_kernel   the same measurement for every kernel of the decode layer
+  c0           the single Q8_0 2048x2048 matvec (matvec.comp) over 64 distinct
+               copies (285 MB, beyond the 256 MB MALL) and hot in cache
+  achievable   the best plain streaming-read GB/s of this GPU (1 GiB read), the
+               practical ceiling next to the 8 TB/s spec
+  latency      the reference's own benchmark semantics (BaseLmEngine::benchmark,
+               baselm.rs:841-880): decode_token with the tied LM head and a host
+               wait per token
   cpu_baseline the CPU oracle's decode throughput on a bounded sample
   prefill      the token-batched prefill of 384 tokens through the 28 layers
                (MFMA projections, causal attention over the cache): wall time and
@@ -79,6 +86,83 @@ def step_bytes(pos, lm_head=False):
     if lm_head:
         b += V * H * 2 + V * 4
     return b
+
+
+C0_BYTES = q8(H, H) + 2 * H * 4   # W + x in + y out (the single-matvec workload)
+
+
+def graph_time_ms(ctx, launch, n_graph_launches=5):
+    """Average wall time (ms) of one replay of a graph captured from launch()."""
+    ctx.graph_begin()
+    launch()
+    g = ctx.graph_end()
+    try:
+        ctx.graph_launch(g)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(n_graph_launches):
+            ctx.graph_launch(g)
+        ctx.sync()
+        return (time.perf_counter() - t0) * 1e3 / n_graph_launches
+    finally:
+        ctx.graph_free(g)
+
+
+def c0_leg(ctx, copies=64, per_graph=256):
+    """y = W.x with W a 2048x2048 Q8_0 matrix (matvec.comp:46-62, the vx_matvec
+    entry point): `copies` distinct matrices (q ~ U[-127,127], d = |N(0,1)|*0.01,
+    x ~ N(0,1)) rotated inside one graph, so every launch reads HBM; and one
+    matrix repeated (hot in the MALL/L2). Per launch, including the launch gap
+    between dependent kernels of a graph."""
+    import ctypes as C
+    from voxgen_amd import abi, synth
+    from voxgen_amd.runtime import Model
+    reg = synth.Region()
+    ts = [reg.add(f"c0.w{i}", abi.DTYPE_Q8_0, (H, H)) for i in range(copies)]
+    data = np.zeros((reg.size + 255) // 256 * 256, np.uint8)
+    for i, t in enumerate(ts):
+        data[t.offset:t.offset + t.nbytes] = synth.q8_0_blocks(H * H // 32, 0x5EED0C00 + i)
+    model = Model(ctx, data, ts)
+    xb = ctx.array(synth.normal_f32(H, 0x5EED0C99))
+    yb = ctx.zeros(H * 4)
+    pushes = [abi.MatvecPush(t.offset, H, H, abi.DTYPE_Q8_0, 0, 1.0) for t in ts]
+
+    def run(seq):
+        def launch():
+            for i in seq:
+                abi.call("vx_matvec", ctx.handle, model.handle, xb.handle, yb.handle, C.byref(pushes[i]))
+        return launch
+
+    cold = graph_time_ms(ctx, run([i % copies for i in range(per_graph)])) / per_graph
+    hot = graph_time_ms(ctx, run([0] * per_graph)) / per_graph
+    model.free()
+    gb = lambda ms: round(C0_BYTES / (ms * 1e-3) / 1e9, 1)
+    return {"workload": "q8_0_matvec_2048x2048", "bytes_per_launch": C0_BYTES,
+            "hbm": {"avg_us": round(cold * 1e3, 3), "GBps": gb(cold), "frac": round(gb(cold) / HBM_PEAK_GBPS, 4),
+                    "copies": copies, "resident_MB": round(copies * q8(H, H) / 1e6, 1)},
+            "hot": {"avg_us": round(hot * 1e3, 3), "GBps": gb(hot)},
+            "note": "per launch inside a graph of 256 dependent launches, including the launch gap"}
+
+
+def achievable_leg(ctx):
+    """Best streaming-read bandwidth of a plain read kernel over 1 GiB (grid and
+    loads in flight swept): the practical HBM ceiling of this GPU."""
+    from voxgen_amd import abi
+    nbytes = 1 << 30
+    src, sink = ctx.zeros(nbytes), ctx.zeros(16 * 16384)
+    best = None
+    for blocks in (2048, 4096, 8192):
+        for unroll in (4, 8):
+            def launch():
+                for _ in range(4):
+                    abi.call("vx_diag_stream_read", ctx.handle, src.handle, 0, nbytes, sink.handle, blocks, unroll)
+            ms = graph_time_ms(ctx, launch) / 4
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            if best is None or gbps > best["GBps"]:
+                best = {"GBps": round(gbps, 1), "blocks": blocks, "unroll": unroll}
+    best["frac_of_spec"] = round(best["GBps"] / HBM_PEAK_GBPS, 4)
+    best["bytes"] = nbytes
+    return best
 
 
 def parse():
@@ -492,9 +576,10 @@ def main():
     tok_s = K / elapsed
     log(f"timed {K} steps at positions {P}..{P + K - 1}: {elapsed * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
 
-    # Per-kernel durations: HIP events on the engine stream around back-to-back
-    # launches of one layer kernel over the 28 layers' weights (750 MB for the
-    # SwiGLU, beyond the 256 MB MALL), at the device position P+K.
+    # Per-kernel cost: one layer kernel over the 28 layers' weights as a graph
+    # chain, each pass after a 384 MiB read that evicts the MALL (so every launch
+    # reads HBM, as in the step), HIP events on the engine stream, the reads
+    # alone subtracted; at the device position P+K. Includes the launch gap.
     pos_k = P + K
     per_kernel = {}
     fam_bytes = fam_ms = 0.0
@@ -516,14 +601,28 @@ def main():
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    achievable = achievable_leg(ctx)
+    log(f"achievable streaming read: {achievable['GBps']:.0f} GB/s ({achievable['frac_of_spec']:.3f} of 8 TB/s)")
     roofline = dict(bound="hbm", achieved=dom["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
                     frac=dom["frac"], traffic=traffic, kernel="k_swiglu (rmsnorm + gate/up Q8_0 matvec + SiLU)",
-                    bytes_per_launch=dom["bytes"], avg_us=dom["avg_us"])
+                    bytes_per_launch=dom["bytes"], avg_us=dom["avg_us"],
+                    achievable_GBps=achievable["GBps"], frac_of_achievable=round(dom["GBps"] / achievable["GBps"], 4))
     mean_step_bytes = float(np.mean([step_bytes(p, args.lm_head) for p in range(P, P + K)]))
+    c0 = c0_leg(ctx)
+    log(f"c0 matvec 2048x2048 Q8_0: {c0['hbm']['avg_us']:.2f} us from HBM ({c0['hbm']['GBps']:.0f} GB/s), "
+        f"{c0['hot']['avg_us']:.2f} us hot")
 
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, m, eng, tokens, P, args)
+    # The reference's own benchmark (baselm.rs:841-880): decode_token with the
+    # tied LM head and a host fence per token, from position 0.
+    lb = eng.benchmark(int(tokens[0]), 4, 32)
+    latency = {"semantics": "BaseLmEngine::benchmark: decode_token with the tied LM head, host wait per token",
+               "mean_ms": round(lb["mean_ms"], 4), "min_ms": round(lb["min_ms"], 4), "max_ms": round(lb["max_ms"], 4),
+               "tok_s": round(lb["tokens_per_second"], 1), "positions": "4..35"}
+    log(f"reference-semantics decode (LM head, sync per token): {lb['mean_ms']:.3f} ms -> "
+        f"{lb['tokens_per_second']:.1f} tok/s")
     prefill = None
     if args.prefill_tokens:
         prefill = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
@@ -555,7 +654,11 @@ def main():
         "roofline": roofline,
         "matvec_family": {"achieved": round(fam_gbps, 1), "unit": "GB/s",
                           "frac": round(fam_gbps / HBM_PEAK_GBPS, 4),
+                          "frac_of_achievable": round(fam_gbps / achievable["GBps"], 4),
                           "kernels": ["qkv", "attn_out", "swiglu", "down"]},
+        "achievable": achievable,
+        "c0": c0,
+        "latency": latency,
         "step": {"bytes_mean": int(mean_step_bytes),
                  "achieved_GBps": round(mean_step_bytes * tok_s / 1e9, 1),
                  "frac": round(mean_step_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4)},

@@ -634,13 +634,16 @@ vx_buf *vx_baselm_buffer(vx_baselm *eng, uint32_t which);
 int vx_baselm_profile_steps(vx_baselm *eng, const uint32_t *tokens, uint32_t n,
                             vx_prof_entry *out, uint32_t cap, uint32_t *count);
 
-/* Average duration of one kernel of the fused decode layer, measured with two
- * HIP events on the engine stream around `reps` back-to-back passes over every
- * layer (after one untimed pass). Each layer reads its own weights, so the
- * passes stream from HBM as a decode step does. `which`: VX_LAYER_KERNEL_*.
- * The kernels read the device position and overwrite the engine's activations
- * and the KV-cache row at that position. No reference counterpart: it is the
- * measurement the gpu_profile spans (vulkan.rs:587-612) give per dispatch. */
+/* Average cost of one kernel of the fused decode layer inside a graph chain:
+ * `reps` passes, each a 384 MiB streaming read that evicts the MALL and the L2s
+ * followed by the kernel over every layer, captured as one graph and timed with
+ * HIP events on the engine stream; a graph of the reads alone is subtracted. Each
+ * launch therefore reads its weights from HBM, as in a decode step, and the
+ * figure includes the launch gap between dependent kernels. Allocates 384 MiB for
+ * the call. `which`: VX_LAYER_KERNEL_*. The kernels read the device position and
+ * overwrite the engine's activations and the KV-cache row at that position. No
+ * reference counterpart: it is the measurement the gpu_profile spans
+ * (vulkan.rs:587-612) give per dispatch. */
 #define VX_LAYER_KERNEL_QKV 0u
 #define VX_LAYER_KERNEL_ATTENTION 1u
 #define VX_LAYER_KERNEL_ATTN_OUT 2u

@@ -164,8 +164,9 @@ class BaseLmEngine:
     LAYER_KERNELS = ("qkv", "attention", "attn_out", "swiglu", "down")
 
     def time_layer_kernel(self, name: str, reps: int = 4) -> float:
-        """Average duration (ms) of one fused layer kernel over `reps` back-to-back
-        passes across all layers, from two HIP events on the engine stream."""
+        """Average cost (ms) of one fused layer kernel inside a graph chain over all
+        layers, each pass after a MALL-evicting read (every launch reads HBM), from
+        HIP events on the engine stream."""
         out = C.c_double()
         abi.call("vx_baselm_time_layer_kernel", self.handle, self.LAYER_KERNELS.index(name), reps,
                  C.byref(out))
