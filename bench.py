@@ -188,6 +188,8 @@ def parse():
     ap.add_argument("--vae-only", action="store_true", help="run only the AudioVAE leg (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the token-batched prefill leg (for profiling)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the prefill, warmup and timed decode steps, no graph-timed legs (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one copy kernel of known size and exit (PMC calibration)")
     return ap.parse_args()
@@ -575,6 +577,13 @@ def main():
     elapsed = time.perf_counter() - t0
     tok_s = K / elapsed
     log(f"timed {K} steps at positions {P}..{P + K - 1}: {elapsed * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
+    if args.decode_only:
+        eng.close()
+        model.free()
+        ctx.close()
+        print(json.dumps({"decode": {"tok_s": round(tok_s, 2), "ms_per_step": round(elapsed * 1e3 / K, 4),
+                                     "exec": args.mode, "positions": f"{P}..{P + K - 1}"}}), flush=True)
+        return
 
     # Per-kernel cost: one layer kernel over the 28 layers' weights as a graph
     # chain, each pass after a 384 MiB read that evicts the MALL (so every launch

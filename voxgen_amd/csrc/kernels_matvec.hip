@@ -140,7 +140,10 @@ struct AttnOutArgs {
 
 template <int WT, int NG, int RPW, int HD, bool BRANCH, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
-    constexpr int E = 16 * NG / WPB;  // outputs merged per thread (all 64*WPB threads merge)
+    // The first MT threads merge E outputs each (float4 units): every one of the
+    // workgroup's threads up to 1024*NG/4 of them.
+    constexpr int MT = 64 * WPB < 256 * NG ? 64 * WPB : 256 * NG;
+    constexpr int E = 1024 * NG / MT;
     static_assert(E >= 4 && E % 4 == 0, "merge works in float4 units");
     __shared__ __align__(16) float xs[NG * kGroupCols];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -149,15 +152,24 @@ __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
     // Every split record of this thread's head is requested up front, whatever
     // the position (records past the active splits get weight 0 by a select), so
     // these loads do not wait for the position and go out ahead of the weights.
-    const uint32_t o0 = (uint32_t)(E * tid), hh = o0 / HD, d0 = o0 % HD;
+    const bool merger = tid < MT;
+    const uint32_t o0 = (uint32_t)(E * (merger ? tid : 0)), hh = o0 / HD, d0 = o0 % HD;
     float2 ml[kMaxFoldedSplits];
     float4 av[kMaxFoldedSplits][E / 4];
 #pragma unroll
     for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
-        const float *rec = a.part + ((size_t)hh * a.splits + (s < a.splits ? s : 0u)) * (HD + 4);
-        ml[s] = *reinterpret_cast<const float2 *>(rec);
+        ml[s] = make_float2(0.f, 0.f);
 #pragma unroll
-        for (int e = 0; e < E / 4; ++e) av[s][e] = *reinterpret_cast<const float4 *>(rec + 4 + d0 + 4 * e);
+        for (int e = 0; e < E / 4; ++e) av[s][e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (merger) {  // wave-uniform: MT is a multiple of 64
+#pragma unroll
+        for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+            const float *rec = a.part + ((size_t)hh * a.splits + (s < a.splits ? s : 0u)) * (HD + 4);
+            ml[s] = *reinterpret_cast<const float2 *>(rec);
+#pragma unroll
+            for (int e = 0; e < E / 4; ++e) av[s][e] = *reinterpret_cast<const float4 *>(rec + 4 + d0 + 4 * e);
+        }
     }
     const SplitPlan plan = split_plan(a.position, a.context, a.splits);
     __builtin_amdgcn_sched_barrier(0);
@@ -192,11 +204,11 @@ __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
     const float inv_l = 1.0f / l;
 #pragma unroll
     for (int e = 0; e < E; e += 4)
-    {
-        const float4 v = make_float4(o[e] * inv_l, o[e + 1] * inv_l, o[e + 2] * inv_l, o[e + 3] * inv_l);
-        *reinterpret_cast<float4 *>(&xs[o0 + e]) = v;
-        if (a.attn && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.attn + o0 + e) = v;
-    }
+        if (merger) {
+            const float4 v = make_float4(o[e] * inv_l, o[e + 1] * inv_l, o[e + 2] * inv_l, o[e + 3] * inv_l);
+            *reinterpret_cast<float4 *>(&xs[o0 + e]) = v;
+            if (a.attn && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.attn + o0 + e) = v;
+        }
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     Frag<NG> f;
@@ -669,7 +681,8 @@ int launch_attn_out(hipStream_t s, const AttnOutLaunch &l) {
     a.position = l.position;
     a.context = l.context;
     a.splits = l.splits;
-    // 2048 columns: 8 waves of one row (256 workgroups for 2048 rows); 1024: 4 waves of two.
+    // 2048 columns: 8 waves of one row (256 workgroups for 2048 rows; 16-wave groups,
+    // half the merge traffic, measured slower: 4.98 against 4.52 us); 1024: 4 waves of two.
 #define VX_AO(WTV, NGV, HDV, RPWV, WPBV)                                                                   \
     do {                                                                                                   \
         const uint32_t grid = (l.mv.rows + (WPBV) * (RPWV) - 1) / ((WPBV) * (RPWV));                      \
