@@ -408,7 +408,9 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
         const float v = h[i] * inv_rms * a.w[i];
         if (a.y) a.y[(size_t)t * a.ldy + i] = v;
         if (a.yh) {
-            const size_t o = a.tiled ? tiled_plane_index(t, i, a.n) : (size_t)t * a.ldp + i;
+            const size_t o = a.tiled == 1   ? tiled_plane_index(t, i, a.n)
+                             : a.tiled == 2 ? frag16_index(t, i, a.n)
+                                            : (size_t)t * a.ldp + i;
             const _Float16 hv = (_Float16)v;
             a.yh[o] = __builtin_bit_cast(__half, hv);
             a.yl[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
@@ -481,7 +483,9 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
         if (a.y) *reinterpret_cast<float4 *>(a.y + (size_t)t * a.ldy + c) = make_float4(o[0], o[1], o[2], o[3]);
         if (a.yh) {
             // Four columns from a multiple of 4 stay inside one 8-column chunk.
-            const size_t po = a.tiled ? tiled_plane_index(t, c, a.n) : (size_t)t * a.ldp + c;
+            const size_t po = a.tiled == 1   ? tiled_plane_index(t, c, a.n)
+                              : a.tiled == 2 ? frag16_index(t, c, a.n)
+                                             : (size_t)t * a.ldp + c;
             uint2 hi, lo;
             split4(make_float4(o[0], o[1], o[2], o[3]), hi, lo);
             *reinterpret_cast<uint2 *>(a.yh + po) = hi;
@@ -913,7 +917,9 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 // per row (lane per key), the values thread per (row, dim); each dot product and
 // sum runs in the order of the three-kernel path.
 constexpr uint32_t kDenseFusedRows = 8;
-template <int HD>   // head_dim when known at compile time (the dot loops unroll), 0: a.head_dim
+// NSLAB > 1 (float4 staging only): q, k and v are the sums of NSLAB partial
+// slabs a.slab_stride floats apart (a split-K projection's plain-store output).
+template <int HD, int NSLAB = 1>   // HD: head_dim when known at compile time (the dot loops unroll), 0: a.head_dim
 __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     extern __shared__ float sm[];
     const uint32_t h = blockIdx.x, bz = blockIdx.y, t0 = blockIdx.z * kDenseFusedRows;
@@ -924,31 +930,107 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     const float *q = a.q + ((size_t)bz * S + t0) * a.q_stride + (size_t)h * D;
     const float *k = a.k + (size_t)bz * S * a.k_stride + (size_t)kv * D;
     const float *v = a.v + (size_t)bz * S * a.v_stride + (size_t)kv * D;
-    float *out = a.out + ((size_t)bz * S + t0) * a.out_stride + (size_t)h * D;
+    const size_t ob = ((size_t)bz * S + t0) * a.out_stride + (size_t)h * D;
     float *ks = sm, *vs = ks + S * DP, *qs = vs + S * DP, *ps = qs + kDenseFusedRows * DP;
-    for (uint32_t i = tid; i < S * D; i += 256u) {
-        const uint32_t t = i / D, d = i - t * D;
-        vs[t * DP + d] = v[(size_t)t * a.v_stride + d];
-        if (!a.rope) ks[t * DP + d] = k[(size_t)t * a.k_stride + d];
-    }
-    if (!a.rope) {
-        for (uint32_t i = tid; i < R * D; i += 256u) {
-            const uint32_t t = i / D, d = i - t * D;
-            qs[t * DP + d] = q[(size_t)t * a.q_stride + d];
+    bool staged = false;
+    if constexpr (HD > 0) {
+        if (a.vec && a.rope) {
+            // Every global load of the stage is issued before the first LDS store:
+            // V rows as float4 chunks, and for K and the query rows the two float4
+            // chunks of a rotated pair (d..d+3, d+D/2..d+D/2+3) with their (cos, sin).
+            constexpr uint32_t H2 = HD / 2, C4 = H2 / 4, V4 = HD / 4;
+            constexpr uint32_t NV = (kDenseFusedMaxTokens * V4 + 255u) / 256u;
+            constexpr uint32_t NKQ = ((kDenseFusedMaxTokens + kDenseFusedRows) * C4 + 255u) / 256u;
+            const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 vv[NV], x0[NKQ], x1[NKQ], c01[NKQ], c23[NKQ];
+#pragma unroll
+            for (uint32_t j = 0; j < NV; ++j) {
+                const uint32_t i = tid + 256u * j, t = i / V4, c = i - t * V4;
+                vv[j] = z4;
+                if (i < S * V4) {
+                    const float *src = v + (size_t)t * a.v_stride + 4u * c;
+                    vv[j] = *reinterpret_cast<const float4 *>(src);
+#pragma unroll
+                    for (int sl = 1; sl < NSLAB; ++sl) vv[j] += *reinterpret_cast<const float4 *>(src + sl * a.slab_stride);
+                }
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < NKQ; ++j) {
+                const uint32_t i = tid + 256u * j, r = i / C4, c = i - r * C4;
+                x0[j] = x1[j] = c01[j] = c23[j] = z4;
+                if (i < (S + R) * C4) {
+                    const bool isk = r < S;
+                    const uint32_t t = isk ? r : r - S, pos = isk ? t : t0 + t;
+                    const float *row = isk ? k + (size_t)t * a.k_stride : q + (size_t)t * a.q_stride;
+                    x0[j] = *reinterpret_cast<const float4 *>(row + 4u * c);
+                    x1[j] = *reinterpret_cast<const float4 *>(row + H2 + 4u * c);
+#pragma unroll
+                    for (int sl = 1; sl < NSLAB; ++sl) {
+                        x0[j] += *reinterpret_cast<const float4 *>(row + sl * a.slab_stride + 4u * c);
+                        x1[j] += *reinterpret_cast<const float4 *>(row + sl * a.slab_stride + H2 + 4u * c);
+                    }
+                    const float4 *cs = reinterpret_cast<const float4 *>(a.rope + (size_t)pos * H2 + 4u * c);
+                    c01[j] = cs[0];
+                    c23[j] = cs[1];
+                }
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < NV; ++j) {
+                const uint32_t i = tid + 256u * j, t = i / V4, c = i - t * V4;
+                if (i < S * V4) {
+                    float *dst = vs + t * DP + 4u * c;
+                    dst[0] = vv[j].x;
+                    dst[1] = vv[j].y;
+                    dst[2] = vv[j].z;
+                    dst[3] = vv[j].w;
+                }
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < NKQ; ++j) {
+                const uint32_t i = tid + 256u * j, r = i / C4, c = i - r * C4;
+                if (i < (S + R) * C4) {
+                    const bool isk = r < S;
+                    const uint32_t t = isk ? r : r - S;
+                    float *dst = (isk ? ks : qs) + t * DP + 4u * c;
+                    const float a0[4] = {x0[j].x, x0[j].y, x0[j].z, x0[j].w};
+                    const float a1[4] = {x1[j].x, x1[j].y, x1[j].z, x1[j].w};
+                    const float co[4] = {c01[j].x, c01[j].z, c23[j].x, c23[j].z};
+                    const float si[4] = {c01[j].y, c01[j].w, c23[j].y, c23[j].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dst[e] = a0[e] * co[e] - a1[e] * si[e];
+                        dst[e + H2] = a1[e] * co[e] + a0[e] * si[e];
+                    }
+                }
+            }
+            staged = true;
         }
-    } else {
-        // Rotated pairs (d, d + D/2) at the row's position within its sequence.
-        const uint32_t half = D >> 1;
-        for (uint32_t i = tid; i < (S + R) * half; i += 256u) {
-            const uint32_t r = i / half, d = i - r * half;
-            const bool isk = r < S;
-            const uint32_t t = isk ? r : r - S, pos = isk ? t : t0 + t;
-            const float *row = isk ? k + (size_t)t * a.k_stride : q + (size_t)t * a.q_stride;
-            float *dst = (isk ? ks : qs) + t * DP;
-            const float x0 = row[d], x1 = row[d + half];
-            const float2 cs = a.rope[pos * half + d];
-            dst[d] = x0 * cs.x - x1 * cs.y;
-            dst[d + half] = x1 * cs.x + x0 * cs.y;
+    }
+    if (!staged) {
+        for (uint32_t i = tid; i < S * D; i += 256u) {
+            const uint32_t t = i / D, d = i - t * D;
+            vs[t * DP + d] = v[(size_t)t * a.v_stride + d];
+            if (!a.rope) ks[t * DP + d] = k[(size_t)t * a.k_stride + d];
+        }
+        if (!a.rope) {
+            for (uint32_t i = tid; i < R * D; i += 256u) {
+                const uint32_t t = i / D, d = i - t * D;
+                qs[t * DP + d] = q[(size_t)t * a.q_stride + d];
+            }
+        } else {
+            // Rotated pairs (d, d + D/2) at the row's position within its sequence.
+            const uint32_t half = D >> 1;
+            for (uint32_t i = tid; i < (S + R) * half; i += 256u) {
+                const uint32_t r = i / half, d = i - r * half;
+                const bool isk = r < S;
+                const uint32_t t = isk ? r : r - S, pos = isk ? t : t0 + t;
+                const float *row = isk ? k + (size_t)t * a.k_stride : q + (size_t)t * a.q_stride;
+                float *dst = (isk ? ks : qs) + t * DP;
+                const float x0 = row[d], x1 = row[d + half];
+                const float2 cs = a.rope[pos * half + d];
+                dst[d] = x0 * cs.x - x1 * cs.y;
+                dst[d + half] = x1 * cs.x + x0 * cs.y;
+            }
         }
     }
     __syncthreads();
@@ -978,7 +1060,15 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
         float z = 0.f;
 #pragma unroll 8
         for (uint32_t key = 0; key < S; ++key) z += ps[t * S + key] * vs[key * DP + d];
-        out[(size_t)t * a.out_stride + d] = z;
+        const size_t po = a.o_frag ? frag16_index((bz * S + t0 + t), h * D + d, a.out_stride)
+                                   : ob + (size_t)t * a.out_stride + d;
+        if (a.oh) {
+            const _Float16 hv = (_Float16)z;
+            a.oh[po] = __builtin_bit_cast(__half, hv);
+            a.ol[po] = __builtin_bit_cast(__half, (_Float16)(z - (float)hv));
+        } else {
+            a.out[po] = z;
+        }
     }
 }
 
@@ -1002,7 +1092,8 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
             return fail(VX_ERR_INVALID_ARG, "gemm swiglu: needs gate and up of equal rows");
         tiles = (a.seg[0].rows + 63u) / 64u;
         if (a.ksplit != 1) return fail(VX_ERR_INVALID_ARG, "gemm swiglu: no split-K");
-        if (a.oh && (!a.ol || !a.ldp)) return fail(VX_ERR_INVALID_ARG, "gemm swiglu: plane output incomplete");
+        if (a.oh && (!a.ol || (!a.ldp && !a.frag)))
+            return fail(VX_ERR_INVALID_ARG, "gemm swiglu: plane output incomplete");
     } else {
         for (uint32_t i = 0; i < a.nseg; ++i) {
             a.seg[i].tile0 = tiles;
@@ -1016,8 +1107,12 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
             return fail(VX_ERR_INVALID_ARG, "gemm: segment %u weight pointers missing", i);
     }
     if (gemm_q8p_eligible(a)) return launch_gemm_q8p(s, a);
+    if (gemm_skinny_eligible(a)) return launch_gemm_skinny(s, a);
+    if (a.frag)
+        return fail(VX_ERR_UNSUPPORTED, "gemm: fragment-layout operands need the short-batch kernel (F16, T <= 128, "
+                                        "16-byte aligned, K %% 32 == 0; got T=%u K=%u)", a.T, a.K);
     if (a.split_store && a.ksplit > 1)
-        return fail(VX_ERR_INVALID_ARG, "gemm: split partial stores need the prefill-layout Q8_0 kernel");
+        return fail(VX_ERR_INVALID_ARG, "gemm: split partial stores need the prefill-layout Q8_0 or the short-batch F16 kernel");
     const uint32_t stages = a.K / GK;
     if (a.ksplit == 0) a.ksplit = 1;
     if (a.ksplit > stages) a.ksplit = stages;
@@ -1163,13 +1258,28 @@ int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a) {
     if (a.tokens > kDenseFusedMaxTokens || a.head_dim == 0 || lds > 65536u)
         return fail(VX_ERR_UNSUPPORTED, "fused dense attention: %u tokens x head_dim %u do not fit", a.tokens,
                     a.head_dim);
+    if (a.oh && !a.ol) return fail(VX_ERR_INVALID_ARG, "fused dense attention: plane output incomplete");
+    if (!a.oh && !a.out) return fail(VX_ERR_INVALID_ARG, "fused dense attention: no output");
+    if (a.o_frag && (!a.oh || a.out_stride % 32u))
+        return fail(VX_ERR_INVALID_ARG, "fused dense attention: fragment-layout planes need width %% 32");
+    DenseAttnArgs b = a;
+    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    b.vec = a.q_stride % 4u == 0 && a.k_stride % 4u == 0 && a.v_stride % 4u == 0 && al16(a.q) && al16(a.k) &&
+            al16(a.v) && al16(a.rope);
+    if (a.nslab > 2 || (a.nslab == 2 && (!b.vec || !a.rope || (a.head_dim != 64u && a.head_dim != 128u) ||
+                                          a.slab_stride % 4u)))
+        return fail(VX_ERR_UNSUPPORTED, "fused dense attention: %u input slabs", a.nslab);
     const dim3 grid(a.q_heads, a.batch, (a.tokens + kDenseFusedRows - 1u) / kDenseFusedRows);
-    if (a.head_dim == 64u)
-        k_dense_attn_fused<64><<<grid, 256, (size_t)lds, s>>>(a);
+    if (a.head_dim == 64u && a.nslab == 2)
+        k_dense_attn_fused<64, 2><<<grid, 256, (size_t)lds, s>>>(b);
+    else if (a.head_dim == 128u && a.nslab == 2)
+        k_dense_attn_fused<128, 2><<<grid, 256, (size_t)lds, s>>>(b);
+    else if (a.head_dim == 64u)
+        k_dense_attn_fused<64><<<grid, 256, (size_t)lds, s>>>(b);
     else if (a.head_dim == 128u)
-        k_dense_attn_fused<128><<<grid, 256, (size_t)lds, s>>>(a);
+        k_dense_attn_fused<128><<<grid, 256, (size_t)lds, s>>>(b);
     else
-        k_dense_attn_fused<0><<<grid, 256, (size_t)lds, s>>>(a);
+        k_dense_attn_fused<0><<<grid, 256, (size_t)lds, s>>>(b);
     VX_LAUNCHED("k_dense_attn_fused");
     return VX_OK;
 }

@@ -32,6 +32,9 @@ namespace {
 struct LocLayer {
     WRef q, k, v, o, gate, up, down;
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    // The same matrices in the fragment layout (frag16_index), for the short-batch
+    // layer stack: q, k, v, o, gate, up, down.
+    const __half *frag[7] = {};
 };
 
 struct Lin {
@@ -64,6 +67,16 @@ struct vx_locdit {
     vx_buf *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     vx_buf *gate = nullptr, *branch = nullptr, *scores = nullptr, *out = nullptr, *seed = nullptr;
     vx_buf *rope_tab = nullptr;   // (cos, sin) per position of a sequence, for the fused attention
+    // Short-batch layer stack (the CFG batch fits the short-batch GEMM): normed
+    // activations, attention output and SwiGLU output as hi/lo f16 planes, and
+    // the split-K partial slabs of attn_output and ffn_down, summed by the
+    // residual rmsnorm that follows each.
+    bool sk = false;
+    uint32_t ks_qkv = 1, ks_o = 1, ks_down = 1;
+    vx_buf *qkvp = nullptr;   // q | k | v rows of each of ks_qkv partial slabs
+    vx_buf *yh = nullptr, *yl = nullptr, *ah = nullptr, *al = nullptr, *acth = nullptr, *actl = nullptr;
+    vx_buf *part = nullptr;
+    vx_buf *wfrag = nullptr;   // every layer's matrices in the fragment layout
     // Time embeddings of every estimator call of a solve, computed as one batch:
     // t values, sinusoid rows, MLP hidden rows, embeddings ([steps][hidden]).
     vx_buf *tvals = nullptr, *trows = nullptr, *tmid = nullptr, *temb = nullptr;
@@ -146,7 +159,9 @@ void free_all(vx_locdit *e) {
                        &e->ttmp,   &e->tvec,    &e->dsin, &e->dtmp,       &e->dvec,          &e->hidden,
                        &e->norm,   &e->q,       &e->k,    &e->v,          &e->attn,          &e->gate,
                        &e->branch, &e->scores,  &e->out,  &e->seed,       &e->rope_tab,
-                       &e->tvals,  &e->trows,   &e->tmid, &e->temb};
+                       &e->tvals,  &e->trows,   &e->tmid, &e->temb,       &e->yh,            &e->yl,
+                       &e->ah,     &e->al,      &e->acth, &e->actl,       &e->part,          &e->wfrag,
+                       &e->qkvp};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -201,32 +216,16 @@ int enqueue_inputs(vx_locdit *e) {
     return VX_OK;
 }
 
-// pack_locdit + record_transformer + out_proj for `batch` sequences (1: the
-// conditional pass; 2: conditional then unconditional).
-int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) {
+// record_transformer (local.rs:482-527) with the general kernels: k_gemm
+// projections (split K by atomic adds into accumulators that the rmsnorm kernels
+// clear), the fused or three-kernel dense attention, and separate residual
+// rmsnorms.
+int enqueue_layers_general(vx_locdit *e, uint32_t batch) {
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_locdit_config &c = e->cfg;
     const uint32_t H = c.hidden, S = e->S, M = S * batch;
     const uint32_t QD = c.q_heads * c.head_dim, KD = c.kv_heads * c.head_dim;
-    {
-        ProfSpan sp(ctx, "local.pack_locdit");
-        PackLocditArgs p;
-        p.mu[0] = F(e->mu);
-        p.mu[1] = F(e->mu) + H;
-        p.time = time_row ? time_row : F(e->tvec);
-        p.cond = c.cond_raw ? F(e->cond_in) : F(e->cond_proj_out);
-        p.x = F(e->patch_proj);
-        p.out = F(e->hidden);
-        p.hidden = H;
-        p.n_mu = c.n_mu;
-        p.n_cond = c.n_cond;
-        p.n_x = c.patch;
-        p.batch = batch;
-        p.zero_mu_mask = 0x2u;                               // the unconditional sequence (local.rs:413-421)
-        p.zero_cond_mask = c.uncond_zero_cond ? 0x2u : 0u;
-        VX_CHECK(launch_pack_locdit(s, p));
-    }
     // Split-K projections add into outputs that the rmsnorm kernels clear on the
     // way: the first norm clears q, k, v and the branch; the residual norm after
     // attn_out clears the branch (the down projection's accumulator) once it has
@@ -344,6 +343,189 @@ int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) 
             for (int z = 0; z < 3; ++z) r.zero[z] = nullptr;
         }
     }
+    return VX_OK;
+}
+
+// record_transformer (local.rs:482-527) for a batch that fits the short-batch
+// GEMM (kernels_skinny.hip), five kernels per sublayer pair and no cleared
+// accumulators:
+//   rmsnorm -> hi/lo planes y
+//   q, k, v = y . Wq|Wk|Wv                       (one GEMM, plain stores)
+//   fused dense attention (RoPE while staging)   -> hi/lo planes of the output
+//   attn_output: K split into ks_o partial slabs (plain stores)
+//   residual rmsnorm: h += sum of the slabs, y = norm(h) * ffn_norm -> planes
+//   gate/up with the SwiGLU epilogue             -> hi/lo planes
+//   ffn_down: K split into ks_down partial slabs
+//   residual rmsnorm: h += sum of the slabs, y = norm(h) * next attn_norm -> planes
+//     (after the last layer: * locdit.norm, f32 rows for out_proj)
+int enqueue_layers_sk(vx_locdit *e, uint32_t batch) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_locdit_config &c = e->cfg;
+    const uint32_t H = c.hidden, S = e->S, M = S * batch;
+    const uint32_t QD = c.q_heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    __half *yh = static_cast<__half *>(e->yh->ptr), *yl = static_cast<__half *>(e->yl->ptr);
+    __half *ah = static_cast<__half *>(e->ah->ptr), *al = static_cast<__half *>(e->al->ptr);
+    __half *acth = static_cast<__half *>(e->acth->ptr), *actl = static_cast<__half *>(e->actl->ptr);
+    float *part = F(e->part);
+    auto wseg = [](const __half *w, uint32_t rows, float *out, uint32_t ldo) {
+        GemmSeg g;
+        g.w = w;
+        g.rows = rows;
+        g.out = out;
+        g.ldo = ldo;
+        return g;
+    };
+    auto gemm = [&](const __half *xh, const __half *xl, uint32_t K) {
+        GemmArgs g;
+        g.wk = WT_F16;
+        g.epi = GEPI_STORE;
+        g.xh = xh;
+        g.xl = xl;
+        g.ldx = K;
+        g.K = K;
+        g.T = M;
+        g.frag = 1;
+        return g;
+    };
+    SeqNormArgs n;
+    n.h = F(e->hidden);
+    n.ldh = H;
+    n.w = e->layers[0].attn_norm;
+    n.n = H;
+    n.eps = c.rms_epsilon;
+    n.yh = yh;
+    n.yl = yl;
+    n.tiled = 2;   // planes in the fragment layout
+    {
+        ProfSpan sp(ctx, "local.seq_rmsnorm");
+        VX_CHECK(launch_seq_rmsnorm(s, n, M));
+    }
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const LocLayer &L = e->layers[l];
+        float *qp = F(e->qkvp), *kp = qp + (size_t)M * QD, *vp = kp + (size_t)M * KD;
+        const uint64_t qkv_slab = (uint64_t)M * (QD + 2u * KD);
+        {
+            ProfSpan sp(ctx, "local.seq_qkv");
+            GemmArgs g = gemm(yh, yl, H);
+            g.seg[0] = wseg(L.frag[0], QD, qp, QD);
+            g.seg[1] = wseg(L.frag[1], KD, kp, KD);
+            g.seg[2] = wseg(L.frag[2], KD, vp, KD);
+            g.nseg = 3;
+            g.ksplit = e->ks_qkv;
+            g.split_store = 1;
+            g.ws_stride = qkv_slab;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "local.attention");
+            DenseAttnArgs a;
+            a.q = qp;
+            a.k = kp;
+            a.v = vp;
+            a.nslab = e->ks_qkv;
+            a.slab_stride = qkv_slab;
+            a.out = F(e->attn);
+            a.oh = ah;
+            a.ol = al;
+            a.o_frag = 1;
+            a.tokens = S;
+            a.q_heads = c.q_heads;
+            a.kv_heads = c.kv_heads;
+            a.head_dim = c.head_dim;
+            a.q_stride = QD;
+            a.k_stride = KD;
+            a.v_stride = KD;
+            a.out_stride = QD;
+            a.score_stride = S;
+            a.batch = batch;
+            a.rope = reinterpret_cast<const float2 *>(e->rope_tab->ptr);
+            VX_CHECK(launch_dense_attn_fused(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_linear");
+            GemmArgs g = gemm(ah, al, QD);
+            g.seg[0] = wseg(L.frag[3], H, part, H);
+            g.ksplit = e->ks_o;
+            g.split_store = 1;
+            g.ws_stride = (uint64_t)M * H;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        SeqNormArgs r = n;
+        r.branch = part;
+        r.ldb = H;
+        r.scale = 1.f;
+        {
+            ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
+            r.nbranch = e->ks_o;
+            r.branch_stride = (uint64_t)M * H;
+            r.w = L.ffn_norm;
+            VX_CHECK(launch_seq_rmsnorm(s, r, M));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_swiglu");
+            GemmArgs g = gemm(yh, yl, H);
+            g.epi = GEPI_SWIGLU;
+            g.seg[0] = wseg(L.frag[4], c.ffn, nullptr, 0);
+            g.seg[1] = wseg(L.frag[5], c.ffn, nullptr, 0);
+            g.nseg = 2;
+            g.oh = acth;
+            g.ol = actl;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_linear");
+            GemmArgs g = gemm(acth, actl, c.ffn);
+            g.seg[0] = wseg(L.frag[6], H, part, H);
+            g.ksplit = e->ks_down;
+            g.split_store = 1;
+            g.ws_stride = (uint64_t)M * H;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
+            const bool last = l + 1 == c.layers;
+            r.nbranch = e->ks_down;
+            r.branch_stride = (uint64_t)M * H;
+            r.w = last ? e->norm_w : e->layers[l + 1].attn_norm;
+            if (last) {   // out_proj reads f32 rows
+                r.y = F(e->norm);
+                r.ldy = H;
+                r.yh = r.yl = nullptr;
+                r.tiled = 0;
+            }
+            VX_CHECK(launch_seq_rmsnorm(s, r, M));
+        }
+    }
+    return VX_OK;
+}
+
+// pack_locdit + record_transformer + out_proj for `batch` sequences (1: the
+// conditional pass; 2: conditional then unconditional).
+int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_locdit_config &c = e->cfg;
+    const uint32_t H = c.hidden, S = e->S;
+    {
+        ProfSpan sp(ctx, "local.pack_locdit");
+        PackLocditArgs p;
+        p.mu[0] = F(e->mu);
+        p.mu[1] = F(e->mu) + H;
+        p.time = time_row ? time_row : F(e->tvec);
+        p.cond = c.cond_raw ? F(e->cond_in) : F(e->cond_proj_out);
+        p.x = F(e->patch_proj);
+        p.out = F(e->hidden);
+        p.hidden = H;
+        p.n_mu = c.n_mu;
+        p.n_cond = c.n_cond;
+        p.n_x = c.patch;
+        p.batch = batch;
+        p.zero_mu_mask = 0x2u;                               // the unconditional sequence (local.rs:413-421)
+        p.zero_cond_mask = c.uncond_zero_cond ? 0x2u : 0u;
+        VX_CHECK(launch_pack_locdit(s, p));
+    }
+    VX_CHECK(e->sk ? enqueue_layers_sk(e, batch) : enqueue_layers_general(e, batch));
     ProfSpan sp(ctx, "local.locdit_out");
     const uint32_t x0 = c.n_mu + 1u + c.n_cond;   // first x token of a sequence
     for (uint32_t b = 0; b < batch; ++b)
@@ -613,6 +795,66 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
     for (auto &b : bufs)
         if (hipMemsetAsync((*b.b)->ptr, 0, (*b.b)->bytes, ctx->stream) != hipSuccess)
             return bail(fail(VX_ERR_HIP, "hipMemsetAsync of LocDiT state failed"));
+    // The short-batch layer stack when the CFG batch and every projection fit the
+    // short-batch GEMM (at most 128 rows, K and N multiples of 128, 16-byte
+    // aligned F16 rows) and the attention runs fused.
+    {
+        auto al16 = [](const WRef &w) { return (reinterpret_cast<uintptr_t>(w.ptr) & 15u) == 0; };
+        bool ok = e->dense_fused && S2 <= 128u && H % 128u == 0 && QD % 128u == 0 && KD % 32u == 0 &&
+                  c.ffn % 128u == 0 && c.head_dim % 8u == 0;
+        for (const LocLayer &L : e->layers)
+            ok = ok && al16(L.q) && al16(L.k) && al16(L.v) && al16(L.o) && al16(L.gate) && al16(L.up) && al16(L.down);
+        if (ok) {
+            // K slabs of attn_output and ffn_down: about one workgroup per CU, at
+            // least four 32-column k-steps per slab, at most the branches the
+            // residual rmsnorm sums.
+            const uint32_t cus = std::max(1, ctx->props.multiProcessorCount);
+            auto slabs = [&](uint32_t rows, uint32_t K) {
+                const uint32_t tiles = (rows + 31u) / 32u;
+                uint32_t k = std::max(1u, cus / tiles);
+                k = std::min(k, std::min(kSeqNormMaxBranch, K / 128u));
+                return std::max(1u, k);
+            };
+            e->ks_qkv = std::min(2u, slabs(QD + 2u * KD, H));   // the attention sums at most two
+            e->ks_o = slabs(H, QD);
+            e->ks_down = slabs(H, c.ffn);
+            const uint64_t ks = std::max(e->ks_o, e->ks_down);
+            const uint64_t R16 = (S2 + 15u) & ~15ull;   // plane rows, padded to whole fragments
+            struct {
+                vx_buf **b;
+                uint64_t bytes;
+            } sk[] = {{&e->yh, R16 * H * 2u},          {&e->yl, R16 * H * 2u},
+                      {&e->ah, R16 * QD * 2u},         {&e->al, R16 * QD * 2u},
+                      {&e->acth, R16 * c.ffn * 2u},    {&e->actl, R16 * c.ffn * 2u},
+                      {&e->part, ks * S2 * H * 4u},
+                      {&e->qkvp, (uint64_t)e->ks_qkv * S2 * (QD + 2u * KD) * 4u}};
+            for (auto &b : sk) {
+                if ((st = vx_alloc(ctx, b.bytes, b.b))) return bail(st);
+                if (hipMemsetAsync((*b.b)->ptr, 0, (*b.b)->bytes, ctx->stream) != hipSuccess)
+                    return bail(fail(VX_ERR_HIP, "hipMemsetAsync of LocDiT state failed"));
+            }
+            // The layer matrices in the fragment layout (a second copy of the
+            // LocDiT weights, streamed by the short-batch GEMM).
+            auto pad16 = [](uint64_t r) { return (r + 15u) & ~15ull; };
+            const uint64_t per_layer = (pad16(QD) + 2u * pad16(KD)) * H + pad16(H) * QD + 2u * pad16(c.ffn) * H +
+                                       pad16(H) * c.ffn;
+            if ((st = vx_alloc(ctx, per_layer * c.layers * 2u, &e->wfrag))) return bail(st);
+            __half *dst = static_cast<__half *>(e->wfrag->ptr);
+            for (LocLayer &L : e->layers) {
+                const WRef *m[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+                const uint32_t rows[7] = {QD, KD, KD, H, c.ffn, c.ffn, H};
+                const uint32_t cols[7] = {H, H, H, QD, H, H, c.ffn};
+                for (int i = 0; i < 7; ++i) {
+                    if ((st = launch_repack_frag16(ctx->stream, static_cast<const __half *>(m[i]->ptr), dst, rows[i],
+                                                   cols[i])))
+                        return bail(st);
+                    L.frag[i] = dst;
+                    dst += pad16(rows[i]) * cols[i];
+                }
+            }
+            e->sk = true;
+        }
+    }
     if (e->dense_fused && (st = launch_rope_pos_table(ctx->stream, reinterpret_cast<float2 *>(e->rope_tab->ptr),
                                                       e->rope_factors, e->S, c.head_dim, c.rope_theta,
                                                       c.rope_scaling)))

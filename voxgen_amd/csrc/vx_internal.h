@@ -329,8 +329,30 @@ struct GemmArgs {
     // stores alpha * (its partial product) to out + s * ws_stride (each segment's
     // [T][ldo]) with plain stores instead of atomic adds; the consumer sums them.
     uint32_t split_store = 0;
+    // 1: the short-batch F16 kernel's operand layout: the weights (seg[i].w) and
+    // the X planes are in the fragment layout (frag16_index), and GEPI_SWIGLU
+    // writes oh/ol in it (width seg[0].rows).
+    uint32_t frag = 0;
 };
 int launch_gemm(hipStream_t s, const GemmArgs &a);
+// Short-batch F16 kernel (kernels_skinny.hip): operands in the fragment layout
+// (GemmArgs::frag), T <= 128, GEPI_STORE (split K only as partial slabs,
+// split_store) or GEPI_SWIGLU. launch_gemm takes every call with frag set.
+bool gemm_skinny_eligible(const GemmArgs &a);
+int launch_gemm_skinny(hipStream_t s, GemmArgs a);
+// Fragment layout of a matrix with K columns (K % 32 == 0) and rows padded to a
+// multiple of 16: one contiguous 1 KB block per 16 rows x 32 columns, blocks of a
+// 16-row group consecutive along K; inside a block, lane l = r + 16 g (r = row
+// % 16, g = column % 32 / 8) holds columns 8g..8g+7 of row r, eight halves. A
+// wave64 16-byte load of one block is then exactly the A or B operand of
+// v_mfma_f32_16x16x32_f16 (rows along M or N, the block's 32 columns along K),
+// and every operand load is 1 KB of contiguous bytes.
+__host__ __device__ __forceinline__ size_t frag16_index(uint32_t r, uint32_t c, uint32_t K) {
+    return (((size_t)(r >> 4) * (K >> 5) + (c >> 5)) << 9) + ((((c >> 3) & 3u) << 4) + (r & 15u)) * 8u + (c & 7u);
+}
+// Rewrites an F16 [rows][K] row-major matrix in the fragment layout (rows padded
+// to a multiple of 16 with zeros): dst holds ceil(rows/16)*16*K halves.
+int launch_repack_frag16(hipStream_t s, const __half *src, __half *dst, uint32_t rows, uint32_t K);
 // Tiled hi/lo plane layout read by the prefill GEMM (kernels_gemm.hip):
 // f16 [T/128][K/32][128][32], i.e. one contiguous 8 KB piece per (128-token
 // tile, 32-column block); the four 8-column chunks of a token's 32 values are
@@ -380,7 +402,8 @@ struct SeqNormArgs {
     uint32_t ldy = 0;
     __half *yh = nullptr, *yl = nullptr;   // nullable hi/lo planes [T][ldp]
     uint32_t ldp = 0;
-    uint32_t tiled = 0;             // 1: planes in the tiled layout of width n (ldp unused)
+    uint32_t tiled = 0;             // 1: planes in the tiled layout of width n, 2: in the fragment
+                                    // layout of width n (frag16_index); ldp unused for both
     float *zero[4] = {nullptr, nullptr, nullptr, nullptr};   // rows of split-K accumulators to clear
     uint32_t zero_n[4] = {0, 0, 0, 0};
     // 1: zero the branch rows (every split) after reading them, so the buffer is the
@@ -568,6 +591,15 @@ struct DenseAttnArgs {
     // position within its sequence; q and k rows are then rotated (NeoX pairs d,
     // d + head_dim / 2) as they are staged, in place of a separate RoPE pass.
     const float2 *rope = nullptr;
+    // Fused kernel only, nullable: the output as hi/lo f16 planes (indexed as out)
+    // in place of the f32 out.
+    __half *oh = nullptr, *ol = nullptr;
+    uint32_t o_frag = 0;   // 1: the planes in the fragment layout of width out_stride
+    // Fused kernel only: q, k, v as the sums of nslab (1 or 2) partial slabs,
+    // slab_stride floats apart (float4-aligned rows and RoPE required for 2).
+    uint32_t nslab = 1;
+    uint64_t slab_stride = 0;
+    uint32_t vec = 0;      // set by launch_dense_attn_fused: 16-byte rows, float4 staging
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
 // table[p][i] = (cos, sin)(p * theta^(-2i/head_dim) / factors[i]) * scaling for
