@@ -598,14 +598,19 @@ __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
 // product from the lane's own registers: its register r (key 8(r/4)+4hs+r%4)
 // is used in k-slot 8hs + r%8 of k-step r/8, and the V^T operand supplies the
 // same keys for those slots.
+// K and V are both staged row per key with 16-byte stores (rows of HD + 8
+// halves), and the V^T operand is gathered from the V rows with 2-byte reads
+// (lane l32 reads dim 32dt + l32 of eight keys): the 32 lanes of a half-wave
+// read 64 contiguous bytes of one key row, and the two half-waves' rows (4 keys
+// apart, 4 * (HD + 8) / 2 dwords) start 16 banks apart, so no read conflicts;
+// transposing V in LDS instead took 2-byte stores that collided 16 ways.
 template <int HD, int QPK>
 __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
     constexpr int TPB = 32 / QPK;
-    constexpr int KROW = HD + 8;   // K block row (f16)
-    constexpr int VROW = 40;       // V^T row: 32 keys + 8 pad (f16)
+    constexpr int KROW = HD + 8;   // K and V block row (f16)
     constexpr int ND = HD / 32;    // output tiles of 32 dims
     constexpr int KS = HD / 16;    // k-steps over the head dim
-    constexpr int WAVE_LDS = 32 * KROW + HD * VROW;   // f16 per wave
+    constexpr int WAVE_LDS = 2 * 32 * KROW;   // f16 per wave
     __shared__ __attribute__((aligned(16))) _Float16 lds[4 * WAVE_LDS];
     static_assert(4 * WAVE_LDS * 2 >= 4 * (ND * 16 * 64 * 4 + 2 * 32 * 4), "merge area");
 
@@ -620,7 +625,8 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
     const uint32_t tlast = min(t0 + (uint32_t)TPB, a.T) - 1u;
     const uint32_t kmax = a.pos_base + tlast;   // last key any row of the block needs
     const uint32_t nblocks = kmax / 32u + 1u;
-    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale2 = 1.4426950408889634f / sqrtf((float)HD);   // log2(e) / sqrt(d)
+    constexpr float kLazyMax = 8.0f;
     const uint32_t kv_dim = a.kv_heads * HD;
 
     h8 qh[KS], ql[KS];
@@ -633,35 +639,44 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
         }
     }
     _Float16 *Ks = lds + w * WAVE_LDS;
-    _Float16 *Vt = Ks + 32 * KROW;
+    _Float16 *Vs = Ks + 32 * KROW;
 
     float m = -INFINITY, l = 0.f;
     acc16 o[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) o[dt] = acc16{};
 
+    // K and V rows of a key block, in registers one block ahead of the block
+    // being multiplied (the wave's next block is fetched while it computes).
+    constexpr int CH = 32 * HD / 8 / 64;   // 16-byte chunks per lane per block
+    uint4 kreg[CH], vreg[CH];
+    auto fetch = [&](uint32_t kb) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const uint32_t c = lane + 64u * i, key = c / (HD / 8), p = c % (HD / 8);
+            const uint32_t kp = kb * 32u + key;
+            kreg[i] = vreg[i] = make_uint4(0, 0, 0, 0);
+            if (kb < nblocks && kp <= kmax && kp < a.context) {
+                const size_t src = ((size_t)a.layer * a.context + kp) * kv_dim + g * HD + 8u * p;
+                kreg[i] = *reinterpret_cast<const uint4 *>(a.kc + src);
+                vreg[i] = *reinterpret_cast<const uint4 *>(a.vc + src);
+            }
+        }
+    };
+    fetch(w);
     for (uint32_t kb = w; kb < nblocks; kb += 4u) {
         const uint32_t key0 = kb * 32u;
-        // Stage K (row per key) and V^T (row per dim) of keys key0..key0+31.
-        constexpr int CHUNKS = 32 * HD / 8;   // 16-byte chunks per block
+        // Stage K and V (row per key) of keys key0..key0+31, then fetch the next block.
 #pragma unroll
-        for (int i = 0; i < CHUNKS / 64; ++i) {
+        for (int i = 0; i < CH; ++i) {
             const uint32_t c = lane + 64u * i, key = c / (HD / 8), p = c % (HD / 8);
-            const uint32_t kp = key0 + key;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-            if (kp <= kmax && kp < a.context) {
-                const size_t src = ((size_t)a.layer * a.context + kp) * kv_dim + g * HD + 8u * p;
-                kv = *reinterpret_cast<const uint4 *>(a.kc + src);
-                vv = *reinterpret_cast<const uint4 *>(a.vc + src);
-            }
-            *reinterpret_cast<uint4 *>(Ks + key * KROW + 8u * p) = kv;
-            const h8 vh = __builtin_bit_cast(h8, vv);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) Vt[(8u * p + j) * VROW + key] = vh[j];
+            *reinterpret_cast<uint4 *>(Ks + key * KROW + 8u * p) = kreg[i];
+            *reinterpret_cast<uint4 *>(Vs + key * KROW + 8u * p) = vreg[i];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        fetch(kb + 4u);
 
         acc16 sc = {};
 #pragma unroll
@@ -670,30 +685,38 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
             sc = mfma(kf, qh[ds], sc);
             sc = mfma(kf, ql[ds], sc);
         }
+        // Scores in log2 units (scale * log2(e) folded in), so p = 2^(s - m).
         float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t key = key0 + 8u * (r >> 2) + 4u * hs + (r & 3);
-            sc[r] = key <= qpos ? sc[r] * scale : -INFINITY;
+            sc[r] = key <= qpos ? sc[r] * scale2 : -INFINITY;
             mloc = fmaxf(mloc, sc[r]);
         }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float mnew = fmaxf(m, mloc);
+        // The row's reference max moves only when the block max exceeds it by more
+        // than kLazyMax (p then stays below 2^kLazyMax, well inside f16), so the
+        // output accumulators are rescaled only on the blocks where some row's
+        // reference moved.
+        const float mnew = mloc > m + kLazyMax ? mloc : m;
         float lsum = 0.f;
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            p[r] = sc[r] == -INFINITY ? 0.f : expf(sc[r] - mnew);
+            p[r] = sc[r] == -INFINITY ? 0.f : exp2f(sc[r] - mnew);
             lsum += p[r];
         }
         lsum += __shfl_xor(lsum, 32, 64);
-        const float alpha = m == -INFINITY ? 0.f : expf(m - mnew);
+        const float alpha = m == -INFINITY ? 0.f : exp2f(m - mnew);
         l = l * alpha + lsum;
+        const bool moved = mnew != m;
         m = mnew;
+        if (__any(moved)) {
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
+            for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        }
         h8 ph[2], pl[2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
@@ -708,10 +731,11 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
         for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) {
-                const _Float16 *vr = Vt + (32u * dt + l32) * VROW + 16u * kh + 4u * hs;
-                const h4 v0 = *reinterpret_cast<const h4 *>(vr);
-                const h4 v1 = *reinterpret_cast<const h4 *>(vr + 8);
-                const h8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                // Slot i of k-step kh is key 16kh + 8(i/4) + 4hs + i%4.
+                const _Float16 *vr = Vs + (16u * kh + 4u * hs) * KROW + 32u * dt + l32;
+                h8 vf;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) vf[i] = vr[(8 * (i >> 2) + (i & 3)) * KROW];
                 o[dt] = mfma(vf, ph[kh], o[dt]);
                 o[dt] = mfma(vf, pl[kh], o[dt]);
             }
@@ -744,7 +768,7 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
         float wt[4], L = 0.f;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            wt[v] = mw[v] == -INFINITY ? 0.f : expf(mw[v] - M);
+            wt[v] = mw[v] == -INFINITY ? 0.f : exp2f(mw[v] - M);
             L += wt[v] * ls[v * 32 + l32];
         }
         const float inv = 1.0f / L;
