@@ -518,7 +518,7 @@ def main():
 
     abi.load()
     K, W, P = args.steps, args.warmup, args.prefill
-    active = max(P + max(K, W) + 1, args.prefill_tokens)
+    active = max(P + max(K, W), args.prefill_tokens)
     cfg = synth.baselm_config(active_context=max(active, 512))
     t0 = time.perf_counter()
     m = synth.build_baselm(cfg, seed=0x5EED0002)
@@ -588,8 +588,10 @@ def main():
     # Per-kernel cost: one layer kernel over the 28 layers' weights as a graph
     # chain, each pass after a 384 MiB read that evicts the MALL (so every launch
     # reads HBM, as in the step), HIP events on the engine stream, the reads
-    # alone subtracted; at the device position P+K. Includes the launch gap.
-    pos_k = P + K
+    # alone subtracted. Includes the launch gap. The device position is then P+K,
+    # one past the context, which the attention clamps to the last cached
+    # position P+K-1 (the qkv kernel stores no KV row there).
+    pos_k = P + K - 1
     per_kernel = {}
     fam_bytes = fam_ms = 0.0
     for name in eng.LAYER_KERNELS:

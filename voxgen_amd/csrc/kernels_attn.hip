@@ -113,9 +113,13 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const uint32_t kv_dim = a.kv_heads * HD;
     const int j = tid >> 2, r = tid & 3;
 
-    // q quarter (independent of the position) and the position, issued together.
-    // Element 8k + e of quarter r is dimension 8(r + 4k) + e, so the four lanes of
-    // a key read 64 contiguous bytes of its row per load.
+    // q and, when the split's keys do not depend on the position
+    // (attn_fixed_chunk), the K and V rows of its one tile are issued
+    // before the position is read: the position is a scalar load issued after
+    // them (a compiler barrier keeps that order), so waiting for it does not wait
+    // for the vector loads.
+    // q quarter: element 8k + e of quarter r is dimension 8(r + 4k) + e, so the
+    // four lanes of a key read 64 contiguous bytes of its row per load.
     float qv[R];
 #pragma unroll
     for (int i = 0; i < R; i += 4) {
@@ -125,23 +129,35 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         qv[i + 2] = v.z;
         qv[i + 3] = v.w;
     }
-    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
+    const float inv_sqrt = 1.0f / sqrtf((float)HD);
+    const size_t layer_base = (size_t)a.layer * a.context;
+    const size_t head_off = (size_t)kvh * HD + (size_t)r * 8;
+    const uint32_t fc = attn_fixed_chunk(a.context, a.splits);
+    const bool fixed = fc <= kAttnFixedChunk;
+    uint4 kpre[R / 8], vpre[R / 8];
+    if (fixed) {
+        const uint32_t key = min(s * fc + (uint32_t)j, a.context - 1u);
+        const size_t row = (layer_base + key) * kv_dim + head_off;
+#pragma unroll
+        for (int i = 0; i < R / 8; ++i) {
+            kpre[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
+            vpre[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
+        }
+    }
+    asm volatile("" ::: "memory");
+    const uint32_t pos_raw = *a.position;
+    const SplitPlan plan = split_plan_at(pos_raw, a.context, a.splits);
     if (s >= plan.active) return;
     const uint32_t t0 = s * plan.chunk;
     const uint32_t t1 = min(plan.n, t0 + plan.chunk);
-    const float inv_sqrt = 1.0f / sqrtf((float)HD);
-    const size_t layer_base = (size_t)a.layer * a.context;
 
     float m_run = -FLT_MAX, l_run = 0.f, acc = 0.f;
-    for (uint32_t tb = t0; tb < t1; tb += kTile) {
+    auto tile = [&](uint32_t tb, const uint4 *kw, uint4 *vw) {
         const uint32_t key = tb + (uint32_t)j;
         const bool valid = key < t1;
-        const size_t row = (layer_base + (valid ? key : t0)) * kv_dim + (size_t)kvh * HD + (size_t)r * 8;
-        uint4 kw[R / 8], vw[R / 8];
+        if (!valid) {   // a fetched row past the slice (or the position) enters with p = 0
 #pragma unroll
-        for (int i = 0; i < R / 8; ++i) {
-            kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
-            vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
+            for (int i = 0; i < R / 8; ++i) vw[i] = make_uint4(0, 0, 0, 0);
         }
         // Score of key j: quarter dot product, then a quad reduction.
         float d0 = 0.f, d1 = 0.f;
@@ -185,6 +201,21 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         }
         acc = acc * corr + v;
         __syncthreads();
+    };
+    if (fixed) {
+        tile(t0, kpre, vpre);
+    } else {
+        for (uint32_t tb = t0; tb < t1; tb += kTile) {
+            const uint32_t key = tb + (uint32_t)j;
+            const size_t row = (layer_base + (key < t1 ? key : t0)) * kv_dim + head_off;
+            uint4 kw[R / 8], vw[R / 8];
+#pragma unroll
+            for (int i = 0; i < R / 8; ++i) {
+                kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
+                vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
+            }
+            tile(tb, kw, vw);
+        }
     }
     accs[tid] = acc;
     __syncthreads();

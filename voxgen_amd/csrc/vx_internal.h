@@ -226,14 +226,32 @@ constexpr uint32_t kAttnMinChunk = 32;      // fewest keys per active split
 struct SplitPlan {
     uint32_t n, active, chunk;
 };
-__device__ __forceinline__ SplitPlan split_plan(const uint32_t *position, uint32_t context, uint32_t splits) {
-    uint32_t pos = *position;
+// Keys of a split when they do not depend on the position: ceil(context /
+// splits), used whenever it is at most kAttnFixedChunk, so that the attention
+// workgroups can fetch their keys before the position arrives.
+constexpr uint32_t kAttnFixedChunk = 64;   // one key tile of k_attn_chunk
+__host__ __device__ __forceinline__ uint32_t attn_fixed_chunk(uint32_t context, uint32_t splits) {
+    return (context + splits - 1u) / splits;
+}
+// The splits of positions 0..pos: slice s is keys [s * chunk, min(n, (s + 1) * chunk)),
+// for s < active. Every kernel that writes or merges the slices computes it the
+// same way from the same position.
+__device__ __forceinline__ SplitPlan split_plan_at(uint32_t pos, uint32_t context, uint32_t splits) {
     if (pos >= context) pos = context - 1u;
     SplitPlan p;
     p.n = pos + 1u;
-    p.active = min(splits, (p.n + kAttnMinChunk - 1u) / kAttnMinChunk);
-    p.chunk = (p.n + p.active - 1u) / p.active;
+    const uint32_t fc = attn_fixed_chunk(context, splits);
+    if (fc <= kAttnFixedChunk) {
+        p.chunk = fc;
+        p.active = (p.n + fc - 1u) / fc;
+    } else {
+        p.active = min(splits, (p.n + kAttnMinChunk - 1u) / kAttnMinChunk);
+        p.chunk = (p.n + p.active - 1u) / p.active;
+    }
     return p;
+}
+__device__ __forceinline__ SplitPlan split_plan(const uint32_t *position, uint32_t context, uint32_t splits) {
+    return split_plan_at(*position, context, splits);
 }
 // attn_out matvec (EPI_RESIDUAL) whose x is merged from the attention partials.
 struct AttnOutLaunch {
