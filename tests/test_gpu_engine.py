@@ -1,5 +1,6 @@
-"""BaseLM engine parity (graph, fused-eager, reference op order and the persistent
-one-kernel step) against the oracle.
+"""BaseLM engine parity (graph, fused-eager and reference op order) against the
+oracle. The persistent one-kernel step, slower than the graph mode and kept only
+as an alternative design, is checked against the graph mode on its own.
 
 One decoder layer at context 512 (the single-layer benchmark workload), short
 multi-layer sequences from position 0 through every decode entry point, error
@@ -15,7 +16,7 @@ from voxgen_amd.baselm import BaseLmEngine
 from voxgen_amd.runtime import Model
 
 pytestmark = pytest.mark.gpu
-MODES = ["graph", "fused", "reference", "persistent"]
+MODES = ["graph", "fused", "reference"]
 
 
 def kv_bits(layers, ctxlen, filled, seed):
@@ -195,7 +196,7 @@ def test_full_stack_from_position_zero(ctx, full_model):
     for pos, t in enumerate(toks):
         wants.append(o.decode_token(t, pos, logits=True))
         tops.append(list(np.argsort(-o.logits, kind="stable")[:5]))
-    for mode in ("graph", "persistent"):
+    for mode in ("graph",):
         eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=True)
         for pos, t in enumerate(toks):
             r = eng.decode_token(t, top_k=5)
@@ -212,7 +213,7 @@ def test_full_stack_decode_at_position_256(ctx, full_model):
     o.kv_k[:] = kk
     o.kv_v[:] = vv
     wants = [o.decode_token(t, 256 + i) for i, t in enumerate(toks)]
-    for mode in ("graph", "reference", "persistent"):
+    for mode in ("graph", "reference"):
         eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=True)
         eng.buffer("kv_k").upload(kk)
         eng.buffer("kv_v").upload(vv)
