@@ -105,6 +105,34 @@ __global__ __launch_bounds__(256) void k_pack_locdit(PackLocditArgs a) {
         v = a.time[d];
     } else if (tok < a.n_mu + 1u + a.n_cond) {
         v = (a.zero_cond_mask >> b) & 1u ? 0.f : a.cond[(tok - a.n_mu - 1u) * a.hidden + d];
+    } else if (a.in_w) {
+        // seq_linear_bias.comp for one x token: bias + W[d] . x (fp32, f16 weights).
+        const uint32_t tx = tok - a.n_mu - 1u - a.n_cond;
+        const __half *w = a.in_w + (size_t)d * a.feat;
+        const float *xp = a.xpatch + (size_t)tx * a.feat;
+        float acc = 0.f;
+        // Eight-column chunks: one 16-byte weight load each, all issued up front
+        // (feat % 8 == 0 and 16-byte rows are checked at launch).
+        constexpr uint32_t kMaxChunks = 16;   // feat <= 128
+        uint4 wc[kMaxChunks];
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxChunks; ++c)
+            wc[c] = 8u * c < a.feat ? *reinterpret_cast<const uint4 *>(w + 8u * c) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxChunks; ++c) {
+            if (8u * c >= a.feat) break;
+            const uint32_t u[4] = {wc[c].x, wc[c].y, wc[c].z, wc[c].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const __half2 h = __builtin_bit_cast(__half2, u[k]);
+                acc = fmaf(__low2float(h), xp[8u * c + 2u * k], acc);
+                acc = fmaf(__high2float(h), xp[8u * c + 2u * k + 1u], acc);
+            }
+        }
+        const float bias = !a.in_b ? 0.f
+                           : a.in_bt == 0 ? static_cast<const float *>(a.in_b)[d]
+                                          : __half2float(static_cast<const __half *>(a.in_b)[d]);
+        v = acc + bias;
     } else {
         v = a.x[(tok - a.n_mu - 1u - a.n_cond) * a.hidden + d];
     }
@@ -163,6 +191,9 @@ int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, con
 int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a) {
     const uint64_t n = (uint64_t)(a.n_mu + 1u + a.n_cond + a.n_x) * a.hidden * a.batch;
     if (!n) return VX_OK;
+    if (a.in_w && (a.feat == 0 || a.feat > 128u || a.feat % 8u || !a.xpatch ||
+                   (reinterpret_cast<uintptr_t>(a.in_w) & 15u)))
+        return fail(VX_ERR_UNSUPPORTED, "pack_locdit: fused in_proj needs feat %% 8 == 0, <= 128, 16-byte rows");
     k_pack_locdit<<<(unsigned)((n + 255u) / 256u), 256, 0, s>>>(a);
     VX_LAUNCHED("k_pack_locdit");
     return VX_OK;

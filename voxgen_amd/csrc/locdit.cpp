@@ -203,13 +203,15 @@ int enqueue_time_rows(vx_locdit *e, uint32_t n) {
     return launch_add_vectors(s, F(e->temb), F(e->dvec), H, n);
 }
 
-// in_proj / cond_proj (record_locdit_common, local.rs:445-449).
+// in_proj / cond_proj (record_locdit_common, local.rs:445-449). The short-batch
+// stack computes in_proj inside the pack instead (enqueue_body).
 int enqueue_inputs(vx_locdit *e) {
     hipStream_t s = e->ctx->stream;
     const vx_locdit_config &c = e->cfg;
     ProfSpan sp(e->ctx, "local.locdit_in");
-    VX_CHECK(enqueue_seq_linear(s, e->in_proj.w, e->in_proj.b, e->in_proj.bt, c.hidden, c.feat_dim, c.patch, F(e->x),
-                                0, c.feat_dim, F(e->patch_proj), 0, c.hidden, 1.f));
+    if (!e->sk)
+        VX_CHECK(enqueue_seq_linear(s, e->in_proj.w, e->in_proj.b, e->in_proj.bt, c.hidden, c.feat_dim, c.patch,
+                                    F(e->x), 0, c.feat_dim, F(e->patch_proj), 0, c.hidden, 1.f));
     if (!c.cond_raw)
         VX_CHECK(enqueue_seq_linear(s, e->cond_proj.w, e->cond_proj.b, e->cond_proj.bt, c.hidden, c.feat_dim, c.patch,
                                     F(e->cond_in), 0, c.feat_dim, F(e->cond_proj_out), 0, c.hidden, 1.f));
@@ -523,6 +525,13 @@ int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) 
         p.batch = batch;
         p.zero_mu_mask = 0x2u;                               // the unconditional sequence (local.rs:413-421)
         p.zero_cond_mask = c.uncond_zero_cond ? 0x2u : 0u;
+        if (e->sk) {   // x tokens = in_proj(x patch) + b, computed by the pack
+            p.in_w = static_cast<const __half *>(e->in_proj.w.ptr);
+            p.in_b = e->in_proj.b;
+            p.in_bt = e->in_proj.bt;
+            p.feat = c.feat_dim;
+            p.xpatch = F(e->x);
+        }
         VX_CHECK(launch_pack_locdit(s, p));
     }
     VX_CHECK(e->sk ? enqueue_layers_sk(e, batch) : enqueue_layers_general(e, batch));
@@ -801,7 +810,8 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
     {
         auto al16 = [](const WRef &w) { return (reinterpret_cast<uintptr_t>(w.ptr) & 15u) == 0; };
         bool ok = e->dense_fused && S2 <= 128u && H % 128u == 0 && QD % 128u == 0 && KD % 32u == 0 &&
-                  c.ffn % 128u == 0 && c.head_dim % 8u == 0;
+                  c.ffn % 128u == 0 && c.head_dim % 8u == 0 && c.feat_dim % 8u == 0 && c.feat_dim <= 128u &&
+                  al16(e->in_proj.w);
         for (const LocLayer &L : e->layers)
             ok = ok && al16(L.q) && al16(L.k) && al16(L.v) && al16(L.o) && al16(L.gate) && al16(L.up) && al16(L.down);
         if (ok) {

@@ -647,6 +647,13 @@ struct PackLocditArgs {
     float *out = nullptr;           // [batch][n_mu + 1 + n_cond + n_x][hidden]
     uint32_t hidden = 0, n_mu = 0, n_cond = 0, n_x = 0, batch = 1;
     uint32_t zero_mu_mask = 0, zero_cond_mask = 0;
+    // Nullable: the x tokens computed here as in_proj(x patch) + b (seq_linear_bias
+    // with F16 weights [hidden][feat], bias f32 (in_bt 0) or f16 (1)) from
+    // xpatch [n_x][feat], in place of the rows at x.
+    const __half *in_w = nullptr;
+    const void *in_b = nullptr;
+    uint32_t in_bt = 0, feat = 0;
+    const float *xpatch = nullptr;
 };
 int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a);
 int launch_silu_inplace(hipStream_t s, float *x, uint32_t n);
