@@ -116,30 +116,49 @@ __global__ __launch_bounds__(256) void k_vae_dwconv_fm(VaeDwArgs a) {
 }
 
 // The same convolution when left_pad = (kernel - 1) * dilation (the causal
-// layers), tiled: a workgroup covers TB = 2048 / CB rows of CB channels, stages
+// layers) and kernel <= KMAX, tiled: a workgroup covers TB = 2048 / CB rows of CB
+// channels (CB a power of two <= 64, so each thread keeps one channel), stages
 // pre(x) for its rows and their left halo in LDS once (pre(0) = 0, so the zero
-// padding stays zero), then takes the taps from LDS.
-__global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32_t CB) {
-    __shared__ float xs[2048 + 64 * 54];
-    const uint32_t TB = 2048u / CB, halo = a.left_pad;
-    const uint32_t t0 = blockIdx.x * TB, c0 = blockIdx.y * CB, C = a.channels, tid = threadIdx.x;
-    for (uint32_t idx = tid; idx < (TB + halo) * CB; idx += 256u) {
-        const uint32_t r = idx / CB, cc = idx - r * CB, c = c0 + cc;
-        const int ti = (int)(t0 + r) - (int)halo;
-        float v = 0.f;
-        if (ti >= 0 && (uint32_t)ti < a.length && c < C) {
-            v = a.x[(size_t)ti * C + c];
-            if (a.alpha_in) v = snake(v, hf(a.alpha_in[c]));
-        }
-        xs[idx] = v;
+// padding stays zero), then takes the taps from LDS with the channel's weights,
+// bias and snake alphas in registers. Every staging load is issued before the
+// first is used.
+template <int KMAX>
+__global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32_t cb_shift) {
+    constexpr uint32_t kMaxHalo = 54u, NS = (2048u + 64u * kMaxHalo + 255u) / 256u;
+    __shared__ float xs[2048 + 64 * kMaxHalo];
+    const uint32_t CB = 1u << cb_shift, TB = 2048u >> cb_shift, halo = a.left_pad;
+    const uint32_t t0 = blockIdx.x * TB, C = a.channels, tid = threadIdx.x;
+    const uint32_t cc = tid & (CB - 1u), c = blockIdx.y * CB + cc;
+    const bool cval = c < C;
+    const uint32_t n_st = (TB + halo) << cb_shift;
+    float xv[NS];
+#pragma unroll
+    for (uint32_t i = 0; i < NS; ++i) {
+        const uint32_t idx = tid + 256u * i;
+        const int ti = (int)(t0 + (idx >> cb_shift)) - (int)halo;
+        xv[i] = idx < n_st && cval && ti >= 0 && (uint32_t)ti < a.length ? a.x[(size_t)ti * C + c] : 0.f;
+    }
+    const float ain = a.alpha_in && cval ? hf(a.alpha_in[c]) : 0.f;
+    const float aout = a.alpha_out && cval ? hf(a.alpha_out[c]) : 0.f;
+    const float bias = cval ? hf(a.b[c]) : 0.f;
+    float wk[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) wk[k] = cval && (uint32_t)k < a.kernel ? hf(a.w[c * a.kernel + k]) : 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < NS; ++i) {
+        const uint32_t idx = tid + 256u * i;
+        if (idx < n_st) xs[idx] = a.alpha_in ? snake(xv[i], ain) : xv[i];
     }
     __syncthreads();
-    for (uint32_t o = tid; o < TB * CB; o += 256u) {
-        const uint32_t r = o / CB, cc = o - r * CB, t = t0 + r, c = c0 + cc;
-        if (t >= a.length || c >= C) continue;
-        float sum = hf(a.b[c]);
-        for (uint32_t k = 0; k < a.kernel; ++k) sum += xs[(r + k * a.dilation) * CB + cc] * hf(a.w[c * a.kernel + k]);
-        if (a.alpha_out) sum = snake(sum, hf(a.alpha_out[c]));
+#pragma unroll
+    for (uint32_t i = 0; i < 8u; ++i) {   // TB * CB = 2048 outputs, 8 per thread
+        const uint32_t r = (tid + 256u * i) >> cb_shift, t = t0 + r;
+        if (t >= a.length || !cval) continue;
+        float sum = bias;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k)
+            if ((uint32_t)k < a.kernel) sum += xs[((r + k * a.dilation) << cb_shift) + cc] * wk[k];
+        if (a.alpha_out) sum = snake(sum, aout);
         a.y[(size_t)t * C + c] = sum;
     }
 }
@@ -179,8 +198,55 @@ __global__ __launch_bounds__(256) void k_vae_repack_convt(const __half *w, const
 
 // y[t][n] (+)= b[n] + sum_k x[t][k] W[n][k] for short K (the GEMM takes K % 128
 // == 0): a workgroup covers NB = min(N, 256) outputs of RB rows, the rows staged
-// in LDS; thread (g, n) computes rows g, g + G, ... (G = 256 / NB).
+// in LDS; thread (g, n) computes rows g, g + G, ... (G = 256 / NB, at most
+// kLinRows of them) together, reading W[n] once in 8-column chunks (K % 8 == 0).
+constexpr uint32_t kLinRows = 8;
 __global__ __launch_bounds__(256) void k_vae_linear_fm(VaeLinearArgs a, uint32_t NB, uint32_t RB) {
+    extern __shared__ float xs[];
+    const uint32_t tid = threadIdx.x, G = 256u / NB, n = blockIdx.x * NB + tid % NB, g = tid / NB;
+    const uint32_t r0 = blockIdx.y * RB;
+    for (uint32_t idx = tid; idx < RB * a.K; idx += 256u) {
+        const uint32_t r = idx / a.K, k = idx - r * a.K;
+        xs[idx] = r0 + r < a.T ? a.x[(size_t)(r0 + r) * a.ldx + k] : 0.f;
+    }
+    __syncthreads();
+    if (n >= a.N || g >= G) return;
+    const __half *w = a.w + (size_t)n * a.K;
+    const float b = a.bias_f32 ? a.bias_f32[n] : (a.bias ? hf(a.bias[n]) : 0.f);
+    float acc[kLinRows];
+#pragma unroll
+    for (uint32_t j = 0; j < kLinRows; ++j) acc[j] = 0.f;
+    for (uint32_t k0 = 0; k0 < a.K; k0 += 8u) {
+        const uint4 wc = *reinterpret_cast<const uint4 *>(w + k0);
+        const uint32_t wu[4] = {wc.x, wc.y, wc.z, wc.w};
+        float wf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const __half2 h = __builtin_bit_cast(__half2, wu[e]);
+            wf[2 * e] = __low2float(h);
+            wf[2 * e + 1] = __high2float(h);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kLinRows; ++j) {
+            const uint32_t r = g + G * j;
+            if (r >= RB) break;
+            const float *xr = xs + r * a.K + k0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[j] += xr[e] * wf[e];
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kLinRows; ++j) {
+        const uint32_t r = g + G * j;
+        if (r >= RB || r0 + r >= a.T) break;
+        const float v = acc[j] + b;
+        float *dst = a.y + (size_t)(r0 + r) * a.ldy + n;
+        *dst = a.residual ? *dst + v : v;
+    }
+}
+
+// Any K and weight alignment: W[n][k] read element by element.
+__global__ __launch_bounds__(256) void k_vae_linear_fm_any(VaeLinearArgs a, uint32_t NB, uint32_t RB) {
     extern __shared__ float xs[];
     const uint32_t tid = threadIdx.x, G = 256u / NB, n = blockIdx.x * NB + tid % NB, g = tid / NB;
     const uint32_t r0 = blockIdx.y * RB;
@@ -287,11 +353,12 @@ int launch_vae_tanh(hipStream_t s, float *x, uint32_t n) {
 int launch_vae_dwconv_fm(hipStream_t s, const VaeDwArgs &a) {
     const uint64_t n = (uint64_t)a.length * a.channels;
     if (!n) return VX_OK;
-    if (a.kernel >= 1u && a.left_pad == (a.kernel - 1u) * a.dilation && a.left_pad <= 54u) {
+    if (a.kernel >= 1u && a.kernel <= 8u && a.left_pad == (a.kernel - 1u) * a.dilation && a.left_pad <= 54u) {
         const uint32_t CB = a.channels < 64u ? a.channels : 64u;   // >= 1; 2048 / CB rows per workgroup
-        if (2048u % CB == 0) {
-            const uint32_t TB = 2048u / CB;
-            k_vae_dwconv_tiled_fm<<<dim3((a.length + TB - 1u) / TB, (a.channels + CB - 1u) / CB), 256, 0, s>>>(a, CB);
+        if ((CB & (CB - 1u)) == 0) {
+            const uint32_t sh = (uint32_t)__builtin_ctz(CB), cblocks = (a.channels + CB - 1u) / CB;
+            const uint32_t tb = 2048u >> sh;
+            k_vae_dwconv_tiled_fm<8><<<dim3((a.length + tb - 1u) / tb, cblocks), 256, 0, s>>>(a, sh);
             VX_LAUNCHED("k_vae_dwconv_tiled_fm");
             return VX_OK;
         }
@@ -320,14 +387,21 @@ int launch_vae_repack_convt(hipStream_t s, const __half *w, const __half *b, uin
 int launch_vae_linear_fm(hipStream_t s, const VaeLinearArgs &a) {
     if (!a.T || !a.N) return VX_OK;
     if (a.K > 4096u) return fail(VX_ERR_UNSUPPORTED, "vae linear: K %u > 4096", a.K);
+    const bool chunks = a.K % 8u == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15u) == 0;
     const uint32_t NB = a.N < 256u ? a.N : 256u, G = 256u / NB;
     uint32_t rpt = 8192u / (G * a.K);
-    rpt = rpt < 1u ? 1u : (rpt > 8u ? 8u : rpt);
+    rpt = rpt < 1u ? 1u : (rpt > kLinRows ? kLinRows : rpt);
     const uint32_t RB = G * rpt;   // RB * K <= max(8192, G * K) floats
     if ((uint64_t)RB * a.K * 4u > 65536u)
         return fail(VX_ERR_UNSUPPORTED, "vae linear: %u rows x K %u exceed the LDS tile", RB, a.K);
-    k_vae_linear_fm<<<dim3((a.N + NB - 1u) / NB, (a.T + RB - 1u) / RB), 256, (size_t)RB * a.K * 4u, s>>>(a, NB, RB);
-    VX_LAUNCHED("k_vae_linear_fm");
+    const dim3 grid((a.N + NB - 1u) / NB, (a.T + RB - 1u) / RB);
+    if (chunks) {
+        k_vae_linear_fm<<<grid, 256, (size_t)RB * a.K * 4u, s>>>(a, NB, RB);
+        VX_LAUNCHED("k_vae_linear_fm");
+    } else {
+        k_vae_linear_fm_any<<<grid, 256, (size_t)RB * a.K * 4u, s>>>(a, NB, RB);
+        VX_LAUNCHED("k_vae_linear_fm_any");
+    }
     return VX_OK;
 }
 
