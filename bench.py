@@ -26,7 +26,8 @@ Prints one JSON line with:
                each kernel's HIP-event span, with the projection GEMMs' algorithmic
                TFLOP/s against the 2.5 PFLOP/s dense f16 MFMA peak
   cfm          the LocDiT flow-matching solve (8 layers, hidden 1024, CFG batch
-               2, 10 timesteps): solve time and weight-streaming GB/s
+               2, 10 timesteps): solve time and weight-streaming GB/s; and the
+               same solve at the reference's 12-layer, 11-token geometry
   residual     the ResidualLM step (FSQ + fusion + 8 F16 layers without RoPE,
                hidden 2048): steps/s and weight-streaming GB/s
   audiovae     the AudioVAE decode of 40 latent frames (1.6 s of 48 kHz audio):
@@ -313,10 +314,49 @@ def cfm_leg(ctx, reps):
         f"-> {gbps:.0f} GB/s")
     per = {k: dict(avg_us=round(v["avg_ms"] * 1e3, 3), calls=v["calls"], total_ms=round(v["total_ms"], 4))
            for k, v in prof.items()}
+    ref = cfm_reference_shape(ctx, reps)
     return {"workload": "locdit_f16_cfm_8L_h1024_16x64_cond32_cfg2_batch2_10steps", "ms": round(ms, 3),
             "euler_steps": steps, "estimator_calls": res["estimator_calls"],
             "weight_bytes_per_solve": int(solve_bytes), "achieved_GBps": round(gbps, 1),
-            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "per_kernel_eager": per}
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "per_kernel_eager": per, "reference_shape": ref}
+
+
+def cfm_reference_shape(ctx, reps):
+    """The same solve at the reference's enforced LocDiT geometry (LocalConfig::
+    from_gguf, local.rs:37-48,85-92): 12 layers x 1024, 16/2 heads x 128, FFN 4096,
+    mu1 + mu2 + time + 4 condition + 4 latent tokens (11 per sequence), strict
+    geometry, 10 timesteps, CFG batch 2."""
+    from voxgen_amd import synth
+    from voxgen_amd.locdit import CfmOptions, LocDit
+    from voxgen_amd.runtime import Model
+    cfg = synth.locdit_config()
+    m = synth.build_locdit(cfg, seed=0x5EED0016)
+    model = Model(ctx, m.data, m.tensors)
+    loc = LocDit(ctx, model, cfg, strict_geometry=True)
+    cond = synth.normal_f32(cfg["patch"] * cfg["feat_dim"], 0x5EED0017)
+    mu = synth.normal_f32(2 * cfg["hidden"], 0x5EED0018)
+    opt = CfmOptions(n_timesteps=10, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0, seed=42,
+                     use_cfg_zero_star=True)
+    out, res = loc.cfm_solve(cond, mu, opt)                # captures the graph
+    times = []
+    for i in range(max(reps, 1)):
+        t0 = time.perf_counter()
+        loc.cfm_solve(cond, mu, CfmOptions(seed=42 + i))
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    loc.close()
+    model.free()
+    H, F, QD, KD, FD = 1024, 4096, 16 * 128, 2 * 128, 64
+    layer = 2 * (H * (QD + 2 * KD) + QD * H + 3 * F * H)
+    step_bytes = 12 * layer + 2 * (4 * H * H + 2 * FD * H)   # + time MLPs, in/out proj
+    steps = res["estimator_calls"] // 2
+    solve_bytes = steps * step_bytes
+    gbps = solve_bytes / (ms * 1e-3) / 1e9
+    log(f"cfm solve at the reference geometry (12L, 11 tokens): {ms:.3f} ms; {solve_bytes / 1e9:.2f} GB of weights "
+        f"-> {gbps:.0f} GB/s")
+    return {"workload": "locdit_f16_cfm_12L_h1024_16q2kv_x128_11tok_cfg2_batch2_10steps", "ms": round(ms, 3),
+            "euler_steps": steps, "weight_bytes_per_solve": int(solve_bytes), "achieved_GBps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
 def residual_step_bytes(pos):
