@@ -77,7 +77,8 @@ def test_cfm_solve_graph_replay_seeds_and_initial_x(ctx, ref_shape):
     a1, _ = loc.cfm_solve(cond, mu, opt)
     b1, _ = loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=3, seed=8))   # same graph, new seed
     a2, _ = loc.cfm_solve(cond, mu, opt)
-    # Replays agree to float rounding (split-K projections accumulate with atomics).
+    # Replays agree to float rounding (the general stack's split-K projections
+    # accumulate with atomics; the short-batch stack replays bit for bit).
     assert rel_l2(a2, a1) < 1e-5 and rel_l2(b1, a1) > 0.1
     assert rel_l2(b1, o.cfm_solve(cond, mu, n_timesteps=3, seed=8)) < 1e-4
     x0 = synth.normal_f32(256, 99)
@@ -99,6 +100,25 @@ def test_cfm_solve_8_layers_16x64_cond32(ctx):
     got, res = loc.cfm_solve(cond, None, CfmOptions(seed=42))
     want = o.cfm_solve(cond, None, seed=42)
     assert res["estimator_calls"] == 18
+    assert rel_l2(got, want) < 1e-4
+    loc.close()
+    model.free()
+
+
+def test_cfm_solve_general_stack_long_condition(ctx):
+    """66 tokens per sequence (61 given condition rows): past the fused dense
+    attention's 64 tokens, so the solve takes the general layer stack (k_gemm with
+    split-K accumulators, the three-kernel dense attention) instead of the
+    short-batch one; 3 timesteps against the oracle."""
+    cfg = synth.locdit_config(layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, n_mu=0, n_cond=61,
+                              cond_raw=1, uncond_zero_cond=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0207)
+    model = Model(ctx, m.data, m.tensors)
+    o = oracle_of(m, cfg)
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, _ = inputs(cfg, 0x5EED0208)
+    got, res = loc.cfm_solve(cond, None, CfmOptions(n_timesteps=3, seed=7))
+    want = o.cfm_solve(cond, None, n_timesteps=3, seed=7)
     assert rel_l2(got, want) < 1e-4
     loc.close()
     model.free()
