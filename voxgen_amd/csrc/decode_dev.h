@@ -228,6 +228,21 @@ struct Q8Row {
     uint2 d[NG];
 };
 
+// Weight streams are read with nontemporal loads: a decode step reads 1.4 GB of
+// weights once, and with ordinary loads they evict the KV cache, the activation
+// vectors and the attention partials (a few MB, reused within the step and from
+// step to step) from the L2s and the MALL. Decode 1433 -> 1491 tok/s.
+typedef uint32_t vx_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vx_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_w16(const void *p) {
+    const vx_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const vx_u32x4 *>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 ld_w8(const void *p) {
+    const vx_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const vx_u32x2 *>(p));
+    return make_uint2(v[0], v[1]);
+}
+
 template <int NG>
 __device__ __forceinline__ void load_row(Q8Row<NG> &r, const WRef &w, uint32_t row, uint32_t cols,
                                          int lane) {
@@ -235,8 +250,8 @@ __device__ __forceinline__ void load_row(Q8Row<NG> &r, const WRef &w, uint32_t r
     const unsigned short *drow = reinterpret_cast<const unsigned short *>(w.d) + (size_t)row * (cols >> 5);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-        r.q[g] = *reinterpret_cast<const uint4 *>(qrow + kGroupCols * g + 16 * lane);
-        r.d[g] = *reinterpret_cast<const uint2 *>(drow + 32 * g + 4 * (lane >> 3));
+        r.q[g] = ld_w16(qrow + kGroupCols * g + 16 * lane);
+        r.d[g] = ld_w8(drow + 32 * g + 4 * (lane >> 3));
     }
 }
 
@@ -282,7 +297,7 @@ __device__ __forceinline__ void load_row(F16Row<NG> &r, const WRef &w, uint32_t 
         for (int h = 0; h < 2; ++h) {
             const uint32_t col = kGroupCols * g + 512u * h + 8u * lane;
             const bool ok = col < cols;
-            const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (ok ? col : 0u));
+            const uint4 v = ld_w16(wrow + (ok ? col : 0u));
             r.c[g][h] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
         }
 }

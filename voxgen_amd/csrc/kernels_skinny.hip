@@ -39,6 +39,14 @@ constexpr uint32_t kSkPairs = 16;  // gate/up row pairs per workgroup (GEPI_SWIG
 constexpr int kSkDepth = 3;        // k-steps in flight per wave
 constexpr uint32_t kSkMaxTokens = 128;
 
+// Weights are read once per launch: nontemporal loads keep them from evicting
+// the activation planes and partial slabs the other kernels of the layer reuse.
+__device__ __forceinline__ uint4 ld_nt16(const __half *p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -103,8 +111,8 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     SkOps<MT> ring[kSkDepth];
     auto load = [&](SkOps<MT> &o, int i) {
         const uint32_t c = (s0 + wv + 4u * (uint32_t)i) << 9;   // block offset of the k-step
-        o.w[0] = *reinterpret_cast<const uint4 *>(wr[0] + c);
-        o.w[1] = *reinterpret_cast<const uint4 *>(wr[1] + c);
+        o.w[0] = ld_nt16(wr[0] + c);
+        o.w[1] = ld_nt16(wr[1] + c);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             o.xh[mt] = *reinterpret_cast<const uint4 *>(xr[mt] + c);
