@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
 // the token's row in registers across the reduction; the branch rows of a chunk
 // are all requested before they are summed. Same arithmetic, summation order
 // h + scale * (b0 + b1 + ...) as k_seq_rmsnorm.
-template <int NV>
+template <int NV, int MAXB>   // MAXB: branches the registers hold (>= a.nbranch)
 __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -435,9 +435,9 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
     for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4 *>(h + 4u * (tid + 256u * j));
     if (a.branch) {
         const float *br = a.branch + (size_t)t * a.ldb;
-        float4 bv[NV][kSeqNormMaxBranch];
+        float4 bv[NV][MAXB];
 #pragma unroll
-        for (int b = 0; b < (int)kSeqNormMaxBranch; ++b)
+        for (int b = 0; b < MAXB; ++b)
 #pragma unroll
             for (int j = 0; j < NV; ++j)
                 bv[j][b] = (uint32_t)b < a.nbranch
@@ -447,7 +447,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
         for (int j = 0; j < NV; ++j) {
             float4 add = bv[j][0];
 #pragma unroll
-            for (int b = 1; b < (int)kSeqNormMaxBranch; ++b)
+            for (int b = 1; b < MAXB; ++b)
                 if ((uint32_t)b < a.nbranch) {
                     add.x += bv[j][b].x;
                     add.y += bv[j][b].y;
@@ -941,73 +941,126 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 // per row (lane per key), the values thread per (row, dim); each dot product and
 // sum runs in the order of the three-kernel path.
 constexpr uint32_t kDenseFusedRows = 8;
+// The attention + O-projection variant: sixteen query tokens (one MFMA A
+// fragment) per workgroup, and at most kOprojBlocks weight blocks per wave.
+constexpr uint32_t kOprojRows = 8;
+constexpr uint32_t kOprojBlocks = 16;
+
+typedef _Float16 oh8 __attribute__((ext_vector_type(8)));
+typedef float of4 __attribute__((ext_vector_type(4)));
+
 // NSLAB > 1 (float4 staging only): q, k and v are the sums of NSLAB partial
 // slabs a.slab_stride floats apart (a split-K projection's plain-store output).
-template <int HD, int NSLAB = 1>   // HD: head_dim when known at compile time (the dot loops unroll), 0: a.head_dim
+//
+// OPROJ: the workgroup then multiplies its kOprojRows x head_dim output by the
+// head's columns of the O projection (a.wo, fragment layout, q_heads * head_dim
+// columns), for the hidden rows of its share (blockIdx.z / row groups of
+// a.nsplit), and stores the product to the head's partial slab
+// (a.oslab + h * a.oslab_stride, [batch * tokens][hidden]): out = sum over the
+// heads' slabs, the split-K of the O projection along its heads. The output
+// enters as hi/lo f16 planes against exact f16 weights, two
+// v_mfma_f32_16x16x32_f16 per 32 columns, the arithmetic of the short-batch GEMM.
+// The weight blocks are requested before the attention starts.
+template <int HD, int NSLAB = 1, bool OPROJ = false>   // HD: head_dim when known at compile time, 0: a.head_dim
 __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
-    extern __shared__ float sm[];
-    const uint32_t h = blockIdx.x, bz = blockIdx.y, t0 = blockIdx.z * kDenseFusedRows;
-    const uint32_t S = a.tokens, D = HD ? (uint32_t)HD : a.head_dim, DP = D + 1u;
-    const uint32_t R = min(kDenseFusedRows, S - t0);
+    extern __shared__ __align__(16) float sm[];
+    constexpr uint32_t ROWS = OPROJ ? kOprojRows : kDenseFusedRows;
+    // Rows of a compile-time head_dim are padded to a multiple of four floats
+    // (float4 LDS access, a four-bank shift per row), others by one float.
+    const uint32_t S = a.tokens, D = HD ? (uint32_t)HD : a.head_dim, DP = HD ? (uint32_t)HD + 4u : D + 1u;
+    const uint32_t ngroups = (S + ROWS - 1u) / ROWS;
+    const uint32_t h = blockIdx.x, bz = blockIdx.y, rg = blockIdx.z % ngroups, t0 = rg * ROWS;
+    const uint32_t R = min(ROWS, S - t0);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t kv = h / (a.q_heads / a.kv_heads);
     const float *q = a.q + ((size_t)bz * S + t0) * a.q_stride + (size_t)h * D;
     const float *k = a.k + (size_t)bz * S * a.k_stride + (size_t)kv * D;
     const float *v = a.v + (size_t)bz * S * a.v_stride + (size_t)kv * D;
     const size_t ob = ((size_t)bz * S + t0) * a.out_stride + (size_t)h * D;
-    float *ks = sm, *vs = ks + S * DP, *qs = vs + S * DP, *ps = qs + kDenseFusedRows * DP;
+    float *ks = sm, *vs = ks + S * DP, *qs = vs + S * DP, *ps = qs + ROWS * DP;
+
+    // O projection: 16-row groups [g0, g1) of the hidden rows, wave w taking
+    // g0 + w, g0 + w + 4, ...; every block load is unconditional (clamped). The
+    // loads are issued after the attention's own (vector loads complete in
+    // order, so a wait for the staged rows would otherwise wait for them too).
+    constexpr uint32_t KB = OPROJ ? (uint32_t)HD / 32u : 1u;     // 32-column blocks of the head
+    constexpr uint32_t GPW = OPROJ ? kOprojBlocks / KB : 1u;     // groups per wave
+    uint4 wb[GPW][KB];
+    uint32_t g0 = 0, g1 = 0;
+    auto fetch_wo = [&]() {
+        if constexpr (OPROJ) {
+            const uint32_t ng = a.hidden >> 4, sp = blockIdx.z / ngroups;
+            g0 = sp * ng / a.nsplit;
+            g1 = (sp + 1u) * ng / a.nsplit;
+            const uint32_t kblocks = (a.q_heads * (uint32_t)HD) >> 5;
+#pragma unroll
+            for (uint32_t i = 0; i < GPW; ++i) {
+                const uint32_t g = min(g0 + wave + 4u * i, g1 - 1u);
+                const __half *blk = a.wo + (((size_t)g * kblocks + h * KB) << 9) + 8u * lane;
+#pragma unroll
+                for (uint32_t kb = 0; kb < KB; ++kb)
+                    wb[i][kb] = *reinterpret_cast<const uint4 *>(blk + ((size_t)kb << 9));
+            }
+        }
+    };
     bool staged = false;
     if constexpr (HD > 0) {
         if (a.vec && a.rope) {
             // Every global load of the stage is issued before the first LDS store:
             // V rows as float4 chunks, and for K and the query rows the two float4
-            // chunks of a rotated pair (d..d+3, d+D/2..d+D/2+3) with their (cos, sin).
+            // chunks of a rotated pair (d..d+3, d+D/2..d+D/2+3) with their (cos, sin),
+            // each slab separately. The loads are unconditional (chunks past the
+            // rows reload the last one and are not stored): a load under a branch
+            // makes the compiler wait for every load in flight at the branch's end.
             constexpr uint32_t H2 = HD / 2, C4 = H2 / 4, V4 = HD / 4;
             constexpr uint32_t NV = (kDenseFusedMaxTokens * V4 + 255u) / 256u;
-            constexpr uint32_t NKQ = ((kDenseFusedMaxTokens + kDenseFusedRows) * C4 + 255u) / 256u;
-            const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            float4 vv[NV], x0[NKQ], x1[NKQ], c01[NKQ], c23[NKQ];
+            constexpr uint32_t NKQ = ((kDenseFusedMaxTokens + ROWS) * C4 + 255u) / 256u;
+            // Slab 0 into vv / x0 / x1, slab 1 (NSLAB == 2) into the *b arrays.
+            constexpr uint32_t NVB = NSLAB > 1 ? NV : 1u, NKB = NSLAB > 1 ? NKQ : 1u;
+            float4 vv[NV], x0[NKQ], x1[NKQ], c01[NKQ], c23[NKQ], vvb[NVB], x0b[NKB], x1b[NKB];
 #pragma unroll
             for (uint32_t j = 0; j < NV; ++j) {
-                const uint32_t i = tid + 256u * j, t = i / V4, c = i - t * V4;
-                vv[j] = z4;
-                if (i < S * V4) {
-                    const float *src = v + (size_t)t * a.v_stride + 4u * c;
-                    vv[j] = *reinterpret_cast<const float4 *>(src);
-#pragma unroll
-                    for (int sl = 1; sl < NSLAB; ++sl) vv[j] += *reinterpret_cast<const float4 *>(src + sl * a.slab_stride);
-                }
+                const uint32_t i = min(tid + 256u * j, S * V4 - 1u), t = i / V4, c = i - t * V4;
+                const float *src = v + (size_t)t * a.v_stride + 4u * c;
+                vv[j] = *reinterpret_cast<const float4 *>(src);
+                if constexpr (NSLAB > 1) vvb[j] = *reinterpret_cast<const float4 *>(src + a.slab_stride);
             }
 #pragma unroll
             for (uint32_t j = 0; j < NKQ; ++j) {
-                const uint32_t i = tid + 256u * j, r = i / C4, c = i - r * C4;
-                x0[j] = x1[j] = c01[j] = c23[j] = z4;
-                if (i < (S + R) * C4) {
-                    const bool isk = r < S;
-                    const uint32_t t = isk ? r : r - S, pos = isk ? t : t0 + t;
-                    const float *row = isk ? k + (size_t)t * a.k_stride : q + (size_t)t * a.q_stride;
-                    x0[j] = *reinterpret_cast<const float4 *>(row + 4u * c);
-                    x1[j] = *reinterpret_cast<const float4 *>(row + H2 + 4u * c);
-#pragma unroll
-                    for (int sl = 1; sl < NSLAB; ++sl) {
-                        x0[j] += *reinterpret_cast<const float4 *>(row + sl * a.slab_stride + 4u * c);
-                        x1[j] += *reinterpret_cast<const float4 *>(row + sl * a.slab_stride + H2 + 4u * c);
-                    }
-                    const float4 *cs = reinterpret_cast<const float4 *>(a.rope + (size_t)pos * H2 + 4u * c);
-                    c01[j] = cs[0];
-                    c23[j] = cs[1];
+                const uint32_t i = min(tid + 256u * j, (S + R) * C4 - 1u), r = i / C4, c = i - r * C4;
+                const bool isk = r < S;
+                const uint32_t t = isk ? r : r - S, pos = isk ? t : t0 + t;
+                const float *row = isk ? k + (size_t)t * a.k_stride : q + (size_t)t * a.q_stride;
+                x0[j] = *reinterpret_cast<const float4 *>(row + 4u * c);
+                x1[j] = *reinterpret_cast<const float4 *>(row + H2 + 4u * c);
+                if constexpr (NSLAB > 1) {
+                    x0b[j] = *reinterpret_cast<const float4 *>(row + a.slab_stride + 4u * c);
+                    x1b[j] = *reinterpret_cast<const float4 *>(row + a.slab_stride + H2 + 4u * c);
                 }
+                const float4 *cs = reinterpret_cast<const float4 *>(a.rope + (size_t)pos * H2 + 4u * c);
+                c01[j] = cs[0];
+                c23[j] = cs[1];
+            }
+            if constexpr (NSLAB > 1) {
+#pragma unroll
+                for (uint32_t j = 0; j < NV; ++j) vv[j] += vvb[j];
+#pragma unroll
+                for (uint32_t j = 0; j < NKQ; ++j) {
+                    x0[j] += x0b[j];
+                    x1[j] += x1b[j];
+                }
+            }
+            if constexpr (OPROJ) {
+                // The weight loads after the staged rows' (with one slab the
+                // compiler keeps that order by itself, and a scheduling barrier
+                // there makes it spill).
+                if constexpr (NSLAB > 1) __builtin_amdgcn_sched_barrier(0);
+                fetch_wo();
             }
 #pragma unroll
             for (uint32_t j = 0; j < NV; ++j) {
                 const uint32_t i = tid + 256u * j, t = i / V4, c = i - t * V4;
-                if (i < S * V4) {
-                    float *dst = vs + t * DP + 4u * c;
-                    dst[0] = vv[j].x;
-                    dst[1] = vv[j].y;
-                    dst[2] = vv[j].z;
-                    dst[3] = vv[j].w;
-                }
+                if (i < S * V4) *reinterpret_cast<float4 *>(vs + t * DP + 4u * c) = vv[j];
             }
 #pragma unroll
             for (uint32_t j = 0; j < NKQ; ++j) {
@@ -1020,17 +1073,21 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
                     const float a1[4] = {x1[j].x, x1[j].y, x1[j].z, x1[j].w};
                     const float co[4] = {c01[j].x, c01[j].z, c23[j].x, c23[j].z};
                     const float si[4] = {c01[j].y, c01[j].w, c23[j].y, c23[j].w};
+                    float lo4[4], hi4[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        dst[e] = a0[e] * co[e] - a1[e] * si[e];
-                        dst[e + H2] = a1[e] * co[e] + a0[e] * si[e];
+                        lo4[e] = a0[e] * co[e] - a1[e] * si[e];
+                        hi4[e] = a1[e] * co[e] + a0[e] * si[e];
                     }
+                    *reinterpret_cast<float4 *>(dst) = make_float4(lo4[0], lo4[1], lo4[2], lo4[3]);
+                    *reinterpret_cast<float4 *>(dst + H2) = make_float4(hi4[0], hi4[1], hi4[2], hi4[3]);
                 }
             }
             staged = true;
         }
     }
     if (!staged) {
+        fetch_wo();
         for (uint32_t i = tid; i < S * D; i += 256u) {
             const uint32_t t = i / D, d = i - t * D;
             vs[t * DP + d] = v[(size_t)t * a.v_stride + d];
@@ -1062,8 +1119,21 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     for (uint32_t e = tid; e < R * S; e += 256u) {
         const uint32_t t = e / S, key = e - t * S;
         float s = 0.f;
+        if constexpr (HD > 0) {
+            const float4 *q4 = reinterpret_cast<const float4 *>(qs + t * DP);
+            const float4 *k4 = reinterpret_cast<const float4 *>(ks + key * DP);
+#pragma unroll
+            for (uint32_t d4 = 0; d4 < (uint32_t)HD / 4u; ++d4) {
+                const float4 x = q4[d4], y = k4[d4];
+                s += x.x * y.x;
+                s += x.y * y.y;
+                s += x.z * y.z;
+                s += x.w * y.w;
+            }
+        } else {
 #pragma unroll 16
-        for (uint32_t d = 0; d < D; ++d) s += qs[t * DP + d] * ks[key * DP + d];
+            for (uint32_t d = 0; d < D; ++d) s += qs[t * DP + d] * ks[key * DP + d];
+        }
         ps[e] = s * scale;
     }
     __syncthreads();
@@ -1079,11 +1149,68 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
         if (lane < S) ps[t * S + lane] = ex / z;
     }
     __syncthreads();
-    for (uint32_t o = tid; o < R * D; o += 256u) {
-        const uint32_t t = o / D, d = o - t * D;
-        float z = 0.f;
-#pragma unroll 8
-        for (uint32_t key = 0; key < S; ++key) z += ps[t * S + key] * vs[key * DP + d];
+    if constexpr (OPROJ) {
+        // The output rows into the q rows' LDS (free once the scores are done),
+        // rows past R as zeros.
+        constexpr uint32_t D4 = (uint32_t)HD / 4u;
+        for (uint32_t o = tid; o < ROWS * D4; o += 256u) {
+            const uint32_t t = o / D4, d4 = o - t * D4;
+            float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < R) {
+#pragma unroll 4
+                for (uint32_t key = 0; key < S; ++key) {
+                    const float p = ps[t * S + key];
+                    const float4 w = *reinterpret_cast<const float4 *>(vs + key * DP + 4u * d4);
+                    z.x += p * w.x;
+                    z.y += p * w.y;
+                    z.z += p * w.z;
+                    z.w += p * w.w;
+                }
+            }
+            *reinterpret_cast<float4 *>(qs + t * DP + 4u * d4) = z;
+        }
+        __syncthreads();
+        // A fragments: lane l = r + 16 c holds columns 8c..8c+7 of block kb for row r.
+        oh8 ah[KB], al[KB];
+        const uint32_t r = lane & 15u, c8 = 8u * (lane >> 4);
+#pragma unroll
+        for (uint32_t kb = 0; kb < KB; ++kb) {
+            float z8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (r < ROWS) {
+                const float4 u0 = *reinterpret_cast<const float4 *>(qs + r * DP + 32u * kb + c8);
+                const float4 u1 = *reinterpret_cast<const float4 *>(qs + r * DP + 32u * kb + c8 + 4u);
+                z8[0] = u0.x; z8[1] = u0.y; z8[2] = u0.z; z8[3] = u0.w;
+                z8[4] = u1.x; z8[5] = u1.y; z8[6] = u1.z; z8[7] = u1.w;
+            }
+#pragma unroll
+            for (uint32_t e = 0; e < 8u; ++e) {
+                const _Float16 hv = (_Float16)z8[e];
+                ah[kb][e] = hv;
+                al[kb][e] = (_Float16)(z8[e] - (float)hv);
+            }
+        }
+        float *slab = a.oslab + (size_t)h * a.oslab_stride + ((size_t)bz * S + t0) * a.hidden;
+        const uint32_t tq = 4u * (lane >> 4);
+#pragma unroll
+        for (uint32_t i = 0; i < GPW; ++i) {
+            const uint32_t g = g0 + wave + 4u * i;
+            if (g >= g1) break;
+            of4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (uint32_t kb = 0; kb < KB; ++kb) {
+                const oh8 b = __builtin_bit_cast(oh8, wb[i][kb]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[kb], b, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[kb], b, acc, 0, 0, 0);
+            }
+            // Lane (j, c) holds tokens 4c..4c+3 for hidden row 16 g + j.
+            const uint32_t n = 16u * g + r;
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e)
+                if (tq + e < R) slab[(size_t)(tq + e) * a.hidden + n] = acc[e];
+        }
+        return;
+    }
+    auto put = [&](uint32_t t, uint32_t d, float z) {
         const size_t po = a.o_frag ? frag16_index((bz * S + t0 + t), h * D + d, a.out_stride)
                                    : ob + (size_t)t * a.out_stride + d;
         if (a.oh) {
@@ -1092,6 +1219,34 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
             a.ol[po] = __builtin_bit_cast(__half, (_Float16)(z - (float)hv));
         } else {
             a.out[po] = z;
+        }
+    };
+    if constexpr (HD > 0) {
+        constexpr uint32_t D4 = (uint32_t)HD / 4u;
+        for (uint32_t o = tid; o < R * D4; o += 256u) {
+            const uint32_t t = o / D4, d4 = o - t * D4;
+            float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+            for (uint32_t key = 0; key < S; ++key) {
+                const float p = ps[t * S + key];
+                const float4 w = *reinterpret_cast<const float4 *>(vs + key * DP + 4u * d4);
+                z.x += p * w.x;
+                z.y += p * w.y;
+                z.z += p * w.z;
+                z.w += p * w.w;
+            }
+            put(t, 4u * d4, z.x);
+            put(t, 4u * d4 + 1u, z.y);
+            put(t, 4u * d4 + 2u, z.z);
+            put(t, 4u * d4 + 3u, z.w);
+        }
+    } else {
+        for (uint32_t o = tid; o < R * D; o += 256u) {
+            const uint32_t t = o / D, d = o - t * D;
+            float z = 0.f;
+#pragma unroll 8
+            for (uint32_t key = 0; key < S; ++key) z += ps[t * S + key] * vs[key * DP + d];
+            put(t, d, z);
         }
     }
 }
@@ -1178,11 +1333,12 @@ int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens) {
     const bool vec = a.n % 1024u == 0 && a.n <= 4096u && a.ldh % 4u == 0 && (!a.branch || (a.ldb % 4u == 0 && a.branch_stride % 4u == 0)) &&
                      (!a.y || a.ldy % 4u == 0) && (!a.yh || a.tiled || a.ldp % 4u == 0);
     if (vec) {
+        const bool wide = a.branch && a.nbranch > 8u;
         switch (a.n / 1024u) {
-            case 1: k_seq_rmsnorm4<1><<<tokens, 256, 0, s>>>(a); break;
-            case 2: k_seq_rmsnorm4<2><<<tokens, 256, 0, s>>>(a); break;
-            case 3: k_seq_rmsnorm4<3><<<tokens, 256, 0, s>>>(a); break;
-            default: k_seq_rmsnorm4<4><<<tokens, 256, 0, s>>>(a); break;
+            case 1: wide ? k_seq_rmsnorm4<1, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<1, 8><<<tokens, 256, 0, s>>>(a); break;
+            case 2: wide ? k_seq_rmsnorm4<2, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<2, 8><<<tokens, 256, 0, s>>>(a); break;
+            case 3: wide ? k_seq_rmsnorm4<3, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<3, 8><<<tokens, 256, 0, s>>>(a); break;
+            default: wide ? k_seq_rmsnorm4<4, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<4, 8><<<tokens, 256, 0, s>>>(a); break;
         }
         VX_LAUNCHED("k_seq_rmsnorm4");
         return VX_OK;
@@ -1271,8 +1427,55 @@ int launch_rope_pos_table(hipStream_t s, float2 *table, const float *factors, ui
     return VX_OK;
 }
 
+uint64_t dense_fused_lds_rows(uint32_t tokens, uint32_t head_dim, uint32_t rows) {
+    const uint32_t pad = head_dim == 64u || head_dim == 128u ? 4u : 1u;   // DP of the kernel
+    return ((2ull * tokens + rows) * (head_dim + pad) + (uint64_t)rows * tokens) * 4u;
+}
+
 uint64_t dense_fused_lds(uint32_t tokens, uint32_t head_dim) {
-    return ((2ull * tokens + kDenseFusedRows) * (head_dim + 1u) + (uint64_t)kDenseFusedRows * tokens) * 4u;
+    return dense_fused_lds_rows(tokens, head_dim, kDenseFusedRows);
+}
+
+bool dense_attn_oproj_eligible(uint32_t tokens, uint32_t head_dim) {
+    return tokens > 0 && tokens <= kDenseFusedMaxTokens && (head_dim == 64u || head_dim == 128u) &&
+           dense_fused_lds_rows(tokens, head_dim, kOprojRows) <= 65536u;
+}
+
+int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a) {
+    if (!a.tokens || !a.q_heads || !a.batch) return VX_OK;
+    if (!a.kv_heads || a.q_heads % a.kv_heads) return fail(VX_ERR_SHAPE, "attention + O projection: head counts");
+    if (!dense_attn_oproj_eligible(a.tokens, a.head_dim))
+        return fail(VX_ERR_UNSUPPORTED, "attention + O projection: %u tokens x head_dim %u", a.tokens, a.head_dim);
+    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!a.wo || !al16(a.wo) || !a.oslab || !a.hidden || a.hidden % 16u || a.oslab_stride < (uint64_t)a.batch * a.tokens * a.hidden)
+        return fail(VX_ERR_INVALID_ARG, "attention + O projection: weights or slabs");
+    if (!a.rope || a.q_stride % 4u || a.k_stride % 4u || a.v_stride % 4u || !al16(a.q) || !al16(a.k) || !al16(a.v) ||
+        !al16(a.rope) || (a.nslab != 1 && a.nslab != 2) || (a.nslab == 2 && a.slab_stride % 4u))
+        return fail(VX_ERR_UNSUPPORTED, "attention + O projection: needs float4 rows, RoPE and 1 or 2 input slabs");
+    DenseAttnArgs b = a;
+    b.vec = 1;
+    b.oh = b.ol = nullptr;
+    b.out = nullptr;
+    // Split the hidden rows so that no wave holds more than kOprojBlocks weight
+    // blocks, and so that the grid reaches about 128 workgroups.
+    const uint32_t ngroups = (a.tokens + kOprojRows - 1u) / kOprojRows, ng = a.hidden / 16u;
+    const uint32_t per_wave = kOprojBlocks / (a.head_dim / 32u);
+    uint32_t nsplit = (ng + 4u * per_wave - 1u) / (4u * per_wave);
+    const uint32_t base = a.q_heads * a.batch * ngroups;
+    while (base * nsplit < 128u && 2u * nsplit <= (ng + 3u) / 4u) nsplit *= 2u;
+    b.nsplit = nsplit;
+    const uint64_t lds = dense_fused_lds_rows(a.tokens, a.head_dim, kOprojRows);
+    const dim3 grid(a.q_heads, a.batch, ngroups * nsplit);
+    if (a.head_dim == 64u && a.nslab == 2)
+        k_dense_attn_fused<64, 2, true><<<grid, 256, (size_t)lds, s>>>(b);
+    else if (a.head_dim == 128u && a.nslab == 2)
+        k_dense_attn_fused<128, 2, true><<<grid, 256, (size_t)lds, s>>>(b);
+    else if (a.head_dim == 64u)
+        k_dense_attn_fused<64, 1, true><<<grid, 256, (size_t)lds, s>>>(b);
+    else
+        k_dense_attn_fused<128, 1, true><<<grid, 256, (size_t)lds, s>>>(b);
+    VX_LAUNCHED("k_dense_attn_fused");
+    return VX_OK;
 }
 
 int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a) {

@@ -72,6 +72,9 @@ struct vx_locdit {
     // the split-K partial slabs of attn_output and ffn_down, summed by the
     // residual rmsnorm that follows each.
     bool sk = false;
+    // The attention kernel also applies the O projection (one partial slab per
+    // query head) in place of a separate attn_output GEMM.
+    bool attn_oproj = false;
     uint32_t ks_qkv = 1, ks_o = 1, ks_down = 1;
     vx_buf *qkvp = nullptr;   // q | k | v rows of each of ks_qkv partial slabs
     vx_buf *yh = nullptr, *yl = nullptr, *ah = nullptr, *al = nullptr, *acth = nullptr, *actl = nullptr;
@@ -419,32 +422,39 @@ int enqueue_layers_sk(vx_locdit *e, uint32_t batch) {
             g.ws_stride = qkv_slab;
             VX_CHECK(launch_gemm(s, g));
         }
-        {
-            ProfSpan sp(ctx, "local.attention");
-            DenseAttnArgs a;
-            a.q = qp;
-            a.k = kp;
-            a.v = vp;
-            a.nslab = e->ks_qkv;
-            a.slab_stride = qkv_slab;
-            a.out = F(e->attn);
-            a.oh = ah;
-            a.ol = al;
-            a.o_frag = 1;
-            a.tokens = S;
-            a.q_heads = c.q_heads;
-            a.kv_heads = c.kv_heads;
-            a.head_dim = c.head_dim;
-            a.q_stride = QD;
-            a.k_stride = KD;
-            a.v_stride = KD;
-            a.out_stride = QD;
-            a.score_stride = S;
-            a.batch = batch;
-            a.rope = reinterpret_cast<const float2 *>(e->rope_tab->ptr);
-            VX_CHECK(launch_dense_attn_fused(s, a));
-        }
-        {
+        DenseAttnArgs a;
+        a.q = qp;
+        a.k = kp;
+        a.v = vp;
+        a.nslab = e->ks_qkv;
+        a.slab_stride = qkv_slab;
+        a.tokens = S;
+        a.q_heads = c.q_heads;
+        a.kv_heads = c.kv_heads;
+        a.head_dim = c.head_dim;
+        a.q_stride = QD;
+        a.k_stride = KD;
+        a.v_stride = KD;
+        a.out_stride = QD;
+        a.score_stride = S;
+        a.batch = batch;
+        a.rope = reinterpret_cast<const float2 *>(e->rope_tab->ptr);
+        if (e->attn_oproj) {
+            ProfSpan sp(ctx, "local.attention_oproj");
+            a.wo = L.frag[3];
+            a.hidden = H;
+            a.oslab = part;
+            a.oslab_stride = (uint64_t)M * H;
+            VX_CHECK(launch_dense_attn_oproj(s, a));
+        } else {
+            {
+                ProfSpan sp(ctx, "local.attention");
+                a.out = F(e->attn);
+                a.oh = ah;
+                a.ol = al;
+                a.o_frag = 1;
+                VX_CHECK(launch_dense_attn_fused(s, a));
+            }
             ProfSpan sp(ctx, "local.seq_linear");
             GemmArgs g = gemm(ah, al, QD);
             g.seg[0] = wseg(L.frag[3], H, part, H);
@@ -459,7 +469,7 @@ int enqueue_layers_sk(vx_locdit *e, uint32_t batch) {
         r.scale = 1.f;
         {
             ProfSpan sp(ctx, "local.seq_residual_rmsnorm");
-            r.nbranch = e->ks_o;
+            r.nbranch = e->attn_oproj ? c.q_heads : e->ks_o;
             r.branch_stride = (uint64_t)M * H;
             r.w = L.ffn_norm;
             VX_CHECK(launch_seq_rmsnorm(s, r, M));
@@ -828,7 +838,8 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
             e->ks_qkv = std::min(2u, slabs(QD + 2u * KD, H));   // the attention sums at most two
             e->ks_o = slabs(H, QD);
             e->ks_down = slabs(H, c.ffn);
-            const uint64_t ks = std::max(e->ks_o, e->ks_down);
+            e->attn_oproj = c.q_heads <= kSeqNormMaxBranch && H % 16u == 0 && dense_attn_oproj_eligible(e->S, c.head_dim);
+            const uint64_t ks = std::max({e->ks_o, e->ks_down, e->attn_oproj ? c.q_heads : 1u});
             const uint64_t R16 = (S2 + 15u) & ~15ull;   // plane rows, padded to whole fragments
             struct {
                 vx_buf **b;

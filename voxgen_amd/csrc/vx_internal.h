@@ -428,7 +428,7 @@ struct SeqNormArgs {
     // cleared accumulator of the next split-K GEMM; the branch memory must be writable.
     uint32_t clear_branch = 0;
 };
-constexpr uint32_t kSeqNormMaxBranch = 8;
+constexpr uint32_t kSeqNormMaxBranch = 16;
 int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens);
 
 struct SeqRopeArgs {
@@ -618,6 +618,15 @@ struct DenseAttnArgs {
     uint32_t nslab = 1;
     uint64_t slab_stride = 0;
     uint32_t vec = 0;      // set by launch_dense_attn_fused: 16-byte rows, float4 staging
+    // launch_dense_attn_oproj only: the O projection [hidden][q_heads * head_dim]
+    // in the fragment layout, and the per-head partial slabs it writes (head h at
+    // oslab + h * oslab_stride, [batch * tokens][hidden]; their sum is the
+    // projection). nsplit is set by the launcher.
+    const __half *wo = nullptr;
+    uint32_t hidden = 0;
+    float *oslab = nullptr;
+    uint64_t oslab_stride = 0;
+    uint32_t nsplit = 1;
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
 // table[p][i] = (cos, sin)(p * theta^(-2i/head_dim) / factors[i]) * scaling for
@@ -630,6 +639,12 @@ int launch_rope_pos_table(hipStream_t s, float2 *table, const float *factors, ui
 constexpr uint32_t kDenseFusedMaxTokens = 64;
 uint64_t dense_fused_lds(uint32_t tokens, uint32_t head_dim);   // bytes of LDS the fused kernel needs
 int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a);
+// The fused attention followed by the head's share of the O projection (16 query
+// tokens per workgroup): one partial slab per query head, summed by the consumer.
+// head_dim 64 or 128, float4-aligned q/k/v rows with RoPE, hidden % 16 == 0,
+// 16-byte aligned weights; VX_ERR_UNSUPPORTED otherwise.
+bool dense_attn_oproj_eligible(uint32_t tokens, uint32_t head_dim);
+int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a);
 // ---------------------------------------------- CFM / LocDiT (kernels_cfm.hip)
 // Noise seed from dev_seed[0..1] (low, high word) when set, else from `seed`.
 int launch_cfm_noise(hipStream_t s, float *x, uint32_t n, const uint32_t *dev_seed, uint64_t seed, float temperature);
