@@ -41,8 +41,9 @@ __global__ __launch_bounds__(256) void k_cfm_noise(float *x, uint32_t n, const u
 // read from `pos` and `neg` (rows of the CFG batch): s = <p,n>/(|n|^2 + 1e-8)
 // under CFG-Zero* (else 1); x -= dt * (n*s + cfg*(p - n*s)). One workgroup; the
 // dot products are block reductions over n <= 1024 elements.
-__global__ __launch_bounds__(256) void k_cfm_cfg_euler(float *x, const float *pos, const float *neg, uint32_t n,
-                                                       float dt, float cfg, uint32_t zero_star) {
+// One 256-thread workgroup: the CFG-Zero* guided velocity and the Euler update.
+__device__ __forceinline__ void cfg_euler_block(float *x, const float *pos, const float *neg, uint32_t n, float dt,
+                                                float cfg, uint32_t zero_star) {
     __shared__ float red[2][4];
     float pn = 0.f, nn = 0.f;
     for (uint32_t i = threadIdx.x; i < n; i += 256u) {
@@ -68,6 +69,79 @@ __global__ __launch_bounds__(256) void k_cfm_cfg_euler(float *x, const float *po
         const float guided = q * scale + cfg * (p - q * scale);
         x[i] -= dt * guided;
     }
+}
+
+__global__ __launch_bounds__(256) void k_cfm_cfg_euler(float *x, const float *pos, const float *neg, uint32_t n,
+                                                       float dt, float cfg, uint32_t zero_star) {
+    cfg_euler_block(x, pos, neg, n, dt, cfg, zero_star);
+}
+
+// The estimator's out_proj for the x tokens of both sequences (seq_linear_bias,
+// F16 weights: one wave per output feature, each lane a contiguous 1/64 of the
+// row, then a wave reduction), and then the update above, run by the last
+// workgroup to finish: each workgroup publishes its outputs with a device-scope
+// release fence and counts itself in a.counter; the one that takes the count to
+// gridDim.x acquires and applies cfg_euler_block, then resets the counter for
+// the next launch. No workgroup waits for another.
+__global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
+    __shared__ uint32_t is_last;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t f = blockIdx.x * 4u + wave, R = 2u * a.patch, n = a.patch * a.feat;
+    if (f < a.feat) {
+        const uint32_t ch = a.hidden >> 6;   // columns per lane, a multiple of 8
+        float acc[kOutEulerMaxRows];
+#pragma unroll
+        for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) acc[r] = 0.f;
+        const __half *wr = a.w + (size_t)f * a.hidden + lane * ch;
+        for (uint32_t c = 0; c < ch; c += 8u) {
+            const uint4 wv = *reinterpret_cast<const uint4 *>(wr + c);
+            const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+            float w8[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 t = __half22float2(*reinterpret_cast<const __half2 *>(&w4[e]));
+                w8[2 * e] = t.x;
+                w8[2 * e + 1] = t.y;
+            }
+#pragma unroll
+            for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) {
+                if (r >= R) break;
+                const uint32_t b = r / a.patch, p = r - b * a.patch;
+                const float *xr = a.rows + ((size_t)b * a.tokens + a.x0 + p) * a.hidden + lane * ch + c;
+                const float4 u0 = *reinterpret_cast<const float4 *>(xr), u1 = *reinterpret_cast<const float4 *>(xr + 4);
+                acc[r] += w8[0] * u0.x;
+                acc[r] += w8[1] * u0.y;
+                acc[r] += w8[2] * u0.z;
+                acc[r] += w8[3] * u0.w;
+                acc[r] += w8[4] * u1.x;
+                acc[r] += w8[5] * u1.y;
+                acc[r] += w8[6] * u1.z;
+                acc[r] += w8[7] * u1.w;
+            }
+        }
+        const float bias = !a.bias ? 0.f
+                           : a.bias_dtype == 0 ? static_cast<const float *>(a.bias)[f]
+                                               : __half2float(static_cast<const __half *>(a.bias)[f]);
+#pragma unroll
+        for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) {
+            if (r >= R) break;
+            float v = acc[r];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (lane == r) {
+                const uint32_t b = r / a.patch, p = r - b * a.patch;
+                a.out[(size_t)b * n + (size_t)p * a.feat + f] = v + bias;
+            }
+        }
+    }
+    __threadfence();   // release this workgroup's outputs device-wide
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(a.counter, 1u) == gridDim.x - 1u;
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();   // acquire every workgroup's outputs
+    cfg_euler_block(a.x, a.out, a.out + n, n, a.dt, a.cfg, a.zero_star);
+    if (threadIdx.x == 0) *a.counter = 0u;
 }
 
 // time_sinusoidal.comp:5: out[i] = sin(a) for i < dim/2, cos(a) after, with
@@ -176,6 +250,21 @@ int launch_cfm_cfg_euler(hipStream_t s, float *x, const float *pos, const float 
     if (!n) return VX_OK;
     k_cfm_cfg_euler<<<1, 256, 0, s>>>(x, pos, neg, n, dt, cfg, zero_star);
     VX_LAUNCHED("k_cfm_cfg_euler");
+    return VX_OK;
+}
+
+bool cfm_out_euler_eligible(uint32_t patch, uint32_t feat, uint32_t hidden, const void *w) {
+    return patch > 0 && 2u * patch <= kOutEulerMaxRows && feat > 0 && hidden % 512u == 0 && w &&
+           (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+}
+
+int launch_cfm_out_euler(hipStream_t s, const CfmOutEulerArgs &a) {
+    if (!cfm_out_euler_eligible(a.patch, a.feat, a.hidden, a.w) || !a.rows || !a.out || !a.x || !a.counter ||
+        (reinterpret_cast<uintptr_t>(a.rows) & 15u))
+        return fail(VX_ERR_UNSUPPORTED, "cfm out_proj + euler: patch %u, feat %u, hidden %u", a.patch, a.feat,
+                    a.hidden);
+    k_cfm_out_euler<<<(a.feat + 3u) / 4u, 256, 0, s>>>(a);
+    VX_LAUNCHED("k_cfm_out_euler");
     return VX_OK;
 }
 

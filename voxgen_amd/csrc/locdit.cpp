@@ -75,6 +75,10 @@ struct vx_locdit {
     // The attention kernel also applies the O projection (one partial slab per
     // query head) in place of a separate attn_output GEMM.
     bool attn_oproj = false;
+    // A solve step's out_proj and CFG-Zero* Euler update run as one launch;
+    // out_ctr is its completion counter (zero between launches).
+    bool out_euler = false;
+    vx_buf *out_ctr = nullptr;
     uint32_t ks_qkv = 1, ks_o = 1, ks_down = 1;
     vx_buf *qkvp = nullptr;   // q | k | v rows of each of ks_qkv partial slabs
     vx_buf *yh = nullptr, *yl = nullptr, *ah = nullptr, *al = nullptr, *acth = nullptr, *actl = nullptr;
@@ -164,7 +168,7 @@ void free_all(vx_locdit *e) {
                        &e->branch, &e->scores,  &e->out,  &e->seed,       &e->rope_tab,
                        &e->tvals,  &e->trows,   &e->tmid, &e->temb,       &e->yh,            &e->yl,
                        &e->ah,     &e->al,      &e->acth, &e->actl,       &e->part,          &e->wfrag,
-                       &e->qkvp};
+                       &e->qkvp,   &e->out_ctr};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -514,7 +518,7 @@ int enqueue_layers_sk(vx_locdit *e, uint32_t batch) {
 
 // pack_locdit + record_transformer + out_proj for `batch` sequences (1: the
 // conditional pass; 2: conditional then unconditional).
-int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) {
+int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr, bool skip_out = false) {
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_locdit_config &c = e->cfg;
@@ -545,6 +549,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr) 
         VX_CHECK(launch_pack_locdit(s, p));
     }
     VX_CHECK(e->sk ? enqueue_layers_sk(e, batch) : enqueue_layers_general(e, batch));
+    if (skip_out) return VX_OK;   // the caller's launch applies out_proj
     ProfSpan sp(ctx, "local.locdit_out");
     const uint32_t x0 = c.n_mu + 1u + c.n_cond;   // first x token of a sequence
     for (uint32_t b = 0; b < batch; ++b)
@@ -634,10 +639,31 @@ int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_
         const float t = span[step - 1], dt = t - span[step];
         (void)t;
         VX_CHECK(enqueue_inputs(e));
-        VX_CHECK(enqueue_body(e, 2, F(e->temb) + (size_t)k++ * e->cfg.hidden));
-        ProfSpan sp(e->ctx, "local.cfm_cfg_euler");
-        VX_CHECK(launch_cfm_cfg_euler(s, F(e->x), F(e->out), F(e->out) + n, n, dt, o.cfg_value,
-                                      o.use_cfg_zero_star ? 1u : 0u));
+        VX_CHECK(enqueue_body(e, 2, F(e->temb) + (size_t)k++ * e->cfg.hidden, e->out_euler));
+        if (e->out_euler) {
+            ProfSpan sp(e->ctx, "local.out_cfg_euler");
+            CfmOutEulerArgs a;
+            a.rows = F(e->norm);
+            a.tokens = e->S;
+            a.x0 = c.n_mu + 1u + c.n_cond;
+            a.patch = c.patch;
+            a.feat = c.feat_dim;
+            a.hidden = c.hidden;
+            a.w = static_cast<const __half *>(e->out_proj.w.ptr);
+            a.bias = e->out_proj.b;
+            a.bias_dtype = e->out_proj.bt;
+            a.out = F(e->out);
+            a.x = F(e->x);
+            a.dt = dt;
+            a.cfg = o.cfg_value;
+            a.zero_star = o.use_cfg_zero_star ? 1u : 0u;
+            a.counter = static_cast<uint32_t *>(e->out_ctr->ptr);
+            VX_CHECK(launch_cfm_out_euler(s, a));
+        } else {
+            ProfSpan sp(e->ctx, "local.cfm_cfg_euler");
+            VX_CHECK(launch_cfm_cfg_euler(s, F(e->x), F(e->out), F(e->out) + n, n, dt, o.cfg_value,
+                                          o.use_cfg_zero_star ? 1u : 0u));
+        }
         est += 2;
     }
     if (calls) *calls = est;
@@ -874,6 +900,15 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
                 }
             }
             e->sk = true;
+            // out_proj + Euler update in one launch (F16 out_proj, rows of the
+            // normed hidden f32 and 16-byte aligned).
+            if (e->out_proj.w.wt == WT_F16 && e->out_proj.w.dtype == 1 &&
+                cfm_out_euler_eligible(c.patch, c.feat_dim, H, e->out_proj.w.ptr)) {
+                if ((st = vx_alloc(ctx, 256u, &e->out_ctr))) return bail(st);
+                if (hipMemsetAsync(e->out_ctr->ptr, 0, 256u, ctx->stream) != hipSuccess)
+                    return bail(fail(VX_ERR_HIP, "hipMemsetAsync of LocDiT state failed"));
+                e->out_euler = true;
+            }
         }
     }
     if (e->dense_fused && (st = launch_rope_pos_table(ctx->stream, reinterpret_cast<float2 *>(e->rope_tab->ptr),

@@ -650,6 +650,24 @@ int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a);
 int launch_cfm_noise(hipStream_t s, float *x, uint32_t n, const uint32_t *dev_seed, uint64_t seed, float temperature);
 int launch_cfm_cfg_euler(hipStream_t s, float *x, const float *pos, const float *neg, uint32_t n, float dt, float cfg,
                          uint32_t zero_star);
+// The estimator's out_proj (F16 weights) for the x tokens of both CFG sequences,
+// then the CFG-Zero* Euler update, in one launch (the update by the last
+// workgroup to finish). counter: a device word that is zero between launches.
+constexpr uint32_t kOutEulerMaxRows = 16;   // 2 * patch
+struct CfmOutEulerArgs {
+    const float *rows = nullptr;     // normed hidden rows [2 * tokens][hidden], 16-byte aligned
+    uint32_t tokens = 0, x0 = 0, patch = 0, feat = 0, hidden = 0;   // x tokens: rows x0 .. x0 + patch - 1
+    const __half *w = nullptr;       // out_proj [feat][hidden]
+    const void *bias = nullptr;      // nullable, [feat], f32 (bias_dtype 0) or f16
+    uint32_t bias_dtype = 0;
+    float *out = nullptr;            // [2][patch * feat]: conditional, unconditional
+    float *x = nullptr;              // [patch * feat], updated in place
+    float dt = 0.f, cfg = 0.f;
+    uint32_t zero_star = 0;
+    uint32_t *counter = nullptr;
+};
+bool cfm_out_euler_eligible(uint32_t patch, uint32_t feat, uint32_t hidden, const void *w);
+int launch_cfm_out_euler(hipStream_t s, const CfmOutEulerArgs &a);
 // t from t_dev[t_index] when t_dev is set.
 // rows > 1: row r from t_dev[t_index + r] into out + r * dim.
 int launch_time_sinusoidal(hipStream_t s, float *out, uint32_t dim, float t, const float *t_dev, uint32_t t_index,
