@@ -42,12 +42,19 @@ __global__ __launch_bounds__(256) void k_cfm_noise(float *x, uint32_t n, const u
 // under CFG-Zero* (else 1); x -= dt * (n*s + cfg*(p - n*s)). One workgroup; the
 // dot products are block reductions over n <= 1024 elements.
 // One 256-thread workgroup: the CFG-Zero* guided velocity and the Euler update.
+// COHERENT: pos and neg were written by other workgroups of the launch and are
+// read with device-scope loads (past this workgroup's L2).
+template <bool COHERENT = false>
 __device__ __forceinline__ void cfg_euler_block(float *x, const float *pos, const float *neg, uint32_t n, float dt,
                                                 float cfg, uint32_t zero_star) {
+    auto ld = [](const float *p) {
+        if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else return *p;
+    };
     __shared__ float red[2][4];
     float pn = 0.f, nn = 0.f;
     for (uint32_t i = threadIdx.x; i < n; i += 256u) {
-        const float p = pos[i], q = neg[i];
+        const float p = ld(pos + i), q = ld(neg + i);
         pn += p * q;
         nn += q * q;
     }
@@ -65,7 +72,7 @@ __device__ __forceinline__ void cfg_euler_block(float *x, const float *pos, cons
     nn = red[1][0] + red[1][1] + red[1][2] + red[1][3];
     const float scale = zero_star ? pn / (nn + 1.0e-8f) : 1.0f;
     for (uint32_t i = threadIdx.x; i < n; i += 256u) {
-        const float p = pos[i], q = neg[i];
+        const float p = ld(pos + i), q = ld(neg + i);
         const float guided = q * scale + cfg * (p - q * scale);
         x[i] -= dt * guided;
     }
@@ -79,10 +86,14 @@ __global__ __launch_bounds__(256) void k_cfm_cfg_euler(float *x, const float *po
 // The estimator's out_proj for the x tokens of both sequences (seq_linear_bias,
 // F16 weights: one wave per output feature, each lane a contiguous 1/64 of the
 // row, then a wave reduction), and then the update above, run by the last
-// workgroup to finish: each workgroup publishes its outputs with a device-scope
-// release fence and counts itself in a.counter; the one that takes the count to
-// gridDim.x acquires and applies cfg_euler_block, then resets the counter for
-// the next launch. No workgroup waits for another.
+// workgroup to finish. Each workgroup stores its outputs with device-scope
+// stores (written through to the device's coherence point), waits until every
+// one is acknowledged, and counts itself in a.counter; the one that takes the
+// count to gridDim.x reads all outputs with device-scope loads, applies
+// cfg_euler_block and resets the counter for the next launch. No workgroup
+// waits for another. (A device-scope fence here would write back and
+// invalidate the whole L2 of every workgroup's XCD: tens of microseconds over a
+// few hundred workgroups on MI355X.)
 __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
     __shared__ uint32_t is_last;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
@@ -130,17 +141,18 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
             for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
             if (lane == r) {
                 const uint32_t b = r / a.patch, p = r - b * a.patch;
-                a.out[(size_t)b * n + (size_t)p * a.feat + f] = v + bias;
+                __hip_atomic_store(a.out + (size_t)b * n + (size_t)p * a.feat + f, v + bias, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
-    __threadfence();   // release this workgroup's outputs device-wide
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0);   // every output store acknowledged
     __syncthreads();
     if (threadIdx.x == 0) is_last = atomicAdd(a.counter, 1u) == gridDim.x - 1u;
     __syncthreads();
     if (!is_last) return;
-    __threadfence();   // acquire every workgroup's outputs
-    cfg_euler_block(a.x, a.out, a.out + n, n, a.dt, a.cfg, a.zero_star);
+    cfg_euler_block<true>(a.x, a.out, a.out + n, n, a.dt, a.cfg, a.zero_star);
     if (threadIdx.x == 0) *a.counter = 0u;
 }
 
