@@ -193,11 +193,49 @@ def parse():
                     help="run only the prefill, warmup and timed decode steps, no graph-timed legs (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one copy kernel of known size and exit (PMC calibration)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="time the vendor library's plain f16 GEMMs (torch.matmul -> hipBLASLt) at the T=384 "
+                         "projection shapes and exit: the library ceiling for these shapes")
     return ap.parse_args()
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def vendor_gemm(T=384, reps=50):
+    """The vendor library's plain f16 GEMM (torch.matmul, which hipBLASLt serves) at
+    the four projection shapes of one prefill layer, single f16 operands (no hi/lo
+    split, no Q8_0 dequant): back-to-back launches timed with torch events. A
+    reference point for the achievable MFMA fraction at this token count."""
+    import torch
+    dev = torch.device("cuda")
+    out = {}
+    total_us = total_fl = 0.0
+    for name, N, K in (("qkv", H + 2 * KV, H), ("attn_out", H, H), ("swiglu", 2 * F, H), ("down", H, F)):
+        a = torch.randn(T, K, device=dev, dtype=torch.float16)
+        b = torch.randn(N, K, device=dev, dtype=torch.float16)
+        for _ in range(5):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c = a @ b.t()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        fl = 2.0 * T * N * K
+        out[name] = {"M": T, "N": N, "K": K, "us": round(us, 2), "tflops": round(fl / us / 1e6, 1),
+                     "frac": round(fl / us / 1e6 / F16_MFMA_PEAK_TFLOPS, 4)}
+        total_us += us
+        total_fl += fl
+        del c
+    out["layer"] = {"us": round(total_us, 2), "frac": round(total_fl / total_us / 1e6 / F16_MFMA_PEAK_TFLOPS, 4),
+                    "prefill_gemm_ms_28L": round(28 * total_us / 1e3, 3)}
+    out["library"] = f"torch {torch.__version__} (hipBLASLt)"
+    log(f"vendor f16 GEMMs, one layer at T={T}: {total_us:.1f} us -> {out['layer']['frac']:.3f} of the f16 peak")
+    print(json.dumps({"vendor_gemm": out}), flush=True)
 
 
 def copy_calibration():
@@ -549,6 +587,9 @@ def main():
         print(f"bench.py runs on one GPU only: the BaseLM decode path has no multi-GPU form "
               f"(got --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    if args.vendor_gemm:
+        vendor_gemm(args.prefill_tokens)
+        return
     if args.copy_calibration:
         copy_calibration()
         return
