@@ -25,11 +25,14 @@ inline float *F(vx_buf *b) { return static_cast<float *>(b->ptr); }
 inline __half *H(vx_buf *b) { return static_cast<__half *>(b->ptr); }
 
 // Split-K factor for a projection of n_tiles 128-row tiles and tt-token tiles:
-// enough workgroups to cover the CUs, at least four 32-column blocks per split.
+// as many workgroups as fit one per CU (rounded down: a second workgroup on a CU
+// runs at well under twice one's throughput, so the CUs that hold two would set
+// the time; measured on MI355X, rounding up instead made the T = 384 prefill 5%
+// slower, T = 256 and 512 2%), at least four 32-column blocks per split.
 uint32_t pick_split(const vx_ctx *ctx, uint32_t tt, uint32_t n_tiles, uint32_t T, uint32_t K) {
     const uint32_t tiles = n_tiles * ((T + tt - 1u) / tt);
     const uint32_t cus = ctx->props.multiProcessorCount > 0 ? (uint32_t)ctx->props.multiProcessorCount : 256u;
-    uint32_t ks = (cus + tiles - 1u) / tiles;
+    uint32_t ks = std::max<uint32_t>(1u, cus / tiles);
     ks = std::min<uint32_t>(ks, tt > 64u ? 8u : 4u);
     ks = std::min<uint32_t>(ks, std::max<uint32_t>(1u, K / 128u));
     return std::max<uint32_t>(ks, 1u);
