@@ -33,7 +33,7 @@
 // weights as exact hi/lo f16 pairs of d*q (three MFMAs per k-step, no scale
 // step), fragments prefetched a block ahead, double-buffered block products,
 // split K to put two workgroups on every CU, a stream-K schedule of the
-// SwiGLU tiles (equal block ranges over two workgroups per CU), and eight-wave
+// SwiGLU tiles (equal block ranges over one or two workgroups per CU), and eight-wave
 // workgroups of 64 x 32 wave tiles (two waves per SIMD from one tile, the
 // gate/up rows exchanged through LDS): 5.0 ms of GEMMs per T = 384 prefill
 // against 4.0 ms, the A fragments then being read from LDS by four waves each.
