@@ -27,7 +27,11 @@
 //     is as long as its 16 MFMAs and a wave issues both in order, so the block
 //     loop is unrolled over the ring slots (constant LDS offsets, no address
 //     VALU), the DMA addresses are scalar, and the block is split by output
-//     half so that scale FMAs and widening issue between MFMAs.
+//     half so that scale FMAs and widening issue between MFMAs;
+//   * the epilogue stages the results in the ring's LDS and writes them with
+//     16-byte stores of contiguous runs (split-K partial slabs, plain outputs and
+//     the tiled SwiGLU planes): per-workgroup timestamps on MI355X showed the
+//     scattered 4-byte partial stores taking 3.8-6.1 us of a 12-58 us launch.
 // Measured alternatives, slower on MI355X at T = 384: 16-column stages, one
 // workgroup per CU with a deeper ring (up to 7 slots), f16 quants in LDS,
 // weights as exact hi/lo f16 pairs of d*q (three MFMAs per k-step, no scale
@@ -317,6 +321,78 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
 
     float *const out0 = sg.out;
     const uint32_t ldo0 = sg.ldo, rows0 = sg.rows;
+    // ---- wide epilogues: the results go through LDS (the ring is free once every
+    // wave has drained its DMA) and leave as 16-byte stores of contiguous runs,
+    // instead of 4- or 2-byte stores scattered over every lane's 64 results.
+    if constexpr (EPI == GEPI_SWIGLU) {
+        // Tiled plane output: each 32-column group of the tile is one contiguous
+        // 8 KB block per plane in that layout, built in LDS and copied out whole.
+        // Token rows past T (the last tile's padding) get zeros.
+        if (a.o_tiled && a.oh && !out0) {
+            _Float16 *const st = reinterpret_cast<_Float16 *>(ring);   // [plane][group][128][32]
+            __syncthreads();   // ring idle: every wave has drained its DMA and read its last block
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t ti = 64u * wm + 32u * (uint32_t)mt + 8u * (uint32_t)(r >> 2) + 4u * hs + (uint32_t)(r & 3);
+                    const float g = acc[mt][0][r], u = acc[mt][1][r];
+                    const float v = m0 + ti < a.T ? g / (1.0f + expf(-g)) * u : 0.f;   // matvec_swiglu.comp:67
+                    const _Float16 hv = (_Float16)v;
+                    const uint32_t o = (wn * 128u + ti) * 32u + 8u * ((l32 >> 3) ^ (((ti >> 1) ^ (ti >> 3)) & 3u)) +
+                                       (l32 & 7u);
+                    st[o] = hv;
+                    st[2u * 128u * 32u + o] = (_Float16)(v - (float)hv);
+                }
+            __syncthreads();
+#pragma unroll
+            for (uint32_t i = tid; i < 4u * 512u; i += 256u) {
+                const uint32_t blk = i / 512u, j = i % 512u;   // block = (plane, group); 512 chunks of 16 bytes
+                const uint32_t col0 = 64u * tn + 32u * (blk & 1u);
+                if (col0 >= rows0) continue;
+                __half *const dst = ((blk >> 1) ? a.ol : a.oh) + tiled_plane_index(m0, col0, a.ldp);
+                *reinterpret_cast<uint4 *>(dst + 8u * j) = *reinterpret_cast<const uint4 *>(st + blk * 4096u + 8u * j);
+            }
+            return;
+        }
+    } else {
+        // Plain stores (a whole product, or one split's partial slab): two passes
+        // of 64 tokens, 512 contiguous bytes per token row.
+        const bool plain =
+            EPI == GEPI_STORE ? (a.ksplit == 1u || a.split_store != 0u) : (a.ws != nullptr && a.ksplit > 1u);
+        if (plain && a.wide) {
+            float *const base = EPI == GEPI_STORE ? out0 + (a.ksplit > 1u ? ks * a.ws_stride : 0u)
+                                                  : a.ws + ks * a.ws_stride;
+            const float f = EPI == GEPI_STORE ? a.alpha : a.scale;
+            float *const st = reinterpret_cast<float *>(ring);
+            constexpr uint32_t kLd = kBN + 8;   // staging row: the two half-waves' tokens 32 banks apart
+            const uint32_t row_base = tile_row<EPI>(tn, sg.tile0, 0);
+#pragma unroll
+            for (uint32_t pass = 0; pass < 2u; ++pass) {
+                __syncthreads();   // ring (pass 0) or the previous pass's reads are done
+                if (wm == pass) {
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                st[(32u * mt + 8u * (uint32_t)(r >> 2) + 4u * hs + (uint32_t)(r & 3)) * kLd +
+                                   64u * wn + 32u * nt + l32] = acc[mt][nt][r] * f;
+                }
+                __syncthreads();
+#pragma unroll
+                for (uint32_t i = tid; i < 64u * (kBN / 4u); i += 256u) {
+                    const uint32_t tl = i / (kBN / 4u), c4 = i % (kBN / 4u);
+                    const uint32_t tok = m0 + 64u * pass + tl, row = row_base + 4u * c4;
+                    if (tok < a.T && row < rows0)
+                        *reinterpret_cast<float4 *>(base + (size_t)tok * ldo0 + row) =
+                            *reinterpret_cast<const float4 *>(st + tl * kLd + 4u * c4);
+                }
+            }
+            return;
+        }
+    }
     // ---- epilogue. Lane (l32, hs) of wave (wm, wn) holds, for tile (mt, nt),
     // weight row rho = 64wn + 32nt + l32 and tokens m0 + 64wm + 32mt + 8(r/4) + 4hs + r%4.
     // It issues stores and atomics only (no loads): a load here would make every
@@ -458,6 +534,11 @@ int launch_gemm_q8p(hipStream_t s, GemmArgs a) {
     if (total == 0) return VX_OK;
     const uint64_t grid = (total + 7u) / 8u * 8u;
     if (grid > 0x7fffffffull) return fail(VX_ERR_UNSUPPORTED, "gemm: grid too large");
+    // 16-byte epilogue stores need every output row start and slab 16-byte aligned.
+    a.wide = (a.ws_stride % 4u == 0u && reinterpret_cast<uintptr_t>(a.ws) % 16u == 0u) ? 1u : 0u;
+    if (a.epi != GEPI_SWIGLU)
+        for (uint32_t i = 0; i < a.nseg; ++i)
+            if (a.seg[i].rows % 4u || a.seg[i].ldo % 4u || reinterpret_cast<uintptr_t>(a.seg[i].out) % 16u) a.wide = 0;
     switch (a.epi) {
         case GEPI_STORE: k_gemm_q8p<GEPI_STORE><<<(unsigned)grid, 256, 0, s>>>(a); break;
         case GEPI_RESIDUAL: k_gemm_q8p<GEPI_RESIDUAL><<<(unsigned)grid, 256, 0, s>>>(a); break;

@@ -347,6 +347,7 @@ struct GemmArgs {
     // stores alpha * (its partial product) to out + s * ws_stride (each segment's
     // [T][ldo]) with plain stores instead of atomic adds; the consumer sums them.
     uint32_t split_store = 0;
+    uint32_t wide = 0;              // set by launch_gemm: plain-store epilogues may use 16-byte stores
     // 1: the short-batch F16 kernel's operand layout: the weights (seg[i].w) and
     // the X planes are in the fragment layout (frag16_index), and GEPI_SWIGLU
     // writes oh/ol in it (width seg[0].rows).
