@@ -543,7 +543,17 @@ typedef struct vx_baselm_options {
     uint32_t strict_geometry;    /* 1: enforce the VoxCPM2 geometry (baselm.rs:102-113);
                                     0: allow other layer counts/sizes for harnesses */
     uint32_t attn_splits;        /* 0 = choose from active_context_length */
+    uint32_t prefill_schedule;   /* VX_PREFILL_* (batched prefill, gate/up GEMM) */
 } vx_baselm_options;
+/* Workgroup schedule of the batched prefill's gate/up projection (no counterpart
+ * in the reference, which has no batched MFMA prefill). */
+#define VX_PREFILL_AUTO 0u       /* stream-K when the tiles just exceed the CUs,
+                                    else one tile per workgroup                  */
+#define VX_PREFILL_TILES 1u      /* one tile per workgroup                       */
+#define VX_PREFILL_STREAMK_TAIL_FIRST 2u /* stream-K with each workgroup's tile
+                                    tail computed before its head: the hand-off
+                                    order AUTO meets only when a workgroup starts
+                                    late; bit-identical results, slower          */
 
 /* BaseLmEngine::new (baselm.rs:451-586). Validates every tensor of the model
  * against the config (validate_layer baselm.rs:227-262) and allocates the

@@ -40,6 +40,9 @@ pub const VX_EXEC_GRAPH: u32 = 0;
 pub const VX_EXEC_FUSED: u32 = 1;
 pub const VX_EXEC_REFERENCE: u32 = 2;
 pub const VX_EXEC_PERSISTENT: u32 = 3;
+pub const VX_PREFILL_AUTO: u32 = 0;
+pub const VX_PREFILL_TILES: u32 = 1;
+pub const VX_PREFILL_STREAMK_TAIL_FIRST: u32 = 2;
 pub const VX_BASELM_BUF_HIDDEN: u32 = 0;
 pub const VX_BASELM_BUF_NORM: u32 = 1;
 pub const VX_BASELM_BUF_Q: u32 = 2;
@@ -881,6 +884,7 @@ pub struct VxBaselmOptions {
     pub exec_mode: u32,
     pub strict_geometry: u32,
     pub attn_splits: u32,
+    pub prefill_schedule: u32,
 }
 
 #[link(name = "voxhip")]

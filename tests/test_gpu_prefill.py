@@ -16,7 +16,7 @@ import pytest
 import voxref
 from conftest import rel_l2
 from voxgen_amd import abi, synth
-from voxgen_amd.baselm import BaseLmEngine
+from voxgen_amd.baselm import BaseLmEngine, config_struct
 from voxgen_amd.runtime import Model
 
 pytestmark = pytest.mark.gpu
@@ -67,6 +67,42 @@ def test_batched_prefill_matches_sequential_oracle(ctx, small, n):
             assert rel_l2(f16(got[l, :n]), f16(want[l, :n])) < 1e-3, (name, l)
         assert np.all(got[:, n:] == 0)
     eng.close()
+
+
+def test_batched_prefill_gate_up_schedules(ctx, small):
+    """The gate/up projection's workgroup schedules over 300 tokens: 3 token tiles x
+    96 tiles of 64 gate/up rows = 288 tiles, just above 256 CUs, so "auto" runs the
+    stream-K kernel. "streamk_tail_first" runs its other hand-off path (the tail
+    stores and counts, the head finishes) and must give the same bits; "tiles"
+    (one tile per workgroup) sums each tile's blocks in one chain instead of two
+    parts, so it differs by fp32 rounding only. All three against the oracle."""
+    cfg, m, model = small
+    n = 300
+    toks = [int(t) for t in synth.uniform_u32(n, 0x5EED010A, cfg["vocab_size"])]
+    o = oracle_of(m, cfg)
+    for p, t in enumerate(toks):
+        o.decode_token(t, p)
+    got = {}
+    for sched in ("auto", "streamk_tail_first", "tiles"):
+        print(f"batched prefill n={n} schedule={sched}", flush=True)
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=False, prefill_schedule=sched)
+        eng.prefill_tokens_batched(toks)
+        got[sched] = (eng.output(), kv_rows(eng, "kv_k", 2, 1024)[:, :n], kv_rows(eng, "kv_v", 2, 1024)[:, :n])
+        eng.close()
+        assert rel_l2(got[sched][0], o.norm) < 1e-3, sched
+        for l in range(2):
+            assert rel_l2(f16(got[sched][1][l]), f16(o.kv_k.reshape(2, 1024, 256)[l, :n])) < 1e-3, (sched, l)
+            assert rel_l2(f16(got[sched][2][l]), f16(o.kv_v.reshape(2, 1024, 256)[l, :n])) < 1e-3, (sched, l)
+    for x, y in zip(got["auto"], got["streamk_tail_first"]):
+        assert np.array_equal(x, y)
+    assert rel_l2(got["auto"][0], got["tiles"][0]) < 1e-4
+    assert np.array_equal(got["auto"][1][0], got["tiles"][1][0])   # layer 0's K rows precede any gate/up
+    assert rel_l2(f16(got["auto"][2][1]), f16(got["tiles"][2][1])) < 1e-3
+    opt = abi.BaseLmOptions(abi.EXEC_GRAPH, 0, 0, 3)   # no such schedule
+    h = abi.ENGINE()
+    with pytest.raises(abi.VxError) as err:
+        abi.call("vx_baselm_create", ctx.handle, model.handle, C.byref(config_struct(cfg)), C.byref(opt), C.byref(h))
+    assert err.value.name == "VX_ERR_INVALID_ARG" and "prefill_schedule" in str(err.value)
 
 
 def test_batched_prefill_continues_a_decode_and_spans_chunks(ctx, small):

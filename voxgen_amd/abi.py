@@ -26,6 +26,7 @@ STATUS_CODE = {v: k for k, v in STATUS.items()}
 
 DTYPE_F32, DTYPE_F16, DTYPE_Q8_0 = 0, 1, 8
 EXEC_GRAPH, EXEC_FUSED, EXEC_REFERENCE, EXEC_PERSISTENT = 0, 1, 2, 3
+PREFILL_AUTO, PREFILL_TILES, PREFILL_STREAMK_TAIL_FIRST = 0, 1, 2
 BUF = dict(HIDDEN=0, NORM=1, Q=2, K=3, V=4, ATTENTION=5, GATE=6, BRANCH=7, LOGITS=8,
            SCORES=9, KV_K=10, KV_V=11, POSITION=12)
 
@@ -132,7 +133,7 @@ BaseLmConfig = _struct("BaseLmConfig", [
     ("rope_longrope", u32), ("embedding_scale", f32), ("residual_scale", f32),
     ("logit_scale", f32), ("tied_output", u32)])
 BaseLmOptions = _struct("BaseLmOptions", [("exec_mode", u32), ("strict_geometry", u32),
-                                          ("attn_splits", u32)])
+                                          ("attn_splits", u32), ("prefill_schedule", u32)])
 TopLogit = _struct("TopLogit", [("token_id", u32), ("logit", f32)])
 StepResult = _struct("StepResult", [("position", u32), ("elapsed_ms", f64),
                                     ("final_hidden_checksum", f64), ("final_hidden_l2", f64),

@@ -16,6 +16,9 @@ from .runtime import Buffer, Context, Model
 
 EXEC_MODES = {"graph": abi.EXEC_GRAPH, "fused": abi.EXEC_FUSED, "reference": abi.EXEC_REFERENCE,
               "persistent": abi.EXEC_PERSISTENT}
+# Workgroup schedule of the batched prefill's gate/up projection (VX_PREFILL_*).
+PREFILL_SCHEDULES = {"auto": abi.PREFILL_AUTO, "tiles": abi.PREFILL_TILES,
+                     "streamk_tail_first": abi.PREFILL_STREAMK_TAIL_FIRST}
 
 
 def config_struct(cfg: dict) -> abi.BaseLmConfig:
@@ -52,10 +55,11 @@ class StepResult:
 
 class BaseLmEngine:
     def __init__(self, ctx: Context, model: Model, config: dict, exec_mode: str = "graph",
-                 strict_geometry: bool = True, attn_splits: int = 0):
+                 strict_geometry: bool = True, attn_splits: int = 0, prefill_schedule: str = "auto"):
         self.ctx, self.model, self.config = ctx, model, dict(config)
         self.handle = None
-        opt = abi.BaseLmOptions(EXEC_MODES[exec_mode], 1 if strict_geometry else 0, attn_splits)
+        opt = abi.BaseLmOptions(EXEC_MODES[exec_mode], 1 if strict_geometry else 0, attn_splits,
+                                PREFILL_SCHEDULES[prefill_schedule])
         h = abi.ENGINE()
         abi.call("vx_baselm_create", ctx.handle, model.handle, C.byref(config_struct(config)),
                  C.byref(opt), C.byref(h))

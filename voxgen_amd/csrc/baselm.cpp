@@ -670,6 +670,7 @@ PrefillStack make_stack(vx_baselm *e) {
     p.kc = H(e->kv_k);
     p.vc = H(e->kv_v);
     p.work = &e->pf;
+    p.schedule = e->opt.prefill_schedule;
     return p;
 }
 
@@ -943,6 +944,8 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
     e->rope_scaling = vx_baselm_rope_scaling_factor(&c);
     // Context splits of the decode attention: one per 64 positions of the active
     // context, at most kMaxFoldedSplits so that attn_out can merge them itself.
+    if (o.prefill_schedule > VX_PREFILL_STREAMK_TAIL_FIRST)
+        return bail(fail(VX_ERR_INVALID_ARG, "unknown prefill_schedule %u", o.prefill_schedule));
     uint32_t splits = o.attn_splits;
     if (splits == 0)
         splits = std::min<uint32_t>(kMaxFoldedSplits, std::max<uint32_t>(1u, (c.active_context_length + 63u) / 64u));

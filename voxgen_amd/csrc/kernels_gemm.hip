@@ -152,29 +152,21 @@ __device__ __forceinline__ void issue_stage(const Src &src, uint32_t blk, uint32
     dma4(src.d + (size_t)blk * kDBytes, 4u * lane, slot + kDOff + (wave & 1u) * 256u);
 }
 
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
+// The LDS ring of the block loop; the epilogues stage their results in it too.
+__device__ __forceinline__ uint8_t *gemm_ring() {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kStageBytes];
-    const uint32_t ring_lds = lds_addr(ring);
+    return ring;
+}
 
-    // XCD-major order: workgroup b runs on XCD b % 8; consecutive ids of one XCD
-    // cover the token tiles of the same weight rows.
-    const uint32_t b = blockIdx.x;
-    const uint32_t id = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
-    const uint32_t per_split = a.ntn * a.ntm;
-    if (id >= per_split * a.ksplit) return;
-    const uint32_t ks = id / per_split, rem = id - ks * per_split;
-    const uint32_t tn = rem / a.ntm, tm = rem - tn * a.ntm;
-    const uint32_t m0 = tm * kBM;
-    uint32_t seg = 0;
-    if constexpr (EPI != GEPI_SWIGLU) {
-        while (seg + 1 < a.nseg && tn >= a.seg[seg + 1].tile0) ++seg;
-    }
-    const GemmSeg &sg = a.seg[seg];
+// Blocks kb0 .. kb0 + nkb - 1 (nkb >= 1) of tile (tn, tm) of segment sg into acc
+// (overwritten). Every DMA of the wave has landed when this returns; the ring is
+// reused only after a barrier (other waves may still read their last block).
+template <int EPI>
+__device__ __forceinline__ void tile_blocks(const GemmArgs &a, const GemmSeg &sg, uint32_t tn, uint32_t tm,
+                                            uint32_t kb0, uint32_t nkb, acc16 (&acc)[2][2]) {
+    uint8_t *const ring = gemm_ring();
+    const uint32_t ring_lds = lds_addr(ring);
     const uint32_t nblk = a.K / 32u;
-    const uint32_t kb0 = ks * nblk / a.ksplit, kb1 = (ks + 1u) * nblk / a.ksplit;
-    if (kb1 == kb0) return;   // nothing to add (ksplit is clamped to the block count)
-    const uint32_t nkb = kb1 - kb0;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -220,7 +212,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
         issue_stage(src, kb0 + ((uint32_t)s < nkb ? (uint32_t)s : nkb - 1u), ring_lds + (uint32_t)s * kStageBytes, wave,
                     lane);
 
-    acc16 acc[2][2], p[2][2];
+    acc16 p[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -318,53 +310,123 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
         for (int r = 0; r < 16; ++r) acc[mt][1][r] = fmaf(dprev1, p[mt][1][r], acc[mt][1][r]);
     // Drain the DMA of the clamped trailing stages before the workgroup ends.
     wait_vm<0>();
+}
 
-    float *const out0 = sg.out;
-    const uint32_t ldo0 = sg.ldo, rows0 = sg.rows;
-    // ---- wide epilogues: the results go through LDS (the ring is free once every
-    // wave has drained its DMA) and leave as 16-byte stores of contiguous runs,
-    // instead of 4- or 2-byte stores scattered over every lane's 64 results.
-    if constexpr (EPI == GEPI_SWIGLU) {
-        // Tiled plane output: each 32-column group of the tile is one contiguous
-        // 8 KB block per plane in that layout, built in LDS and copied out whole.
-        // Token rows past T (the last tile's padding) get zeros.
-        if (a.o_tiled && a.oh && !out0) {
-            _Float16 *const st = reinterpret_cast<_Float16 *>(ring);   // [plane][group][128][32]
-            __syncthreads();   // ring idle: every wave has drained its DMA and read its last block
+// Accumulator layout: lane (l32, hs) of wave (wm, wn) holds, for tile (mt, nt),
+// tile row rho = 64wn + 32nt + l32 and tokens m0 + 64wm + 32mt + 8(r/4) + 4hs + r%4.
+// SwiGLU tiles interleave 32 gate rows (nt = 0) with the same 32 up rows (nt = 1),
+// so output column 64tn + 32wn + l32 is silu(acc[.][0]) * acc[.][1].
+
+// SwiGLU output to tiled planes: each 32-column group of the tile is one
+// contiguous 8 KB block per plane in that layout, built in LDS and copied out
+// whole with 16-byte stores. Token rows past T (the last tile's padding) get
+// zeros. Every thread of the workgroup calls it (barriers inside).
+__device__ __forceinline__ void swiglu_planes(const GemmArgs &a, uint32_t tn, uint32_t m0, const acc16 (&acc)[2][2]) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave & 1u, wn = wave >> 1;
+    _Float16 *const st = reinterpret_cast<_Float16 *>(gemm_ring());   // [plane][group][128][32]
+    __syncthreads();   // ring idle: every wave has drained its DMA and read its last block
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t ti = 64u * wm + 32u * (uint32_t)mt + 8u * (uint32_t)(r >> 2) + 4u * hs + (uint32_t)(r & 3);
-                    const float g = acc[mt][0][r], u = acc[mt][1][r];
-                    const float v = m0 + ti < a.T ? g / (1.0f + expf(-g)) * u : 0.f;   // matvec_swiglu.comp:67
-                    const _Float16 hv = (_Float16)v;
-                    const uint32_t o = (wn * 128u + ti) * 32u + 8u * ((l32 >> 3) ^ (((ti >> 1) ^ (ti >> 3)) & 3u)) +
-                                       (l32 & 7u);
-                    st[o] = hv;
-                    st[2u * 128u * 32u + o] = (_Float16)(v - (float)hv);
-                }
-            __syncthreads();
-#pragma unroll
-            for (uint32_t i = tid; i < 4u * 512u; i += 256u) {
-                const uint32_t blk = i / 512u, j = i % 512u;   // block = (plane, group); 512 chunks of 16 bytes
-                const uint32_t col0 = 64u * tn + 32u * (blk & 1u);
-                if (col0 >= rows0) continue;
-                __half *const dst = ((blk >> 1) ? a.ol : a.oh) + tiled_plane_index(m0, col0, a.ldp);
-                *reinterpret_cast<uint4 *>(dst + 8u * j) = *reinterpret_cast<const uint4 *>(st + blk * 4096u + 8u * j);
-            }
-            return;
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t ti = 64u * wm + 32u * (uint32_t)mt + 8u * (uint32_t)(r >> 2) + 4u * hs + (uint32_t)(r & 3);
+            const float g = acc[mt][0][r], u = acc[mt][1][r];
+            const float v = m0 + ti < a.T ? g / (1.0f + expf(-g)) * u : 0.f;   // matvec_swiglu.comp:67
+            const _Float16 hv = (_Float16)v;
+            const uint32_t o =
+                (wn * 128u + ti) * 32u + 8u * ((l32 >> 3) ^ (((ti >> 1) ^ (ti >> 3)) & 3u)) + (l32 & 7u);
+            st[o] = hv;
+            st[2u * 128u * 32u + o] = (_Float16)(v - (float)hv);
         }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t i = tid; i < 4u * 512u; i += 256u) {
+        const uint32_t blk = i / 512u, j = i % 512u;   // block = (plane, group); 512 chunks of 16 bytes
+        const uint32_t col0 = 64u * tn + 32u * (blk & 1u);
+        if (col0 >= a.seg[0].rows) continue;
+        __half *const dst = ((blk >> 1) ? a.ol : a.oh) + tiled_plane_index(m0, col0, a.ldp);
+        *reinterpret_cast<uint4 *>(dst + 8u * j) = *reinterpret_cast<const uint4 *>(st + blk * 4096u + 8u * j);
+    }
+}
+
+// SwiGLU output with per-element stores: the f32 output and/or row-major planes.
+// Stores only (no loads): a load here would make every element wait for the
+// stores before it.
+__device__ __forceinline__ void swiglu_scalar(const GemmArgs &a, uint32_t tn, uint32_t m0, const acc16 (&acc)[2][2]) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave & 1u, wn = wave >> 1;
+    float *const out0 = a.seg[0].out;
+    const uint32_t ldo0 = a.seg[0].ldo;
+    const uint32_t row = tile_row<GEPI_SWIGLU>(tn, 0, 64u * wn + l32);
+    if (row >= a.seg[0].rows) return;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const uint32_t tbase = m0 + 64u * wm + 32u * (uint32_t)mt + 4u * hs;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t tok = tbase + 8u * (uint32_t)(r >> 2) + (uint32_t)(r & 3);
+            if (tok >= a.T) continue;
+            const float g = acc[mt][0][r], u = acc[mt][1][r];
+            const float v = g / (1.0f + expf(-g)) * u;   // matvec_swiglu.comp:67
+            if (out0) out0[(size_t)tok * ldo0 + row] = v;
+            if (a.oh) {
+                const size_t o = a.o_tiled ? tiled_plane_index(tok, row, a.ldp) : (size_t)tok * a.ldp + row;
+                const _Float16 hv = (_Float16)v;
+                a.oh[o] = __builtin_bit_cast(__half, hv);
+                a.ol[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
+            }
+        }
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
+    // XCD-major order: workgroup b runs on XCD b % 8; consecutive ids of one XCD
+    // cover the token tiles of the same weight rows.
+    const uint32_t b = blockIdx.x;
+    const uint32_t id = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
+    const uint32_t per_split = a.ntn * a.ntm;
+    if (id >= per_split * a.ksplit) return;
+    const uint32_t ks = id / per_split, rem = id - ks * per_split;
+    const uint32_t tn = rem / a.ntm, tm = rem - tn * a.ntm;
+    const uint32_t m0 = tm * kBM;
+    uint32_t seg = 0;
+    if constexpr (EPI != GEPI_SWIGLU) {
+        while (seg + 1 < a.nseg && tn >= a.seg[seg + 1].tile0) ++seg;
+    }
+    const GemmSeg &sg = a.seg[seg];
+    const uint32_t nblk = a.K / 32u;
+    const uint32_t kb0 = ks * nblk / a.ksplit, kb1 = (ks + 1u) * nblk / a.ksplit;
+    if (kb1 == kb0) return;   // nothing to add (ksplit is clamped to the block count)
+
+    acc16 acc[2][2];
+    tile_blocks<EPI>(a, sg, tn, tm, kb0, kb1 - kb0, acc);
+
+    if constexpr (EPI == GEPI_SWIGLU) {
+        if (a.o_tiled && a.oh && !a.seg[0].out)
+            swiglu_planes(a, tn, m0, acc);
+        else
+            swiglu_scalar(a, tn, m0, acc);
     } else {
-        // Plain stores (a whole product, or one split's partial slab): two passes
-        // of 64 tokens, 512 contiguous bytes per token row.
+        const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, hs = lane >> 5;
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t wm = wave & 1u, wn = wave >> 1;
+        float *const out0 = sg.out;
+        const uint32_t ldo0 = sg.ldo, rows0 = sg.rows;
+        // Plain stores (a whole product, or one split's partial slab) go through
+        // LDS (the ring is free once every wave has drained its DMA) in two passes
+        // of 64 tokens and leave as 16-byte stores, 512 contiguous bytes per token
+        // row, instead of 4-byte stores scattered over every lane's 64 results.
         const bool plain =
             EPI == GEPI_STORE ? (a.ksplit == 1u || a.split_store != 0u) : (a.ws != nullptr && a.ksplit > 1u);
         if (plain && a.wide) {
             float *const base = EPI == GEPI_STORE ? out0 + (a.ksplit > 1u ? ks * a.ws_stride : 0u)
                                                   : a.ws + ks * a.ws_stride;
             const float f = EPI == GEPI_STORE ? a.alpha : a.scale;
-            float *const st = reinterpret_cast<float *>(ring);
+            float *const st = reinterpret_cast<float *>(gemm_ring());
             constexpr uint32_t kLd = kBN + 8;   // staging row: the two half-waves' tokens 32 banks apart
             const uint32_t row_base = tile_row<EPI>(tn, sg.tile0, 0);
 #pragma unroll
@@ -392,35 +454,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
             }
             return;
         }
-    }
-    // ---- epilogue. Lane (l32, hs) of wave (wm, wn) holds, for tile (mt, nt),
-    // weight row rho = 64wn + 32nt + l32 and tokens m0 + 64wm + 32mt + 8(r/4) + 4hs + r%4.
-    // It issues stores and atomics only (no loads): a load here would make every
-    // element wait for the stores before it. Residual adds are atomic adds, which
-    // with one contributor (no split) give exactly h + v; split residual
-    // products go to the partial workspace when one is given.
+        // Per-element epilogue: stores and atomics only (no loads). Residual adds
+        // are atomic adds, which with one contributor (no split) give exactly
+        // h + v; split residual products go to the partial workspace when one is
+        // given.
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const uint32_t tbase = m0 + 64u * wm + 32u * (uint32_t)mt + 4u * hs;
-        if constexpr (EPI == GEPI_SWIGLU) {
-            const uint32_t row = tile_row<EPI>(tn, 0, 64u * wn + l32);
-            if (row < rows0) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t tok = tbase + 8u * (uint32_t)(r >> 2) + (uint32_t)(r & 3);
-                    if (tok >= a.T) continue;
-                    const float g = acc[mt][0][r], u = acc[mt][1][r];
-                    const float v = g / (1.0f + expf(-g)) * u;   // matvec_swiglu.comp:67
-                    if (out0) out0[(size_t)tok * ldo0 + row] = v;
-                    if (a.oh) {
-                        const size_t o = a.o_tiled ? tiled_plane_index(tok, row, a.ldp) : (size_t)tok * a.ldp + row;
-                        const _Float16 hv = (_Float16)v;
-                        a.oh[o] = __builtin_bit_cast(__half, hv);
-                        a.ol[o] = __builtin_bit_cast(__half, (_Float16)(v - (float)hv));
-                    }
-                }
-            }
-        } else {
+        for (int mt = 0; mt < 2; ++mt) {
+            const uint32_t tbase = m0 + 64u * wm + 32u * (uint32_t)mt + 4u * hs;
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const uint32_t row = tile_row<EPI>(tn, sg.tile0, 64u * wn + 32u * (uint32_t)nt + l32);
@@ -446,6 +486,124 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
                 }
             }
         }
+    }
+}
+
+// A tile part in a slot: element (i, j, r) of thread t at float (32i + 16j + r) * 256 + t,
+// so every store or load of a wave covers 256 contiguous bytes.
+__device__ __forceinline__ void sk_store(float *slot, const acc16 (&acc)[2][2]) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                __hip_atomic_store(slot + (size_t)(32 * i + 16 * j + r) * 256u + tid, acc[i][j][r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0);   // every part store acknowledged before the count
+    __syncthreads();
+}
+__device__ __forceinline__ void sk_add(const float *slot, acc16 (&acc)[2][2]) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                acc[i][j][r] += __hip_atomic_load(slot + (size_t)(32 * i + 16 * j + r) * 256u + tid, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Stream-K schedule of the SwiGLU tiles, for a tile count a little above the
+// CU count (which would leave a few CUs a second whole tile): the sequence of
+// (tile, block) pairs, tile major, is cut into gridDim.x equal ranges of
+// a.sk_per > K/32 blocks, one workgroup (one CU) each, so a tile is shared by at
+// most two neighbouring workgroups: its head ends the range of workgroup w and
+// its tail starts that of w + 1. A workgroup first computes the head it holds and
+// stores it to its slot (device-scope stores, past the XCD's L2), acknowledged
+// before it counts itself on the counter of boundary w; then its whole tiles;
+// last the tail it holds, by which time the previous workgroup's head is normally
+// stored: the counter says so, and the tail adds that head (device-scope loads)
+// and runs the epilogue. If the head is not there yet, the tail stores itself and
+// counts, and whichever of the two counts second finishes the tile and clears the
+// counter. Nothing waits on another workgroup, and fp32 addition of the two parts
+// commutes, so the result does not depend on which finishes. TAIL_FIRST computes
+// the tail first, so the store-and-count path runs every time (same result bits).
+template <bool TAIL_FIRST>
+__global__ __launch_bounds__(256, 2) void k_gemm_q8p_sk(GemmArgs a) {
+    __shared__ uint32_t flag;
+    const uint32_t b = blockIdx.x;
+    const uint32_t id = (b & 7u) * (gridDim.x >> 3) + (b >> 3);   // XCD-major, as k_gemm_q8p
+    const uint32_t nblk = a.K / 32u;
+    const uint32_t total = a.ntn * a.ntm * nblk;
+    const uint32_t g0 = min(id * a.sk_per, total), g1 = min(g0 + a.sk_per, total);
+    if (g0 >= g1) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t t_first = g0 / nblk, t_last = (g1 - 1u) / nblk;
+    const uint32_t tail_kb = g0 % nblk, head_n = g1 % nblk;   // 0: the range starts / ends on a tile edge
+    auto slot = [&](uint32_t w, uint32_t part) { return a.sk_ws + ((size_t)w * 2u + part) * kSkTileFloats; };
+    const bool has_head = head_n != 0u, has_tail = tail_kb != 0u;
+    bool first = true;
+    auto run = [&](uint32_t tile, uint32_t kb, uint32_t n, acc16 (&acc)[2][2]) {
+        if (!first) __syncthreads();   // the previous piece's ring and staging reads are done
+        first = false;
+        const uint32_t tn = tile / a.ntm, tm = tile - tn * a.ntm;
+        tile_blocks<GEPI_SWIGLU>(a, a.seg[0], tn, tm, kb, n, acc);
+    };
+    auto finish = [&](uint32_t tile, const acc16 (&acc)[2][2]) {
+        const uint32_t tn = tile / a.ntm;
+        swiglu_planes(a, tn, (tile - tn * a.ntm) * kBM, acc);
+    };
+    auto head = [&]() {   // the head of tile t_last; its tail starts range id + 1
+        acc16 acc[2][2];
+        run(t_last, 0u, head_n, acc);
+        sk_store(slot(id, 1u), acc);
+        if (tid == 0) flag = atomicAdd(a.sk_cnt + id, 1u);
+        __syncthreads();
+        if (flag != 0u) {   // the tail is stored already: finish the tile here
+            sk_add(slot(id + 1u, 0u), acc);
+            if (tid == 0) __hip_atomic_store(a.sk_cnt + id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            finish(t_last, acc);
+        }
+    };
+    auto tail = [&]() {   // the tail of tile t_first; its head ends range id - 1
+        acc16 acc[2][2];
+        run(t_first, tail_kb, nblk - tail_kb, acc);
+        const uint32_t bnd = id - 1u;
+        if (tid == 0) flag = __hip_atomic_load(a.sk_cnt + bnd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        bool done_here = flag != 0u;
+        if (!done_here) {   // the head is still being computed: store, count, and see who is second
+            sk_store(slot(id, 0u), acc);
+            if (tid == 0) flag = atomicAdd(a.sk_cnt + bnd, 1u);
+            __syncthreads();
+            done_here = flag != 0u;
+        }
+        if (done_here) {
+            sk_add(slot(bnd, 1u), acc);
+            if (tid == 0) __hip_atomic_store(a.sk_cnt + bnd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            finish(t_first, acc);
+        }
+    };
+    auto whole = [&]() {
+        const uint32_t full0 = has_tail ? t_first + 1u : t_first, full1 = has_head ? t_last : t_last + 1u;
+        for (uint32_t tile = full0; tile < full1; ++tile) {
+            acc16 acc[2][2];
+            run(tile, 0u, nblk, acc);
+            finish(tile, acc);
+        }
+    };
+    if constexpr (TAIL_FIRST) {
+        if (has_tail) tail();
+        if (has_head) head();
+        whole();
+    } else {
+        if (has_head) head();
+        whole();
+        if (has_tail) tail();
     }
 }
 
@@ -534,6 +692,23 @@ int launch_gemm_q8p(hipStream_t s, GemmArgs a) {
     if (total == 0) return VX_OK;
     const uint64_t grid = (total + 7u) / 8u * 8u;
     if (grid > 0x7fffffffull) return fail(VX_ERR_UNSUPPORTED, "gemm: grid too large");
+    const uint64_t tiles_all = (uint64_t)a.ntn * a.ntm;
+    if (a.epi == GEPI_SWIGLU && a.sk_ws && a.sk_cnt && a.sk_grid >= 8u && a.sk_grid % 8u == 0u && a.o_tiled &&
+        a.oh && !a.seg[0].out && tiles_all > a.sk_grid && tiles_all * 4u <= (uint64_t)a.sk_grid * 5u &&
+        tiles_all * nblk <= 0xffffffffull) {
+        // Stream-K: more tiles than workgroups, so every range is longer than a
+        // tile (at most two workgroups share one; a range that ends inside a tile
+        // has a successor, one that starts inside one a predecessor), and at most
+        // 1.25 tiles per CU, where the second-tile imbalance is worth removing
+        // (from 1.5 up, two resident workgroups per CU do better).
+        a.sk_per = (uint32_t)((tiles_all * nblk + a.sk_grid - 1u) / a.sk_grid);
+        if (a.sk_tail_first)
+            k_gemm_q8p_sk<true><<<a.sk_grid, 256, 0, s>>>(a);
+        else
+            k_gemm_q8p_sk<false><<<a.sk_grid, 256, 0, s>>>(a);
+        VX_LAUNCHED("k_gemm_q8p_sk");
+        return VX_OK;
+    }
     // 16-byte epilogue stores need every output row start and slab 16-byte aligned.
     a.wide = (a.ws_stride % 4u == 0u && reinterpret_cast<uintptr_t>(a.ws) % 16u == 0u) ? 1u : 0u;
     if (a.epi != GEPI_SWIGLU)

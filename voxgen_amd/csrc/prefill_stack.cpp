@@ -93,17 +93,28 @@ int prefill_stack_alloc(vx_ctx *ctx, uint32_t cap, uint32_t nH, uint32_t nF, uin
     // Split-K partials: of the residual projections ([split][T][H]) and of QKV
     // ([split][T][H + 2 KV]); the two uses never overlap in time.
     VX_CHECK(vx_alloc(ctx, (uint64_t)kPrefillMaxSplit * T * (H + 2u * KV) * 4u, &w->ws));
+    // Stream-K SwiGLU: two tile parts per workgroup and a counter per workgroup
+    // boundary, one workgroup per CU; the counters start at zero.
+    const uint32_t cus = ctx->props.multiProcessorCount > 0 ? (uint32_t)ctx->props.multiProcessorCount : 256u;
+    w->sk_grid = cus / 8u * 8u;
+    if (w->sk_grid) {
+        VX_CHECK(vx_alloc(ctx, (uint64_t)w->sk_grid * 2u * kSkTileFloats * 4u, &w->sk_ws));
+        VX_CHECK(vx_alloc(ctx, (uint64_t)w->sk_grid * 4u, &w->sk_cnt));
+        VX_HIP(hipMemsetAsync(w->sk_cnt->ptr, 0, w->sk_cnt->bytes, ctx->stream));
+    }
     w->cap = cap;
     return VX_OK;
 }
 
 void prefill_stack_free(vx_ctx *ctx, StackWork *w) {
-    vx_buf **bufs[] = {&w->h, &w->xh, &w->xl, &w->ah, &w->al, &w->qh, &w->ql, &w->q, &w->k, &w->v, &w->ws};
+    vx_buf **bufs[] = {&w->h,  &w->xh, &w->xl, &w->ah, &w->al,    &w->qh,
+                       &w->ql, &w->q,  &w->k,  &w->v,  &w->ws, &w->sk_ws, &w->sk_cnt};
     for (vx_buf **b : bufs) {
         if (*b) vx_free(ctx, *b);
         *b = nullptr;
     }
     w->cap = 0;
+    w->sk_grid = 0;
 }
 
 int enqueue_prefill_stack(const PrefillStack &p, uint32_t pos0, uint32_t T) {
@@ -309,6 +320,12 @@ int enqueue_prefill_stack(const PrefillStack &p, uint32_t pos0, uint32_t T) {
             g.oh = H(w.ah);
             g.ol = H(w.al);
             g.ldp = nF;
+            if (tiled && w.sk_grid && p.schedule != VX_PREFILL_TILES) {
+                g.sk_ws = F(w.sk_ws);
+                g.sk_cnt = static_cast<uint32_t *>(w.sk_cnt->ptr);
+                g.sk_grid = w.sk_grid;
+                g.sk_tail_first = p.schedule == VX_PREFILL_STREAMK_TAIL_FIRST ? 1u : 0u;
+            }
             VX_CHECK(launch_gemm(s, g));
         }
         {

@@ -348,6 +348,17 @@ struct GemmArgs {
     // [T][ldo]) with plain stores instead of atomic adds; the consumer sums them.
     uint32_t split_store = 0;
     uint32_t wide = 0;              // set by launch_gemm: plain-store epilogues may use 16-byte stores
+    // GEPI_SWIGLU on the prefill-layout kernel with tiled plane output: with
+    // sk_grid set (a multiple of 8, normally the CU count) and a little more than
+    // sk_grid tiles, the tiles' blocks are cut into sk_grid equal ranges, one
+    // workgroup each (stream-K). sk_ws holds 2 * sk_grid tile parts of
+    // kSkTileFloats floats, sk_cnt sk_grid counters, zero before a launch and
+    // zero again after it.
+    float *sk_ws = nullptr;
+    uint32_t *sk_cnt = nullptr;
+    uint32_t sk_grid = 0;
+    uint32_t sk_per = 0;            // blocks per workgroup, set by launch_gemm
+    uint32_t sk_tail_first = 0;     // 1: each workgroup computes its tile tail before its head
     // 1: the short-batch F16 kernel's operand layout: the weights (seg[i].w) and
     // the X planes are in the fragment layout (frag16_index), and GEPI_SWIGLU
     // writes oh/ol in it (width seg[0].rows).
@@ -467,9 +478,12 @@ struct StackWork {                  // activations of one chunk of rows (cap row
     vx_buf *h = nullptr;            // residual stream [cap][nH] f32: the input rows, then the output
     vx_buf *xh = nullptr, *xl = nullptr, *ah = nullptr, *al = nullptr, *qh = nullptr, *ql = nullptr;
     vx_buf *q = nullptr, *k = nullptr, *v = nullptr, *ws = nullptr;
+    vx_buf *sk_ws = nullptr, *sk_cnt = nullptr;   // stream-K SwiGLU tile parts and counters
+    uint32_t sk_grid = 0;                         // its workgroups: the CU count rounded down to 8
 };
 constexpr uint32_t kPrefillChunk = 512;     // rows per chunk
 constexpr uint32_t kPrefillMaxSplit = 8;    // split-K factor bound
+constexpr uint32_t kSkTileFloats = 128u * 128u;   // accumulators of one 128 x 128 prefill GEMM tile
 struct PrefillStack {
     vx_ctx *ctx = nullptr;
     uint32_t nH = 0, nF = 0, nKV = 0, q_heads = 0, kv_heads = 0, head_dim = 0, context = 0, n_layers = 0;
@@ -481,6 +495,7 @@ struct PrefillStack {
     float theta = 10000.f, rope_scaling = 1.f;
     __half *kc = nullptr, *vc = nullptr;       // f16 caches [layer][context][nKV]
     const StackWork *work = nullptr;
+    uint32_t schedule = VX_PREFILL_AUTO;       // gate/up GEMM schedule (VX_PREFILL_*)
 };
 int prefill_stack_check(const PrefillStack &p);
 int prefill_stack_alloc(vx_ctx *ctx, uint32_t cap, uint32_t nH, uint32_t nF, uint32_t nKV, StackWork *w);
