@@ -548,7 +548,8 @@ typedef struct vx_baselm_options {
 /* Workgroup schedule of the batched prefill's gate/up projection (no counterpart
  * in the reference, which has no batched MFMA prefill). */
 #define VX_PREFILL_AUTO 0u       /* stream-K when the tiles just exceed the CUs,
-                                    else one tile per workgroup                  */
+                                    whole and half-K tiles side by side up to 1.5
+                                    tiles per CU, else one tile per workgroup    */
 #define VX_PREFILL_TILES 1u      /* one tile per workgroup                       */
 #define VX_PREFILL_STREAMK_TAIL_FIRST 2u /* stream-K with each workgroup's tile
                                     tail computed before its head: the hand-off

@@ -105,6 +105,31 @@ def test_batched_prefill_gate_up_schedules(ctx, small):
     assert err.value.name == "VX_ERR_INVALID_ARG" and "prefill_schedule" in str(err.value)
 
 
+def test_batched_prefill_gate_up_half_tiles(ctx, small):
+    """512 tokens (a full prefill chunk): 4 token tiles x 96 = 384 gate/up tiles, 1.5
+    per 256 CUs, so "auto" runs 256 whole tiles and 128 tiles as two K halves that
+    hand over through the part slots. Against "tiles" (one tile per workgroup; fp32
+    rounding only) and the oracle."""
+    cfg, m, model = small
+    n = 512
+    toks = [int(t) for t in synth.uniform_u32(n, 0x5EED010B, cfg["vocab_size"])]
+    o = oracle_of(m, cfg)
+    for p, t in enumerate(toks):
+        o.decode_token(t, p)
+    got = {}
+    for sched in ("auto", "tiles"):
+        print(f"batched prefill n={n} schedule={sched}", flush=True)
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=False, prefill_schedule=sched)
+        eng.prefill_tokens_batched(toks)
+        got[sched] = (eng.output(), kv_rows(eng, "kv_v", 2, 1024)[:, :n])
+        eng.close()
+        assert rel_l2(got[sched][0], o.norm) < 1e-3, sched
+        for l in range(2):
+            assert rel_l2(f16(got[sched][1][l]), f16(o.kv_v.reshape(2, 1024, 256)[l, :n])) < 1e-3, (sched, l)
+    assert rel_l2(got["auto"][0], got["tiles"][0]) < 1e-4
+    assert rel_l2(f16(got["auto"][1][1]), f16(got["tiles"][1][1])) < 1e-3
+
+
 def test_batched_prefill_continues_a_decode_and_spans_chunks(ctx, small):
     """Prefill at a non-zero position, longer than one 512-token chunk, then decode on."""
     cfg, m, model = small

@@ -607,6 +607,46 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p_sk(GemmArgs a) {
     }
 }
 
+// Gate/up tiles between 1.25 and 1.5 per CU (T = 385..512 for the 6144-row FFN
+// on 256 CUs): the first a.sk_grid tiles run whole, one workgroup each, and every
+// other tile runs as two K halves in two workgroups, which the dispatcher places
+// in the second workgroup slot of the CUs (blocks are dispatched in order), so a
+// CU runs a whole tile and at most one half side by side instead of up to two
+// whole tiles. The halves of a tile (on one XCD) store their parts, count on the
+// tile's counter, and the second to count adds the other part and runs the
+// epilogue, then clears the counter; nothing waits, and the sum commutes.
+__global__ __launch_bounds__(256, 2) void k_gemm_q8p_half(GemmArgs a) {
+    __shared__ uint32_t flag;
+    const uint32_t b = blockIdx.x, G = a.sk_grid, nblk = a.K / 32u;
+    const uint32_t tid = threadIdx.x;
+    uint32_t tile, kb0, nkb, hid = 0;
+    const bool half = b >= G;
+    if (!half) {
+        tile = (b & 7u) * (G >> 3) + (b >> 3);   // XCD-major over the whole tiles
+        kb0 = 0u;
+        nkb = nblk;
+    } else {
+        const uint32_t h = b - G, H = gridDim.x - G;   // H % 16 == 0: a tile's halves on one XCD
+        hid = (h & 7u) * (H >> 3) + (h >> 3);
+        tile = G + (hid >> 1);
+        kb0 = (hid & 1u) ? nblk / 2u : 0u;
+        nkb = (hid & 1u) ? nblk - nblk / 2u : nblk / 2u;
+    }
+    const uint32_t tn = tile / a.ntm, tm = tile - tn * a.ntm;
+    acc16 acc[2][2];
+    tile_blocks<GEPI_SWIGLU>(a, a.seg[0], tn, tm, kb0, nkb, acc);
+    if (half) {
+        uint32_t *const cnt = a.sk_cnt + (hid >> 1);
+        sk_store(a.sk_ws + (size_t)hid * kSkTileFloats, acc);
+        if (tid == 0) flag = atomicAdd(cnt, 1u);
+        __syncthreads();
+        if (flag == 0u) return;   // the other half finishes the tile
+        sk_add(a.sk_ws + (size_t)(hid ^ 1u) * kSkTileFloats, acc);
+        if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    swiglu_planes(a, tn, tm * kBM, acc);
+}
+
 // One thread per 32-byte quant row piece (tile, block b, row n) of the output.
 __global__ __launch_bounds__(256) void k_repack_prefill(const uint8_t *raw, uint32_t off0, uint32_t off1,
                                                         uint32_t rows, uint32_t K, int interleave, uint64_t total,
@@ -707,6 +747,18 @@ int launch_gemm_q8p(hipStream_t s, GemmArgs a) {
         else
             k_gemm_q8p_sk<false><<<a.sk_grid, 256, 0, s>>>(a);
         VX_LAUNCHED("k_gemm_q8p_sk");
+        return VX_OK;
+    }
+    if (a.epi == GEPI_SWIGLU && a.sk_ws && a.sk_cnt && a.sk_grid >= 8u && a.sk_grid % 8u == 0u && a.o_tiled &&
+        a.oh && !a.seg[0].out && tiles_all * 4u > (uint64_t)a.sk_grid * 5u && tiles_all * 2u <= (uint64_t)a.sk_grid * 3u &&
+        (tiles_all - a.sk_grid) % 8u == 0u && nblk >= 2u) {
+        // Whole tiles for the first sk_grid, K halves for the rest: 2 (tiles - sk_grid)
+        // <= sk_grid halves (a multiple of 16, so a tile's halves share an XCD), at
+        // most one per CU beside its whole tile; a part slot per half, a counter per
+        // split tile.
+        const uint32_t halves = 2u * (uint32_t)(tiles_all - a.sk_grid);
+        k_gemm_q8p_half<<<a.sk_grid + halves, 256, 0, s>>>(a);
+        VX_LAUNCHED("k_gemm_q8p_half");
         return VX_OK;
     }
     // 16-byte epilogue stores need every output row start and slab 16-byte aligned.
