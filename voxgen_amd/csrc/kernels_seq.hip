@@ -604,6 +604,16 @@ __global__ __launch_bounds__(256) void k_seq_rope_store(SeqRopeArgs a) {
 // read 64 contiguous bytes of one key row, and the two half-waves' rows (4 keys
 // apart, 4 * (HD + 8) / 2 dwords) start 16 banks apart, so no read conflicts;
 // transposing V in LDS instead took 2-byte stores that collided 16 ways.
+typedef short h4s __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (gfx950): eight bytes per lane from LDS, transposed within
+// each group of 16 lanes as described at its use.
+__device__ __forceinline__ h4s lds_read_tr16(const _Float16 *p) {
+    typedef __attribute__((address_space(3))) h4s lds_h4s;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_h4s *)(__attribute__((address_space(3))) _Float16 *)p);
+}
+
 template <int HD, int QPK>
 __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
     constexpr int TPB = 32 / QPK;
@@ -728,17 +738,29 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
                 pl[kh][i] = (_Float16)(v - (float)hv);
             }
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
+        for (int kh = 0; kh < 2; ++kh) {
+            h8 vf[ND];
 #pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                // Slot i of k-step kh is key 16kh + 8(i/4) + 4hs + i%4.
-                const _Float16 *vr = Vs + (16u * kh + 4u * hs) * KROW + 32u * dt + l32;
-                h8 vf;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) vf[i] = vr[(8 * (i >> 2) + (i & 3)) * KROW];
-                o[dt] = mfma(vf, ph[kh], o[dt]);
-                o[dt] = mfma(vf, pl[kh], o[dt]);
+            for (int dt = 0; dt < ND; ++dt) {
+                // Slot i of k-step kh is key 16kh + 8(i/4) + 4hs + i%4, dimension
+                // 32dt + l32. ds_read_b64_tr_b16 hands lane 16g + 4a + b element j =
+                // column b of the 8-byte row read by lane 16g + a + 4j of its group,
+                // so the lane of the group with (a, j) = (lane % 4, lane / 4 % 4)
+                // reads dims 4a..4a+3 of key 4hs + j (the group's 16 dims start
+                // at 32dt + 16(g % 2), hs = g / 2) and every lane receives keys
+                // +0..3 of its own dimension: slots 0..3, then 4..7 from 8 keys on.
+                const _Float16 *vr = Vs + (16u * kh + 4u * hs + ((lane >> 2) & 3u)) * KROW + 32u * dt +
+                                     16u * ((lane >> 4) & 1u) + 4u * (lane & 3u);
+                const h4s lo4 = lds_read_tr16(vr), hi4 = lds_read_tr16(vr + 8 * KROW);
+                vf[dt] = __builtin_shufflevector(__builtin_bit_cast(h4, lo4), __builtin_bit_cast(h4, hi4), 0, 1, 2, 3,
+                                                 4, 5, 6, 7);
             }
+            // The ND accumulators in turn, so no MFMA waits on the one before it.
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) o[dt] = mfma(vf[dt], ph[kh], o[dt]);
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) o[dt] = mfma(vf[dt], pl[kh], o[dt]);
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
