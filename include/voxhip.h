@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define VX_ABI_VERSION 1
+#define VX_ABI_VERSION 2   /* 2: vx_baselm_options.prefill_schedule */
 
 /* ------------------------------------------------------------------------- */
 /* Status codes. The conditions mirror the reference's anyhow bails.          */

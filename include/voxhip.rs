@@ -31,7 +31,7 @@ pub const VX_ERR_NO_DEVICE: c_int = -13;
 pub const VX_ERR_STATE: c_int = -14;
 
 // Constants (#define).
-pub const VX_ABI_VERSION: u32 = 1;
+pub const VX_ABI_VERSION: u32 = 2;
 pub const VX_DTYPE_F32: u32 = 0;
 pub const VX_DTYPE_F16: u32 = 1;
 pub const VX_DTYPE_Q8_0: u32 = 8;

@@ -96,7 +96,7 @@ def test_rope_scaling_factor_host():
 
 def test_errors_are_codes_not_crashes():
     lib = abi.load()
-    assert lib.vx_abi_version() == 1
+    assert lib.vx_abi_version() == 2
     st = lib.vx_alloc(None, 16, C.byref(abi.BUFP()))
     assert st == abi.STATUS_CODE["VX_ERR_INVALID_ARG"]
     assert b"null" in lib.vx_last_error()
