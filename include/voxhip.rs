@@ -3,9 +3,10 @@
 // The drop-in for VoxGen's Vulkan layer (src/vulkan.rs) on the BaseLM compute
 // path: src/hip.rs of the reference crate can be this file. Every function and
 // struct of voxhip.h appears here in the header's order, with the same parameter
-// types and #[repr(C)] field layout; tests/test_rust_binding.py checks that
-// against the header. Status codes are c_int (VX_OK = 0, negative = error; the
-// message is vx_last_error()). Link with build.rs:
+// types and #[repr(C)] field layout. Generated from the header by
+// `python tests/test_rust_binding.py --write`; do not edit by hand. Status codes
+// are c_int (VX_OK = 0, negative = error; the message is vx_last_error()). Link
+// with build.rs:
 //     println!("cargo:rustc-link-lib=dylib=voxhip");
 //     println!("cargo:rustc-link-search=native=<dir of libvoxhip.so>");
 #![allow(non_camel_case_types, non_upper_case_globals, dead_code)]

@@ -1,5 +1,13 @@
 """The Rust binding include/voxhip.rs against the C header include/voxhip.h.
 
+The binding is generated from the header by render_rust() below; after a header
+change, regenerate it with
+
+    python tests/test_rust_binding.py --write
+
+and test_binding_is_the_rendered_header checks that the committed file is that
+output.
+
 The reference engine is Rust (src/baselm.rs, src/local.rs, src/acoustic.rs call
 the Vulkan layer in src/vulkan.rs); a maintainer swaps that layer for these
 extern "C" declarations. No Rust toolchain exists here, so the binding is checked
@@ -11,6 +19,7 @@ lengths, and the status codes and #define constants carry the header's values.
 from __future__ import annotations
 
 import re
+import sys
 from pathlib import Path
 
 import pytest
@@ -191,3 +200,100 @@ def test_status_codes_and_constants_carry_the_header_values(both):
             continue
         assert k in consts, k
         assert rust_value(consts[k][1]) == c_value(v, defines), k
+
+
+# ------------------------------------------------------------ the generator
+RUST_KEYWORDS = {
+    "type", "ref", "in", "match", "move", "fn", "loop", "use", "mod", "impl", "self", "box", "where", "async",
+    "await", "dyn", "final", "override", "priv", "pub", "static", "struct", "trait", "true", "false", "unsafe",
+    "virtual", "yield", "crate", "super", "const", "enum", "extern", "let", "mut", "return", "while", "for", "if",
+    "else", "break", "continue", "as", "macro", "abstract", "become", "do", "typeof", "unsized", "try",
+}
+
+RUST_PREAMBLE = """// voxhip.rs: Rust declarations of the C ABI in voxhip.h (libvoxhip.so).
+//
+// The drop-in for VoxGen's Vulkan layer (src/vulkan.rs) on the BaseLM compute
+// path: src/hip.rs of the reference crate can be this file. Every function and
+// struct of voxhip.h appears here in the header's order, with the same parameter
+// types and #[repr(C)] field layout. Generated from the header by
+// `python tests/test_rust_binding.py --write`; do not edit by hand. Status codes
+// are c_int (VX_OK = 0, negative = error; the message is vx_last_error()). Link
+// with build.rs:
+//     println!("cargo:rustc-link-lib=dylib=voxhip");
+//     println!("cargo:rustc-link-search=native=<dir of libvoxhip.so>");
+#![allow(non_camel_case_types, non_upper_case_globals, dead_code)]
+
+use std::os::raw::{c_char, c_int, c_void};
+"""
+
+
+def _rid(n: str) -> str:
+    return f"r#{n}" if n in RUST_KEYWORDS else n
+
+
+def render_rust(text: str) -> str:
+    """include/voxhip.rs for the header text: status codes, #define constants,
+    opaque handles, then structs and functions in the header's order."""
+    funcs, structs, enums, enum_values, opaque, defines = parse_header(text)
+    s = _strip(text)
+    items = []
+    for m in re.finditer(r"typedef\s+struct\s+\w+\s*\{.*?\}\s*(\w+)\s*;", s, flags=re.S):
+        items.append((m.start(), m.group(1)))
+    for m in re.finditer(r"typedef\s+struct\s+(\w+)\s+\1\s*;", s):
+        items.append((m.start(), m.group(1)))
+    body = re.sub(r"typedef\s+(?:struct|enum)\s+\w+\s*\{.*?\}\s*\w+\s*;", lambda m: " " * len(m.group(0)), s,
+                  flags=re.S)
+    for m in re.finditer(r"\b(vx_\w+)\s*\(", body):
+        items.append((m.start(), m.group(1)))
+    order = [n for _, n in sorted(items)]
+    out = [RUST_PREAMBLE, "// Status codes (vx_status).", "pub type VxStatus = c_int;"]
+    out += [f"pub const {k}: c_int = {v};" for k, v in enum_values.items()]
+    out += ["", "// Constants (#define)."]
+    out += [f"pub const {k}: u32 = {c_value(v, defines)};" for k, v in defines.items()]
+    out += ["", "// Opaque handles."]
+    out += [f"#[repr(C)] pub struct {rust_name(n)} {{ _p: [u8; 0] }}" for n in order if n in opaque]
+    out.append("")
+    emitted, pending = set(), []
+
+    def flush():
+        if pending:
+            out.extend(['#[link(name = "voxhip")]', 'extern "C" {', *pending, "}", ""])
+            pending.clear()
+
+    for n in order:
+        if n in structs and n not in emitted:
+            flush()
+            emitted.add(n)
+            out += ["#[repr(C)]", "#[derive(Clone, Copy)]", f"pub struct {rust_name(n)} {{"]
+            for (fname, base, const, ptr, arr) in structs[n]:
+                ty = rust_type(base, const, ptr, enums)
+                if arr is not None:
+                    ty = f"[{ty}; {c_value(arr, defines) if not arr.isdigit() else int(arr)}]"
+                out.append(f"    pub {_rid(fname)}: {ty},")
+            out += ["}", ""]
+        elif n in funcs and n not in emitted:
+            emitted.add(n)
+            ret_base, ret_const, ret_ptr, params = funcs[n]
+            ps = [f"{_rid(pname)}: {rust_type(base, const, ptr, enums)}" for (pname, base, const, ptr, _) in params]
+            ret = "" if (ret_base == "void" and ret_ptr == 0) else " -> " + rust_type(ret_base, ret_const, ret_ptr,
+                                                                                       enums)
+            line = f"    pub fn {n}({', '.join(ps)}){ret};"
+            if len(line) > 110:
+                line = f"    pub fn {n}(\n        " + ",\n        ".join(ps) + f",\n    ){ret};"
+            pending.append(line)
+    flush()
+    missing = (set(funcs) | set(structs)) - emitted
+    assert not missing, missing
+    return "\n".join(out).rstrip() + "\n"
+
+
+def test_binding_is_the_rendered_header():
+    assert RUST.read_text() == render_rust(HEADER.read_text()), \
+        "include/voxhip.rs is stale: run python tests/test_rust_binding.py --write"
+
+
+if __name__ == "__main__":
+    if sys.argv[1:] != ["--write"]:
+        sys.exit("usage: python tests/test_rust_binding.py --write")
+    RUST.write_text(render_rust(HEADER.read_text()))
+    print(f"wrote {RUST}")
