@@ -182,6 +182,8 @@ def parse():
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--cfm-reps", type=int, default=5, help="CFM solves timed (0 skips the CFM leg)")
     ap.add_argument("--cfm-only", action="store_true", help="run only the LocDiT CFM leg (for profiling)")
+    ap.add_argument("--long-context", type=int, default=1,
+                    help="1: also time decode with --max-context 8192 at positions up to 8000")
     ap.add_argument("--residual-steps", type=int, default=64,
                     help="ResidualLM steps timed (0 skips the ResidualLM leg)")
     ap.add_argument("--residual-only", action="store_true", help="run only the ResidualLM leg (for profiling)")
@@ -406,6 +408,46 @@ def residual_step_bytes(pos):
     fusion = 2 * (Hr * 2 * Hr + Hr)
     layer = 2 * (Hr * (Hr + 2 * KVr) + Hr * Hr + 3 * Fr * Hr) + 2 * Hr * 4 + 2 * (pos + 1) * KVr * 2
     return fsq + fusion + Lr * layer + Hr * 4
+
+
+LONG_POSITIONS = (512, 1024, 2048, 4096, 8000)
+
+
+def long_context_leg(ctx, model, cfg, steps=16, reps=4):
+    """Decode with --max-context 8192 (the reference default, main.rs:97-99) at
+    positions up to 8000: tok/s over `steps` graph steps from each position, and
+    the per-layer cost of the attention (partials, plus the combine on the wide
+    path) and of attn_out there, in graph chains with HBM-resident weights. The
+    engine's own choice (the wide attention from 1024 keys on) is timed next to the
+    folded path alone (attn_splits = 8), which it replaces there. The cache holds
+    zeros: timing does not depend on its values."""
+    from voxgen_amd.baselm import BaseLmEngine
+    lcfg = dict(cfg, active_context_length=8192)
+    toks = synth_tokens(steps, cfg)
+    out = {}
+    for label, splits in (("engine", 0), ("folded_8_splits", 8)):
+        eng = BaseLmEngine(ctx, model, lcfg, exec_mode="graph", strict_geometry=True, attn_splits=splits)
+        res = {}
+        for p in LONG_POSITIONS:
+            eng.set_position(p)
+            eng.decode_tokens_gpu_only(toks)   # warm (captures the graph of this path)
+            ctx.sync()
+            eng.set_position(p)
+            t0 = time.perf_counter()
+            eng.decode_tokens_gpu_only(toks)
+            ctx.sync()
+            el = time.perf_counter() - t0
+            # The kernels are timed at the device position the steps left: p + steps.
+            att = eng.time_layer_kernel("attention", reps) * 1e3
+            ao = eng.time_layer_kernel("attn_out", reps) * 1e3
+            keys = p + steps + 1
+            res[str(p)] = {"tok_s": round(steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+                           "attention_us": round(att, 3), "attn_out_us": round(ao, 3), "keys_timed": keys}
+            log(f"context 8192 ({label}), position {p}: {steps / el:.1f} tok/s; attention {att:.2f} us, "
+                f"attn_out {ao:.2f} us per layer at {keys} keys")
+        eng.close()
+        out[label] = res
+    return out
 
 
 def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384, cpu_steps=0):
@@ -715,6 +757,7 @@ def main():
                "tok_s": round(lb["tokens_per_second"], 1), "positions": "4..35"}
     log(f"reference-semantics decode (LM head, sync per token): {lb['mean_ms']:.3f} ms -> "
         f"{lb['tokens_per_second']:.1f} tok/s")
+    long_ctx = long_context_leg(ctx, model, cfg) if args.long_context else None
     prefill = None
     if args.prefill_tokens:
         prefill = prefill_leg(ctx, eng, cfg, args.prefill_tokens, args.prefill_reps)
@@ -756,6 +799,7 @@ def main():
                  "frac": round(mean_step_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4)},
         "per_kernel": per_kernel,
         "cpu_baseline": cpu,
+        "long_context": long_ctx,
         "prefill": prefill,
         "cfm": cfm,
         "residual": residual,

@@ -242,6 +242,15 @@ int vx_copy(vx_ctx *ctx, vx_buf *dst, uint64_t dst_offset, const vx_buf *src,
 int vx_fill_u32(vx_ctx *ctx, vx_buf *dst, uint64_t dst_offset, uint32_t value, uint64_t count);
 /* submit_and_wait (vulkan.rs:637-657): block until the stream drains. */
 int vx_sync(vx_ctx *ctx);
+/* Cancellation (the AtomicBool of Runtime::synthesize_cancelable,
+ * runtime.rs:745-808). The caller registers a word it may set from any thread
+ * (null unregisters it). Every step-level entry point of the engines on this
+ * context reads it before enqueuing a step (BaseLM decode, each token of a
+ * multi-token call, each chunk of a batched prefill, a ResidualLM step or
+ * prefix, a LocDiT estimate or CFM solve, an AudioVAE decode) and, while it is
+ * nonzero, returns VX_ERR_CANCELLED ("speech synthesis cancelled") with that
+ * step not enqueued. Work already enqueued runs to completion. */
+int vx_set_cancel_flag(vx_ctx *ctx, const uint32_t *flag);
 
 /* Graph capture of enqueued work (replaces recording one command buffer). */
 int vx_graph_begin(vx_ctx *ctx);

@@ -422,6 +422,7 @@ extern "C" {
     ) -> c_int;
     pub fn vx_fill_u32(ctx: *mut VxCtx, dst: *mut VxBuf, dst_offset: u64, value: u32, count: u64) -> c_int;
     pub fn vx_sync(ctx: *mut VxCtx) -> c_int;
+    pub fn vx_set_cancel_flag(ctx: *mut VxCtx, flag: *const u32) -> c_int;
     pub fn vx_graph_begin(ctx: *mut VxCtx) -> c_int;
     pub fn vx_graph_end(ctx: *mut VxCtx, out: *mut *mut VxGraph) -> c_int;
     pub fn vx_graph_launch(ctx: *mut VxCtx, graph: *mut VxGraph) -> c_int;

@@ -97,6 +97,7 @@ def test_rope_scaling_factor_host():
 def test_errors_are_codes_not_crashes():
     lib = abi.load()
     assert lib.vx_abi_version() == 2
+    assert lib.vx_set_cancel_flag(None, None) == abi.STATUS_CODE["VX_ERR_INVALID_ARG"]
     st = lib.vx_alloc(None, 16, C.byref(abi.BUFP()))
     assert st == abi.STATUS_CODE["VX_ERR_INVALID_ARG"]
     assert b"null" in lib.vx_last_error()

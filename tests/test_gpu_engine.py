@@ -287,3 +287,35 @@ def test_gguf_file_through_the_loader_decodes_like_the_oracle(ctx, full_model, t
     finally:
         model.free()
         g.close()
+
+
+def test_cancellation_flag_stops_steps_before_they_are_enqueued(ctx, two_layers):
+    """synthesize_cancelable's flag (runtime.rs:745-808): set before a step, the
+    step fails with VX_ERR_CANCELLED and the engine position does not move; the
+    steps already taken stay, and clearing the flag resumes decoding where it
+    stopped, matching the oracle."""
+    cfg, m, model = two_layers
+    eng = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=False)
+    o = voxref.BaseLm(m.data, {t.name: t for t in m.tensors}, cfg)
+    toks = [int(t) for t in synth.uniform_u32(6, 0x5EED000B, 2048)]
+    try:
+        eng.decode_tokens_gpu_only(toks[:2])
+        for p in range(2):
+            o.decode_token(toks[p], p)
+        ctx.set_cancelled(True)
+        for call in (lambda: eng.decode_token(toks[2]), lambda: eng.decode_token_gpu_only(toks[2]),
+                     lambda: eng.decode_tokens_gpu_only(toks[2:4]), lambda: eng.prefill_tokens(toks[2:4]),
+                     lambda: eng.prefill_tokens_batched(toks[2:4]),
+                     lambda: eng.decode_embedding(synth.normal_f32(2048, 5, 0.0, 0.5))):
+            with pytest.raises(abi.VxError) as e:
+                call()
+            assert e.value.name == "VX_ERR_CANCELLED" and "cancelled" in str(e.value)
+            assert eng.position == 2
+        ctx.set_cancelled(False)
+        for p in (2, 3):
+            r = eng.decode_token(toks[p])
+            assert r.position == p
+            assert rel_l2(eng.output(), o.decode_token(toks[p], p)) < 1e-3, p
+    finally:
+        ctx.set_cancelled(False)
+        eng.close()

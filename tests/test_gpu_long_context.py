@@ -1,0 +1,184 @@
+"""BaseLM decode over the reference's context range and product modes, against the oracle.
+
+* Long contexts: VoxGen runs with --max-context 8192 (main.rs:97-99), which sizes
+  the KV cache (baselm.rs:182-192). The engine's decode attention has three tiers by
+  key count: 8 slices of at most 64 keys (k_attn_chunk) up to 1024 keys, then 8 and
+  from 2561 keys 16 streamed slices of many keys (k_attn_stream); attn_out merges the
+  slices of each. All are checked against the oracle, across both switches and at
+  positions 4096 and 8000 of the 28-layer stack.
+* LongRoPE with context_length > rope_original_context_length: the long factors and
+  a scaling factor != 1 (rope_scaling_factor, baselm.rs:194-205; factor choice,
+  baselm.rs:902-913) on the device.
+* The F16-weight BaseLM (--base-format f16, build_linux/smoke_f16.sh:6; the F16
+  branch of matvec.comp) at the full 28-layer geometry.
+"""
+import numpy as np
+import pytest
+
+import voxref
+from conftest import rel_l2
+from voxgen_amd import synth
+from voxgen_amd.baselm import BaseLmEngine, rope_scaling_factor
+from voxgen_amd.runtime import Model
+
+pytestmark = pytest.mark.gpu
+
+def kv_bits(layers, ctxlen, filled, seed, kv_dim=256):
+    k = synth.kv_cache_fill(layers, ctxlen, kv_dim, filled, seed).view(np.uint16).ravel().copy()
+    v = synth.kv_cache_fill(layers, ctxlen, kv_dim, filled, seed + 1).view(np.uint16).ravel().copy()
+    return k, v
+
+
+def oracle(m, cfg):
+    return voxref.BaseLm(m.data, {t.name: t for t in m.tensors}, cfg)
+
+
+@pytest.mark.parametrize("mode", ["graph", "fused"])
+@pytest.mark.parametrize("active,start", [(2048, 1019), (4096, 2555)])
+def test_decode_across_the_attention_tiers(ctx, mode, active, start):
+    """One layer (so the attention vector is the kernel's output on the layer's
+    own q, not a product of upstream rounding): twelve positions from `start`
+    step from one attention tier into the next (1024 -> 1025 keys: k_attn_chunk
+    to 8 streamed slices; 2560 -> 2561 keys: 8 to 16 streamed slices); every
+    output, the attention vector and the stored K/V rows follow the oracle."""
+    cfg = synth.baselm_config(layers=1, vocab=2048, context_length=32768, active_context=active)
+    # Small Q8_0 scales keep the model's own keys from dominating the softmax (see
+    # long_model below): the test compares kernels, not conditioning.
+    m = synth.build_baselm(cfg, seed=0x5EED0301, q8_scale_sigma=0.002)
+    model = Model(ctx, m.data, m.tensors)
+    kk, vv = kv_bits(1, active, start, 0x5EED0302)
+    o = oracle(m, cfg)
+    o.kv_k[:] = kk
+    o.kv_v[:] = vv
+    eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=False)
+    eng.buffer("kv_k").upload(kk)
+    eng.buffer("kv_v").upload(vv)
+    eng.set_position(start)
+    toks = [int(t) for t in synth.uniform_u32(12, 0x5EED0303, 2048)]
+    for i, t in enumerate(toks):
+        pos = start + i
+        r = eng.decode_token(t)
+        assert r.position == pos
+        want = o.decode_token(t, pos)
+        assert rel_l2(eng.output(), want) < 1e-3, pos
+        assert rel_l2(eng.buffer("attention").download(np.float32, 2048), o.attention) < 1e-3, pos
+    got = eng.buffer("kv_k").download(np.uint16, kk.size).reshape(1, active, 256)
+    ref = o.kv_k.reshape(1, active, 256)
+    assert np.array_equal(got[:, :start], ref[:, :start])
+    assert rel_l2(got[:, start:start + 12].view(np.float16), ref[:, start:start + 12].view(np.float16)) < 1e-3
+    assert np.all(got[:, start + 12:] == 0)
+    eng.close()
+    model.free()
+
+
+@pytest.fixture(scope="module")
+def long_model(ctx):
+    # Q8_0 scales |N(0,1)| * 0.002 instead of 0.01: with 0.01 the synthetic q and k
+    # entries are ~26, the model's own key rows score in the hundreds and two of
+    # them (positions 4096 and 8000) split the softmax, so a 1e-4 rounding
+    # difference in q moves the output by 2e-2 in every implementation alike
+    # (the reference-granular kernels included). Smaller weights keep the test
+    # well conditioned; the kernels are the same.
+    cfg = synth.baselm_config(active_context=8192)
+    m = synth.build_baselm(cfg, seed=0x5EED0304, q8_scale_sigma=0.002)
+    model = Model(ctx, m.data, m.tensors)
+    yield cfg, m, model
+    model.free()
+
+
+def test_full_stack_decode_at_positions_4096_and_8000(ctx, long_model):
+    """28 layers with --max-context 8192: the cache random-filled up to 8000, one
+    decode at 4096 and one at 8000 (16 streamed slices of 501 keys), graph and
+    reference op order, against the oracle's sequential decode."""
+    cfg, m, model = long_model
+    kk, vv = kv_bits(28, 8192, 8000, 0x5EED0305)
+    toks = [int(t) for t in synth.uniform_u32(2, 0x5EED0306, cfg["vocab_size"])]
+    o = oracle(m, cfg)
+    o.kv_k[:] = kk
+    o.kv_v[:] = vv
+    wants = [o.decode_token(toks[0], 4096), o.decode_token(toks[1], 8000)]
+    want_k = o.kv_k.reshape(28, 8192, 256)[:, [4096, 8000]].copy()
+    outs = {}
+    for mode in ("graph", "reference"):
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=True)
+        eng.buffer("kv_k").upload(kk)
+        eng.buffer("kv_v").upload(vv)
+        outs[mode] = []
+        for pos, t, w in zip((4096, 8000), toks, wants):
+            eng.set_position(pos)
+            eng.decode_token_gpu_only(t)
+            outs[mode].append(eng.output())
+            assert rel_l2(outs[mode][-1], w) < 5e-3, (mode, pos)
+        got = eng.buffer("kv_k").download(np.uint16, kk.size).reshape(28, 8192, 256)
+        assert rel_l2(got[:, [4096, 8000]].view(np.float16), want_k.view(np.float16)) < 5e-3, mode
+        assert np.array_equal(got[:, :4096], kk.reshape(28, 8192, 256)[:, :4096]), mode
+        eng.close()
+    # The streamed attention (16 slices) against the reference-granular kernels: same
+    # arithmetic, different reduction order.
+    for a, b in zip(outs["graph"], outs["reference"]):
+        assert rel_l2(a, b) < 1e-3
+
+
+def test_longrope_long_factors_and_scaling(ctx):
+    """context_length 32768 over an original 4096: the engine takes
+    rope_factors_long (non-uniform here) and scales cos/sin by
+    sqrt(1 + ln(8) / ln(4096)); decode from position 0 and at 3000 in the graph,
+    fused and reference modes against the oracle."""
+    cfg = synth.baselm_config(layers=2, vocab=2048, context_length=32768, active_context=4096,
+                              original_context=4096)
+    s = rope_scaling_factor(cfg)
+    assert abs(s - np.sqrt(1.0 + np.log(8.0) / np.log(4096.0))) < 1e-6
+    m = synth.build_baselm(cfg, seed=0x5EED0307)
+    half = cfg["head_dim"] // 2
+    for name, fac in (("rope_factors_long.weight", 1.0 + 7.0 * np.arange(half) / half),
+                      ("rope_factors_short.weight", 1.0 + 0.1 * np.arange(half) / half)):
+        t = next(t for t in m.tensors if t.name == name)
+        m.data[t.offset:t.offset + t.nbytes].view(np.float32)[:] = fac.astype(np.float32)
+    model = Model(ctx, m.data, m.tensors)
+    kk, vv = kv_bits(2, 4096, 3000, 0x5EED0308)
+    toks = [int(t) for t in synth.uniform_u32(4, 0x5EED0309, 2048)]
+    for mode in ("graph", "fused", "reference"):
+        o = oracle(m, cfg)
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=False)
+        for pos, t in enumerate(toks[:3]):
+            eng.decode_token(t)
+            assert rel_l2(eng.output(), o.decode_token(t, pos)) < 1e-3, (mode, pos)
+            assert rel_l2(eng.buffer("q").download(np.float32, 2048), o.q) < 1e-3, (mode, pos)
+        o.kv_k[:] = kk
+        o.kv_v[:] = vv
+        eng.buffer("kv_k").upload(kk)
+        eng.buffer("kv_v").upload(vv)
+        eng.set_position(3000)
+        eng.decode_token(toks[3])
+        assert rel_l2(eng.output(), o.decode_token(toks[3], 3000)) < 1e-3, mode
+        assert rel_l2(eng.buffer("k").download(np.float32, 256), o.k) < 1e-3, mode
+        eng.close()
+    model.free()
+
+
+def test_f16_weights_full_stack(ctx):
+    """The 28-layer BaseLM with F16 projections: three tokens from position 0, then
+    one at 256 over a random-filled cache, graph mode against the oracle."""
+    cfg = synth.baselm_config(active_context=512)
+    m = synth.build_baselm(cfg, seed=0x5EED030A, weight_type="f16")
+    model = Model(ctx, m.data, m.tensors)
+    try:
+        o = oracle(m, cfg)
+        toks = [int(t) for t in synth.uniform_u32(4, 0x5EED030B, cfg["vocab_size"])]
+        eng = BaseLmEngine(ctx, model, cfg, exec_mode="graph", strict_geometry=True)
+        for pos, t in enumerate(toks[:3]):
+            r = eng.decode_token(t, top_k=3)
+            want = o.decode_token(t, pos, logits=True)
+            assert rel_l2(eng.output(), want) < 5e-3, pos
+            assert [i for i, _ in r.top_logits][:2] == list(np.argsort(-o.logits, kind="stable")[:2]), pos
+        kk, vv = kv_bits(28, 512, 256, 0x5EED030C)
+        o.kv_k[:] = kk
+        o.kv_v[:] = vv
+        eng.buffer("kv_k").upload(kk)
+        eng.buffer("kv_v").upload(vv)
+        eng.set_position(256)
+        eng.decode_token_gpu_only(toks[3])
+        assert rel_l2(eng.output(), o.decode_token(toks[3], 256)) < 5e-3
+        eng.close()
+    finally:
+        model.free()

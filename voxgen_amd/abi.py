@@ -209,6 +209,7 @@ PROTOTYPES = {
     "vx_copy": (i32, [CTX, BUFP, u64, BUFP, u64, u64]),
     "vx_fill_u32": (i32, [CTX, BUFP, u64, u32, u64]),
     "vx_sync": (i32, [CTX]),
+    "vx_set_cancel_flag": (i32, [CTX, P(u32)]),
     "vx_graph_begin": (i32, [CTX]),
     "vx_graph_end": (i32, [CTX, P(GRAPH)]),
     "vx_graph_launch": (i32, [CTX, GRAPH]),

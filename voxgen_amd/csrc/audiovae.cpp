@@ -391,6 +391,7 @@ uint64_t vx_audiovae_scratch_bytes(const vx_audiovae *e) {
 
 int vx_audiovae_decode_latents_gpu(vx_audiovae *e, const vx_buf *frame_major, uint32_t frames, vx_buf *wave) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_audiovae_decode_latents_gpu: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     const vx_audiovae_config &c = e->cfg;
     if (frames == 0 || frames % c.patch_size)
         return fail(VX_ERR_SHAPE, "VoxCPM2 AudioVAE decode expects latent frames in groups of %u, got %u",
@@ -406,6 +407,7 @@ int vx_audiovae_decode_latents_gpu(vx_audiovae *e, const vx_buf *frame_major, ui
 int vx_audiovae_decode_latents(vx_audiovae *e, const float *frame_major, uint64_t n_values, float *wave,
                                uint64_t wave_cap, vx_audio_decode_stats *out) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_audiovae_decode_latents: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     const vx_audiovae_config &c = e->cfg;
     const uint64_t ld = c.latent_dim;
     if (!frame_major || n_values == 0 || n_values % ld)

@@ -49,8 +49,13 @@ struct vx_baselm {
     float residual_scale = 1.f, embedding_alpha = 1.f, logit_alpha = 1.f, rope_scaling = 1.f;
     uint32_t splits = 8;
     bool fold_attn_merge = false;  // attention merge folded into the attn_out matvec
+    // Attention tiers by the step's key count (attn_tier): tier 0 is the short
+    // contexts' k_attn_chunk over `splits` slices; tiers 1 and 2 stream
+    // tier_splits[t] slices of many keys through k_attn_stream (0: tier unused).
+    // attn_out merges the slices of every tier.
+    uint32_t tier_splits[3] = {0, 0, 0};
     uint32_t pos = 0;
-    vx_graph *graphs[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+    vx_graph *graphs[2][2][3] = {};   // [embedding input][LM head][attention tier]
     // Token-batched prefill workspace (allocated on first use): residual stream,
     // hi/lo f16 planes of the GEMM inputs, q/k/v, roped q planes, token ids.
     StackWork pf;
@@ -161,12 +166,13 @@ int validate_config(const vx_baselm_config &c, bool strict) {
 int alloc(vx_ctx *ctx, uint64_t bytes, vx_buf **out) { return vx_alloc(ctx, bytes, out); }
 
 void free_all(vx_baselm *e) {
-    for (auto &row : e->graphs)
-        for (auto &g : row)
-            if (g) {
-                vx_graph_free(e->ctx, g);
-                g = nullptr;
-            }
+    for (auto &plane : e->graphs)
+        for (auto &row : plane)
+            for (auto &g : row)
+                if (g) {
+                    vx_graph_free(e->ctx, g);
+                    g = nullptr;
+                }
     vx_buf **bufs[] = {&e->hidden, &e->norm,   &e->q,      &e->k,        &e->v,
                        &e->attention, &e->gate, &e->branch, &e->logits, &e->scores,
                        &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table,
@@ -190,8 +196,25 @@ enum LayerKernel : uint32_t { LK_QKV = 0, LK_ATTENTION = 1, LK_ATTN_OUT = 2, LK_
 const char *const kLayerKernelNames[LK_COUNT] = {"baselm.qkv", "baselm.attention", "baselm.attn_out",
                                                  "baselm.swiglu", "baselm.down"};
 
+// Attention tier of a step over `pos + 1` keys. Up to kTier1FromKeys keys the
+// short contexts' kShortSplits slices of k_attn_chunk (whose keys are fetched
+// before the position is known while a slice holds at most 64 of them); then
+// kShortSplits streamed slices of eight waves; from kTier2FromKeys keys
+// kMaxFoldedSplits streamed slices of four waves. Measured on MI355X per layer,
+// attention + attn_out at 1041 / 2065 / 4113 / 8017 keys: tier 0 11.5 / 15.3 /
+// 23.1 / 36.8 us, tier 1 10.3 / 11.8 / 14.3 / 19.3 us, tier 2 10.9 / 11.9 /
+// 13.6 / 16.1 us.
+constexpr uint32_t kTier1FromKeys = 1025;
+constexpr uint32_t kTier2FromKeys = 2561;
+uint32_t attn_tier(const vx_baselm *e, uint32_t pos) {
+    const uint32_t n = pos + 1u;
+    if (n >= kTier2FromKeys && e->tier_splits[2]) return 2;
+    if (n >= kTier1FromKeys && e->tier_splits[1]) return 1;
+    return 0;
+}
+
 // Enqueue one kernel of layer l (all read the decode position from device memory).
-int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l) {
+int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l, uint32_t tier) {
     hipStream_t s = e->ctx->stream;
     const vx_baselm_config &c = e->cfg;
     const Layer &L = e->layers[l];
@@ -207,7 +230,8 @@ int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l) {
     at.head_dim = c.head_dim;
     at.q_heads = c.head_count;
     at.kv_heads = c.head_count_kv;
-    at.splits = e->splits;
+    at.splits = tier ? e->tier_splits[tier] : e->splits;
+    const bool fold = e->fold_attn_merge;
     switch (which) {
         case LK_QKV: {
             QkvFusedLaunch a;
@@ -237,7 +261,8 @@ int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l) {
         }
         case LK_ATTENTION:
             // Partials only when attn_out merges them; else partials + merge.
-            return e->fold_attn_merge ? launch_attn_partials(s, at) : launch_attn_decode(s, at);
+            if (tier) return launch_attn_stream(s, at);   // tiers 1 and 2 imply the fold
+            return fold ? launch_attn_partials(s, at) : launch_attn_decode(s, at);
         case LK_ATTN_OUT: {
             MatvecLaunch ao;
             ao.w = L.o;
@@ -247,7 +272,7 @@ int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l) {
             ao.epi = EPI_RESIDUAL;
             ao.y = F(e->hidden);
             ao.scale = e->residual_scale;
-            if (!e->fold_attn_merge) return launch_matvec(s, ao);
+            if (!fold) return launch_matvec(s, ao);
             AttnOutLaunch a;
             a.mv = ao;
             a.partials = at.partials;
@@ -302,7 +327,7 @@ int enqueue_logits(vx_baselm *e) {
 }
 
 // The fused decode step, enqueued on the context stream.
-int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
+int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits, uint32_t tier) {
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_baselm_config &c = e->cfg;
@@ -320,7 +345,7 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits) {
     for (uint32_t l = 0; l < c.block_count; ++l)
         for (uint32_t k = 0; k < LK_COUNT; ++k) {
             ProfSpan sp(ctx, kLayerKernelNames[k]);
-            VX_CHECK(enqueue_layer_kernel(e, k, l));
+            VX_CHECK(enqueue_layer_kernel(e, k, l, tier));
         }
     {
         ProfSpan sp(ctx, "baselm.output_norm");
@@ -604,13 +629,15 @@ int enqueue_reference(vx_baselm *e, uint32_t position, bool with_embedding, uint
 int run_step(vx_baselm *e, bool with_embedding, uint32_t token, bool logits) {
     if (e->opt.exec_mode == VX_EXEC_REFERENCE) return enqueue_reference(e, e->pos, with_embedding, token, logits);
     const bool persistent = e->opt.exec_mode == VX_EXEC_PERSISTENT;
+    const uint32_t tier = persistent ? 0u : attn_tier(e, e->pos);
     if (e->ctx->prof_enabled)
-        return persistent ? enqueue_persistent(e, with_embedding, logits) : enqueue_fused(e, with_embedding, logits);
-    if (e->opt.exec_mode == VX_EXEC_FUSED) return enqueue_fused(e, with_embedding, logits);
-    vx_graph *&g = e->graphs[with_embedding ? 1 : 0][logits ? 1 : 0];
+        return persistent ? enqueue_persistent(e, with_embedding, logits) : enqueue_fused(e, with_embedding, logits, tier);
+    if (e->opt.exec_mode == VX_EXEC_FUSED) return enqueue_fused(e, with_embedding, logits, tier);
+    vx_graph *&g = e->graphs[with_embedding ? 1 : 0][logits ? 1 : 0][tier];
     if (!g) {
         VX_CHECK(vx_graph_begin(e->ctx));
-        int st = persistent ? enqueue_persistent(e, with_embedding, logits) : enqueue_fused(e, with_embedding, logits);
+        int st = persistent ? enqueue_persistent(e, with_embedding, logits)
+                            : enqueue_fused(e, with_embedding, logits, tier);
         vx_graph *ng = nullptr;
         int st2 = vx_graph_end(e->ctx, &ng);
         if (st != VX_OK) {
@@ -759,15 +786,20 @@ int enqueue_prefill(vx_baselm *e, const uint32_t *tokens, uint32_t n, float *row
     VX_CHECK(ensure_prefill_weights(e));
     hipStream_t s = e->ctx->stream;
     VX_HIP(hipMemcpyAsync(e->pf_tok->ptr, tokens, (size_t)n * 4u, hipMemcpyHostToDevice, s));
-    for (uint32_t done = 0; done < n;) {
+    uint32_t done = 0;
+    int cancelled = VX_OK;
+    while (done < n) {
+        // A cancellation between chunks keeps the chunks already enqueued (their
+        // K/V rows and position), as a host-side stop between decode steps does.
+        if ((cancelled = check_cancel(e->ctx)) != VX_OK) break;
         const uint32_t T = std::min<uint32_t>(e->pf.cap, n - done);
         VX_CHECK(enqueue_prefill_chunk(e, U(e->pf_tok) + done, e->pos + done, T,
                                        rows ? rows + (size_t)done * e->cfg.embedding_length : nullptr));
         done += T;
     }
-    VX_CHECK(launch_set_step(s, U(e->tokens), U(e->position), e->pos + n, 0, 0));
-    e->pos += n;
-    return VX_OK;
+    VX_CHECK(launch_set_step(s, U(e->tokens), U(e->position), e->pos + done, 0, 0));
+    e->pos += done;
+    return cancelled;
 }
 
 int ensure_context(const vx_baselm *e, uint32_t steps) {  // baselm.rs:882-890
@@ -943,18 +975,25 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
     e->logit_alpha = effective_scale(c.logit_scale);
     e->rope_scaling = vx_baselm_rope_scaling_factor(&c);
     // Context splits of the decode attention: one per 64 positions of the active
-    // context, at most kMaxFoldedSplits so that attn_out can merge them itself.
+    // context, at most kShortSplits (attn_out merges them itself).
     if (o.prefill_schedule > VX_PREFILL_STREAMK_TAIL_FIRST)
         return bail(fail(VX_ERR_INVALID_ARG, "unknown prefill_schedule %u", o.prefill_schedule));
     uint32_t splits = o.attn_splits;
     if (splits == 0)
-        splits = std::min<uint32_t>(kMaxFoldedSplits, std::max<uint32_t>(1u, (c.active_context_length + 63u) / 64u));
+        splits = std::min<uint32_t>(kShortSplits, std::max<uint32_t>(1u, (c.active_context_length + 63u) / 64u));
     if (splits > kMaxAttnSplits)
         return bail(fail(VX_ERR_INVALID_ARG, "attn_splits must be at most %u", kMaxAttnSplits));
     e->splits = splits;
-    e->fold_attn_merge = splits <= kMaxFoldedSplits && c.head_count * c.head_dim == c.embedding_length &&
-                         (c.embedding_length == 1024u || c.embedding_length == 2048u) &&
-                         (c.head_dim == 64u || c.head_dim == 128u);
+    // The streamed attention tiers of long contexts (unless the caller fixed the
+    // split count).
+    const bool foldable = c.head_count * c.head_dim == c.embedding_length &&
+                          (c.embedding_length == 1024u || c.embedding_length == 2048u) &&
+                          (c.head_dim == 64u || c.head_dim == 128u);
+    if (o.attn_splits == 0 && foldable && o.exec_mode != VX_EXEC_REFERENCE && o.exec_mode != VX_EXEC_PERSISTENT) {
+        if (c.active_context_length >= kTier1FromKeys) e->tier_splits[1] = kShortSplits;
+        if (c.active_context_length >= kTier2FromKeys) e->tier_splits[2] = kMaxFoldedSplits;
+    }
+    e->fold_attn_merge = splits <= kMaxFoldedSplits && foldable;
     // Buffers (BaseLmEngine::new, baselm.rs:479-506).
     const uint64_t f = 4;
     const uint64_t cache = vx_baselm_kv_cache_bytes(&c) / 2u;
@@ -966,7 +1005,8 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
         (st = alloc(ctx, (uint64_t)c.head_count * c.active_context_length * f, &e->scores)) ||
         (st = alloc(ctx, cache, &e->kv_k)) || (st = alloc(ctx, cache, &e->kv_v)) ||
         (st = alloc(ctx, 256, &e->position)) || (st = alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->tokens)) ||
-        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, splits), &e->attn_scratch)) ||
+        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, std::max(splits, e->tier_splits[2])),
+                    &e->attn_scratch)) ||
         (st = alloc(ctx, (uint64_t)c.head_dim * 4u, &e->rope_table)))
         return bail(st);
     if (o.exec_mode == VX_EXEC_PERSISTENT && (st = setup_persistent(e))) return bail(st);
@@ -1007,6 +1047,7 @@ int vx_baselm_set_position(vx_baselm *e, uint32_t position) {
 
 int vx_baselm_decode_token(vx_baselm *e, uint32_t token_id, uint32_t top_k, vx_step_result *res, vx_top_logit *top) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_token: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     VX_CHECK(check_token(e, token_id));
     VX_CHECK(ensure_context(e, 1));
     const uint32_t position = e->pos;
@@ -1022,6 +1063,7 @@ int vx_baselm_decode_token(vx_baselm *e, uint32_t token_id, uint32_t top_k, vx_s
 int vx_baselm_decode_embedding(vx_baselm *e, const float *embedding, uint32_t n, uint32_t top_k,
                                vx_step_result *res, vx_top_logit *top) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_embedding: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     VX_CHECK(ensure_context(e, 1));
     VX_CHECK(upload_embedding(e, embedding, n));
     const uint32_t position = e->pos;
@@ -1036,6 +1078,7 @@ int vx_baselm_decode_embedding(vx_baselm *e, const float *embedding, uint32_t n,
 
 int vx_baselm_decode_token_gpu_only(vx_baselm *e, uint32_t token_id, uint32_t *position_out) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_token_gpu_only: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     VX_CHECK(check_token(e, token_id));
     VX_CHECK(ensure_context(e, 1));
     const uint32_t position = e->pos;
@@ -1048,6 +1091,7 @@ int vx_baselm_decode_token_gpu_only(vx_baselm *e, uint32_t token_id, uint32_t *p
 
 int vx_baselm_decode_embedding_gpu_only(vx_baselm *e, const float *embedding, uint32_t n, uint32_t *position_out) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_embedding_gpu_only: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     VX_CHECK(ensure_context(e, 1));
     VX_CHECK(upload_embedding(e, embedding, n));
     const uint32_t position = e->pos;
@@ -1060,6 +1104,7 @@ int vx_baselm_decode_embedding_gpu_only(vx_baselm *e, const float *embedding, ui
 
 int vx_baselm_decode_embedding_from_gpu_only(vx_baselm *e, const vx_buf *source, uint32_t *position_out) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_baselm_decode_embedding_from_gpu_only: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     if (!source || source->bytes < (uint64_t)e->cfg.embedding_length * 4u)  // baselm.rs:799-801
         return fail(VX_ERR_BOUNDS, "GPU embedding source is too small for BaseLM %u-float input",
                     e->cfg.embedding_length);
@@ -1079,10 +1124,12 @@ int vx_baselm_decode_tokens_gpu_only(vx_baselm *e, const uint32_t *tokens, uint3
     if (n == 0) return VX_OK;
     for (uint32_t i = 0; i < n; ++i) VX_CHECK(check_token(e, tokens[i]));
     VX_CHECK(ensure_context(e, n));
+    VX_CHECK(check_cancel(e->ctx));
     VX_HIP(hipMemcpyAsync(U(e->tokens) + e->pos, tokens, (size_t)n * 4u, hipMemcpyHostToDevice, e->ctx->stream));
     VX_HIP(hipStreamSynchronize(e->ctx->stream));
     VX_CHECK(launch_set_step(e->ctx->stream, U(e->tokens), U(e->position), e->pos, 0, 0));
     for (uint32_t i = 0; i < n; ++i) {
+        VX_CHECK(check_cancel(e->ctx));   // each token is a step: earlier ones stay done
         if (e->opt.exec_mode == VX_EXEC_REFERENCE) {
             VX_CHECK(enqueue_reference(e, e->pos, true, tokens[i], false));
         } else {
@@ -1192,7 +1239,7 @@ int vx_baselm_profile_steps(vx_baselm *e, const uint32_t *tokens, uint32_t n, vx
             else if (e->opt.exec_mode == VX_EXEC_PERSISTENT)
                 st = enqueue_persistent(e, true, false);
             else
-                st = enqueue_fused(e, true, false);
+                st = enqueue_fused(e, true, false, attn_tier(e, e->pos));
         }
         if (st == VX_OK) st = vx_sync(ctx);
         if (st == VX_OK && e->opt.exec_mode == VX_EXEC_PERSISTENT) st = collect_persistent_trace(e);
@@ -1228,7 +1275,7 @@ int vx_baselm_time_layer_kernel(vx_baselm *e, uint32_t which, uint32_t reps, dou
         for (uint32_t r = 0; r < reps && s2 == VX_OK; ++r) {
             s2 = vx_diag_stream_read(ctx, ev, 0, kEvict, sink, kEvictBlocks, 4);
             for (uint32_t l = 0; with_kernel && l < e->cfg.block_count && s2 == VX_OK; ++l)
-                s2 = enqueue_layer_kernel(e, which, l);
+                s2 = enqueue_layer_kernel(e, which, l, attn_tier(e, e->pos));
         }
         const int s3 = vx_graph_end(ctx, out);
         return s2 != VX_OK ? s2 : s3;

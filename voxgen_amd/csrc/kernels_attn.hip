@@ -205,16 +205,29 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     if (fixed) {
         tile(t0, kpre, vpre);
     } else {
-        for (uint32_t tb = t0; tb < t1; tb += kTile) {
+        // Slices of several tiles: the next tile's rows are requested before the
+        // current tile is computed, so each tile after the first waits only for
+        // what its predecessor's arithmetic did not cover.
+        auto fetch = [&](uint32_t tb, uint4 *kw, uint4 *vw) {
             const uint32_t key = tb + (uint32_t)j;
             const size_t row = (layer_base + (key < t1 ? key : t0)) * kv_dim + head_off;
-            uint4 kw[R / 8], vw[R / 8];
 #pragma unroll
             for (int i = 0; i < R / 8; ++i) {
                 kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
                 vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
             }
+        };
+        uint4 kw[R / 8], vw[R / 8], kn[R / 8], vn[R / 8];
+        fetch(t0, kw, vw);
+        for (uint32_t tb = t0; tb < t1; tb += kTile) {
+            const bool more = tb + kTile < t1;   // workgroup-uniform
+            if (more) fetch(tb + kTile, kn, vn);
             tile(tb, kw, vw);
+#pragma unroll
+            for (int i = 0; i < R / 8; ++i) {
+                kw[i] = kn[i];
+                vw[i] = vn[i];
+            }
         }
     }
     accs[tid] = acc;
@@ -232,21 +245,209 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     }
 }
 
-// Merge the active slices of one query head: one block per head, one lane per dim.
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a) {
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
-    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
-    float m = -FLT_MAX;
-    for (uint32_t s = 0; s < plan.active; ++s) m = fmaxf(m, part_rec<HD>(a, h, s)[0]);
-    float l = 0.f, v = 0.f;
-    for (uint32_t s = 0; s < plan.active; ++s) {
-        const float *rec = part_rec<HD>(a, h, s);
-        const float w = expf(rec[0] - m);
-        l = fmaf(rec[1], w, l);
-        v = fmaf(rec[4 + d], w, v);
+// k_attn_stream: the same partial records for slices of many keys (long
+// contexts). Each of the NW waves streams its own keys, 16 per step (lane = key
+// j of the step x quarter r of the head dimension, as in k_attn_chunk's score
+// layout), with the K and V rows of the next two steps in flight while a step is
+// computed, and keeps a wave-uniform running max, a per-lane partial sum of p
+// and per-lane partial accumulators p * V[j] over its quarter's dimensions. No
+// LDS or barrier inside the key loop: the 16 key slots of a wave are summed by
+// lane rotations and swaps after it, and the waves meet once in LDS. Wave w
+// takes keys t0 + 16 NW i + 16 w + j.
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
+    constexpr int R = HD / 4;            // dimensions per lane
+    constexpr int NI = R / 8;            // 16-byte loads per K (and V) row and lane
+    constexpr uint32_t STEP = 16u * NW;  // keys per workgroup step
+    __shared__ float osh[NW][HD];        // per-wave accumulators
+    __shared__ float wm[NW], wl[NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane >> 2, r = lane & 3;
+    const uint32_t s = blockIdx.x, h = blockIdx.y;
+    const uint32_t kvh = h / (a.q_heads / a.kv_heads);
+    const uint32_t kv_dim = a.kv_heads * HD;
+    // Element 8k + e of quarter r is dimension 8(r + 4k) + e: each load of a
+    // key's four lanes reads 64 contiguous bytes of its row.
+    float qv[R];
+#pragma unroll
+    for (int i = 0; i < R; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * (r + 4 * (i >> 3)) + (i & 7));
+        qv[i] = v.x;
+        qv[i + 1] = v.y;
+        qv[i + 2] = v.z;
+        qv[i + 3] = v.w;
     }
-    a.out[(size_t)h * HD + d] = v / l;
+    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
+    if (s >= plan.active) return;
+    const uint32_t t0 = s * plan.chunk;
+    const uint32_t t1 = min(plan.n, t0 + plan.chunk);
+    const size_t layer_base = (size_t)a.layer * a.context;
+    const size_t head_off = (size_t)kvh * HD + (size_t)r * 8;
+    const float inv_sqrt = 1.0f / sqrtf((float)HD);
+    auto fetch = [&](uint32_t key, uint4 *kw, uint4 *vw) {
+        const size_t row = (layer_base + (key < t1 ? key : t0)) * kv_dim + head_off;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
+            vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
+        }
+    };
+    float m = -FLT_MAX, lp = 0.f, o[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) o[i] = 0.f;
+    // One step: 16 keys of the wave from the rows in (kw, vw).
+    auto step = [&](uint32_t base, const uint4 *kw, const uint4 *vw) {
+        const bool valid = base + (uint32_t)j < t1;
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t w4[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float2 kf = h2f2(w4[t]);
+                d0 = fmaf(qv[8 * i + 2 * t], kf.x, d0);
+                d1 = fmaf(qv[8 * i + 2 * t + 1], kf.y, d1);
+            }
+        }
+        const float sc = valid ? quad_sum(d0 + d1) * inv_sqrt : -FLT_MAX;
+        const float m_new = fmaxf(m, wave_max_dpp(sc));
+        const float corr = expf(m - m_new);
+        const float p = valid ? expf(sc - m_new) : 0.f;
+        lp = fmaf(lp, corr, r == 0 ? p : 0.f);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t w4[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float2 vf = h2f2(w4[t]);
+                o[8 * i + 2 * t] = fmaf(p, vf.x, o[8 * i + 2 * t] * corr);
+                o[8 * i + 2 * t + 1] = fmaf(p, vf.y, o[8 * i + 2 * t + 1] * corr);
+            }
+        }
+        m = m_new;
+    };
+    // Three steps of rows in flight per wave (a ring of three register sets): a
+    // step's arithmetic is shorter than a round trip to memory.
+    const uint32_t base0 = t0 + 16u * (uint32_t)wave;   // wave-uniform
+    const uint32_t key0 = base0 + (uint32_t)j;
+    uint4 k0[NI], v0[NI], k1[NI], v1[NI], k2[NI], v2[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) k1[i] = v1[i] = k2[i] = v2[i] = make_uint4(0u, 0u, 0u, 0u);
+    fetch(key0, k0, v0);
+    if (base0 + STEP < t1) fetch(key0 + STEP, k1, v1);
+    if (base0 + 2u * STEP < t1) fetch(key0 + 2u * STEP, k2, v2);
+    for (uint32_t b = base0; b < t1; b += 3u * STEP) {
+        step(b, k0, v0);
+        if (b + 3u * STEP < t1) fetch(key0 + (b - base0) + 3u * STEP, k0, v0);
+        if (b + STEP >= t1) break;
+        step(b + STEP, k1, v1);
+        if (b + 4u * STEP < t1) fetch(key0 + (b - base0) + 4u * STEP, k1, v1);
+        if (b + 2u * STEP >= t1) break;
+        step(b + 2u * STEP, k2, v2);
+        if (b + 5u * STEP < t1) fetch(key0 + (b - base0) + 5u * STEP, k2, v2);
+    }
+    // A wave with no key (slice shorter than 16 w + 1) keeps m = -FLT_MAX, lp = 0, o = 0.
+    // Sum over the 16 key slots of each quarter (lanes r + 4j): rotations by 4
+    // and 8 inside each 16-lane row, then swaps of rows.
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        float v = o[i];
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf,
+                                                                   false));   // row_ror:4
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf,
+                                                                   false));   // row_ror:8
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        o[i] = v;
+    }
+    if (j == 0) {
+#pragma unroll
+        for (int i = 0; i < R; i += 8)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) osh[wave][8 * (r + 4 * (i >> 3)) + e] = o[i + e];
+    }
+    const float lw = wave_sum_dpp(lp);
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = lw;
+    }
+    __syncthreads();
+    float mm = wm[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mm = fmaxf(mm, wm[w]);
+    float sw[NW], ll = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        sw[w] = wl[w] > 0.f ? expf(wm[w] - mm) : 0.f;
+        ll = fmaf(wl[w], sw[w], ll);
+    }
+    float *rec = part_rec<HD>(a, h, s);
+    if (tid < HD) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc = fmaf(osh[w][tid], sw[w], acc);
+        rec[4 + tid] = acc;
+    }
+    if (tid == 0) {
+        rec[0] = mm;
+        rec[1] = ll;
+    }
+}
+
+// Merge the active slices of one query head (one block of 512 threads per head).
+// The block is G = 512 / HD groups of HD threads; group g takes slices
+// g, g + G, ... and every lane issues the loads of all its slices' (max, sum)
+// and accumulator before using any, so the merge costs one round trip to memory
+// whatever the slice count. The groups' partial merges meet in LDS.
+constexpr uint32_t kCombineThreads = 512;
+template <int HD>
+__global__ __launch_bounds__(kCombineThreads) void k_attn_combine(AttnArgs a) {
+    constexpr uint32_t G = kCombineThreads / HD;          // slice groups
+    constexpr uint32_t U = kMaxAttnSplits / G;            // slices per group at most
+    __shared__ float gm[G], gl[G];
+    __shared__ float gv[G][HD];
+    const uint32_t h = blockIdx.x, d = threadIdx.x % HD, g = threadIdx.x / HD;
+    const SplitPlan plan = split_plan(a.position, a.context, a.splits);
+    float2 ml[U];
+    float av[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t sl = g + G * u;
+        const float *rec = part_rec<HD>(a, h, sl < plan.active ? sl : 0u);
+        ml[u] = *reinterpret_cast<const float2 *>(rec);
+        av[u] = rec[4 + d];
+    }
+    float m = -FLT_MAX;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+        if (g + G * u < plan.active) m = fmaxf(m, ml[u].x);
+    float l = 0.f, v = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+        const bool on = g + G * u < plan.active;
+        const float w = on ? expf(ml[u].x - m) : 0.f;
+        l = fmaf(ml[u].y, w, l);
+        v = fmaf(av[u], w, v);
+    }
+    if (d == 0) {
+        gm[g] = m;
+        gl[g] = l;
+    }
+    gv[g][d] = v;
+    __syncthreads();
+    if (g == 0) {
+        float mm = gm[0];
+#pragma unroll
+        for (uint32_t i = 1; i < G; ++i) mm = fmaxf(mm, gm[i]);
+        float ll = 0.f, vv = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < G; ++i) {
+            const float w = gl[i] > 0.f ? expf(gm[i] - mm) : 0.f;   // a group with no active slice adds nothing
+            ll = fmaf(gl[i], w, ll);
+            vv = fmaf(gv[i][d], w, vv);
+        }
+        a.out[(size_t)h * HD + d] = vv / ll;
+    }
 }
 
 // ------------------------------------------------ reference-granular kernels
@@ -360,13 +561,30 @@ int launch_attn_partials(hipStream_t s, const AttnLaunch &l) {
     return VX_OK;
 }
 
+int launch_attn_stream(hipStream_t s, const AttnLaunch &l) {
+    VX_CHECK(attn_validate(l));
+    const AttnArgs a = attn_args(l);
+    dim3 grid(l.splits, l.q_heads);
+    // Eight waves per slice when the slices are few (each then holds more keys).
+    const bool eight = l.splits <= kShortSplits;
+    if (l.head_dim == 128) {
+        if (eight) k_attn_stream<128, 8><<<grid, 512, 0, s>>>(a);
+        else k_attn_stream<128, 4><<<grid, 256, 0, s>>>(a);
+    } else {
+        if (eight) k_attn_stream<64, 8><<<grid, 512, 0, s>>>(a);
+        else k_attn_stream<64, 4><<<grid, 256, 0, s>>>(a);
+    }
+    VX_LAUNCHED("k_attn_stream");
+    return VX_OK;
+}
+
 int launch_attn_decode(hipStream_t s, const AttnLaunch &l) {
     VX_CHECK(launch_attn_partials(s, l));
     const AttnArgs a = attn_args(l);
     if (l.head_dim == 128)
-        k_attn_combine<128><<<l.q_heads, 128, 0, s>>>(a);
+        k_attn_combine<128><<<l.q_heads, kCombineThreads, 0, s>>>(a);
     else
-        k_attn_combine<64><<<l.q_heads, 64, 0, s>>>(a);
+        k_attn_combine<64><<<l.q_heads, kCombineThreads, 0, s>>>(a);
     VX_LAUNCHED("k_attn_combine");
     return VX_OK;
 }

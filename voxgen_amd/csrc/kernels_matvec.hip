@@ -138,7 +138,7 @@ struct AttnOutArgs {
     uint32_t context, splits;
 };
 
-template <int WT, int NG, int RPW, int HD, bool BRANCH, int WPB>
+template <int WT, int NG, int RPW, int HD, bool BRANCH, int WPB, int FS>
 __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
     // The first MT threads merge E outputs each (float4 units): every one of the
     // workgroup's threads up to 1024*NG/4 of them.
@@ -154,17 +154,17 @@ __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
     // these loads do not wait for the position and go out ahead of the weights.
     const bool merger = tid < MT;
     const uint32_t o0 = (uint32_t)(E * (merger ? tid : 0)), hh = o0 / HD, d0 = o0 % HD;
-    float2 ml[kMaxFoldedSplits];
-    float4 av[kMaxFoldedSplits][E / 4];
+    float2 ml[FS];
+    float4 av[FS][E / 4];
 #pragma unroll
-    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+    for (uint32_t s = 0; s < FS; ++s) {
         ml[s] = make_float2(0.f, 0.f);
 #pragma unroll
         for (int e = 0; e < E / 4; ++e) av[s][e] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (merger) {  // wave-uniform: MT is a multiple of 64
 #pragma unroll
-        for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+        for (uint32_t s = 0; s < FS; ++s) {
             const float *rec = a.part + ((size_t)hh * a.splits + (s < a.splits ? s : 0u)) * (HD + 4);
             ml[s] = *reinterpret_cast<const float2 *>(rec);
 #pragma unroll
@@ -183,13 +183,13 @@ __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
     // Merge of the partials (k_attn_combine's arithmetic).
     float mx = -3.402823466e+38f;
 #pragma unroll
-    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s)
+    for (uint32_t s = 0; s < FS; ++s)
         if (s < plan.active) mx = fmaxf(mx, ml[s].x);
     float l = 0.f, o[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) o[e] = 0.f;
 #pragma unroll
-    for (uint32_t s = 0; s < kMaxFoldedSplits; ++s) {
+    for (uint32_t s = 0; s < FS; ++s) {
         const bool on = s < plan.active;
         const float w = on ? expf(ml[s].x - mx) : 0.f;
         l = on ? fmaf(ml[s].y, w, l) : l;
@@ -683,13 +683,20 @@ int launch_attn_out(hipStream_t s, const AttnOutLaunch &l) {
     a.splits = l.splits;
     // 2048 columns: 8 waves of one row (256 workgroups for 2048 rows; 16-wave groups,
     // half the merge traffic, measured slower: 4.98 against 4.52 us); 1024: 4 waves of two.
-#define VX_AO(WTV, NGV, HDV, RPWV, WPBV)                                                                   \
+#define VX_AO_FS(WTV, NGV, HDV, RPWV, WPBV, FSV)                                                           \
     do {                                                                                                   \
         const uint32_t grid = (l.mv.rows + (WPBV) * (RPWV) - 1) / ((WPBV) * (RPWV));                      \
         if (l.mv.y2)                                                                                       \
-            k_attn_out<WTV, NGV, RPWV, HDV, true, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                 \
+            k_attn_out<WTV, NGV, RPWV, HDV, true, WPBV, FSV><<<grid, 64 * (WPBV), 0, s>>>(a);            \
         else                                                                                               \
-            k_attn_out<WTV, NGV, RPWV, HDV, false, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                \
+            k_attn_out<WTV, NGV, RPWV, HDV, false, WPBV, FSV><<<grid, 64 * (WPBV), 0, s>>>(a);           \
+    } while (0)
+    // The merge loads every record slot up to FS whatever the position: 8 slots
+    // for the short contexts' splits, 16 for long ones.
+#define VX_AO(WTV, NGV, HDV, RPWV, WPBV)                               \
+    do {                                                               \
+        if (l.splits <= kShortSplits) VX_AO_FS(WTV, NGV, HDV, RPWV, WPBV, 8);   \
+        else VX_AO_FS(WTV, NGV, HDV, RPWV, WPBV, 16);                  \
     } while (0)
 #define VX_AO_WT(WTV)                                                                \
     if (ng == 2u) {                                                                  \
@@ -704,6 +711,7 @@ int launch_attn_out(hipStream_t s, const AttnOutLaunch &l) {
     }
 #undef VX_AO_WT
 #undef VX_AO
+#undef VX_AO_FS
     VX_LAUNCHED("k_attn_out");
     return VX_OK;
 }

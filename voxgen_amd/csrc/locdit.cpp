@@ -931,6 +931,7 @@ int vx_locdit_destroy(vx_locdit *e) {
 int vx_locdit_estimate(vx_locdit *e, const float *x, const float *cond, const float *mu, float t, float dt,
                        float *out) {
     if (!e || !x || !out) return fail(VX_ERR_INVALID_ARG, "vx_locdit_estimate: null argument");
+    VX_CHECK(check_cancel(e->ctx));
     const vx_locdit_config &c = e->cfg;
     const uint64_t n = (uint64_t)c.patch * c.feat_dim;
     if (!std::isfinite(t) || !std::isfinite(dt))  // check_time (local.rs:563)
@@ -1032,6 +1033,7 @@ extern "C" {
 int vx_locdit_cfm_solve(vx_locdit *e, const float *cond, const float *mu, const vx_cfm_options *opt,
                         const float *initial_x, float *out_patch, vx_cfm_result *res) {
     if (!e || !opt || !out_patch) return fail(VX_ERR_INVALID_ARG, "vx_locdit_cfm_solve: null argument");
+    VX_CHECK(check_cancel(e->ctx));
     return solve(e, cond, mu, nullptr, opt, initial_x, out_patch, res);
 }
 
@@ -1040,6 +1042,7 @@ int vx_locdit_cfm_solve_from_model_hiddens(vx_locdit *e, const vx_buf *current_l
                                            float *out_patch, vx_cfm_result *res) {
     if (!e || !opt || !out_patch)
         return fail(VX_ERR_INVALID_ARG, "vx_locdit_cfm_solve_from_model_hiddens: null argument");
+    VX_CHECK(check_cancel(e->ctx));
     if (!e->has_mu_proj)
         return fail(VX_ERR_NOT_FOUND, "required GGUF tensor \"projections.lm_to_dit_proj.weight\" is missing");
     if (e->cfg.n_mu != 2u)

@@ -479,6 +479,7 @@ int run_step(vx_residual *e, bool fsq, const float *base, const float *emb) {
 
 // step_record_submit (acoustic.rs:847-893) after the inputs are in place.
 int submit_step(vx_residual *e, bool fsq, const float *base, const float *emb, vx_residual_step_result *out) {
+    VX_CHECK(check_cancel(e->ctx));
     const uint32_t position = e->pos;
     const double t0 = now_ms();
     VX_CHECK(run_step(e, fsq, base, emb));
@@ -500,6 +501,7 @@ int submit_step(vx_residual *e, bool fsq, const float *base, const float *emb, v
 
 // step_record_submit_gpu_only (acoustic.rs:830-845): waits, reads nothing back.
 int submit_step_gpu_only(vx_residual *e, bool fsq, const float *base, const float *emb, vx_residual_gpu_step *out) {
+    VX_CHECK(check_cancel(e->ctx));
     const uint32_t position = e->pos;
     const double t0 = now_ms();
     VX_CHECK(run_step(e, fsq, base, emb));
@@ -533,6 +535,7 @@ int upload_host(vx_residual *e, vx_buf *dst, const float *src) {
 
 // Stop predictor (acoustic.rs:619-652): Linear(H->H)+b, SiLU, Linear(H->2).
 int predict_stop(vx_residual *e, const float *x, vx_stop_prediction *out) {
+    VX_CHECK(check_cancel(e->ctx));
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_acoustic_config &c = e->cfg;
@@ -645,6 +648,7 @@ extern "C" {
 
 int vx_residual_prefill_text_from_gpu_rows(vx_residual *e, const vx_buf *rows, uint32_t n) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_residual_prefill_text_from_gpu_rows: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     if (!rows || rows->bytes < (uint64_t)n * e->cfg.embedding_length * 4u)
         return fail(VX_ERR_BOUNDS, "BaseLM output rows buffer is too small for %u x %u f32 values", n,
                     e->cfg.embedding_length);
@@ -659,6 +663,7 @@ int vx_residual_prefill_text_from_gpu_rows(vx_residual *e, const vx_buf *rows, u
 
 int vx_prefill_text_cross_engine(vx_baselm *base, vx_residual *e, const uint32_t *tokens, uint32_t n) {
     if (!base || !e) return fail(VX_ERR_INVALID_ARG, "vx_prefill_text_cross_engine: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     if (baselm_context(base) != e->ctx)
         return fail(VX_ERR_INVALID_ARG, "the BaseLM and ResidualLM engines must share one context");
     if (baselm_hidden_size(base) != e->cfg.embedding_length)
@@ -729,7 +734,7 @@ int vx_residual_create(vx_ctx *ctx, const vx_model *model, const vx_acoustic_con
     }
     // Attention splits as in the BaseLM engine: one per 64 positions of the
     // active context, at most the number attn_out merges itself.
-    e->splits = std::min<uint32_t>(kMaxFoldedSplits, std::max<uint32_t>(1u, (c.active_context_length + 63u) / 64u));
+    e->splits = std::min<uint32_t>(kShortSplits, std::max<uint32_t>(1u, (c.active_context_length + 63u) / 64u));
     e->fold_attn_merge = (Hd == 1024u || Hd == 2048u) && (c.head_dim == 64u || c.head_dim == 128u);
     // Buffers (ResidualFsqEngine::new, acoustic.rs:470-504) plus the device
     // position and the attention partials.
@@ -806,6 +811,7 @@ vx_buf *vx_residual_buffer(vx_residual *e, uint32_t which) {
 
 int vx_residual_fsq_only(vx_residual *e, const float *base_hidden, uint32_t n, vx_fsq_result *out) {
     if (!e) return fail(VX_ERR_INVALID_ARG, "vx_residual_fsq_only: null engine");
+    VX_CHECK(check_cancel(e->ctx));
     VX_CHECK(check_host(e, base_hidden, n, "FSQ input"));
     VX_CHECK(upload_host(e, e->base_input, base_hidden));
     const double t0 = now_ms();

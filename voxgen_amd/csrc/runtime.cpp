@@ -27,6 +27,12 @@ int fail(int code, const char *fmt, ...) {
 
 void clear_error() { g_last_error.clear(); }
 
+int check_cancel(const vx_ctx *ctx) {
+    if (ctx && ctx->cancel && __atomic_load_n(ctx->cancel, __ATOMIC_ACQUIRE) != 0u)
+        return fail(VX_ERR_CANCELLED, "speech synthesis cancelled");  // runtime.rs:746-808
+    return VX_OK;
+}
+
 int need_buf(const vx_buf *b, uint64_t bytes, const char *what) {
     if (!b || !b->ptr) return fail(VX_ERR_INVALID_ARG, "%s: null buffer", what);
     if (b->bytes < bytes)
@@ -240,6 +246,12 @@ int vx_fill_u32(vx_ctx *ctx, vx_buf *dst, uint64_t dst_offset, uint32_t value, u
         return fail(VX_ERR_BOUNDS, "vx_fill_u32: range exceeds buffer");
     if (!count) return VX_OK;
     return launch_fill_u32(ctx->stream, (uint32_t *)((uint8_t *)dst->ptr + dst_offset), value, count);
+}
+
+int vx_set_cancel_flag(vx_ctx *ctx, const uint32_t *flag) {
+    if (!ctx) return fail(VX_ERR_INVALID_ARG, "vx_set_cancel_flag: null context");
+    ctx->cancel = flag;
+    return VX_OK;
 }
 
 int vx_sync(vx_ctx *ctx) {

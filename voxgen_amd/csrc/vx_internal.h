@@ -98,6 +98,7 @@ struct vx_ctx {
     std::vector<std::string> prof_order;
     hipDeviceProp_t props{};
     void *noalloc_scratch = nullptr;  // device address of this GPU's no-allocation scratch
+    const uint32_t *cancel = nullptr; // caller's cancellation word (vx_set_cancel_flag), nullable
 };
 
 struct vx_model {
@@ -148,6 +149,8 @@ int resolve_vector(const vx_model *m, uint32_t offset, uint32_t dtype, uint32_t 
 
 // Buffer validation.
 int need_buf(const vx_buf *b, uint64_t bytes, const char *what);
+// VX_ERR_CANCELLED when the context's cancellation word is set (acquire load).
+int check_cancel(const vx_ctx *ctx);
 
 // ------------------------------------------------------------ launchers
 // Epilogues of the matvec kernel.
@@ -219,7 +222,8 @@ struct AttnLaunch {
 // floats: max, sum, 2 pad words, acc[head_dim].
 uint64_t attn_scratch_bytes(uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads, uint32_t splits);
 constexpr uint32_t kMaxAttnSplits = 64;     // splits of a standalone attention call
-constexpr uint32_t kMaxFoldedSplits = 8;    // splits the attn_out prologue merges
+constexpr uint32_t kMaxFoldedSplits = 16;   // splits the attn_out prologue merges
+constexpr uint32_t kShortSplits = 8;        // splits of a short context (at most 64 keys each at 512)
 constexpr uint32_t kAttnMinChunk = 32;      // fewest keys per active split
 // Split of the context [0, position] into `active` contiguous chunks, identical
 // in every kernel that reads the partials.
@@ -264,6 +268,8 @@ struct AttnOutLaunch {
 int launch_attn_out(hipStream_t s, const AttnOutLaunch &a);
 // Partials only (k_attn_chunk), and partials + per-head merge (k_attn_combine).
 int launch_attn_partials(hipStream_t s, const AttnLaunch &a);
+// The same partials from k_attn_stream, for slices of many keys (long contexts).
+int launch_attn_stream(hipStream_t s, const AttnLaunch &a);
 int launch_attn_decode(hipStream_t s, const AttnLaunch &a);
 
 // Reference-granular kernels.

@@ -162,6 +162,16 @@ class Context:
     def sync(self) -> None:
         abi.call("vx_sync", self.handle)
 
+    def set_cancelled(self, cancelled: bool) -> None:
+        """Set or clear this context's cancellation word (the AtomicBool of
+        synthesize_cancelable, runtime.rs:745-808): while it is set, every engine
+        step on the context fails with VX_ERR_CANCELLED before it is enqueued.
+        The word lives in this object and is registered on first use."""
+        if getattr(self, "_cancel", None) is None:
+            self._cancel = C.c_uint32(0)
+            abi.call("vx_set_cancel_flag", self.handle, C.byref(self._cancel))
+        self._cancel.value = 1 if cancelled else 0
+
     # graphs
     def graph_begin(self) -> None:
         abi.call("vx_graph_begin", self.handle)
