@@ -176,7 +176,7 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=8, help="passes over the 28 layers per kernel timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target length of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference", "persistent"])
+    ap.add_argument("--mode", default="graph", choices=["graph", "fused", "reference"])
     ap.add_argument("--prefill-tokens", type=int, default=384,
                     help="tokens of the token-batched prefill leg (0 skips it)")
     ap.add_argument("--prefill-reps", type=int, default=5)

@@ -542,10 +542,9 @@ uint64_t vx_baselm_kv_cache_bytes(const vx_baselm_config *cfg);
 #define VX_EXEC_GRAPH 0u     /* fused kernels, each step replayed as one hipGraph */
 #define VX_EXEC_FUSED 1u     /* fused kernels launched eagerly                   */
 #define VX_EXEC_REFERENCE 2u /* the reference's 11 per-op dispatches per layer   */
-#define VX_EXEC_PERSISTENT 3u /* every layer in one persistent kernel per step,
-                                 replayed as one hipGraph; needs the VoxCPM2
-                                 layer geometry, Q8_0 weights and one workgroup
-                                 slot per CU (VX_ERR_UNSUPPORTED otherwise)     */
+#define VX_EXEC_PERSISTENT 3u /* reserved: the one-kernel persistent step, measured
+                                 slower than VX_EXEC_GRAPH on MI355X and removed;
+                                 vx_baselm_create refuses it (VX_ERR_UNSUPPORTED) */
 
 typedef struct vx_baselm_options {
     uint32_t exec_mode;          /* VX_EXEC_* */

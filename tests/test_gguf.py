@@ -389,6 +389,23 @@ def test_rank_up_to_8_is_accepted(tmp_path):
     assert g.baselm_config(4096)["block_count"] == 28
 
 
+def test_zero_element_tensor_with_large_upper_dims_is_accepted(tmp_path):
+    """gguf.rs's checked element product is 0 once a dim is 0, so a tensor with a
+    zero dim loads whatever its other dims; folding dims 5..8 of such a tensor
+    into dims[3] must not fail on an overflow the element count never has."""
+    big = 1 << 40
+    extra = synth.TensorDesc("unused.empty", 0, (0, 3, 4, big, big, 7), 0)
+    cfg = synth.baselm_config(context_length=32768)
+    m = synth.build_baselm(cfg, with_data=False)
+    tensors = list(m.tensors) + [extra]
+    size = max(t.offset + t.nbytes for t in tensors)
+    p = gguf.write(tmp_path / "z.gguf", m.metadata, tensors, None, data_bytes=size)
+    g = Gguf(p)
+    t = {x.name: x for x in g.tensors()}["unused.empty"]
+    assert t.dims[:3] == (0, 3, 4) and t.dims[3] == 0 and t.nbytes == 0
+    assert g.baselm_config(4096)["block_count"] == 28
+
+
 @pytest.mark.parametrize("text,ok", [("28", True), ("+28", True), (" 28", False), ("28 ", False),
                                      ("0x1c", False), ("-28", False), ("2.8e1", False), ("", False)])
 def test_string_metadata_parses_like_rust_u32(tmp_path, text, ok):

@@ -1,6 +1,5 @@
 """BaseLM engine parity (graph, fused-eager and reference op order) against the
-oracle. The persistent one-kernel step, slower than the graph mode and kept only
-as an alternative design, is checked against the graph mode on its own.
+oracle.
 
 One decoder layer at context 512 (the single-layer benchmark workload), short
 multi-layer sequences from position 0 through every decode entry point, error
@@ -224,40 +223,13 @@ def test_full_stack_decode_at_position_256(ctx, full_model):
         eng.close()
 
 
-def test_persistent_mode_matches_graph_over_a_sequence(ctx, two_layers):
-    """Graph and persistent modes through every decode entry point, step for step."""
+def test_persistent_mode_is_refused(ctx, two_layers):
+    """The one-kernel persistent step is not built (its in-kernel phase hand-offs
+    cost more than kernel boundaries on MI355X): the mode is a clear error."""
     cfg, m, model = two_layers
-    toks = [int(t) for t in synth.uniform_u32(10, 0x5EED0009, 2048)]
-    outs = {}
-    for mode in ("graph", "persistent"):
-        eng = BaseLmEngine(ctx, model, cfg, exec_mode=mode, strict_geometry=False)
-        got = []
-        eng.decode_tokens_gpu_only(toks[:5])
-        got.append(eng.output())
-        for t in toks[5:8]:
-            eng.decode_token_gpu_only(t)
-            got.append(eng.output())
-        r = eng.prefill_tokens(toks[8:], top_k_last=4)
-        got.append(eng.output())
-        got.append(eng.buffer("kv_k").download(np.uint16, 2 * 64 * 256).view(np.float16)[: 2 * 64 * 256])
-        outs[mode] = (got, [t for t, _ in r.top_logits])
-        prof = eng.profile_steps([1, 2]) if mode == "persistent" else None
-        if prof is not None:
-            assert prof["baselm.layers"]["calls"] == 2 and "baselm.qkv" not in prof
-        eng.close()
-    for a, b in zip(outs["graph"][0], outs["persistent"][0]):
-        assert rel_l2(b.astype(np.float32), a.astype(np.float32)) < 1e-3
-    assert outs["graph"][1] == outs["persistent"][1]
-
-
-def test_persistent_mode_rejects_other_geometry(ctx):
-    cfg = synth.baselm_config(layers=1, hidden=1024, ffn=3072, vocab=512, q_heads=8, active_context=32)
-    m = synth.build_baselm(cfg, seed=0x5EED000A)
-    model = Model(ctx, m.data, m.tensors)
     with pytest.raises(abi.VxError) as e:
         BaseLmEngine(ctx, model, cfg, exec_mode="persistent", strict_geometry=False)
-    assert e.value.name == "VX_ERR_UNSUPPORTED"
-    model.free()
+    assert e.value.name == "VX_ERR_UNSUPPORTED" and "persistent" in str(e.value)
 
 
 def test_gguf_file_through_the_loader_decodes_like_the_oracle(ctx, full_model, tmp_path):

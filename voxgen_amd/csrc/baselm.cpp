@@ -65,11 +65,6 @@ struct vx_baselm {
     std::vector<StackPrefillWeights> pw;
     vx_buf *pw_arena = nullptr;
     bool pw_tried = false;
-    // Persistent decode step: per-layer weight table, phase counters, sticky
-    // error word, attention partials.
-    vx_buf *ps_layers = nullptr, *ps_cnt = nullptr, *ps_err = nullptr, *ps_part = nullptr;
-    vx_buf *ps_trace = nullptr;   // phase timeline, allocated by the first profiled step
-    uint32_t ps_grid = 0, ps_splits = 0;
 };
 
 namespace {
@@ -176,8 +171,7 @@ void free_all(vx_baselm *e) {
     vx_buf **bufs[] = {&e->hidden, &e->norm,   &e->q,      &e->k,        &e->v,
                        &e->attention, &e->gate, &e->branch, &e->logits, &e->scores,
                        &e->kv_k, &e->kv_v,     &e->position, &e->tokens, &e->attn_scratch, &e->rope_table,
-                       &e->pf_tok, &e->ps_layers, &e->ps_cnt, &e->ps_err, &e->ps_part, &e->ps_trace,
-                       &e->pw_arena};
+                       &e->pf_tok, &e->pw_arena};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -356,177 +350,6 @@ int enqueue_fused(vx_baselm *e, bool with_embedding, bool logits, uint32_t tier)
     return VX_OK;
 }
 
-// The persistent decode step: embedding, RoPE table, counter clear, every layer
-// in k_decode_persistent, output rmsnorm (+ position advance), LM head.
-int enqueue_persistent(vx_baselm *e, bool with_embedding, bool logits) {
-    vx_ctx *ctx = e->ctx;
-    hipStream_t s = ctx->stream;
-    const vx_baselm_config &c = e->cfg;
-    if (with_embedding) {
-        ProfSpan sp(ctx, "baselm.embedding");
-        VX_CHECK(launch_embedding(s, e->model->raw, e->embd_offset, e->embd_dtype, c.embedding_length, 0,
-                                  U(e->tokens), U(e->position), c.vocab_size, e->embedding_alpha, F(e->hidden),
-                                  c.active_context_length));
-    }
-    {
-        ProfSpan sp(ctx, "baselm.rope_table");
-        VX_CHECK(launch_rope_table(s, e->rope_factors, U(e->position), c.head_dim, c.rope_theta, e->rope_scaling,
-                                   reinterpret_cast<float2 *>(e->rope_table->ptr)));
-    }
-    const uint64_t words = persist_counter_words(c.block_count, c.head_count);
-    {
-        ProfSpan sp(ctx, "baselm.persist_clear");
-        VX_CHECK(launch_fill_u32(s, U(e->ps_cnt), 0u, words));
-    }
-    {
-        ProfSpan sp(ctx, "baselm.layers");
-        PersistArgs a;
-        a.layers = static_cast<const PLayer *>(e->ps_layers->ptr);
-        a.n_layers = c.block_count;
-        a.H = c.embedding_length;
-        a.F = c.feed_forward_length;
-        a.KV = c.kv_dim;
-        a.q_heads = c.head_count;
-        a.kv_heads = c.head_count_kv;
-        a.context = c.active_context_length;
-        a.splits = e->ps_splits;
-        a.eps = c.rms_epsilon;
-        a.scale = e->residual_scale;
-        a.h = F(e->hidden);
-        a.q = F(e->q);
-        a.k = F(e->k);
-        a.v = F(e->v);
-        a.att = F(e->attention);
-        a.act = F(e->gate);
-        a.part = F(e->ps_part);
-        a.kc = H(e->kv_k);
-        a.vc = H(e->kv_v);
-        a.position = U(e->position);
-        a.rope_cs = reinterpret_cast<const float2 *>(e->rope_table->ptr);
-        a.cnt = U(e->ps_cnt);
-        a.head_cnt = U(e->ps_cnt) + (uint64_t)c.block_count * kPersistPhases * kPersistCntStride;
-        a.err = U(e->ps_err);
-        if (ctx->prof_enabled && !ctx->capturing) {
-            const uint64_t bytes = (uint64_t)kPersistGroups * e->ps_grid * c.block_count * kPersistPhases * 4u * 8u;
-            if (!e->ps_trace) VX_CHECK(alloc(ctx, bytes, &e->ps_trace));
-            a.trace = static_cast<unsigned long long *>(e->ps_trace->ptr);
-        }
-        VX_CHECK(launch_decode_persistent(s, a, e->ps_grid));
-    }
-    {
-        ProfSpan sp(ctx, "baselm.output_norm");
-        VX_CHECK(launch_rmsnorm(s, F(e->hidden), F(e->norm), e->output_norm, c.embedding_length, c.rms_epsilon,
-                                U(e->position)));
-    }
-    if (logits) VX_CHECK(enqueue_logits(e));
-    return VX_OK;
-}
-
-// Profile entries of one persistent step from its phase timeline (after a sync):
-// per phase, the mean over the workgroups that ran it of the wait and of the work
-// after it, and
-// the whole kernel from the first phase start to the last completion.
-int collect_persistent_trace(vx_baselm *e) {
-    if (!e->ps_trace) return VX_OK;
-    vx_ctx *ctx = e->ctx;
-    const uint32_t G = e->ps_grid, P = e->cfg.block_count * kPersistPhases;
-    std::vector<unsigned long long> t((size_t)kPersistGroups * G * P * 4u);
-    VX_CHECK(vx_download(ctx, e->ps_trace, 0, t.data(), t.size() * 8u));
-    int khz = 0;
-    VX_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device));
-    const double ms_per_tick = khz > 0 ? 1.0 / (double)khz : 1e-5;
-    auto add = [&](const std::string &name, double ms) {
-        auto it = ctx->prof_totals.find(name);
-        if (it == ctx->prof_totals.end()) {
-            ctx->prof_order.push_back(name);
-            it = ctx->prof_totals.emplace(name, ProfTotal{}).first;
-        }
-        it->second.total_ms += ms;
-        it->second.calls += 1;
-    };
-    static const char *const phase[kPersistPhases] = {"qkv", "attention", "attn_out", "swiglu", "down"};
-    unsigned long long first = ~0ull, last = 0;
-    for (uint32_t p = 0; p < P; ++p) {
-        double wait = 0.0, work = 0.0;
-        const uint32_t g0 = (p % kPersistGroups) * G;   // the group that ran phase p
-        for (uint32_t g = g0; g < g0 + G; ++g) {
-            const unsigned long long *r = &t[((size_t)g * P + p) * 4u];
-            wait += (double)(long long)(r[1] - r[0]);
-            work += (double)(long long)(r[2] - r[1]);
-            first = std::min(first, r[0]);
-            last = std::max(last, r[2]);
-        }
-        const std::string base = std::string("persist.") + phase[p % kPersistPhases];
-        add(base + ".wait", wait / G * ms_per_tick);
-        add(base + ".work", work / G * ms_per_tick);
-    }
-    add("persist.kernel", (double)(long long)(last - first) * ms_per_tick);
-    return VX_OK;
-}
-
-// A phase wait of the persistent step that ran out of spins leaves the sticky
-// error word set: report it (and clear it) at the next host synchronisation.
-int check_persistent(vx_baselm *e) {
-    if (e->opt.exec_mode != VX_EXEC_PERSISTENT) return VX_OK;
-    uint32_t err = 0;
-    VX_CHECK(vx_download(e->ctx, e->ps_err, 0, &err, 4u));
-    if (err == 0u) return VX_OK;
-    const uint32_t zero = 0u;
-    VX_CHECK(vx_upload(e->ctx, e->ps_err, 0, &zero, 4u));
-    return fail(VX_ERR_HIP, "persistent decode step: a phase wait timed out (workgroups not co-resident?)");
-}
-
-// Device table of the layer weights and the buffers of the persistent step.
-int setup_persistent(vx_baselm *e) {
-    vx_ctx *ctx = e->ctx;
-    const vx_baselm_config &c = e->cfg;
-    const uint32_t cus = ctx->props.multiProcessorCount > 0 ? (uint32_t)ctx->props.multiProcessorCount : 0u;
-    if (!persistent_supported(c.embedding_length, c.feed_forward_length, c.kv_dim, c.head_count, c.head_dim, cus))
-        return fail(VX_ERR_UNSUPPORTED,
-                    "persistent decode step needs H=2048, F=6144, head_dim 128 and 256 CUs (H=%u F=%u hd=%u CUs=%u)",
-                    c.embedding_length, c.feed_forward_length, c.head_dim, cus);
-    int per_cu = 0;
-    VX_CHECK(persistent_occupancy(&per_cu));
-    if (per_cu < (int)kPersistGroups)
-        return fail(VX_ERR_UNSUPPORTED, "persistent decode kernel: %d workgroups fit on a CU, %u needed", per_cu,
-                    kPersistGroups);
-    std::vector<PLayer> table(c.block_count);
-    for (uint32_t l = 0; l < c.block_count; ++l) {
-        const Layer &L = e->layers[l];
-        const WRef *m[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
-        for (const WRef *w : m)
-            if (w->wt != WT_Q8 || !w->ptr || !w->d)
-                return fail(VX_ERR_UNSUPPORTED, "persistent decode step needs repacked Q8_0 matrices (layer %u)", l);
-        PLayer &p = table[l];
-        p.q = L.q.ptr;
-        p.k = L.k.ptr;
-        p.v = L.v.ptr;
-        p.o = L.o.ptr;
-        p.g = L.gate.ptr;
-        p.u = L.up.ptr;
-        p.dn = L.down.ptr;
-        p.qd = L.q.d;
-        p.kd = L.k.d;
-        p.vd = L.v.d;
-        p.od = L.o.d;
-        p.gd = L.gate.d;
-        p.ud = L.up.d;
-        p.dnd = L.down.d;
-        p.attn_norm = L.attn_norm;
-        p.ffn_norm = L.ffn_norm;
-    }
-    e->ps_grid = cus;
-    e->ps_splits = std::min<uint32_t>(16u, std::max<uint32_t>(1u, cus / c.head_count));
-    VX_CHECK(alloc(ctx, table.size() * sizeof(PLayer), &e->ps_layers));
-    VX_CHECK(alloc(ctx, persist_counter_words(c.block_count, c.head_count) * 4u, &e->ps_cnt));
-    VX_CHECK(alloc(ctx, 256, &e->ps_err));
-    VX_CHECK(alloc(ctx, (uint64_t)c.head_count * e->ps_splits * (c.head_dim + 4u) * 4u, &e->ps_part));
-    VX_CHECK(vx_upload(ctx, e->ps_layers, 0, table.data(), table.size() * sizeof(PLayer)));
-    VX_HIP(hipMemsetAsync(e->ps_err->ptr, 0, e->ps_err->bytes, ctx->stream));
-    VX_HIP(hipMemsetAsync(e->ps_part->ptr, 0, e->ps_part->bytes, ctx->stream));
-    return VX_OK;
-}
-
 // The reference's dispatch sequence (record_transformer) with a host position.
 int enqueue_reference(vx_baselm *e, uint32_t position, bool with_embedding, uint32_t token, bool logits) {
     vx_ctx *ctx = e->ctx;
@@ -628,16 +451,13 @@ int enqueue_reference(vx_baselm *e, uint32_t position, bool with_embedding, uint
 // One step at host position e->pos. The device position buffer already holds it.
 int run_step(vx_baselm *e, bool with_embedding, uint32_t token, bool logits) {
     if (e->opt.exec_mode == VX_EXEC_REFERENCE) return enqueue_reference(e, e->pos, with_embedding, token, logits);
-    const bool persistent = e->opt.exec_mode == VX_EXEC_PERSISTENT;
-    const uint32_t tier = persistent ? 0u : attn_tier(e, e->pos);
-    if (e->ctx->prof_enabled)
-        return persistent ? enqueue_persistent(e, with_embedding, logits) : enqueue_fused(e, with_embedding, logits, tier);
+    const uint32_t tier = attn_tier(e, e->pos);
+    if (e->ctx->prof_enabled) return enqueue_fused(e, with_embedding, logits, tier);
     if (e->opt.exec_mode == VX_EXEC_FUSED) return enqueue_fused(e, with_embedding, logits, tier);
     vx_graph *&g = e->graphs[with_embedding ? 1 : 0][logits ? 1 : 0][tier];
     if (!g) {
         VX_CHECK(vx_graph_begin(e->ctx));
-        int st = persistent ? enqueue_persistent(e, with_embedding, logits)
-                            : enqueue_fused(e, with_embedding, logits, tier);
+        int st = enqueue_fused(e, with_embedding, logits, tier);
         vx_graph *ng = nullptr;
         int st2 = vx_graph_end(e->ctx, &ng);
         if (st != VX_OK) {
@@ -822,7 +642,6 @@ double now_ms() {
 // collect_result (baselm.rs:1204-1231).
 int collect_result(vx_baselm *e, uint32_t position, double elapsed_ms, uint32_t top_k, vx_step_result *res,
                    vx_top_logit *top) {
-    VX_CHECK(check_persistent(e));
     const uint32_t n = e->cfg.embedding_length;
     std::vector<float> h(n);
     VX_CHECK(vx_download(e->ctx, e->norm, 0, h.data(), (uint64_t)n * 4u));
@@ -916,6 +735,9 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
     o.strict_geometry = 1;
     if (opt) o = *opt;
     if (o.exec_mode > VX_EXEC_PERSISTENT) return fail(VX_ERR_INVALID_ARG, "unknown exec_mode %u", o.exec_mode);
+    if (o.exec_mode == VX_EXEC_PERSISTENT)
+        return fail(VX_ERR_UNSUPPORTED, "the persistent decode step is not built: its in-kernel phase hand-offs "
+                                        "cost more than kernel boundaries on this GPU; use VX_EXEC_GRAPH");
     VX_CHECK(validate_config(*cfg, o.strict_geometry != 0));
     const vx_baselm_config &c = *cfg;
     vx_baselm *e = new vx_baselm();
@@ -989,7 +811,7 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
     const bool foldable = c.head_count * c.head_dim == c.embedding_length &&
                           (c.embedding_length == 1024u || c.embedding_length == 2048u) &&
                           (c.head_dim == 64u || c.head_dim == 128u);
-    if (o.attn_splits == 0 && foldable && o.exec_mode != VX_EXEC_REFERENCE && o.exec_mode != VX_EXEC_PERSISTENT) {
+    if (o.attn_splits == 0 && foldable && o.exec_mode != VX_EXEC_REFERENCE) {
         if (c.active_context_length >= kTier1FromKeys) e->tier_splits[1] = kShortSplits;
         if (c.active_context_length >= kTier2FromKeys) e->tier_splits[2] = kMaxFoldedSplits;
     }
@@ -1009,7 +831,6 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
                     &e->attn_scratch)) ||
         (st = alloc(ctx, (uint64_t)c.head_dim * 4u, &e->rope_table)))
         return bail(st);
-    if (o.exec_mode == VX_EXEC_PERSISTENT && (st = setup_persistent(e))) return bail(st);
     // Zero state once (outside any graph). Cache contents are otherwise only ever
     // overwritten, as in the reference (reset leaves stale KV, baselm.rs:616-620).
     vx_buf *zero[] = {e->hidden, e->norm, e->kv_k, e->kv_v, e->position, e->tokens, e->attn_scratch, e->logits};
@@ -1236,18 +1057,14 @@ int vx_baselm_profile_steps(vx_baselm *e, const uint32_t *tokens, uint32_t n, vx
         if (st == VX_OK) {
             if (e->opt.exec_mode == VX_EXEC_REFERENCE)
                 st = enqueue_reference(e, e->pos, true, tokens[i], false);
-            else if (e->opt.exec_mode == VX_EXEC_PERSISTENT)
-                st = enqueue_persistent(e, true, false);
             else
                 st = enqueue_fused(e, true, false, attn_tier(e, e->pos));
         }
         if (st == VX_OK) st = vx_sync(ctx);
-        if (st == VX_OK && e->opt.exec_mode == VX_EXEC_PERSISTENT) st = collect_persistent_trace(e);
         e->pos += 1;
     }
     ctx->prof_enabled = was;
     VX_CHECK(st);
-    VX_CHECK(check_persistent(e));
     return vx_prof_snapshot(ctx, out, cap, count);
 }
 

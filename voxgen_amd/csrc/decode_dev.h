@@ -1,6 +1,5 @@
-// Device helpers of the batch-1 matrix-vector kernels, shared by the per-kernel
-// decode step (kernels_matvec.hip) and the persistent decode step
-// (kernels_persist.hip): wave64 row fragments over the lane-interleaved Q8_0
+// Device helpers of the batch-1 matrix-vector kernels of the decode step
+// (kernels_matvec.hip): wave64 row fragments over the lane-interleaved Q8_0
 // repack (or F16 rows), x staged through LDS with an optional fused rmsnorm,
 // fp32 dot products and DPP wave reductions. Everything is inline and lives in
 // an unnamed namespace of the including translation unit.

@@ -375,8 +375,16 @@ int vx_gguf_open(const char *path, vx_gguf **out) {
         t.n_dims = n_dims < 4u ? n_dims : 4u;
         for (uint32_t d = 0; d < t.n_dims; ++d) t.dims[d] = dims[d];
         for (uint32_t d = 4; d < n_dims; ++d) {
-            if (dims[d] && t.dims[3] > UINT64_MAX / dims[d])
+            if (dims[d] && t.dims[3] > UINT64_MAX / dims[d]) {
+                // gguf.rs's checked product is 0 once any dim is 0, so a tensor with
+                // no elements is accepted whatever its other dims: list it with a
+                // folded dim of 0 instead of failing on the fold.
+                if (elements == 0) {
+                    t.dims[3] = 0;
+                    break;
+                }
                 return bail(VX_ERR_GGUF, "element-count overflow for " + name);
+            }
             t.dims[3] *= dims[d];
         }
         std::string err;

@@ -146,6 +146,11 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
             }
         }
     }
+    // Hand-off to the last workgroup: agent-scope relaxed atomic stores, their
+    // acknowledgements awaited, then the counter; the last workgroup reads the rows
+    // with agent-scope relaxed atomic loads (cfg_euler_block<true>). This rests on
+    // gfx942/gfx950 compiling agent-scope atomics past the per-XCD L2 (sc1), not on
+    // the HIP memory model; see the stream-K part hand-off in kernels_gemm.hip.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0);   // every output store acknowledged
     __syncthreads();

@@ -491,6 +491,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8p(GemmArgs a) {
 
 // A tile part in a slot: element (i, j, r) of thread t at float (32i + 16j + r) * 256 + t,
 // so every store or load of a wave covers 256 contiguous bytes.
+//
+// How a part passes between workgroups, and the hardware property it rests on:
+// the part is written with agent-scope relaxed atomic stores, the writer waits for
+// their acknowledgements (s_waitcnt 0) before its counter atomic, and the reader,
+// once it has seen the count, reads the part with agent-scope relaxed atomic loads.
+// The HIP memory model gives relaxed atomics no ordering: a release on the count
+// and an acquire on its read would. This code instead relies on how LLVM compiles
+// agent-scope atomics for gfx942/gfx950 (AMDGPUUsage, "Memory Model GFX942"):
+// loads and stores carry sc1, so they bypass the non-coherent per-XCD L2 and are
+// performed at the device-coherent level, and a store's acknowledgement means it
+// is visible there (checked in this build's ISA: global_store/global_load ... sc1).
+// The release/acquire pair would add an L2 write-back (buffer_wbl2 sc1) and an L2
+// invalidation (buffer_inv sc1); measured on MI355X inside a decode-size kernel
+// the release alone cost about 5 us per hand-off against 1.3 us for this protocol.
+// Keep every access to a part an agent-scope atomic: a plain store or load here
+// would break the hand-off without any error. The bit-exact test of both hand-off
+// orders (VX_PREFILL_STREAMK_TAIL_FIRST) is the guard.
 __device__ __forceinline__ void sk_store(float *slot, const acc16 (&acc)[2][2]) {
     const uint32_t tid = threadIdx.x;
 #pragma unroll

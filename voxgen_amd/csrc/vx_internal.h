@@ -723,40 +723,5 @@ int launch_seq_embedding(hipStream_t s, const uint8_t *raw, uint32_t weight_offs
 int launch_repack_q8(hipStream_t s, const uint8_t *raw_tensor, uint32_t rows, uint32_t cols,
                      int8_t *qs, __half *d);
 
-// ------------------------------------- persistent decode step (kernels_persist.hip)
-// Every layer of one decode step in one launch of kPersistGroups workgroups per CU
-// (groups take phases in turn). Phase completion is counted on 8 per-XCD
-// counters per phase, 128 bytes apart.
-constexpr uint32_t kPersistCntStride = 256;   // uints per phase
-constexpr uint32_t kPersistPhases = 5;        // per layer: qkv, attention, attn_out, swiglu, down
-constexpr uint32_t kPersistGroups = 1;        // workgroup groups (one workgroup per CU each)
-struct PLayer {                               // repacked Q8_0 matrices of one layer
-    const void *q, *k, *v, *o, *g, *u, *dn;
-    const __half *qd, *kd, *vd, *od, *gd, *ud, *dnd;
-    const float *attn_norm, *ffn_norm;
-};
-struct PersistArgs {
-    const PLayer *layers = nullptr;           // device array [n_layers]
-    uint32_t n_layers = 0, H = 0, F = 0, KV = 0, q_heads = 0, kv_heads = 0, context = 0, splits = 0;
-    float eps = 0.f, scale = 1.f;
-    float *h = nullptr;                       // residual stream [H] (in and out)
-    float *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *act = nullptr;
-    float *part = nullptr;                    // [q_heads][splits][head_dim + 4] attention partials
-    __half *kc = nullptr, *vc = nullptr;
-    const uint32_t *position = nullptr;
-    const float2 *rope_cs = nullptr;          // per-step (cos, sin) table
-    unsigned *cnt = nullptr;                  // [n_layers * 5][kPersistCntStride], zero at launch
-    unsigned *head_cnt = nullptr;             // [n_layers][q_heads], zero at launch
-    unsigned *err = nullptr;                  // sticky: nonzero after a wait timed out
-    // Nullable phase timeline for profiling: per workgroup and phase, the 100 MHz
-    // device clock at phase start, after its wait and after its completion count.
-    unsigned long long *trace = nullptr;      // [grid][n_layers * 5][4] (the running group's rows)
-};
-uint64_t persist_counter_words(uint32_t n_layers, uint32_t q_heads);
-// Whether the persistent step is compiled for this geometry with `cus` workgroups
-// per group; the launch grid is kPersistGroups * cus.
-bool persistent_supported(uint32_t H, uint32_t F, uint32_t KV, uint32_t q_heads, uint32_t head_dim, uint32_t cus);
-int launch_decode_persistent(hipStream_t s, const PersistArgs &a, uint32_t cus);
-int persistent_occupancy(int *blocks_per_cu);
 
 }  // namespace vx
