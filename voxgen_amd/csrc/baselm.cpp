@@ -255,7 +255,7 @@ int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l, uint32_t tier
         }
         case LK_ATTENTION:
             // Partials only when attn_out merges them; else partials + merge.
-            if (tier) return launch_attn_stream(s, at);   // tiers 1 and 2 imply the fold
+            if (tier) return launch_attn_stream(s, at, tier == 1 ? 8u : 4u);   // tiers 1 and 2 imply the fold
             return fold ? launch_attn_partials(s, at) : launch_attn_decode(s, at);
         case LK_ATTN_OUT: {
             MatvecLaunch ao;

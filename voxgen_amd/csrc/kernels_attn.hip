@@ -348,7 +348,9 @@ __global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
     }
     // A wave with no key (slice shorter than 16 w + 1) keeps m = -FLT_MAX, lp = 0, o = 0.
     // Sum over the 16 key slots of each quarter (lanes r + 4j): rotations by 4
-    // and 8 inside each 16-lane row, then swaps of rows.
+    // and 8 inside each 16-lane row (DPP), then the rows pairwise by the gfx950
+    // lane swaps (v_permlane16_swap: rows 0 <-> 1 and 2 <-> 3; v_permlane32_swap:
+    // the two halves), whose two results summed are the pair's sum in every lane.
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         float v = o[i];
@@ -356,9 +358,12 @@ __global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
                                                                    false));   // row_ror:4
         v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf,
                                                                    false));   // row_ror:8
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        o[i] = v;
+        const uint32_t u = __builtin_bit_cast(uint32_t, v);
+        const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        v = __builtin_bit_cast(float, (uint32_t)p16[0]) + __builtin_bit_cast(float, (uint32_t)p16[1]);
+        const uint32_t u2 = __builtin_bit_cast(uint32_t, v);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
+        o[i] = __builtin_bit_cast(float, (uint32_t)p32[0]) + __builtin_bit_cast(float, (uint32_t)p32[1]);
     }
     if (j == 0) {
 #pragma unroll
@@ -561,12 +566,12 @@ int launch_attn_partials(hipStream_t s, const AttnLaunch &l) {
     return VX_OK;
 }
 
-int launch_attn_stream(hipStream_t s, const AttnLaunch &l) {
+int launch_attn_stream(hipStream_t s, const AttnLaunch &l, uint32_t waves) {
     VX_CHECK(attn_validate(l));
+    if (waves != 4u && waves != 8u) return fail(VX_ERR_INVALID_ARG, "stream attention runs 4 or 8 waves");
     const AttnArgs a = attn_args(l);
     dim3 grid(l.splits, l.q_heads);
-    // Eight waves per slice when the slices are few (each then holds more keys).
-    const bool eight = l.splits <= kShortSplits;
+    const bool eight = waves == 8u;
     if (l.head_dim == 128) {
         if (eight) k_attn_stream<128, 8><<<grid, 512, 0, s>>>(a);
         else k_attn_stream<128, 4><<<grid, 256, 0, s>>>(a);
