@@ -11,7 +11,9 @@ Prints one JSON line with:
   value        tok/s over the K timed graph replays (inputs resident in HBM)
   roofline     the dominant kernel (the gate/up SwiGLU matvec): algorithmic bytes
                per launch / its average duration, measured with two HIP events on
-               the engine stream around back-to-back launches over all 28 layers
+               the engine stream around back-to-back launches over all 28 layers;
+               roofline.rocprof is the same kernel's average duration in the
+               committed rocprofv3 trace (profiles/kernels_decode28_q8.json)
   per_kernel   the same measurement for every kernel of the decode layer
   c0           the single Q8_0 2048x2048 matvec (matvec.comp) over 64 distinct
                copies (285 MB, beyond the 256 MB MALL) and hot in cache
@@ -33,8 +35,12 @@ Prints one JSON line with:
   audiovae     the AudioVAE decode of 40 latent frames (1.6 s of 48 kHz audio):
                time, real-time factor and GEMM-form TFLOP/s
 
+  long_context the decode at --max-context 8192, positions 512..8000: tok/s and
+               the attention and attn_out cost per layer
+
 `--copy-calibration` instead runs one plain copy kernel of known size (the
-reference point for the FETCH_SIZE / WRITE_SIZE counters).
+reference point for the FETCH_SIZE / WRITE_SIZE counters); `--timeline` the
+graph-mode per-kernel timeline of a -DVX_STAMPS build.
 """
 from __future__ import annotations
 
@@ -193,6 +199,8 @@ def parse():
                     help="run only the token-batched prefill leg (for profiling)")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the prefill, warmup and timed decode steps, no graph-timed legs (for profiling)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="graph-mode per-kernel timeline (needs the -DVX_STAMPS library in VOXHIP_LIBRARY)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one copy kernel of known size and exit (PMC calibration)")
     ap.add_argument("--vendor-gemm", action="store_true",
@@ -450,6 +458,120 @@ def long_context_leg(ctx, model, cfg, steps=16, reps=4):
     return out
 
 
+TIMELINE_KINDS = {1: "qkv", 2: "attention", 3: "attention", 4: "attn_out", 5: "swiglu", 6: "down"}
+TICK_US = 0.01   # s_memrealtime's nominal 100 MHz; timeline_leg measures the rate
+
+
+def read_timeline(ctx):
+    """Launch table and per-wave (start, end) ticks of a -DVX_STAMPS library."""
+    import ctypes as C
+    from voxgen_amd import abi
+    nl, nw = C.c_uint64(), C.c_uint64()
+    abi.call("vx_diag_timeline_read", ctx.handle, None, 0, None, 0, C.byref(nl), C.byref(nw))
+    launches = np.zeros(3 * nl.value, np.uint64)
+    ticks = np.zeros(2 * nw.value, np.uint64)
+    abi.call("vx_diag_timeline_read", ctx.handle, launches.ctypes.data_as(C.POINTER(C.c_uint64)), nl.value,
+             ticks.ctypes.data_as(C.POINTER(C.c_uint64)), nw.value, C.byref(nl), C.byref(nw))
+    return launches.reshape(-1, 3), ticks.reshape(-1, 2).astype(np.int64)
+
+
+def timeline_spans(launches, ticks, first, count):
+    """Per launch (kind, start, end, mean wave life, waves) over launches
+    [first, first + count), ticks relative to the first launch's start."""
+    rows = []
+    for kind, w0, nw in launches[first:first + count]:
+        t = ticks[int(w0):int(w0 + nw)]
+        rows.append((int(kind), int(t[:, 0].min()), int(t[:, 1].max()), float((t[:, 1] - t[:, 0]).mean()), int(nw)))
+    base = rows[0][1]
+    return [(k, s - base, e - base, life, nw) for k, s, e, life, nw in rows], base
+
+
+def timeline_summary(rows_per_step, layers=28, per_layer=5, tick_us=TICK_US):
+    """Mean over steps: per kernel of the layer its span (first wave start to last
+    wave end), the gap before it (previous stamped kernel's last wave end to its
+    first wave start) and the mean wave life; the layer period; the step span."""
+    spans = np.array([[e - s for _, s, e, _, _ in rows] for rows in rows_per_step], float) * tick_us
+    starts = np.array([[s for _, s, _, _, _ in rows] for rows in rows_per_step], float) * tick_us
+    ends = np.array([[e for _, _, e, _, _ in rows] for rows in rows_per_step], float) * tick_us
+    lives = np.array([[l for _, _, _, l, _ in rows] for rows in rows_per_step], float) * tick_us
+    gaps = np.zeros_like(spans)
+    gaps[:, 1:] = starts[:, 1:] - ends[:, :-1]
+    kinds = [TIMELINE_KINDS[k] for k, *_ in rows_per_step[0]]
+    out = {}
+    for j in range(per_layer):
+        idx = list(range(j, layers * per_layer, per_layer))
+        g = gaps[:, idx]
+        if j == 0:
+            g = g[:, 1:]   # layer 0's qkv follows the unstamped embedding and RoPE-table kernels
+        out[kinds[j]] = {"span_us": round(float(spans[:, idx].mean()), 3),
+                         "gap_before_us": round(float(g.mean()), 3),
+                         "wave_life_us": round(float(lives[:, idx].mean()), 3),
+                         "waves": rows_per_step[0][j][4]}
+    period = (ends[:, per_layer * layers - 1] - ends[:, per_layer - 1]) / (layers - 1)
+    return {"kernels": out, "layer_period_us": round(float(period.mean()), 3),
+            "stamped_span_us": round(float((ends[:, -1] - starts[:, 0]).mean()), 3)}
+
+
+def timeline_leg(steps=12):
+    """Graph-mode decode timeline from a library built with -DVX_STAMPS (python -m
+    voxgen_amd.build --timeline; VOXHIP_LIBRARY=voxgen_amd/timeline/libvoxhip.so):
+    the 28-layer step of the headline workload (context 512, positions 256..,
+    k_attn_chunk) and with --max-context 8192 at position 8000 (16 streamed
+    slices). Each step is one graph replay; a replay's waves' ticks are read back
+    after it."""
+    from voxgen_amd import abi, synth
+    from voxgen_amd.baselm import BaseLmEngine
+    from voxgen_amd.runtime import Context, Model
+    cfg = synth.baselm_config(active_context=512)
+    m = synth.build_baselm(cfg, seed=0x5EED0002)
+    toks = synth.uniform_u32(256 + steps + 16, 0x5EED0012, cfg["vocab_size"]).astype(np.uint32)
+    ctx = Context(0)
+    model = Model(ctx, m.data, m.tensors)
+    abi.call("vx_diag_timeline_arm", ctx.handle, 1 << 22)
+    report = {}
+    for label, ecfg, start in (("context_512_position_256", cfg, 256),
+                               ("context_8192_position_8000", dict(cfg, active_context_length=8192), 8000)):
+        eng = BaseLmEngine(ctx, model, ecfg, exec_mode="graph", strict_geometry=True)
+        launches0, _ = read_timeline(ctx)
+        eng.set_position(start)
+        eng.decode_tokens_gpu_only(toks[:4])   # captures this position's graph
+        ctx.sync()
+        launches, _ = read_timeline(ctx)
+        first, count = len(launches0), len(launches) - len(launches0)
+        assert count == 5 * cfg["block_count"], count
+        # Each sample is a burst of `burst` back-to-back replays (the GPU at its
+        # running clocks) whose last replay leaves the timeline. The tick rate:
+        # samples 20 ms apart, the last launch's end ticks fitted against the host
+        # clock after the burst's sync (tens of microseconds of error over 0.3 s).
+        rows, walls, host_t, dev_t = [], [], [], []
+        burst = 16
+        for i in range(steps):
+            eng.set_position(start + 4 + i)
+            time.sleep(0.02)
+            t0 = time.perf_counter()
+            eng.decode_tokens_gpu_only(toks[4 + i:4 + i + burst])
+            ctx.sync()
+            t1 = time.perf_counter()
+            walls.append((t1 - t0) / burst)
+            launches, ticks = read_timeline(ctx)
+            r, base = timeline_spans(launches, ticks, first, count)
+            rows.append(r)
+            host_t.append(t1)
+            dev_t.append(base + r[-1][2])
+        hz = float(np.polyfit(np.array(host_t) - host_t[0], np.array(dev_t, float) - dev_t[0], 1)[0])
+        summ = timeline_summary(rows, cfg["block_count"], tick_us=1e6 / hz)
+        summ["tick_mhz"] = round(hz / 1e6, 3)
+        summ["host_ms_per_step"] = round(float(np.median(walls)) * 1e3, 4)
+        report[label] = summ
+        log(f"timeline {label}: layer period {summ['layer_period_us']} us, stamped span "
+            f"{summ['stamped_span_us']} us, host {summ['host_ms_per_step']} ms/step; " +
+            ", ".join(f"{k} {v['span_us']} (+{v['gap_before_us']})" for k, v in summ["kernels"].items()))
+        eng.close()
+    model.free()
+    ctx.close()
+    return report
+
+
 def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384, cpu_steps=0):
     """The ResidualLM step of the VoxCPM2 acoustic model (acoustic.rs:830-1035):
     FSQ of the BaseLM hidden, fusion with the acoustic embedding, 8 F16 layers
@@ -635,6 +757,9 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.timeline:
+        print(json.dumps({"timeline": timeline_leg()}), flush=True)
+        return
     from voxgen_amd import abi, synth
     from voxgen_amd.baselm import BaseLmEngine
     from voxgen_amd.runtime import Context, Model
@@ -735,12 +860,25 @@ def main():
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    # The same kernel's average duration from the committed rocprofv3 kernel trace
+    # of the eager decode (kernel execution only, no launch gap).
+    rocprof = None
+    rfile = ROOT / "profiles" / "kernels_decode28_q8.json"
+    if rfile.exists():
+        try:
+            r = json.loads(rfile.read_text())
+            gbps = r["algorithmic_bytes_per_launch"] / (r["avg_us"] * 1e-6) / 1e9
+            rocprof = {"kernel": r["kernel"], "avg_us": r["avg_us"], "achieved": round(gbps, 1),
+                       "frac": round(gbps / HBM_PEAK_GBPS, 4), "source": "profiles/kernels_decode28_q8.json"}
+        except (OSError, ValueError, KeyError):
+            rocprof = None
     achievable = achievable_leg(ctx)
     log(f"achievable streaming read: {achievable['GBps']:.0f} GB/s ({achievable['frac_of_spec']:.3f} of 8 TB/s)")
     roofline = dict(bound="hbm", achieved=dom["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
                     frac=dom["frac"], traffic=traffic, kernel="k_swiglu (rmsnorm + gate/up Q8_0 matvec + SiLU)",
                     bytes_per_launch=dom["bytes"], avg_us=dom["avg_us"],
-                    achievable_GBps=achievable["GBps"], frac_of_achievable=round(dom["GBps"] / achievable["GBps"], 4))
+                    achievable_GBps=achievable["GBps"], frac_of_achievable=round(dom["GBps"] / achievable["GBps"], 4),
+                    rocprof=rocprof)
     mean_step_bytes = float(np.mean([step_bytes(p, args.lm_head) for p in range(P, P + K)]))
     c0 = c0_leg(ctx)
     log(f"c0 matvec 2048x2048 Q8_0: {c0['hbm']['avg_us']:.2f} us from HBM ({c0['hbm']['GBps']:.0f} GB/s), "

@@ -485,6 +485,21 @@ int vx_diag_stream_read(vx_ctx *ctx, const vx_buf *src, uint64_t offset, uint64_
                         uint32_t blocks, uint32_t unroll);
 /* Copy `bytes` (multiple of 16) from src to dst with `blocks` x 256 threads. */
 int vx_diag_stream_copy(vx_ctx *ctx, vx_buf *dst, const vx_buf *src, uint64_t bytes, uint32_t blocks);
+/* Decode-kernel timeline, for a library built with -DVX_STAMPS (`python -m
+ * voxgen_amd.build --timeline`); the shipped library returns VX_ERR_UNSUPPORTED.
+ * vx_diag_timeline_arm reserves room for `waves` wave records on ctx's device
+ * (cleared) and empties the launch table: every decode kernel enqueued or
+ * captured into a graph afterwards (qkv, attention, attn_out, SwiGLU, matvec)
+ * gets one record per wave, which each run of the kernel (each graph replay)
+ * overwrites with its s_memrealtime ticks (100 MHz) at the wave's start and end.
+ * Launches past the reserved room are not recorded. One timeline per process. */
+int vx_diag_timeline_arm(vx_ctx *ctx, uint64_t waves);
+/* After vx_sync: copies up to max_launches launch records, three u64 each
+ * (kind: 1 qkv, 2 attention chunk, 3 attention stream, 4 attn_out, 5 SwiGLU,
+ * 6 matvec; first wave record; wave count), and up to max_waves (start, end)
+ * tick pairs; *n_launches and *n_waves receive the totals recorded. */
+int vx_diag_timeline_read(vx_ctx *ctx, uint64_t *launches, uint64_t max_launches, uint64_t *ticks,
+                          uint64_t max_waves, uint64_t *n_launches, uint64_t *n_waves);
 
 /* ------------------------------------------------------------------------- */
 /* GGUF (gguf.rs:222-286): host-side parse of a model file.                   */

@@ -819,6 +819,16 @@ extern "C" {
         bytes: u64,
         blocks: u32,
     ) -> c_int;
+    pub fn vx_diag_timeline_arm(ctx: *mut VxCtx, waves: u64) -> c_int;
+    pub fn vx_diag_timeline_read(
+        ctx: *mut VxCtx,
+        launches: *mut u64,
+        max_launches: u64,
+        ticks: *mut u64,
+        max_waves: u64,
+        n_launches: *mut u64,
+        n_waves: *mut u64,
+    ) -> c_int;
     pub fn vx_gguf_open(path: *const c_char, out: *mut *mut VxGguf) -> c_int;
     pub fn vx_gguf_close(g: *mut VxGguf) -> c_int;
 }

@@ -232,6 +232,19 @@ def test_persistent_mode_is_refused(ctx, two_layers):
     assert e.value.name == "VX_ERR_UNSUPPORTED" and "persistent" in str(e.value)
 
 
+def test_timeline_entry_points_need_the_timeline_build(ctx):
+    """The shipped library has no per-wave stamps in its kernels: the timeline
+    diagnostics (a -DVX_STAMPS build's) are a clear error there."""
+    import ctypes as C
+    if abi.load().vx_diag_timeline_arm(ctx.handle, 1024) == 0:
+        pytest.skip("this is the -DVX_STAMPS build")
+    assert "VX_STAMPS" in abi.load().vx_last_error().decode()
+    nl, nw = C.c_uint64(7), C.c_uint64(7)
+    with pytest.raises(abi.VxError) as e:
+        abi.call("vx_diag_timeline_read", ctx.handle, None, 0, None, 0, C.byref(nl), C.byref(nw))
+    assert e.value.name == "VX_ERR_UNSUPPORTED" and nl.value == 0 and nw.value == 0
+
+
 def test_gguf_file_through_the_loader_decodes_like_the_oracle(ctx, full_model, tmp_path):
     """The real load path: the 28-layer model written as a GGUF v3 file, parsed by
     vx_gguf_open (load_summary, gguf.rs:222-286), configured by

@@ -275,6 +275,8 @@ PROTOTYPES = {
     "vx_fused_rms_swiglu": (i32, [CTX, MODEL, BUFP, BUFP, P(FusedSwigluArgs)]),
     "vx_diag_stream_read": (i32, [CTX, BUFP, u64, u64, BUFP, u32, u32]),
     "vx_diag_stream_copy": (i32, [CTX, BUFP, BUFP, u64, u32]),
+    "vx_diag_timeline_arm": (i32, [CTX, u64]),
+    "vx_diag_timeline_read": (i32, [CTX, P(u64), u64, P(u64), u64, P(u64), P(u64)]),
     "vx_gguf_open": (i32, [C.c_char_p, P(GGUF)]),
     "vx_gguf_close": (i32, [GGUF]),
     "vx_gguf_summary_get": (i32, [GGUF, P(GgufSummary)]),

@@ -3,6 +3,10 @@
   voxgen_amd/libvoxhip.so    HIP kernels for gfx950 + C ABI (include/voxhip.h)
   voxgen_amd/libvoxsynth.so  host-side deterministic input generator
 
+`--timeline` instead builds voxgen_amd/timeline/libvoxhip.so with -DVX_STAMPS: the
+same library whose decode kernels also record per-wave s_memrealtime ticks
+(vx_diag_timeline_*), loaded through VOXHIP_LIBRARY by `bench.py --timeline`.
+
 Device code is compiled with packed-FP32 instructions disabled
 (-Xclang -target-feature -Xclang -packed-fp32-ops).
 Run as a script or call build_all(); every call recompiles.
@@ -55,29 +59,33 @@ SANITIZE_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize
                  "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
                  "-Xarch_host", "-shared-libasan"]
 ASAN_DIR = ROOT / "_build" / "asan"
+TIMELINE_OBJ = ROOT / "_build" / "timeline"
+TIMELINE_DIR = PKG / "timeline"
 
 
-def _compile(src: Path, sanitize: bool = False) -> Path:
-    odir = ASAN_DIR / "obj" if sanitize else OBJ
+def _compile(src: Path, sanitize: bool = False, timeline: bool = False) -> Path:
+    odir = ASAN_DIR / "obj" if sanitize else TIMELINE_OBJ if timeline else OBJ
     odir.mkdir(parents=True, exist_ok=True)
     obj = odir / (src.name + ".o")
     # hipcc treats .cpp as HIP source too; both get the gfx950 device flags.
     cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), *(SANITIZE_HOST if sanitize else []),
-           "-c", str(src), "-o", str(obj)]
+           *(["-DVX_STAMPS"] if timeline else []), "-c", str(src), "-o", str(obj)]
     _run(cmd)
     return obj
 
 
-def build_voxhip(jobs: int | None = None, sanitize: bool = False) -> Path:
-    """Build libvoxhip.so in the package, or with sanitize=True the host-sanitized
+def build_voxhip(jobs: int | None = None, sanitize: bool = False, timeline: bool = False) -> Path:
+    """Build libvoxhip.so in the package; with sanitize=True the host-sanitized
     variant at _build/asan/libvoxhip.so (load it with VOXHIP_LIBRARY and the ASan
-    runtime preloaded)."""
+    runtime preloaded); with timeline=True the -DVX_STAMPS variant at
+    voxgen_amd/timeline/libvoxhip.so."""
     sources = sorted(CSRC.glob("*.hip")) + sorted(
         p for p in CSRC.glob("*.cpp"))
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda src: _compile(src, sanitize), sources))
-    out = (ASAN_DIR if sanitize else PKG) / "libvoxhip.so"
+        objs = list(ex.map(lambda src: _compile(src, sanitize, timeline), sources))
+    out = (ASAN_DIR if sanitize else TIMELINE_DIR if timeline else PKG) / "libvoxhip.so"
+    out.parent.mkdir(parents=True, exist_ok=True)
     tmp = out.with_name("libvoxhip.so.tmp")
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *(SANITIZE_HOST if sanitize else []),
           "-o", str(tmp), *map(str, objs)])
@@ -114,4 +122,7 @@ def build_all(verbose: bool = False) -> None:
 
 
 if __name__ == "__main__":
-    build_all(verbose=True)
+    if "--timeline" in sys.argv[1:]:
+        print(f"built {build_voxhip(timeline=True).relative_to(ROOT)}")
+    else:
+        build_all(verbose=True)

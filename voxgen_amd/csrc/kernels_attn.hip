@@ -88,6 +88,7 @@ struct AttnArgs {
     float *out, *part;
     const uint32_t *position;
     uint32_t layer, context, q_heads, kv_heads, splits;
+    VX_STAMP_FIELD
 };
 
 // Partial record of one (head, slice): m, l, 2 pad words, acc[HD] (16-byte aligned acc).
@@ -99,6 +100,7 @@ __device__ __forceinline__ float *part_rec(const AttnArgs &a, uint32_t h, uint32
 // k_attn_chunk: see the file comment.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     constexpr int R = HD / 4;            // dims per quarter (scores)
     constexpr int KG = 256 / HD;         // key groups (P.V)
     constexpr int KPG = kTile / KG;      // keys per group
@@ -256,6 +258,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 // takes keys t0 + 16 NW i + 16 w + j.
 template <int HD, int NW>
 __global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     constexpr int R = HD / 4;            // dimensions per lane
     constexpr int NI = R / 8;            // 16-byte loads per K (and V) row and lane
     constexpr uint32_t STEP = 16u * NW;  // keys per workgroup step
@@ -556,8 +559,9 @@ AttnArgs attn_args(const AttnLaunch &l) {
 
 int launch_attn_partials(hipStream_t s, const AttnLaunch &l) {
     VX_CHECK(attn_validate(l));
-    const AttnArgs a = attn_args(l);
+    AttnArgs a = attn_args(l);
     dim3 grid(l.splits, l.q_heads);
+    VX_SET_STAMPS(a, ST_ATTN_CHUNK, (uint64_t)l.splits * l.q_heads * 4u);
     if (l.head_dim == 128)
         k_attn_chunk<128><<<grid, 256, 0, s>>>(a);
     else
@@ -569,9 +573,10 @@ int launch_attn_partials(hipStream_t s, const AttnLaunch &l) {
 int launch_attn_stream(hipStream_t s, const AttnLaunch &l, uint32_t waves) {
     VX_CHECK(attn_validate(l));
     if (waves != 4u && waves != 8u) return fail(VX_ERR_INVALID_ARG, "stream attention runs 4 or 8 waves");
-    const AttnArgs a = attn_args(l);
+    AttnArgs a = attn_args(l);
     dim3 grid(l.splits, l.q_heads);
     const bool eight = waves == 8u;
+    VX_SET_STAMPS(a, ST_ATTN_STREAM, (uint64_t)l.splits * l.q_heads * waves);
     if (l.head_dim == 128) {
         if (eight) k_attn_stream<128, 8><<<grid, 512, 0, s>>>(a);
         else k_attn_stream<128, 4><<<grid, 256, 0, s>>>(a);

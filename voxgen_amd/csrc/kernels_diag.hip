@@ -1,6 +1,8 @@
 // Streaming diagnostics: a plain HBM read and a plain copy. They calibrate the
 // roofline (achievable read bandwidth next to the 8 TB/s spec) and the PMC byte
 // counters (FETCH_SIZE/WRITE_SIZE of a copy of known size).
+#include <algorithm>
+
 #include "vx_internal.h"
 
 namespace vx {
@@ -34,6 +36,27 @@ __global__ __launch_bounds__(256) void k_stream_copy(uint4 *dst, const uint4 *sr
 }
 
 }  // namespace
+
+#ifdef VX_STAMPS
+namespace {
+struct Timeline {
+    uint64_t *ticks = nullptr;   // device: (start, end) per wave record
+    uint64_t cap = 0, used = 0;  // wave records
+    int device = -1;
+    std::vector<uint64_t> launches;   // (kind, first record, waves) per launch
+};
+Timeline g_timeline;
+}  // namespace
+
+uint64_t *stamp_slots(uint32_t kind, uint64_t waves) {
+    Timeline &t = g_timeline;
+    if (!t.ticks || waves > t.cap - t.used) return nullptr;
+    uint64_t *p = t.ticks + 2u * t.used;
+    t.launches.insert(t.launches.end(), {(uint64_t)kind, t.used, waves});
+    t.used += waves;
+    return p;
+}
+#endif
 }  // namespace vx
 
 using namespace vx;
@@ -75,5 +98,58 @@ int vx_diag_stream_copy(vx_ctx *ctx, vx_buf *dst, const vx_buf *src, uint64_t by
     VX_LAUNCHED("k_stream_copy");
     return VX_OK;
 }
+
+#ifdef VX_STAMPS
+int vx_diag_timeline_arm(vx_ctx *ctx, uint64_t waves) {
+    if (!ctx || waves == 0 || waves > (1ull << 26))
+        return fail(VX_ERR_INVALID_ARG, "vx_diag_timeline_arm: null context or waves outside 1..2^26");
+    Timeline &t = g_timeline;
+    VX_HIP(hipSetDevice(ctx->device));
+    // A graph captured under an earlier arm keeps writing the old records, so
+    // those stay allocated until the process ends.
+    t = Timeline{};
+    void *p = nullptr;
+    if (hipMalloc(&p, waves * 16u) != hipSuccess) return fail(VX_ERR_OOM, "vx_diag_timeline_arm: %llu records",
+                                                              (unsigned long long)waves);
+    VX_HIP(hipMemset(p, 0, waves * 16u));
+    VX_HIP(hipDeviceSynchronize());
+    t.ticks = static_cast<uint64_t *>(p);
+    t.cap = waves;
+    t.device = ctx->device;
+    return VX_OK;
+}
+
+int vx_diag_timeline_read(vx_ctx *ctx, uint64_t *launches, uint64_t max_launches, uint64_t *ticks,
+                          uint64_t max_waves, uint64_t *n_launches, uint64_t *n_waves) {
+    if (!ctx || !n_launches || !n_waves || (max_launches && !launches) || (max_waves && !ticks))
+        return fail(VX_ERR_INVALID_ARG, "vx_diag_timeline_read: null argument");
+    const Timeline &t = g_timeline;
+    if (!t.ticks || t.device != ctx->device) return fail(VX_ERR_STATE, "vx_diag_timeline_read: no timeline armed");
+    *n_launches = t.launches.size() / 3u;
+    *n_waves = t.used;
+    const uint64_t nl = std::min<uint64_t>(max_launches, *n_launches);
+    std::copy(t.launches.begin(), t.launches.begin() + 3u * nl, launches);
+    const uint64_t nw = std::min<uint64_t>(max_waves, t.used);
+    if (nw) {
+        VX_HIP(hipSetDevice(ctx->device));
+        VX_HIP(hipMemcpy(ticks, t.ticks, nw * 16u, hipMemcpyDeviceToHost));
+    }
+    return VX_OK;
+}
+#else
+int vx_diag_timeline_arm(vx_ctx *ctx, uint64_t waves) {
+    (void)ctx;
+    (void)waves;
+    return fail(VX_ERR_UNSUPPORTED, "vx_diag_timeline_arm: this library was built without -DVX_STAMPS");
+}
+
+int vx_diag_timeline_read(vx_ctx *ctx, uint64_t *launches, uint64_t max_launches, uint64_t *ticks,
+                          uint64_t max_waves, uint64_t *n_launches, uint64_t *n_waves) {
+    (void)ctx, (void)launches, (void)max_launches, (void)ticks, (void)max_waves;
+    if (n_launches) *n_launches = 0;
+    if (n_waves) *n_waves = 0;
+    return fail(VX_ERR_UNSUPPORTED, "vx_diag_timeline_read: this library was built without -DVX_STAMPS");
+}
+#endif
 
 }  // extern "C"

@@ -34,6 +34,7 @@ struct MvArgs {
     uint32_t bias_dtype;
     float *y, *y2;
     float scale;
+    VX_STAMP_FIELD
 };
 
 // Epilogue variants are compile-time: each kernel instance has one
@@ -85,6 +86,7 @@ __device__ __forceinline__ void epilogue(const MvArgs &a, uint32_t row, float ac
 // 5.28 -> 4.90 us, attn_out-shaped 3.03 -> 2.74 us against 4-wave groups).
 template <int WT, int NG, int RPW, int EP, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_matvec(MvArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     __shared__ __align__(16) float xs[NG * kGroupCols];
     __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & 63;
@@ -140,6 +142,7 @@ struct AttnOutArgs {
 
 template <int WT, int NG, int RPW, int HD, bool BRANCH, int WPB, int FS>
 __global__ __launch_bounds__(64 * WPB) void k_attn_out(AttnOutArgs a) {
+    VX_WAVE_STAMP(a.mv.stamps);
     // The first MT threads merge E outputs each (float4 units): every one of the
     // workgroup's threads up to 1024*NG/4 of them.
     constexpr int MT = 64 * WPB < 256 * NG ? 64 * WPB : 256 * NG;
@@ -286,6 +289,7 @@ struct SwArgs {
     float eps;
     uint32_t rows, cols, row_base;
     float *y;
+    VX_STAMP_FIELD
 };
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -296,6 +300,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // reduced dot products: silu(g/rms) * (u/rms).
 template <int WT, int NG, int RPW, bool NORM, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_swiglu(SwArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     __shared__ __align__(16) float xs[NG * kGroupCols];
     __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & 63;
@@ -369,6 +374,7 @@ struct QkvArgs {
     const uint32_t *position;
     const float2 *rope_cs;
     uint32_t no_rope;
+    VX_STAMP_FIELD
 };
 
 // One wave per rotary pair: Q/K rows (i, i + head_dim/2) of a head, or two
@@ -376,6 +382,7 @@ struct QkvArgs {
 // (store_kv.comp:21-23) run on the reduced pair in lane 0.
 template <int WT, int NG, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_qkv_fused(QkvArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row math
     __shared__ __align__(16) float xs[NG * kGroupCols];
@@ -502,7 +509,10 @@ int dispatch_matvec_ng(hipStream_t s, const MvArgs &a, uint32_t ng) {
 #define VX_MV(NGV, RPWV, WPBV)                                                                       \
     do {                                                                                             \
         const uint32_t per_block = (WPBV) * (RPWV);                                                  \
-        k_matvec<WT, NGV, RPWV, EP, WPBV><<<(n + per_block - 1) / per_block, 64 * (WPBV), 0, s>>>(a); \
+        const uint32_t grid = (n + per_block - 1) / per_block;                                       \
+        MvArgs b = a;                                                                                \
+        VX_SET_STAMPS(b, ST_MATVEC, (uint64_t)grid * (WPBV));                                        \
+        k_matvec<WT, NGV, RPWV, EP, WPBV><<<grid, 64 * (WPBV), 0, s>>>(b);                           \
     } while (0)
     switch (ng) {
         case 1:
@@ -599,6 +609,7 @@ int launch_swiglu(hipStream_t s, const SwigluLaunch &l) {
 #define VX_SW(WTV, NGV, RPWV, WPBV)                                                                     \
     do {                                                                                                \
         const uint32_t grid = (n + (WPBV) * (RPWV) - 1) / ((WPBV) * (RPWV));                           \
+        VX_SET_STAMPS(a, ST_SWIGLU, (uint64_t)grid * (WPBV));                                           \
         if (l.norm)                                                                                     \
             k_swiglu<WTV, NGV, RPWV, true, WPBV><<<grid, 64 * (WPBV), 0, s>>>(a);                       \
         else                                                                                            \
@@ -640,6 +651,7 @@ int launch_qkv_fused(hipStream_t s, const QkvFusedLaunch &l) {
     // 8-wave workgroups (one staging of x per 8 rotary pairs).
     constexpr uint32_t WPB = 8;
     const uint32_t grid = (pairs + WPB - 1) / WPB;
+    VX_SET_STAMPS(a, ST_QKV, (uint64_t)grid * WPB);
 #define VX_QKV(WTV, NGV) k_qkv_fused<WTV, NGV, WPB><<<grid, 64 * WPB, 0, s>>>(a)
 #define VX_QKV_NG(WTV)                      \
     switch (ng) {                           \
@@ -686,6 +698,7 @@ int launch_attn_out(hipStream_t s, const AttnOutLaunch &l) {
 #define VX_AO_FS(WTV, NGV, HDV, RPWV, WPBV, FSV)                                                           \
     do {                                                                                                   \
         const uint32_t grid = (l.mv.rows + (WPBV) * (RPWV) - 1) / ((WPBV) * (RPWV));                      \
+        VX_SET_STAMPS(a.mv, ST_ATTN_OUT, (uint64_t)grid * (WPBV));                                         \
         if (l.mv.y2)                                                                                       \
             k_attn_out<WTV, NGV, RPWV, HDV, true, WPBV, FSV><<<grid, 64 * (WPBV), 0, s>>>(a);            \
         else                                                                                               \

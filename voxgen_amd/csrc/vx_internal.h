@@ -43,6 +43,45 @@ void clear_error();
                               hipGetErrorString(e_));                                     \
     } while (0)
 
+// ------------------------------------------------------- timeline build
+// A library built with -DVX_STAMPS (never the shipped one) records a timeline of
+// the decode kernels: each wave writes one (start, end) pair of s_memrealtime
+// ticks into slots that stamp_slots hands out launch by launch when the launch
+// is enqueued or captured, so every replay of a captured graph rewrites its own
+// launches' slots (vx_diag_timeline_arm / _read).
+#ifdef VX_STAMPS
+enum StampKind : uint32_t {
+    ST_QKV = 1, ST_ATTN_CHUNK = 2, ST_ATTN_STREAM = 3, ST_ATTN_OUT = 4, ST_SWIGLU = 5, ST_MATVEC = 6,
+};
+// Slots for `waves` waves, or nullptr when no timeline is armed or it is full.
+uint64_t *stamp_slots(uint32_t kind, uint64_t waves);
+struct WaveStamp {
+    uint64_t *slot;
+    uint64_t t0 = 0;
+    __device__ explicit WaveStamp(uint64_t *base) : slot(base) {
+        if (slot) {
+            const uint64_t wg = blockIdx.x + (uint64_t)gridDim.x * (blockIdx.y + (uint64_t)gridDim.y * blockIdx.z);
+            slot += 2 * (wg * (blockDim.x >> 6) + (threadIdx.x >> 6));
+            t0 = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+    __device__ ~WaveStamp() {
+        if (slot && (threadIdx.x & 63) == 0) {
+            const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+            slot[0] = t0;
+            slot[1] = t1;
+        }
+    }
+};
+#define VX_STAMP_FIELD uint64_t *stamps = nullptr;
+#define VX_WAVE_STAMP(p) ::vx::WaveStamp vx_wave_stamp_(p)
+#define VX_SET_STAMPS(args, kind, waves) ((args).stamps = ::vx::stamp_slots((kind), (waves)))
+#else
+#define VX_STAMP_FIELD
+#define VX_WAVE_STAMP(p) ((void)0)
+#define VX_SET_STAMPS(args, kind, waves) ((void)0)
+#endif
+
 // ------------------------------------------------------- weight references
 enum WeightType : uint32_t { WT_Q8 = 0, WT_F16 = 1, WT_F32 = 2 };
 
