@@ -2,10 +2,11 @@
 
 * Long contexts: VoxGen runs with --max-context 8192 (main.rs:97-99), which sizes
   the KV cache (baselm.rs:182-192). The engine's decode attention has three tiers by
-  key count: 8 slices of at most 64 keys (k_attn_chunk) up to 1024 keys, then 8 and
-  from 2561 keys 16 streamed slices of many keys (k_attn_stream); attn_out merges the
-  slices of each. All are checked against the oracle, across both switches and at
-  positions 4096 and 8000 of the 28-layer stack.
+  key count: up to 1024 keys 8 slices (k_attn_chunk while a slice holds at most 64
+  keys whatever the position, else k_attn_rows), then 8 and from 2561 keys 16
+  streamed slices of many keys (k_attn_rows); attn_out merges the slices of each.
+  All are checked against the oracle, across both switches (head_dim 128 and 64)
+  and at positions 4096 and 8000 of the 28-layer stack.
 * LongRoPE with context_length > rope_original_context_length: the long factors and
   a scaling factor != 1 (rope_scaling_factor, baselm.rs:194-205; factor choice,
   baselm.rs:902-913) on the device.
@@ -34,19 +35,24 @@ def oracle(m, cfg):
 
 
 @pytest.mark.parametrize("mode", ["graph", "fused"])
-@pytest.mark.parametrize("active,start", [(2048, 1019), (4096, 2555)])
-def test_decode_across_the_attention_tiers(ctx, mode, active, start):
+@pytest.mark.parametrize("active,start,head_dim", [(2048, 1019, 128), (4096, 2555, 128), (4096, 1019, 64),
+                                                   (4096, 2555, 64)])
+def test_decode_across_the_attention_tiers(ctx, mode, active, start, head_dim):
     """One layer (so the attention vector is the kernel's output on the layer's
     own q, not a product of upstream rounding): twelve positions from `start`
-    step from one attention tier into the next (1024 -> 1025 keys: k_attn_chunk
-    to 8 streamed slices; 2560 -> 2561 keys: 8 to 16 streamed slices); every
+    step from one attention tier into the next (1024 -> 1025 keys: 8 slices of
+    four waves to 8 of eight; 2560 -> 2561 keys: 8 to 16 slices), at head_dim 128
+    (hidden 2048) and 64 (hidden 1024, 8 lanes per key row in k_attn_rows); every
     output, the attention vector and the stored K/V rows follow the oracle."""
-    cfg = synth.baselm_config(layers=1, vocab=2048, context_length=32768, active_context=active)
+    hidden = 16 * head_dim
+    cfg = synth.baselm_config(layers=1, hidden=hidden, vocab=2048, context_length=32768, active_context=active,
+                              head_dim=head_dim)
     # Small Q8_0 scales keep the model's own keys from dominating the softmax (see
     # long_model below): the test compares kernels, not conditioning.
     m = synth.build_baselm(cfg, seed=0x5EED0301, q8_scale_sigma=0.002)
     model = Model(ctx, m.data, m.tensors)
-    kk, vv = kv_bits(1, active, start, 0x5EED0302)
+    kv_dim = 2 * head_dim
+    kk, vv = kv_bits(1, active, start, 0x5EED0302, kv_dim)
     o = oracle(m, cfg)
     o.kv_k[:] = kk
     o.kv_v[:] = vv
@@ -61,9 +67,9 @@ def test_decode_across_the_attention_tiers(ctx, mode, active, start):
         assert r.position == pos
         want = o.decode_token(t, pos)
         assert rel_l2(eng.output(), want) < 1e-3, pos
-        assert rel_l2(eng.buffer("attention").download(np.float32, 2048), o.attention) < 1e-3, pos
-    got = eng.buffer("kv_k").download(np.uint16, kk.size).reshape(1, active, 256)
-    ref = o.kv_k.reshape(1, active, 256)
+        assert rel_l2(eng.buffer("attention").download(np.float32, hidden), o.attention) < 1e-3, pos
+    got = eng.buffer("kv_k").download(np.uint16, kk.size).reshape(1, active, kv_dim)
+    ref = o.kv_k.reshape(1, active, kv_dim)
     assert np.array_equal(got[:, :start], ref[:, :start])
     assert rel_l2(got[:, start:start + 12].view(np.float16), ref[:, start:start + 12].view(np.float16)) < 1e-3
     assert np.all(got[:, start + 12:] == 0)

@@ -51,7 +51,7 @@ struct vx_baselm {
     bool fold_attn_merge = false;  // attention merge folded into the attn_out matvec
     // Attention tiers by the step's key count (attn_tier): tier 0 is the short
     // contexts' k_attn_chunk over `splits` slices; tiers 1 and 2 stream
-    // tier_splits[t] slices of many keys through k_attn_stream (0: tier unused).
+    // tier_splits[t] slices of many keys through k_attn_rows (0: tier unused).
     // attn_out merges the slices of every tier.
     uint32_t tier_splits[3] = {0, 0, 0};
     uint32_t pos = 0;
@@ -191,13 +191,18 @@ const char *const kLayerKernelNames[LK_COUNT] = {"baselm.qkv", "baselm.attention
                                                  "baselm.swiglu", "baselm.down"};
 
 // Attention tier of a step over `pos + 1` keys. Up to kTier1FromKeys keys the
-// short contexts' kShortSplits slices of k_attn_chunk (whose keys are fetched
-// before the position is known while a slice holds at most 64 of them); then
-// kShortSplits streamed slices of eight waves; from kTier2FromKeys keys
-// kMaxFoldedSplits streamed slices of four waves. Measured on MI355X per layer,
-// attention + attn_out at 1041 / 2065 / 4113 / 8017 keys: tier 0 11.5 / 15.3 /
-// 23.1 / 36.8 us, tier 1 10.3 / 11.8 / 14.3 / 19.3 us, tier 2 10.9 / 11.9 /
-// 13.6 / 16.1 us.
+// short contexts' kShortSplits slices: k_attn_chunk while the slices are
+// position-independent (context <= 64 * splits: their keys are fetched before the
+// position is known), else k_attn_rows with four waves; then kShortSplits slices
+// of k_attn_rows with eight waves; from kTier2FromKeys keys kMaxFoldedSplits
+// slices of four waves. With the first stream kernel (64-byte row pieces, expf),
+// measured on MI355X per layer, attention + attn_out at 1041 / 2065 / 4113 / 8017
+// keys: tier 0 11.5 / 15.3 / 23.1 / 36.8 us, tier 1 10.3 / 11.8 / 14.3 / 19.3 us,
+// tier 2 10.9 / 11.9 / 13.6 / 16.1 us. k_attn_rows (whole-row loads, exp2, 32-bit
+// row offsets: 892 against 1221 VALU instructions per kernel) took the attention at
+// 2065 / 4113 / 8017 keys from 7.9 / 7.7 / 10.0 to 6.3 / 6.5 / 8.8 us, and at 513
+// keys of an 8192 context (tier 0, position-dependent slices) from 5.4 (k_attn_chunk)
+// to 4.3 us; wave counts 4 or 8 in tiers 1 and 2 measured alike.
 constexpr uint32_t kTier1FromKeys = 1025;
 constexpr uint32_t kTier2FromKeys = 2561;
 uint32_t attn_tier(const vx_baselm *e, uint32_t pos) {
@@ -256,6 +261,10 @@ int enqueue_layer_kernel(vx_baselm *e, uint32_t which, uint32_t l, uint32_t tier
         case LK_ATTENTION:
             // Partials only when attn_out merges them; else partials + merge.
             if (tier) return launch_attn_stream(s, at, tier == 1 ? 8u : 4u);   // tiers 1 and 2 imply the fold
+            // k_attn_chunk while its slices are position-independent (their rows are
+            // requested before the position); otherwise the whole-row stream kernel.
+            if (fold && attn_fixed_chunk(at.context, at.splits) > kAttnFixedChunk)
+                return launch_attn_stream(s, at, 4u);
             return fold ? launch_attn_partials(s, at) : launch_attn_decode(s, at);
         case LK_ATTN_OUT: {
             MatvecLaunch ao;
@@ -827,7 +836,7 @@ int vx_baselm_create(vx_ctx *ctx, const vx_model *model, const vx_baselm_config 
         (st = alloc(ctx, (uint64_t)c.head_count * c.active_context_length * f, &e->scores)) ||
         (st = alloc(ctx, cache, &e->kv_k)) || (st = alloc(ctx, cache, &e->kv_v)) ||
         (st = alloc(ctx, 256, &e->position)) || (st = alloc(ctx, (uint64_t)c.active_context_length * 4u, &e->tokens)) ||
-        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, std::max(splits, e->tier_splits[2])),
+        (st = alloc(ctx, attn_scratch_bytes(c.head_dim, c.head_count, c.head_count_kv, std::max({splits, e->tier_splits[1], e->tier_splits[2]})),
                     &e->attn_scratch)) ||
         (st = alloc(ctx, (uint64_t)c.head_dim * 4u, &e->rope_table)))
         return bail(st);

@@ -8,7 +8,9 @@
 // head_dim dims x 256/head_dim key groups for P.V out of LDS. It writes one
 // (max, sum, acc) partial per (head, slice). Every load a tile needs (q, K and V rows) is issued
 // before any of it is used. The GQA map is attn_scores.comp's kvh = qh / q_per_kv.
-// k_attn_combine merges the slices of each head; the engine's decode step folds
+// k_attn_rows writes the same records for slices of many keys, each wave
+// streaming its keys with whole-row loads (below). k_attn_combine merges the
+// slices of each head; the engine's decode step folds
 // that merge into the attn_out matvec instead (k_attn_out in kernels_matvec.hip).
 // Mathematically this is attn_scores.comp -> softmax.comp -> attn_values.comp
 // (baselm.rs:969-996).
@@ -247,134 +249,181 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     }
 }
 
-// k_attn_stream: the same partial records for slices of many keys (long
-// contexts). Each of the NW waves streams its own keys, 16 per step (lane = key
-// j of the step x quarter r of the head dimension, as in k_attn_chunk's score
-// layout), with the K and V rows of the next two steps in flight while a step is
-// computed, and keeps a wave-uniform running max, a per-lane partial sum of p
-// and per-lane partial accumulators p * V[j] over its quarter's dimensions. No
-// LDS or barrier inside the key loop: the 16 key slots of a wave are summed by
-// lane rotations and swaps after it, and the waves meet once in LDS. Wave w
-// takes keys t0 + 16 NW i + 16 w + j.
+// Lane-group reductions for k_attn_rows. A group is CH = 8 or 16 aligned lanes.
+template <int CH>
+__device__ __forceinline__ float group_sum(float v) {   // result in every lane of the group
+    v += dpp<0xb1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror: the other quad of the half-row
+    if constexpr (CH == 16) v += dpp<0x140>(v);   // row_mirror: the other half-row
+    return v;
+}
+// The two values of a row pair (v_permlane16_swap: rows 0/1, 2/3) or of a
+// half-wave pair (v_permlane32_swap): element 0 holds the lower row's value and
+// element 1 the upper row's, in every lane of both rows.
+__device__ __forceinline__ float2 pair16(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return make_float2(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float2 pair32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return make_float2(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+// Over the wave's groups, lane c of every group meeting lane c of the others
+// (for CH = 8 the two groups of a row first, by a rotation of 8).
+template <int CH>
+__device__ __forceinline__ float groups_sum(float v) {
+    if constexpr (CH == 8) v += dpp<0x128>(v);   // row_ror:8
+    float2 t = pair16(v);
+    v = t.x + t.y;
+    t = pair32(v);
+    return t.x + t.y;
+}
+template <int CH>
+__device__ __forceinline__ float groups_max(float v) {
+    if constexpr (CH == 8) v = fmaxf(v, dpp<0x128>(v));
+    float2 t = pair16(v);
+    v = fmaxf(t.x, t.y);
+    t = pair32(v);
+    return fmaxf(t.x, t.y);
+}
+
+// k_attn_rows: the same partial records for slices of many keys (long contexts,
+// and short ones whose slices depend on the position). Each of the NW waves
+// streams its own keys with no LDS or barrier inside the key loop. A lane is
+// chunk c (8 dimensions) of key group g, CH = HD / 8 lanes per key, so one
+// 16-byte load instruction of the wave reads KPI = 64 / CH consecutive keys'
+// rows of the KV head whole (256 bytes each at head_dim 128). A wave step is NL load instructions of K and of V (16 keys
+// at head_dim 128), key base + KPI i + g in load i; scores are reduced over the
+// group's lanes (DPP) and kept in log2 units (exp2 on the hardware's v_exp_f32),
+// and the running max, the sum of p and the 8 accumulators per lane follow the
+// online softmax. Rows are addressed by 32-bit byte offsets from the layer's
+// (uniform) KV base. When a slice holds at most one step of keys whatever the
+// position (attn_fixed_chunk <= STEP), the rows are requested before the position
+// is read, as in k_attn_chunk, and rows past the position enter with p = 0 and
+// zeroed V. After the loop the groups' accumulators meet by lane swaps, and the
+// NW waves meet once in LDS. Three steps of rows are in flight per wave. The
+// record's max is stored in natural-log units, like k_attn_chunk's.
 template <int HD, int NW>
-__global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
+__global__ __launch_bounds__(64 * NW) void k_attn_rows(AttnArgs a) {
     VX_WAVE_STAMP(a.stamps);
-    constexpr int R = HD / 4;            // dimensions per lane
-    constexpr int NI = R / 8;            // 16-byte loads per K (and V) row and lane
-    constexpr uint32_t STEP = 16u * NW;  // keys per workgroup step
-    __shared__ float osh[NW][HD];        // per-wave accumulators
+    constexpr int CH = HD / 8;             // lanes per key
+    constexpr int KPI = 64 / CH;           // keys per load instruction
+    constexpr int NL = 4;                  // load instructions per step (K and V each)
+    constexpr uint32_t STEPW = KPI * NL;   // keys per wave step
+    constexpr uint32_t STEP = STEPW * NW;  // keys per workgroup step
+    __shared__ float osh[NW][HD];
     __shared__ float wm[NW], wl[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane >> 2, r = lane & 3;
+    const int g = lane / CH, c = lane % CH;
     const uint32_t s = blockIdx.x, h = blockIdx.y;
     const uint32_t kvh = h / (a.q_heads / a.kv_heads);
-    const uint32_t kv_dim = a.kv_heads * HD;
-    // Element 8k + e of quarter r is dimension 8(r + 4k) + e: each load of a
-    // key's four lanes reads 64 contiguous bytes of its row.
-    float qv[R];
+    const uint32_t row_bytes = a.kv_heads * HD * 2u;   // < 2^24, as is every key index (launch checks)
+    const size_t layer_off = ((size_t)a.layer * a.context * a.kv_heads + kvh) * HD;
+    const char *kb = reinterpret_cast<const char *>(a.kc + layer_off);
+    const char *vb = reinterpret_cast<const char *>(a.vc + layer_off);
+    const uint32_t lane_bytes = 16u * (uint32_t)c;
+    auto fetch = [&](uint32_t base, uint32_t last, uint4 *kw, uint4 *vw) {
 #pragma unroll
-    for (int i = 0; i < R; i += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * (r + 4 * (i >> 3)) + (i & 7));
-        qv[i] = v.x;
-        qv[i + 1] = v.y;
-        qv[i + 2] = v.z;
-        qv[i + 3] = v.w;
+        for (int i = 0; i < NL; ++i) {
+            const uint32_t off = __umul24(min(base + KPI * i + g, last), row_bytes) + lane_bytes;
+            kw[i] = *reinterpret_cast<const uint4 *>(kb + off);
+            vw[i] = *reinterpret_cast<const uint4 *>(vb + off);
+        }
+    };
+    const uint32_t fc = attn_fixed_chunk(a.context, a.splits);
+    const bool fixed = fc <= kAttnFixedChunk && fc <= STEP;   // one step per slice, position-independent
+    uint4 k0[NL], v0[NL], k1[NL], v1[NL], k2[NL], v2[NL];
+    if (fixed) fetch(s * fc + STEPW * (uint32_t)wave, a.context - 1u, k0, v0);
+    float qv[8];
+    {
+        const float4 q0 = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * c);
+        const float4 q1 = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * c + 4);
+        qv[0] = q0.x, qv[1] = q0.y, qv[2] = q0.z, qv[3] = q0.w;
+        qv[4] = q1.x, qv[5] = q1.y, qv[6] = q1.z, qv[7] = q1.w;
     }
+    asm volatile("" ::: "memory");   // the fixed rows are requested before the position
     const SplitPlan plan = split_plan(a.position, a.context, a.splits);
     if (s >= plan.active) return;
     const uint32_t t0 = s * plan.chunk;
     const uint32_t t1 = min(plan.n, t0 + plan.chunk);
-    const size_t layer_base = (size_t)a.layer * a.context;
-    const size_t head_off = (size_t)kvh * HD + (size_t)r * 8;
-    const float inv_sqrt = 1.0f / sqrtf((float)HD);
-    auto fetch = [&](uint32_t key, uint4 *kw, uint4 *vw) {
-        const size_t row = (layer_base + (key < t1 ? key : t0)) * kv_dim + head_off;
+    const float scale = 1.4426950408889634f / sqrtf((float)HD);   // log2(e) / sqrt(d)
+    float m = -FLT_MAX, lp = 0.f, o[8];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            kw[i] = *reinterpret_cast<const uint4 *>(a.kc + row + 32 * i);
-            vw[i] = *reinterpret_cast<const uint4 *>(a.vc + row + 32 * i);
-        }
-    };
-    float m = -FLT_MAX, lp = 0.f, o[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) o[i] = 0.f;
-    // One step: 16 keys of the wave from the rows in (kw, vw).
+    for (int e = 0; e < 8; ++e) o[e] = 0.f;
     auto step = [&](uint32_t base, const uint4 *kw, const uint4 *vw) {
-        const bool valid = base + (uint32_t)j < t1;
-        float d0 = 0.f, d1 = 0.f;
+        float sc[NL];
+        bool valid[NL];
+        float smax = -FLT_MAX;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
+        for (int i = 0; i < NL; ++i) {
             const uint32_t w4[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+            float d0 = 0.f, d1 = 0.f;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const float2 kf = h2f2(w4[t]);
-                d0 = fmaf(qv[8 * i + 2 * t], kf.x, d0);
-                d1 = fmaf(qv[8 * i + 2 * t + 1], kf.y, d1);
+                d0 = fmaf(qv[2 * t], kf.x, d0);
+                d1 = fmaf(qv[2 * t + 1], kf.y, d1);
             }
+            const float d = group_sum<CH>(d0 + d1);
+            valid[i] = base + KPI * i + g < t1;
+            sc[i] = valid[i] ? d * scale : -FLT_MAX;
+            smax = fmaxf(smax, sc[i]);
         }
-        const float sc = valid ? quad_sum(d0 + d1) * inv_sqrt : -FLT_MAX;
-        const float m_new = fmaxf(m, wave_max_dpp(sc));
-        const float corr = expf(m - m_new);
-        const float p = valid ? expf(sc - m_new) : 0.f;
-        lp = fmaf(lp, corr, r == 0 ? p : 0.f);
+        const float m_new = fmaxf(m, groups_max<CH>(smax));
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);
+        float ps = 0.f;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
+        for (int e = 0; e < 8; ++e) o[e] *= corr;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const float p = valid[i] ? __builtin_amdgcn_exp2f(sc[i] - m_new) : 0.f;
+            ps += p;
             const uint32_t w4[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const float2 vf = h2f2(w4[t]);
-                o[8 * i + 2 * t] = fmaf(p, vf.x, o[8 * i + 2 * t] * corr);
-                o[8 * i + 2 * t + 1] = fmaf(p, vf.y, o[8 * i + 2 * t + 1] * corr);
+                o[2 * t] = fmaf(p, vf.x, o[2 * t]);
+                o[2 * t + 1] = fmaf(p, vf.y, o[2 * t + 1]);
             }
         }
+        lp = fmaf(lp, corr, ps);
         m = m_new;
     };
-    // Three steps of rows in flight per wave (a ring of three register sets): a
-    // step's arithmetic is shorter than a round trip to memory.
-    const uint32_t base0 = t0 + 16u * (uint32_t)wave;   // wave-uniform
-    const uint32_t key0 = base0 + (uint32_t)j;
-    uint4 k0[NI], v0[NI], k1[NI], v1[NI], k2[NI], v2[NI];
+    const uint32_t base0 = t0 + STEPW * (uint32_t)wave;   // wave-uniform
+    if (fixed) {
+        // Rows past the position may hold anything; 0 * inf would not be 0.
 #pragma unroll
-    for (int i = 0; i < NI; ++i) k1[i] = v1[i] = k2[i] = v2[i] = make_uint4(0u, 0u, 0u, 0u);
-    fetch(key0, k0, v0);
-    if (base0 + STEP < t1) fetch(key0 + STEP, k1, v1);
-    if (base0 + 2u * STEP < t1) fetch(key0 + 2u * STEP, k2, v2);
+        for (int i = 0; i < NL; ++i)
+            if (base0 + KPI * i + g >= t1) v0[i] = make_uint4(0u, 0u, 0u, 0u);
+    } else {
+        fetch(base0, t1 - 1u, k0, v0);
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) k1[i] = v1[i] = k2[i] = v2[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (base0 + STEP < t1) fetch(base0 + STEP, t1 - 1u, k1, v1);
+    if (base0 + 2u * STEP < t1) fetch(base0 + 2u * STEP, t1 - 1u, k2, v2);
     for (uint32_t b = base0; b < t1; b += 3u * STEP) {
         step(b, k0, v0);
-        if (b + 3u * STEP < t1) fetch(key0 + (b - base0) + 3u * STEP, k0, v0);
+        if (b + 3u * STEP < t1) fetch(b + 3u * STEP, t1 - 1u, k0, v0);
         if (b + STEP >= t1) break;
         step(b + STEP, k1, v1);
-        if (b + 4u * STEP < t1) fetch(key0 + (b - base0) + 4u * STEP, k1, v1);
+        if (b + 4u * STEP < t1) fetch(b + 4u * STEP, t1 - 1u, k1, v1);
         if (b + 2u * STEP >= t1) break;
         step(b + 2u * STEP, k2, v2);
-        if (b + 5u * STEP < t1) fetch(key0 + (b - base0) + 5u * STEP, k2, v2);
+        if (b + 5u * STEP < t1) fetch(b + 5u * STEP, t1 - 1u, k2, v2);
     }
-    // A wave with no key (slice shorter than 16 w + 1) keeps m = -FLT_MAX, lp = 0, o = 0.
-    // Sum over the 16 key slots of each quarter (lanes r + 4j): rotations by 4
-    // and 8 inside each 16-lane row (DPP), then the rows pairwise by the gfx950
-    // lane swaps (v_permlane16_swap: rows 0 <-> 1 and 2 <-> 3; v_permlane32_swap:
-    // the two halves), whose two results summed are the pair's sum in every lane.
+    // A wave with no key keeps m = -FLT_MAX, lp = 0, o = 0. Every lane of a
+    // group holds the group's sum of p; each group is counted once.
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-        float v = o[i];
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf,
-                                                                   false));   // row_ror:4
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf,
-                                                                   false));   // row_ror:8
-        const uint32_t u = __builtin_bit_cast(uint32_t, v);
-        const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        v = __builtin_bit_cast(float, (uint32_t)p16[0]) + __builtin_bit_cast(float, (uint32_t)p16[1]);
-        const uint32_t u2 = __builtin_bit_cast(uint32_t, v);
-        const auto p32 = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
-        o[i] = __builtin_bit_cast(float, (uint32_t)p32[0]) + __builtin_bit_cast(float, (uint32_t)p32[1]);
+    for (int e = 0; e < 8; ++e) o[e] = groups_sum<CH>(o[e]);
+    const float lw = groups_sum<CH>(lp);
+    if (g == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) osh[wave][8 * c + e] = o[e];
     }
-    if (j == 0) {
-#pragma unroll
-        for (int i = 0; i < R; i += 8)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) osh[wave][8 * (r + 4 * (i >> 3)) + e] = o[i + e];
-    }
-    const float lw = wave_sum_dpp(lp);
     if (lane == 0) {
         wm[wave] = m;
         wl[wave] = lw;
@@ -386,7 +435,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
     float sw[NW], ll = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        sw[w] = wl[w] > 0.f ? expf(wm[w] - mm) : 0.f;
+        sw[w] = wl[w] > 0.f ? __builtin_amdgcn_exp2f(wm[w] - mm) : 0.f;
         ll = fmaf(wl[w], sw[w], ll);
     }
     float *rec = part_rec<HD>(a, h, s);
@@ -397,7 +446,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_stream(AttnArgs a) {
         rec[4 + tid] = acc;
     }
     if (tid == 0) {
-        rec[0] = mm;
+        rec[0] = mm * 0.6931471805599453f;   // natural-log units
         rec[1] = ll;
     }
 }
@@ -573,23 +622,26 @@ int launch_attn_partials(hipStream_t s, const AttnLaunch &l) {
 int launch_attn_stream(hipStream_t s, const AttnLaunch &l, uint32_t waves) {
     VX_CHECK(attn_validate(l));
     if (waves != 4u && waves != 8u) return fail(VX_ERR_INVALID_ARG, "stream attention runs 4 or 8 waves");
+    // k_attn_rows addresses a layer's rows by 32-bit byte offsets and 24-bit products.
+    if (l.context >= (1u << 24) || (uint64_t)l.context * l.kv_heads * l.head_dim * 2u >= (1ull << 32))
+        return fail(VX_ERR_UNSUPPORTED, "stream attention: a layer's K (or V) rows must span under 4 GiB");
     AttnArgs a = attn_args(l);
     dim3 grid(l.splits, l.q_heads);
     const bool eight = waves == 8u;
     VX_SET_STAMPS(a, ST_ATTN_STREAM, (uint64_t)l.splits * l.q_heads * waves);
     if (l.head_dim == 128) {
-        if (eight) k_attn_stream<128, 8><<<grid, 512, 0, s>>>(a);
-        else k_attn_stream<128, 4><<<grid, 256, 0, s>>>(a);
+        if (eight) k_attn_rows<128, 8><<<grid, 512, 0, s>>>(a);
+        else k_attn_rows<128, 4><<<grid, 256, 0, s>>>(a);
     } else {
-        if (eight) k_attn_stream<64, 8><<<grid, 512, 0, s>>>(a);
-        else k_attn_stream<64, 4><<<grid, 256, 0, s>>>(a);
+        if (eight) k_attn_rows<64, 8><<<grid, 512, 0, s>>>(a);
+        else k_attn_rows<64, 4><<<grid, 256, 0, s>>>(a);
     }
-    VX_LAUNCHED("k_attn_stream");
+    VX_LAUNCHED("k_attn_rows");
     return VX_OK;
 }
 
-int launch_attn_decode(hipStream_t s, const AttnLaunch &l) {
-    VX_CHECK(launch_attn_partials(s, l));
+int launch_attn_combine(hipStream_t s, const AttnLaunch &l) {
+    VX_CHECK(attn_validate(l));
     const AttnArgs a = attn_args(l);
     if (l.head_dim == 128)
         k_attn_combine<128><<<l.q_heads, kCombineThreads, 0, s>>>(a);
@@ -597,6 +649,11 @@ int launch_attn_decode(hipStream_t s, const AttnLaunch &l) {
         k_attn_combine<64><<<l.q_heads, kCombineThreads, 0, s>>>(a);
     VX_LAUNCHED("k_attn_combine");
     return VX_OK;
+}
+
+int launch_attn_decode(hipStream_t s, const AttnLaunch &l) {
+    VX_CHECK(launch_attn_partials(s, l));
+    return launch_attn_combine(s, l);
 }
 
 int launch_attn_scores(hipStream_t s, const float *q, const __half *kc, float *scores, uint32_t layer,

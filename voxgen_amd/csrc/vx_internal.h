@@ -307,10 +307,12 @@ struct AttnOutLaunch {
 int launch_attn_out(hipStream_t s, const AttnOutLaunch &a);
 // Partials only (k_attn_chunk), and partials + per-head merge (k_attn_combine).
 int launch_attn_partials(hipStream_t s, const AttnLaunch &a);
-// The same partials from k_attn_stream (4 or 8 waves per slice): every wave
+// The same partials from k_attn_rows (4 or 8 waves per slice): every wave
 // streams its own keys with no barrier inside the key loop.
 int launch_attn_stream(hipStream_t s, const AttnLaunch &a, uint32_t waves);
 int launch_attn_decode(hipStream_t s, const AttnLaunch &a);
+// The per-head merge of the partial records alone (k_attn_combine) into a.out.
+int launch_attn_combine(hipStream_t s, const AttnLaunch &a);
 
 // Reference-granular kernels.
 int launch_rmsnorm(hipStream_t s, const float *x, float *y, const float *w, uint32_t n, float eps,
