@@ -295,18 +295,21 @@ __device__ __forceinline__ float groups_max(float v) {
 // streams its own keys with no LDS or barrier inside the key loop. A lane is
 // chunk c (8 dimensions) of key group g, CH = HD / 8 lanes per key, so one
 // 16-byte load instruction of the wave reads KPI = 64 / CH consecutive keys'
-// rows of the KV head whole (256 bytes each at head_dim 128). A wave step is NL load instructions of K and of V (16 keys
-// at head_dim 128), key base + KPI i + g in load i; scores are reduced over the
-// group's lanes (DPP) and kept in log2 units (exp2 on the hardware's v_exp_f32),
-// and the running max, the sum of p and the 8 accumulators per lane follow the
-// online softmax. Rows are addressed by 32-bit byte offsets from the layer's
-// (uniform) KV base. When a slice holds at most one step of keys whatever the
+// rows of the KV head whole (256 bytes each at head_dim 128). A wave step is NL
+// load instructions of K and of V (16 keys at head_dim 128), key base + KPI i + g
+// in load i; scores are reduced over the group's lanes (DPP) and kept in log2
+// units (exp2 on the hardware's v_exp_f32), and the sum of p and the 8
+// accumulators per lane follow the online softmax with a lazy reference max (it
+// moves only when a step's max exceeds it by more than 8 in log2 units). Rows
+// are addressed by 32-bit byte offsets from the layer's (uniform) KV base. When a slice holds at most one step of keys whatever the
 // position (attn_fixed_chunk <= STEP), the rows are requested before the position
 // is read, as in k_attn_chunk, and rows past the position enter with p = 0 and
 // zeroed V. After the loop the groups' accumulators meet by lane swaps, and the
-// NW waves meet once in LDS. Three steps of rows are in flight per wave. The
-// record's max is stored in natural-log units, like k_attn_chunk's.
-template <int HD, int NW>
+// NW waves meet once in LDS. DEPTH steps of rows are in flight per wave (3: five
+// and seven measured slower at 4113 and 8017 keys, 6.8 / 8.8 and 6.8 / 9.5 us
+// against 6.3 / 8.6). The record's max is stored in natural-log units, like
+// k_attn_chunk's.
+template <int HD, int NW, int DEPTH = 3>
 __global__ __launch_bounds__(64 * NW) void k_attn_rows(AttnArgs a) {
     VX_WAVE_STAMP(a.stamps);
     constexpr int CH = HD / 8;             // lanes per key
@@ -325,18 +328,30 @@ __global__ __launch_bounds__(64 * NW) void k_attn_rows(AttnArgs a) {
     const char *kb = reinterpret_cast<const char *>(a.kc + layer_off);
     const char *vb = reinterpret_cast<const char *>(a.vc + layer_off);
     const uint32_t lane_bytes = 16u * (uint32_t)c;
+    // A step whose keys all lie at or before `last` (the common case: wave-uniform)
+    // steps one offset by KPI rows per load; a step across `last` clamps each key.
+    const uint32_t load_stride = KPI * row_bytes;
     auto fetch = [&](uint32_t base, uint32_t last, uint4 *kw, uint4 *vw) {
+        if (base + STEPW - 1u <= last) {
+            uint32_t off = __umul24(base + g, row_bytes) + lane_bytes;
 #pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const uint32_t off = __umul24(min(base + KPI * i + g, last), row_bytes) + lane_bytes;
-            kw[i] = *reinterpret_cast<const uint4 *>(kb + off);
-            vw[i] = *reinterpret_cast<const uint4 *>(vb + off);
+            for (int i = 0; i < NL; ++i, off += load_stride) {
+                kw[i] = *reinterpret_cast<const uint4 *>(kb + off);
+                vw[i] = *reinterpret_cast<const uint4 *>(vb + off);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NL; ++i) {
+                const uint32_t off = __umul24(min(base + KPI * i + g, last), row_bytes) + lane_bytes;
+                kw[i] = *reinterpret_cast<const uint4 *>(kb + off);
+                vw[i] = *reinterpret_cast<const uint4 *>(vb + off);
+            }
         }
     };
     const uint32_t fc = attn_fixed_chunk(a.context, a.splits);
     const bool fixed = fc <= kAttnFixedChunk && fc <= STEP;   // one step per slice, position-independent
-    uint4 k0[NL], v0[NL], k1[NL], v1[NL], k2[NL], v2[NL];
-    if (fixed) fetch(s * fc + STEPW * (uint32_t)wave, a.context - 1u, k0, v0);
+    uint4 kr[DEPTH][NL], vr[DEPTH][NL];   // ring of DEPTH steps of rows in flight
+    if (fixed) fetch(s * fc + STEPW * (uint32_t)wave, a.context - 1u, kr[0], vr[0]);
     float qv[8];
     {
         const float4 q0 = *reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * c);
@@ -372,14 +387,20 @@ __global__ __launch_bounds__(64 * NW) void k_attn_rows(AttnArgs a) {
             sc[i] = valid[i] ? d * scale : -FLT_MAX;
             smax = fmaxf(smax, sc[i]);
         }
-        const float m_new = fmaxf(m, groups_max<CH>(smax));
-        const float corr = __builtin_amdgcn_exp2f(m - m_new);
+        // Lazy reference max (the same in every lane): it moves, and rescales the
+        // sums, only when a step's max exceeds it by more than 2^8 in p.
+        const float smax_all = groups_max<CH>(smax);
+        if (smax_all > m + 8.f) {
+            const float corr = __builtin_amdgcn_exp2f(m - smax_all);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] *= corr;
+            lp *= corr;
+            m = smax_all;
+        }
         float ps = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] *= corr;
-#pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const float p = valid[i] ? __builtin_amdgcn_exp2f(sc[i] - m_new) : 0.f;
+            const float p = valid[i] ? __builtin_amdgcn_exp2f(sc[i] - m) : 0.f;
             ps += p;
             const uint32_t w4[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
 #pragma unroll
@@ -389,31 +410,31 @@ __global__ __launch_bounds__(64 * NW) void k_attn_rows(AttnArgs a) {
                 o[2 * t + 1] = fmaf(p, vf.y, o[2 * t + 1]);
             }
         }
-        lp = fmaf(lp, corr, ps);
-        m = m_new;
+        lp += ps;
     };
     const uint32_t base0 = t0 + STEPW * (uint32_t)wave;   // wave-uniform
     if (fixed) {
         // Rows past the position may hold anything; 0 * inf would not be 0.
 #pragma unroll
         for (int i = 0; i < NL; ++i)
-            if (base0 + KPI * i + g >= t1) v0[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (base0 + KPI * i + g >= t1) vr[0][i] = make_uint4(0u, 0u, 0u, 0u);
     } else {
-        fetch(base0, t1 - 1u, k0, v0);
+        fetch(base0, t1 - 1u, kr[0], vr[0]);
     }
 #pragma unroll
-    for (int i = 0; i < NL; ++i) k1[i] = v1[i] = k2[i] = v2[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (base0 + STEP < t1) fetch(base0 + STEP, t1 - 1u, k1, v1);
-    if (base0 + 2u * STEP < t1) fetch(base0 + 2u * STEP, t1 - 1u, k2, v2);
-    for (uint32_t b = base0; b < t1; b += 3u * STEP) {
-        step(b, k0, v0);
-        if (b + 3u * STEP < t1) fetch(b + 3u * STEP, t1 - 1u, k0, v0);
-        if (b + STEP >= t1) break;
-        step(b + STEP, k1, v1);
-        if (b + 4u * STEP < t1) fetch(b + 4u * STEP, t1 - 1u, k1, v1);
-        if (b + 2u * STEP >= t1) break;
-        step(b + 2u * STEP, k2, v2);
-        if (b + 5u * STEP < t1) fetch(b + 5u * STEP, t1 - 1u, k2, v2);
+    for (int u = 1; u < DEPTH; ++u) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) kr[u][i] = vr[u][i] = make_uint4(0u, 0u, 0u, 0u);
+        if (base0 + u * STEP < t1) fetch(base0 + u * STEP, t1 - 1u, kr[u], vr[u]);
+    }
+    for (uint32_t b = base0; b < t1; b += DEPTH * STEP) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) {
+            const uint32_t bu = b + u * STEP;
+            if (bu >= t1) break;
+            step(bu, kr[u], vr[u]);
+            if (bu + DEPTH * STEP < t1) fetch(bu + DEPTH * STEP, t1 - 1u, kr[u], vr[u]);
+        }
     }
     // A wave with no key keeps m = -FLT_MAX, lp = 0, o = 0. Every lane of a
     // group holds the group's sum of p; each group is counted once.
