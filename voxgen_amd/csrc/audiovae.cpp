@@ -11,6 +11,7 @@
 //             3 residual units (dilation 1, 3, 9):
 //               snake -> depthwise k=7 dilated -> snake  k_vae_dwconv_fm
 //               x += 1x1 conv + bias                     k_gemm residual (or k_vae_linear_fm)
+//               (32 and 64 channels: both in one pass, k_vae_resunit_fm)
 //   head      snake -> conv k=7 to one channel -> tanh   k_vae_head_fm
 // Row j of the transposed convolution's output phases r = 0..s-1 is output time
 // s j + r, so the GEMM's [L][s Cout] output is the frame-major [s L][Cout] output.
@@ -225,6 +226,23 @@ int enqueue_decode(vx_audiovae *e, const float *in, uint32_t frames, float *wave
         ch = S.cout;
         for (const Res &R : S.res) {
             ProfSpan sp(ctx, "audiovae.residual");
+            VaeResUnitArgs u;
+            u.x = cur;
+            u.y = tmp;
+            u.a1 = R.a1;
+            u.dw = R.dw_w;
+            u.db = R.dw_b;
+            u.a2 = R.a2;
+            u.pw = R.pw_w;
+            u.pb = R.pw_b;
+            u.channels = ch;
+            u.length = len;
+            u.dilation = R.dilation;
+            if (vae_resunit_eligible(u)) {
+                VX_CHECK(launch_vae_resunit_fm(s, u));
+                std::swap(cur, tmp);
+                continue;
+            }
             VaeDwArgs d;
             d.x = cur;
             d.y = tmp;

@@ -163,6 +163,80 @@ __global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32
     }
 }
 
+// A residual unit of a narrow stage (C = 32 or 64 channels) in one pass: the
+// workgroup stages snake_a1(x) for TB = 4096 / C rows and their causal halo
+// (6 d rows) in LDS, computes the depthwise conv and snake_a2 into a second LDS
+// tile, then the 1x1 conv with each thread's weight row in registers (the tile's
+// row read as float4 broadcasts) plus bias and the residual x. Two launches and a
+// round trip of the intermediate through HBM become one; every staging load is
+// issued before the first is used. (At 128 channels the same pass, 93 KB of LDS
+// and 128 FMAs per output on one workgroup per CU, took 79.5 us against 27.3 for
+// the depthwise kernel plus the MFMA GEMM.)
+template <int C>
+__global__ __launch_bounds__(256) void k_vae_resunit_fm(VaeResUnitArgs a) {
+    static_assert(C == 32 || C == 64, "narrow stages only");
+    constexpr uint32_t TB = 4096u / C, kMaxHalo = 54u, K = 7u;
+    constexpr uint32_t NS = ((TB + kMaxHalo) * C + 255u) / 256u;
+    constexpr uint32_t G = 256u / C;   // row groups of the thread block
+    __shared__ __align__(16) float xs[(TB + kMaxHalo) * C];
+    __shared__ __align__(16) float hs[TB * C];
+    const uint32_t tid = threadIdx.x, t0 = blockIdx.x * TB, halo = 6u * a.dilation;
+    const uint32_t n_st = (TB + halo) * C;
+    const uint32_t c = tid % C;   // n_st, C are multiples of 256 / C, so idx % C == c
+    float xv[NS];
+#pragma unroll
+    for (uint32_t i = 0; i < NS; ++i) {
+        const uint32_t idx = tid + 256u * i;
+        const int ti = (int)(t0 + idx / C) - (int)halo;
+        xv[i] = idx < n_st && ti >= 0 && (uint32_t)ti < a.length ? a.x[(size_t)ti * C + c] : 0.f;
+    }
+    const float a1 = hf(a.a1[c]), a2 = hf(a.a2[c]), db = hf(a.db[c]);
+#pragma unroll
+    for (uint32_t i = 0; i < NS; ++i) {
+        const uint32_t idx = tid + 256u * i;
+        if (idx < n_st) xs[idx] = snake(xv[i], a1);   // snake(0) = 0: the padding stays zero
+    }
+    float wk[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) wk[k] = hf(a.dw[c * K + k]);
+    float pw[C];
+#pragma unroll
+    for (uint32_t j = 0; j < C; j += 8) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(a.pw + (size_t)c * C + j);
+        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const __half2 h = __builtin_bit_cast(__half2, uw[e]);
+            pw[j + 2 * e] = __low2float(h);
+            pw[j + 2 * e + 1] = __high2float(h);
+        }
+    }
+    const float pb = hf(a.pb[c]);
+    __syncthreads();
+    for (uint32_t r = tid / C; r < TB; r += G) {
+        float sum = db;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) sum += xs[(r + k * a.dilation) * C + c] * wk[k];
+        hs[r * C + c] = snake(sum, a2);
+    }
+    __syncthreads();
+    for (uint32_t r = tid / C; r < TB; r += G) {
+        const uint32_t t = t0 + r;
+        if (t >= a.length) break;
+        const float4 *h4 = reinterpret_cast<const float4 *>(hs + r * C);
+        float s0 = pb, s1 = 0.f;
+#pragma unroll
+        for (uint32_t j = 0; j < C / 4; ++j) {
+            const float4 v = h4[j];
+            s0 = fmaf(v.x, pw[4 * j], s0);
+            s1 = fmaf(v.y, pw[4 * j + 1], s1);
+            s0 = fmaf(v.z, pw[4 * j + 2], s0);
+            s1 = fmaf(v.w, pw[4 * j + 3], s1);
+        }
+        a.y[(size_t)t * C + c] = a.x[(size_t)t * C + c] + (s0 + s1);
+    }
+}
+
 // Input of a stride-s transposed convolution as a GEMM: row j of X2 is
 // [pre(x[j]) | pre(x[j-1])] (zeros for j = 0), pre = snake(alpha)(x * scale + bias)
 // with the per-channel scale/bias of the sample-rate bucket.
@@ -365,6 +439,27 @@ int launch_vae_dwconv_fm(hipStream_t s, const VaeDwArgs &a) {
     }
     k_vae_dwconv_fm<<<grid1(n), 256, 0, s>>>(a);
     VX_LAUNCHED("k_vae_dwconv_fm");
+    return VX_OK;
+}
+
+bool vae_resunit_eligible(const VaeResUnitArgs &a) {
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.pw) | reinterpret_cast<uintptr_t>(a.x) |
+                           reinterpret_cast<uintptr_t>(a.y)) & 15u) == 0;
+    return (a.channels == 32u || a.channels == 64u) && a.dilation >= 1u &&
+           6u * a.dilation <= 54u && aligned && a.x != a.y;
+}
+
+int launch_vae_resunit_fm(hipStream_t s, const VaeResUnitArgs &a) {
+    if (!a.length) return VX_OK;
+    if (!vae_resunit_eligible(a)) return fail(VX_ERR_UNSUPPORTED, "vae residual unit: %u channels, dilation %u",
+                                              a.channels, a.dilation);
+    const uint32_t tb = 4096u / a.channels;
+    const uint32_t grid = (a.length + tb - 1u) / tb;
+    if (a.channels == 32u)
+        k_vae_resunit_fm<32><<<grid, 256, 0, s>>>(a);
+    else
+        k_vae_resunit_fm<64><<<grid, 256, 0, s>>>(a);
+    VX_LAUNCHED("k_vae_resunit_fm");
     return VX_OK;
 }
 

@@ -576,6 +576,17 @@ struct VaeDwArgs {                  // depthwise conv over frame-major rows
     uint32_t channels = 0, length = 0, kernel = 7, dilation = 1, left_pad = 0;
 };
 int launch_vae_dwconv_fm(hipStream_t s, const VaeDwArgs &a);
+// A decoder residual unit in one pass for 32 or 64 channels:
+//   y[t][n] = x[t][n] + pb[n] + sum_c pw[n][c] snake_a2(db[c] + sum_k dw[c][k] snake_a1(x[t + k d - 6d][c]))
+// (the depthwise conv, kernel 7, causal, and the 1x1 conv). y must not alias x.
+struct VaeResUnitArgs {
+    const float *x = nullptr;
+    float *y = nullptr;
+    const __half *a1 = nullptr, *dw = nullptr, *db = nullptr, *a2 = nullptr, *pw = nullptr, *pb = nullptr;
+    uint32_t channels = 0, length = 0, dilation = 1;
+};
+bool vae_resunit_eligible(const VaeResUnitArgs &a);
+int launch_vae_resunit_fm(hipStream_t s, const VaeResUnitArgs &a);
 struct VaeConvtInArgs {             // [pre(x[j]) | pre(x[j-1])] rows for the transposed-conv GEMM
     const float *x = nullptr;
     float *x2 = nullptr;
