@@ -24,6 +24,13 @@ __device__ __forceinline__ float snake(float x, float a) {
     const float s = sinf(a * x);
     return x + (s * s) / (a + 1e-9f);
 }
+// The decode engine's snake with the channel's 1 / (a + 1e-9) computed once.
+__device__ __forceinline__ float snake_inv(float a) { return 1.0f / (a + 1e-9f); }
+// (The native __sinf measured no faster here: 0.72 against 0.69 ms per decode.)
+__device__ __forceinline__ float snake_fm(float x, float a, float inv) {
+    const float s = sinf(a * x);
+    return fmaf(s * s, inv, x);
+}
 
 // ------------------------------------------------------------ channel-major
 __global__ __launch_bounds__(256) void k_vae_conv1d_cm(VaeConvArgs a) {
@@ -140,6 +147,7 @@ __global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32
     }
     const float ain = a.alpha_in && cval ? hf(a.alpha_in[c]) : 0.f;
     const float aout = a.alpha_out && cval ? hf(a.alpha_out[c]) : 0.f;
+    const float iin = snake_inv(ain), iout = snake_inv(aout);
     const float bias = cval ? hf(a.b[c]) : 0.f;
     float wk[KMAX];
 #pragma unroll
@@ -147,7 +155,7 @@ __global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32
 #pragma unroll
     for (uint32_t i = 0; i < NS; ++i) {
         const uint32_t idx = tid + 256u * i;
-        if (idx < n_st) xs[idx] = a.alpha_in ? snake(xv[i], ain) : xv[i];
+        if (idx < n_st) xs[idx] = a.alpha_in ? snake_fm(xv[i], ain, iin) : xv[i];
     }
     __syncthreads();
 #pragma unroll
@@ -158,7 +166,7 @@ __global__ __launch_bounds__(256) void k_vae_dwconv_tiled_fm(VaeDwArgs a, uint32
 #pragma unroll
         for (int k = 0; k < KMAX; ++k)
             if ((uint32_t)k < a.kernel) sum += xs[((r + k * a.dilation) << cb_shift) + cc] * wk[k];
-        if (a.alpha_out) sum = snake(sum, aout);
+        if (a.alpha_out) sum = snake_fm(sum, aout, iout);
         a.y[(size_t)t * C + c] = sum;
     }
 }
@@ -191,10 +199,11 @@ __global__ __launch_bounds__(256) void k_vae_resunit_fm(VaeResUnitArgs a) {
         xv[i] = idx < n_st && ti >= 0 && (uint32_t)ti < a.length ? a.x[(size_t)ti * C + c] : 0.f;
     }
     const float a1 = hf(a.a1[c]), a2 = hf(a.a2[c]), db = hf(a.db[c]);
+    const float i1 = snake_inv(a1), i2 = snake_inv(a2);
 #pragma unroll
     for (uint32_t i = 0; i < NS; ++i) {
         const uint32_t idx = tid + 256u * i;
-        if (idx < n_st) xs[idx] = snake(xv[i], a1);   // snake(0) = 0: the padding stays zero
+        if (idx < n_st) xs[idx] = snake_fm(xv[i], a1, i1);   // snake(0) = 0: the padding stays zero
     }
     float wk[K];
 #pragma unroll
@@ -217,7 +226,7 @@ __global__ __launch_bounds__(256) void k_vae_resunit_fm(VaeResUnitArgs a) {
         float sum = db;
 #pragma unroll
         for (uint32_t k = 0; k < K; ++k) sum += xs[(r + k * a.dilation) * C + c] * wk[k];
-        hs[r * C + c] = snake(sum, a2);
+        hs[r * C + c] = snake_fm(sum, a2, i2);
     }
     __syncthreads();
     for (uint32_t r = tid / C; r < TB; r += G) {
@@ -250,7 +259,8 @@ __global__ __launch_bounds__(256) void k_vae_convt_input_fm(VaeConvtInArgs a) {
     if (j >= tap) {
         const float x = a.x[(size_t)(j - tap) * C + c];
         const float pre = a.scale ? x * hf(a.scale[c]) + hf(a.bias[c]) : x;
-        v = snake(pre, hf(a.alpha[c]));
+        const float al = hf(a.alpha[c]);
+        v = snake_fm(pre, al, snake_inv(al));
     }
     a.x2[i] = v;
 }
@@ -366,7 +376,8 @@ __global__ __launch_bounds__(256) void k_vae_head_tiled_fm(VaeHeadArgs a) {
     for (uint32_t idx = threadIdx.x; idx < (256u + halo) * C; idx += 256u) {
         const uint32_t r = idx / C, c = idx - r * C;
         const int ti = (int)(t0 + r) - (int)halo;
-        xs[r * S + c] = ti >= 0 && (uint32_t)ti < a.length ? snake(a.x[(size_t)ti * C + c], hf(a.alpha[c])) : 0.f;
+        const float al = hf(a.alpha[c]);
+        xs[r * S + c] = ti >= 0 && (uint32_t)ti < a.length ? snake_fm(a.x[(size_t)ti * C + c], al, snake_inv(al)) : 0.f;
     }
     __syncthreads();
     const uint32_t t = t0 + threadIdx.x;
