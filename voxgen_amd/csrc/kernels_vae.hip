@@ -369,22 +369,47 @@ __global__ __launch_bounds__(256) void k_vae_head_fm(VaeHeadArgs a) {
 }
 
 // The head tiled over 256 output rows: snake(x) of the rows and the left halo
-// staged once in LDS (row stride C + 1), C <= 48.
+// staged once in LDS (row stride C + 1), C <= 48, with the conv weights in LDS.
+// For the decoder's 32 output channels (NC = 32) every staging load is issued
+// before the first is used; NC = 0 takes any C with a plain staging loop.
+template <uint32_t NC>
 __global__ __launch_bounds__(256) void k_vae_head_tiled_fm(VaeHeadArgs a) {
     __shared__ float xs[(256 + 6) * 49];
-    const uint32_t C = a.channels, S = C + 1u, t0 = blockIdx.x * 256u, halo = a.left_pad;
-    for (uint32_t idx = threadIdx.x; idx < (256u + halo) * C; idx += 256u) {
-        const uint32_t r = idx / C, c = idx - r * C;
-        const int ti = (int)(t0 + r) - (int)halo;
-        const float al = hf(a.alpha[c]);
-        xs[r * S + c] = ti >= 0 && (uint32_t)ti < a.length ? snake_fm(a.x[(size_t)ti * C + c], al, snake_inv(al)) : 0.f;
+    __shared__ float ws[48 * 7];
+    const uint32_t C = NC ? NC : a.channels, S = C + 1u, t0 = blockIdx.x * 256u, halo = a.left_pad;
+    const uint32_t n_st = (256u + halo) * C, tid = threadIdx.x;
+    for (uint32_t i = tid; i < C * a.kernel; i += 256u) ws[i] = hf(a.w[i]);
+    if constexpr (NC != 0) {
+        constexpr uint32_t NS = ((256u + 6u) * NC + 255u) / 256u;
+        float xv[NS];
+#pragma unroll
+        for (uint32_t i = 0; i < NS; ++i) {
+            const uint32_t idx = tid + 256u * i, r = idx / NC, c = idx % NC;
+            const int ti = (int)(t0 + r) - (int)halo;
+            xv[i] = idx < n_st && ti >= 0 && (uint32_t)ti < a.length ? a.x[(size_t)ti * NC + c] : 0.f;
+        }
+        const uint32_t c = tid % NC;   // NC divides 256: each thread keeps one channel
+        const float al = hf(a.alpha[c]), inv = snake_inv(al);
+#pragma unroll
+        for (uint32_t i = 0; i < NS; ++i) {
+            const uint32_t idx = tid + 256u * i;
+            if (idx < n_st) xs[(idx / NC) * S + c] = snake_fm(xv[i], al, inv);   // snake(0) = 0
+        }
+    } else {
+        for (uint32_t idx = tid; idx < n_st; idx += 256u) {
+            const uint32_t r = idx / C, c = idx - r * C;
+            const int ti = (int)(t0 + r) - (int)halo;
+            const float al = hf(a.alpha[c]);
+            xs[r * S + c] = ti >= 0 && (uint32_t)ti < a.length ? snake_fm(a.x[(size_t)ti * C + c], al, snake_inv(al))
+                                                               : 0.f;
+        }
     }
     __syncthreads();
-    const uint32_t t = t0 + threadIdx.x;
+    const uint32_t t = t0 + tid;
     if (t >= a.length) return;
     float sum = hf(a.b[0]);
     for (uint32_t c = 0; c < C; ++c)
-        for (uint32_t k = 0; k < a.kernel; ++k) sum += xs[(threadIdx.x + k) * S + c] * hf(a.w[c * a.kernel + k]);
+        for (uint32_t k = 0; k < a.kernel; ++k) sum += xs[(tid + k) * S + c] * ws[c * a.kernel + k];
     a.y[t] = tanhf(sum);
 }
 
@@ -514,7 +539,10 @@ int launch_vae_linear_fm(hipStream_t s, const VaeLinearArgs &a) {
 int launch_vae_head_fm(hipStream_t s, const VaeHeadArgs &a) {
     if (!a.length) return VX_OK;
     if (a.channels <= 48u && a.left_pad <= 6u && a.kernel == a.left_pad + 1u) {
-        k_vae_head_tiled_fm<<<grid1(a.length), 256, 0, s>>>(a);
+        if (a.channels == 32u)
+            k_vae_head_tiled_fm<32><<<grid1(a.length), 256, 0, s>>>(a);
+        else
+            k_vae_head_tiled_fm<0><<<grid1(a.length), 256, 0, s>>>(a);
         VX_LAUNCHED("k_vae_head_tiled_fm");
         return VX_OK;
     }
