@@ -40,7 +40,8 @@ Prints one JSON line with:
 
 `--copy-calibration` instead runs one plain copy kernel of known size (the
 reference point for the FETCH_SIZE / WRITE_SIZE counters); `--timeline` the
-graph-mode per-kernel timeline of a -DVX_STAMPS build.
+graph-mode per-kernel timelines of a -DVX_STAMPS build (the decode step, and the
+LocDiT CFM solve).
 """
 from __future__ import annotations
 
@@ -568,8 +569,72 @@ def timeline_leg(steps=12):
             ", ".join(f"{k} {v['span_us']} (+{v['gap_before_us']})" for k, v in summ["kernels"].items()))
         eng.close()
     model.free()
+    report["cfm_locdit8"] = cfm_timeline(ctx, 1e6 / hz)
     ctx.close()
     return report
+
+
+CFM_LAYER_KERNELS = ("qkv", "attention_oproj", "rmsnorm_ffn", "gate_up", "down", "rmsnorm_next")
+CFM_LAYER_KINDS = (7, 8, 9, 7, 7, 9)   # k_gemm_sk, k_dense_attn_fused (O projection), k_seq_rmsnorm4
+
+
+def cfm_timeline(ctx, tick_us, solves=8):
+    """The LocDiT CFM solve graph at cfm_leg's shape and options, from the same
+    -DVX_STAMPS library: per stamped kernel of a layer (the short-batch GEMMs, the
+    fused attention with the O projection, the residual rmsnorms), the mean over
+    the solve's 72 layer passes and `solves` samples (each the last of four
+    back-to-back solves) of its span, the gap after the previous stamped kernel,
+    and the mean wave life."""
+    from voxgen_amd import synth
+    from voxgen_amd.locdit import CfmOptions, LocDit
+    from voxgen_amd.runtime import Model
+    cfg = synth.locdit_config(layers=8, q_heads=16, kv_heads=16, head_dim=64, n_mu=0, n_cond=32, cond_raw=1,
+                              uncond_zero_cond=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0014)
+    model = Model(ctx, m.data, m.tensors)
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    cond = synth.normal_f32(32 * 1024, 0x5EED0015)
+    launches0, _ = read_timeline(ctx)
+    loc.cfm_solve(cond, None, CfmOptions(n_timesteps=10, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0,
+                                         seed=42, use_cfg_zero_star=True))   # captures the solve's graph
+    launches, _ = read_timeline(ctx)
+    first, count = len(launches0), len(launches) - len(launches0)
+    acc = {k: [] for k in CFM_LAYER_KERNELS}
+    walls = []
+    for i in range(solves):
+        time.sleep(0.02)
+        t0 = time.perf_counter()
+        for j in range(4):
+            loc.cfm_solve(cond, None, CfmOptions(seed=43 + 4 * i + j))
+        walls.append((time.perf_counter() - t0) / 4)
+        launches, ticks = read_timeline(ctx)
+        rows, _ = timeline_spans(launches, ticks, first, count)
+        seq, prev_end = [], None
+        for kind, st, en, life, nw in rows:
+            seq.append((kind, en - st, st - prev_end if prev_end is not None else np.nan, life, nw))
+            prev_end = en
+        j = 0
+        while j + len(CFM_LAYER_KINDS) <= len(seq):
+            if tuple(r[0] for r in seq[j:j + len(CFM_LAYER_KINDS)]) == CFM_LAYER_KINDS:
+                for q, name in enumerate(CFM_LAYER_KERNELS):
+                    acc[name].append(seq[j + q][1:])
+                j += len(CFM_LAYER_KINDS)
+            else:
+                j += 1
+    loc.close()
+    model.free()
+    out = {}
+    for name, v in acc.items():
+        v = np.array(v, float)
+        out[name] = {"span_us": round(float(v[:, 0].mean()) * tick_us, 3),
+                     "gap_before_us": round(float(np.nanmean(v[:, 1])) * tick_us, 3),
+                     "wave_life_us": round(float(v[:, 2].mean()) * tick_us, 3), "waves": int(v[0, 3]),
+                     "layer_passes": len(v)}
+    period = sum(k["span_us"] + k["gap_before_us"] for k in out.values())
+    summ = {"kernels": out, "layer_period_us": round(period, 3), "host_ms_per_solve": round(float(np.median(walls)) * 1e3, 4)}
+    log(f"timeline cfm_locdit8: layer period {summ['layer_period_us']} us, host {summ['host_ms_per_solve']} ms/solve; " +
+        ", ".join(f"{k} {v['span_us']} (+{v['gap_before_us']})" for k, v in out.items()))
+    return summ
 
 
 def residual_leg(ctx, steps, warmup=8, baselm=None, bcfg=None, prefix=384, cpu_steps=0):

@@ -427,6 +427,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm(SeqNormArgs a) {
 // h + scale * (b0 + b1 + ...) as k_seq_rmsnorm.
 template <int NV, int MAXB>   // MAXB: branches the registers hold (>= a.nbranch)
 __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     __shared__ float red[4];
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     float *h = a.h + (size_t)t * a.ldh;
@@ -985,6 +986,7 @@ typedef float of4 __attribute__((ext_vector_type(4)));
 // The weight blocks are requested before the attention starts.
 template <int HD, int NSLAB = 1, bool OPROJ = false>   // HD: head_dim when known at compile time, 0: a.head_dim
 __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     extern __shared__ __align__(16) float sm[];
     constexpr uint32_t ROWS = OPROJ ? kOprojRows : kDenseFusedRows;
     // Rows of a compile-time head_dim are padded to a multiple of four floats
@@ -1356,11 +1358,13 @@ int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens) {
                      (!a.y || a.ldy % 4u == 0) && (!a.yh || a.tiled || a.ldp % 4u == 0);
     if (vec) {
         const bool wide = a.branch && a.nbranch > 8u;
+        SeqNormArgs b = a;
+        VX_SET_STAMPS(b, ST_SEQ_NORM, (uint64_t)tokens * 4u);
         switch (a.n / 1024u) {
-            case 1: wide ? k_seq_rmsnorm4<1, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<1, 8><<<tokens, 256, 0, s>>>(a); break;
-            case 2: wide ? k_seq_rmsnorm4<2, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<2, 8><<<tokens, 256, 0, s>>>(a); break;
-            case 3: wide ? k_seq_rmsnorm4<3, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<3, 8><<<tokens, 256, 0, s>>>(a); break;
-            default: wide ? k_seq_rmsnorm4<4, 16><<<tokens, 256, 0, s>>>(a) : k_seq_rmsnorm4<4, 8><<<tokens, 256, 0, s>>>(a); break;
+            case 1: wide ? k_seq_rmsnorm4<1, 16><<<tokens, 256, 0, s>>>(b) : k_seq_rmsnorm4<1, 8><<<tokens, 256, 0, s>>>(b); break;
+            case 2: wide ? k_seq_rmsnorm4<2, 16><<<tokens, 256, 0, s>>>(b) : k_seq_rmsnorm4<2, 8><<<tokens, 256, 0, s>>>(b); break;
+            case 3: wide ? k_seq_rmsnorm4<3, 16><<<tokens, 256, 0, s>>>(b) : k_seq_rmsnorm4<3, 8><<<tokens, 256, 0, s>>>(b); break;
+            default: wide ? k_seq_rmsnorm4<4, 16><<<tokens, 256, 0, s>>>(b) : k_seq_rmsnorm4<4, 8><<<tokens, 256, 0, s>>>(b); break;
         }
         VX_LAUNCHED("k_seq_rmsnorm4");
         return VX_OK;
@@ -1488,6 +1492,7 @@ int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a) {
     b.nsplit = nsplit;
     const uint64_t lds = dense_fused_lds_rows(a.tokens, a.head_dim, kOprojRows);
     const dim3 grid(a.q_heads, a.batch, ngroups * nsplit);
+    VX_SET_STAMPS(b, ST_DENSE_ATTN, (uint64_t)grid.x * grid.y * grid.z * 4u);
     if (a.head_dim == 64u && a.nslab == 2)
         k_dense_attn_fused<64, 2, true><<<grid, 256, (size_t)lds, s>>>(b);
     else if (a.head_dim == 128u && a.nslab == 2)

@@ -62,6 +62,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // Grid: a.ntn row tiles x a.ksplit k-slabs, 256 threads.
 template <int MT, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
+    VX_WAVE_STAMP(a.stamps);
     // Partial tiles of the four waves: [wave][mt][fragment][lane] x 4 floats.
     __shared__ f4 red[4][MT][2][64];
     const uint32_t tile = blockIdx.x % a.ntn, ks = blockIdx.x / a.ntn;
@@ -251,6 +252,7 @@ int launch_gemm_skinny(hipStream_t s, GemmArgs a) {
     const uint64_t grid = (uint64_t)tiles * a.ksplit;
     if (grid == 0) return VX_OK;
     if (grid > 0x7fffffffull) return fail(VX_ERR_UNSUPPORTED, "skinny gemm: grid too large");
+    VX_SET_STAMPS(a, ST_GEMM_SK, grid * 4u);
     return a.epi == GEPI_SWIGLU ? launch_sk<GEPI_SWIGLU>(s, a, (uint32_t)grid)
                                 : launch_sk<GEPI_STORE>(s, a, (uint32_t)grid);
 }

@@ -52,6 +52,7 @@ void clear_error();
 #ifdef VX_STAMPS
 enum StampKind : uint32_t {
     ST_QKV = 1, ST_ATTN_CHUNK = 2, ST_ATTN_STREAM = 3, ST_ATTN_OUT = 4, ST_SWIGLU = 5, ST_MATVEC = 6,
+    ST_GEMM_SK = 7, ST_DENSE_ATTN = 8, ST_SEQ_NORM = 9,   // the LocDiT short-batch stack
 };
 // Slots for `waves` waves, or nullptr when no timeline is armed or it is full.
 uint64_t *stamp_slots(uint32_t kind, uint64_t waves);
@@ -396,6 +397,7 @@ struct GemmArgs {
     // [T][ldo]) with plain stores instead of atomic adds; the consumer sums them.
     uint32_t split_store = 0;
     uint32_t wide = 0;              // set by launch_gemm: plain-store epilogues may use 16-byte stores
+    VX_STAMP_FIELD
     // GEPI_SWIGLU on the prefill-layout kernel with tiled plane output: with
     // sk_grid set (a multiple of 8, normally the CU count) and a little more than
     // sk_grid tiles, the tiles' blocks are cut into sk_grid equal ranges, one
@@ -487,6 +489,7 @@ struct SeqNormArgs {
     // 1: zero the branch rows (every split) after reading them, so the buffer is the
     // cleared accumulator of the next split-K GEMM; the branch memory must be writable.
     uint32_t clear_branch = 0;
+    VX_STAMP_FIELD
 };
 constexpr uint32_t kSeqNormMaxBranch = 16;
 int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens);
@@ -702,6 +705,7 @@ struct DenseAttnArgs {
     float *oslab = nullptr;
     uint64_t oslab_stride = 0;
     uint32_t nsplit = 1;
+    VX_STAMP_FIELD
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
 // table[p][i] = (cos, sin)(p * theta^(-2i/head_dim) / factors[i]) * scaling for
