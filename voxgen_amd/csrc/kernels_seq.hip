@@ -431,9 +431,11 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     float *h = a.h + (size_t)t * a.ldh;
+    // Four consecutive columns from a multiple of 4 stay contiguous in frag32 order.
+    auto hat = [&](uint32_t c) { return a.h_frag ? a.h + frag32_index(t, c, a.n) : h + c; };
     float4 v[NV];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4 *>(h + 4u * (tid + 256u * j));
+    for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4 *>(hat(4u * (tid + 256u * j)));
     if (a.branch) {
         const float *br = a.branch + (size_t)t * a.ldb;
         float4 bv[NV][MAXB];
@@ -457,7 +459,7 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
                 }
             v[j] = make_float4(v[j].x + add.x * a.scale, v[j].y + add.y * a.scale, v[j].z + add.z * a.scale,
                                v[j].w + add.w * a.scale);
-            *reinterpret_cast<float4 *>(h + 4u * (tid + 256u * j)) = v[j];
+            *reinterpret_cast<float4 *>(hat(4u * (tid + 256u * j))) = v[j];
         }
         if (a.clear_branch)
             for (uint32_t b = 0; b < a.nbranch; ++b)
@@ -465,6 +467,10 @@ __global__ __launch_bounds__(256) void k_seq_rmsnorm4(SeqNormArgs a) {
                 for (int j = 0; j < NV; ++j)
                     *reinterpret_cast<float4 *>(const_cast<float *>(br) + (size_t)b * a.branch_stride +
                                                 4u * (tid + 256u * j)) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (a.hf) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) *reinterpret_cast<float4 *>(a.hf + frag32_index(t, 4u * (tid + 256u * j), a.n)) = v[j];
     }
     if (!a.w) return;   // residual update only
     float ss = 0.f;
@@ -984,7 +990,12 @@ typedef float of4 __attribute__((ext_vector_type(4)));
 // enters as hi/lo f16 planes against exact f16 weights, two
 // v_mfma_f32_16x16x32_f16 per 32 columns, the arithmetic of the short-batch GEMM.
 // The weight blocks are requested before the attention starts.
-template <int HD, int NSLAB = 1, bool OPROJ = false>   // HD: head_dim when known at compile time, 0: a.head_dim
+//
+// RES (with OPROJ): the residual-stream form. q, k and v are products of the
+// un-normalised rows, and the staging multiplies each row by its 1/rms (from the
+// K slabs' sums of squares in a.ssq); the projection is added to a.hres (the
+// residual stream, frag32_index order) with atomic adds instead of head slabs.
+template <int HD, int NSLAB = 1, bool OPROJ = false, bool RES = false>   // HD: head_dim when known at compile time, 0: a.head_dim
 __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     VX_WAVE_STAMP(a.stamps);
     extern __shared__ __align__(16) float sm[];
@@ -1042,12 +1053,19 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
             // Slab 0 into vv / x0 / x1, slab 1 (NSLAB == 2) into the *b arrays.
             constexpr uint32_t NVB = NSLAB > 1 ? NV : 1u, NKB = NSLAB > 1 ? NKQ : 1u;
             float4 vv[NV], x0[NKQ], x1[NKQ], c01[NKQ], c23[NKQ], vvb[NVB], x0b[NKB], x1b[NKB];
+            // RES: each staged row's sums of squares (one per K slab).
+            constexpr uint32_t NSV = RES ? NV : 1u, NSK = RES ? NKQ : 1u;
+            float sv[NSV][NSLAB], sk[NSK][NSLAB];
 #pragma unroll
             for (uint32_t j = 0; j < NV; ++j) {
                 const uint32_t i = min(tid + 256u * j, S * V4 - 1u), t = i / V4, c = i - t * V4;
                 const float *src = v + (size_t)t * a.v_stride + 4u * c;
                 vv[j] = *reinterpret_cast<const float4 *>(src);
                 if constexpr (NSLAB > 1) vvb[j] = *reinterpret_cast<const float4 *>(src + a.slab_stride);
+                if constexpr (RES) {
+#pragma unroll
+                    for (int sl = 0; sl < NSLAB; ++sl) sv[j][sl] = a.ssq[sl * a.ssq_stride + (size_t)bz * S + t];
+                }
             }
 #pragma unroll
             for (uint32_t j = 0; j < NKQ; ++j) {
@@ -1064,6 +1082,10 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
                 const float4 *cs = reinterpret_cast<const float4 *>(a.rope + (size_t)pos * H2 + 4u * c);
                 c01[j] = cs[0];
                 c23[j] = cs[1];
+                if constexpr (RES) {
+#pragma unroll
+                    for (int sl = 0; sl < NSLAB; ++sl) sk[j][sl] = a.ssq[sl * a.ssq_stride + (size_t)bz * S + pos];
+                }
             }
             if constexpr (NSLAB > 1) {
 #pragma unroll
@@ -1072,6 +1094,25 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
                 for (uint32_t j = 0; j < NKQ; ++j) {
                     x0[j] += x0b[j];
                     x1[j] += x1b[j];
+                }
+            }
+            if constexpr (RES) {   // rmsnorm.comp:36-38: 1/rms of the row, from its slabs' sums
+                auto inv_rms = [&](const float (&p)[NSLAB]) {
+                    float sum = p[0];
+#pragma unroll
+                    for (int sl = 1; sl < NSLAB; ++sl) sum += p[sl];
+                    return 1.0f / sqrtf(sum / (float)a.norm_n + a.eps);
+                };
+#pragma unroll
+                for (uint32_t j = 0; j < NV; ++j) {
+                    const float f = inv_rms(sv[j]);
+                    vv[j] = make_float4(vv[j].x * f, vv[j].y * f, vv[j].z * f, vv[j].w * f);
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < NKQ; ++j) {
+                    const float f = inv_rms(sk[j]);
+                    x0[j] = make_float4(x0[j].x * f, x0[j].y * f, x0[j].z * f, x0[j].w * f);
+                    x1[j] = make_float4(x1[j].x * f, x1[j].y * f, x1[j].z * f, x1[j].w * f);
                 }
             }
             if constexpr (OPROJ) {
@@ -1213,7 +1254,10 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
                 al[kb][e] = (_Float16)(z8[e] - (float)hv);
             }
         }
-        float *slab = a.oslab + (size_t)h * a.oslab_stride + ((size_t)bz * S + t0) * a.hidden;
+        float *slab = RES ? nullptr : a.oslab + (size_t)h * a.oslab_stride + ((size_t)bz * S + t0) * a.hidden;
+        // RES: the workgroup's [ROWS][W] product tile, past the attention's LDS.
+        float *ot = ps + ROWS * S;
+        const uint32_t W = (g1 - g0) * 16u;
         const uint32_t tq = 4u * (lane >> 4);
 #pragma unroll
         for (uint32_t i = 0; i < GPW; ++i) {
@@ -1230,7 +1274,23 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
             const uint32_t n = 16u * g + r;
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e)
-                if (tq + e < R) slab[(size_t)(tq + e) * a.hidden + n] = acc[e];
+                if (tq + e < R) {
+                    if constexpr (RES)
+                        ot[(tq + e) * W + (n - 16u * g0)] = acc[e];
+                    else
+                        slab[(size_t)(tq + e) * a.hidden + n] = acc[e];
+                }
+        }
+        if constexpr (RES) {
+            // Atomic adds in the stream's order: column groups of four, then rows,
+            // so consecutive threads add to consecutive addresses (a row step is
+            // four floats in frag32 order).
+            __syncthreads();
+            const uint32_t row0 = bz * S + t0;
+            for (uint32_t idx = tid; idx < W * ROWS; idx += 256u) {
+                const uint32_t e = idx & 3u, t = (idx >> 2) % ROWS, c = 4u * (idx / (4u * ROWS)) + e;
+                if (t < R) unsafeAtomicAdd(a.hres + frag32_index(row0 + t, 16u * g0 + c, a.hidden), ot[t * W + c]);
+            }
         }
         return;
     }
@@ -1287,6 +1347,14 @@ int launch_gemm(hipStream_t s, const GemmArgs &in) {
     if (a.wk == WT_Q8 ? (a.K % 1024u) : (a.K % (uint32_t)GK))
         return fail(VX_ERR_UNSUPPORTED, "gemm: K=%u must be a multiple of %u for this weight type", a.K,
                     a.wk == WT_Q8 ? 1024u : (uint32_t)GK);
+    if (a.frag && (a.xn || a.res_frag)) {   // the short-batch kernel's residual-stream forms
+        if (!gemm_skinny_eligible(a))
+            return fail(VX_ERR_UNSUPPORTED, "gemm: residual-stream operands need the short-batch kernel "
+                                            "(F16, T <= 128, aligned rows, K %% 32 == 0)");
+        for (uint32_t i = 0; i < a.nseg; ++i)
+            if (!a.seg[i].w) return fail(VX_ERR_INVALID_ARG, "gemm: segment %u weight pointers missing", i);
+        return launch_gemm_skinny(s, a);
+    }
     if (a.xf32 ? (!a.xf || (a.ldx % 4u)) : (!a.xh || !a.xl || (a.ldx % 8u)))
         return fail(VX_ERR_INVALID_ARG, "gemm: input rows must be 16-byte aligned");
     uint32_t tiles = 0;
@@ -1354,6 +1422,8 @@ int launch_seq_rmsnorm(hipStream_t s, const SeqNormArgs &a, uint32_t tokens) {
     if (a.yh && a.tiled && a.n % 32u) return fail(VX_ERR_INVALID_ARG, "seq rmsnorm: tiled planes need n %% 32");
     if (a.nbranch == 0 || a.nbranch > kSeqNormMaxBranch)
         return fail(VX_ERR_INVALID_ARG, "seq rmsnorm: 1..%u branches", kSeqNormMaxBranch);
+    if ((a.h_frag || a.hf) && (a.n % 1024u || a.n > 4096u || (a.h_frag && a.branch)))
+        return fail(VX_ERR_UNSUPPORTED, "seq rmsnorm: the frag32 residual stream needs n = 1024 * k <= 4096, no branch");
     const bool vec = a.n % 1024u == 0 && a.n <= 4096u && a.ldh % 4u == 0 && (!a.branch || (a.ldb % 4u == 0 && a.branch_stride % 4u == 0)) &&
                      (!a.y || a.ldy % 4u == 0) && (!a.yh || a.tiled || a.ldp % 4u == 0);
     if (vec) {
@@ -1473,7 +1543,12 @@ int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a) {
     if (!dense_attn_oproj_eligible(a.tokens, a.head_dim))
         return fail(VX_ERR_UNSUPPORTED, "attention + O projection: %u tokens x head_dim %u", a.tokens, a.head_dim);
     auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (!a.wo || !al16(a.wo) || !a.oslab || !a.hidden || a.hidden % 16u || a.oslab_stride < (uint64_t)a.batch * a.tokens * a.hidden)
+    const bool res = a.hres != nullptr;
+    if (res != (a.ssq != nullptr) || (res && (a.hidden % 32u || !a.norm_n)))
+        return fail(VX_ERR_INVALID_ARG, "attention + O projection: the residual-stream form needs hres, ssq, "
+                                        "norm_n and hidden %% 32 == 0");
+    if (!a.wo || !al16(a.wo) || !a.hidden || a.hidden % 16u ||
+        (!res && (!a.oslab || a.oslab_stride < (uint64_t)a.batch * a.tokens * a.hidden)))
         return fail(VX_ERR_INVALID_ARG, "attention + O projection: weights or slabs");
     if (!a.rope || a.q_stride % 4u || a.k_stride % 4u || a.v_stride % 4u || !al16(a.q) || !al16(a.k) || !al16(a.v) ||
         !al16(a.rope) || (a.nslab != 1 && a.nslab != 2) || (a.nslab == 2 && a.slab_stride % 4u))
@@ -1490,17 +1565,26 @@ int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a) {
     const uint32_t base = a.q_heads * a.batch * ngroups;
     while (base * nsplit < 128u && 2u * nsplit <= (ng + 3u) / 4u) nsplit *= 2u;
     b.nsplit = nsplit;
-    const uint64_t lds = dense_fused_lds_rows(a.tokens, a.head_dim, kOprojRows);
+    uint64_t lds = dense_fused_lds_rows(a.tokens, a.head_dim, kOprojRows);
+    if (res) {   // the product tile of the residual-stream form
+        lds += (uint64_t)kOprojRows * ((ng + nsplit - 1u) / nsplit) * 16u * 4u;
+        if (lds > 65536u) return fail(VX_ERR_UNSUPPORTED, "attention + O projection: residual tile exceeds LDS");
+    }
     const dim3 grid(a.q_heads, a.batch, ngroups * nsplit);
     VX_SET_STAMPS(b, ST_DENSE_ATTN, (uint64_t)grid.x * grid.y * grid.z * 4u);
-    if (a.head_dim == 64u && a.nslab == 2)
-        k_dense_attn_fused<64, 2, true><<<grid, 256, (size_t)lds, s>>>(b);
-    else if (a.head_dim == 128u && a.nslab == 2)
-        k_dense_attn_fused<128, 2, true><<<grid, 256, (size_t)lds, s>>>(b);
-    else if (a.head_dim == 64u)
-        k_dense_attn_fused<64, 1, true><<<grid, 256, (size_t)lds, s>>>(b);
-    else
-        k_dense_attn_fused<128, 1, true><<<grid, 256, (size_t)lds, s>>>(b);
+#define VX_OPROJ(HDV, NS, RS) k_dense_attn_fused<HDV, NS, true, RS><<<grid, 256, (size_t)lds, s>>>(b)
+    if (res) {
+        if (a.head_dim == 64u && a.nslab == 2) VX_OPROJ(64, 2, true);
+        else if (a.head_dim == 128u && a.nslab == 2) VX_OPROJ(128, 2, true);
+        else if (a.head_dim == 64u) VX_OPROJ(64, 1, true);
+        else VX_OPROJ(128, 1, true);
+    } else {
+        if (a.head_dim == 64u && a.nslab == 2) VX_OPROJ(64, 2, false);
+        else if (a.head_dim == 128u && a.nslab == 2) VX_OPROJ(128, 2, false);
+        else if (a.head_dim == 64u) VX_OPROJ(64, 1, false);
+        else VX_OPROJ(128, 1, false);
+    }
+#undef VX_OPROJ
     VX_LAUNCHED("k_dense_attn_fused");
     return VX_OK;
 }

@@ -26,6 +26,17 @@
 //   * split K across workgroups writes partial slabs with plain stores (slab s
 //     at out + s * ws_stride); the consumer sums them. No atomics and no
 //     cleared accumulators, so a captured graph replays it as is.
+//   * with GemmArgs::xn (XN) X is the residual stream itself, f32 in the same
+//     fragment order (frag32_index), and the rmsnorm in front of the projection
+//     is folded in: each lane multiplies its eight values by the norm weights and
+//     splits them to hi/lo f16 in registers, and accumulates their squares; the
+//     row sums of squares meet in LDS, and 1/rms scales the row's products
+//     (rmsnorm(x) w . W = (1/rms) ((x w) . W)), in the SwiGLU epilogue or, for a
+//     split projection, in its consumer (the slabs' sums of squares are stored).
+//   * with GemmArgs::res_frag the products are added to the residual stream with
+//     atomic adds (every K slab), in place of partial slabs and a reduction pass.
+#include <type_traits>
+
 #include "vx_internal.h"
 
 namespace vx {
@@ -56,15 +67,22 @@ struct SkOps {
     uint4 w[2];
     uint4 xh[MT], xl[MT];
 };
+template <int MT>
+struct SkOpsN {      // X from the f32 residual stream: 8 values per lane and token fragment
+    uint4 w[2];
+    float4 x[MT][2];
+    float4 nw[2];    // the lane's 8 norm weights
+};
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 // Grid: a.ntn row tiles x a.ksplit k-slabs, 256 threads.
-template <int MT, int EPI>
+template <int MT, int EPI, bool XN = false>
 __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     VX_WAVE_STAMP(a.stamps);
     // Partial tiles of the four waves: [wave][mt][fragment][lane] x 4 floats.
     __shared__ f4 red[4][MT][2][64];
+    __shared__ float ssl[XN ? 4 : 1][XN ? MT : 1][16];   // XN: each wave's row sums of squares
     const uint32_t tile = blockIdx.x % a.ntn, ks = blockIdx.x / a.ntn;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -108,23 +126,57 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     f4 acc[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
+    float ss[MT];   // XN: the lane's sum of squares per token fragment
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) ss[mt] = 0.f;
 
-    SkOps<MT> ring[kSkDepth];
-    auto load = [&](SkOps<MT> &o, int i) {
-        const uint32_t c = (s0 + wv + 4u * (uint32_t)i) << 9;   // block offset of the k-step
+    using Ops = typename std::conditional<XN, SkOpsN<MT>, SkOps<MT>>::type;
+    Ops ring[kSkDepth];
+    auto load = [&](Ops &o, int i) {
+        const uint32_t step = s0 + wv + 4u * (uint32_t)i;
+        const uint32_t c = step << 9;   // block offset of the k-step (halves of W; floats of xn)
         o.w[0] = ld_nt16(wr[0] + c);
         o.w[1] = ld_nt16(wr[1] + c);
+        if constexpr (XN) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            o.xh[mt] = *reinterpret_cast<const uint4 *>(xr[mt] + c);
-            o.xl[mt] = *reinterpret_cast<const uint4 *>(xr[mt] + lo + c);
+            for (int mt = 0; mt < MT; ++mt) {
+                const float *p = a.xn + ((size_t)mt * S << 9) + c + 4u * lane;
+                o.x[mt][0] = *reinterpret_cast<const float4 *>(p);
+                o.x[mt][1] = *reinterpret_cast<const float4 *>(p + 256);
+            }
+            const float *nw = a.xn_w + (step << 5) + 8u * (lane >> 4);
+            o.nw[0] = *reinterpret_cast<const float4 *>(nw);
+            o.nw[1] = *reinterpret_cast<const float4 *>(nw + 4);
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                o.xh[mt] = *reinterpret_cast<const uint4 *>(xr[mt] + c);
+                o.xl[mt] = *reinterpret_cast<const uint4 *>(xr[mt] + lo + c);
+            }
         }
     };
-    auto mma = [&](const SkOps<MT> &o) {
+    auto mma = [&](const Ops &o) {
         const h8 b0 = __builtin_bit_cast(h8, o.w[0]), b1 = __builtin_bit_cast(h8, o.w[1]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const h8 ah = __builtin_bit_cast(h8, o.xh[mt]), al = __builtin_bit_cast(h8, o.xl[mt]);
+            h8 ah, al;
+            if constexpr (XN) {
+                const float xv[8] = {o.x[mt][0].x, o.x[mt][0].y, o.x[mt][0].z, o.x[mt][0].w,
+                                     o.x[mt][1].x, o.x[mt][1].y, o.x[mt][1].z, o.x[mt][1].w};
+                const float wv8[8] = {o.nw[0].x, o.nw[0].y, o.nw[0].z, o.nw[0].w,
+                                      o.nw[1].x, o.nw[1].y, o.nw[1].z, o.nw[1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float y = xv[e] * wv8[e];
+                    const _Float16 hv = (_Float16)y;
+                    ah[e] = hv;
+                    al[e] = (_Float16)(y - (float)hv);
+                    ss[mt] = fmaf(xv[e], xv[e], ss[mt]);
+                }
+            } else {
+                ah = __builtin_bit_cast(h8, o.xh[mt]);
+                al = __builtin_bit_cast(h8, o.xl[mt]);
+            }
             acc[mt][0] = mfma16(ah, b0, acc[mt][0]);
             acc[mt][1] = mfma16(ah, b1, acc[mt][1]);
             acc[mt][0] = mfma16(al, b0, acc[mt][0]);
@@ -154,7 +206,22 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
         red[wv][mt][0][lane] = acc[mt][0];
         red[wv][mt][1][lane] = acc[mt][1];
     }
+    if constexpr (XN) {
+        // Lanes r, r + 16, r + 32, r + 48 hold row r's columns.
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            float v = ss[mt];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (lane < 16u) ssl[wv][mt][lane] = v;
+        }
+    }
     __syncthreads();
+    // XN: the workgroup's sum of squares of token tok (over its K range).
+    auto row_ss = [&](uint32_t tok) {
+        const uint32_t mt = tok >> 4, r = tok & 15u;
+        return (ssl[0][mt][r] + ssl[1][mt][r]) + (ssl[2][mt][r] + ssl[3][mt][r]);
+    };
     auto part = [&](uint32_t mt, uint32_t f, uint32_t tl, uint32_t n) {
         const uint32_t ln = n + 16u * ((tl >> 2) & 3u), r = tl & 3u;
         return red[0][mt][f][ln][r] + red[1][mt][f][ln][r] + red[2][mt][f][ln][r] + red[3][mt][f][ln][r];
@@ -164,7 +231,13 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
             const uint32_t n = o & 15u, tl = o >> 4, mt = tl >> 4;
             const uint32_t tok = tl, row = kSkPairs * tile + n;
             if (tok >= a.T || row >= a.seg[0].rows) continue;
-            const float v = silu_mul(part(mt, 0, tl & 15u, n), part(mt, 1, tl & 15u, n));
+            float g = part(mt, 0, tl & 15u, n), u = part(mt, 1, tl & 15u, n);
+            if constexpr (XN) {   // rmsnorm.comp:36-38 over the full row (no split K here)
+                const float inv = 1.0f / sqrtf(row_ss(tok) / (float)a.K + a.xn_eps);
+                g *= inv;
+                u *= inv;
+            }
+            const float v = silu_mul(g, u);
             if (a.seg[0].out) a.seg[0].out[(size_t)tok * a.seg[0].ldo + row] = v;
             if (a.oh) {
                 const size_t po = frag16_index(tok, row, a.seg[0].rows);
@@ -174,6 +247,26 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
             }
         }
     } else {
+        if constexpr (XN) {   // the K slab's sums of squares, once (the first row tile)
+            if (a.xn_ss && tile == 0u && tid < 16u * MT && tid < a.T) a.xn_ss[(size_t)ks * a.xn_ss_stride + tid] = row_ss(tid);
+        }
+        if (a.res_frag) {
+            // The tile's outputs are MT whole 2 KB blocks of the stream (32 columns
+            // of its rows, 16 tokens each): thread order = block order, so every
+            // wave's atomic adds cover 256 contiguous bytes.
+            for (uint32_t o = tid; o < 512u * MT; o += 256u) {
+                const uint32_t mt = o >> 9, w = o & 511u, li = (w >> 2) & 63u;
+                const uint32_t r = li & 15u, nl = 8u * (li >> 4) + 4u * (w >> 8) + (w & 3u);
+                const uint32_t tok = 16u * mt + r, row = kSkRows * (tile - sg.tile0) + nl;
+                if (tok >= a.T || row >= sg.rows) continue;
+                float v = part(mt, nl >> 4, r, nl & 15u);
+                if (sg.bias && ks == 0)
+                    v += sg.bias_dtype == 0 ? static_cast<const float *>(sg.bias)[row]
+                                            : __half2float(static_cast<const __half *>(sg.bias)[row]);
+                unsafeAtomicAdd(a.res_frag + frag32_index(tok, row, sg.rows), v * a.alpha);
+            }
+            return;
+        }
         float *out = sg.out + (a.ksplit > 1 ? (size_t)ks * a.ws_stride : 0);
         for (uint32_t o = tid; o < 512u * MT; o += 256u) {
             const uint32_t nl = o & 31u, tl = o >> 5, mt = tl >> 4;
@@ -188,13 +281,13 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     }
 }
 
-template <int EPI>
+template <int EPI, bool XN>
 int launch_sk(hipStream_t s, const GemmArgs &a, uint32_t grid) {
     const uint32_t mt = (a.T + 15u) / 16u;
     switch (mt) {
 #define VX_SK_CASE(M)                                  \
     case M:                                            \
-        k_gemm_sk<M, EPI><<<grid, 256, 0, s>>>(a);     \
+        k_gemm_sk<M, EPI, XN><<<grid, 256, 0, s>>>(a); \
         break;
         VX_SK_CASE(1)
         VX_SK_CASE(2)
@@ -225,11 +318,16 @@ __global__ __launch_bounds__(256) void k_repack_frag16(const __half *src, __half
 
 bool gemm_skinny_eligible(const GemmArgs &a) {
     if (!a.frag || a.wk != WT_F16 || a.xf32 || a.x_tiled || a.T == 0 || a.T > kSkMaxTokens || a.K % 32u) return false;
-    if (!a.xh || !a.xl || ((reinterpret_cast<uintptr_t>(a.xh) | reinterpret_cast<uintptr_t>(a.xl)) & 15u)) return false;
+    if (a.xn) {
+        if (!a.xn_w || ((reinterpret_cast<uintptr_t>(a.xn) | reinterpret_cast<uintptr_t>(a.xn_w)) & 15u)) return false;
+    } else if (!a.xh || !a.xl || ((reinterpret_cast<uintptr_t>(a.xh) | reinterpret_cast<uintptr_t>(a.xl)) & 15u)) {
+        return false;
+    }
+    if (a.res_frag && (a.epi != GEPI_STORE || a.nseg != 1 || a.seg[0].rows % 32u)) return false;
     for (uint32_t i = 0; i < a.nseg; ++i)
         if (!a.seg[i].w || (reinterpret_cast<uintptr_t>(a.seg[i].w) & 15u) || a.seg[i].rows == 0) return false;
     if (a.epi == GEPI_SWIGLU) return a.ksplit <= 1 && !a.o_tiled && a.nseg == 2 && a.seg[0].rows % 32u == 0;
-    if (a.epi == GEPI_STORE) return a.ksplit <= 1 || a.split_store;
+    if (a.epi == GEPI_STORE) return a.ksplit <= 1 || a.split_store || a.res_frag;
     return false;
 }
 
@@ -253,8 +351,11 @@ int launch_gemm_skinny(hipStream_t s, GemmArgs a) {
     if (grid == 0) return VX_OK;
     if (grid > 0x7fffffffull) return fail(VX_ERR_UNSUPPORTED, "skinny gemm: grid too large");
     VX_SET_STAMPS(a, ST_GEMM_SK, grid * 4u);
-    return a.epi == GEPI_SWIGLU ? launch_sk<GEPI_SWIGLU>(s, a, (uint32_t)grid)
-                                : launch_sk<GEPI_STORE>(s, a, (uint32_t)grid);
+    if (a.xn)
+        return a.epi == GEPI_SWIGLU ? launch_sk<GEPI_SWIGLU, true>(s, a, (uint32_t)grid)
+                                    : launch_sk<GEPI_STORE, true>(s, a, (uint32_t)grid);
+    return a.epi == GEPI_SWIGLU ? launch_sk<GEPI_SWIGLU, false>(s, a, (uint32_t)grid)
+                                : launch_sk<GEPI_STORE, false>(s, a, (uint32_t)grid);
 }
 
 int launch_repack_frag16(hipStream_t s, const __half *src, __half *dst, uint32_t rows, uint32_t K) {

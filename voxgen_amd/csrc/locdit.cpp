@@ -84,6 +84,12 @@ struct vx_locdit {
     vx_buf *yh = nullptr, *yl = nullptr, *ah = nullptr, *al = nullptr, *acth = nullptr, *actl = nullptr;
     vx_buf *part = nullptr;
     vx_buf *wfrag = nullptr;   // every layer's matrices in the fragment layout
+    // The residual stream as f32 in the fragment order (frag32_index), with both
+    // rmsnorms of a layer folded into the projections that read it (QKV, gate/up)
+    // and the attention/O and ffn_down products added to it atomically: four
+    // launches per layer instead of six. ssq: the QKV K slabs' row sums of squares.
+    bool fold_norm = false;
+    vx_buf *hres = nullptr, *ssq = nullptr;
     // Time embeddings of every estimator call of a solve, computed as one batch:
     // t values, sinusoid rows, MLP hidden rows, embeddings ([steps][hidden]).
     vx_buf *tvals = nullptr, *trows = nullptr, *tmid = nullptr, *temb = nullptr;
@@ -168,7 +174,7 @@ void free_all(vx_locdit *e) {
                        &e->branch, &e->scores,  &e->out,  &e->seed,       &e->rope_tab,
                        &e->tvals,  &e->trows,   &e->tmid, &e->temb,       &e->yh,            &e->yl,
                        &e->ah,     &e->al,      &e->acth, &e->actl,       &e->part,          &e->wfrag,
-                       &e->qkvp,   &e->out_ctr};
+                       &e->qkvp,   &e->out_ctr, &e->hres, &e->ssq};
     for (vx_buf **b : bufs) {
         vx_free(e->ctx, *b);
         *b = nullptr;
@@ -353,6 +359,146 @@ int enqueue_layers_general(vx_locdit *e, uint32_t batch) {
         }
     }
     return VX_OK;
+}
+
+constexpr uint64_t kFoldNormMaxRows = 32;   // CFG batch rows up to which fold_norm is chosen
+
+// record_transformer (local.rs:482-527) on the residual stream (fold_norm): four
+// launches per layer, the rmsnorms folded into the projections that read h.
+//   h (rows) -> the residual stream hres (frag32 order)        (once per pass)
+//   per layer:
+//     q|k|v slabs = (hres * attn_norm) . Wq|Wk|Wv, each K slab's row sums of
+//       squares to ssq                                          (k_gemm_sk, XN)
+//     attention over q, k, v scaled by 1/rms (RoPE while staging),
+//       hres += O projection, atomic adds                      (k_dense_attn_fused, RES)
+//     act = silu(g / rms) * (u / rms), g|u = (hres * ffn_norm) . Wg|Wu
+//                                                              (k_gemm_sk, XN, SwiGLU)
+//     hres += act . Wdown, atomic adds from every K slab       (k_gemm_sk, res_frag)
+//   norm = rmsnorm(hres) * locdit.norm, f32 rows for out_proj   (once per pass)
+// The fp32 atomic additions make the order of a residual row's sums vary from
+// run to run (results agree to rounding, not bit for bit).
+int enqueue_layers_residual(vx_locdit *e, uint32_t batch) {
+    vx_ctx *ctx = e->ctx;
+    hipStream_t s = ctx->stream;
+    const vx_locdit_config &c = e->cfg;
+    const uint32_t H = c.hidden, S = e->S, M = S * batch;
+    const uint32_t QD = c.q_heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    const uint64_t R16 = ((uint64_t)2u * S + 15u) & ~15ull;   // rows of the stream, as allocated
+    float *hres = F(e->hres), *ssq = F(e->ssq);
+    __half *acth = static_cast<__half *>(e->acth->ptr), *actl = static_cast<__half *>(e->actl->ptr);
+    auto wseg = [](const __half *w, uint32_t rows, float *out, uint32_t ldo) {
+        GemmSeg g;
+        g.w = w;
+        g.rows = rows;
+        g.out = out;
+        g.ldo = ldo;
+        return g;
+    };
+    auto gemm = [&](uint32_t K) {
+        GemmArgs g;
+        g.wk = WT_F16;
+        g.epi = GEPI_STORE;
+        g.ldx = K;
+        g.K = K;
+        g.T = M;
+        g.frag = 1;
+        return g;
+    };
+    {
+        ProfSpan sp(ctx, "local.residual_stream");
+        SeqNormArgs n;
+        n.h = F(e->hidden);
+        n.ldh = H;
+        n.n = H;
+        n.eps = c.rms_epsilon;
+        n.hf = hres;   // a copy only (no gains)
+        VX_CHECK(launch_seq_rmsnorm(s, n, M));
+    }
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const LocLayer &L = e->layers[l];
+        float *qp = F(e->qkvp), *kp = qp + (size_t)M * QD, *vp = kp + (size_t)M * KD;
+        const uint64_t qkv_slab = (uint64_t)M * (QD + 2u * KD);
+        {
+            ProfSpan sp(ctx, "local.seq_qkv");
+            GemmArgs g = gemm(H);
+            g.xn = hres;
+            g.xn_w = L.attn_norm;
+            g.xn_eps = c.rms_epsilon;
+            g.xn_ss = ssq;
+            g.xn_ss_stride = R16;
+            g.seg[0] = wseg(L.frag[0], QD, qp, QD);
+            g.seg[1] = wseg(L.frag[1], KD, kp, KD);
+            g.seg[2] = wseg(L.frag[2], KD, vp, KD);
+            g.nseg = 3;
+            g.ksplit = e->ks_qkv;
+            g.split_store = 1;
+            g.ws_stride = qkv_slab;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "local.attention_oproj");
+            DenseAttnArgs a;
+            a.q = qp;
+            a.k = kp;
+            a.v = vp;
+            a.nslab = e->ks_qkv;
+            a.slab_stride = qkv_slab;
+            a.tokens = S;
+            a.q_heads = c.q_heads;
+            a.kv_heads = c.kv_heads;
+            a.head_dim = c.head_dim;
+            a.q_stride = QD;
+            a.k_stride = KD;
+            a.v_stride = KD;
+            a.out_stride = QD;
+            a.score_stride = S;
+            a.batch = batch;
+            a.rope = reinterpret_cast<const float2 *>(e->rope_tab->ptr);
+            a.wo = L.frag[3];
+            a.hidden = H;
+            a.hres = hres;
+            a.ssq = ssq;
+            a.ssq_stride = R16;
+            a.norm_n = H;
+            a.eps = c.rms_epsilon;
+            VX_CHECK(launch_dense_attn_oproj(s, a));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_swiglu");
+            GemmArgs g = gemm(H);
+            g.epi = GEPI_SWIGLU;
+            g.xn = hres;
+            g.xn_w = L.ffn_norm;
+            g.xn_eps = c.rms_epsilon;
+            g.seg[0] = wseg(L.frag[4], c.ffn, nullptr, 0);
+            g.seg[1] = wseg(L.frag[5], c.ffn, nullptr, 0);
+            g.nseg = 2;
+            g.oh = acth;
+            g.ol = actl;
+            VX_CHECK(launch_gemm(s, g));
+        }
+        {
+            ProfSpan sp(ctx, "local.seq_linear");
+            GemmArgs g = gemm(c.ffn);
+            g.xh = acth;
+            g.xl = actl;
+            g.seg[0] = wseg(L.frag[6], H, nullptr, H);
+            g.ksplit = e->ks_down;
+            g.res_frag = hres;
+            VX_CHECK(launch_gemm(s, g));
+        }
+    }
+    ProfSpan sp(ctx, "local.seq_rmsnorm");
+    SeqNormArgs r;
+    r.h = hres;
+    r.h_frag = 1;
+    r.ldh = H;
+    r.n = H;
+    r.eps = c.rms_epsilon;
+    r.w = e->norm_w;
+    r.y = F(e->norm);   // out_proj reads f32 rows
+    r.ldy = H;
+    return launch_seq_rmsnorm(s, r, M);
 }
 
 // record_transformer (local.rs:482-527) for a batch that fits the short-batch
@@ -548,7 +694,8 @@ int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr, 
         }
         VX_CHECK(launch_pack_locdit(s, p));
     }
-    VX_CHECK(e->sk ? enqueue_layers_sk(e, batch) : enqueue_layers_general(e, batch));
+    VX_CHECK(e->fold_norm ? enqueue_layers_residual(e, batch)
+                          : e->sk ? enqueue_layers_sk(e, batch) : enqueue_layers_general(e, batch));
     if (skip_out) return VX_OK;   // the caller's launch applies out_proj
     ProfSpan sp(ctx, "local.locdit_out");
     const uint32_t x0 = c.n_mu + 1u + c.n_cond;   // first x token of a sequence
@@ -865,6 +1012,12 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
             e->ks_o = slabs(H, QD);
             e->ks_down = slabs(H, c.ffn);
             e->attn_oproj = c.q_heads <= kSeqNormMaxBranch && H % 16u == 0 && dense_attn_oproj_eligible(e->S, c.head_dim);
+            // The residual-stream stack when the CFG batch is at most two token
+            // fragments: each of its GEMM workgroups splits the whole f32 stream
+            // itself (what the rmsnorm did once), which at 2 x 11 tokens costs less
+            // than the two rmsnorm launches it removes (the 12-layer, 11-token
+            // solve 4.00 -> 3.63 ms) but at 2 x 37 tokens more (3.81 -> 3.93 ms).
+            e->fold_norm = e->attn_oproj && H % 1024u == 0 && H <= 4096u && S2 <= kFoldNormMaxRows;
             const uint64_t ks = std::max({e->ks_o, e->ks_down, e->attn_oproj ? c.q_heads : 1u});
             const uint64_t R16 = (S2 + 15u) & ~15ull;   // plane rows, padded to whole fragments
             struct {
@@ -874,7 +1027,9 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
                       {&e->ah, R16 * QD * 2u},         {&e->al, R16 * QD * 2u},
                       {&e->acth, R16 * c.ffn * 2u},    {&e->actl, R16 * c.ffn * 2u},
                       {&e->part, ks * S2 * H * 4u},
-                      {&e->qkvp, (uint64_t)e->ks_qkv * S2 * (QD + 2u * KD) * 4u}};
+                      {&e->qkvp, (uint64_t)e->ks_qkv * S2 * (QD + 2u * KD) * 4u},
+                      {&e->hres, R16 * H * 4u},
+                      {&e->ssq, 2u * R16 * 4u}};
             for (auto &b : sk) {
                 if ((st = vx_alloc(ctx, b.bytes, b.b))) return bail(st);
                 if (hipMemsetAsync((*b.b)->ptr, 0, (*b.b)->bytes, ctx->stream) != hipSuccess)

@@ -413,6 +413,21 @@ struct GemmArgs {
     // the X planes are in the fragment layout (frag16_index), and GEPI_SWIGLU
     // writes oh/ol in it (width seg[0].rows).
     uint32_t frag = 0;
+    // Short-batch kernel only. xn (nullable): X is rmsnorm(xn) * xn_w with xn an
+    // f32 [T][K] matrix in frag32_index order; the kernel multiplies by xn_w and
+    // splits to hi/lo in registers, and 1/rms of each row (from the sum of squares
+    // of its xn values, eps xn_eps) scales the products: GEPI_SWIGLU applies it
+    // before the SiLU; GEPI_STORE leaves the products unscaled and the workgroups
+    // of the first row tile store each K slab's sums of squares to xn_ss +
+    // slab * xn_ss_stride ([T]), for the consumer to finish the norm.
+    const float *xn = nullptr, *xn_w = nullptr;
+    float xn_eps = 0.f;
+    float *xn_ss = nullptr;
+    uint64_t xn_ss_stride = 0;
+    // Short-batch GEPI_STORE only, nullable: add alpha * the product (every K slab)
+    // to res_frag, an f32 [T][seg[0].rows] matrix in frag32_index order, with
+    // atomic adds (a residual update; no slabs).
+    float *res_frag = nullptr;
 };
 int launch_gemm(hipStream_t s, const GemmArgs &a);
 // Short-batch F16 kernel (kernels_skinny.hip): operands in the fragment layout
@@ -429,6 +444,15 @@ int launch_gemm_skinny(hipStream_t s, GemmArgs a);
 // and every operand load is 1 KB of contiguous bytes.
 __host__ __device__ __forceinline__ size_t frag16_index(uint32_t r, uint32_t c, uint32_t K) {
     return (((size_t)(r >> 4) * (K >> 5) + (c >> 5)) << 9) + ((((c >> 3) & 3u) << 4) + (r & 15u)) * 8u + (c & 7u);
+}
+// The same fragment order for an f32 matrix (the LocDiT residual stream): one 2 KB
+// block per 16 rows x 32 columns, in two 1 KB halves, half h holding for every
+// lane l = r + 16 g the four columns 8g + 4h .. 8g + 4h + 3 of row r. A wave's two
+// 16-byte loads of a block give each lane the eight values of its f16 fragment,
+// each load 1 KB of contiguous bytes.
+__host__ __device__ __forceinline__ size_t frag32_index(uint32_t r, uint32_t c, uint32_t K) {
+    return (((size_t)(r >> 4) * (K >> 5) + (c >> 5)) << 9) + (((c >> 2) & 1u) << 8) +
+           ((((c >> 3) & 3u) << 4) + (r & 15u)) * 4u + (c & 3u);
 }
 // Rewrites an F16 [rows][K] row-major matrix in the fragment layout (rows padded
 // to a multiple of 16 with zeros): dst holds ceil(rows/16)*16*K halves.
@@ -489,6 +513,11 @@ struct SeqNormArgs {
     // 1: zero the branch rows (every split) after reading them, so the buffer is the
     // cleared accumulator of the next split-K GEMM; the branch memory must be writable.
     uint32_t clear_branch = 0;
+    // k_seq_rmsnorm4 only: h_frag = 1 reads h in frag32_index order (width n, ldh
+    // unused; no branch); hf (nullable) receives h, after any residual update, in
+    // frag32_index order of width n.
+    uint32_t h_frag = 0;
+    float *hf = nullptr;
     VX_STAMP_FIELD
 };
 constexpr uint32_t kSeqNormMaxBranch = 16;
@@ -705,6 +734,17 @@ struct DenseAttnArgs {
     float *oslab = nullptr;
     uint64_t oslab_stride = 0;
     uint32_t nsplit = 1;
+    // launch_dense_attn_oproj only. hres (nullable): add the projection to hres,
+    // the residual stream [batch * tokens][hidden] in frag32_index order, with
+    // atomic adds, instead of writing the head slabs. ssq (nullable): q, k and v
+    // are products of the un-normalised rows, and ssq + s * ssq_stride (s < nslab)
+    // hold the K slabs' sums of squares of each row: the staging scales every q,
+    // k and v row by 1 / sqrt(sum / norm_n + eps).
+    float *hres = nullptr;
+    const float *ssq = nullptr;
+    uint64_t ssq_stride = 0;
+    uint32_t norm_n = 0;
+    float eps = 0.f;
     VX_STAMP_FIELD
 };
 int launch_dense_attn(hipStream_t s, const DenseAttnArgs &a, int which);
