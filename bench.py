@@ -570,42 +570,56 @@ def timeline_leg(steps=12):
         eng.close()
     model.free()
     report["cfm_locdit8"] = cfm_timeline(ctx, 1e6 / hz)
+    report["cfm_reference_12L"] = cfm_timeline(ctx, 1e6 / hz, reference=True)
     ctx.close()
     return report
 
 
+# Stamped kernels of a LocDiT layer (kinds: 7 k_gemm_sk, 8 k_dense_attn_fused with
+# the O projection, 9 k_seq_rmsnorm4): the slab stack of 2 x 37 rows, and the
+# residual-stream stack of 2 x 11 rows (the rmsnorms folded into the projections).
 CFM_LAYER_KERNELS = ("qkv", "attention_oproj", "rmsnorm_ffn", "gate_up", "down", "rmsnorm_next")
-CFM_LAYER_KINDS = (7, 8, 9, 7, 7, 9)   # k_gemm_sk, k_dense_attn_fused (O projection), k_seq_rmsnorm4
+CFM_LAYER_KINDS = (7, 8, 9, 7, 7, 9)
+CFM_REF_LAYER_KERNELS = ("qkv", "attention_oproj", "gate_up", "down")
+CFM_REF_LAYER_KINDS = (7, 8, 7, 7)
 
 
-def cfm_timeline(ctx, tick_us, solves=8):
-    """The LocDiT CFM solve graph at cfm_leg's shape and options, from the same
-    -DVX_STAMPS library: per stamped kernel of a layer (the short-batch GEMMs, the
-    fused attention with the O projection, the residual rmsnorms), the mean over
-    the solve's 72 layer passes and `solves` samples (each the last of four
-    back-to-back solves) of its span, the gap after the previous stamped kernel,
-    and the mean wave life."""
+def cfm_timeline(ctx, tick_us, solves=8, reference=False):
+    """The LocDiT CFM solve graph at cfm_leg's shape and options (reference=True:
+    cfm_reference_shape's), from the same -DVX_STAMPS library: per stamped kernel
+    of a layer, the mean over the solve's layer passes and `solves` samples (each
+    the last of four back-to-back solves) of its span, the gap after the previous
+    stamped kernel, and the mean wave life."""
     from voxgen_amd import synth
     from voxgen_amd.locdit import CfmOptions, LocDit
     from voxgen_amd.runtime import Model
-    cfg = synth.locdit_config(layers=8, q_heads=16, kv_heads=16, head_dim=64, n_mu=0, n_cond=32, cond_raw=1,
-                              uncond_zero_cond=1)
-    m = synth.build_locdit(cfg, seed=0x5EED0014)
+    if reference:
+        cfg = synth.locdit_config()
+        m = synth.build_locdit(cfg, seed=0x5EED0016)
+        cond = synth.normal_f32(cfg["patch"] * cfg["feat_dim"], 0x5EED0017)
+        mu = synth.normal_f32(2 * cfg["hidden"], 0x5EED0018)
+        names, kinds = CFM_REF_LAYER_KERNELS, CFM_REF_LAYER_KINDS
+    else:
+        cfg = synth.locdit_config(layers=8, q_heads=16, kv_heads=16, head_dim=64, n_mu=0, n_cond=32, cond_raw=1,
+                                  uncond_zero_cond=1)
+        m = synth.build_locdit(cfg, seed=0x5EED0014)
+        cond = synth.normal_f32(32 * 1024, 0x5EED0015)
+        mu = None
+        names, kinds = CFM_LAYER_KERNELS, CFM_LAYER_KINDS
     model = Model(ctx, m.data, m.tensors)
-    loc = LocDit(ctx, model, cfg, strict_geometry=False)
-    cond = synth.normal_f32(32 * 1024, 0x5EED0015)
+    loc = LocDit(ctx, model, cfg, strict_geometry=reference)
     launches0, _ = read_timeline(ctx)
-    loc.cfm_solve(cond, None, CfmOptions(n_timesteps=10, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0,
-                                         seed=42, use_cfg_zero_star=True))   # captures the solve's graph
+    loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=10, cfg_value=2.0, temperature=1.0, sway_sampling_coef=1.0,
+                                       seed=42, use_cfg_zero_star=True))   # captures the solve's graph
     launches, _ = read_timeline(ctx)
     first, count = len(launches0), len(launches) - len(launches0)
-    acc = {k: [] for k in CFM_LAYER_KERNELS}
+    acc = {k: [] for k in names}
     walls = []
     for i in range(solves):
         time.sleep(0.02)
         t0 = time.perf_counter()
         for j in range(4):
-            loc.cfm_solve(cond, None, CfmOptions(seed=43 + 4 * i + j))
+            loc.cfm_solve(cond, mu, CfmOptions(seed=43 + 4 * i + j))
         walls.append((time.perf_counter() - t0) / 4)
         launches, ticks = read_timeline(ctx)
         rows, _ = timeline_spans(launches, ticks, first, count)
@@ -614,11 +628,11 @@ def cfm_timeline(ctx, tick_us, solves=8):
             seq.append((kind, en - st, st - prev_end if prev_end is not None else np.nan, life, nw))
             prev_end = en
         j = 0
-        while j + len(CFM_LAYER_KINDS) <= len(seq):
-            if tuple(r[0] for r in seq[j:j + len(CFM_LAYER_KINDS)]) == CFM_LAYER_KINDS:
-                for q, name in enumerate(CFM_LAYER_KERNELS):
+        while j + len(kinds) <= len(seq):
+            if tuple(r[0] for r in seq[j:j + len(kinds)]) == kinds:
+                for q, name in enumerate(names):
                     acc[name].append(seq[j + q][1:])
-                j += len(CFM_LAYER_KINDS)
+                j += len(kinds)
             else:
                 j += 1
     loc.close()
@@ -632,7 +646,8 @@ def cfm_timeline(ctx, tick_us, solves=8):
                      "layer_passes": len(v)}
     period = sum(k["span_us"] + k["gap_before_us"] for k in out.values())
     summ = {"kernels": out, "layer_period_us": round(period, 3), "host_ms_per_solve": round(float(np.median(walls)) * 1e3, 4)}
-    log(f"timeline cfm_locdit8: layer period {summ['layer_period_us']} us, host {summ['host_ms_per_solve']} ms/solve; " +
+    log(f"timeline cfm {'reference 12L' if reference else 'locdit8'}: layer period {summ['layer_period_us']} us, "
+        f"host {summ['host_ms_per_solve']} ms/solve; " +
         ", ".join(f"{k} {v['span_us']} (+{v['gap_before_us']})" for k, v in out.items()))
     return summ
 
