@@ -995,7 +995,10 @@ typedef float of4 __attribute__((ext_vector_type(4)));
 // un-normalised rows, and the staging multiplies each row by its 1/rms (from the
 // K slabs' sums of squares in a.ssq); the projection is added to a.hres (the
 // residual stream, frag32_index order) with atomic adds instead of head slabs.
-template <int HD, int NSLAB = 1, bool OPROJ = false, bool RES = false>   // HD: head_dim when known at compile time, 0: a.head_dim
+// MAXT: the most tokens a sequence may have, which sizes the staging's register
+// arrays (16: sequences of at most 16 tokens, a quarter of the loads).
+template <int HD, int NSLAB = 1, bool OPROJ = false, bool RES = false,
+          uint32_t MAXT = kDenseFusedMaxTokens>   // HD: head_dim when known at compile time, 0: a.head_dim
 __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     VX_WAVE_STAMP(a.stamps);
     extern __shared__ __align__(16) float sm[];
@@ -1048,8 +1051,8 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
             // rows reload the last one and are not stored): a load under a branch
             // makes the compiler wait for every load in flight at the branch's end.
             constexpr uint32_t H2 = HD / 2, C4 = H2 / 4, V4 = HD / 4;
-            constexpr uint32_t NV = (kDenseFusedMaxTokens * V4 + 255u) / 256u;
-            constexpr uint32_t NKQ = ((kDenseFusedMaxTokens + ROWS) * C4 + 255u) / 256u;
+            constexpr uint32_t NV = (MAXT * V4 + 255u) / 256u;
+            constexpr uint32_t NKQ = ((MAXT + ROWS) * C4 + 255u) / 256u;
             // Slab 0 into vv / x0 / x1, slab 1 (NSLAB == 2) into the *b arrays.
             constexpr uint32_t NVB = NSLAB > 1 ? NV : 1u, NKB = NSLAB > 1 ? NKQ : 1u;
             float4 vv[NV], x0[NKQ], x1[NKQ], c01[NKQ], c23[NKQ], vvb[NVB], x0b[NKB], x1b[NKB];
@@ -1572,7 +1575,12 @@ int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a) {
     }
     const dim3 grid(a.q_heads, a.batch, ngroups * nsplit);
     VX_SET_STAMPS(b, ST_DENSE_ATTN, (uint64_t)grid.x * grid.y * grid.z * 4u);
-#define VX_OPROJ(HDV, NS, RS) k_dense_attn_fused<HDV, NS, true, RS><<<grid, 256, (size_t)lds, s>>>(b)
+    const bool short_seq = a.tokens <= 16u;
+#define VX_OPROJ(HDV, NS, RS)                                                               \
+    do {                                                                                    \
+        if (short_seq) k_dense_attn_fused<HDV, NS, true, RS, 16u><<<grid, 256, (size_t)lds, s>>>(b); \
+        else k_dense_attn_fused<HDV, NS, true, RS><<<grid, 256, (size_t)lds, s>>>(b);       \
+    } while (0)
     if (res) {
         if (a.head_dim == 64u && a.nslab == 2) VX_OPROJ(64, 2, true);
         else if (a.head_dim == 128u && a.nslab == 2) VX_OPROJ(128, 2, true);
@@ -1608,7 +1616,12 @@ int launch_dense_attn_fused(hipStream_t s, const DenseAttnArgs &a) {
                                           a.slab_stride % 4u)))
         return fail(VX_ERR_UNSUPPORTED, "fused dense attention: %u input slabs", a.nslab);
     const dim3 grid(a.q_heads, a.batch, (a.tokens + kDenseFusedRows - 1u) / kDenseFusedRows);
-    if (a.head_dim == 64u && a.nslab == 2)
+    const bool short_seq = a.tokens <= 16u;
+    if (a.head_dim == 64u && a.nslab == 2 && short_seq)
+        k_dense_attn_fused<64, 2, false, false, 16u><<<grid, 256, (size_t)lds, s>>>(b);
+    else if (a.head_dim == 128u && a.nslab == 2 && short_seq)
+        k_dense_attn_fused<128, 2, false, false, 16u><<<grid, 256, (size_t)lds, s>>>(b);
+    else if (a.head_dim == 64u && a.nslab == 2)
         k_dense_attn_fused<64, 2><<<grid, 256, (size_t)lds, s>>>(b);
     else if (a.head_dim == 128u && a.nslab == 2)
         k_dense_attn_fused<128, 2><<<grid, 256, (size_t)lds, s>>>(b);
