@@ -968,7 +968,11 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 // rows, the head's k and v rows (each padded by one float) and the rows x tokens
 // probabilities live in LDS. Scores are thread per (row, key), the softmax a wave
 // per row (lane per key), the values thread per (row, dim); each dot product and
-// sum runs in the order of the three-kernel path.
+// sum runs in the order of the three-kernel path. Sequences of at most 16 tokens
+// (the MAXT = 16 instantiation) take scores and softmax in one pass instead: a
+// half-wave per query row, its two 16-lane rows each half of the head's dims
+// (four partial sums per lane), the halves met by a row swap and the row max and
+// sum by DPP, with no LDS round trip and one barrier fewer.
 constexpr uint32_t kDenseFusedRows = 8;
 // The attention + O-projection variant: sixteen query tokens (one MFMA A
 // fragment) per workgroup, and at most kOprojBlocks weight blocks per wave.
@@ -977,6 +981,33 @@ constexpr uint32_t kOprojBlocks = 16;
 
 typedef _Float16 oh8 __attribute__((ext_vector_type(8)));
 typedef float of4 __attribute__((ext_vector_type(4)));
+
+// Lane exchanges of the short-sequence softmax (gfx9 DPP controls).
+template <int CTRL>
+__device__ __forceinline__ float seq_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// Max and sum over each 16-lane row: quad swaps, then the half-row and row mirrors.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, seq_dpp<0xb1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, seq_dpp<0x4e>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, seq_dpp<0x141>(v));   // row_half_mirror
+    return fmaxf(v, seq_dpp<0x140>(v));   // row_mirror
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += seq_dpp<0xb1>(v);
+    v += seq_dpp<0x4e>(v);
+    v += seq_dpp<0x141>(v);
+    return v + seq_dpp<0x140>(v);
+}
+// Rows 0 + 1 and 2 + 3 of the wave, lane by lane: v_permlane16_swap leaves the
+// lower row's value in element 0 and the upper row's in element 1 in every lane
+// of both rows, so both rows of a pair hold the same sum.
+__device__ __forceinline__ float row_pair_sum(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
 
 // NSLAB > 1 (float4 staging only): q, k and v are the sums of NSLAB partial
 // slabs a.slab_stride floats apart (a split-K projection's plain-store output).
@@ -1184,6 +1215,31 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     }
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)D);
+    if constexpr (HD > 0 && MAXT <= 16u) {
+        static_assert(ROWS <= 8u, "a half-wave per query row");
+        // Lane (t, part, key): query row t = 2 wave + lane / 32, dims
+        // [part HD/2, (part + 1) HD/2) with part = lane / 16 % 2, key = lane % 16.
+        // Rows and keys past R and S read the last valid one and are not stored.
+        const uint32_t t = 2u * wave + (lane >> 5), part = (lane >> 4) & 1u, key = lane & 15u;
+        const float4 *q4 = reinterpret_cast<const float4 *>(qs + min(t, R - 1u) * DP + part * (uint32_t)(HD / 2));
+        const float4 *k4 = reinterpret_cast<const float4 *>(ks + min(key, S - 1u) * DP + part * (uint32_t)(HD / 2));
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t d4 = 0; d4 < (uint32_t)HD / 8u; ++d4) {
+            const float4 x = q4[d4], y = k4[d4];
+            float &p = acc[d4 & 3u];
+            p += x.x * y.x;
+            p += x.y * y.y;
+            p += x.z * y.z;
+            p += x.w * y.w;
+        }
+        float sc = row_pair_sum((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale;
+        sc = key < S ? sc : -FLT_MAX;
+        const float m = row16_max(sc);
+        const float ex = key < S ? expf(sc - m) : 0.f;
+        const float z = row16_sum(ex);
+        if (part == 0u && t < R && key < S) ps[t * S + key] = ex / z;
+    } else {
     for (uint32_t e = tid; e < R * S; e += 256u) {
         const uint32_t t = e / S, key = e - t * S;
         float s = 0.f;
@@ -1215,6 +1271,7 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o, 64);
         if (lane < S) ps[t * S + lane] = ex / z;
+    }
     }
     __syncthreads();
     if constexpr (OPROJ) {

@@ -219,8 +219,12 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     __syncthreads();
     // XN: the workgroup's sum of squares of token tok (over its K range).
     auto row_ss = [&](uint32_t tok) {
-        const uint32_t mt = tok >> 4, r = tok & 15u;
-        return (ssl[0][mt][r] + ssl[1][mt][r]) + (ssl[2][mt][r] + ssl[3][mt][r]);
+        if constexpr (XN) {
+            const uint32_t mt = tok >> 4, r = tok & 15u;
+            return (ssl[0][mt][r] + ssl[1][mt][r]) + (ssl[2][mt][r] + ssl[3][mt][r]);
+        } else {
+            return 0.f;
+        }
     };
     auto part = [&](uint32_t mt, uint32_t f, uint32_t tl, uint32_t n) {
         const uint32_t ln = n + 16u * ((tl >> 2) & 3u), r = tl & 3u;
