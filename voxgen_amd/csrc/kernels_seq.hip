@@ -967,25 +967,29 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 // kDenseFusedRows query tokens of one head of one sequence in a workgroup: their q
 // rows, the head's k and v rows (each padded by one float) and the rows x tokens
 // probabilities live in LDS. Scores are thread per (row, key), the softmax a wave
-// per row (lane per key), the values thread per (row, dim); each dot product and
-// sum runs in the order of the three-kernel path. Sequences of at most 16 tokens
-// (the MAXT = 16 instantiation) take scores and softmax in one pass instead: a
-// half-wave per query row, its two 16-lane rows each half of the head's dims
-// (four partial sums per lane), the halves met by a row swap and the row max and
-// sum by DPP, with no LDS round trip and one barrier fewer.
+// per row (lane per key, its max and sum reduced by DPP), the values thread per
+// (row, dim); each dot product and value sum runs in the order of the three-kernel
+// path. Sequences of at most 16 tokens (the MAXT = 16 instantiation) take scores
+// and softmax in one pass instead: a half-wave per query row, its two 16-lane rows
+// each half of the head's dims (four partial sums per lane), the halves met by a
+// row swap and the row max and sum by DPP, with no LDS round trip and one barrier
+// fewer.
 constexpr uint32_t kDenseFusedRows = 8;
-// The attention + O-projection variant: sixteen query tokens (one MFMA A
-// fragment) per workgroup, and at most kOprojBlocks weight blocks per wave.
+// The attention + O-projection variant: eight query tokens (rows 0-7 of an MFMA
+// A fragment, the rest zero) per workgroup, and at most kOprojBlocks weight
+// blocks per wave.
 constexpr uint32_t kOprojRows = 8;
 constexpr uint32_t kOprojBlocks = 16;
 
 typedef _Float16 oh8 __attribute__((ext_vector_type(8)));
 typedef float of4 __attribute__((ext_vector_type(4)));
 
-// Lane exchanges of the short-sequence softmax (gfx9 DPP controls).
-template <int CTRL>
-__device__ __forceinline__ float seq_dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+// Lane exchanges of the fused softmax (gfx9 DPP controls); lanes of rows outside
+// ROW_MASK get `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float seq_dpp(float v, float old = 0.f) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                                 CTRL, ROW_MASK, 0xf, false));
 }
 // Max and sum over each 16-lane row: quad swaps, then the half-row and row mirrors.
 __device__ __forceinline__ float row16_max(float v) {
@@ -999,6 +1003,20 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += seq_dpp<0x4e>(v);
     v += seq_dpp<0x141>(v);
     return v + seq_dpp<0x140>(v);
+}
+// Over the whole wave: the 16-lane rows' results, then row_bcast15/31 fold the
+// four rows into lane 63, read back as a wave-uniform value.
+__device__ __forceinline__ float wave64_max(float v) {
+    v = row16_max(v);
+    v = fmaxf(v, seq_dpp<0x142, 0xa>(v, v));   // row_bcast:15 into rows 1 and 3
+    v = fmaxf(v, seq_dpp<0x143, 0xc>(v, v));   // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave64_sum(float v) {
+    v = row16_sum(v);
+    v += seq_dpp<0x142, 0xa>(v);
+    v += seq_dpp<0x143, 0xc>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 // Rows 0 + 1 and 2 + 3 of the wave, lane by lane: v_permlane16_swap leaves the
 // lower row's value in element 0 and the upper row's in element 1 in every lane
@@ -1263,13 +1281,9 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     __syncthreads();
     for (uint32_t t = wave; t < R; t += 4u) {
         const float x = lane < S ? ps[t * S + lane] : -FLT_MAX;
-        float m = x;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float m = wave64_max(x);
         const float ex = lane < S ? expf(x - m) : 0.f;
-        float z = ex;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o, 64);
+        const float z = wave64_sum(ex);
         if (lane < S) ps[t * S + lane] = ex / z;
     }
     }
@@ -1618,12 +1632,14 @@ int launch_dense_attn_oproj(hipStream_t s, const DenseAttnArgs &a) {
     b.oh = b.ol = nullptr;
     b.out = nullptr;
     // Split the hidden rows so that no wave holds more than kOprojBlocks weight
-    // blocks, and so that the grid reaches about 128 workgroups.
+    // blocks, and so that the grid reaches about 128 workgroups (512 for
+    // sequences of at most 16 tokens, whose workgroups are short: two per CU
+    // overlap one's staging with the other's projection).
     const uint32_t ngroups = (a.tokens + kOprojRows - 1u) / kOprojRows, ng = a.hidden / 16u;
     const uint32_t per_wave = kOprojBlocks / (a.head_dim / 32u);
     uint32_t nsplit = (ng + 4u * per_wave - 1u) / (4u * per_wave);
-    const uint32_t base = a.q_heads * a.batch * ngroups;
-    while (base * nsplit < 128u && 2u * nsplit <= (ng + 3u) / 4u) nsplit *= 2u;
+    const uint32_t base = a.q_heads * a.batch * ngroups, target = a.tokens <= 16u ? 512u : 128u;
+    while (base * nsplit < target && 2u * nsplit <= (ng + 3u) / 4u) nsplit *= 2u;
     b.nsplit = nsplit;
     uint64_t lds = dense_fused_lds_rows(a.tokens, a.head_dim, kOprojRows);
     if (res) {   // the product tile of the residual-stream form
