@@ -93,10 +93,13 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     }
     const GemmSeg &sg = a.seg[seg];
     const uint32_t S = a.K >> 5;
-    // Row groups past a matrix are clamped to its last one, and token rows past T
-    // in the last A block are whatever the producer left there: loaded and
-    // multiplied like the others, never stored (each output row of an MFMA
-    // depends only on its own A row).
+    // Row groups past a matrix are clamped to its last one. Token rows past T in
+    // the last A block are multiplied like the others and never stored (each
+    // output row of an MFMA depends only on its own A row). With at most two A
+    // blocks, when T - 1 is among the last block's first eight rows, rows past it
+    // read row T - 1 instead, so that rows 8-15 (the second 128 bytes of each
+    // 256-byte column group) add no cache line of their own; otherwise they read
+    // whatever the producer left there.
     const __half *wr[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
@@ -115,9 +118,15 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
         if (rg > last) rg = last;
         wr[f] = base + ((size_t)rg * S << 9) + 8u * lane;
     }
+    uint32_t xlane[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t last = a.T - 1u - min(a.T - 1u, 16u * (uint32_t)mt);
+        xlane[mt] = MT <= 2 && last < 8u ? (lane & ~15u) | min(lane & 15u, last) : lane;
+    }
     const __half *xr[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xr[mt] = a.xh + ((size_t)mt * S << 9) + 8u * lane;
+    for (int mt = 0; mt < MT; ++mt) xr[mt] = a.xh + ((size_t)mt * S << 9) + 8u * xlane[mt];
     const ptrdiff_t lo = a.xl - a.xh;
 
     const uint32_t s0 = ks * S / a.ksplit, s1 = (ks + 1u) * S / a.ksplit;
@@ -140,7 +149,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
         if constexpr (XN) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const float *p = a.xn + ((size_t)mt * S << 9) + c + 4u * lane;
+                const float *p = a.xn + ((size_t)mt * S << 9) + c + 4u * xlane[mt];
                 o.x[mt][0] = *reinterpret_cast<const float4 *>(p);
                 o.x[mt][1] = *reinterpret_cast<const float4 *>(p + 256);
             }
