@@ -105,6 +105,29 @@ def test_cfm_solve_8_layers_16x64_cond32(ctx):
     model.free()
 
 
+@pytest.mark.parametrize("n_mu,n_cond,q_heads,kv_heads,head_dim", [(0, 1, 16, 2, 128), (2, 9, 16, 2, 128),
+                                                                    (2, 9, 16, 16, 64), (2, 10, 16, 2, 128)])
+def test_cfm_solve_short_sequences(ctx, n_mu, n_cond, q_heads, kv_heads, head_dim):
+    """Sequences of 6, 16 and 17 tokens (n_mu + time + n_cond + 4 latent rows): the
+    fused attention's 16-token instantiation at both ends (scores and softmax in
+    one pass, the projection over 512 workgroups, the residual-stream stack) and,
+    at 17 tokens, the general one of the slab stack; 3 timesteps against the
+    oracle."""
+    cfg = synth.locdit_config(layers=2, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, n_mu=n_mu,
+                              n_cond=n_cond, cond_raw=1, uncond_zero_cond=1)
+    m = synth.build_locdit(cfg, seed=0x5EED0209 + n_cond)
+    model = Model(ctx, m.data, m.tensors)
+    o = oracle_of(m, cfg)
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, mu = inputs(cfg, 0x5EED020A + n_cond)
+    mu = mu if n_mu else None
+    got, res = loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=3, seed=11))
+    want = o.cfm_solve(cond, mu, n_timesteps=3, seed=11)
+    assert rel_l2(got, want) < 1e-4
+    loc.close()
+    model.free()
+
+
 def test_cfm_solve_general_stack_long_condition(ctx):
     """66 tokens per sequence (61 given condition rows): past the fused dense
     attention's 64 tokens, so the solve takes the general layer stack (k_gemm with
