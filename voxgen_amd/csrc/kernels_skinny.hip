@@ -47,7 +47,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kSkRows = 32;   // weight rows per workgroup (GEPI_STORE): two 16-row fragments
 constexpr uint32_t kSkPairs = 16;  // gate/up row pairs per workgroup (GEPI_SWIGLU)
-constexpr int kSkDepth = 3;        // k-steps in flight per wave
+constexpr int kSkDepth = 3;        // k-steps in flight per wave (4 with at most two token fragments)
 constexpr uint32_t kSkMaxTokens = 128;
 
 // Weights are read once per launch: nontemporal loads keep them from evicting
@@ -140,7 +140,11 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     for (int mt = 0; mt < MT; ++mt) ss[mt] = 0.f;
 
     using Ops = typename std::conditional<XN, SkOpsN<MT>, SkOps<MT>>::type;
-    Ops ring[kSkDepth];
+    // With at most two token fragments a k-step's operands are fewer registers, and
+    // four steps in flight cover the whole K range of a wave in the QKV and
+    // ffn_down launches of the 11-token contract (four k-steps each).
+    constexpr int DEPTH = MT <= 2 ? 4 : kSkDepth;
+    Ops ring[DEPTH];
     auto load = [&](Ops &o, int i) {
         const uint32_t step = s0 + wv + 4u * (uint32_t)i;
         const uint32_t c = step << 9;   // block offset of the k-step (halves of W; floats of xn)
@@ -197,12 +201,12 @@ __global__ __launch_bounds__(256) void k_gemm_sk(GemmArgs a) {
     // the branch not taken and wait for every load in flight before each MFMA.
     if (n_it > 0) {
 #pragma unroll
-        for (int u = 0; u < kSkDepth - 1; ++u) load(ring[u], min(u, n_it - 1));
-        for (int it = 0; it < n_it; it += kSkDepth) {
+        for (int u = 0; u < DEPTH - 1; ++u) load(ring[u], min(u, n_it - 1));
+        for (int it = 0; it < n_it; it += DEPTH) {
 #pragma unroll
-            for (int u = 0; u < kSkDepth; ++u) {
+            for (int u = 0; u < DEPTH; ++u) {
                 const int i = it + u;
-                load(ring[(u + kSkDepth - 1) % kSkDepth], min(i + kSkDepth - 1, n_it - 1));
+                load(ring[(u + DEPTH - 1) % DEPTH], min(i + DEPTH - 1, n_it - 1));
                 if (i < n_it) mma(ring[u]);
             }
         }
