@@ -2,7 +2,7 @@
 // seeded Gaussian noise, the CFG-Zero* Euler update, the sinusoidal time
 // embedding, LocDiT token packing, and small elementwise ops. All fp32; the
 // noise hash is exact integer arithmetic.
-#include "vx_internal.h"
+#include "decode_dev.h"   // wave_sum_dpp
 
 namespace vx {
 namespace {
@@ -52,17 +52,29 @@ __device__ __forceinline__ void cfg_euler_block(float *x, const float *pos, cons
         else return *p;
     };
     __shared__ float red[2][4];
+    // The first NR chunks of 256 stay in registers for the update (one round of
+    // loads instead of two); the wave sums reduce by DPP.
+    constexpr uint32_t NR = 4;
+    float pr[NR], qr[NR];
     float pn = 0.f, nn = 0.f;
-    for (uint32_t i = threadIdx.x; i < n; i += 256u) {
+#pragma unroll
+    for (uint32_t j = 0; j < NR; ++j) {
+        const uint32_t i = threadIdx.x + 256u * j;
+        pr[j] = i < n ? ld(pos + i) : 0.f;
+        qr[j] = i < n ? ld(neg + i) : 0.f;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NR; ++j) {
+        pn += pr[j] * qr[j];
+        nn += qr[j] * qr[j];
+    }
+    for (uint32_t i = threadIdx.x + 256u * NR; i < n; i += 256u) {
         const float p = ld(pos + i), q = ld(neg + i);
         pn += p * q;
         nn += q * q;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        pn += __shfl_xor(pn, o, 64);
-        nn += __shfl_xor(nn, o, 64);
-    }
+    pn = wave_sum_dpp(pn);
+    nn = wave_sum_dpp(nn);
     if ((threadIdx.x & 63u) == 0) {
         red[0][threadIdx.x >> 6] = pn;
         red[1][threadIdx.x >> 6] = nn;
@@ -71,7 +83,12 @@ __device__ __forceinline__ void cfg_euler_block(float *x, const float *pos, cons
     pn = red[0][0] + red[0][1] + red[0][2] + red[0][3];
     nn = red[1][0] + red[1][1] + red[1][2] + red[1][3];
     const float scale = zero_star ? pn / (nn + 1.0e-8f) : 1.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += 256u) {
+#pragma unroll
+    for (uint32_t j = 0; j < NR; ++j) {
+        const uint32_t i = threadIdx.x + 256u * j;
+        if (i < n) x[i] -= dt * (qr[j] * scale + cfg * (pr[j] - qr[j] * scale));
+    }
+    for (uint32_t i = threadIdx.x + 256u * NR; i < n; i += 256u) {
         const float p = ld(pos + i), q = ld(neg + i);
         const float guided = q * scale + cfg * (p - q * scale);
         x[i] -= dt * guided;
@@ -136,9 +153,7 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
 #pragma unroll
         for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) {
             if (r >= R) break;
-            float v = acc[r];
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            const float v = wave_sum_dpp(acc[r]);   // wave-uniform
             if (lane == r) {
                 const uint32_t b = r / a.patch, p = r - b * a.patch;
                 __hip_atomic_store(a.out + (size_t)b * n + (size_t)p * a.feat + f, v + bias, __ATOMIC_RELAXED,
