@@ -111,15 +111,16 @@ __global__ __launch_bounds__(256) void k_cfm_cfg_euler(float *x, const float *po
 // waits for another. (A device-scope fence here would write back and
 // invalidate the whole L2 of every workgroup's XCD: tens of microseconds over a
 // few hundred workgroups on MI355X.)
+template <bool FRAG>   // a.rows_frag
 __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
     __shared__ uint32_t is_last;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t f = blockIdx.x * 4u + wave, R = 2u * a.patch, n = a.patch * a.feat;
     if (f < a.feat) {
         const uint32_t ch = a.hidden >> 6;   // columns per lane, a multiple of 8
-        float acc[kOutEulerMaxRows];
+        float acc[kOutEulerMaxRows], ss[kOutEulerMaxRows];
 #pragma unroll
-        for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) acc[r] = 0.f;
+        for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) acc[r] = ss[r] = 0.f;
         const __half *wr = a.w + (size_t)f * a.hidden + lane * ch;
         for (uint32_t c = 0; c < ch; c += 8u) {
             const uint4 wv = *reinterpret_cast<const uint4 *>(wr + c);
@@ -131,12 +132,29 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
                 w8[2 * e] = t.x;
                 w8[2 * e + 1] = t.y;
             }
+            const uint32_t c0 = lane * ch + c;   // a multiple of 8
+            if constexpr (FRAG) {   // the final norm's weights folded into the row of W
+                const float4 n0 = *reinterpret_cast<const float4 *>(a.norm_w + c0);
+                const float4 n1 = *reinterpret_cast<const float4 *>(a.norm_w + c0 + 4);
+                w8[0] *= n0.x; w8[1] *= n0.y; w8[2] *= n0.z; w8[3] *= n0.w;
+                w8[4] *= n1.x; w8[5] *= n1.y; w8[6] *= n1.z; w8[7] *= n1.w;
+            }
 #pragma unroll
             for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) {
                 if (r >= R) break;
-                const uint32_t b = r / a.patch, p = r - b * a.patch;
-                const float *xr = a.rows + ((size_t)b * a.tokens + a.x0 + p) * a.hidden + lane * ch + c;
-                const float4 u0 = *reinterpret_cast<const float4 *>(xr), u1 = *reinterpret_cast<const float4 *>(xr + 4);
+                const uint32_t b = r / a.patch, p = r - b * a.patch, row = b * a.tokens + a.x0 + p;
+                float4 u0, u1;
+                if constexpr (FRAG) {   // columns c0..c0+3 and c0+4..c0+7: two float4 of the stream
+                    const float *xr = a.rows + frag32_index(row, c0, a.hidden);
+                    u0 = *reinterpret_cast<const float4 *>(xr);
+                    u1 = *reinterpret_cast<const float4 *>(xr + 256);
+                    ss[r] += u0.x * u0.x + u0.y * u0.y + u0.z * u0.z + u0.w * u0.w +
+                             u1.x * u1.x + u1.y * u1.y + u1.z * u1.z + u1.w * u1.w;
+                } else {
+                    const float *xr = a.rows + (size_t)row * a.hidden + c0;
+                    u0 = *reinterpret_cast<const float4 *>(xr);
+                    u1 = *reinterpret_cast<const float4 *>(xr + 4);
+                }
                 acc[r] += w8[0] * u0.x;
                 acc[r] += w8[1] * u0.y;
                 acc[r] += w8[2] * u0.z;
@@ -153,7 +171,8 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
 #pragma unroll
         for (uint32_t r = 0; r < kOutEulerMaxRows; ++r) {
             if (r >= R) break;
-            const float v = wave_sum_dpp(acc[r]);   // wave-uniform
+            float v = wave_sum_dpp(acc[r]);   // wave-uniform
+            if constexpr (FRAG) v *= 1.0f / sqrtf(wave_sum_dpp(ss[r]) / (float)a.hidden + a.eps);   // rmsnorm.comp:36-38
             if (lane == r) {
                 const uint32_t b = r / a.patch, p = r - b * a.patch;
                 __hip_atomic_store(a.out + (size_t)b * n + (size_t)p * a.feat + f, v + bias, __ATOMIC_RELAXED,
@@ -242,7 +261,8 @@ __global__ __launch_bounds__(256) void k_pack_locdit(PackLocditArgs a) {
     } else {
         v = a.x[(tok - a.n_mu - 1u - a.n_cond) * a.hidden + d];
     }
-    a.out[i] = v;
+    if (a.out_frag) a.out[frag32_index(b * seq_tokens + tok, d, a.hidden)] = v;
+    else a.out[i] = v;
 }
 
 // silu_inplace.comp:5 and add_vectors.comp:6.
@@ -292,10 +312,12 @@ bool cfm_out_euler_eligible(uint32_t patch, uint32_t feat, uint32_t hidden, cons
 
 int launch_cfm_out_euler(hipStream_t s, const CfmOutEulerArgs &a) {
     if (!cfm_out_euler_eligible(a.patch, a.feat, a.hidden, a.w) || !a.rows || !a.out || !a.x || !a.counter ||
-        (reinterpret_cast<uintptr_t>(a.rows) & 15u))
+        (reinterpret_cast<uintptr_t>(a.rows) & 15u) ||
+        (a.rows_frag && (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) & 15u))))
         return fail(VX_ERR_UNSUPPORTED, "cfm out_proj + euler: patch %u, feat %u, hidden %u", a.patch, a.feat,
                     a.hidden);
-    k_cfm_out_euler<<<(a.feat + 3u) / 4u, 256, 0, s>>>(a);
+    if (a.rows_frag) k_cfm_out_euler<true><<<(a.feat + 3u) / 4u, 256, 0, s>>>(a);
+    else k_cfm_out_euler<false><<<(a.feat + 3u) / 4u, 256, 0, s>>>(a);
     VX_LAUNCHED("k_cfm_out_euler");
     return VX_OK;
 }
@@ -315,6 +337,8 @@ int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a) {
     if (a.in_w && (a.feat == 0 || a.feat > 128u || a.feat % 8u || !a.xpatch ||
                    (reinterpret_cast<uintptr_t>(a.in_w) & 15u)))
         return fail(VX_ERR_UNSUPPORTED, "pack_locdit: fused in_proj needs feat %% 8 == 0, <= 128, 16-byte rows");
+    if (a.out_frag && a.hidden % 32u)
+        return fail(VX_ERR_UNSUPPORTED, "pack_locdit: a frag32 stream needs hidden %% 32 == 0");
     k_pack_locdit<<<(unsigned)((n + 255u) / 256u), 256, 0, s>>>(a);
     VX_LAUNCHED("k_pack_locdit");
     return VX_OK;

@@ -377,7 +377,9 @@ constexpr uint64_t kFoldNormMaxRows = 32;   // CFG batch rows up to which fold_n
 //   norm = rmsnorm(hres) * locdit.norm, f32 rows for out_proj   (once per pass)
 // The fp32 atomic additions make the order of a residual row's sums vary from
 // run to run (results agree to rounding, not bit for bit).
-int enqueue_layers_residual(vx_locdit *e, uint32_t batch) {
+// The pack wrote the stream (hres) itself. final_norm false: the caller's
+// out_proj + Euler launch folds the final rmsnorm in (CfmOutEulerArgs::rows_frag).
+int enqueue_layers_residual(vx_locdit *e, uint32_t batch, bool final_norm) {
     vx_ctx *ctx = e->ctx;
     hipStream_t s = ctx->stream;
     const vx_locdit_config &c = e->cfg;
@@ -404,16 +406,6 @@ int enqueue_layers_residual(vx_locdit *e, uint32_t batch) {
         g.frag = 1;
         return g;
     };
-    {
-        ProfSpan sp(ctx, "local.residual_stream");
-        SeqNormArgs n;
-        n.h = F(e->hidden);
-        n.ldh = H;
-        n.n = H;
-        n.eps = c.rms_epsilon;
-        n.hf = hres;   // a copy only (no gains)
-        VX_CHECK(launch_seq_rmsnorm(s, n, M));
-    }
     for (uint32_t l = 0; l < c.layers; ++l) {
         const LocLayer &L = e->layers[l];
         float *qp = F(e->qkvp), *kp = qp + (size_t)M * QD, *vp = kp + (size_t)M * KD;
@@ -488,6 +480,7 @@ int enqueue_layers_residual(vx_locdit *e, uint32_t batch) {
             VX_CHECK(launch_gemm(s, g));
         }
     }
+    if (!final_norm) return VX_OK;
     ProfSpan sp(ctx, "local.seq_rmsnorm");
     SeqNormArgs r;
     r.h = hres;
@@ -677,7 +670,8 @@ int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr, 
         p.time = time_row ? time_row : F(e->tvec);
         p.cond = c.cond_raw ? F(e->cond_in) : F(e->cond_proj_out);
         p.x = F(e->patch_proj);
-        p.out = F(e->hidden);
+        p.out = e->fold_norm ? F(e->hres) : F(e->hidden);
+        p.out_frag = e->fold_norm ? 1u : 0u;   // the residual-stream stack's stream
         p.hidden = H;
         p.n_mu = c.n_mu;
         p.n_cond = c.n_cond;
@@ -694,7 +688,7 @@ int enqueue_body(vx_locdit *e, uint32_t batch, const float *time_row = nullptr, 
         }
         VX_CHECK(launch_pack_locdit(s, p));
     }
-    VX_CHECK(e->fold_norm ? enqueue_layers_residual(e, batch)
+    VX_CHECK(e->fold_norm ? enqueue_layers_residual(e, batch, !skip_out)
                           : e->sk ? enqueue_layers_sk(e, batch) : enqueue_layers_general(e, batch));
     if (skip_out) return VX_OK;   // the caller's launch applies out_proj
     ProfSpan sp(ctx, "local.locdit_out");
@@ -791,6 +785,12 @@ int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_
             ProfSpan sp(e->ctx, "local.out_cfg_euler");
             CfmOutEulerArgs a;
             a.rows = F(e->norm);
+            if (e->fold_norm) {   // the stream itself, the final norm folded in
+                a.rows = F(e->hres);
+                a.rows_frag = 1;
+                a.norm_w = e->norm_w;
+                a.eps = c.rms_epsilon;
+            }
             a.tokens = e->S;
             a.x0 = c.n_mu + 1u + c.n_cond;
             a.patch = c.patch;

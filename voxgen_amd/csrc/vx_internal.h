@@ -784,6 +784,12 @@ struct CfmOutEulerArgs {
     float dt = 0.f, cfg = 0.f;
     uint32_t zero_star = 0;
     uint32_t *counter = nullptr;
+    // 1: rows is the un-normalised residual stream in frag32_index order, and the
+    // final rmsnorm (weights norm_w, eps over hidden) is folded in: each x row's
+    // 1/rms scales its products with (w . norm_w).
+    uint32_t rows_frag = 0;
+    const float *norm_w = nullptr;
+    float eps = 0.f;
 };
 bool cfm_out_euler_eligible(uint32_t patch, uint32_t feat, uint32_t hidden, const void *w);
 int launch_cfm_out_euler(hipStream_t s, const CfmOutEulerArgs &a);
@@ -806,6 +812,9 @@ struct PackLocditArgs {
     const void *in_b = nullptr;
     uint32_t in_bt = 0, feat = 0;
     const float *xpatch = nullptr;
+    // 1: out is a residual stream in frag32_index order (rows batch * tokens,
+    // hidden % 32 == 0) instead of f32 rows.
+    uint32_t out_frag = 0;
 };
 int launch_pack_locdit(hipStream_t s, const PackLocditArgs &a);
 int launch_silu_inplace(hipStream_t s, float *x, uint32_t n);
