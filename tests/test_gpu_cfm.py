@@ -87,6 +87,34 @@ def test_cfm_solve_graph_replay_seeds_and_initial_x(ctx, ref_shape):
     loc.close()
 
 
+def test_cfm_solve_switching_options(ctx, ref_shape):
+    """The time-embedding rows are computed outside the solve graph, once per
+    option set: solves alternating between step counts, sway coefficients and
+    CFG-Zero* on one engine each match the oracle, the profiled (eager) solve
+    included."""
+    cfg, m, model, o = ref_shape
+    loc = LocDit(ctx, model, cfg, strict_geometry=False)
+    _, cond, mu = inputs(cfg, 0x5EED020B)
+    cases = [dict(n_timesteps=3, sway=1.0, zero_star=True), dict(n_timesteps=5, sway=0.5, zero_star=False),
+             dict(n_timesteps=3, sway=1.0, zero_star=True), dict(n_timesteps=3, sway=0.0, zero_star=True)]
+    for i, k in enumerate(cases):
+        opt = CfmOptions(n_timesteps=k["n_timesteps"], sway_sampling_coef=k["sway"], use_cfg_zero_star=k["zero_star"],
+                         seed=21 + i)
+        if i == 3:
+            ctx.prof_enable(True)
+        got, _ = loc.cfm_solve(cond, mu, opt)
+        if i == 3:
+            ctx.prof_enable(False)
+        want = o.cfm_solve(cond, mu, n_timesteps=k["n_timesteps"], sway=k["sway"], zero_star=k["zero_star"],
+                           seed=21 + i)
+        assert rel_l2(got, want) < 1e-4, (i, k)
+    # The graph cached by case 2 replays after the profiled solve left other rows in temb.
+    got, _ = loc.cfm_solve(cond, mu, CfmOptions(n_timesteps=3, sway_sampling_coef=1.0, use_cfg_zero_star=True,
+                                                seed=30))
+    assert rel_l2(got, o.cfm_solve(cond, mu, n_timesteps=3, sway=1.0, zero_star=True, seed=30)) < 1e-4
+    loc.close()
+
+
 def test_cfm_solve_8_layers_16x64_cond32(ctx):
     """The benchmark's LocDiT shape: 8 layers, 16 x 64 MHA, 32 given condition rows
     zeroed in the unconditional pass, no mu tokens; 10 timesteps, cfg 2.0."""

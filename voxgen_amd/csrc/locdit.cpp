@@ -96,6 +96,10 @@ struct vx_locdit {
     uint32_t trows_cap = 0;
     vx_graph *graph = nullptr;
     vx_cfm_options graph_opt{};
+    // temb holds the time rows of these options (set by the last eager
+    // computation); the cached graph reads them and does not recompute them.
+    bool temb_ready = false;
+    vx_cfm_options temb_opt{};
     int graph_initial_x = -1;
     const float *graph_mu_src[2] = {nullptr, nullptr};   // model-hidden sources the graph projects, or null
 };
@@ -758,7 +762,7 @@ int enqueue_project_mu(vx_locdit *e, const float *current_lm, const float *resid
 // mu_src set, the mu tokens are first projected from those device vectors
 // (cfm_from_model_hiddens, local.rs:379-381,399-401).
 int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_t *calls,
-                  const float *const *mu_src = nullptr) {
+                  const float *const *mu_src = nullptr, bool time_rows = true) {
     hipStream_t s = e->ctx->stream;
     const vx_locdit_config &c = e->cfg;
     const uint32_t n = c.patch * c.feat_dim;
@@ -774,7 +778,9 @@ int enqueue_solve(vx_locdit *e, const vx_cfm_options &o, bool initial_x, uint32_
     uint32_t active = 0;
     for (size_t step = 1; step < span.size(); ++step) active += step > zi ? 1u : 0u;
     if (active > e->trows_cap) return fail(VX_ERR_STATE, "CFM time rows were not prepared for %u steps", active);
-    if (active) VX_CHECK(enqueue_time_rows(e, active));   // mean_mode = false: estimator dt is zero
+    // mean_mode = false: estimator dt is zero. Without time_rows the caller has
+    // already filled temb for these options.
+    if (active && time_rows) VX_CHECK(enqueue_time_rows(e, active));
     for (size_t step = 1; step < span.size(); ++step) {
         if (step <= zi) continue;
         const float t = span[step - 1], dt = t - span[step];
@@ -842,6 +848,7 @@ int prepare_time_rows(vx_locdit *e, const vx_cfm_options &o) {
                 *b = nullptr;
             }
         e->trows_cap = 0;
+        e->temb_ready = false;
         VX_CHECK(vx_alloc(ctx, (uint64_t)n * 4u, &e->tvals));
         VX_CHECK(vx_alloc(ctx, (uint64_t)n * H * 4u, &e->trows));
         VX_CHECK(vx_alloc(ctx, (uint64_t)n * H * 4u, &e->tmid));
@@ -1128,8 +1135,24 @@ int solve(vx_locdit *e, const float *cond, const float *mu, const float *const *
     VX_CHECK(prepare_time_rows(e, *opt));
     uint32_t calls = 0;
     if (ctx->prof_enabled) {
+        e->temb_ready = false;
         VX_CHECK(enqueue_solve(e, *opt, initial_x != nullptr, &calls, mu_src));
+        e->temb_opt = *opt;
+        e->temb_ready = true;
     } else {
+        // The time rows depend on the options only: computed eagerly when they
+        // change, outside the graph that every replay of these options runs.
+        if (!e->temb_ready || !same_options(e->temb_opt, *opt)) {
+            std::vector<float> span;
+            VX_CHECK(time_span(opt->n_timesteps, opt->sway_sampling_coef, span));
+            const uint32_t zi = zero_init_steps(*opt, span.size());
+            uint32_t active = 0;
+            for (size_t step = 1; step < span.size(); ++step) active += step > zi ? 1u : 0u;
+            e->temb_ready = false;
+            if (active) VX_CHECK(enqueue_time_rows(e, active));
+            e->temb_opt = *opt;
+            e->temb_ready = true;
+        }
         const int ix = initial_x ? 1 : 0;
         const float *src0 = mu_src ? mu_src[0] : nullptr, *src1 = mu_src ? mu_src[1] : nullptr;
         if (!e->graph || !same_options(e->graph_opt, *opt) || e->graph_initial_x != ix ||
@@ -1139,7 +1162,7 @@ int solve(vx_locdit *e, const float *cond, const float *mu, const float *const *
                 e->graph = nullptr;
             }
             VX_CHECK(vx_graph_begin(ctx));
-            const int st = enqueue_solve(e, *opt, initial_x != nullptr, &calls, mu_src);
+            const int st = enqueue_solve(e, *opt, initial_x != nullptr, &calls, mu_src, false);
             vx_graph *g = nullptr;
             const int st2 = vx_graph_end(ctx, &g);
             if (st != VX_OK) {
