@@ -969,7 +969,8 @@ __global__ __launch_bounds__(256) void k_dense_values(DenseAttnArgs a) {
 // probabilities live in LDS. Scores are thread per (row, key), the softmax a wave
 // per row (lane per key, its max and sum reduced by DPP), the values thread per
 // (row, dim); each dot product and value sum runs in the order of the three-kernel
-// path. Sequences of at most 16 tokens (the MAXT = 16 instantiation) take scores
+// path (with the O projection and fewer outputs than threads, lane pairs take the
+// even and odd keys of a value sum). Sequences of at most 16 tokens (the MAXT = 16 instantiation) take scores
 // and softmax in one pass instead: a half-wave per query row, its two 16-lane rows
 // each half of the head's dims (four partial sums per lane), the halves met by a
 // row swap and the row max and sum by DPP, with no LDS round trip and one barrier
@@ -1290,14 +1291,16 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
     __syncthreads();
     if constexpr (OPROJ) {
         // The output rows into the q rows' LDS (free once the scores are done),
-        // rows past R as zeros.
+        // rows past R as zeros. With fewer outputs than threads, lane pairs split
+        // the keys (even and odd) and meet by a DPP swap.
         constexpr uint32_t D4 = (uint32_t)HD / 4u;
-        for (uint32_t o = tid; o < ROWS * D4; o += 256u) {
-            const uint32_t t = o / D4, d4 = o - t * D4;
+        constexpr uint32_t KS = ROWS * D4 * 2u <= 256u ? 2u : 1u;
+        for (uint32_t o = tid; o < ROWS * D4 * KS; o += 256u) {
+            const uint32_t item = o / KS, half = o % KS, t = item / D4, d4 = item - t * D4;
             float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
             if (t < R) {
 #pragma unroll 4
-                for (uint32_t key = 0; key < S; ++key) {
+                for (uint32_t key = half; key < S; key += KS) {
                     const float p = ps[t * S + key];
                     const float4 w = *reinterpret_cast<const float4 *>(vs + key * DP + 4u * d4);
                     z.x += p * w.x;
@@ -1306,7 +1309,13 @@ __global__ __launch_bounds__(256) void k_dense_attn_fused(DenseAttnArgs a) {
                     z.w += p * w.w;
                 }
             }
-            *reinterpret_cast<float4 *>(qs + t * DP + 4u * d4) = z;
+            if constexpr (KS == 2) {   // quad_perm [1,0,3,2]: the pair's other half
+                z = make_float4(z.x + seq_dpp<0xb1>(z.x), z.y + seq_dpp<0xb1>(z.y), z.z + seq_dpp<0xb1>(z.z),
+                                z.w + seq_dpp<0xb1>(z.w));
+                if (half == 0u) *reinterpret_cast<float4 *>(qs + t * DP + 4u * d4) = z;
+            } else {
+                *reinterpret_cast<float4 *>(qs + t * DP + 4u * d4) = z;
+            }
         }
         __syncthreads();
         // A fragments: lane l = r + 16 c holds columns 8c..8c+7 of block kb for row r.
