@@ -116,6 +116,21 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
     __shared__ uint32_t is_last;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t f = blockIdx.x * 4u + wave, R = 2u * a.patch, n = a.patch * a.feat;
+    // FRAG: the x rows copied from the stream into LDS as f32 rows (16-byte pieces
+    // of frag32 order, four columns each), so that the lanes' reads below are
+    // contiguous; a lane's own columns of one row in frag32 order lie in another
+    // 2 KB block each.
+    extern __shared__ __align__(16) float xrows[];
+    if constexpr (FRAG) {
+        const uint32_t h4 = a.hidden >> 2;
+        for (uint32_t i = threadIdx.x; i < R * h4; i += 256u) {
+            const uint32_t r = i / h4, c = 4u * (i - r * h4);
+            const uint32_t b = r / a.patch, p = r - b * a.patch, row = b * a.tokens + a.x0 + p;
+            *reinterpret_cast<float4 *>(xrows + (size_t)r * a.hidden + c) =
+                *reinterpret_cast<const float4 *>(a.rows + frag32_index(row, c, a.hidden));
+        }
+        __syncthreads();
+    }
     if (f < a.feat) {
         const uint32_t ch = a.hidden >> 6;   // columns per lane, a multiple of 8
         float acc[kOutEulerMaxRows], ss[kOutEulerMaxRows];
@@ -144,10 +159,11 @@ __global__ __launch_bounds__(256) void k_cfm_out_euler(CfmOutEulerArgs a) {
                 if (r >= R) break;
                 const uint32_t b = r / a.patch, p = r - b * a.patch, row = b * a.tokens + a.x0 + p;
                 float4 u0, u1;
-                if constexpr (FRAG) {   // columns c0..c0+3 and c0+4..c0+7: two float4 of the stream
-                    const float *xr = a.rows + frag32_index(row, c0, a.hidden);
+                if constexpr (FRAG) {   // the row's columns c0..c0+7 from LDS
+                    (void)row;
+                    const float *xr = xrows + (size_t)r * a.hidden + c0;
                     u0 = *reinterpret_cast<const float4 *>(xr);
-                    u1 = *reinterpret_cast<const float4 *>(xr + 256);
+                    u1 = *reinterpret_cast<const float4 *>(xr + 4);
                     ss[r] += u0.x * u0.x + u0.y * u0.y + u0.z * u0.z + u0.w * u0.w +
                              u1.x * u1.x + u1.y * u1.y + u1.z * u1.z + u1.w * u1.w;
                 } else {
@@ -316,7 +332,12 @@ int launch_cfm_out_euler(hipStream_t s, const CfmOutEulerArgs &a) {
         (a.rows_frag && (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) & 15u))))
         return fail(VX_ERR_UNSUPPORTED, "cfm out_proj + euler: patch %u, feat %u, hidden %u", a.patch, a.feat,
                     a.hidden);
-    if (a.rows_frag) k_cfm_out_euler<true><<<(a.feat + 3u) / 4u, 256, 0, s>>>(a);
+    if (a.rows_frag) {
+        const uint64_t lds = (uint64_t)2u * a.patch * a.hidden * 4u;
+        if (lds > 65536u) return fail(VX_ERR_UNSUPPORTED, "cfm out_proj + euler: %u x rows of %u in LDS", 2u * a.patch,
+                                      a.hidden);
+        k_cfm_out_euler<true><<<(a.feat + 3u) / 4u, 256, (size_t)lds, s>>>(a);
+    }
     else k_cfm_out_euler<false><<<(a.feat + 3u) / 4u, 256, 0, s>>>(a);
     VX_LAUNCHED("k_cfm_out_euler");
     return VX_OK;
