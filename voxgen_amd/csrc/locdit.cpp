@@ -1063,8 +1063,11 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
             }
             e->sk = true;
             // out_proj + Euler update in one launch (F16 out_proj, rows of the
-            // normed hidden f32 and 16-byte aligned).
-            if (e->out_proj.w.wt == WT_F16 && e->out_proj.w.dtype == 1 &&
+            // normed hidden f32 and 16-byte aligned). On the residual stream it
+            // stages the 2 x patch stream rows in LDS (at most 64 KB); past that
+            // the final rmsnorm runs and the launch reads its rows instead.
+            const bool rows_fit = !e->fold_norm || 2ull * c.patch * H * 4u <= 65536u;
+            if (e->out_proj.w.wt == WT_F16 && e->out_proj.w.dtype == 1 && rows_fit &&
                 cfm_out_euler_eligible(c.patch, c.feat_dim, H, e->out_proj.w.ptr)) {
                 if ((st = vx_alloc(ctx, 256u, &e->out_ctr))) return bail(st);
                 if (hipMemsetAsync(e->out_ctr->ptr, 0, 256u, ctx->stream) != hipSuccess)
