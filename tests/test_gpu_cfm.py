@@ -156,18 +156,21 @@ def test_cfm_solve_short_sequences(ctx, n_mu, n_cond, q_heads, kv_heads, head_di
     model.free()
 
 
-def test_cfm_solve_residual_stream_wide_rows(ctx):
-    """Residual-stream stack at hidden 2048 and patch 8: the 16 stream rows the
-    out_proj + Euler launch would stage (128 KB) exceed its 64 KB of LDS, so the
-    final rmsnorm runs and that launch reads the normed rows; 3 timesteps against
-    the oracle."""
-    cfg = synth.locdit_config(layers=2, hidden=2048, q_heads=16, kv_heads=2, head_dim=128, ffn=2048, patch=8,
-                              n_mu=0, n_cond=1, cond_raw=1, uncond_zero_cond=1)
-    m = synth.build_locdit(cfg, seed=0x5EED020C)
+@pytest.mark.parametrize("hidden,patch,fused", [(2048, 8, False), (4096, 2, True)])
+def test_cfm_solve_residual_stream_wide_rows(ctx, hidden, patch, fused):
+    """Residual-stream stack at the out_proj + Euler launch's LDS limit: at hidden
+    4096 and patch 2 its 4 stream rows fill the 64 KB exactly and the launch folds
+    the final rmsnorm in; at hidden 2048 and patch 8 the 16 rows (128 KB) do not
+    fit, so the final rmsnorm runs and that launch reads the normed rows; 3
+    timesteps against the oracle."""
+    cfg = synth.locdit_config(layers=2, hidden=hidden, q_heads=16, kv_heads=2, head_dim=128,
+                              ffn=1024 if fused else 2048, patch=patch, n_mu=0, n_cond=1, cond_raw=1,
+                              uncond_zero_cond=1)
+    m = synth.build_locdit(cfg, seed=0x5EED020C + patch)
     model = Model(ctx, m.data, m.tensors)
     o = oracle_of(m, cfg)
     loc = LocDit(ctx, model, cfg, strict_geometry=False)
-    _, cond, _ = inputs(cfg, 0x5EED020D)
+    _, cond, _ = inputs(cfg, 0x5EED020D + patch)
     want = o.cfm_solve(cond, None, n_timesteps=3, seed=5)
     got, _ = loc.cfm_solve(cond, None, CfmOptions(n_timesteps=3, seed=5))
     assert rel_l2(got, want) < 1e-4
@@ -177,10 +180,13 @@ def test_cfm_solve_residual_stream_wide_rows(ctx):
     ctx.prof_enable(False)
     spans = ctx.prof_snapshot()
     assert rel_l2(got, want) < 1e-4
-    # The residual stream (no per-layer residual rmsnorm), its final rmsnorm once
-    # per step, then out_proj and the Euler update as two launches.
-    assert "local.seq_residual_rmsnorm" not in spans and "local.out_cfg_euler" not in spans
-    assert spans["local.seq_rmsnorm"]["calls"] == spans["local.cfm_cfg_euler"]["calls"] > 0
+    # The residual stream: no per-layer residual rmsnorm.
+    assert "local.seq_residual_rmsnorm" not in spans
+    if fused:   # one out_proj + Euler launch per step, the final norm folded in
+        assert "local.seq_rmsnorm" not in spans and spans["local.out_cfg_euler"]["calls"] > 0
+    else:   # the final rmsnorm once per step, then out_proj and the Euler update
+        assert "local.out_cfg_euler" not in spans
+        assert spans["local.seq_rmsnorm"]["calls"] == spans["local.cfm_cfg_euler"]["calls"] > 0
     loc.close()
     model.free()
 
