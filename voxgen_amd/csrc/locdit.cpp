@@ -1023,7 +1023,7 @@ int vx_locdit_create(vx_ctx *ctx, const vx_model *model, const vx_model *rope_mo
             // fragments: each of its GEMM workgroups splits the whole f32 stream
             // itself (what the rmsnorm did once), which at 2 x 11 tokens costs less
             // than the two rmsnorm launches it removes (the 12-layer, 11-token
-            // solve 4.00 -> 3.63 ms) but at 2 x 37 tokens more (3.81 -> 3.93 ms).
+            // solve 4.00 -> 3.63 ms) but at 2 x 37 tokens more (3.71 -> 3.81 ms).
             e->fold_norm = e->attn_oproj && H % 1024u == 0 && H <= 4096u && S2 <= kFoldNormMaxRows;
             const uint64_t ks = std::max({e->ks_o, e->ks_down, e->attn_oproj ? c.q_heads : 1u});
             const uint64_t R16 = (S2 + 15u) & ~15ull;   // plane rows, padded to whole fragments
